@@ -1,0 +1,170 @@
+"""Benchmark of the ACE hot path on one MI355X.
+
+A step = stage 1 (fused density) + stage 2 (B-feature product) over the whole
+synthetic workload, inputs resident in HBM.  Default workload: configuration 4
+(50 000 nodes x 16 channels, 24 neighbours, l<=3, nu=3, L in {0,1,2}, fp32),
+the configuration BASELINE.json's HBM target is stated on.
+
+Prints ONE JSON line (rank 0).  Per-kernel durations come from HIP events
+recorded on the stream the kernels run on (torch's current stream).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_bytes(cfg, plan, elem):
+    """Compulsory traffic per launch (each input read once, each output written once)."""
+    d = cfg.density
+    N, K = d.atom_count, d.neighbors_per_atom
+    E = N * K
+    C = d.channel_count
+    a_row = C * d.radial_rows * (d.l_max + 1) ** 2
+    stage1 = E * (3 * elem + 8) + (N + 1) * 8 + N * a_row * elem
+    if d.node_channels:
+        stage1 += N * d.node_channels * elem + d.node_channels * (d.n_max + 1) * elem
+    if d.species_count:
+        stage1 += N * 4
+    samples = cfg.samples()
+    stage2 = samples * plan.a_width * elem + samples * plan.feature_count * elem
+    return stage1, stage2
+
+
+def cpu_baseline(cfg, pipe, target_seconds=10.0):
+    """The C oracle (restatement of the reference CPU path) on a bounded sample."""
+    import numpy as np
+
+    import oracle
+
+    threads = oracle.max_threads()
+
+    def run(atoms):
+        sub = type(cfg.density)(**{**cfg.density.__dict__, "atom_count": atoms})
+        inp = sub.generate()
+        t0 = time.perf_counter()
+        A = oracle.ace_density(inp)
+        t1 = time.perf_counter()
+        oracle.ace_product_flat(A.reshape(-1, pipe.plan.a_width), pipe.plan.flat_arrays())
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1
+
+    pipe.plan.flat_arrays()  # table build is host compile work, not timed
+    probe = 200
+    s1, s2 = run(probe)
+    atoms = int(min(cfg.density.atom_count, max(probe, probe * target_seconds / max(s1 + s2, 1e-6))))
+    s1, s2 = run(atoms)
+    per_atom_features = cfg.samples() // cfg.density.atom_count * pipe.plan.feature_count
+    total = s1 + s2
+    return {"value": atoms * per_atom_features / total, "unit": "B-features/s", "cores": threads,
+            "kind": "port", "atoms_per_s": atoms / total,
+            "sample": f"{atoms} atoms of the same workload; stage1 {s1:.2f}s (serial edge loop, as the reference), "
+                      f"stage2 {s2:.2f}s (OpenMP over samples, {threads} threads)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=4)
+    ap.add_argument("--dtype", default=None)
+    ap.add_argument("--max-slots", type=int, default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "the ACE product is per-sample independent and shards by atoms, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from ye3t_amd.ace import workloads as W
+    from ye3t_amd.ace.pipeline import ACEPipeline, to_device_inputs
+    from ye3t_amd.ace.program import program_stats
+
+    cfg = W.config(args.config)
+    dtype = args.dtype or cfg.dtypes[0]
+    elem = 8 if dtype == "f64" else 4
+    t_build = time.perf_counter()
+    pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots)
+    t_build = time.perf_counter() - t_build
+    inp = cfg.density.generate()
+    dev = to_device_inputs(inp, dtype, "cuda")
+    d = cfg.density
+    A = torch.empty((d.atom_count, d.channel_count, d.radial_rows, (d.l_max + 1) ** 2),
+                    dtype=torch.float64 if dtype == "f64" else torch.float32, device="cuda")
+    rows = A.reshape(-1, pipe.plan.a_width)
+    B = torch.empty((rows.shape[0], pipe.feature_count), dtype=A.dtype, device="cuda")
+
+    def step():
+        pipe.density(dev, out=A)
+        pipe.product(rows, out=B)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1, e2 in ev:
+        e0.record()
+        pipe.density(dev, out=A)
+        e1.record()
+        pipe.product(rows, out=B)
+        e2.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    s1 = float(np.mean([a.elapsed_time(b) for a, b, _ in ev])) * 1e-3
+    s2 = float(np.mean([b.elapsed_time(c) for _, b, c in ev])) * 1e-3
+    ms_per_step = wall / args.steps * 1e3
+    b1, b2 = algorithmic_bytes(cfg, pipe.plan, elem)
+    features = rows.shape[0] * pipe.feature_count
+    value = features / (wall / args.steps)
+    stats = program_stats(pipe.program)
+    line = {
+        "metric": "B-features/sec (atoms/s) on 1 MI355X; achieved HBM GB/s vs peak",
+        "value": value,
+        "unit": "B-features/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic (seeded counter RNG, BASELINE.json configuration shapes)",
+        "config": {"workload": f"config{cfg.config_id}-{cfg.name}", "atoms": d.atom_count,
+                   "neighbors_per_atom": d.neighbors_per_atom, "channels": d.channel_count,
+                   "samples": int(rows.shape[0]), "features_per_sample": pipe.feature_count,
+                   "n_max": d.n_max, "l_max": d.l_max, "nu_max": cfg.feature_spec.nu_max,
+                   "targets": list(cfg.feature_spec.targets), "parallelism": "single GPU"},
+        "atoms_per_s": d.atom_count / (wall / args.steps),
+        "roofline": {"bound": "hbm", "achieved": b2 / s2 / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": b2 / s2 / 1e9 / HBM_PEAK_GBS, "traffic": None, "kernel": "product_kernel",
+                     "algorithmic_bytes": b2, "avg_kernel_us": s2 * 1e6},
+        "stage1": {"kernel": "ace_density_kernel", "avg_kernel_us": s1 * 1e6, "algorithmic_bytes": b1,
+                   "achieved_gbs": b1 / s1 / 1e9, "frac": b1 / s1 / 1e9 / HBM_PEAK_GBS},
+        "stage2": {"kernel": "product_kernel", "avg_kernel_us": s2 * 1e6, "algorithmic_bytes": b2,
+                   "achieved_gbs": b2 / s2 / 1e9, "frac": b2 / s2 / 1e9 / HBM_PEAK_GBS,
+                   "program": stats, "plan_compile_s": t_build},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(cfg, pipe, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

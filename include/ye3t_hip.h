@@ -1,0 +1,175 @@
+/*
+ * ye3t_hip -- C ABI of the MI355X (gfx950) HIP backend for the ACE
+ * native-execution-plan hot path.
+ *
+ * Conventions
+ *   - All array arguments are device pointers to contiguous row-major memory
+ *     (host pointers only where a comment says "host").
+ *   - `dtype` is YE3T_F32 or YE3T_F64; float arrays of one call share it.
+ *   - Work is enqueued on `stream` (NULL = default stream); calls never
+ *     synchronise the device except plan creation, which copies tables.
+ *   - Return 0 on success, a negative ye3t_status on failure; the message of
+ *     the last failure on the calling thread is ye3t_hip_last_error().
+ *     Nothing throws across this boundary.
+ */
+#ifndef YE3T_HIP_H
+#define YE3T_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define YE3T_HIP_ABI_VERSION 43 /* reference native ABI floor is 42 (execution_plan.py:35) */
+
+typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
+
+enum ye3t_dtype { YE3T_F32 = 0, YE3T_F64 = 1 };
+
+enum ye3t_status {
+  YE3T_OK = 0,
+  YE3T_EINVAL = -1,      /* invalid argument / shape */
+  YE3T_ELAUNCH = -2,     /* HIP launch or runtime failure */
+  YE3T_EDTYPE = -3,      /* unsupported dtype */
+  YE3T_ENOMEM = -4,      /* device allocation failed */
+  YE3T_EUNSUPPORTED = -5 /* size outside the compiled kernel limits */
+};
+
+/* Library ABI version; replaces core_abi_version() of the reference's pybind
+ * module (ye3t/runtime/csrc/execution_plan_torch.cpp:7924-7934). */
+int ye3t_hip_abi_version(void);
+
+/* Thread-local message of the last failed call ("" if none). */
+const char* ye3t_hip_last_error(void);
+
+typedef struct {
+  char arch[64];            /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int device;
+  int cu_count;
+  int wavefront_size;
+  int lds_bytes_per_block;  /* max shared memory per block */
+  int clock_khz;
+  int64_t hbm_bytes;
+  double hbm_peak_gbs;      /* nominal peak used for roofline fractions */
+} ye3t_hip_caps;
+
+/* Device facts for the capability report (has_cuda()/has_cpu() counterpart,
+ * execution_plan_torch.cpp:7924-7934). */
+int ye3t_hip_device_caps(int device, ye3t_hip_caps* out);
+
+/* ChebExpCos radial table and d/dr, [E, n_max+1] each.
+ * Replaces the CUDA branch of ye3t_runtime::cheb_exp_cos_radial_table_with_derivative
+ * (schema execution_plan_torch.cpp:7237-7240; kernel execution_plan_cuda.cu:3386-3470).
+ * `derivatives` may be NULL. */
+int ye3t_hip_radial_table(int dtype, const void* radii, const void* cutoffs, const void* lambdas,
+                          int64_t edge_count, int64_t max_radial_index, void* values, void* derivatives,
+                          ye3t_stream_t stream);
+
+/* Real spherical-harmonic table [E, (l_max+1)^2] and Cartesian gradient
+ * [E, (l_max+1)^2, 3] of edge vectors [E, 3].  Replaces the CUDA branch of
+ * ye3t_runtime::spherical_harmonics_table_with_derivative with real_output=true
+ * (schema execution_plan_torch.cpp:7250-7253; kernel execution_plan_cuda.cu:4266-4365).
+ * `gradients` may be NULL.  l_max <= 12. */
+int ye3t_hip_real_sph_table(int dtype, const void* edge_vectors, int64_t edge_count, int64_t l_max,
+                            double epsilon, void* values, void* gradients, ye3t_stream_t stream);
+
+/* out[i, c] = sum over edges e in [row_offsets[i], row_offsets[i+1]) of
+ * edge_values[e, c]; deterministic CSR segment reduction, no atomics.
+ * Replaces ye3t_runtime::density_accumulate (schema execution_plan_torch.cpp:7284-7286,
+ * CUDA atomics kernel execution_plan_cuda.cu:281-301) for centre-sorted edges. */
+int ye3t_hip_density_accumulate_csr(int dtype, const void* edge_values, const int64_t* row_offsets,
+                                    int64_t atom_count, int64_t channel_count, void* out,
+                                    ye3t_stream_t stream);
+
+/* Fused stage 1: A[i, c, r, lm] = sum_{e in row i} w_c(e) R_r(|v_e|) Y_lm(v_e/|v_e|).
+ * One pass over edges: radial basis and real SH in registers, per-atom CSR
+ * segment reduction, no atomics.  Fuses the reference chain
+ * cheb_exp_cos_radial_table -> spherical_harmonics_table ->
+ * scheduled_radial_angular_channels -> density_accumulate
+ * (execution_plan.py:7298, 7479, 7675, 7913). */
+typedef struct {
+  int dtype;
+  int64_t atom_count;
+  int64_t edge_count;
+  const int64_t* row_offsets;   /* [N+1] edges sorted by centre */
+  const int64_t* neighbors;     /* [E] neighbour atom of each edge */
+  const void* edge_vectors;     /* [E, 3] r_j - r_i */
+  const int32_t* species;       /* [N] one-hot channel of each atom, or NULL */
+  const void* node_features;    /* [N, C] channel weights h[j, c], or NULL */
+  const void* radial_mix;       /* [C, n_max+1]: R_c = sum_n mix[c,n] R_n, or NULL */
+  int64_t channel_count;        /* C (species count, feature channels, or 1) */
+  int64_t max_radial_index;     /* n_max <= 15 */
+  int64_t max_angular;          /* l_max <= 8 */
+  double cutoff;
+  double lambda;
+  double epsilon;
+} ye3t_density_args;
+
+/* A has shape [N, C, R, (l_max+1)^2] with R = 1 when radial_mix is set, else n_max+1. */
+int ye3t_hip_ace_density_forward(const ye3t_density_args* args, void* A, ye3t_stream_t stream);
+
+/* S[b, o] = sum_{t in [output_offsets[o], output_offsets[o+1])} monomial_values[t]
+ *           * prod_c input[b, c]^monomial_counts[t, c].
+ * Replaces the CUDA branch of ye3t_runtime::symmetric_power_monomial
+ * (kernel execution_plan_cuda.cu:5229; CPU ye3t_runtime_core.cpp:5279-5315). */
+int ye3t_hip_symmetric_power_monomial(int dtype, const void* input, int64_t batch, int64_t input_dim,
+                                      const int64_t* monomial_counts, const int64_t* output_offsets,
+                                      const void* monomial_values, int64_t output_dim, void* output,
+                                      ye3t_stream_t stream);
+
+/* out[b, k] = sum_{t in k} coeffs[t] prod_blk block_values[b, label_k, blk, block_m_indices[t, blk]].
+ * Device counterpart of evaluate_factorized_schedule_cpu
+ * (ye3t/core/csrc/factorized_runtime.cpp:426-548; evaluator core :251-285). */
+int ye3t_hip_evaluate_factorized_schedule(int dtype, const void* block_values, int64_t batch,
+                                          int64_t basis_count, int64_t block_count, int64_t magnetic_dim,
+                                          const int64_t* component_offsets,
+                                          const int64_t* component_label_index,
+                                          const int64_t* block_m_indices, const void* coeffs,
+                                          int64_t component_count, void* out, ye3t_stream_t stream);
+
+/* ---- Fused stage 2: compiled product plan (DAG of shared CG couplings) ---- */
+
+/* Host-side description of a compiled product plan (see ye3t_amd/ace/program.py).
+ * The plan is split into `chunk_count` programs; each produces a contiguous
+ * range of output columns from a [samples, a_width] density. */
+typedef struct {
+  int dtype;
+  int64_t a_width;              /* values per density row */
+  int64_t feature_count;        /* output columns */
+  int64_t chunk_count;
+  int64_t workspace_slots;      /* max slots of any chunk (LDS per wave = slots*65*elem) */
+  const int64_t* chunk_word_offsets;   /* host [chunk_count+1] into words */
+  const int64_t* chunk_coeff_offsets;  /* host [chunk_count+1] into coeffs */
+  const int64_t* chunk_out_offsets;    /* host [chunk_count+1] into out_slots */
+  const int64_t* chunk_first_column;   /* host [chunk_count] */
+  const uint32_t* words;        /* host program words */
+  int64_t word_count;
+  const void* coeffs;           /* host coefficients (dtype) */
+  int64_t coeff_count;
+  const uint16_t* out_slots;    /* host workspace slot of each output column, chunk-major */
+  int64_t out_slot_count;
+} ye3t_product_plan_desc;
+
+typedef struct ye3t_hip_product_plan ye3t_hip_product_plan;
+
+/* Copies the tables to the current device (synchronous). Counterpart of the
+ * reference's plan buffers (execution_plan.py:12918-13151). */
+int ye3t_hip_product_plan_create(const ye3t_product_plan_desc* desc, ye3t_hip_product_plan** out);
+void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* plan);
+
+/* B[samples, feature_count] from A[samples, a_width].  Replaces the CUDA
+ * factorized_angular forward (execution_plan_cuda.cu:6228-6358, launcher
+ * :11488-11672; schema execution_plan_torch.cpp:7586-7594) for ACE products. */
+int ye3t_hip_product_forward(const ye3t_hip_product_plan* plan, const void* A, int64_t samples, void* B,
+                             ye3t_stream_t stream);
+
+/* Kernel name/launch geometry of the last product_forward (for profiling). */
+int ye3t_hip_product_launch_info(const ye3t_hip_product_plan* plan, int64_t samples, int64_t* grid,
+                                 int64_t* block, int64_t* lds_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* YE3T_HIP_H */

@@ -1,0 +1,188 @@
+"""CPU oracle for the ACE hot path -- TEST INFRASTRUCTURE ONLY.
+
+Thin numpy/ctypes wrappers over ``liboracle.so`` (the C restatement in
+``ye3t_oracle.c``) and, where it has been built from the reference sources in
+this container, ``_ref/libye3t_ref.so`` (the reference's own CPU core).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg
+may import this package, and only as the checker / the timed CPU baseline.
+The product library (``ye3t_amd``) never imports it.
+
+Pinning status of each function is recorded in ``tests/test_oracle.py``.
+"""
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+_REF = None
+
+_d = ctypes.POINTER(ctypes.c_double)
+_i64 = ctypes.POINTER(ctypes.c_int64)
+_i32 = ctypes.POINTER(ctypes.c_int32)
+_I = ctypes.c_int64
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "liboracle.so")
+        if not os.path.exists(path):
+            build()
+        _LIB = ctypes.CDLL(path)
+        L = _LIB
+        L.oracle_radial_table.argtypes = [_d, _d, _d, _I, _I, _d, _d]
+        L.oracle_real_sph_table.argtypes = [_d, _I, _I, ctypes.c_double, _d, _d]
+        L.oracle_density_accumulate.argtypes = [_d, _i64, _I, _I, _I, _d]
+        L.oracle_ace_density.argtypes = [_I, _I, _i64, _i64, _d, _i32, _d, _d, _I, _I, _I,
+                                         ctypes.c_double, ctypes.c_double, ctypes.c_double, _d]
+        L.oracle_symmetric_power_monomial.argtypes = [_d, _I, _I, _i64, _i64, _d, _I, _d]
+        L.oracle_evaluate_componentwise.argtypes = [_d, _i64, _i64, _i64, _d, _d, _I, _I, _I, _I, _I]
+        L.oracle_ace_product_flat.argtypes = [_d, _I, _I, _I, _i64, _d, _i32, _I, _i64, _d, _i32, _d]
+        L.oracle_max_threads.restype = ctypes.c_int
+        L.oracle_set_threads.argtypes = [ctypes.c_int]
+    return _LIB
+
+
+def ref_lib():
+    """The reference's own CPU core built in ``_ref/`` (None if not built)."""
+    global _REF
+    if _REF is None:
+        path = os.path.join(_HERE, "_ref", "libye3t_ref.so")
+        if not os.path.exists(path):
+            return None
+        _REF = ctypes.CDLL(path)
+        _REF.ref_radial_table.argtypes = [_d, _d, _d, _I, _I, _d, _d]
+        _REF.ref_real_sph_table.argtypes = [_d, _I, _I, ctypes.c_double, _d, _d]
+        _REF.ref_density_accumulate.argtypes = [_d, _i64, _I, _I, _I, _d]
+        _REF.ref_symmetric_power_monomial.argtypes = [_d, _I, _I, _i64, _i64, _d, _I, _I, _d]
+    return _REF
+
+
+def _p(a, t=_d):
+    return a.ctypes.data_as(t)
+
+
+def _f64(a):
+    return np.ascontiguousarray(a, dtype=np.float64)
+
+
+def _i64a(a):
+    return np.ascontiguousarray(a, dtype=np.int64)
+
+
+def set_threads(n):
+    lib().oracle_set_threads(int(n))
+
+
+def max_threads():
+    return int(lib().oracle_max_threads())
+
+
+def radial_table(radii, cutoffs, lambdas, n_max, *, use_reference=False):
+    radii, cutoffs, lambdas = _f64(radii), _f64(cutoffs), _f64(lambdas)
+    E = radii.shape[0]
+    v = np.zeros((E, n_max + 1))
+    d = np.zeros((E, n_max + 1))
+    if use_reference:
+        ref_lib().ref_radial_table(_p(radii), _p(cutoffs), _p(lambdas), E, n_max, _p(v), _p(d))
+    else:
+        lib().oracle_radial_table(_p(radii), _p(cutoffs), _p(lambdas), E, n_max, _p(v), _p(d))
+    return v, d
+
+
+def real_sph_table(vectors, l_max, epsilon=1e-12, *, use_reference=False):
+    vectors = _f64(vectors).reshape(-1, 3)
+    E = vectors.shape[0]
+    w = (l_max + 1) ** 2
+    v = np.zeros((E, w))
+    g = np.zeros((E, w, 3))
+    if use_reference:
+        ref_lib().ref_real_sph_table(_p(vectors), E, l_max, epsilon, _p(v), _p(g))
+    else:
+        lib().oracle_real_sph_table(_p(vectors), E, l_max, epsilon, _p(v), _p(g))
+    return v, g
+
+
+def density_accumulate(edge_values, centers, atom_count, *, use_reference=False):
+    ev = _f64(edge_values)
+    E, C = ev.shape
+    centers = _i64a(centers)
+    out = np.zeros((atom_count, C))
+    f = ref_lib().ref_density_accumulate if use_reference else lib().oracle_density_accumulate
+    f(_p(ev), _p(centers, _i64), E, C, atom_count, _p(out))
+    return out
+
+
+def ace_density(inp):
+    """Stage-1 oracle on a workload dict (see ``ye3t_amd.ace.workloads``)."""
+    N, E = int(inp["atom_count"]), int(inp["edge_count"])
+    centers = _i64a(inp["centers"])
+    neighbors = _i64a(inp["neighbors"])
+    vec = _f64(inp["edge_vectors"])
+    species = inp.get("species")
+    feats = inp.get("node_features")
+    mix = inp.get("radial_mix")
+    C, n_max, l_max = int(inp["channel_count"]), int(inp["n_max"]), int(inp["l_max"])
+    rows = 1 if mix is not None else n_max + 1
+    out = np.zeros((N, C, rows, (l_max + 1) ** 2))
+    sp = np.ascontiguousarray(species, dtype=np.int32) if species is not None else None
+    fe = _f64(feats) if feats is not None else None
+    mx = _f64(mix) if mix is not None else None
+    lib().oracle_ace_density(N, E, _p(centers, _i64), _p(neighbors, _i64), _p(vec),
+                             _p(sp, _i32) if sp is not None else None,
+                             _p(fe) if fe is not None else None, _p(mx) if mx is not None else None,
+                             C, n_max, l_max, float(inp["cutoff"]), float(inp["lambda"]),
+                             float(inp.get("epsilon", 1e-12)), _p(out))
+    return out
+
+
+def symmetric_power_monomial(inp, monomial_counts, output_offsets, monomial_values, *, use_reference=False):
+    x = _f64(inp)
+    B, D = x.shape
+    counts = _i64a(monomial_counts)
+    offs = _i64a(output_offsets)
+    vals = _f64(monomial_values)
+    out_dim = offs.shape[0] - 1
+    out = np.zeros((B, out_dim))
+    if use_reference:
+        ref_lib().ref_symmetric_power_monomial(_p(x), B, D, _p(counts, _i64), _p(offs, _i64), _p(vals),
+                                               vals.shape[0], out_dim, _p(out))
+    else:
+        lib().oracle_symmetric_power_monomial(_p(x), B, D, _p(counts, _i64), _p(offs, _i64), _p(vals),
+                                              out_dim, _p(out))
+    return out
+
+
+def evaluate_componentwise(block_values, flat):
+    """``evaluate_factorized_schedule_cpu`` restatement on a schedule's flat arrays."""
+    bv = _f64(block_values)
+    B, basis, blocks, mdim = bv.shape
+    K = flat["component_offsets"].shape[0] - 1
+    out = np.zeros((B, K))
+    lib().oracle_evaluate_componentwise(
+        _p(bv), _p(_i64a(flat["component_offsets"]), _i64), _p(_i64a(flat["component_label_index"]), _i64),
+        _p(_i64a(flat["block_m_indices"]), _i64), _p(_f64(flat["coeffs"])), _p(out), B, basis, mdim, K, blocks)
+    return out
+
+
+def ace_product_flat(A, plan_arrays):
+    A = _f64(A)
+    S, W = A.shape
+    pa = plan_arrays
+    K = pa["column_offsets"].shape[0] - 1
+    out = np.zeros((S, K))
+    lib().oracle_ace_product_flat(
+        _p(A), S, W, int(pa["value_count"]), _p(_i64a(pa["value_offsets"]), _i64), _p(_f64(pa["value_coeffs"])),
+        _p(np.ascontiguousarray(pa["value_factors"], dtype=np.int32), _i32), K,
+        _p(_i64a(pa["column_offsets"]), _i64), _p(_f64(pa["term_coeffs"])),
+        _p(np.ascontiguousarray(pa["term_refs"], dtype=np.int32), _i32), _p(out))
+    return out

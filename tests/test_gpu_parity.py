@@ -1,0 +1,216 @@
+"""HIP kernels vs the CPU oracle on identical seeded inputs (needs an MI355X)."""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import TOL, column_rel_error, flush, rounded_inputs
+from ye3t_amd.ace import workloads as W
+from ye3t_amd.ace.pipeline import ACEPipeline, to_device_inputs
+from ye3t_amd.ace.plan import ProductPlan
+from ye3t_amd.runtime import native
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _t(x, dtype, dev):
+    import torch
+
+    return torch.as_tensor(np.asarray(x), dtype=torch.float64 if dtype == "f64" else torch.float32, device=dev)
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+def test_radial_table(gpu, dtype):
+    flush(f"radial_table {dtype}")
+    rng = np.random.default_rng(10)
+    E = 3001
+    r = rng.uniform(0, 6, E)
+    rc = rng.uniform(2, 5.5, E)
+    lam = rng.uniform(0.1, 2.0, E)
+    ref_in = [np.asarray(x, dtype=np.float32).astype(np.float64) if dtype == "f32" else x for x in (r, rc, lam)]
+    v_ref, d_ref = oracle.radial_table(*ref_in, 12)
+    v, d = native.radial_table(*(_t(x, dtype, gpu) for x in (r, rc, lam)), 12)
+    tol = 1e-12 if dtype == "f64" else 2e-5
+    assert column_rel_error(v.cpu().numpy(), v_ref) < tol
+    assert column_rel_error(d.cpu().numpy(), d_ref) < tol * 10
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+def test_real_sph_table(gpu, dtype):
+    flush(f"real_sph_table {dtype}")
+    rng = np.random.default_rng(11)
+    vec = rng.normal(size=(2049, 3)) * rng.uniform(0.5, 5, (2049, 1))
+    vec[5] = 0.0
+    ref_vec = np.asarray(vec, dtype=np.float32).astype(np.float64) if dtype == "f32" else vec
+    for lmax in (0, 3, 6, 8):
+        y_ref, g_ref = oracle.real_sph_table(ref_vec, lmax)
+        y, g = native.real_sph_table(_t(vec, dtype, gpu), lmax)
+        tol = 1e-12 if dtype == "f64" else 2e-5
+        assert column_rel_error(y.cpu().numpy(), y_ref) < tol, lmax
+        assert column_rel_error(g.cpu().numpy().reshape(len(vec), -1), g_ref.reshape(len(vec), -1)) < tol * 10
+
+
+def test_density_accumulate_unsorted(gpu):
+    flush("density_accumulate")
+    import torch
+
+    from ye3t_amd.runtime import density_accumulate
+
+    rng = np.random.default_rng(12)
+    E, C, N = 5000, 33, 700
+    ev = rng.normal(size=(E, C))
+    centers = rng.integers(0, N - 50, E)  # the last atoms get no edges
+    ref = oracle.density_accumulate(ev, centers, N)
+    got = density_accumulate(torch.as_tensor(ev, device=gpu), torch.as_tensor(centers, device=gpu), N)
+    assert column_rel_error(got.cpu().numpy(), ref) < 1e-12
+    with pytest.raises(RuntimeError, match="out of range"):
+        density_accumulate(torch.as_tensor(ev, device=gpu), torch.as_tensor(centers + 100, device=gpu), N)
+
+
+def _ragged_workload(dtype_mode):
+    """Atoms with 0, 1, 63, 64, 65 and 130 neighbours (empty rows and multi-tile rows)."""
+    rng = np.random.default_rng(13)
+    counts = np.array([0, 1, 63, 64, 65, 130, 0, 7])
+    N = len(counts)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    E = int(offsets[-1])
+    vec = rng.normal(size=(E, 3))
+    vec = vec / np.linalg.norm(vec, axis=1, keepdims=True) * rng.uniform(0.8, 5.0, (E, 1))
+    inp = {"atom_count": N, "edge_count": E, "centers": np.repeat(np.arange(N), counts), "row_offsets": offsets,
+           "neighbors": rng.integers(0, N, E), "edge_vectors": vec, "n_max": 8, "l_max": 4, "cutoff": 5.0,
+           "lambda": W.LAMBDA, "epsilon": 1e-12, "species": None, "node_features": None, "radial_mix": None}
+    if dtype_mode == "species":
+        inp.update(channel_count=3, species=rng.integers(0, 3, N).astype(np.int32))
+    elif dtype_mode == "features":
+        inp.update(channel_count=5, node_features=rng.normal(size=(N, 5)), radial_mix=rng.normal(size=(5, 9)) / 3)
+    else:
+        inp.update(channel_count=1)
+    return inp
+
+
+@pytest.mark.parametrize("mode", ["single", "species", "features"])
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+def test_ace_density_ragged(gpu, mode, dtype):
+    flush(f"ace_density ragged {mode} {dtype}")
+    inp = _ragged_workload(mode)
+    ref = oracle.ace_density(rounded_inputs(inp, dtype))
+    pipe_inp = to_device_inputs(inp, dtype, gpu)
+    A = native.ace_density_forward(
+        pipe_inp["edge_vectors"], pipe_inp["row_offsets"], pipe_inp["neighbors"], atom_count=inp["atom_count"],
+        channel_count=inp["channel_count"], n_max=inp["n_max"], l_max=inp["l_max"], cutoff=inp["cutoff"],
+        lam=inp["lambda"], species=pipe_inp.get("species"), node_features=pipe_inp.get("node_features"),
+        radial_mix=pipe_inp.get("radial_mix"))
+    got = A.cpu().numpy()
+    assert np.all(got[0] == 0) and np.all(got[6] == 0)
+    assert column_rel_error(got.reshape(inp["atom_count"], -1), ref.reshape(inp["atom_count"], -1)) < TOL[dtype]
+
+
+@pytest.mark.parametrize("cid,dtype", [(2, "f64"), (3, "f64"), (3, "f32"), (4, "f32"), (4, "f64"), (5, "f32")])
+def test_ace_density_configs(gpu, cid, dtype):
+    flush(f"ace_density config {cid} {dtype}")
+    cfg = W.config(cid, atom_count=300)
+    inp = cfg.density.generate()
+    ref = oracle.ace_density(rounded_inputs(inp, dtype))
+    dev = to_device_inputs(inp, dtype, gpu)
+    A = native.ace_density_forward(
+        dev["edge_vectors"], dev["row_offsets"], dev["neighbors"], atom_count=inp["atom_count"],
+        channel_count=inp["channel_count"], n_max=inp["n_max"], l_max=inp["l_max"], cutoff=inp["cutoff"],
+        lam=inp["lambda"], species=dev.get("species"), node_features=dev.get("node_features"),
+        radial_mix=dev.get("radial_mix"))
+    err = column_rel_error(A.cpu().numpy().reshape(300, -1), ref.reshape(300, -1))
+    flush(f"  err {err:.3e}")
+    assert err < TOL[dtype]
+
+
+def test_symmetric_monomial_golden_fixture_on_gpu(gpu):
+    import torch
+
+    fx = json.load(open(os.path.join(GOLDEN, "shared_monomial_plan_v1.json")))
+    D = int(fx["input_dimension"])
+    mono = np.array(fx["monomial_counts"], dtype=np.int64).reshape(-1, D)
+    terms = np.array(fx["coefficient_terms"], dtype=np.int64)
+    x = torch.as_tensor(np.array(fx["input"]).reshape(-1, D), device=gpu)
+    out = native.symmetric_power_monomial(x, mono[terms], np.array(fx["output_offsets"]),
+                                          torch.as_tensor(fx["coefficient_values"], dtype=torch.float64))
+    np.testing.assert_allclose(out.cpu().numpy().reshape(-1), fx["expected_output"], rtol=0, atol=5e-13)
+
+
+def test_config1_schedule_evaluation(gpu):
+    """Config 1: README sector on supplied factors through the compiled schedule."""
+    flush("config 1 schedule evaluation")
+    import torch
+
+    from ye3t_amd.core.symmetric_power import complex_monomial_entries
+    from ye3t_amd.couplings import compile_ace_factorized_schedules_by_L
+
+    a11, a20 = W.config1_factors()
+    rep = compile_ace_factorized_schedules_by_L(content=(1, 1, 2), input_Ls=(1, 1, 0))
+    x = torch.as_tensor(a11.reshape(-1, 3), device=gpu)
+    for L, sched in rep.schedules_by_L.items():
+        spec = sched.block_specs[0][0]
+        rows = complex_monomial_entries(2, 1, spec["Lambda"], 0)
+        counts = np.array([r[1] for r in rows], dtype=np.int64)
+        outs = np.array([r[0] for r in rows])
+        order = np.argsort(outs, kind="stable")
+        offs = np.searchsorted(outs[order], np.arange(2 * spec["Lambda"] + 2))
+        vals = torch.as_tensor(np.array([r[2] for r in rows])[order])
+        sym = native.symmetric_power_monomial(x, counts[order], offs, vals)
+        sym_ref = oracle.symmetric_power_monomial(a11.reshape(-1, 3), counts[order], offs, vals.numpy())
+        assert column_rel_error(sym.cpu().numpy(), sym_ref) < 1e-12
+        mdim = sched.flat_arrays()["max_block_m_dim"]
+        bv = torch.zeros((x.shape[0], 1, 2, mdim), dtype=torch.float64, device=gpu)
+        bv[:, 0, 0, :sym.shape[1]] = sym
+        bv[:, 0, 1, 0] = torch.as_tensor(a20.reshape(-1), device=gpu)
+        got = rep.evaluate(bv, target_L=L).cpu().numpy()
+        ref = oracle.evaluate_componentwise(bv.cpu().numpy(), sched.flat_arrays())
+        assert got.shape == (32768, 2 * L + 1)
+        assert column_rel_error(got, ref) < 1e-12
+
+
+def _species_rank4_spec():
+    from ye3t_amd.ace.plan import ACEFeatureSpec
+
+    # config-3 shaped (species-folded channels, l<=4, rank up to 4) at a test-sized truncation
+    return ACEFeatureSpec(channel_count=44, l_max=4, nu_max=4, targets=(0,), parity="even",
+                          radial_per_species=11, caps={1: (11, 0), 2: (3, 4), 3: (2, 2), 4: (1, 2)})
+
+
+@pytest.mark.parametrize("cid,dtype,samples,max_slots", [
+    (4, "f32", 1000, None), (4, "f64", 333, None), (4, "f32", 63, 250), (4, "f32", 130, 48),
+    (2, "f64", 200, None), (3, "f32", 100, None), (3, "f64", 70, None)])
+def test_product_kernel_vs_flat_oracle(gpu, cid, dtype, samples, max_slots):
+    flush(f"product config {cid} {dtype} samples={samples} slots={max_slots}")
+    import torch
+
+    spec = _species_rank4_spec() if cid == 3 else W.config(cid).feature_spec
+    pipe = ACEPipeline(spec, dtype, max_slots)
+    A = np.random.default_rng(14).normal(size=(samples, pipe.plan.a_width))
+    A_dev = _t(A, dtype, gpu)
+    B = pipe.product(A_dev).cpu().numpy()
+    ref = oracle.ace_product_flat(A_dev.double().cpu().numpy(), pipe.plan.flat_arrays())
+    err = column_rel_error(B, ref)
+    flush(f"  err {err:.3e}")
+    assert err < TOL[dtype]
+    # determinism: bit-identical on a second run
+    assert np.array_equal(B, pipe.product(A_dev).cpu().numpy())
+
+
+@pytest.mark.parametrize("cid,dtype", [(4, "f32"), (2, "f64")])
+def test_end_to_end_small(gpu, cid, dtype):
+    flush(f"end to end config {cid} {dtype}")
+    cfg = W.config(cid, atom_count=257)
+    inp = cfg.density.generate()
+    pipe = ACEPipeline(cfg.feature_spec, dtype)
+    A, B = pipe.forward(to_device_inputs(inp, dtype, gpu), channelwise=cfg.channelwise)
+    A_ref = oracle.ace_density(rounded_inputs(inp, dtype))
+    assert column_rel_error(A.cpu().numpy().reshape(257, -1), A_ref.reshape(257, -1)) < TOL[dtype]
+    rows = A_ref.reshape(-1, pipe.plan.a_width)
+    B_ref = oracle.ace_product_flat(rows, pipe.plan.flat_arrays())
+    err = column_rel_error(B.cpu().numpy(), B_ref)
+    flush(f"  err {err:.3e}")
+    assert err < TOL[dtype]

@@ -1,0 +1,62 @@
+"""End-to-end ACE hot path on one GPU: density (stage 1) then B-features (stage 2).
+
+``ACEPipeline`` owns a compiled :class:`~ye3t_amd.ace.plan.ProductPlan`, its
+device program, and the stage-1 parameters.  Inputs stay resident in HBM;
+``forward`` launches exactly two kernels on the current stream.
+"""
+
+import numpy as np
+
+from ye3t_amd.ace.plan import ProductPlan
+from ye3t_amd.ace.program import compile_program
+from ye3t_amd.runtime import native
+
+
+def to_device_inputs(inp, dtype, device="cuda"):
+    """Move a workload dict (``workloads.DensityWorkload.generate``) to the GPU."""
+    import torch
+
+    real = torch.float64 if dtype == "f64" else torch.float32
+    out = {k: v for k, v in inp.items() if not isinstance(v, np.ndarray)}
+    out["row_offsets"] = torch.as_tensor(inp["row_offsets"], dtype=torch.int64, device=device)
+    out["neighbors"] = torch.as_tensor(inp["neighbors"], dtype=torch.int64, device=device)
+    out["edge_vectors"] = torch.as_tensor(inp["edge_vectors"], dtype=real, device=device).contiguous()
+    for key in ("species",):
+        if inp.get(key) is not None:
+            out[key] = torch.as_tensor(inp[key], dtype=torch.int32, device=device)
+    for key in ("node_features", "radial_mix"):
+        if inp.get(key) is not None:
+            out[key] = torch.as_tensor(inp[key], dtype=real, device=device).contiguous()
+    return out
+
+
+class ACEPipeline:
+    def __init__(self, feature_spec, dtype="f32", max_slots=None, plan=None):
+        self.spec = feature_spec
+        self.dtype = dtype
+        self.plan = plan if plan is not None else ProductPlan(feature_spec)
+        self.program = compile_program(self.plan, dtype, max_slots)
+        self.handle = native.ProductPlanHandle(self.program)
+
+    @property
+    def feature_count(self):
+        return self.plan.feature_count
+
+    def density(self, dev_inp, out=None):
+        return native.ace_density_forward(
+            dev_inp["edge_vectors"], dev_inp["row_offsets"], dev_inp["neighbors"],
+            atom_count=int(dev_inp["atom_count"]), channel_count=int(dev_inp["channel_count"]),
+            n_max=int(dev_inp["n_max"]), l_max=int(dev_inp["l_max"]), cutoff=float(dev_inp["cutoff"]),
+            lam=float(dev_inp["lambda"]), epsilon=float(dev_inp.get("epsilon", 1e-12)),
+            species=dev_inp.get("species"), node_features=dev_inp.get("node_features"),
+            radial_mix=dev_inp.get("radial_mix"), out=out)
+
+    def product(self, A_rows, out=None):
+        return self.handle.forward(A_rows, out=out)
+
+    def forward(self, dev_inp, channelwise=False, A_out=None, B_out=None):
+        A = self.density(dev_inp, out=A_out)
+        rows = A.reshape(-1, self.plan.a_width) if channelwise else A.reshape(A.shape[0], -1)
+        if rows.shape[1] != self.plan.a_width:
+            raise ValueError(f"density row width {rows.shape[1]} != plan width {self.plan.a_width}")
+        return A, self.product(rows, out=B_out)

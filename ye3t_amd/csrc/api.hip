@@ -1,0 +1,279 @@
+// ye3t_hip: library bookkeeping (errors, ABI, device caps, SH normalisation)
+// and the standalone per-edge tables (radial, real SH) and CSR density scatter.
+#include <cmath>
+#include <mutex>
+
+#include "common.h"
+#include "sph.h"
+
+namespace ye3t {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+const NormTable& norm_table() {
+  static NormTable table;
+  static std::once_flag once;
+  std::call_once(once, [] {
+    for (int l = 0; l <= kMaxL; ++l) {
+      for (int m = 0; m <= kMaxL; ++m) {
+        double v = 0.0;
+        if (m <= l) {
+          // (2l+1)/(4 pi) * (l-m)!/(l+m)!  computed as a product of reciprocals
+          double ratio = 1.0;
+          for (int k = l - m + 1; k <= l + m; ++k) ratio /= double(k);
+          v = std::sqrt((2.0 * l + 1.0) / (4.0 * M_PI) * ratio);
+        }
+        table.v[l * (kMaxL + 1) + m] = v;
+      }
+    }
+  });
+  return table;
+}
+
+// ---------------------------------------------------------------------------
+// Radial table: one thread per edge, one Chebyshev pass over n.
+template <typename Real>
+__global__ __launch_bounds__(256) void radial_table_kernel(const Real* __restrict__ radii,
+                                                           const Real* __restrict__ cutoffs,
+                                                           const Real* __restrict__ lambdas, int64_t E,
+                                                           int n_max, Real* __restrict__ values,
+                                                           Real* __restrict__ derivs) {
+  Real v[16], d[16];
+  for (int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < E; e += int64_t(gridDim.x) * blockDim.x) {
+    if (derivs) {
+      cheb_exp_cos_row<Real, true>(radii[e], cutoffs[e], lambdas[e], n_max, v, d);
+      for (int n = 0; n <= n_max; ++n) {
+        values[e * (n_max + 1) + n] = v[n];
+        derivs[e * (n_max + 1) + n] = d[n];
+      }
+    } else {
+      cheb_exp_cos_row<Real, false>(radii[e], cutoffs[e], lambdas[e], n_max, v, d);
+      for (int n = 0; n <= n_max; ++n) values[e * (n_max + 1) + n] = v[n];
+    }
+  }
+}
+
+// Real SH table with optional Cartesian gradient.  Gradients w.r.t. the unit
+// vector use d/dz Q_l^m = Q_l^{m+1}, projected with (I - u u^T)/|r|
+// (reference ye3t_runtime_core.cpp:226-286, 808-843).
+template <typename Real>
+__global__ __launch_bounds__(128) void real_sph_table_kernel(const Real* __restrict__ vec, int64_t E, int lmax,
+                                                             Real eps, NormTable nt, Real* __restrict__ values,
+                                                             Real* __restrict__ grads) {
+  const int width = (lmax + 1) * (lmax + 1);
+  const Real sqrt2 = Real(1.4142135623730950488016887242096981);
+  for (int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < E; e += int64_t(gridDim.x) * blockDim.x) {
+    const Real x0 = vec[3 * e], y0 = vec[3 * e + 1], z0 = vec[3 * e + 2];
+    const Real r = d_sqrt(x0 * x0 + y0 * y0 + z0 * z0);
+    const Real sr = r > eps ? r : eps;
+    const Real u[3] = {x0 / sr, y0 / sr, z0 / sr};
+    Real* row = values + e * width;
+    if (!grads) {
+      real_sph_row<Real>(u[0], u[1], u[2], lmax, nt, row, 1);
+      continue;
+    }
+    // Q[l][m] for m <= l+1 (Q_l^{l+1} = 0)
+    Real Q[kMaxL + 2][kMaxL + 2];
+    Real qmm = Real(1);
+    for (int m = 0; m <= lmax + 1; ++m) {
+      if (m > 0) qmm *= Real(2 * m - 1);
+      Real q2 = Real(0), q1 = Real(0);
+      for (int l = 0; l <= lmax; ++l) {
+        Real q;
+        if (l < m) {
+          q = Real(0);
+        } else if (l == m) {
+          q = qmm;
+        } else if (l == m + 1) {
+          q = Real(2 * m + 1) * u[2] * qmm;
+        } else {
+          q = (Real(2 * l - 1) * u[2] * q1 - Real(l + m - 1) * q2) / Real(l - m);
+        }
+        if (l >= m) {
+          q2 = q1;
+          q1 = q;
+        }
+        Q[l][m] = q;
+      }
+    }
+    Real cr = Real(1), ci = Real(0), pr = Real(1), pi = Real(0);
+    for (int m = 0; m <= lmax; ++m) {
+      if (m > 0) {
+        pr = cr;
+        pi = ci;
+        const Real nr = cr * u[0] - ci * u[1];
+        const Real ni = cr * u[1] + ci * u[0];
+        cr = nr;
+        ci = ni;
+      }
+      for (int l = m; l <= lmax; ++l) {
+        const Real n = Real(nt.v[l * (kMaxL + 1) + m]);
+        const int base = l * l + l;
+        Real ug[2][3];
+        int idx[2];
+        int count;
+        if (m == 0) {
+          row[base] = n * Q[l][0];
+          ug[0][0] = Real(0);
+          ug[0][1] = Real(0);
+          ug[0][2] = n * Q[l][1];
+          idx[0] = base;
+          count = 1;
+        } else {
+          const Real s = sqrt2 * n;
+          const Real q = Q[l][m], qz = Q[l][m + 1];
+          row[base + m] = s * q * cr;
+          row[base - m] = -s * q * ci;
+          ug[0][0] = s * q * (Real(m) * pr);
+          ug[0][1] = s * q * (-Real(m) * pi);
+          ug[0][2] = s * qz * cr;
+          ug[1][0] = -s * q * (Real(m) * pi);
+          ug[1][1] = -s * q * (Real(m) * pr);
+          ug[1][2] = -s * qz * ci;
+          idx[0] = base + m;
+          idx[1] = base - m;
+          count = 2;
+        }
+        for (int c = 0; c < count; ++c) {
+          for (int a = 0; a < 3; ++a) {
+            Real g = Real(0);
+            for (int b = 0; b < 3; ++b) {
+              Real jac;
+              if (r > eps) {
+                jac = ((a == b ? Real(1) : Real(0)) - u[a] * u[b]) / sr;
+              } else {
+                jac = (a == b) ? Real(1) / sr : Real(0);
+              }
+              g += ug[c][b] * jac;
+            }
+            grads[(e * width + idx[c]) * 3 + a] = g;
+          }
+        }
+      }
+    }
+  }
+}
+
+// CSR segment reduction: thread per (atom, channel), edges summed in order.
+template <typename Real>
+__global__ __launch_bounds__(256) void density_csr_kernel(const Real* __restrict__ ev,
+                                                          const int64_t* __restrict__ offsets, int64_t N,
+                                                          int64_t C, Real* __restrict__ out) {
+  const int64_t total = N * C;
+  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t i = idx / C, c = idx - (idx / C) * C;
+    Real acc = Real(0);
+    for (int64_t e = offsets[i]; e < offsets[i + 1]; ++e) acc += ev[e * C + c];
+    out[idx] = acc;
+  }
+}
+
+inline unsigned grid_for(int64_t work, int threads) {
+  int64_t g = (work + threads - 1) / threads;
+  if (g < 1) g = 1;
+  if (g > (1 << 20)) g = 1 << 20;
+  return unsigned(g);
+}
+
+}  // namespace ye3t
+
+using namespace ye3t;
+
+extern "C" {
+
+int ye3t_hip_abi_version(void) { return YE3T_HIP_ABI_VERSION; }
+
+const char* ye3t_hip_last_error(void) { return g_last_error.c_str(); }
+
+int ye3t_hip_device_caps(int device, ye3t_hip_caps* out) {
+  YE3T_REQUIRE(out != nullptr, "caps output is NULL");
+  hipDeviceProp_t prop;
+  YE3T_CHECK_HIP(hipGetDeviceProperties(&prop, device));
+  std::snprintf(out->arch, sizeof out->arch, "%s", prop.gcnArchName);
+  out->device = device;
+  out->cu_count = prop.multiProcessorCount;
+  out->wavefront_size = prop.warpSize;
+  out->lds_bytes_per_block = int(prop.sharedMemPerBlock);
+  out->clock_khz = prop.clockRate;
+  out->hbm_bytes = int64_t(prop.totalGlobalMem);
+  out->hbm_peak_gbs = 8000.0;  // MI355X nominal HBM3E peak
+  return YE3T_OK;
+}
+
+int ye3t_hip_radial_table(int dtype, const void* radii, const void* cutoffs, const void* lambdas, int64_t E,
+                          int64_t n_max, void* values, void* derivs, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(E >= 0, "edge_count must be non-negative");
+  YE3T_REQUIRE(n_max >= 0 && n_max < 16, "max_radial_index must be in [0, 15], got %lld", (long long)n_max);
+  if (E == 0) return YE3T_OK;
+  YE3T_REQUIRE(radii && cutoffs && lambdas && values, "NULL input or output");
+  const unsigned grid = grid_for(E, 256);
+  if (dtype == YE3T_F64) {
+    hipLaunchKernelGGL(radial_table_kernel<double>, dim3(grid), dim3(256), 0, as_stream(stream),
+                       (const double*)radii, (const double*)cutoffs, (const double*)lambdas, E, int(n_max),
+                       (double*)values, (double*)derivs);
+  } else if (dtype == YE3T_F32) {
+    hipLaunchKernelGGL(radial_table_kernel<float>, dim3(grid), dim3(256), 0, as_stream(stream),
+                       (const float*)radii, (const float*)cutoffs, (const float*)lambdas, E, int(n_max),
+                       (float*)values, (float*)derivs);
+  } else {
+    return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);
+  }
+  return check_launch("radial_table_kernel");
+}
+
+int ye3t_hip_real_sph_table(int dtype, const void* vec, int64_t E, int64_t lmax, double eps, void* values,
+                            void* grads, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(E >= 0, "edge_count must be non-negative");
+  YE3T_REQUIRE(lmax >= 0 && lmax <= kMaxL, "maximum_angular_momentum must be in [0, %d]", kMaxL);
+  if (E == 0) return YE3T_OK;
+  YE3T_REQUIRE(vec && values, "NULL input or output");
+  const unsigned grid = grid_for(E, 128);
+  if (dtype == YE3T_F64) {
+    hipLaunchKernelGGL(real_sph_table_kernel<double>, dim3(grid), dim3(128), 0, as_stream(stream),
+                       (const double*)vec, E, int(lmax), eps, norm_table(), (double*)values, (double*)grads);
+  } else if (dtype == YE3T_F32) {
+    hipLaunchKernelGGL(real_sph_table_kernel<float>, dim3(grid), dim3(128), 0, as_stream(stream),
+                       (const float*)vec, E, int(lmax), float(eps), norm_table(), (float*)values, (float*)grads);
+  } else {
+    return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);
+  }
+  return check_launch("real_sph_table_kernel");
+}
+
+int ye3t_hip_density_accumulate_csr(int dtype, const void* ev, const int64_t* offsets, int64_t N, int64_t C,
+                                    void* out, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(N >= 0 && C >= 0, "negative size");
+  if (N * C == 0) return YE3T_OK;
+  YE3T_REQUIRE(offsets && out, "NULL offsets or output");
+  const unsigned grid = grid_for(N * C, 256);
+  if (dtype == YE3T_F64) {
+    hipLaunchKernelGGL(density_csr_kernel<double>, dim3(grid), dim3(256), 0, as_stream(stream),
+                       (const double*)ev, offsets, N, C, (double*)out);
+  } else if (dtype == YE3T_F32) {
+    hipLaunchKernelGGL(density_csr_kernel<float>, dim3(grid), dim3(256), 0, as_stream(stream),
+                       (const float*)ev, offsets, N, C, (float*)out);
+  } else {
+    return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);
+  }
+  return check_launch("density_csr_kernel");
+}
+
+}  // extern "C"

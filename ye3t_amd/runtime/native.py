@@ -1,0 +1,321 @@
+"""ctypes binding of the in-tree HIP library ``libye3t_hip.so`` (C ABI: ``include/ye3t_hip.h``).
+
+Torch provides device memory and the current stream; every entry point takes
+raw device pointers.  There is no CPU fallback here: if the library is missing
+or a call fails, a ``RuntimeError`` carrying the library's message is raised.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+_PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
+ABI_VERSION = 43
+_LIB = None
+
+F32, F64 = 0, 1
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+
+
+class DensityArgs(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int), ("atom_count", _i64), ("edge_count", _i64),
+                ("row_offsets", _vp), ("neighbors", _vp), ("edge_vectors", _vp), ("species", _vp),
+                ("node_features", _vp), ("radial_mix", _vp), ("channel_count", _i64),
+                ("max_radial_index", _i64), ("max_angular", _i64), ("cutoff", ctypes.c_double),
+                ("lambda_", ctypes.c_double), ("epsilon", ctypes.c_double)]
+
+
+class ProductPlanDesc(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int), ("a_width", _i64), ("feature_count", _i64), ("chunk_count", _i64),
+                ("workspace_slots", _i64), ("chunk_word_offsets", _vp), ("chunk_coeff_offsets", _vp),
+                ("chunk_out_offsets", _vp), ("chunk_first_column", _vp), ("words", _vp), ("word_count", _i64),
+                ("coeffs", _vp), ("coeff_count", _i64), ("out_slots", _vp), ("out_slot_count", _i64)]
+
+
+class Caps(ctypes.Structure):
+    _fields_ = [("arch", ctypes.c_char * 64), ("device", ctypes.c_int), ("cu_count", ctypes.c_int),
+                ("wavefront_size", ctypes.c_int), ("lds_bytes_per_block", ctypes.c_int),
+                ("clock_khz", ctypes.c_int), ("hbm_bytes", _i64), ("hbm_peak_gbs", ctypes.c_double)]
+
+
+def library_path():
+    return LIB_PATH
+
+
+def available():
+    return os.path.exists(LIB_PATH)
+
+
+def lib():
+    """Load the HIP library; raises if it has not been built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"ye3t_amd HIP library not built: {LIB_PATH} is missing (run __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    L.ye3t_hip_abi_version.restype = ctypes.c_int
+    L.ye3t_hip_last_error.restype = ctypes.c_char_p
+    L.ye3t_hip_device_caps.argtypes = [ctypes.c_int, ctypes.POINTER(Caps)]
+    L.ye3t_hip_radial_table.argtypes = [ctypes.c_int, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp]
+    L.ye3t_hip_real_sph_table.argtypes = [ctypes.c_int, _vp, _i64, _i64, ctypes.c_double, _vp, _vp, _vp]
+    L.ye3t_hip_density_accumulate_csr.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _vp]
+    L.ye3t_hip_ace_density_forward.argtypes = [ctypes.POINTER(DensityArgs), _vp, _vp]
+    L.ye3t_hip_symmetric_power_monomial.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp]
+    L.ye3t_hip_evaluate_factorized_schedule.argtypes = [ctypes.c_int, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp,
+                                                        _vp, _i64, _vp, _vp]
+    L.ye3t_hip_product_plan_create.argtypes = [ctypes.POINTER(ProductPlanDesc), ctypes.POINTER(_vp)]
+    L.ye3t_hip_product_plan_destroy.argtypes = [_vp]
+    L.ye3t_hip_product_plan_destroy.restype = None
+    L.ye3t_hip_product_forward.argtypes = [_vp, _vp, _i64, _vp, _vp]
+    L.ye3t_hip_product_launch_info.argtypes = [_vp, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                                               ctypes.POINTER(_i64)]
+    version = L.ye3t_hip_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"ye3t_hip ABI {version} does not match the bindings ({ABI_VERSION})")
+    _LIB = L
+    return L
+
+
+EXPORTED_SYMBOLS = (
+    "ye3t_hip_abi_version", "ye3t_hip_last_error", "ye3t_hip_device_caps", "ye3t_hip_radial_table",
+    "ye3t_hip_real_sph_table", "ye3t_hip_density_accumulate_csr", "ye3t_hip_ace_density_forward",
+    "ye3t_hip_symmetric_power_monomial", "ye3t_hip_evaluate_factorized_schedule",
+    "ye3t_hip_product_plan_create", "ye3t_hip_product_plan_destroy", "ye3t_hip_product_forward",
+    "ye3t_hip_product_launch_info",
+)
+
+
+def _check(rc, what):
+    if rc != 0:
+        msg = lib().ye3t_hip_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def _dtype_code(t):
+    import torch
+
+    if t.dtype == torch.float64:
+        return F64
+    if t.dtype == torch.float32:
+        return F32
+    raise TypeError(f"unsupported dtype {t.dtype}; expected float32 or float64")
+
+
+def _stream():
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(t, name):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _opt(t, name):
+    return None if t is None else _dev(t, name)
+
+
+def device_caps(device=0):
+    caps = Caps()
+    _check(lib().ye3t_hip_device_caps(int(device), ctypes.byref(caps)), "ye3t_hip_device_caps")
+    return {"arch": caps.arch.decode(), "device": caps.device, "cu_count": caps.cu_count,
+            "wavefront_size": caps.wavefront_size, "lds_bytes_per_block": caps.lds_bytes_per_block,
+            "clock_khz": caps.clock_khz, "hbm_bytes": int(caps.hbm_bytes), "hbm_peak_gbs": caps.hbm_peak_gbs}
+
+
+def radial_table(radii, cutoffs, lambdas, n_max, with_derivative=True):
+    import torch
+
+    E = int(radii.shape[0])
+    for t, n in ((radii, "radii"), (cutoffs, "cutoffs"), (lambdas, "lambdas")):
+        if t.shape != (E,) or t.dtype != radii.dtype:
+            raise ValueError(f"{n} must be a [{E}] tensor of dtype {radii.dtype}")
+    values = torch.empty((E, n_max + 1), dtype=radii.dtype, device=radii.device)
+    derivs = torch.empty_like(values) if with_derivative else None
+    _check(lib().ye3t_hip_radial_table(_dtype_code(radii), _dev(radii, "radii"), _dev(cutoffs, "cutoffs"),
+                                       _dev(lambdas, "lambdas"), E, int(n_max), _dev(values, "values"),
+                                       _opt(derivs, "derivatives"), _stream()), "ye3t_hip_radial_table")
+    return values, derivs
+
+
+def real_sph_table(vectors, l_max, epsilon=1e-12, with_gradient=True):
+    import torch
+
+    if vectors.ndim != 2 or vectors.shape[1] != 3:
+        raise ValueError("edge_vectors must have shape [E, 3]")
+    E = int(vectors.shape[0])
+    width = (l_max + 1) ** 2
+    values = torch.empty((E, width), dtype=vectors.dtype, device=vectors.device)
+    grads = torch.empty((E, width, 3), dtype=vectors.dtype, device=vectors.device) if with_gradient else None
+    _check(lib().ye3t_hip_real_sph_table(_dtype_code(vectors), _dev(vectors, "edge_vectors"), E, int(l_max),
+                                         float(epsilon), _dev(values, "values"), _opt(grads, "gradients"),
+                                         _stream()), "ye3t_hip_real_sph_table")
+    return values, grads
+
+
+def density_accumulate_csr(edge_values, row_offsets, atom_count):
+    import torch
+
+    if edge_values.ndim != 2:
+        raise ValueError("edge_values must be [E, C]")
+    if row_offsets.dtype != torch.int64 or row_offsets.shape != (atom_count + 1,):
+        raise ValueError("row_offsets must be int64 [N+1]")
+    C = int(edge_values.shape[1])
+    out = torch.empty((atom_count, C), dtype=edge_values.dtype, device=edge_values.device)
+    _check(lib().ye3t_hip_density_accumulate_csr(_dtype_code(edge_values), _dev(edge_values, "edge_values"),
+                                                 _dev(row_offsets, "row_offsets"), int(atom_count), C,
+                                                 _dev(out, "out"), _stream()), "ye3t_hip_density_accumulate_csr")
+    return out
+
+
+def ace_density_forward(edge_vectors, row_offsets, neighbors, *, atom_count, channel_count, n_max, l_max, cutoff,
+                        lam, epsilon=1e-12, species=None, node_features=None, radial_mix=None, out=None):
+    """Fused stage 1; returns ``A[N, C, R, (l_max+1)^2]``."""
+    import torch
+
+    rows = 1 if radial_mix is not None else n_max + 1
+    shape = (atom_count, channel_count, rows, (l_max + 1) ** 2)
+    if out is None:
+        out = torch.empty(shape, dtype=edge_vectors.dtype, device=edge_vectors.device)
+    elif tuple(out.shape) != shape or out.dtype != edge_vectors.dtype:
+        raise ValueError(f"out must be {shape} of dtype {edge_vectors.dtype}")
+    if row_offsets.dtype != torch.int64 or row_offsets.shape != (atom_count + 1,):
+        raise ValueError("row_offsets must be int64 [N+1]")
+    if neighbors is not None and neighbors.dtype != torch.int64:
+        raise ValueError("neighbors must be int64")
+    if species is not None and species.dtype != torch.int32:
+        raise ValueError("species must be int32")
+    for t, n in ((node_features, "node_features"), (radial_mix, "radial_mix")):
+        if t is not None and t.dtype != edge_vectors.dtype:
+            raise ValueError(f"{n} must have dtype {edge_vectors.dtype}")
+    args = DensityArgs(
+        dtype=_dtype_code(edge_vectors), atom_count=int(atom_count), edge_count=int(edge_vectors.shape[0]),
+        row_offsets=_dev(row_offsets, "row_offsets"), neighbors=_opt(neighbors, "neighbors"),
+        edge_vectors=_dev(edge_vectors, "edge_vectors"), species=_opt(species, "species"),
+        node_features=_opt(node_features, "node_features"), radial_mix=_opt(radial_mix, "radial_mix"),
+        channel_count=int(channel_count), max_radial_index=int(n_max), max_angular=int(l_max),
+        cutoff=float(cutoff), lambda_=float(lam), epsilon=float(epsilon))
+    _check(lib().ye3t_hip_ace_density_forward(ctypes.byref(args), _dev(out, "A"), _stream()),
+           "ye3t_hip_ace_density_forward")
+    return out
+
+
+def symmetric_power_monomial(x, monomial_counts, output_offsets, monomial_values):
+    import torch
+
+    B, D = (int(s) for s in x.shape)
+    T = int(monomial_values.shape[0])
+    counts = np.asarray(monomial_counts.cpu() if hasattr(monomial_counts, "cpu") else monomial_counts)
+    offs = np.asarray(output_offsets.cpu() if hasattr(output_offsets, "cpu") else output_offsets)
+    if counts.shape != (T, D) or offs.ndim != 1 or offs[0] != 0 or offs[-1] != T or np.any(np.diff(offs) < 0):
+        raise ValueError("invalid monomial table")
+    if np.any(counts < 0):
+        raise ValueError("negative monomial exponent")
+    O = int(offs.shape[0] - 1)
+    out = torch.empty((B, O), dtype=x.dtype, device=x.device)
+    dc = torch.as_tensor(counts, dtype=torch.int64, device=x.device).contiguous()
+    do = torch.as_tensor(offs, dtype=torch.int64, device=x.device).contiguous()
+    dv = monomial_values.to(device=x.device, dtype=x.dtype).contiguous()
+    _check(lib().ye3t_hip_symmetric_power_monomial(_dtype_code(x), _dev(x, "input"), B, D, _dev(dc, "counts"),
+                                                   _dev(do, "offsets"), _dev(dv, "values"), O, _dev(out, "out"),
+                                                   _stream()), "ye3t_hip_symmetric_power_monomial")
+    return out
+
+
+def evaluate_factorized_schedule(block_values, schedule):
+    """Device evaluation of a :class:`FactorizedCoefficientSchedule` (validated on the host)."""
+    import torch
+
+    flat = schedule.flat_arrays()
+    bv = block_values.contiguous()
+    B, basis, blocks, mdim = (int(s) for s in bv.shape)
+    K = schedule.component_count
+    offs, labels, midx = flat["component_offsets"], flat["component_label_index"], flat["block_m_indices"]
+    T = int(flat["coeffs"].shape[0])
+    if offs.shape != (K + 1,) or offs[0] != 0 or offs[-1] != T or np.any(np.diff(offs) < 0):
+        raise ValueError("component_offsets are inconsistent")
+    if labels.size and (labels.min() < 0 or labels.max() >= basis):
+        raise ValueError("component_label_index out of range")
+    if midx.size and (midx.min() < 0 or midx.max() >= mdim):
+        raise ValueError("block_m_indices out of range")
+    if midx.shape != (T, blocks):
+        raise ValueError("block_m_indices shape mismatch")
+    dev = bv.device
+    out = torch.empty((B, K), dtype=bv.dtype, device=dev)
+    t_offs = torch.as_tensor(offs, device=dev)
+    t_lab = torch.as_tensor(labels, device=dev)
+    t_m = torch.as_tensor(midx, device=dev).contiguous()
+    t_c = torch.as_tensor(flat["coeffs"], dtype=bv.dtype, device=dev)
+    _check(lib().ye3t_hip_evaluate_factorized_schedule(
+        _dtype_code(bv), _dev(bv, "block_values"), B, basis, blocks, mdim, _dev(t_offs, "offsets"),
+        _dev(t_lab, "labels"), _dev(t_m, "m_indices") if T else None, _dev(t_c, "coeffs") if T else None, K,
+        _dev(out, "out"), _stream()), "ye3t_hip_evaluate_factorized_schedule")
+    return out
+
+
+class ProductPlanHandle:
+    """Device-resident compiled product program (owns a ``ye3t_hip_product_plan``)."""
+
+    def __init__(self, program):
+        self.program = program
+        self.dtype = program["dtype"]
+        self._keep = {k: np.ascontiguousarray(v) for k, v in program.items() if isinstance(v, np.ndarray)}
+        k = self._keep
+
+        def ptr(name):
+            return ctypes.c_void_p(k[name].ctypes.data) if k[name].size else None
+
+        desc = ProductPlanDesc(
+            dtype=F64 if self.dtype == "f64" else F32, a_width=program["a_width"],
+            feature_count=program["feature_count"], chunk_count=program["chunk_count"],
+            workspace_slots=program["workspace_slots"], chunk_word_offsets=ptr("chunk_word_offsets"),
+            chunk_coeff_offsets=ptr("chunk_coeff_offsets"), chunk_out_offsets=ptr("chunk_out_offsets"),
+            chunk_first_column=ptr("chunk_first_column"), words=ptr("words"), word_count=int(k["words"].size),
+            coeffs=ptr("coeffs"), coeff_count=int(k["coeffs"].size), out_slots=ptr("out_slots"),
+            out_slot_count=int(k["out_slots"].size))
+        handle = ctypes.c_void_p()
+        _check(lib().ye3t_hip_product_plan_create(ctypes.byref(desc), ctypes.byref(handle)),
+               "ye3t_hip_product_plan_create")
+        self._handle = handle
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h is not None and h.value and _LIB is not None:
+            _LIB.ye3t_hip_product_plan_destroy(h)
+            self._handle = None
+
+    @property
+    def feature_count(self):
+        return int(self.program["feature_count"])
+
+    def launch_info(self, samples):
+        g, b, l = _i64(), _i64(), _i64()
+        _check(lib().ye3t_hip_product_launch_info(self._handle, int(samples), ctypes.byref(g), ctypes.byref(b),
+                                                  ctypes.byref(l)), "ye3t_hip_product_launch_info")
+        return {"grid": g.value, "block": b.value, "lds_bytes": l.value}
+
+    def forward(self, A, out=None):
+        import torch
+
+        if A.ndim != 2 or int(A.shape[1]) != int(self.program["a_width"]):
+            raise ValueError(f"A must be [samples, {self.program['a_width']}]")
+        want = torch.float64 if self.dtype == "f64" else torch.float32
+        if A.dtype != want:
+            raise ValueError(f"A must be {want} for this plan")
+        S = int(A.shape[0])
+        if out is None:
+            out = torch.empty((S, self.feature_count), dtype=A.dtype, device=A.device)
+        elif tuple(out.shape) != (S, self.feature_count) or out.dtype != A.dtype:
+            raise ValueError("out has the wrong shape or dtype")
+        _check(lib().ye3t_hip_product_forward(self._handle, _dev(A, "A"), S, _dev(out, "B"), _stream()),
+               "ye3t_hip_product_forward")
+        return out
