@@ -164,6 +164,24 @@ void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* plan);
 int ye3t_hip_product_forward(const ye3t_hip_product_plan* plan, const void* A, int64_t samples, void* B,
                              ye3t_stream_t stream);
 
+/* Compile HIP source for the current device's architecture with hipRTC.
+ * On success *code is a malloc'ed code object of *size bytes (free with
+ * ye3t_hip_free).  Used for plan-specialised kernels; no reference counterpart
+ * (the reference JIT-compiles its whole extension, execution_plan.py:253-292). */
+int ye3t_hip_rtc_compile(const char* source, const char* name, const char* arch, void** code, int64_t* size);
+void ye3t_hip_free(void* ptr);
+
+/* Attach a plan-specialised kernel (code object from ye3t_hip_rtc_compile of
+ * ye3t_amd/ace/codegen.py output) to `plan`; product_forward then launches it
+ * with grid (ceil(samples/64), chunk_count).  The kernel signature is
+ * (const T* A, long samples, T* B). */
+int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* plan, const void* code, int64_t size,
+                                           const char* kernel_name, int64_t chunk_count);
+
+/* Select which kernel product_forward launches: 0 = generated (if attached),
+ * 1 = generic interpreter. */
+int ye3t_hip_product_plan_select(ye3t_hip_product_plan* plan, int use_interpreter);
+
 /* Kernel name/launch geometry of the last product_forward (for profiling). */
 int ye3t_hip_product_launch_info(const ye3t_hip_product_plan* plan, int64_t samples, int64_t* grid,
                                  int64_t* block, int64_t* lds_bytes);

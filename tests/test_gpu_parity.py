@@ -180,15 +180,18 @@ def _species_rank4_spec():
                           radial_per_species=11, caps={1: (11, 0), 2: (3, 4), 3: (2, 2), 4: (1, 2)})
 
 
-@pytest.mark.parametrize("cid,dtype,samples,max_slots", [
-    (4, "f32", 1000, None), (4, "f64", 333, None), (4, "f32", 63, 250), (4, "f32", 130, 48),
-    (2, "f64", 200, None), (3, "f32", 100, None), (3, "f64", 70, None)])
-def test_product_kernel_vs_flat_oracle(gpu, cid, dtype, samples, max_slots):
-    flush(f"product config {cid} {dtype} samples={samples} slots={max_slots}")
+@pytest.mark.parametrize("cid,dtype,samples,max_slots,kernel", [
+    (4, "f32", 1000, None, "interpreter"), (4, "f64", 333, None, "interpreter"), (4, "f32", 63, 250, "interpreter"),
+    (4, "f32", 130, 48, "interpreter"), (2, "f64", 200, None, "interpreter"), (3, "f32", 100, None, "interpreter"),
+    (3, "f64", 70, None, "interpreter"), (4, "f32", 1000, None, "generated"), (4, "f64", 333, None, "generated"),
+    (4, "f32", 63, None, "generated"), (4, "f32", 65, None, "generated")])
+def test_product_kernel_vs_flat_oracle(gpu, cid, dtype, samples, max_slots, kernel):
+    flush(f"product config {cid} {dtype} samples={samples} slots={max_slots} kernel={kernel}")
     import torch
 
     spec = _species_rank4_spec() if cid == 3 else W.config(cid).feature_spec
-    pipe = ACEPipeline(spec, dtype, max_slots)
+    pipe = ACEPipeline(spec, dtype, max_slots, kernel=kernel)
+    assert pipe.kernel == kernel
     A = np.random.default_rng(14).normal(size=(samples, pipe.plan.a_width))
     A_dev = _t(A, dtype, gpu)
     B = pipe.product(A_dev).cpu().numpy()
@@ -198,6 +201,23 @@ def test_product_kernel_vs_flat_oracle(gpu, cid, dtype, samples, max_slots):
     assert err < TOL[dtype]
     # determinism: bit-identical on a second run
     assert np.array_equal(B, pipe.product(A_dev).cpu().numpy())
+
+
+def test_generated_and_interpreter_agree_on_config4(gpu):
+    flush("generated vs interpreter, config 4 full sample count")
+    import torch
+
+    cfg = W.config(4)
+    pipe = ACEPipeline(cfg.feature_spec, "f32", kernel="generated")
+    A = torch.randn((800000, 16), dtype=torch.float32, device=gpu)
+    B_gen = pipe.product(A)
+    pipe.handle.select(use_interpreter=True)
+    B_int = pipe.product(A)
+    torch.cuda.synchronize()
+    rms = B_int.double().pow(2).mean(dim=0).sqrt().clamp_min(1e-30)
+    err = ((B_gen.double() - B_int.double()).abs().amax(dim=0) / rms).max().item()
+    flush(f"  err {err:.3e}")
+    assert err < 2e-5
 
 
 @pytest.mark.parametrize("cid,dtype", [(4, "f32"), (2, "f64")])

@@ -30,13 +30,32 @@ def to_device_inputs(inp, dtype, device="cuda"):
     return out
 
 
+# plans up to this many DAG terms get a plan-specialised (generated) kernel;
+# larger plans run the generic interpreter (hipRTC time grows with code size)
+GENERATED_MAX_TERMS = 5000
+
+
 class ACEPipeline:
-    def __init__(self, feature_spec, dtype="f32", max_slots=None, plan=None):
+    """``kernel``: "auto" (generated kernel when the plan is small enough),
+    "generated" or "interpreter" (the generic table-driven product kernel)."""
+
+    def __init__(self, feature_spec, dtype="f32", max_slots=None, plan=None, kernel="auto", max_live=None):
         self.spec = feature_spec
         self.dtype = dtype
         self.plan = plan if plan is not None else ProductPlan(feature_spec)
         self.program = compile_program(self.plan, dtype, max_slots)
         self.handle = native.ProductPlanHandle(self.program)
+        terms = sum(len(nd.get("terms", ())) for nd in self.plan.nodes)
+        use_gen = kernel == "generated" or (kernel == "auto" and terms <= GENERATED_MAX_TERMS)
+        if kernel not in {"auto", "generated", "interpreter"}:
+            raise ValueError(f"unknown product kernel {kernel!r}")
+        self.kernel = "interpreter"
+        if use_gen:
+            from ye3t_amd.ace.codegen import generate
+
+            source, meta = generate(self.plan, dtype, max_live)
+            self.handle.attach_generated(source, meta)
+            self.kernel = "generated"
 
     @property
     def feature_count(self):

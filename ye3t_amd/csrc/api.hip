@@ -40,6 +40,8 @@ const NormTable& norm_table() {
         table.v[l * (kMaxL + 1) + m] = v;
       }
     }
+    table.inv[0] = 0.0;
+    for (int k = 1; k < 2 * kMaxL + 2; ++k) table.inv[k] = 1.0 / double(k);
   });
   return table;
 }
@@ -52,17 +54,19 @@ __global__ __launch_bounds__(256) void radial_table_kernel(const Real* __restric
                                                            const Real* __restrict__ lambdas, int64_t E,
                                                            int n_max, Real* __restrict__ values,
                                                            Real* __restrict__ derivs) {
-  Real v[16], d[16];
+  // The basis is evaluated in fp64 for both storage types: the Chebyshev
+  // recurrence amplifies rounding of the warped variable by ~n^2.
+  double v[16], d[16];
   for (int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < E; e += int64_t(gridDim.x) * blockDim.x) {
     if (derivs) {
-      cheb_exp_cos_row<Real, true>(radii[e], cutoffs[e], lambdas[e], n_max, v, d);
+      cheb_exp_cos_row<double, true>(double(radii[e]), double(cutoffs[e]), double(lambdas[e]), n_max, v, d);
       for (int n = 0; n <= n_max; ++n) {
-        values[e * (n_max + 1) + n] = v[n];
-        derivs[e * (n_max + 1) + n] = d[n];
+        values[e * (n_max + 1) + n] = Real(v[n]);
+        derivs[e * (n_max + 1) + n] = Real(d[n]);
       }
     } else {
-      cheb_exp_cos_row<Real, false>(radii[e], cutoffs[e], lambdas[e], n_max, v, d);
-      for (int n = 0; n <= n_max; ++n) values[e * (n_max + 1) + n] = v[n];
+      cheb_exp_cos_row<double, false>(double(radii[e]), double(cutoffs[e]), double(lambdas[e]), n_max, v, d);
+      for (int n = 0; n <= n_max; ++n) values[e * (n_max + 1) + n] = Real(v[n]);
     }
   }
 }
@@ -72,36 +76,38 @@ __global__ __launch_bounds__(256) void radial_table_kernel(const Real* __restric
 // (reference ye3t_runtime_core.cpp:226-286, 808-843).
 template <typename Real>
 __global__ __launch_bounds__(128) void real_sph_table_kernel(const Real* __restrict__ vec, int64_t E, int lmax,
-                                                             Real eps, NormTable nt, Real* __restrict__ values,
+                                                             double eps, NormTable nt, Real* __restrict__ values,
                                                              Real* __restrict__ grads) {
   const int width = (lmax + 1) * (lmax + 1);
-  const Real sqrt2 = Real(1.4142135623730950488016887242096981);
+  const double sqrt2 = double(1.4142135623730950488016887242096981);
   for (int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < E; e += int64_t(gridDim.x) * blockDim.x) {
-    const Real x0 = vec[3 * e], y0 = vec[3 * e + 1], z0 = vec[3 * e + 2];
-    const Real r = d_sqrt(x0 * x0 + y0 * y0 + z0 * z0);
-    const Real sr = r > eps ? r : eps;
-    const Real u[3] = {x0 / sr, y0 / sr, z0 / sr};
+    const double x0 = double(vec[3 * e]), y0 = double(vec[3 * e + 1]), z0 = double(vec[3 * e + 2]);
+    const double r = d_sqrt(x0 * x0 + y0 * y0 + z0 * z0);
+    const double sr = r > eps ? r : eps;
+    const double u[3] = {x0 / sr, y0 / sr, z0 / sr};
     Real* row = values + e * width;
     if (!grads) {
-      real_sph_row<Real>(u[0], u[1], u[2], lmax, nt, row, 1);
+      double yrow[(kMaxL + 1) * (kMaxL + 1)];
+      real_sph_row<double>(u[0], u[1], u[2], lmax, nt, yrow, 1);
+      for (int k = 0; k < width; ++k) row[k] = Real(yrow[k]);
       continue;
     }
     // Q[l][m] for m <= l+1 (Q_l^{l+1} = 0)
-    Real Q[kMaxL + 2][kMaxL + 2];
-    Real qmm = Real(1);
+    double Q[kMaxL + 2][kMaxL + 2];
+    double qmm = double(1);
     for (int m = 0; m <= lmax + 1; ++m) {
-      if (m > 0) qmm *= Real(2 * m - 1);
-      Real q2 = Real(0), q1 = Real(0);
+      if (m > 0) qmm *= double(2 * m - 1);
+      double q2 = double(0), q1 = double(0);
       for (int l = 0; l <= lmax; ++l) {
-        Real q;
+        double q;
         if (l < m) {
-          q = Real(0);
+          q = double(0);
         } else if (l == m) {
           q = qmm;
         } else if (l == m + 1) {
-          q = Real(2 * m + 1) * u[2] * qmm;
+          q = double(2 * m + 1) * u[2] * qmm;
         } else {
-          q = (Real(2 * l - 1) * u[2] * q1 - Real(l + m - 1) * q2) / Real(l - m);
+          q = (double(2 * l - 1) * u[2] * q1 - double(l + m - 1) * q2) / double(l - m);
         }
         if (l >= m) {
           q2 = q1;
@@ -110,39 +116,39 @@ __global__ __launch_bounds__(128) void real_sph_table_kernel(const Real* __restr
         Q[l][m] = q;
       }
     }
-    Real cr = Real(1), ci = Real(0), pr = Real(1), pi = Real(0);
+    double cr = double(1), ci = double(0), pr = double(1), pi = double(0);
     for (int m = 0; m <= lmax; ++m) {
       if (m > 0) {
         pr = cr;
         pi = ci;
-        const Real nr = cr * u[0] - ci * u[1];
-        const Real ni = cr * u[1] + ci * u[0];
+        const double nr = cr * u[0] - ci * u[1];
+        const double ni = cr * u[1] + ci * u[0];
         cr = nr;
         ci = ni;
       }
       for (int l = m; l <= lmax; ++l) {
-        const Real n = Real(nt.v[l * (kMaxL + 1) + m]);
+        const double n = double(nt.v[l * (kMaxL + 1) + m]);
         const int base = l * l + l;
-        Real ug[2][3];
+        double ug[2][3];
         int idx[2];
         int count;
         if (m == 0) {
-          row[base] = n * Q[l][0];
-          ug[0][0] = Real(0);
-          ug[0][1] = Real(0);
+          row[base] = Real(n * Q[l][0]);
+          ug[0][0] = double(0);
+          ug[0][1] = double(0);
           ug[0][2] = n * Q[l][1];
           idx[0] = base;
           count = 1;
         } else {
-          const Real s = sqrt2 * n;
-          const Real q = Q[l][m], qz = Q[l][m + 1];
-          row[base + m] = s * q * cr;
-          row[base - m] = -s * q * ci;
-          ug[0][0] = s * q * (Real(m) * pr);
-          ug[0][1] = s * q * (-Real(m) * pi);
+          const double s = sqrt2 * n;
+          const double q = Q[l][m], qz = Q[l][m + 1];
+          row[base + m] = Real(s * q * cr);
+          row[base - m] = Real(-s * q * ci);
+          ug[0][0] = s * q * (double(m) * pr);
+          ug[0][1] = s * q * (-double(m) * pi);
           ug[0][2] = s * qz * cr;
-          ug[1][0] = -s * q * (Real(m) * pi);
-          ug[1][1] = -s * q * (Real(m) * pr);
+          ug[1][0] = -s * q * (double(m) * pi);
+          ug[1][1] = -s * q * (double(m) * pr);
           ug[1][2] = -s * qz * ci;
           idx[0] = base + m;
           idx[1] = base - m;
@@ -150,17 +156,17 @@ __global__ __launch_bounds__(128) void real_sph_table_kernel(const Real* __restr
         }
         for (int c = 0; c < count; ++c) {
           for (int a = 0; a < 3; ++a) {
-            Real g = Real(0);
+            double g = double(0);
             for (int b = 0; b < 3; ++b) {
-              Real jac;
+              double jac;
               if (r > eps) {
-                jac = ((a == b ? Real(1) : Real(0)) - u[a] * u[b]) / sr;
+                jac = ((a == b ? double(1) : double(0)) - u[a] * u[b]) / sr;
               } else {
-                jac = (a == b) ? Real(1) / sr : Real(0);
+                jac = (a == b) ? double(1) / sr : double(0);
               }
               g += ug[c][b] * jac;
             }
-            grads[(e * width + idx[c]) * 3 + a] = g;
+            grads[(e * width + idx[c]) * 3 + a] = Real(g);
           }
         }
       }
@@ -250,7 +256,7 @@ int ye3t_hip_real_sph_table(int dtype, const void* vec, int64_t E, int64_t lmax,
                        (const double*)vec, E, int(lmax), eps, norm_table(), (double*)values, (double*)grads);
   } else if (dtype == YE3T_F32) {
     hipLaunchKernelGGL(real_sph_table_kernel<float>, dim3(grid), dim3(128), 0, as_stream(stream),
-                       (const float*)vec, E, int(lmax), float(eps), norm_table(), (float*)values, (float*)grads);
+                       (const float*)vec, E, int(lmax), eps, norm_table(), (float*)values, (float*)grads);
   } else {
     return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);
   }

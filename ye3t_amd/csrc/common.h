@@ -65,37 +65,38 @@ struct Eps<double> {
 // passed by value as a kernel argument (lives in the scalar/constant cache).
 constexpr int kMaxL = 12;
 struct NormTable {
-  double v[(kMaxL + 1) * (kMaxL + 1)];  // index l*(l+1)/2 + m would be tighter; keep l*(kMaxL+1)+m
+  double v[(kMaxL + 1) * (kMaxL + 1)];  // N_lm at l*(kMaxL+1)+m
+  double inv[2 * kMaxL + 2];            // 1/k, k = 0..2 kMaxL+1 (inv[0] unused)
 };
 const NormTable& norm_table();
 
 // Radial ChebExpCos values (and d/dr) for n = 0..n_max, same algebra as the
 // reference CPU core (ye3t_runtime_core.cpp:321-423) but one Chebyshev pass.
-template <typename Real, bool WithDeriv>
-__device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max, Real* v, Real* d) {
+template <typename Real, bool WithDeriv, typename Out = Real>
+__device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max, Out* v, Out* d) {
   const Real pi = Real(3.141592653589793238462643383279502884);
   const Real rc = rc_in > Eps<Real>::value ? rc_in : Eps<Real>::value;
   const Real s = r / rc;
   if (s > Real(1)) {
     for (int n = 0; n <= n_max; ++n) {
-      v[n] = Real(0);
-      if (WithDeriv) d[n] = Real(0);
+      v[n] = Out(0);
+      if (WithDeriv) d[n] = Out(0);
     }
     return;
   }
   const Real c = d_cos(pi * s);
-  const Real sn = d_sin(pi * s);
-  v[0] = Real(1);
-  if (WithDeriv) d[0] = Real(0);
+  const Real sn = WithDeriv ? d_sin(pi * s) : Real(0);
+  v[0] = Out(1);
+  if (WithDeriv) d[0] = Out(0);
   if (n_max >= 1) {
-    v[1] = Real(0.5) * (Real(1) + c);
-    if (WithDeriv) d[1] = -Real(0.5) * pi * sn / rc;
+    v[1] = Out(Real(0.5) * (Real(1) + c));
+    if (WithDeriv) d[1] = Out(-Real(0.5) * pi * sn / rc);
   }
   if (n_max >= 2) {
-    const Real ex = d_exp(-lam * (s - Real(1)));
     const Real den = d_expm1(lam);
-    const Real x = Real(1) - Real(2) * d_expm1(-lam * (s - Real(1))) / den;
-    const Real dx = Real(2) * lam * ex / (den * rc);
+    const Real em1 = d_expm1(-lam * (s - Real(1)));
+    const Real x = Real(1) - Real(2) * em1 / den;
+    const Real dx = WithDeriv ? Real(2) * lam * d_exp(-lam * (s - Real(1))) / (den * rc) : Real(0);
     const Real env = Real(1) + c;
     const Real denv = -pi * sn / rc;
     Real t0 = Real(1), t1 = x;     // T_{n-2}, T_{n-1}
@@ -103,8 +104,8 @@ __device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max,
     for (int n = 2; n <= n_max; ++n) {
       const Real t2 = Real(2) * x * t1 - t0;
       // derivative of T_n is n U_{n-1}; U_{n-1} is u1 here
-      v[n] = Real(0.25) * (Real(1) - t2) * env;
-      if (WithDeriv) d[n] = Real(0.25) * (-(Real(n) * u1) * dx * env + (Real(1) - t2) * denv);
+      v[n] = Out(Real(0.25) * (Real(1) - t2) * env);
+      if (WithDeriv) d[n] = Out(Real(0.25) * (-(Real(n) * u1) * dx * env + (Real(1) - t2) * denv));
       t0 = t1;
       t1 = t2;
       const Real u2 = Real(2) * x * u1 - u0;

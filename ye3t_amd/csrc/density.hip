@@ -2,22 +2,23 @@
 //
 //   A[i, c, r, lm] = sum_{e in row i} w_c(e) R_r(|v_e|) Y_lm(v_e / |v_e|)
 //
-// One workgroup (256 threads = 4 waves) owns one atom at a time, so the
-// segment reduction over its CSR edge range needs no atomics and the result is
-// bit-reproducible.  Per tile of up to 64 edges:
-//   phase 1  wave 0 computes radial basis and real SH of each edge in
-//            registers and stages them in LDS (Y[j][lm], R[j][r]); for one-hot
-//            species it also builds per-species edge lists with ballots;
-//   phase 1b (node-feature weights) all threads form HW[j][c] = h[nbr_j, c] * R_c(j);
-//   phase 2  every thread owns output elements (c, r, lm) -- consecutive
-//            threads take consecutive lm, so the A row store is coalesced.
+// A workgroup of 256 threads owns `apb` consecutive atoms (apb ~ 256 / degree),
+// so the segment reduction over their CSR edge ranges needs no atomics and the
+// result is bit-reproducible.  Edges of those atoms are processed in tiles of
+// up to 256 (one edge per thread):
+//   phase 1  each thread evaluates the radial basis and real SH of its edge in
+//            registers (fp64 for both storage types) and stages them in LDS;
+//   phase 1b (node-feature weights) HW[j][c] = h[nbr_j, c] * sum_n mix[c, n] R_n(j);
+//   phase 2  each thread owns output elements (atom, c, r, lm) and sums over
+//            that atom's edges of the tile; consecutive threads take
+//            consecutive lm, so the A row store is coalesced.
 #include "common.h"
 #include "sph.h"
 
 namespace ye3t {
 
-constexpr int kTile = 64;
 constexpr int kDensityThreads = 256;
+constexpr int kEdgeTile = 256;
 
 template <typename Real>
 struct DensityParams {
@@ -31,9 +32,11 @@ struct DensityParams {
   int C;
   int n_max;
   int lmax;
-  Real cutoff;
-  Real lambda;
-  Real eps;
+  int apb;   // atoms per block
+  int tile;  // edges per LDS tile (<= kEdgeTile)
+  double cutoff;
+  double lambda;
+  double eps;
   Real* __restrict__ A;
 };
 
@@ -45,86 +48,84 @@ __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityPar
   const int LW = (p.lmax + 1) * (p.lmax + 1);
   const int NR = p.n_max + 1;
   const int rows = (MODE == 2) ? 1 : NR;
-  const int RS = (MODE == 2) ? p.C : NR;  // radial/weight stride per edge in LDS
-  Real* Ys = reinterpret_cast<Real*>(smem_raw);  // [kTile][LW]
-  Real* Rs = Ys + kTile * LW;                    // [kTile][RS]
-  Real* Rt = Rs + kTile * RS;                    // [kTile][NR] raw radials (MODE 2)
-  int* lists = reinterpret_cast<int*>(Rt + (MODE == 2 ? kTile * NR : 0));  // [C][kTile] (MODE 1)
-  int* counts = lists + (MODE == 1 ? p.C * kTile : 0);                    // [C]
+  const int RS = (MODE == 2) ? p.C : NR;
+  const int T = p.tile;
+  Real* Ys = reinterpret_cast<Real*>(smem_raw);  // [T][LW]
+  Real* Rs = Ys + T * LW;                        // [T][RS]
+  Real* Rt = Rs + T * RS;                        // [T][NR] raw radials (MODE 2)
+  int* Sp = reinterpret_cast<int*>(Rt + (MODE == 2 ? T * NR : 0));  // [T] species (MODE 1)
+  __shared__ int64_t atom_lo[64 + 1];
+
   const int tid = threadIdx.x;
   const int row_elems = p.C * rows * LW;
+  const int64_t a0 = int64_t(blockIdx.x) * p.apb;
+  if (a0 >= p.N) return;
+  const int na = int((p.N - a0) < p.apb ? (p.N - a0) : p.apb);
+  if (tid <= na) atom_lo[tid] = p.offsets[a0 + tid];
+  __syncthreads();
+  const int64_t e_begin = atom_lo[0], e_end = atom_lo[na];
+  const int items = na * row_elems;
+  Real* Ablk = p.A + a0 * int64_t(row_elems);
 
-  for (int64_t atom = blockIdx.x; atom < p.N; atom += gridDim.x) {
-    const int64_t e0 = p.offsets[atom], e1 = p.offsets[atom + 1];
-    Real* Arow = p.A + atom * int64_t(row_elems);
-    if (e1 <= e0) {
-      for (int k = tid; k < row_elems; k += kDensityThreads) Arow[k] = Real(0);
-      continue;
-    }
-    bool first = true;
-    for (int64_t t0 = e0; t0 < e1; t0 += kTile) {
-      const int cnt = int((e1 - t0) < kTile ? (e1 - t0) : kTile);
-      if (tid < kTile) {
-        const int j = tid;
-        int sp = -1;
-        if (j < cnt) {
-          const int64_t e = t0 + j;
-          const Real x = p.vec[3 * e], y = p.vec[3 * e + 1], z = p.vec[3 * e + 2];
-          const Real r = d_sqrt(x * x + y * y + z * z);
-          const Real sr = r > p.eps ? r : p.eps;
-          real_sph_row<Real>(x / sr, y / sr, z / sr, p.lmax, nt, Ys + j * LW, 1);
-          Real rad[16];
-          cheb_exp_cos_row<Real, false>(r, p.cutoff, p.lambda, p.n_max, rad, nullptr);
-          if (MODE == 2) {
-            for (int n = 0; n < NR; ++n) Rt[j * NR + n] = rad[n];
-          } else {
-            for (int n = 0; n < NR; ++n) Rs[j * NR + n] = rad[n];
-          }
-          if (MODE == 1) sp = p.species[p.nbr[e]];
-        }
-        if (MODE == 1) {
-          // stable per-species edge lists (tile = one wave of 64 lanes)
-          const uint64_t lt = (j == 0) ? 0ull : (~0ull >> (64 - j));
-          for (int c = 0; c < p.C; ++c) {
-            const uint64_t mask = __ballot(sp == c);
-            if (sp == c) lists[c * kTile + __popcll(mask & lt)] = j;
-            if (j == 0) counts[c] = __popcll(mask);
-          }
-        }
-      }
-      __syncthreads();
+  // atoms without any edge still get their zero row
+  for (int k = tid; k < items; k += kDensityThreads) {
+    const int a = k / row_elems;
+    if (atom_lo[a + 1] == atom_lo[a]) Ablk[k] = Real(0);
+  }
+
+  for (int64_t t0 = e_begin; t0 < e_end; t0 += T) {
+    const int cnt = int((e_end - t0) < T ? (e_end - t0) : T);
+    if (tid < cnt) {
+      const int j = tid;
+      const int64_t e = t0 + j;
+      const double x = double(p.vec[3 * e]), y = double(p.vec[3 * e + 1]), z = double(p.vec[3 * e + 2]);
+      const double r = sqrt(x * x + y * y + z * z);
+      const double sr = r > p.eps ? r : p.eps;
+      const double inv = 1.0 / sr;
+      real_sph_row<double, Real>(x * inv, y * inv, z * inv, p.lmax, nt, Ys + j * LW, 1);
       if (MODE == 2) {
-        for (int q = tid; q < cnt * p.C; q += kDensityThreads) {
-          const int j = q / p.C, c = q - (q / p.C) * p.C;
-          const int64_t nb = p.nbr[t0 + j];
-          Real rc = Real(0);
-          for (int n = 0; n < NR; ++n) rc = d_fma(p.mix[c * NR + n], Rt[j * NR + n], rc);
-          Rs[j * p.C + c] = p.feats[nb * p.C + c] * rc;
-        }
-        __syncthreads();
+        cheb_exp_cos_row<double, false, Real>(r, p.cutoff, p.lambda, p.n_max, Rt + j * NR, nullptr);
+      } else {
+        cheb_exp_cos_row<double, false, Real>(r, p.cutoff, p.lambda, p.n_max, Rs + j * NR, nullptr);
       }
-      for (int k = tid; k < row_elems; k += kDensityThreads) {
-        const int lm = k % LW;
-        const int cr = k / LW;  // c * rows + r
-        const int c = cr / rows;
-        const int r = cr - c * rows;
-        Real acc = first ? Real(0) : Arow[k];
-        if (MODE == 0) {
-          for (int j = 0; j < cnt; ++j) acc = d_fma(Rs[j * NR + r], Ys[j * LW + lm], acc);
-        } else if (MODE == 1) {
-          const int n_c = counts[c];
-          for (int q = 0; q < n_c; ++q) {
-            const int j = lists[c * kTile + q];
-            acc = d_fma(Rs[j * NR + r], Ys[j * LW + lm], acc);
-          }
-        } else {
-          for (int j = 0; j < cnt; ++j) acc = d_fma(Rs[j * p.C + c], Ys[j * LW + lm], acc);
-        }
-        Arow[k] = acc;
+      if (MODE == 1) Sp[j] = p.species[p.nbr[e]];
+    }
+    __syncthreads();
+    if (MODE == 2) {
+      for (int q = tid; q < cnt * p.C; q += kDensityThreads) {
+        const int j = q / p.C, c = q - (q / p.C) * p.C;
+        const int64_t nb = p.nbr[t0 + j];
+        Real rc = Real(0);
+        for (int n = 0; n < NR; ++n) rc = d_fma(p.mix[c * NR + n], Rt[j * NR + n], rc);
+        Rs[j * p.C + c] = p.feats[nb * p.C + c] * rc;
       }
-      first = false;
       __syncthreads();
     }
+    for (int k = tid; k < items; k += kDensityThreads) {
+      const int a = k / row_elems;
+      const int64_t lo = atom_lo[a], hi = atom_lo[a + 1];
+      const int64_t j0 = lo > t0 ? lo : t0;
+      const int64_t j1 = hi < t0 + cnt ? hi : t0 + cnt;
+      if (j0 >= j1) continue;  // this atom has no edge in the tile
+      const int rem = k - a * row_elems;
+      const int lm = rem % LW;
+      const int cr = rem / LW;  // c * rows + r
+      const int c = cr / rows;
+      const int rr = cr - c * rows;
+      Real acc = (lo >= t0) ? Real(0) : Ablk[k];  // first tile of this atom starts from zero
+      const int jb = int(j0 - t0), je = int(j1 - t0);
+      if (MODE == 0) {
+        for (int j = jb; j < je; ++j) acc = d_fma(Rs[j * NR + rr], Ys[j * LW + lm], acc);
+      } else if (MODE == 1) {
+        for (int j = jb; j < je; ++j) {
+          if (Sp[j] == c) acc = d_fma(Rs[j * NR + rr], Ys[j * LW + lm], acc);
+        }
+      } else {
+        for (int j = jb; j < je; ++j) acc = d_fma(Rs[j * p.C + c], Ys[j * LW + lm], acc);
+      }
+      Ablk[k] = acc;
+    }
+    __syncthreads();
   }
 }
 
@@ -141,21 +142,28 @@ int launch_density(const ye3t_density_args* a, void* A, hipStream_t stream) {
   p.C = int(a->channel_count);
   p.n_max = int(a->max_radial_index);
   p.lmax = int(a->max_angular);
-  p.cutoff = Real(a->cutoff);
-  p.lambda = Real(a->lambda);
-  p.eps = Real(a->epsilon);
+  p.cutoff = a->cutoff;
+  p.lambda = a->lambda;
+  p.eps = a->epsilon;
   p.A = static_cast<Real*>(A);
   const int LW = (p.lmax + 1) * (p.lmax + 1);
   const int NR = p.n_max + 1;
   const int RS = (MODE == 2) ? p.C : NR;
-  size_t lds = sizeof(Real) * size_t(kTile) * (LW + RS + (MODE == 2 ? NR : 0));
-  if (MODE == 1) lds += sizeof(int) * size_t(p.C) * (kTile + 1);
-  if (lds > 64 * 1024) {
-    return set_error(YE3T_EUNSUPPORTED, "density tile needs %zu bytes of LDS (limit 65536)", lds);
-  }
-  int64_t grid = p.N;
-  if (grid > (1 << 20)) grid = 1 << 20;
-  if (grid < 1) grid = 1;
+  // edge tile: as many edges as fit in 60 KiB of LDS, a multiple of 64, <= 256
+  const size_t per_edge = sizeof(Real) * size_t(LW + RS + (MODE == 2 ? NR : 0)) + (MODE == 1 ? sizeof(int) : 0);
+  int tile = int((60 * 1024) / per_edge) / 64 * 64;
+  if (tile > kEdgeTile) tile = kEdgeTile;
+  if (tile < 64) return set_error(YE3T_EUNSUPPORTED, "density row too wide for one LDS tile (%zu B/edge)", per_edge);
+  p.tile = tile;
+  // atoms per block from the mean degree: about one edge tile per block
+  const double mean_degree = a->atom_count ? double(a->edge_count) / double(a->atom_count) : 1.0;
+  int apb = int(double(tile) / (mean_degree > 1.0 ? mean_degree : 1.0));
+  if (apb < 1) apb = 1;
+  if (apb > 64) apb = 64;
+  p.apb = apb;
+  const size_t lds = per_edge * size_t(tile);
+  const int64_t grid = (p.N + apb - 1) / apb;
+  if (grid > 0x7FFFFFFF) return set_error(YE3T_EUNSUPPORTED, "too many atoms for one launch");
   hipLaunchKernelGGL((ace_density_kernel<Real, MODE>), dim3(unsigned(grid)), dim3(kDensityThreads), lds, stream, p,
                      norm_table());
   return check_launch("ace_density_kernel");

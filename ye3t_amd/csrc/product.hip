@@ -11,6 +11,10 @@
 //     columns of one row.
 // (b) evaluate_schedule_kernel / sym_monomial_kernel: device versions of the
 //     reference's flat schedule evaluator and symmetric-power contraction.
+#include <hip/hiprtc.h>
+
+#include <cstdlib>
+#include <cstring>
 #include <vector>
 
 #include "common.h"
@@ -29,6 +33,11 @@ struct ye3t_hip_product_plan {
   int64_t* coeff_off;  // [chunks+1]
   int64_t* out_off;    // [chunks+1]
   int64_t* first_col;  // [chunks]
+  // plan-specialised kernel (optional)
+  hipModule_t module;
+  hipFunction_t generated;
+  int64_t generated_chunks;
+  int use_interpreter;
 };
 
 namespace ye3t {
@@ -213,6 +222,7 @@ void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* p) {
   (void)hipFree(p->coeff_off);
   (void)hipFree(p->out_off);
   (void)hipFree(p->first_col);
+  if (p->module) (void)hipModuleUnload(p->module);
   (void)hipSetDevice(prev);
   delete p;
 }
@@ -294,6 +304,74 @@ int ye3t_hip_product_plan_create(const ye3t_product_plan_desc* d, ye3t_hip_produ
   return YE3T_OK;
 }
 
+int ye3t_hip_rtc_compile(const char* source, const char* name, const char* arch, void** code, int64_t* size) {
+  clear_error();
+  YE3T_REQUIRE(source && code && size, "NULL argument");
+  *code = nullptr;
+  *size = 0;
+  std::string arch_opt = std::string("--offload-arch=") + (arch && *arch ? arch : "gfx950");
+  const char* opts[] = {arch_opt.c_str(), "-O3", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, source, name ? name : "ye3t_generated.hip", 0, nullptr, nullptr) !=
+      HIPRTC_SUCCESS) {
+    return set_error(YE3T_ELAUNCH, "hiprtcCreateProgram failed");
+  }
+  const hiprtcResult rc = hiprtcCompileProgram(prog, int(sizeof(opts) / sizeof(opts[0])), opts);
+  if (rc != HIPRTC_SUCCESS) {
+    size_t log_size = 0;
+    hiprtcGetProgramLogSize(prog, &log_size);
+    std::string log(log_size + 1, '\0');
+    if (log_size) hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    return set_error(YE3T_ELAUNCH, "hiprtc compile failed: %s", log.substr(0, 900).c_str());
+  }
+  size_t n = 0;
+  hiprtcGetCodeSize(prog, &n);
+  void* buf = std::malloc(n ? n : 1);
+  if (!buf) {
+    hiprtcDestroyProgram(&prog);
+    return set_error(YE3T_ENOMEM, "out of host memory");
+  }
+  hiprtcGetCode(prog, static_cast<char*>(buf));
+  hiprtcDestroyProgram(&prog);
+  *code = buf;
+  *size = int64_t(n);
+  return YE3T_OK;
+}
+
+void ye3t_hip_free(void* ptr) { std::free(ptr); }
+
+int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* p, const void* code, int64_t size,
+                                           const char* kernel_name, int64_t chunk_count) {
+  clear_error();
+  YE3T_REQUIRE(p && code && size > 0 && kernel_name, "NULL argument");
+  YE3T_REQUIRE(chunk_count >= 1 && chunk_count <= 65535, "bad generated chunk count");
+  int prev = 0;
+  YE3T_CHECK_HIP(hipGetDevice(&prev));
+  YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
+  hipModule_t module;
+  YE3T_CHECK_HIP(hipModuleLoadData(&module, code));
+  hipFunction_t fn;
+  if (hipModuleGetFunction(&fn, module, kernel_name) != hipSuccess) {
+    (void)hipModuleUnload(module);
+    return set_error(YE3T_EINVAL, "kernel %s not found in code object", kernel_name);
+  }
+  if (p->module) (void)hipModuleUnload(p->module);
+  p->module = module;
+  p->generated = fn;
+  p->generated_chunks = chunk_count;
+  p->use_interpreter = 0;
+  return YE3T_OK;
+}
+
+int ye3t_hip_product_plan_select(ye3t_hip_product_plan* p, int use_interpreter) {
+  clear_error();
+  YE3T_REQUIRE(p != nullptr, "NULL plan");
+  YE3T_REQUIRE(use_interpreter || p->generated, "no generated kernel attached");
+  p->use_interpreter = use_interpreter ? 1 : 0;
+  return YE3T_OK;
+}
+
 int ye3t_hip_product_launch_info(const ye3t_hip_product_plan* p, int64_t samples, int64_t* grid, int64_t* block,
                                  int64_t* lds) {
   YE3T_REQUIRE(p != nullptr, "NULL plan");
@@ -312,6 +390,16 @@ int ye3t_hip_product_forward(const ye3t_hip_product_plan* p, const void* A, int6
   if (samples == 0) return YE3T_OK;
   YE3T_REQUIRE(A && B, "NULL input or output");
   const int64_t tiles = (samples + kLanes - 1) / kLanes;
+  if (p->generated && !p->use_interpreter) {
+    YE3T_REQUIRE(tiles <= int64_t(0x7FFFFFFF), "too many samples for one launch");
+    long s_arg = long(samples);
+    const void* a_arg = A;
+    void* b_arg = B;
+    void* args[] = {&a_arg, &s_arg, &b_arg};
+    YE3T_CHECK_HIP(hipModuleLaunchKernel(p->generated, unsigned(tiles), unsigned(p->generated_chunks), 1, kLanes, 1,
+                                         1, 0, as_stream(stream), args, nullptr));
+    return YE3T_OK;
+  }
   const int64_t grid = tiles * p->chunk_count;
   YE3T_REQUIRE(grid <= int64_t(0x7FFFFFFF), "too many samples for one launch");
   const size_t lds = product_lds_bytes(p);

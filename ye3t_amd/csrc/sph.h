@@ -14,9 +14,10 @@
 
 namespace ye3t {
 
-// Writes the (lmax+1)^2 values of one unit vector to out[stride * k].
-template <typename Real>
-__device__ inline void real_sph_row(Real x, Real y, Real z, int lmax, const NormTable& nt, Real* out,
+// Writes the (lmax+1)^2 values of one unit vector to out[stride * k],
+// computing in `Real` and storing as `Out`.
+template <typename Real, typename Out = Real>
+__device__ inline void real_sph_row(Real x, Real y, Real z, int lmax, const NormTable& nt, Out* out,
                                     int stride) {
   const Real sqrt2 = Real(1.4142135623730950488016887242096981);
   Real cr = Real(1), ci = Real(0);  // (x + i y)^m
@@ -37,18 +38,18 @@ __device__ inline void real_sph_row(Real x, Real y, Real z, int lmax, const Norm
       } else if (l == m + 1) {
         q = Real(2 * m + 1) * z * qmm;
       } else {
-        q = (Real(2 * l - 1) * z * q1 - Real(l + m - 1) * q2) / Real(l - m);
+        q = (Real(2 * l - 1) * z * q1 - Real(l + m - 1) * q2) * Real(nt.inv[l - m]);
       }
       q2 = q1;
       q1 = q;
       const Real n = Real(nt.v[l * (kMaxL + 1) + m]);
       const int base = l * l + l;
       if (m == 0) {
-        out[stride * base] = n * q;
+        out[stride * base] = Out(n * q);
       } else {
         const Real s = sqrt2 * n * q;
-        out[stride * (base + m)] = s * cr;
-        out[stride * (base - m)] = -s * ci;
+        out[stride * (base + m)] = Out(s * cr);
+        out[stride * (base - m)] = Out(-s * ci);
       }
     }
   }

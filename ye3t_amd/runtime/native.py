@@ -74,6 +74,12 @@ def lib():
     L.ye3t_hip_product_forward.argtypes = [_vp, _vp, _i64, _vp, _vp]
     L.ye3t_hip_product_launch_info.argtypes = [_vp, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                                                ctypes.POINTER(_i64)]
+    L.ye3t_hip_rtc_compile.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_vp),
+                                       ctypes.POINTER(_i64)]
+    L.ye3t_hip_free.argtypes = [_vp]
+    L.ye3t_hip_free.restype = None
+    L.ye3t_hip_product_plan_attach_generated.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, _i64]
+    L.ye3t_hip_product_plan_select.argtypes = [_vp, ctypes.c_int]
     version = L.ye3t_hip_abi_version()
     if version != ABI_VERSION:
         raise RuntimeError(f"ye3t_hip ABI {version} does not match the bindings ({ABI_VERSION})")
@@ -86,7 +92,8 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_real_sph_table", "ye3t_hip_density_accumulate_csr", "ye3t_hip_ace_density_forward",
     "ye3t_hip_symmetric_power_monomial", "ye3t_hip_evaluate_factorized_schedule",
     "ye3t_hip_product_plan_create", "ye3t_hip_product_plan_destroy", "ye3t_hip_product_forward",
-    "ye3t_hip_product_launch_info",
+    "ye3t_hip_product_launch_info", "ye3t_hip_rtc_compile", "ye3t_hip_free",
+    "ye3t_hip_product_plan_attach_generated", "ye3t_hip_product_plan_select",
 )
 
 
@@ -262,6 +269,37 @@ def evaluate_factorized_schedule(block_values, schedule):
     return out
 
 
+def _jit_cache_dir():
+    import tempfile
+
+    path = os.environ.get("YE3T_AMD_JIT_CACHE") or os.path.join(tempfile.gettempdir(), "ye3t_amd_jit")
+    os.makedirs(path, exist_ok=True)
+    return path
+
+
+def rtc_compile(source, name="ye3t_generated.hip", arch="gfx950"):
+    """Compile HIP source with hipRTC (cached on disk by source hash); returns the code object bytes."""
+    import hashlib
+
+    key = hashlib.sha256((arch + "\0" + source).encode()).hexdigest()[:24]
+    path = os.path.join(_jit_cache_dir(), key + ".co")
+    if os.path.exists(path):
+        with open(path, "rb") as fh:
+            return fh.read()
+    code, size = _vp(), _i64()
+    _check(lib().ye3t_hip_rtc_compile(source.encode(), name.encode(), arch.encode(), ctypes.byref(code),
+                                      ctypes.byref(size)), "ye3t_hip_rtc_compile")
+    try:
+        blob = ctypes.string_at(code, size.value)
+    finally:
+        lib().ye3t_hip_free(code)
+    tmp = path + f".{os.getpid()}.tmp"
+    with open(tmp, "wb") as fh:
+        fh.write(blob)
+    os.replace(tmp, path)
+    return blob
+
+
 class ProductPlanHandle:
     """Device-resident compiled product program (owns a ``ye3t_hip_product_plan``)."""
 
@@ -296,6 +334,23 @@ class ProductPlanHandle:
     @property
     def feature_count(self):
         return int(self.program["feature_count"])
+
+    def attach_generated(self, source, meta):
+        """Compile and attach a plan-specialised kernel (``ye3t_amd.ace.codegen``)."""
+        if meta["feature_count"] != self.feature_count or meta["a_width"] != self.program["a_width"]:
+            raise ValueError("generated kernel does not match this plan")
+        if meta["dtype"] != self.dtype:
+            raise ValueError("generated kernel dtype does not match this plan")
+        blob = rtc_compile(source)
+        self._code = ctypes.create_string_buffer(blob, len(blob))
+        _check(lib().ye3t_hip_product_plan_attach_generated(self._handle, self._code, len(blob),
+                                                            meta["kernel"].encode(), int(meta["chunks"])),
+               "ye3t_hip_product_plan_attach_generated")
+        self.generated = meta
+
+    def select(self, use_interpreter):
+        _check(lib().ye3t_hip_product_plan_select(self._handle, 1 if use_interpreter else 0),
+               "ye3t_hip_product_plan_select")
 
     def launch_info(self, samples):
         g, b, l = _i64(), _i64(), _i64()
