@@ -80,6 +80,10 @@ def main():
     ap.add_argument("--max-slots", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--kernel", default="auto", choices=["auto", "generated", "interpreter"])
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="after the timed region, copy B once (a plain copy kernel of known size, for "
+                         "calibrating FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -97,7 +101,7 @@ def main():
     dtype = args.dtype or cfg.dtypes[0]
     elem = 8 if dtype == "f64" else 4
     t_build = time.perf_counter()
-    pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots)
+    pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots, kernel=args.kernel)
     t_build = time.perf_counter() - t_build
     inp = cfg.density.generate()
     dev = to_device_inputs(inp, dtype, "cuda")
@@ -126,10 +130,17 @@ def main():
         e2.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    copy_bytes = None
+    if args.copy_probe:
+        probe = torch.empty_like(B)
+        probe.copy_(B)
+        torch.cuda.synchronize()
+        copy_bytes = 2 * B.numel() * B.element_size()
     s1 = float(np.mean([a.elapsed_time(b) for a, b, _ in ev])) * 1e-3
     s2 = float(np.mean([b.elapsed_time(c) for _, b, c in ev])) * 1e-3
     ms_per_step = wall / args.steps * 1e3
     b1, b2 = algorithmic_bytes(cfg, pipe.plan, elem)
+    k2 = "ye3t_product_generated" if pipe.kernel == "generated" else "product_kernel"
     features = rows.shape[0] * pipe.feature_count
     value = features / (wall / args.steps)
     stats = program_stats(pipe.program)
@@ -153,14 +164,16 @@ def main():
                    "targets": list(cfg.feature_spec.targets), "parallelism": "single GPU"},
         "atoms_per_s": d.atom_count / (wall / args.steps),
         "roofline": {"bound": "hbm", "achieved": b2 / s2 / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": b2 / s2 / 1e9 / HBM_PEAK_GBS, "traffic": None, "kernel": "product_kernel",
+                     "frac": b2 / s2 / 1e9 / HBM_PEAK_GBS, "traffic": None, "kernel": k2,
                      "algorithmic_bytes": b2, "avg_kernel_us": s2 * 1e6},
         "stage1": {"kernel": "ace_density_kernel", "avg_kernel_us": s1 * 1e6, "algorithmic_bytes": b1,
                    "achieved_gbs": b1 / s1 / 1e9, "frac": b1 / s1 / 1e9 / HBM_PEAK_GBS},
-        "stage2": {"kernel": "product_kernel", "avg_kernel_us": s2 * 1e6, "algorithmic_bytes": b2,
+        "stage2": {"kernel": k2, "avg_kernel_us": s2 * 1e6, "algorithmic_bytes": b2,
                    "achieved_gbs": b2 / s2 / 1e9, "frac": b2 / s2 / 1e9 / HBM_PEAK_GBS,
-                   "program": stats, "plan_compile_s": t_build},
+                   "program": stats, "plan_compile_s": t_build, "product_kernel": pipe.kernel},
     }
+    if copy_bytes is not None:
+        line["copy_probe_bytes"] = copy_bytes
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, pipe, args.cpu_seconds)
     print(json.dumps(line), flush=True)

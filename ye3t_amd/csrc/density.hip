@@ -40,35 +40,56 @@ struct DensityParams {
   Real* __restrict__ A;
 };
 
+template <typename Real>
+struct Vec;
+template <>
+struct Vec<float> {
+  using T = float4;
+  static constexpr int N = 4;
+};
+template <>
+struct Vec<double> {
+  using T = double2;
+  static constexpr int N = 2;
+};
+
 // MODE 0: one channel, weight 1.  MODE 1: one-hot species channels.
 // MODE 2: node-feature weights with per-channel radial mix (one radial row).
 template <typename Real, int MODE>
 __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityParams<Real> p, NormTable nt) {
+  using V = typename Vec<Real>::T;
+  constexpr int VN = Vec<Real>::N;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int LW = (p.lmax + 1) * (p.lmax + 1);
+  const int LWp = (LW + VN - 1) / VN * VN;  // padded row of the SH tile (16-byte multiple)
   const int NR = p.n_max + 1;
   const int rows = (MODE == 2) ? 1 : NR;
   const int RS = (MODE == 2) ? p.C : NR;
   const int T = p.tile;
-  Real* Ys = reinterpret_cast<Real*>(smem_raw);  // [T][LW]
-  Real* Rs = Ys + T * LW;                        // [T][RS]
+  Real* Ys = reinterpret_cast<Real*>(smem_raw);  // [T][LWp]
+  Real* Rs = Ys + T * LWp;                       // [T][RS]
   Real* Rt = Rs + T * RS;                        // [T][NR] raw radials (MODE 2)
   int* Sp = reinterpret_cast<int*>(Rt + (MODE == 2 ? T * NR : 0));  // [T] species (MODE 1)
+  Real* Mx = Rt + (MODE == 2 ? T * NR : 0);                          // [C][NR] radial mix (MODE 2)
   __shared__ int64_t atom_lo[64 + 1];
 
   const int tid = threadIdx.x;
   const int row_elems = p.C * rows * LW;
+  const int groups = LWp / VN;
+  const int ipa = p.C * rows * groups;  // vector items per atom
   const int64_t a0 = int64_t(blockIdx.x) * p.apb;
   if (a0 >= p.N) return;
   const int na = int((p.N - a0) < p.apb ? (p.N - a0) : p.apb);
   if (tid <= na) atom_lo[tid] = p.offsets[a0 + tid];
+  if (MODE == 2) {
+    for (int q = tid; q < p.C * NR; q += kDensityThreads) Mx[q] = p.mix[q];
+  }
   __syncthreads();
   const int64_t e_begin = atom_lo[0], e_end = atom_lo[na];
-  const int items = na * row_elems;
   Real* Ablk = p.A + a0 * int64_t(row_elems);
 
   // atoms without any edge still get their zero row
-  for (int k = tid; k < items; k += kDensityThreads) {
+  for (int k = tid; k < na * row_elems; k += kDensityThreads) {
     const int a = k / row_elems;
     if (atom_lo[a + 1] == atom_lo[a]) Ablk[k] = Real(0);
   }
@@ -82,7 +103,8 @@ __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityPar
       const double r = sqrt(x * x + y * y + z * z);
       const double sr = r > p.eps ? r : p.eps;
       const double inv = 1.0 / sr;
-      real_sph_row<double, Real>(x * inv, y * inv, z * inv, p.lmax, nt, Ys + j * LW, 1);
+      real_sph_row<double, Real>(x * inv, y * inv, z * inv, p.lmax, nt, Ys + j * LWp, 1);
+      for (int k = LW; k < LWp; ++k) Ys[j * LWp + k] = Real(0);
       if (MODE == 2) {
         cheb_exp_cos_row<double, false, Real>(r, p.cutoff, p.lambda, p.n_max, Rt + j * NR, nullptr);
       } else {
@@ -92,38 +114,91 @@ __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityPar
     }
     __syncthreads();
     if (MODE == 2) {
-      for (int q = tid; q < cnt * p.C; q += kDensityThreads) {
-        const int j = q / p.C, c = q - (q / p.C) * p.C;
-        const int64_t nb = p.nbr[t0 + j];
-        Real rc = Real(0);
-        for (int n = 0; n < NR; ++n) rc = d_fma(p.mix[c * NR + n], Rt[j * NR + n], rc);
-        Rs[j * p.C + c] = p.feats[nb * p.C + c] * rc;
+      // HW[j][c] = h[nbr_j, c] * sum_n mix[c, n] R_n(j)
+      if (kDensityThreads % p.C == 0) {
+        const int c = tid % p.C;
+        const int jstep = kDensityThreads / p.C;
+        const Real* mrow = Mx + c * NR;
+        for (int j = tid / p.C; j < cnt; j += jstep) {
+          const Real h = p.feats[p.nbr[t0 + j] * p.C + c];
+          const Real* rrow = Rt + j * NR;
+          Real r0 = Real(0), r1 = Real(0);
+          int n = 0;
+          for (; n + 2 <= NR; n += 2) {
+            r0 = d_fma(mrow[n], rrow[n], r0);
+            r1 = d_fma(mrow[n + 1], rrow[n + 1], r1);
+          }
+          if (n < NR) r0 = d_fma(mrow[n], rrow[n], r0);
+          Rs[j * p.C + c] = h * (r0 + r1);
+        }
+      } else {
+        for (int q = tid; q < cnt * p.C; q += kDensityThreads) {
+          const int j = q / p.C, c = q - (q / p.C) * p.C;
+          const Real h = p.feats[p.nbr[t0 + j] * p.C + c];
+          Real rc = Real(0);
+          for (int n = 0; n < NR; ++n) rc = d_fma(Mx[c * NR + n], Rt[j * NR + n], rc);
+          Rs[j * p.C + c] = h * rc;
+        }
       }
       __syncthreads();
     }
-    for (int k = tid; k < items; k += kDensityThreads) {
-      const int a = k / row_elems;
+    // phase 2: vector item = (atom, c, r, group of VN consecutive lm)
+    for (int item = tid; item < na * ipa; item += kDensityThreads) {
+      const int a = item / ipa;
+      const int rem = item - a * ipa;
+      const int g = rem % groups;
+      const int cr = rem / groups;  // c * rows + r
+      const int c = cr / rows;
+      const int rr = cr - c * rows;
       const int64_t lo = atom_lo[a], hi = atom_lo[a + 1];
       const int64_t j0 = lo > t0 ? lo : t0;
       const int64_t j1 = hi < t0 + cnt ? hi : t0 + cnt;
       if (j0 >= j1) continue;  // this atom has no edge in the tile
-      const int rem = k - a * row_elems;
-      const int lm = rem % LW;
-      const int cr = rem / LW;  // c * rows + r
-      const int c = cr / rows;
-      const int rr = cr - c * rows;
-      Real acc = (lo >= t0) ? Real(0) : Ablk[k];  // first tile of this atom starts from zero
       const int jb = int(j0 - t0), je = int(j1 - t0);
-      if (MODE == 0) {
-        for (int j = jb; j < je; ++j) acc = d_fma(Rs[j * NR + rr], Ys[j * LW + lm], acc);
-      } else if (MODE == 1) {
-        for (int j = jb; j < je; ++j) {
-          if (Sp[j] == c) acc = d_fma(Rs[j * NR + rr], Ys[j * LW + lm], acc);
-        }
-      } else {
-        for (int j = jb; j < je; ++j) acc = d_fma(Rs[j * p.C + c], Ys[j * LW + lm], acc);
+      const Real* rcol = (MODE == 2) ? (Rs + c) : (Rs + rr);
+      const V* ycol = reinterpret_cast<const V*>(Ys + g * VN);
+      const int ystride = LWp / VN;
+      Real acc[VN], acc2[VN];
+      for (int v = 0; v < VN; ++v) {
+        acc[v] = Real(0);
+        acc2[v] = Real(0);
       }
-      Ablk[k] = acc;
+      int j = jb;
+      for (; j + 2 <= je; j += 2) {
+        const V y0 = ycol[j * ystride];
+        const V y1 = ycol[(j + 1) * ystride];
+        Real w0 = rcol[j * RS], w1 = rcol[(j + 1) * RS];
+        if (MODE == 1) {
+          w0 = Sp[j] == c ? w0 : Real(0);
+          w1 = Sp[j + 1] == c ? w1 : Real(0);
+        }
+        const Real* y0p = reinterpret_cast<const Real*>(&y0);
+        const Real* y1p = reinterpret_cast<const Real*>(&y1);
+        for (int v = 0; v < VN; ++v) {
+          acc[v] = d_fma(w0, y0p[v], acc[v]);
+          acc2[v] = d_fma(w1, y1p[v], acc2[v]);
+        }
+      }
+      if (j < je) {
+        const V y0 = ycol[j * ystride];
+        Real w0 = rcol[j * RS];
+        if (MODE == 1) w0 = Sp[j] == c ? w0 : Real(0);
+        const Real* y0p = reinterpret_cast<const Real*>(&y0);
+        for (int v = 0; v < VN; ++v) acc[v] = d_fma(w0, y0p[v], acc[v]);
+      }
+      Real* dst = Ablk + int64_t(a) * row_elems + int64_t(cr) * LW + g * VN;
+      const int valid = (LW - g * VN) < VN ? (LW - g * VN) : VN;
+      for (int v = 0; v < VN; ++v) {
+        if (v < valid) {
+          const Real part = acc[v] + acc2[v];
+          // the first tile holding this atom's edges starts from zero
+          if (lo >= t0) {
+            dst[v] = part;
+          } else {
+            dst[v] = dst[v] + part;
+          }
+        }
+      }
     }
     __syncthreads();
   }
@@ -150,8 +225,12 @@ int launch_density(const ye3t_density_args* a, void* A, hipStream_t stream) {
   const int NR = p.n_max + 1;
   const int RS = (MODE == 2) ? p.C : NR;
   // edge tile: as many edges as fit in 60 KiB of LDS, a multiple of 64, <= 256
-  const size_t per_edge = sizeof(Real) * size_t(LW + RS + (MODE == 2 ? NR : 0)) + (MODE == 1 ? sizeof(int) : 0);
-  int tile = int((60 * 1024) / per_edge) / 64 * 64;
+  constexpr int VN = Vec<Real>::N;
+  const int LWp = (LW + VN - 1) / VN * VN;
+  const size_t per_edge = sizeof(Real) * size_t(LWp + RS + (MODE == 2 ? NR : 0)) + (MODE == 1 ? sizeof(int) : 0);
+  const size_t fixed = (MODE == 2) ? sizeof(Real) * size_t(p.C) * NR : 0;
+  if (fixed > 16 * 1024) return set_error(YE3T_EUNSUPPORTED, "radial mix table too large for LDS");
+  int tile = int((60 * 1024 - fixed) / per_edge) / 64 * 64;
   if (tile > kEdgeTile) tile = kEdgeTile;
   if (tile < 64) return set_error(YE3T_EUNSUPPORTED, "density row too wide for one LDS tile (%zu B/edge)", per_edge);
   p.tile = tile;
@@ -161,7 +240,7 @@ int launch_density(const ye3t_density_args* a, void* A, hipStream_t stream) {
   if (apb < 1) apb = 1;
   if (apb > 64) apb = 64;
   p.apb = apb;
-  const size_t lds = per_edge * size_t(tile);
+  const size_t lds = per_edge * size_t(tile) + (MODE == 2 ? sizeof(Real) * size_t(p.C) * NR : 0);
   const int64_t grid = (p.N + apb - 1) / apb;
   if (grid > 0x7FFFFFFF) return set_error(YE3T_EUNSUPPORTED, "too many atoms for one launch");
   hipLaunchKernelGGL((ace_density_kernel<Real, MODE>), dim3(unsigned(grid)), dim3(kDensityThreads), lds, stream, p,
