@@ -84,7 +84,9 @@ __device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max,
     }
     return;
   }
-  const Real c = d_cos(pi * s);
+  // the envelope is evaluated in the output precision (it enters linearly);
+  // the warped variable stays in `Real` because T_n amplifies its error by n^2
+  const Real c = (sizeof(Out) < sizeof(Real) && !WithDeriv) ? Real(d_cos(float(pi * s))) : d_cos(pi * s);
   const Real sn = WithDeriv ? d_sin(pi * s) : Real(0);
   v[0] = Out(1);
   if (WithDeriv) d[0] = Out(0);

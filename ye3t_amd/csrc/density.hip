@@ -12,6 +12,9 @@
 //   phase 2  each thread owns output elements (atom, c, r, lm) and sums over
 //            that atom's edges of the tile; consecutive threads take
 //            consecutive lm, so the A row store is coalesced.
+#include <cstdlib>
+#include <type_traits>
+
 #include "common.h"
 #include "sph.h"
 
@@ -40,6 +43,16 @@ struct DensityParams {
   Real* __restrict__ A;
 };
 
+// LDS row stride (elements) of the SH tile: a multiple of the vector width,
+// odd in vector units so per-lane row writes spread over the banks.
+template <typename Real>
+inline __host__ __device__ int ys_stride(int LW) {
+  constexpr int VN = 16 / int(sizeof(Real));
+  int vecs = (LW + VN - 1) / VN;
+  if (vecs % 2 == 0) vecs += 1;
+  return vecs * VN;
+}
+
 template <typename Real>
 struct Vec;
 template <>
@@ -55,25 +68,29 @@ struct Vec<double> {
 
 // MODE 0: one channel, weight 1.  MODE 1: one-hot species channels.
 // MODE 2: node-feature weights with per-channel radial mix (one radial row).
-template <typename Real, int MODE>
+template <typename Real, int MODE, typename BasisT>
 __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityParams<Real> p, NormTable nt) {
   using V = typename Vec<Real>::T;
   constexpr int VN = Vec<Real>::N;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int LW = (p.lmax + 1) * (p.lmax + 1);
-  const int LWp = (LW + VN - 1) / VN * VN;  // padded row of the SH tile (16-byte multiple)
+  const int LWp = (LW + VN - 1) / VN * VN;  // lm values per SH row, padded to a 16-byte multiple
+  const int YS = ys_stride<Real>(LW);        // LDS row stride of the SH tile (bank spread)
+  const int HC = p.C | 1;                    // odd row stride of the feature tile
   const int NR = p.n_max + 1;
   const int rows = (MODE == 2) ? 1 : NR;
   const int RS = (MODE == 2) ? p.C : NR;
   const int T = p.tile;
-  Real* Ys = reinterpret_cast<Real*>(smem_raw);  // [T][LWp]
-  Real* Rs = Ys + T * LWp;                       // [T][RS]
+  Real* Ys = reinterpret_cast<Real*>(smem_raw);  // [T][YS]
+  Real* Rs = Ys + T * YS;                        // [T][RS]
   Real* Rt = Rs + T * RS;                        // [T][NR] raw radials (MODE 2)
   int* Sp = reinterpret_cast<int*>(Rt + (MODE == 2 ? T * NR : 0));  // [T] species (MODE 1)
-  Real* Mx = Rt + (MODE == 2 ? T * NR : 0);                          // [C][NR] radial mix (MODE 2)
+  Real* Hs = Rt + (MODE == 2 ? T * NR : 0);                          // [T][HC] neighbour features (MODE 2)
+  Real* Mx = Hs + (MODE == 2 ? T * HC : 0);                          // [C][NR] radial mix (MODE 2)
   __shared__ int64_t atom_lo[64 + 1];
 
   const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
   const int row_elems = p.C * rows * LW;
   const int groups = LWp / VN;
   const int ipa = p.C * rows * groups;  // vector items per atom
@@ -82,16 +99,17 @@ __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityPar
   const int na = int((p.N - a0) < p.apb ? (p.N - a0) : p.apb);
   if (tid <= na) atom_lo[tid] = p.offsets[a0 + tid];
   if (MODE == 2) {
-    for (int q = tid; q < p.C * NR; q += kDensityThreads) Mx[q] = p.mix[q];
+    for (int q = tid; q < p.C * NR; q += nthreads) Mx[q] = p.mix[q];
   }
   __syncthreads();
   const int64_t e_begin = atom_lo[0], e_end = atom_lo[na];
   Real* Ablk = p.A + a0 * int64_t(row_elems);
 
   // atoms without any edge still get their zero row
-  for (int k = tid; k < na * row_elems; k += kDensityThreads) {
-    const int a = k / row_elems;
-    if (atom_lo[a + 1] == atom_lo[a]) Ablk[k] = Real(0);
+  for (int a = 0; a < na; ++a) {
+    if (atom_lo[a + 1] == atom_lo[a]) {
+      for (int k = tid; k < row_elems; k += nthreads) Ablk[int64_t(a) * row_elems + k] = Real(0);
+    }
   }
 
   for (int64_t t0 = e_begin; t0 < e_end; t0 += T) {
@@ -99,28 +117,36 @@ __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityPar
     if (tid < cnt) {
       const int j = tid;
       const int64_t e = t0 + j;
-      const double x = double(p.vec[3 * e]), y = double(p.vec[3 * e + 1]), z = double(p.vec[3 * e + 2]);
-      const double r = sqrt(x * x + y * y + z * z);
-      const double sr = r > p.eps ? r : p.eps;
-      const double inv = 1.0 / sr;
-      real_sph_row<double, Real>(x * inv, y * inv, z * inv, p.lmax, nt, Ys + j * LWp, 1);
-      for (int k = LW; k < LWp; ++k) Ys[j * LWp + k] = Real(0);
+      const BasisT x = BasisT(p.vec[3 * e]), y = BasisT(p.vec[3 * e + 1]), z = BasisT(p.vec[3 * e + 2]);
+      const BasisT r = d_sqrt(x * x + y * y + z * z);
+      const BasisT sr = r > BasisT(p.eps) ? r : BasisT(p.eps);
+      const BasisT inv = BasisT(1) / sr;
+      real_sph_row<BasisT, Real>(x * inv, y * inv, z * inv, p.lmax, nt, Ys + j * YS, 1);
+      for (int k = LW; k < LWp; ++k) Ys[j * YS + k] = Real(0);
+      // the radial basis is always evaluated in fp64: the Chebyshev recurrence
+      // amplifies rounding of the warped variable by ~n^2
       if (MODE == 2) {
-        cheb_exp_cos_row<double, false, Real>(r, p.cutoff, p.lambda, p.n_max, Rt + j * NR, nullptr);
+        cheb_exp_cos_row<double, false, Real>(double(r), p.cutoff, p.lambda, p.n_max, Rt + j * NR, nullptr);
       } else {
-        cheb_exp_cos_row<double, false, Real>(r, p.cutoff, p.lambda, p.n_max, Rs + j * NR, nullptr);
+        cheb_exp_cos_row<double, false, Real>(double(r), p.cutoff, p.lambda, p.n_max, Rs + j * NR, nullptr);
       }
       if (MODE == 1) Sp[j] = p.species[p.nbr[e]];
+      if (MODE == 2) {
+        // gather the neighbour's feature row once (independent loads, one latency)
+        const Real* hrow = p.feats + p.nbr[e] * p.C;
+        Real* hdst = Hs + j * HC;
+        for (int c = 0; c < p.C; ++c) hdst[c] = hrow[c];
+      }
     }
     __syncthreads();
     if (MODE == 2) {
       // HW[j][c] = h[nbr_j, c] * sum_n mix[c, n] R_n(j)
-      if (kDensityThreads % p.C == 0) {
+      if (nthreads % p.C == 0) {
         const int c = tid % p.C;
-        const int jstep = kDensityThreads / p.C;
+        const int jstep = nthreads / p.C;
         const Real* mrow = Mx + c * NR;
         for (int j = tid / p.C; j < cnt; j += jstep) {
-          const Real h = p.feats[p.nbr[t0 + j] * p.C + c];
+          const Real h = Hs[j * HC + c];
           const Real* rrow = Rt + j * NR;
           Real r0 = Real(0), r1 = Real(0);
           int n = 0;
@@ -132,9 +158,9 @@ __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityPar
           Rs[j * p.C + c] = h * (r0 + r1);
         }
       } else {
-        for (int q = tid; q < cnt * p.C; q += kDensityThreads) {
+        for (int q = tid; q < cnt * p.C; q += nthreads) {
           const int j = q / p.C, c = q - (q / p.C) * p.C;
-          const Real h = p.feats[p.nbr[t0 + j] * p.C + c];
+          const Real h = Hs[j * HC + c];
           Real rc = Real(0);
           for (int n = 0; n < NR; ++n) rc = d_fma(Mx[c * NR + n], Rt[j * NR + n], rc);
           Rs[j * p.C + c] = h * rc;
@@ -142,60 +168,68 @@ __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityPar
       }
       __syncthreads();
     }
-    // phase 2: vector item = (atom, c, r, group of VN consecutive lm)
-    for (int item = tid; item < na * ipa; item += kDensityThreads) {
-      const int a = item / ipa;
-      const int rem = item - a * ipa;
+    // phase 2: vector item = (atom, c, r, group of VN consecutive lm).  When the
+    // per-atom item count divides the workgroup, each thread keeps one
+    // (c, r, group) and strides over atoms (decoded once).
+    const bool fixed_rem = (nthreads % ipa) == 0;
+    const int a_first = fixed_rem ? tid / ipa : 0;
+    const int a_step = fixed_rem ? nthreads / ipa : 1;
+    for (int it = fixed_rem ? tid % ipa : tid; it < (fixed_rem ? ipa : na * ipa);
+         it += fixed_rem ? ipa : nthreads) {
+      const int a_gen = fixed_rem ? 0 : it / ipa;
+      const int rem = fixed_rem ? it : it - a_gen * ipa;
       const int g = rem % groups;
       const int cr = rem / groups;  // c * rows + r
       const int c = cr / rows;
       const int rr = cr - c * rows;
-      const int64_t lo = atom_lo[a], hi = atom_lo[a + 1];
-      const int64_t j0 = lo > t0 ? lo : t0;
-      const int64_t j1 = hi < t0 + cnt ? hi : t0 + cnt;
-      if (j0 >= j1) continue;  // this atom has no edge in the tile
-      const int jb = int(j0 - t0), je = int(j1 - t0);
       const Real* rcol = (MODE == 2) ? (Rs + c) : (Rs + rr);
       const V* ycol = reinterpret_cast<const V*>(Ys + g * VN);
-      const int ystride = LWp / VN;
-      Real acc[VN], acc2[VN];
-      for (int v = 0; v < VN; ++v) {
-        acc[v] = Real(0);
-        acc2[v] = Real(0);
-      }
-      int j = jb;
-      for (; j + 2 <= je; j += 2) {
-        const V y0 = ycol[j * ystride];
-        const V y1 = ycol[(j + 1) * ystride];
-        Real w0 = rcol[j * RS], w1 = rcol[(j + 1) * RS];
-        if (MODE == 1) {
-          w0 = Sp[j] == c ? w0 : Real(0);
-          w1 = Sp[j + 1] == c ? w1 : Real(0);
-        }
-        const Real* y0p = reinterpret_cast<const Real*>(&y0);
-        const Real* y1p = reinterpret_cast<const Real*>(&y1);
-        for (int v = 0; v < VN; ++v) {
-          acc[v] = d_fma(w0, y0p[v], acc[v]);
-          acc2[v] = d_fma(w1, y1p[v], acc2[v]);
-        }
-      }
-      if (j < je) {
-        const V y0 = ycol[j * ystride];
-        Real w0 = rcol[j * RS];
-        if (MODE == 1) w0 = Sp[j] == c ? w0 : Real(0);
-        const Real* y0p = reinterpret_cast<const Real*>(&y0);
-        for (int v = 0; v < VN; ++v) acc[v] = d_fma(w0, y0p[v], acc[v]);
-      }
-      Real* dst = Ablk + int64_t(a) * row_elems + int64_t(cr) * LW + g * VN;
+      const int ystride = YS / VN;
       const int valid = (LW - g * VN) < VN ? (LW - g * VN) : VN;
-      for (int v = 0; v < VN; ++v) {
-        if (v < valid) {
-          const Real part = acc[v] + acc2[v];
-          // the first tile holding this atom's edges starts from zero
-          if (lo >= t0) {
-            dst[v] = part;
-          } else {
-            dst[v] = dst[v] + part;
+      for (int a = fixed_rem ? a_first : a_gen; a < na; a += fixed_rem ? a_step : na) {
+        const int64_t lo = atom_lo[a], hi = atom_lo[a + 1];
+        const int64_t j0 = lo > t0 ? lo : t0;
+        const int64_t j1 = hi < t0 + cnt ? hi : t0 + cnt;
+        if (j0 >= j1) continue;  // this atom has no edge in the tile
+        const int jb = int(j0 - t0), je = int(j1 - t0);
+        Real acc[VN], acc2[VN];
+        for (int v = 0; v < VN; ++v) {
+          acc[v] = Real(0);
+          acc2[v] = Real(0);
+        }
+        int j = jb;
+        for (; j + 2 <= je; j += 2) {
+          const V y0 = ycol[j * ystride];
+          const V y1 = ycol[(j + 1) * ystride];
+          Real w0 = rcol[j * RS], w1 = rcol[(j + 1) * RS];
+          if (MODE == 1) {
+            w0 = Sp[j] == c ? w0 : Real(0);
+            w1 = Sp[j + 1] == c ? w1 : Real(0);
+          }
+          const Real* y0p = reinterpret_cast<const Real*>(&y0);
+          const Real* y1p = reinterpret_cast<const Real*>(&y1);
+          for (int v = 0; v < VN; ++v) {
+            acc[v] = d_fma(w0, y0p[v], acc[v]);
+            acc2[v] = d_fma(w1, y1p[v], acc2[v]);
+          }
+        }
+        if (j < je) {
+          const V y0 = ycol[j * ystride];
+          Real w0 = rcol[j * RS];
+          if (MODE == 1) w0 = Sp[j] == c ? w0 : Real(0);
+          const Real* y0p = reinterpret_cast<const Real*>(&y0);
+          for (int v = 0; v < VN; ++v) acc[v] = d_fma(w0, y0p[v], acc[v]);
+        }
+        Real* dst = Ablk + int64_t(a) * row_elems + int64_t(cr) * LW + g * VN;
+        for (int v = 0; v < VN; ++v) {
+          if (v < valid) {
+            const Real part = acc[v] + acc2[v];
+            // the first tile holding this atom's edges starts from zero
+            if (lo >= t0) {
+              dst[v] = part;
+            } else {
+              dst[v] = dst[v] + part;
+            }
           }
         }
       }
@@ -204,8 +238,8 @@ __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityPar
   }
 }
 
-template <typename Real, int MODE>
-int launch_density(const ye3t_density_args* a, void* A, hipStream_t stream) {
+template <typename Real, int MODE, typename BasisT>
+int launch_density(const ye3t_density_args* a, void* A, hipStream_t stream, int nthreads) {
   DensityParams<Real> p;
   p.N = a->atom_count;
   p.offsets = a->row_offsets;
@@ -225,13 +259,12 @@ int launch_density(const ye3t_density_args* a, void* A, hipStream_t stream) {
   const int NR = p.n_max + 1;
   const int RS = (MODE == 2) ? p.C : NR;
   // edge tile: as many edges as fit in 60 KiB of LDS, a multiple of 64, <= 256
-  constexpr int VN = Vec<Real>::N;
-  const int LWp = (LW + VN - 1) / VN * VN;
-  const size_t per_edge = sizeof(Real) * size_t(LWp + RS + (MODE == 2 ? NR : 0)) + (MODE == 1 ? sizeof(int) : 0);
+  const int YS = ys_stride<Real>(LW);
+  const size_t per_edge = sizeof(Real) * size_t(YS + RS + (MODE == 2 ? NR + (p.C | 1) : 0)) + (MODE == 1 ? sizeof(int) : 0);
   const size_t fixed = (MODE == 2) ? sizeof(Real) * size_t(p.C) * NR : 0;
   if (fixed > 16 * 1024) return set_error(YE3T_EUNSUPPORTED, "radial mix table too large for LDS");
   int tile = int((60 * 1024 - fixed) / per_edge) / 64 * 64;
-  if (tile > kEdgeTile) tile = kEdgeTile;
+  if (tile > nthreads) tile = nthreads;
   if (tile < 64) return set_error(YE3T_EUNSUPPORTED, "density row too wide for one LDS tile (%zu B/edge)", per_edge);
   p.tile = tile;
   // atoms per block from the mean degree: about one edge tile per block
@@ -243,16 +276,40 @@ int launch_density(const ye3t_density_args* a, void* A, hipStream_t stream) {
   const size_t lds = per_edge * size_t(tile) + (MODE == 2 ? sizeof(Real) * size_t(p.C) * NR : 0);
   const int64_t grid = (p.N + apb - 1) / apb;
   if (grid > 0x7FFFFFFF) return set_error(YE3T_EUNSUPPORTED, "too many atoms for one launch");
-  hipLaunchKernelGGL((ace_density_kernel<Real, MODE>), dim3(unsigned(grid)), dim3(kDensityThreads), lds, stream, p,
+  hipLaunchKernelGGL((ace_density_kernel<Real, MODE, BasisT>), dim3(unsigned(grid)), dim3(nthreads), lds, stream, p,
                      norm_table());
   return check_launch("ace_density_kernel");
 }
 
+// Launch knobs (tuning, like the reference's YE3T_* policy variables):
+//   YE3T_DENSITY_THREADS  workgroup size, 64..256 in steps of 64 (default 256)
+//   YE3T_DENSITY_SH_FP32  1: evaluate the real SH of fp32 runs in fp32 (default: fp64)
+inline int env_int(const char* name, int fallback) {
+  const char* v = std::getenv(name);
+  return (v && *v) ? std::atoi(v) : fallback;
+}
+
+template <typename Real, int MODE>
+int launch_mode(const ye3t_density_args* a, void* A, hipStream_t s) {
+  int threads = env_int("YE3T_DENSITY_THREADS", 256);
+  if (threads < 64 || threads > 256 || threads % 64) threads = 256;
+  if (std::is_same<Real, float>::value && env_int("YE3T_DENSITY_SH_FP32", 0) == 1) {
+    return launch_density<Real, MODE, float>(a, A, s, threads);
+  }
+  return launch_density<Real, MODE, double>(a, A, s, threads);
+}
+
+int launch_density_mfma(const ye3t_density_args* a, void* A, hipStream_t stream);
+
 template <typename Real>
 int dispatch_density(const ye3t_density_args* a, void* A, hipStream_t s) {
-  if (a->node_features) return launch_density<Real, 2>(a, A, s);
-  if (a->species) return launch_density<Real, 1>(a, A, s);
-  return launch_density<Real, 0>(a, A, s);
+  // fp32 single-channel and node-feature densities run on the matrix cores
+  const int rc = launch_density_mfma(a, A, s);
+  if (rc != YE3T_EUNSUPPORTED) return rc;
+  clear_error();
+  if (a->node_features) return launch_mode<Real, 2>(a, A, s);
+  if (a->species) return launch_mode<Real, 1>(a, A, s);
+  return launch_mode<Real, 0>(a, A, s);
 }
 
 }  // namespace ye3t
