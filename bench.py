@@ -22,21 +22,47 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 
 
-def algorithmic_bytes(cfg, plan, elem):
-    """Compulsory traffic per launch (each input read once, each output written once)."""
+def algorithmic_bytes(cfg, plan, elem, a_elem):
+    """Compulsory traffic per launch (each input read once, each output written once).
+
+    ``elem``: bytes of an input / B-feature value; ``a_elem``: bytes of a density value.
+    """
     d = cfg.density
     N, K = d.atom_count, d.neighbors_per_atom
     E = N * K
     C = d.channel_count
     a_row = C * d.radial_rows * (d.l_max + 1) ** 2
-    stage1 = E * (3 * elem + 8) + (N + 1) * 8 + N * a_row * elem
+    stage1 = E * (3 * elem + 8) + (N + 1) * 8 + N * a_row * a_elem
     if d.node_channels:
         stage1 += N * d.node_channels * elem + d.node_channels * (d.n_max + 1) * elem
     if d.species_count:
         stage1 += N * 4
     samples = cfg.samples()
-    stage2 = samples * plan.a_width * elem + samples * plan.feature_count * elem
+    stage2 = samples * plan.a_width * a_elem + samples * plan.feature_count * elem
     return stage1, stage2
+
+
+def counter_traffic(kernel, workload, dtype):
+    """HBM bytes per launch from the committed rocprofv3 PMC summaries.
+
+    Each ``profiles/*.md`` summary carries ``traffic:`` lines with the mean
+    FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of one kernel on one workload,
+    and the factors that map each counter onto the bytes of a plain copy kernel
+    of known size.  Returns ``(bytes, source)`` or ``(None, None)``.
+    """
+    import glob
+
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        with open(path) as fh:
+            for line in fh:
+                if not line.startswith("traffic:"):
+                    continue
+                kv = dict(item.split("=", 1) for item in line[len("traffic:"):].split())
+                if kv.get("kernel") == kernel and kv.get("workload") == workload and kv.get("dtype") == dtype:
+                    kib = float(kv["fetch_kib"]) * float(kv["fetch_scale"]) + \
+                        float(kv["write_kib"]) * float(kv["write_scale"])
+                    return kib * 1024.0, os.path.relpath(path, ROOT)
+    return None, None
 
 
 def cpu_baseline(cfg, pipe, target_seconds=10.0):
@@ -76,14 +102,15 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=4)
-    ap.add_argument("--dtype", default=None)
+    ap.add_argument("--dtype", default=None, help="storage type of inputs and B-features (f32 / f64)")
+    ap.add_argument("--accumulate", default=None, help="type of A and of the arithmetic (default per config)")
     ap.add_argument("--max-slots", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--kernel", default="auto", choices=["auto", "generated", "interpreter"])
     ap.add_argument("--copy-probe", action="store_true",
-                    help="after the timed region, copy B once (a plain copy kernel of known size, for "
-                         "calibrating FETCH_SIZE / WRITE_SIZE counters)")
+                    help="after the timed region, negate B into a new tensor once (a plain elementwise copy "
+                         "kernel of known size, for calibrating FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -99,17 +126,20 @@ def main():
 
     cfg = W.config(args.config)
     dtype = args.dtype or cfg.dtypes[0]
+    accumulate = args.accumulate or (cfg.accumulate if dtype == "f32" else None) or dtype
     elem = 8 if dtype == "f64" else 4
+    a_elem = 8 if accumulate == "f64" else 4
     t_build = time.perf_counter()
-    pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots, kernel=args.kernel)
+    pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots, kernel=args.kernel, accumulate=accumulate)
     t_build = time.perf_counter() - t_build
     inp = cfg.density.generate()
     dev = to_device_inputs(inp, dtype, "cuda")
     d = cfg.density
     A = torch.empty((d.atom_count, d.channel_count, d.radial_rows, (d.l_max + 1) ** 2),
-                    dtype=torch.float64 if dtype == "f64" else torch.float32, device="cuda")
+                    dtype=torch.float64 if accumulate == "f64" else torch.float32, device="cuda")
     rows = A.reshape(-1, pipe.plan.a_width)
-    B = torch.empty((rows.shape[0], pipe.feature_count), dtype=A.dtype, device="cuda")
+    B = torch.empty((rows.shape[0], pipe.feature_count),
+                    dtype=torch.float64 if dtype == "f64" else torch.float32, device="cuda")
 
     def step():
         pipe.density(dev, out=A)
@@ -132,18 +162,25 @@ def main():
     wall = time.perf_counter() - t0
     copy_bytes = None
     if args.copy_probe:
+        # an elementwise kernel that reads B once and writes a same-size tensor once
         probe = torch.empty_like(B)
-        probe.copy_(B)
+        torch.neg(B, out=probe)
         torch.cuda.synchronize()
-        copy_bytes = 2 * B.numel() * B.element_size()
+        copy_bytes = {"read": B.numel() * B.element_size(), "write": probe.numel() * probe.element_size()}
     s1 = float(np.mean([a.elapsed_time(b) for a, b, _ in ev])) * 1e-3
     s2 = float(np.mean([b.elapsed_time(c) for _, b, c in ev])) * 1e-3
     ms_per_step = wall / args.steps * 1e3
-    b1, b2 = algorithmic_bytes(cfg, pipe.plan, elem)
+    b1, b2 = algorithmic_bytes(cfg, pipe.plan, elem, a_elem)
     k2 = "ye3t_product_generated" if pipe.kernel == "generated" else "product_kernel"
     features = rows.shape[0] * pipe.feature_count
     value = features / (wall / args.steps)
     stats = program_stats(pipe.program)
+    workload = f"config{cfg.config_id}-{cfg.name}"
+    traffic, traffic_src = counter_traffic(k2, workload, accumulate)
+    # fp32 single-channel / node-feature densities run on the matrix-core kernel
+    k1 = ("ace_density_mfma_kernel" if accumulate == "f32" and not d.species_count
+          and os.environ.get("YE3T_DENSITY_MFMA", "1") != "0" else "ace_density_kernel")
+    traffic1, traffic1_src = counter_traffic(k1, workload, accumulate)
     line = {
         "metric": "B-features/sec (atoms/s) on 1 MI355X; achieved HBM GB/s vs peak",
         "value": value,
@@ -155,19 +192,22 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": dtype,
+        "dtype": accumulate,
+        "storage_dtype": dtype,
         "data": "synthetic (seeded counter RNG, BASELINE.json configuration shapes)",
-        "config": {"workload": f"config{cfg.config_id}-{cfg.name}", "atoms": d.atom_count,
+        "config": {"workload": workload, "atoms": d.atom_count,
                    "neighbors_per_atom": d.neighbors_per_atom, "channels": d.channel_count,
                    "samples": int(rows.shape[0]), "features_per_sample": pipe.feature_count,
                    "n_max": d.n_max, "l_max": d.l_max, "nu_max": cfg.feature_spec.nu_max,
                    "targets": list(cfg.feature_spec.targets), "parallelism": "single GPU"},
         "atoms_per_s": d.atom_count / (wall / args.steps),
         "roofline": {"bound": "hbm", "achieved": b2 / s2 / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": b2 / s2 / 1e9 / HBM_PEAK_GBS, "traffic": None, "kernel": k2,
+                     "frac": b2 / s2 / 1e9 / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
+                     "kernel": k2,
                      "algorithmic_bytes": b2, "avg_kernel_us": s2 * 1e6},
-        "stage1": {"kernel": "ace_density_kernel", "avg_kernel_us": s1 * 1e6, "algorithmic_bytes": b1,
-                   "achieved_gbs": b1 / s1 / 1e9, "frac": b1 / s1 / 1e9 / HBM_PEAK_GBS},
+        "stage1": {"kernel": k1, "avg_kernel_us": s1 * 1e6, "algorithmic_bytes": b1,
+                   "achieved_gbs": b1 / s1 / 1e9, "frac": b1 / s1 / 1e9 / HBM_PEAK_GBS,
+                   "traffic": traffic1, "traffic_source": traffic1_src},
         "stage2": {"kernel": k2, "avg_kernel_us": s2 * 1e6, "algorithmic_bytes": b2,
                    "achieved_gbs": b2 / s2 / 1e9, "frac": b2 / s2 / 1e9 / HBM_PEAK_GBS,
                    "program": stats, "plan_compile_s": t_build, "product_kernel": pipe.kernel},

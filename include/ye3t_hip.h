@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 43 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 44 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -104,6 +104,8 @@ typedef struct {
   double cutoff;
   double lambda;
   double epsilon;
+  int out_dtype;                /* dtype of A and of the accumulation; -1 = dtype.  YE3T_F64 with
+                                   dtype YE3T_F32 keeps fp32 inputs but an fp64 density */
 } ye3t_density_args;
 
 /* A has shape [N, C, R, (l_max+1)^2] with R = 1 when radial_mix is set, else n_max+1. */
@@ -149,6 +151,8 @@ typedef struct {
   int64_t coeff_count;
   const uint16_t* out_slots;    /* host workspace slot of each output column, chunk-major */
   int64_t out_slot_count;
+  int out_dtype;                /* dtype of B; -1 = dtype.  A and the arithmetic use dtype, so an
+                                   fp64 plan may write fp32 features (rounded once, at the store) */
 } ye3t_product_plan_desc;
 
 typedef struct ye3t_hip_product_plan ye3t_hip_product_plan;
@@ -158,7 +162,7 @@ typedef struct ye3t_hip_product_plan ye3t_hip_product_plan;
 int ye3t_hip_product_plan_create(const ye3t_product_plan_desc* desc, ye3t_hip_product_plan** out);
 void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* plan);
 
-/* B[samples, feature_count] from A[samples, a_width].  Replaces the CUDA
+/* B[samples, feature_count] (out_dtype) from A[samples, a_width] (dtype).  Replaces the CUDA
  * factorized_angular forward (execution_plan_cuda.cu:6228-6358, launcher
  * :11488-11672; schema execution_plan_torch.cpp:7586-7594) for ACE products. */
 int ye3t_hip_product_forward(const ye3t_hip_product_plan* plan, const void* A, int64_t samples, void* B,
@@ -174,7 +178,7 @@ void ye3t_hip_free(void* ptr);
 /* Attach a plan-specialised kernel (code object from ye3t_hip_rtc_compile of
  * ye3t_amd/ace/codegen.py output) to `plan`; product_forward then launches it
  * with grid (ceil(samples/64), chunk_count).  The kernel signature is
- * (const T* A, long samples, T* B). */
+ * (const T* A, long samples, U* B), T = the plan's dtype, U = its out_dtype. */
 int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* plan, const void* code, int64_t size,
                                            const char* kernel_name, int64_t chunk_count);
 

@@ -220,17 +220,58 @@ def test_generated_and_interpreter_agree_on_config4(gpu):
     assert err < 2e-5
 
 
-@pytest.mark.parametrize("cid,dtype", [(4, "f32"), (2, "f64")])
-def test_end_to_end_small(gpu, cid, dtype):
-    flush(f"end to end config {cid} {dtype}")
-    cfg = W.config(cid, atom_count=257)
+@pytest.mark.parametrize("cid,dtype,atoms", [(4, "f32", 257), (2, "f64", 257), (3, "f64", 67), (3, "f32", 67),
+                                              (5, "f32", 33)])
+def test_end_to_end_small(gpu, cid, dtype, atoms):
+    """Full feature plans of every density configuration, on a few seeded atoms."""
+    flush(f"end to end config {cid} {dtype} atoms={atoms}")
+    cfg = W.config(cid, atom_count=atoms)
     inp = cfg.density.generate()
-    pipe = ACEPipeline(cfg.feature_spec, dtype)
+    pipe = ACEPipeline(cfg.feature_spec, dtype, accumulate=cfg.accumulate if dtype == "f32" else None)
+    flush(f"  plan built: {pipe.feature_count} features, kernel {pipe.kernel}, accumulate {pipe.accumulate}")
     A, B = pipe.forward(to_device_inputs(inp, dtype, gpu), channelwise=cfg.channelwise)
     A_ref = oracle.ace_density(rounded_inputs(inp, dtype))
-    assert column_rel_error(A.cpu().numpy().reshape(257, -1), A_ref.reshape(257, -1)) < TOL[dtype]
+    assert column_rel_error(A.cpu().numpy().reshape(atoms, -1), A_ref.reshape(atoms, -1)) < TOL[dtype]
     rows = A_ref.reshape(-1, pipe.plan.a_width)
     B_ref = oracle.ace_product_flat(rows, pipe.plan.flat_arrays())
     err = column_rel_error(B.cpu().numpy(), B_ref)
     flush(f"  err {err:.3e}")
     assert err < TOL[dtype]
+
+
+@pytest.mark.parametrize("kernel", ["interpreter", "generated"])
+def test_fp64_plan_with_fp32_features(gpu, kernel):
+    """accumulate=f64 with f32 storage: only the final store rounds."""
+    flush(f"mixed precision product, kernel {kernel}")
+    import torch
+
+    pipe = ACEPipeline(W.config(4).feature_spec, "f32", kernel=kernel, accumulate="f64")
+    A = np.random.default_rng(15).normal(size=(300, pipe.plan.a_width))
+    B = pipe.product(torch.as_tensor(A, dtype=torch.float64, device=gpu))
+    assert B.dtype == torch.float32
+    ref = oracle.ace_product_flat(A, pipe.plan.flat_arrays())
+    # per column, relative to the column RMS: the fp32 rounding of the result only
+    err = column_rel_error(B.cpu().numpy(), ref)
+    flush(f"  err {err:.3e}")
+    assert err < 1e-6
+
+
+@pytest.mark.parametrize("mode", ["single", "species", "features"])
+def test_fp64_density_of_fp32_inputs(gpu, mode):
+    """out_dtype=f64 with f32 inputs: the fp64 density of the fp32-rounded data."""
+    flush(f"fp64 density of fp32 inputs, {mode}")
+    import torch
+
+    inp = _ragged_workload(mode)
+    dev = to_device_inputs(inp, "f32", gpu)
+    A = native.ace_density_forward(
+        dev["edge_vectors"], dev["row_offsets"], dev["neighbors"], atom_count=inp["atom_count"],
+        channel_count=inp["channel_count"], n_max=inp["n_max"], l_max=inp["l_max"], cutoff=inp["cutoff"],
+        lam=inp["lambda"], epsilon=inp["epsilon"], species=dev.get("species"), node_features=dev.get("node_features"),
+        radial_mix=dev.get("radial_mix"), out_dtype=torch.float64)
+    assert A.dtype == torch.float64
+    ref = oracle.ace_density(rounded_inputs(inp, "f32"))
+    N = inp["atom_count"]
+    err = column_rel_error(A.cpu().numpy().reshape(N, -1), ref.reshape(N, -1))
+    flush(f"  err {err:.3e}")
+    assert err < TOL["f64"]

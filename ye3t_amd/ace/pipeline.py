@@ -36,15 +36,27 @@ GENERATED_MAX_TERMS = 5000
 
 
 class ACEPipeline:
-    """``kernel``: "auto" (generated kernel when the plan is small enough),
+    """``dtype``: storage type of the inputs and of the B-features.
+
+    ``accumulate``: type of the density ``A`` and of all arithmetic (default:
+    ``dtype``).  "f64" with ``dtype="f32"`` keeps fp32 inputs and outputs but
+    carries the density and the CG products in fp64, for plans whose features
+    cancel too strongly for fp32 intermediates.
+
+    ``kernel``: "auto" (generated kernel when the plan is small enough),
     "generated" or "interpreter" (the generic table-driven product kernel)."""
 
-    def __init__(self, feature_spec, dtype="f32", max_slots=None, plan=None, kernel="auto", max_live=None):
+    def __init__(self, feature_spec, dtype="f32", max_slots=None, plan=None, kernel="auto", max_live=None,
+                 accumulate=None):
         self.spec = feature_spec
         self.dtype = dtype
+        self.accumulate = accumulate or dtype
+        if dtype not in ("f32", "f64") or self.accumulate not in ("f32", "f64") or (
+                dtype == "f64" and self.accumulate == "f32"):
+            raise ValueError(f"unsupported precision: dtype {dtype!r}, accumulate {accumulate!r}")
         self.plan = plan if plan is not None else ProductPlan(feature_spec)
-        self.program = compile_program(self.plan, dtype, max_slots)
-        self.handle = native.ProductPlanHandle(self.program)
+        self.program = compile_program(self.plan, self.accumulate, max_slots)
+        self.handle = native.ProductPlanHandle(self.program, out_dtype=dtype)
         terms = sum(len(nd.get("terms", ())) for nd in self.plan.nodes)
         use_gen = kernel == "generated" or (kernel == "auto" and terms <= GENERATED_MAX_TERMS)
         if kernel not in {"auto", "generated", "interpreter"}:
@@ -53,7 +65,7 @@ class ACEPipeline:
         if use_gen:
             from ye3t_amd.ace.codegen import generate
 
-            source, meta = generate(self.plan, dtype, max_live)
+            source, meta = generate(self.plan, self.accumulate, max_live, out_dtype=dtype)
             self.handle.attach_generated(source, meta)
             self.kernel = "generated"
 
@@ -62,13 +74,16 @@ class ACEPipeline:
         return self.plan.feature_count
 
     def density(self, dev_inp, out=None):
+        import torch
+
         return native.ace_density_forward(
             dev_inp["edge_vectors"], dev_inp["row_offsets"], dev_inp["neighbors"],
             atom_count=int(dev_inp["atom_count"]), channel_count=int(dev_inp["channel_count"]),
             n_max=int(dev_inp["n_max"]), l_max=int(dev_inp["l_max"]), cutoff=float(dev_inp["cutoff"]),
             lam=float(dev_inp["lambda"]), epsilon=float(dev_inp.get("epsilon", 1e-12)),
             species=dev_inp.get("species"), node_features=dev_inp.get("node_features"),
-            radial_mix=dev_inp.get("radial_mix"), out=out)
+            radial_mix=dev_inp.get("radial_mix"), out=out,
+            out_dtype=torch.float64 if self.accumulate == "f64" else torch.float32)
 
     def product(self, A_rows, out=None):
         return self.handle.forward(A_rows, out=out)

@@ -132,6 +132,7 @@ class Config:
     feature_spec: ACEFeatureSpec = None
     dtypes: tuple = ("f64",)
     channelwise: bool = False       # samples are (atom, channel) rows of A
+    accumulate: str = None          # type of A and of the arithmetic (None: the storage dtype)
     note: str = ""
 
     def samples(self):
@@ -160,8 +161,11 @@ def config(config_id, *, atom_count=None):
     if config_id == 5:
         d = DensityWorkload(atom_count or 200000, 48, 5.5, 0.8, 12, 6, species_count=8, config_id=5)
         spec = ACEFeatureSpec(channel_count=104, l_max=6, nu_max=4, targets=(0, 1, 2), parity="any",
-                              radial_per_species=13, caps={1: (13, 2), 2: (4, 6), 3: (2, 3), 4: (1, 2)})
-        return Config(5, "large-scale-stress", d, spec, ("f32",))
+                              radial_per_species=13, caps={1: (13, 2), 2: (4, 6), 3: (1, 3), 4: (1, 1)})
+        # fp32 storage, fp64 intermediates: odd-L couplings of two l=6 densities of
+        # neighbouring radial channels cancel to ~1e-4 of their terms, beyond what
+        # fp32 intermediates resolve at the 2e-5 feature tolerance
+        return Config(5, "large-scale-stress", d, spec, ("f32",), accumulate="f64")
     raise ValueError(f"unknown config {config_id}")
 
 

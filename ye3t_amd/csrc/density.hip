@@ -23,15 +23,16 @@ namespace ye3t {
 constexpr int kDensityThreads = 256;
 constexpr int kEdgeTile = 256;
 
-template <typename Real>
+// Real: accumulation and A storage type; In: storage type of the inputs.
+template <typename Real, typename In>
 struct DensityParams {
   int64_t N;
   const int64_t* __restrict__ offsets;
   const int64_t* __restrict__ nbr;
-  const Real* __restrict__ vec;
+  const In* __restrict__ vec;
   const int32_t* __restrict__ species;
-  const Real* __restrict__ feats;
-  const Real* __restrict__ mix;
+  const In* __restrict__ feats;
+  const In* __restrict__ mix;
   int C;
   int n_max;
   int lmax;
@@ -68,8 +69,8 @@ struct Vec<double> {
 
 // MODE 0: one channel, weight 1.  MODE 1: one-hot species channels.
 // MODE 2: node-feature weights with per-channel radial mix (one radial row).
-template <typename Real, int MODE, typename BasisT>
-__global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityParams<Real> p, NormTable nt) {
+template <typename Real, int MODE, typename BasisT, typename In>
+__global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityParams<Real, In> p, NormTable nt) {
   using V = typename Vec<Real>::T;
   constexpr int VN = Vec<Real>::N;
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityPar
   const int na = int((p.N - a0) < p.apb ? (p.N - a0) : p.apb);
   if (tid <= na) atom_lo[tid] = p.offsets[a0 + tid];
   if (MODE == 2) {
-    for (int q = tid; q < p.C * NR; q += nthreads) Mx[q] = p.mix[q];
+    for (int q = tid; q < p.C * NR; q += nthreads) Mx[q] = Real(p.mix[q]);
   }
   __syncthreads();
   const int64_t e_begin = atom_lo[0], e_end = atom_lo[na];
@@ -133,9 +134,9 @@ __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityPar
       if (MODE == 1) Sp[j] = p.species[p.nbr[e]];
       if (MODE == 2) {
         // gather the neighbour's feature row once (independent loads, one latency)
-        const Real* hrow = p.feats + p.nbr[e] * p.C;
+        const In* hrow = p.feats + p.nbr[e] * p.C;
         Real* hdst = Hs + j * HC;
-        for (int c = 0; c < p.C; ++c) hdst[c] = hrow[c];
+        for (int c = 0; c < p.C; ++c) hdst[c] = Real(hrow[c]);
       }
     }
     __syncthreads();
@@ -238,16 +239,16 @@ __global__ __launch_bounds__(kDensityThreads) void ace_density_kernel(DensityPar
   }
 }
 
-template <typename Real, int MODE, typename BasisT>
+template <typename Real, int MODE, typename BasisT, typename In>
 int launch_density(const ye3t_density_args* a, void* A, hipStream_t stream, int nthreads) {
-  DensityParams<Real> p;
+  DensityParams<Real, In> p;
   p.N = a->atom_count;
   p.offsets = a->row_offsets;
   p.nbr = a->neighbors;
-  p.vec = static_cast<const Real*>(a->edge_vectors);
+  p.vec = static_cast<const In*>(a->edge_vectors);
   p.species = a->species;
-  p.feats = static_cast<const Real*>(a->node_features);
-  p.mix = static_cast<const Real*>(a->radial_mix);
+  p.feats = static_cast<const In*>(a->node_features);
+  p.mix = static_cast<const In*>(a->radial_mix);
   p.C = int(a->channel_count);
   p.n_max = int(a->max_radial_index);
   p.lmax = int(a->max_angular);
@@ -276,8 +277,8 @@ int launch_density(const ye3t_density_args* a, void* A, hipStream_t stream, int 
   const size_t lds = per_edge * size_t(tile) + (MODE == 2 ? sizeof(Real) * size_t(p.C) * NR : 0);
   const int64_t grid = (p.N + apb - 1) / apb;
   if (grid > 0x7FFFFFFF) return set_error(YE3T_EUNSUPPORTED, "too many atoms for one launch");
-  hipLaunchKernelGGL((ace_density_kernel<Real, MODE, BasisT>), dim3(unsigned(grid)), dim3(nthreads), lds, stream, p,
-                     norm_table());
+  hipLaunchKernelGGL((ace_density_kernel<Real, MODE, BasisT, In>), dim3(unsigned(grid)), dim3(nthreads), lds, stream,
+                     p, norm_table());
   return check_launch("ace_density_kernel");
 }
 
@@ -289,27 +290,29 @@ inline int env_int(const char* name, int fallback) {
   return (v && *v) ? std::atoi(v) : fallback;
 }
 
-template <typename Real, int MODE>
+template <typename Real, int MODE, typename In>
 int launch_mode(const ye3t_density_args* a, void* A, hipStream_t s) {
   int threads = env_int("YE3T_DENSITY_THREADS", 256);
   if (threads < 64 || threads > 256 || threads % 64) threads = 256;
   if (std::is_same<Real, float>::value && env_int("YE3T_DENSITY_SH_FP32", 0) == 1) {
-    return launch_density<Real, MODE, float>(a, A, s, threads);
+    return launch_density<Real, MODE, float, In>(a, A, s, threads);
   }
-  return launch_density<Real, MODE, double>(a, A, s, threads);
+  return launch_density<Real, MODE, double, In>(a, A, s, threads);
 }
 
 int launch_density_mfma(const ye3t_density_args* a, void* A, hipStream_t stream);
 
-template <typename Real>
+template <typename Real, typename In>
 int dispatch_density(const ye3t_density_args* a, void* A, hipStream_t s) {
-  // fp32 single-channel and node-feature densities run on the matrix cores
-  const int rc = launch_density_mfma(a, A, s);
-  if (rc != YE3T_EUNSUPPORTED) return rc;
-  clear_error();
-  if (a->node_features) return launch_mode<Real, 2>(a, A, s);
-  if (a->species) return launch_mode<Real, 1>(a, A, s);
-  return launch_mode<Real, 0>(a, A, s);
+  if (std::is_same<Real, float>::value) {
+    // fp32 single-channel and node-feature densities run on the matrix cores
+    const int rc = launch_density_mfma(a, A, s);
+    if (rc != YE3T_EUNSUPPORTED) return rc;
+    clear_error();
+  }
+  if (a->node_features) return launch_mode<Real, 2, In>(a, A, s);
+  if (a->species) return launch_mode<Real, 1, In>(a, A, s);
+  return launch_mode<Real, 0, In>(a, A, s);
 }
 
 }  // namespace ye3t
@@ -332,7 +335,9 @@ extern "C" int ye3t_hip_ace_density_forward(const ye3t_density_args* a, void* A,
   YE3T_REQUIRE(a->row_offsets && A, "NULL row_offsets or output");
   YE3T_REQUIRE(a->edge_count == 0 || (a->edge_vectors && (a->neighbors || (!a->species && !a->node_features))),
                "NULL edge arrays");
-  if (a->dtype == YE3T_F64) return dispatch_density<double>(a, A, as_stream(stream));
-  if (a->dtype == YE3T_F32) return dispatch_density<float>(a, A, as_stream(stream));
-  return set_error(YE3T_EDTYPE, "unsupported dtype %d", a->dtype);
+  const int out_dtype = a->out_dtype < 0 ? a->dtype : a->out_dtype;
+  if (a->dtype == YE3T_F64 && out_dtype == YE3T_F64) return dispatch_density<double, double>(a, A, as_stream(stream));
+  if (a->dtype == YE3T_F32 && out_dtype == YE3T_F32) return dispatch_density<float, float>(a, A, as_stream(stream));
+  if (a->dtype == YE3T_F32 && out_dtype == YE3T_F64) return dispatch_density<double, float>(a, A, as_stream(stream));
+  return set_error(YE3T_EDTYPE, "unsupported dtype pair (inputs %d, density %d)", a->dtype, out_dtype);
 }

@@ -20,7 +20,8 @@
 #include "common.h"
 
 struct ye3t_hip_product_plan {
-  int dtype;
+  int dtype;      // A, coefficients and arithmetic
+  int out_dtype;  // B
   int64_t a_width;
   int64_t feature_count;
   int64_t chunk_count;
@@ -47,9 +48,9 @@ constexpr int kPad = 65;  // LDS row stride in elements
 
 enum : uint32_t { OP_LOAD = 1, OP_ACC1 = 2, OP_ACC2 = 3, OP_ACC3 = 4, OP_ACC4 = 5 };
 
-template <typename Real>
+template <typename Real, typename Out>
 __global__ __launch_bounds__(kLanes) void product_kernel(
-    const Real* __restrict__ A, int64_t samples, int64_t a_width, Real* __restrict__ B, int64_t F,
+    const Real* __restrict__ A, int64_t samples, int64_t a_width, Out* __restrict__ B, int64_t F,
     const uint32_t* __restrict__ words, const int64_t* __restrict__ word_off, const Real* __restrict__ coeffs,
     const int64_t* __restrict__ coeff_off, const uint16_t* __restrict__ out_slots,
     const int64_t* __restrict__ out_off, const int64_t* __restrict__ first_col, int64_t chunks) {
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(kLanes) void product_kernel(
   for (int idx = lane; idx < total; idx += kLanes) {
     const int r = idx / nf;
     const int c = idx - r * nf;
-    B[(s0 + r) * F + c0 + c] = ws[int(out_slots[o0 + c]) * kPad + r];
+    B[(s0 + r) * F + c0 + c] = Out(ws[int(out_slots[o0 + c]) * kPad + r]);
   }
 }
 
@@ -232,6 +233,9 @@ int ye3t_hip_product_plan_create(const ye3t_product_plan_desc* d, ye3t_hip_produ
   YE3T_REQUIRE(d && out, "NULL plan description or output");
   *out = nullptr;
   YE3T_REQUIRE(d->dtype == YE3T_F32 || d->dtype == YE3T_F64, "unsupported dtype %d", d->dtype);
+  const int out_dtype = d->out_dtype < 0 ? d->dtype : d->out_dtype;
+  YE3T_REQUIRE(out_dtype == d->dtype || (d->dtype == YE3T_F64 && out_dtype == YE3T_F32),
+               "unsupported output dtype %d for a plan of dtype %d", d->out_dtype, d->dtype);
   YE3T_REQUIRE(d->chunk_count >= 1 && d->a_width >= 1 && d->a_width <= 65536 && d->feature_count >= 1,
                "bad plan sizes");
   YE3T_REQUIRE(d->workspace_slots >= 1 && d->workspace_slots <= 65535, "bad workspace size");
@@ -283,6 +287,7 @@ int ye3t_hip_product_plan_create(const ye3t_product_plan_desc* d, ye3t_hip_produ
   }
   auto* p = new ye3t_hip_product_plan();
   p->dtype = d->dtype;
+  p->out_dtype = out_dtype;
   p->a_width = d->a_width;
   p->feature_count = d->feature_count;
   p->chunk_count = C;
@@ -403,13 +408,18 @@ int ye3t_hip_product_forward(const ye3t_hip_product_plan* p, const void* A, int6
   const int64_t grid = tiles * p->chunk_count;
   YE3T_REQUIRE(grid <= int64_t(0x7FFFFFFF), "too many samples for one launch");
   const size_t lds = product_lds_bytes(p);
-  if (p->dtype == YE3T_F64) {
-    hipLaunchKernelGGL(product_kernel<double>, dim3(unsigned(grid)), dim3(kLanes), lds, as_stream(stream),
+  if (p->dtype == YE3T_F64 && p->out_dtype == YE3T_F64) {
+    hipLaunchKernelGGL((product_kernel<double, double>), dim3(unsigned(grid)), dim3(kLanes), lds, as_stream(stream),
                        (const double*)A, samples, p->a_width, (double*)B, p->feature_count, p->words, p->word_off,
                        (const double*)p->coeffs, p->coeff_off, p->out_slots, p->out_off, p->first_col,
                        p->chunk_count);
+  } else if (p->dtype == YE3T_F64) {
+    hipLaunchKernelGGL((product_kernel<double, float>), dim3(unsigned(grid)), dim3(kLanes), lds, as_stream(stream),
+                       (const double*)A, samples, p->a_width, (float*)B, p->feature_count, p->words, p->word_off,
+                       (const double*)p->coeffs, p->coeff_off, p->out_slots, p->out_off, p->first_col,
+                       p->chunk_count);
   } else {
-    hipLaunchKernelGGL(product_kernel<float>, dim3(unsigned(grid)), dim3(kLanes), lds, as_stream(stream),
+    hipLaunchKernelGGL((product_kernel<float, float>), dim3(unsigned(grid)), dim3(kLanes), lds, as_stream(stream),
                        (const float*)A, samples, p->a_width, (float*)B, p->feature_count, p->words, p->word_off,
                        (const float*)p->coeffs, p->coeff_off, p->out_slots, p->out_off, p->first_col,
                        p->chunk_count);

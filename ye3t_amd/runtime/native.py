@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 43
+ABI_VERSION = 44
 _LIB = None
 
 F32, F64 = 0, 1
@@ -26,14 +26,15 @@ class DensityArgs(ctypes.Structure):
                 ("row_offsets", _vp), ("neighbors", _vp), ("edge_vectors", _vp), ("species", _vp),
                 ("node_features", _vp), ("radial_mix", _vp), ("channel_count", _i64),
                 ("max_radial_index", _i64), ("max_angular", _i64), ("cutoff", ctypes.c_double),
-                ("lambda_", ctypes.c_double), ("epsilon", ctypes.c_double)]
+                ("lambda_", ctypes.c_double), ("epsilon", ctypes.c_double), ("out_dtype", ctypes.c_int)]
 
 
 class ProductPlanDesc(ctypes.Structure):
     _fields_ = [("dtype", ctypes.c_int), ("a_width", _i64), ("feature_count", _i64), ("chunk_count", _i64),
                 ("workspace_slots", _i64), ("chunk_word_offsets", _vp), ("chunk_coeff_offsets", _vp),
                 ("chunk_out_offsets", _vp), ("chunk_first_column", _vp), ("words", _vp), ("word_count", _i64),
-                ("coeffs", _vp), ("coeff_count", _i64), ("out_slots", _vp), ("out_slot_count", _i64)]
+                ("coeffs", _vp), ("coeff_count", _i64), ("out_slots", _vp), ("out_slot_count", _i64),
+                ("out_dtype", ctypes.c_int)]
 
 
 class Caps(ctypes.Structure):
@@ -185,16 +186,23 @@ def density_accumulate_csr(edge_values, row_offsets, atom_count):
 
 
 def ace_density_forward(edge_vectors, row_offsets, neighbors, *, atom_count, channel_count, n_max, l_max, cutoff,
-                        lam, epsilon=1e-12, species=None, node_features=None, radial_mix=None, out=None):
-    """Fused stage 1; returns ``A[N, C, R, (l_max+1)^2]``."""
+                        lam, epsilon=1e-12, species=None, node_features=None, radial_mix=None, out=None,
+                        out_dtype=None):
+    """Fused stage 1; returns ``A[N, C, R, (l_max+1)^2]``.
+
+    ``out_dtype`` (a torch dtype, default: that of the inputs) is the type of
+    ``A`` and of the accumulation; float64 with float32 inputs gives an fp64
+    density of fp32 data.
+    """
     import torch
 
     rows = 1 if radial_mix is not None else n_max + 1
     shape = (atom_count, channel_count, rows, (l_max + 1) ** 2)
+    a_dtype = edge_vectors.dtype if out_dtype is None else out_dtype
     if out is None:
-        out = torch.empty(shape, dtype=edge_vectors.dtype, device=edge_vectors.device)
-    elif tuple(out.shape) != shape or out.dtype != edge_vectors.dtype:
-        raise ValueError(f"out must be {shape} of dtype {edge_vectors.dtype}")
+        out = torch.empty(shape, dtype=a_dtype, device=edge_vectors.device)
+    elif tuple(out.shape) != shape or out.dtype != a_dtype:
+        raise ValueError(f"out must be {shape} of dtype {a_dtype}")
     if row_offsets.dtype != torch.int64 or row_offsets.shape != (atom_count + 1,):
         raise ValueError("row_offsets must be int64 [N+1]")
     if neighbors is not None and neighbors.dtype != torch.int64:
@@ -210,7 +218,7 @@ def ace_density_forward(edge_vectors, row_offsets, neighbors, *, atom_count, cha
         edge_vectors=_dev(edge_vectors, "edge_vectors"), species=_opt(species, "species"),
         node_features=_opt(node_features, "node_features"), radial_mix=_opt(radial_mix, "radial_mix"),
         channel_count=int(channel_count), max_radial_index=int(n_max), max_angular=int(l_max),
-        cutoff=float(cutoff), lambda_=float(lam), epsilon=float(epsilon))
+        cutoff=float(cutoff), lambda_=float(lam), epsilon=float(epsilon), out_dtype=_dtype_code(out))
     _check(lib().ye3t_hip_ace_density_forward(ctypes.byref(args), _dev(out, "A"), _stream()),
            "ye3t_hip_ace_density_forward")
     return out
@@ -301,11 +309,18 @@ def rtc_compile(source, name="ye3t_generated.hip", arch="gfx950"):
 
 
 class ProductPlanHandle:
-    """Device-resident compiled product program (owns a ``ye3t_hip_product_plan``)."""
+    """Device-resident compiled product program (owns a ``ye3t_hip_product_plan``).
 
-    def __init__(self, program):
+    ``A`` and the arithmetic use the program's dtype; ``out_dtype`` ("f32" or
+    "f64", default: the same) is the type of the B-features.
+    """
+
+    def __init__(self, program, out_dtype=None):
         self.program = program
         self.dtype = program["dtype"]
+        self.out_dtype = out_dtype or self.dtype
+        if self.out_dtype not in ("f32", "f64") or (self.dtype == "f32" and self.out_dtype == "f64"):
+            raise ValueError(f"unsupported output dtype {self.out_dtype!r} for a {self.dtype} plan")
         self._keep = {k: np.ascontiguousarray(v) for k, v in program.items() if isinstance(v, np.ndarray)}
         k = self._keep
 
@@ -319,7 +334,7 @@ class ProductPlanHandle:
             chunk_coeff_offsets=ptr("chunk_coeff_offsets"), chunk_out_offsets=ptr("chunk_out_offsets"),
             chunk_first_column=ptr("chunk_first_column"), words=ptr("words"), word_count=int(k["words"].size),
             coeffs=ptr("coeffs"), coeff_count=int(k["coeffs"].size), out_slots=ptr("out_slots"),
-            out_slot_count=int(k["out_slots"].size))
+            out_slot_count=int(k["out_slots"].size), out_dtype=F64 if self.out_dtype == "f64" else F32)
         handle = ctypes.c_void_p()
         _check(lib().ye3t_hip_product_plan_create(ctypes.byref(desc), ctypes.byref(handle)),
                "ye3t_hip_product_plan_create")
@@ -339,8 +354,8 @@ class ProductPlanHandle:
         """Compile and attach a plan-specialised kernel (``ye3t_amd.ace.codegen``)."""
         if meta["feature_count"] != self.feature_count or meta["a_width"] != self.program["a_width"]:
             raise ValueError("generated kernel does not match this plan")
-        if meta["dtype"] != self.dtype:
-            raise ValueError("generated kernel dtype does not match this plan")
+        if meta["dtype"] != self.dtype or meta.get("out_dtype", meta["dtype"]) != self.out_dtype:
+            raise ValueError("generated kernel dtypes do not match this plan")
         blob = rtc_compile(source)
         self._code = ctypes.create_string_buffer(blob, len(blob))
         _check(lib().ye3t_hip_product_plan_attach_generated(self._handle, self._code, len(blob),
@@ -366,10 +381,11 @@ class ProductPlanHandle:
         want = torch.float64 if self.dtype == "f64" else torch.float32
         if A.dtype != want:
             raise ValueError(f"A must be {want} for this plan")
+        out_t = torch.float64 if self.out_dtype == "f64" else torch.float32
         S = int(A.shape[0])
         if out is None:
-            out = torch.empty((S, self.feature_count), dtype=A.dtype, device=A.device)
-        elif tuple(out.shape) != (S, self.feature_count) or out.dtype != A.dtype:
+            out = torch.empty((S, self.feature_count), dtype=out_t, device=A.device)
+        elif tuple(out.shape) != (S, self.feature_count) or out.dtype != out_t:
             raise ValueError("out has the wrong shape or dtype")
         _check(lib().ye3t_hip_product_forward(self._handle, _dev(A, "A"), S, _dev(out, "B"), _stream()),
                "ye3t_hip_product_forward")
