@@ -123,6 +123,7 @@ def main():
     from ye3t_amd.ace import workloads as W
     from ye3t_amd.ace.pipeline import ACEPipeline, to_device_inputs
     from ye3t_amd.ace.program import program_stats
+    from ye3t_amd.runtime import native
 
     cfg = W.config(args.config)
     dtype = args.dtype or cfg.dtypes[0]
@@ -177,9 +178,7 @@ def main():
     stats = program_stats(pipe.program)
     workload = f"config{cfg.config_id}-{cfg.name}"
     traffic, traffic_src = counter_traffic(k2, workload, accumulate)
-    # fp32 single-channel / node-feature densities run on the matrix-core kernel
-    k1 = ("ace_density_mfma_kernel" if accumulate == "f32" and not d.species_count
-          and os.environ.get("YE3T_DENSITY_MFMA", "1") != "0" else "ace_density_kernel")
+    k1 = native.last_density_kernel()
     traffic1, traffic1_src = counter_traffic(k1, workload, accumulate)
     line = {
         "metric": "B-features/sec (atoms/s) on 1 MI355X; achieved HBM GB/s vs peak",

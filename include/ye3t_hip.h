@@ -111,6 +111,10 @@ typedef struct {
 /* A has shape [N, C, R, (l_max+1)^2] with R = 1 when radial_mix is set, else n_max+1. */
 int ye3t_hip_ace_density_forward(const ye3t_density_args* args, void* A, ye3t_stream_t stream);
 
+/* Name of the kernel the last ye3t_hip_ace_density_forward call on this thread
+ * launched ("" if none), for profiling.  No reference counterpart. */
+const char* ye3t_hip_last_density_kernel(void);
+
 /* S[b, o] = sum_{t in [output_offsets[o], output_offsets[o+1])} monomial_values[t]
  *           * prod_c input[b, c]^monomial_counts[t, c].
  * Replaces the CUDA branch of ye3t_runtime::symmetric_power_monomial

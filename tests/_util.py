@@ -30,3 +30,25 @@ def rounded_inputs(inp, dtype):
 
 def flush(msg):
     print(msg, flush=True)
+
+
+def rotation(seed):
+    """A random proper rotation (unit quaternion)."""
+    q = np.random.default_rng(seed).normal(size=4)
+    q /= np.linalg.norm(q)
+    a, b, c, d = q
+    return np.array([[a * a + b * b - c * c - d * d, 2 * (b * c - a * d), 2 * (b * d + a * c)],
+                     [2 * (b * c + a * d), a * a - b * b + c * c - d * d, 2 * (c * d - a * b)],
+                     [2 * (b * d - a * c), 2 * (c * d + a * b), a * a - b * b - c * c + d * d]])
+
+
+def wigner_real(R, L):
+    """Real-basis D^L(R) with Y_L(R u) = D^L Y_L(u), least squares over random directions."""
+    u = np.random.default_rng(3).normal(size=(400, 3))
+    u /= np.linalg.norm(u, axis=1, keepdims=True)
+    import oracle
+
+    y0 = oracle.real_sph_table(u, L)[0][:, L * L:(L + 1) ** 2]
+    y1 = oracle.real_sph_table(u @ R.T, L)[0][:, L * L:(L + 1) ** 2]
+    D, *_ = np.linalg.lstsq(y0, y1, rcond=None)
+    return D.T

@@ -275,3 +275,61 @@ def test_fp64_density_of_fp32_inputs(gpu, mode):
     err = column_rel_error(A.cpu().numpy().reshape(N, -1), ref.reshape(N, -1))
     flush(f"  err {err:.3e}")
     assert err < TOL["f64"]
+
+
+def _random_csr_workload(mode, atoms, max_degree, seed, n_max=8, l_max=3, channels=16):
+    """Random degrees in [0, max_degree] (empty atoms included) for the compiled fp64 MFMA shapes."""
+    rng = np.random.default_rng(seed)
+    counts = rng.integers(0, max_degree + 1, atoms)
+    counts[0] = 0
+    counts[-1] = 0
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    E = int(offsets[-1])
+    vec = rng.normal(size=(E, 3))
+    vec = vec / np.linalg.norm(vec, axis=1, keepdims=True) * rng.uniform(0.8, 5.2, (E, 1))  # some beyond cutoff
+    inp = {"atom_count": atoms, "edge_count": E, "centers": np.repeat(np.arange(atoms), counts),
+           "row_offsets": offsets, "neighbors": rng.integers(0, atoms, E), "edge_vectors": vec, "n_max": n_max,
+           "l_max": l_max, "cutoff": 5.0, "lambda": W.LAMBDA, "epsilon": 1e-12, "species": None,
+           "node_features": None, "radial_mix": None}
+    if mode == "features":
+        inp.update(channel_count=channels, node_features=rng.normal(size=(atoms, channels)),
+                   radial_mix=rng.normal(size=(channels, n_max + 1)) / 3)
+    else:
+        inp.update(channel_count=1)
+    return inp
+
+
+@pytest.mark.parametrize("waves", [None, "1", "5", "64"])
+@pytest.mark.parametrize("mode,shape", [("features", (8, 3)), ("single", (8, 3)), ("single", (10, 4)),
+                                        ("single", (12, 6))])
+@pytest.mark.parametrize("storage", ["f32", "f64"])
+def test_fp64_mfma_density_random_csr(gpu, monkeypatch, mode, shape, storage, waves):
+    """The fp64 matrix-core density (per-atom MFMA over CSR k-blocks) on ragged CSR rows."""
+    flush(f"fp64 MFMA density {mode} n_max,l_max={shape} storage {storage} waves={waves}")
+    import torch
+
+    if waves is not None:
+        monkeypatch.setenv("YE3T_DENSITY_WAVES", waves)
+    inp = _random_csr_workload(mode, 301, 150, 31, n_max=shape[0], l_max=shape[1])
+    dev = to_device_inputs(inp, storage, gpu)
+    N = inp["atom_count"]
+    ref = oracle.ace_density(rounded_inputs(inp, storage)).reshape(N, -1)
+    outs = {}
+    kernels = {"1": ("1", "1"), "0": ("0", "1")}  # fp64 MFMA kernels / VALU kernel
+    if mode == "features":
+        kernels["mix-on-valu"] = ("1", "0")  # MFMA accumulation with the radial mix on VALU
+    for mfma, (flag64, flagmix) in kernels.items():
+        monkeypatch.setenv("YE3T_DENSITY_MFMA64", flag64)
+        monkeypatch.setenv("YE3T_DENSITY_MIX_MFMA", flagmix)
+        A = native.ace_density_forward(
+            dev["edge_vectors"], dev["row_offsets"], dev["neighbors"], atom_count=N,
+            channel_count=inp["channel_count"], n_max=inp["n_max"], l_max=inp["l_max"], cutoff=inp["cutoff"],
+            lam=inp["lambda"], epsilon=inp["epsilon"], node_features=dev.get("node_features"),
+            radial_mix=dev.get("radial_mix"), out_dtype=torch.float64)
+        outs[mfma] = A.cpu().numpy().reshape(N, -1)
+        err = column_rel_error(outs[mfma], ref)
+        flush(f"  mfma64={mfma} err {err:.3e}")
+        assert err < TOL["f64"]
+    # empty atoms are exact zeros
+    empty = np.diff(inp["row_offsets"]) == 0
+    assert not np.any(outs["1"][empty])

@@ -197,3 +197,23 @@ def test_evaluate_componentwise_brute_force():
                     v *= bv[b, flat["component_label_index"][k], blk, flat["block_m_indices"][t, blk]]
                 brute[b, k] += v
     np.testing.assert_allclose(out, brute, atol=1e-13)
+
+
+def test_config4_features_rotate_by_wigner_d():
+    """Oracle density -> plan product: every L block of B rotates by D^L(R) (L = 0 invariant)."""
+    from tests._util import rotation, wigner_real
+    from ye3t_amd.ace import workloads as W
+    from ye3t_amd.ace.plan import ProductPlan
+
+    cfg = W.config(4, atom_count=40)
+    inp = cfg.density.generate()
+    plan = ProductPlan(cfg.feature_spec)
+    R = rotation(5)
+    rot = dict(inp)
+    rot["edge_vectors"] = inp["edge_vectors"] @ R.T
+    B0 = oracle.ace_product_flat(oracle.ace_density(inp).reshape(-1, plan.a_width), plan.flat_arrays())
+    B1 = oracle.ace_product_flat(oracle.ace_density(rot).reshape(-1, plan.a_width), plan.flat_arrays())
+    for L, _ci, _lab, first in plan.label_records:
+        cols = slice(first, first + 2 * L + 1)
+        np.testing.assert_allclose(B1[:, cols], B0[:, cols] @ wigner_real(R, L).T, rtol=1e-9,
+                                   atol=1e-9 * np.abs(B0[:, cols]).max())

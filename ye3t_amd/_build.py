@@ -15,12 +15,15 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libye3t_hip.so")
-SOURCES = ("api.hip", "density.hip", "density_mfma.hip", "product.hip")
+SOURCES = ("api.hip", "density.hip", "density_mfma.hip", "density_mfma64.hip", "product.hip")
 ARCH = os.environ.get("YE3T_HIP_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: no AGPR copies around each MFMA in
+    # the branchy per-atom accumulation loops of the density kernels
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result", f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 

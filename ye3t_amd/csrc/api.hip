@@ -10,7 +10,10 @@ namespace ye3t {
 
 namespace {
 thread_local std::string g_last_error;
+thread_local const char* g_last_density_kernel = "";
 }
+
+void set_density_kernel(const char* name) { g_last_density_kernel = name; }
 
 int set_error(int code, const char* fmt, ...) {
   char buf[1024];
@@ -205,6 +208,8 @@ extern "C" {
 int ye3t_hip_abi_version(void) { return YE3T_HIP_ABI_VERSION; }
 
 const char* ye3t_hip_last_error(void) { return g_last_error.c_str(); }
+
+const char* ye3t_hip_last_density_kernel(void) { return g_last_density_kernel; }
 
 int ye3t_hip_device_caps(int device, ye3t_hip_caps* out) {
   YE3T_REQUIRE(out != nullptr, "caps output is NULL");

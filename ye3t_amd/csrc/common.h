@@ -14,6 +14,8 @@ namespace ye3t {
 
 int set_error(int code, const char* fmt, ...);
 void clear_error();
+// records the kernel an ace_density_forward call launched (static string)
+void set_density_kernel(const char* name);
 
 #define YE3T_CHECK_HIP(expr)                                                              \
   do {                                                                                    \
@@ -72,14 +74,15 @@ const NormTable& norm_table();
 
 // Radial ChebExpCos values (and d/dr) for n = 0..n_max, same algebra as the
 // reference CPU core (ye3t_runtime_core.cpp:321-423) but one Chebyshev pass.
+// Value n goes to v[n * vs], its derivative to d[n].
 template <typename Real, bool WithDeriv, typename Out = Real>
-__device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max, Out* v, Out* d) {
+__device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max, Out* v, Out* d, int vs = 1) {
   const Real pi = Real(3.141592653589793238462643383279502884);
   const Real rc = rc_in > Eps<Real>::value ? rc_in : Eps<Real>::value;
   const Real s = r / rc;
   if (s > Real(1)) {
     for (int n = 0; n <= n_max; ++n) {
-      v[n] = Out(0);
+      v[n * vs] = Out(0);
       if (WithDeriv) d[n] = Out(0);
     }
     return;
@@ -91,7 +94,7 @@ __device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max,
   v[0] = Out(1);
   if (WithDeriv) d[0] = Out(0);
   if (n_max >= 1) {
-    v[1] = Out(Real(0.5) * (Real(1) + c));
+    v[vs] = Out(Real(0.5) * (Real(1) + c));
     if (WithDeriv) d[1] = Out(-Real(0.5) * pi * sn / rc);
   }
   if (n_max >= 2) {
@@ -106,7 +109,7 @@ __device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max,
     for (int n = 2; n <= n_max; ++n) {
       const Real t2 = Real(2) * x * t1 - t0;
       // derivative of T_n is n U_{n-1}; U_{n-1} is u1 here
-      v[n] = Out(Real(0.25) * (Real(1) - t2) * env);
+      v[n * vs] = Out(Real(0.25) * (Real(1) - t2) * env);
       if (WithDeriv) d[n] = Out(Real(0.25) * (-(Real(n) * u1) * dx * env + (Real(1) - t2) * denv));
       t0 = t1;
       t1 = t2;

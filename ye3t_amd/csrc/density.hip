@@ -279,6 +279,7 @@ int launch_density(const ye3t_density_args* a, void* A, hipStream_t stream, int 
   if (grid > 0x7FFFFFFF) return set_error(YE3T_EUNSUPPORTED, "too many atoms for one launch");
   hipLaunchKernelGGL((ace_density_kernel<Real, MODE, BasisT, In>), dim3(unsigned(grid)), dim3(nthreads), lds, stream,
                      p, norm_table());
+  set_density_kernel("ace_density_kernel");
   return check_launch("ace_density_kernel");
 }
 
@@ -301,12 +302,19 @@ int launch_mode(const ye3t_density_args* a, void* A, hipStream_t s) {
 }
 
 int launch_density_mfma(const ye3t_density_args* a, void* A, hipStream_t stream);
+template <typename In>
+int launch_density_mfma64(const ye3t_density_args* a, void* A, hipStream_t stream);
 
 template <typename Real, typename In>
 int dispatch_density(const ye3t_density_args* a, void* A, hipStream_t s) {
   if (std::is_same<Real, float>::value) {
     // fp32 single-channel and node-feature densities run on the matrix cores
     const int rc = launch_density_mfma(a, A, s);
+    if (rc != YE3T_EUNSUPPORTED) return rc;
+    clear_error();
+  } else {
+    // so do fp64 densities of the compiled shapes (fp64 MFMA)
+    const int rc = launch_density_mfma64<In>(a, A, s);
     if (rc != YE3T_EUNSUPPORTED) return rc;
     clear_error();
   }

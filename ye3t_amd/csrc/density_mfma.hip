@@ -251,6 +251,7 @@ int launch_density_mfma(const ye3t_density_args* a, void* A, hipStream_t stream)
     hipLaunchKernelGGL(ace_density_mfma_kernel<false>, dim3(unsigned(grid)), dim3(kMfmaThreads), lds, stream, p,
                        norm_table());
   }
+  set_density_kernel("ace_density_mfma_kernel");
   return check_launch("ace_density_mfma_kernel");
 }
 

@@ -1,0 +1,569 @@
+// Stage 1 with an fp64 density on the matrix cores:
+//
+//   A[i, r, lm] = sum_{e in row i} w_r(e) Y_lm(e)
+//
+// computed as per-atom [rows x edges] x [edges x lm] products with
+// v_mfma_f64_16x16x4f64 (fp64 products and accumulation), so the density is
+// exact to fp64 rounding whatever the input storage type.
+//
+// One wave (one 64-thread workgroup, no block barriers between waves) owns a
+// contiguous range of atoms (as many waves as the device holds at once) and streams
+// their CSR edge range in chunks of 64, one edge per lane:
+//   phase 1  each lane evaluates the radial basis, the real SH and the row
+//            weights of its edge in fp64 registers and writes them to LDS
+//            transposed ([row][edge], [lm][edge]);
+//   phase 2  the wave walks the chunk in k-blocks of 4 edges; each k-block is
+//            one MFMA per (row tile, lm tile) for the atom that owns those
+//            edges (edges of other atoms masked to zero), alternating between
+//            two accumulator sets, and an atom's 16x16 tiles go straight from
+//            registers to A when its last edge has been consumed.
+// Global loads run one chunk ahead (edge vectors, neighbour feature rows) and
+// two chunks ahead (neighbour indices), so no chunk waits on a fresh request.
+//
+// Operand layout of v_mfma_f64_16x16x4f64 (l = lane):
+//   A[i][k]: lane l supplies A[l % 16][l / 16]
+//   B[k][j]: lane l supplies B[l / 16][l % 16]
+//   D[i][j]: lane l holds D[l / 16 + 4 v][l % 16], v = 0..3
+//
+// Rows: MODE 0 -- one channel, rows are radial indices n, w_n(e) = g_n(e);
+//       MODE 2 -- node features with a per-channel radial mix, rows are
+//                 channels c, w_c(e) = h[nbr_e, c] * sum_n mix[c, n] g_n(e).
+#include <cmath>
+#include <cstdlib>
+
+#include "common.h"
+#include "sph.h"
+
+namespace ye3t {
+
+typedef double mfma_d4 __attribute__((ext_vector_type(4)));
+
+// LDS row pitch (doubles) of the transposed tiles: k-block reads of a partial
+// chunk reach edge column cnt + 2 <= 65, and columns 64.. stay zero; 67 is odd,
+// so 16 lanes reading one column of 16 rows hit 16 distinct bank pairs
+constexpr int kPitch64 = 67;
+
+template <typename In>
+struct Density64Params {
+  int64_t N;
+  const int64_t* __restrict__ offsets;
+  const int64_t* __restrict__ nbr;
+  const In* __restrict__ vec;
+  const In* __restrict__ feats;  // [N, C] (MODE 2)
+  const In* __restrict__ mix;    // [C, NR] (MODE 2)
+  int64_t waves;                 // wave w owns atoms [w N / waves, (w + 1) N / waves)
+  double cutoff;                 // max(cutoff, eps of double)
+  double lambda;
+  double den;                    // expm1(lambda)
+  double eps;
+  double* __restrict__ A;
+};
+
+__device__ inline int64_t readlane64(int64_t v, int idx) {
+  const int lo = __builtin_amdgcn_readlane(int(uint32_t(uint64_t(v))), idx);
+  const int hi = __builtin_amdgcn_readlane(int(uint32_t(uint64_t(v) >> 32)), idx);
+  return int64_t((uint64_t(uint32_t(hi)) << 32) | uint64_t(uint32_t(lo)));
+}
+
+// ChebExpCos radial values g_0..g_NMAX of one distance (the algebra of
+// cheb_exp_cos_row with the per-launch constants hoisted), g_n to out[n * stride].
+template <int NMAX, typename P>
+__device__ inline void radial_row64(double r, const P& p, double* out, int stride) {
+  const double s = r / p.cutoff;
+  if (s > 1.0) {
+#pragma unroll
+    for (int n = 0; n <= NMAX; ++n) out[n * stride] = 0.0;
+    return;
+  }
+  const double env = 1.0 + cospi(s);
+  out[0] = 1.0;
+  if (NMAX >= 1) out[stride] = 0.5 * env;
+  if (NMAX >= 2) {
+    const double x = 1.0 - 2.0 * expm1(-p.lambda * (s - 1.0)) / p.den;
+    double t0 = 1.0, t1 = x;
+#pragma unroll
+    for (int n = 2; n <= NMAX; ++n) {
+      const double t2 = 2.0 * x * t1 - t0;
+      out[n * stride] = 0.25 * (1.0 - t2) * env;
+      t0 = t1;
+      t1 = t2;
+    }
+  }
+}
+
+// CSR offsets of a wave's contiguous atom range, read 64 at a time: lane q
+// holds offsets[win + q].  Windows are reloaded (wave-uniformly) as the walk
+// passes their end.
+struct OffsetWindow {
+  const int64_t* __restrict__ offsets;
+  int64_t a_end;  // last atom of the range + 1; offsets[a_end] is the range's edge end
+  int64_t win;
+  int64_t off;
+  int lane;
+  __device__ void load(int64_t base) {
+    win = base;
+    off = (lane <= a_end - base) ? offsets[base + lane] : 0;
+  }
+  // offsets[atom] for atom in [win, a_end]
+  __device__ int64_t at(int64_t atom) {
+    if (atom - win > 63) load(atom);
+    return readlane64(off, int(atom - win));
+  }
+};
+
+template <int MODE, typename In, int LMAX, int NMAX, int C>
+__global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<In> p, NormTable nt) {
+  constexpr int NR = NMAX + 1;
+  constexpr int LW = (LMAX + 1) * (LMAX + 1);
+  constexpr int ROWS = MODE == 2 ? C : NR;
+  constexpr int RT = (ROWS + 15) / 16;
+  constexpr int CT = (LW + 15) / 16;
+  constexpr int HC = MODE == 2 ? C : 1;
+  __shared__ double Wt[RT * 16 * kPitch64];
+  __shared__ double Yt[CT * 16 * kPitch64];
+  __shared__ double Mx[MODE == 2 ? C * NR : 1];
+
+  const int lane = threadIdx.x;
+  const int kq = lane >> 4, cc = lane & 15;
+  const int64_t a_begin = int64_t(blockIdx.x) * p.N / p.waves;
+  const int64_t a_end = (int64_t(blockIdx.x) + 1) * p.N / p.waves;
+  if (a_begin >= a_end) return;
+  OffsetWindow ow{p.offsets, a_end, 0, 0, lane};
+  ow.load(a_begin);
+  // padding rows / columns of the tiles stay zero
+  for (int q = lane; q < RT * 16 * kPitch64; q += 64) Wt[q] = 0.0;
+  for (int q = lane; q < CT * 16 * kPitch64; q += 64) Yt[q] = 0.0;
+  if (MODE == 2) {
+    for (int q = lane; q < C * NR; q += 64) Mx[q] = double(p.mix[q]);
+  }
+  __syncthreads();
+  const int64_t e_begin = ow.at(a_begin), e_end = p.offsets[a_end];
+  double* __restrict__ Aw = p.A;
+
+  // k-blocks whose operands are read from LDS in one batch
+  constexpr int KB = (RT + CT <= 2) ? 16 : ((RT + CT <= 5) ? 8 : 4);
+  mfma_d4 acc[2][RT][CT];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[s2][rt][ct] = mfma_d4{0.0, 0.0, 0.0, 0.0};
+  };
+  zero_acc();
+  int64_t a = a_begin;  // current atom (wave-uniform)
+  int64_t lo = e_begin, hi = ow.at(a_begin + 1);
+
+  auto store_atom = [&](int64_t atom) {
+    double* __restrict__ dst = Aw + atom * (ROWS * LW);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = rt * 16 + kq + 4 * v, col = ct * 16 + cc;
+          if ((ROWS % 16 == 0 || row < ROWS) && (LW % 16 == 0 || col < LW))
+            dst[row * LW + col] = acc[0][rt][ct][v] + acc[1][rt][ct][v];
+        }
+  };
+  auto in_chunk = [&](int64_t t) { return t < e_end && lane < e_end - t; };
+
+  // Software pipeline over 64-edge chunks i: on entry to chunk i the lane holds
+  // its edge vector and feature row of chunk i and its neighbour index of
+  // chunk i + 1; chunk i + 1's vector and feature row and chunk i + 2's
+  // neighbour index are requested before chunk i is computed.
+  In vx = In(0), vy = In(0), vz = In(0);
+  In h[HC];
+  int64_t nb1 = 0;  // neighbour index of chunk i + 1
+#pragma unroll
+  for (int c = 0; c < HC; ++c) h[c] = In(0);
+  if (in_chunk(e_begin)) {
+    const int64_t e = e_begin + lane;
+    vx = p.vec[3 * e];
+    vy = p.vec[3 * e + 1];
+    vz = p.vec[3 * e + 2];
+    if (MODE == 2) {
+      const int64_t nb = p.nbr[e];
+#pragma unroll
+      for (int c = 0; c < HC; ++c) h[c] = p.feats[nb * C + c];
+    }
+  }
+  if (MODE == 2 && e_begin < e_end) nb1 = p.nbr[(e_begin + 64 + lane) < e_end ? (e_begin + 64 + lane) : (e_end - 1)];
+
+  for (int64_t t0 = e_begin; t0 < e_end; t0 += 64) {
+    const int cnt = int((e_end - t0) < 64 ? (e_end - t0) : 64);
+    // requests for the following chunks; lanes past the wave's last edge
+    // re-read that edge (unconditional loads keep the requests in flight)
+    const int64_t e1 = (t0 + 64 + lane) < e_end ? (t0 + 64 + lane) : (e_end - 1);
+    const In nvx = p.vec[3 * e1], nvy = p.vec[3 * e1 + 1], nvz = p.vec[3 * e1 + 2];
+    In nh[HC];
+#pragma unroll
+    for (int c = 0; c < HC; ++c) nh[c] = MODE == 2 ? p.feats[nb1 * C + c] : In(0);
+    const int64_t e2 = (t0 + 128 + lane) < e_end ? (t0 + 128 + lane) : (e_end - 1);
+    const int64_t nb2 = MODE == 2 ? p.nbr[e2] : 0;
+
+    // ---- phase 1: basis and row weights of this lane's edge, in fp64
+    if (lane < cnt) {
+      const double x = double(vx), y = double(vy), z = double(vz);
+      const double r = sqrt(x * x + y * y + z * z);
+      const double sr = r > p.eps ? r : p.eps;
+      const double inv = 1.0 / sr;
+      real_sph_row<double, double>(x * inv, y * inv, z * inv, LMAX, nt, Yt + lane, kPitch64);
+      if (MODE == 0) {
+        radial_row64<NMAX>(r, p, Wt + lane, kPitch64);
+      } else {
+        double g[NR];
+        radial_row64<NMAX>(r, p, g, 1);
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          double s0 = 0.0, s1 = 0.0;
+#pragma unroll
+          for (int n = 0; n + 1 < NR; n += 2) {
+            s0 = fma(Mx[c * NR + n], g[n], s0);
+            s1 = fma(Mx[c * NR + n + 1], g[n + 1], s1);
+          }
+          if (NR % 2) s0 = fma(Mx[c * NR + NR - 1], g[NR - 1], s0);
+          Wt[c * kPitch64 + lane] = double(h[c]) * (s0 + s1);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LW; ++q) Yt[q * kPitch64 + lane] = 0.0;
+#pragma unroll
+      for (int q = 0; q < ROWS; ++q) Wt[q * kPitch64 + lane] = 0.0;
+    }
+    __syncthreads();  // one wave: orders the LDS tile writes before the operand reads
+
+    // ---- phase 2: per-atom MFMA accumulation over k-blocks of 4 edges.  The
+    // operands of KB k-blocks are read from LDS in one batch; consecutive
+    // k-blocks alternate between two accumulator sets (independent MFMAs)
+    const int nkb = (cnt + 3) >> 2;
+    for (int j0 = 0; j0 < nkb; j0 += KB) {
+      double wv[KB][RT], yv[KB][CT];
+#pragma unroll
+      for (int jj = 0; jj < KB; ++jj) {
+        const int el = 4 * (j0 + jj) + kq;  // <= 63: columns cnt..63 hold zeros
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) wv[jj][rt] = Wt[(rt * 16 + cc) * kPitch64 + el];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) yv[jj][ct] = Yt[(ct * 16 + cc) * kPitch64 + el];
+      }
+#pragma unroll
+      for (int jj = 0; jj < KB; ++jj) {
+        const int j = j0 + jj;
+        const int64_t e = t0 + 4 * j + kq;
+        const int64_t kend = t0 + 4 * j + 4;
+        bool more = j < nkb;
+        while (more) {
+          const bool in = e >= lo && e < hi;
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            const double w = in ? wv[jj][rt] : 0.0;
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+              acc[jj & 1][rt][ct] =
+                  __builtin_amdgcn_mfma_f64_16x16x4f64(w, yv[jj][ct], acc[jj & 1][rt][ct], 0, 0, 0);
+          }
+          // the atom continues in a later k-block, or it ends here
+          more = hi <= kend;
+          if (more) {
+            store_atom(a);
+            zero_acc();
+            ++a;
+            more = a < a_end;
+            if (more) {
+              lo = hi;
+              hi = ow.at(a + 1);
+              more = lo < kend;  // the next atom has edges in this k-block
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();  // operand reads done before the next chunk's tile writes
+
+    vx = nvx;
+    vy = nvy;
+    vz = nvz;
+#pragma unroll
+    for (int c = 0; c < HC; ++c) h[c] = nh[c];
+    nb1 = nb2;
+  }
+  // atoms after the last edge (no edges of their own) get zero rows
+  for (; a < a_end; ++a) store_atom(a);
+}
+
+// MODE 2 (node features with a per-channel radial mix, C = 16 rows) with the
+// radial mix on the matrix cores as well.  Per chunk of 64 edges:
+//   phase 1  lane = edge: real SH and radial basis g_n in fp64 -> LDS
+//            ([lm][edge], [n][edge]); the lane's neighbour feature row
+//            h[nbr_e, :] -> LDS ([c][edge], columns permuted as below);
+//   phase 2  per 16-edge tile t, the mix  Wr[e][c] = sum_n g_n(e) mix[c][n]
+//            is one MFMA chain over n (A = G from LDS, B = mix^T in
+//            registers); lane l then holds Wr[16t + l/16 + 4v][l%16], scales
+//            it by h and writes W^T[c][e] over the tile's (consumed) columns
+//            of G; the density product then runs over k-blocks of 4 edges
+//            with both operands from LDS, as in the generic kernel.
+template <typename In, int LMAX, int NMAX>
+__global__ __launch_bounds__(64) void ace_density_mfma64_mix_kernel(Density64Params<In> p, NormTable nt) {
+  constexpr int C = 16;
+  constexpr int NR = NMAX + 1;
+  constexpr int KS = (NR + 3) / 4;  // k-steps of the mix product
+  static_assert(4 * KS <= 16, "radial basis must fit the 16 rows of the G/W tile");
+  constexpr int LW = (LMAX + 1) * (LMAX + 1);
+  constexpr int CT = (LW + 15) / 16;
+  constexpr int P = 65;  // LDS pitch: reads stay below column 64
+  __shared__ double Gt[16 * P];           // g_n (rows n < NR), then W^T (rows c)
+  __shared__ double Yt[CT * 16 * P];
+  __shared__ In Ht[C * P];                // h[nbr_e][c] at column perm(e)
+
+  const int lane = threadIdx.x;
+  const int kq = lane >> 4, cc = lane & 15;
+  // edge e = 16 t + 4 v + k is kept at column 16 t + 4 k + v of Ht, so lane
+  // (k = kq, c = cc) reads its four values of tile t as one 16-byte word
+  const int hcol = (lane & ~15) | ((lane & 3) << 2) | ((lane >> 2) & 3);
+  const int64_t a_begin = int64_t(blockIdx.x) * p.N / p.waves;
+  const int64_t a_end = (int64_t(blockIdx.x) + 1) * p.N / p.waves;
+  if (a_begin >= a_end) return;
+  OffsetWindow ow{p.offsets, a_end, 0, 0, lane};
+  ow.load(a_begin);
+  for (int q = lane; q < 16 * P; q += 64) Gt[q] = 0.0;
+  for (int q = lane; q < CT * 16 * P; q += 64) Yt[q] = 0.0;
+  // B operand of the mix: mix^T[n = 4 ks + kq][c = cc]
+  double mixB[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int n = 4 * ks + kq;
+    mixB[ks] = n < NR ? double(p.mix[cc * NR + n]) : 0.0;
+  }
+  __syncthreads();
+  const int64_t e_begin = ow.at(a_begin), e_end = p.offsets[a_end];
+
+  mfma_d4 acc[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) acc[ct] = mfma_d4{0.0, 0.0, 0.0, 0.0};
+  int64_t a = a_begin;
+  int64_t lo = e_begin, hi = ow.at(a_begin + 1);
+  auto store_atom = [&](int64_t atom) {
+    double* __restrict__ dst = p.A + atom * (C * LW);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq + 4 * v, col = ct * 16 + cc;
+        if (LW % 16 == 0 || col < LW) dst[row * LW + col] = acc[ct][v];
+      }
+  };
+  auto clamp_edge = [&](int64_t e) { return e < e_end ? e : e_end - 1; };
+
+  // Software pipeline: on entry to chunk i the lane holds the vector and the
+  // feature row of its edge of chunk i and the neighbour index of its edge of
+  // chunk i + 1 (lanes past the last edge re-read that edge).
+  In vx = In(0), vy = In(0), vz = In(0);
+  In h[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) h[c] = In(0);
+  int64_t nb1 = 0;
+  if (e_begin < e_end) {
+    const int64_t e = clamp_edge(e_begin + lane);
+    vx = p.vec[3 * e];
+    vy = p.vec[3 * e + 1];
+    vz = p.vec[3 * e + 2];
+    const int64_t nb = p.nbr[e];
+#pragma unroll
+    for (int c = 0; c < C; ++c) h[c] = p.feats[nb * C + c];
+    nb1 = p.nbr[clamp_edge(e_begin + 64 + lane)];
+  }
+
+  for (int64_t t0 = e_begin; t0 < e_end; t0 += 64) {
+    const int cnt = int((e_end - t0) < 64 ? (e_end - t0) : 64);
+    const int64_t e1 = clamp_edge(t0 + 64 + lane);
+    const In nvx = p.vec[3 * e1], nvy = p.vec[3 * e1 + 1], nvz = p.vec[3 * e1 + 2];
+    In nh[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) nh[c] = p.feats[nb1 * C + c];
+    const int64_t nb2 = p.nbr[clamp_edge(t0 + 128 + lane)];
+
+    // ---- phase 1
+    if (lane < cnt) {
+      const double x = double(vx), y = double(vy), z = double(vz);
+      const double r = sqrt(x * x + y * y + z * z);
+      const double sr = r > p.eps ? r : p.eps;
+      const double inv = 1.0 / sr;
+      real_sph_row<double, double>(x * inv, y * inv, z * inv, LMAX, nt, Yt + lane, P);
+      radial_row64<NMAX>(r, p, Gt + lane, P);
+#pragma unroll
+      for (int c = 0; c < C; ++c) Ht[c * P + hcol] = h[c];
+    } else {
+#pragma unroll
+      for (int q = 0; q < LW; ++q) Yt[q * P + lane] = 0.0;
+#pragma unroll
+      for (int q = 0; q < NR; ++q) Gt[q * P + lane] = 0.0;
+#pragma unroll
+      for (int c = 0; c < C; ++c) Ht[c * P + hcol] = In(0);
+    }
+#pragma unroll
+    for (int q = NR; q < 4 * KS; ++q) Gt[q * P + lane] = 0.0;  // rows the mix k-steps pad with
+    __syncthreads();  // one wave: orders the LDS tile writes before the operand reads
+
+    // ---- phase 2a: W^T[c][e] = h[e][c] * sum_n mix[c][n] g_n(e), tile by tile
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (16 * t < cnt) {
+        mfma_d4 D = mfma_d4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          D = __builtin_amdgcn_mfma_f64_16x16x4f64(Gt[(4 * ks + kq) * P + 16 * t + cc], mixB[ks], D, 0, 0, 0);
+        const In* hp = Ht + cc * P + 16 * t + 4 * kq;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) Gt[cc * P + 16 * t + 4 * v + kq] = D[v] * double(hp[v]);
+      }
+    }
+    __syncthreads();
+
+    // ---- phase 2b: per-atom MFMA accumulation over k-blocks of 4 edges; the
+    // operands of k-block j + 1 are read before k-block j's MFMAs
+    const int nkb = (cnt + 3) >> 2;
+    double wn = Gt[cc * P + kq];
+    double yn[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) yn[ct] = Yt[(ct * 16 + cc) * P + kq];
+    for (int j = 0; j < nkb; ++j) {
+      const double wv = wn;
+      double yv[CT];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) yv[ct] = yn[ct];
+      if (j + 1 < nkb) {
+        const int el1 = 4 * j + 4 + kq;
+        wn = Gt[cc * P + el1];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) yn[ct] = Yt[(ct * 16 + cc) * P + el1];
+      }
+      const int64_t e = t0 + 4 * j + kq;
+      const int64_t kend = t0 + 4 * j + 4;
+      for (;;) {
+        const double w = (e >= lo && e < hi) ? wv : 0.0;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[ct] = __builtin_amdgcn_mfma_f64_16x16x4f64(w, yv[ct], acc[ct], 0, 0, 0);
+        if (hi > kend) break;  // the atom continues in a later k-block
+        store_atom(a);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[ct] = mfma_d4{0.0, 0.0, 0.0, 0.0};
+        ++a;
+        if (a >= a_end) break;
+        lo = hi;
+        hi = ow.at(a + 1);
+        if (lo >= kend) break;  // the next atom starts in a later k-block
+      }
+    }
+    __syncthreads();  // operand reads done before the next chunk's tile writes
+
+    vx = nvx;
+    vy = nvy;
+    vz = nvz;
+#pragma unroll
+    for (int c = 0; c < C; ++c) h[c] = nh[c];
+    nb1 = nb2;
+  }
+  for (; a < a_end; ++a) store_atom(a);
+}
+
+static int env_int64(const char* name, int fallback) {
+  const char* v = std::getenv(name);
+  return (v && *v) ? std::atoi(v) : fallback;
+}
+
+// Waves (64-thread workgroups) of one launch: as many as the device holds at
+// once for `kernel` (one round, no tail), each walking a contiguous atom range
+// (YE3T_DENSITY_WAVES overrides).
+static int64_t density_waves(int64_t atoms, const void* kernel) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    cus = 256;
+  }
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64, 0) != hipSuccess || per_cu <= 0) per_cu = 4;
+  int64_t waves = env_int64("YE3T_DENSITY_WAVES", int(int64_t(cus) * per_cu));
+  if (waves < 1) waves = 1;
+  if (waves > 0x7FFFFFFF) waves = 0x7FFFFFFF;
+  return atoms < waves ? (atoms > 0 ? atoms : 1) : waves;
+}
+
+template <typename In, int LMAX, int NMAX>
+int launch64_mix(const ye3t_density_args* a, void* A, hipStream_t stream);
+
+template <int MODE, typename In, int LMAX, int NMAX, int C>
+int launch64(const ye3t_density_args* a, void* A, hipStream_t stream) {
+  Density64Params<In> p;
+  p.N = a->atom_count;
+  p.offsets = a->row_offsets;
+  p.nbr = a->neighbors;
+  p.vec = static_cast<const In*>(a->edge_vectors);
+  p.feats = static_cast<const In*>(a->node_features);
+  p.mix = static_cast<const In*>(a->radial_mix);
+  p.cutoff = a->cutoff > 2.220446049250313e-16 ? a->cutoff : 2.220446049250313e-16;
+  p.lambda = a->lambda;
+  p.den = std::expm1(a->lambda);
+  p.eps = a->epsilon;
+  p.A = static_cast<double*>(A);
+  // about three 64-edge chunks per wave
+  const int64_t grid =
+      density_waves(p.N, reinterpret_cast<const void*>(&ace_density_mfma64_kernel<MODE, In, LMAX, NMAX, C>));
+  p.waves = grid;
+  hipLaunchKernelGGL((ace_density_mfma64_kernel<MODE, In, LMAX, NMAX, C>), dim3(unsigned(grid)), dim3(64), 0,
+                     stream, p, norm_table());
+  set_density_kernel("ace_density_mfma64_kernel");
+  return check_launch("ace_density_mfma64_kernel");
+}
+
+template <typename In, int LMAX, int NMAX>
+int launch64_mix(const ye3t_density_args* a, void* A, hipStream_t stream) {
+  Density64Params<In> p;
+  p.N = a->atom_count;
+  p.offsets = a->row_offsets;
+  p.nbr = a->neighbors;
+  p.vec = static_cast<const In*>(a->edge_vectors);
+  p.feats = static_cast<const In*>(a->node_features);
+  p.mix = static_cast<const In*>(a->radial_mix);
+  p.cutoff = a->cutoff > 2.220446049250313e-16 ? a->cutoff : 2.220446049250313e-16;
+  p.lambda = a->lambda;
+  p.den = std::expm1(a->lambda);
+  p.eps = a->epsilon;
+  p.A = static_cast<double*>(A);
+  const int64_t grid = density_waves(p.N, reinterpret_cast<const void*>(&ace_density_mfma64_mix_kernel<In, LMAX, NMAX>));
+  p.waves = grid;
+  hipLaunchKernelGGL((ace_density_mfma64_mix_kernel<In, LMAX, NMAX>), dim3(unsigned(grid)), dim3(64), 0, stream, p,
+                     norm_table());
+  set_density_kernel("ace_density_mfma64_mix_kernel");
+  return check_launch("ace_density_mfma64_mix_kernel");
+}
+
+// fp64 densities of the compiled shapes; YE3T_EUNSUPPORTED (nothing launched)
+// for the others, which run on the VALU kernel.
+template <typename In>
+int launch_density_mfma64(const ye3t_density_args* a, void* A, hipStream_t stream) {
+  if (a->species) return YE3T_EUNSUPPORTED;
+  if (env_int64("YE3T_DENSITY_MFMA64", 1) == 0) return YE3T_EUNSUPPORTED;
+  const int64_t L = a->max_angular, Nm = a->max_radial_index;
+  if (a->node_features) {
+    // neighbour indices are read as 32-bit values by the mix kernel
+    if (L == 3 && Nm == 8 && a->channel_count == 16 && a->atom_count < (int64_t(1) << 31)) {
+      // radial mix on the matrix cores (opt-in: measured even with the VALU mix)
+      if (env_int64("YE3T_DENSITY_MIX_MFMA", 0)) return launch64_mix<In, 3, 8>(a, A, stream);
+      return launch64<2, In, 3, 8, 16>(a, A, stream);
+    }
+    return YE3T_EUNSUPPORTED;
+  }
+  if (a->channel_count != 1) return YE3T_EUNSUPPORTED;
+  if (L == 3 && Nm == 8) return launch64<0, In, 3, 8, 1>(a, A, stream);
+  if (L == 4 && Nm == 10) return launch64<0, In, 4, 10, 1>(a, A, stream);
+  if (L == 6 && Nm == 12) return launch64<0, In, 6, 12, 1>(a, A, stream);
+  return YE3T_EUNSUPPORTED;
+}
+
+template int launch_density_mfma64<float>(const ye3t_density_args*, void*, hipStream_t);
+template int launch_density_mfma64<double>(const ye3t_density_args*, void*, hipStream_t);
+
+}  // namespace ye3t

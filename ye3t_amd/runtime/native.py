@@ -61,6 +61,7 @@ def lib():
     L = ctypes.CDLL(LIB_PATH)
     L.ye3t_hip_abi_version.restype = ctypes.c_int
     L.ye3t_hip_last_error.restype = ctypes.c_char_p
+    L.ye3t_hip_last_density_kernel.restype = ctypes.c_char_p
     L.ye3t_hip_device_caps.argtypes = [ctypes.c_int, ctypes.POINTER(Caps)]
     L.ye3t_hip_radial_table.argtypes = [ctypes.c_int, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp]
     L.ye3t_hip_real_sph_table.argtypes = [ctypes.c_int, _vp, _i64, _i64, ctypes.c_double, _vp, _vp, _vp]
@@ -94,7 +95,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_symmetric_power_monomial", "ye3t_hip_evaluate_factorized_schedule",
     "ye3t_hip_product_plan_create", "ye3t_hip_product_plan_destroy", "ye3t_hip_product_forward",
     "ye3t_hip_product_launch_info", "ye3t_hip_rtc_compile", "ye3t_hip_free",
-    "ye3t_hip_product_plan_attach_generated", "ye3t_hip_product_plan_select",
+    "ye3t_hip_product_plan_attach_generated", "ye3t_hip_product_plan_select", "ye3t_hip_last_density_kernel",
 )
 
 
@@ -222,6 +223,11 @@ def ace_density_forward(edge_vectors, row_offsets, neighbors, *, atom_count, cha
     _check(lib().ye3t_hip_ace_density_forward(ctypes.byref(args), _dev(out, "A"), _stream()),
            "ye3t_hip_ace_density_forward")
     return out
+
+
+def last_density_kernel():
+    """Kernel launched by the last ``ace_density_forward`` call on this thread."""
+    return lib().ye3t_hip_last_density_kernel().decode()
 
 
 def symmetric_power_monomial(x, monomial_counts, output_offsets, monomial_values):
