@@ -181,10 +181,16 @@ void ye3t_hip_free(void* ptr);
 
 /* Attach a plan-specialised kernel (code object from ye3t_hip_rtc_compile of
  * ye3t_amd/ace/codegen.py output) to `plan`; product_forward then launches it
- * with grid (ceil(samples/64), chunk_count).  The kernel signature is
- * (const T* A, long samples, U* B), T = the plan's dtype, U = its out_dtype. */
+ * with 64 threads per workgroup and grid (ceil(samples / rows_per_tile),
+ * chunk_count), rows_per_tile in [1, 64] being the samples one workgroup
+ * produces.  `persistent` != 0: a one-chunk kernel whose workgroups loop over
+ * 64-row tiles; it is launched with at most as many workgroups as the device
+ * holds at once and needs a 16-byte aligned B (else the generic kernel runs).
+ * The kernel signature is (const T* A, long samples, U* B), T = the plan's
+ * dtype, U = its out_dtype. */
 int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* plan, const void* code, int64_t size,
-                                           const char* kernel_name, int64_t chunk_count);
+                                           const char* kernel_name, int64_t chunk_count, int64_t rows_per_tile,
+                                           int persistent);
 
 /* Select which kernel product_forward launches: 0 = generated (if attached),
  * 1 = generic interpreter. */

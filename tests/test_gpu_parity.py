@@ -333,3 +333,32 @@ def test_fp64_mfma_density_random_csr(gpu, monkeypatch, mode, shape, storage, wa
     # empty atoms are exact zeros
     empty = np.diff(inp["row_offsets"]) == 0
     assert not np.any(outs["1"][empty])
+
+
+@pytest.mark.parametrize("accumulate", ["f32", "f64"])
+def test_persistent_generated_kernel_tiles_and_misaligned_output(gpu, accumulate):
+    """Persistent plan-specialised kernel: partial last tiles, more tiles than resident
+    workgroups, and an output view that is not 16-byte aligned (generic kernel runs)."""
+    flush(f"persistent generated kernel, accumulate {accumulate}")
+    import torch
+
+    pipe = ACEPipeline(W.config(4).feature_spec, "f32", kernel="generated", accumulate=accumulate)
+    assert pipe.handle.generated.get("persistent")
+    real = torch.float64 if accumulate == "f64" else torch.float32
+    for samples in (1, 64, 65, 4097, 200003):
+        A = torch.as_tensor(np.random.default_rng(samples).normal(size=(samples, pipe.plan.a_width)), dtype=real,
+                            device=gpu)
+        ref = oracle.ace_product_flat(A.double().cpu().numpy(), pipe.plan.flat_arrays()) if samples <= 4097 else None
+        B = pipe.product(A)
+        flat = torch.empty(samples * pipe.feature_count + 1, dtype=torch.float32, device=gpu)
+        B_mis = flat[1:].view(samples, pipe.feature_count)
+        pipe.product(A, out=B_mis)
+        torch.cuda.synchronize()
+        got, got_mis = B.cpu().numpy(), B_mis.cpu().numpy()
+        if ref is not None:
+            err = column_rel_error(got, ref)
+            flush(f"  samples={samples} err {err:.3e}")
+            # fp64 arithmetic: only the fp32 rounding of each value, up to ~20x the column RMS
+            assert err < (1e-5 if accumulate == "f64" else TOL["f32"])
+        # the generic kernel on the misaligned view agrees with the persistent kernel
+        assert column_rel_error(got_mis, got.astype(np.float64)) < (1e-6 if accumulate == "f64" else 1e-5)

@@ -19,6 +19,7 @@ import hashlib
 from ye3t_amd.ace.program import _closure
 
 GROUP = 32  # output columns staged per flush
+CHAINS = 4  # independent partial sums per output component (persistent kernel)
 
 
 def _lit(value, dtype):
@@ -46,13 +47,17 @@ def _chunks(plan, max_live):
     return chunks
 
 
-def _emit_tile_store(w, F, pitch, dtype):
+def _emit_tile_store(w, F, pitch, dtype, vector=True):
     """Write the staged [rows, F] tile (type OUT) to B[s0*F : (s0+rows)*F] (contiguous)."""
     vec = 4 if dtype == "f32" else 2
     vtype = "float4" if dtype == "f32" else "double2"
     w(f"    const long total = (long)rows * {F};")
     w(f"    OUT* __restrict__ dst = B + s0 * {F}L;")
-    if pitch == F:
+    if pitch == F and not vector:
+        # one element per lane and instruction: each store covers 64 consecutive values
+        w("    #pragma unroll 8")
+        w("    for (long i = lane; i < total; i += 64) dst[i] = st[i];")
+    elif pitch == F:
         # flat copy; dst is 16-byte aligned when s0*F*sizeof(REAL) is (F*64*elem % 16 == 0)
         w(f"    if ((((unsigned long)dst) & 15) == 0) {{")
         w(f"      const long nv = total / {vec};")
@@ -70,11 +75,178 @@ def _emit_tile_store(w, F, pitch, dtype):
         w(f"    for (long i = lane; i < total; i += 64) {{ const long r = i / {F}; dst[i] = st[r * {pitch} + (i - r * {F})]; }}")
 
 
-def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generated", out_dtype=None):
+# LDS of a compute unit: a tile that fits a quarter of it lets four one-wave
+# workgroups (one per SIMD) run on each CU
+CU_LDS_BYTES = 160 * 1024
+
+
+def tile_rows(F, out_dtype, rows=None):
+    """Samples per workgroup: 64, or fewer when that lets one more tile fit per CU."""
+    if rows is not None:
+        return int(rows)
+    elem = 8 if out_dtype == "f64" else 4
+    pitch = F if F % 2 else F + 1
+    fit64 = CU_LDS_BYTES // (64 * pitch * elem)
+    for r in range(63, 55, -1):
+        if CU_LDS_BYTES // (r * pitch * elem) > fit64 and CU_LDS_BYTES // (r * pitch * elem) <= 4:
+            return r
+    return 64
+
+
+def _emit_node_code(w, nodes, n, emitted, dtype, src, lit=None):
+    """Emit node ``n`` (and its dependencies) as straight-line register code.
+
+    ``src(c)`` is the expression of density column ``c`` of the sample and
+    ``lit(value)`` that of a coefficient (default: an instruction literal).
+    """
+    if lit is None:
+        lit = lambda value: _lit(value, dtype)  # noqa: E731
+    if n in emitted:
+        return
+    nd = nodes[n]
+    for d in nd["deps"]:
+        _emit_node_code(w, nodes, d, emitted, dtype, src, lit)
+    emitted.add(n)
+    fma = "fma" if dtype == "f64" else "fmaf"
+    if nd["kind"] == "leaf":
+        for c in range(nd["dim"]):
+            w(f"      const REAL v{n}_{c} = {src(nd['a_offset'] + c)};")
+        return
+    per = [[] for _ in range(nd["dim"])]
+    if nd["kind"] == "sym":
+        srcn = nd["deps"][0]
+        for oc, value, factors in nd["terms"]:
+            per[oc].append((value, tuple(f"v{srcn}_{q}" for q in factors)))
+    else:
+        da, db = nd["deps"]
+        for oc, value, (i, j) in nd["terms"]:
+            per[oc].append((value, (f"v{da}_{i}", f"v{db}_{j}")))
+    for c, terms in enumerate(per):
+        if not terms:
+            w(f"      const REAL v{n}_{c} = (REAL)0;")
+            continue
+        groups = {}
+        for value, fac in terms:
+            groups.setdefault(fac[0], []).append((value, fac[1:]))
+        # sum_head head * (sum c * tail), as up to CHAINS independent fma chains
+        # added at the end (instruction-level parallelism for one wave per SIMD)
+        chains = [None] * min(CHAINS, len(groups))
+        for g, (head, rest) in enumerate(groups.items()):
+            inner = None
+            for value, tail in rest:
+                prod = " * ".join(tail) if tail else "(REAL)1"
+                inner = (f"{lit(value)} * {prod}" if inner is None
+                         else f"{fma}({lit(value)}, {prod}, {inner})")
+            k = g % len(chains)
+            chains[k] = f"{head} * ({inner})" if chains[k] is None else f"{fma}({head}, {inner}, {chains[k]})"
+        while len(chains) > 1:
+            chains = [f"({chains[i]} + {chains[i + 1]})" if i + 1 < len(chains) else chains[i]
+                      for i in range(0, len(chains), 2)]
+        w(f"      const REAL v{n}_{c} = {chains[0]};")
+
+
+def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_product_generated"):
+    """Persistent variant of the single-chunk kernel: a workgroup loops over
+    64-sample tiles ``blockIdx.x, blockIdx.x + gridDim.x, ...``.
+
+    The next tile's density rows are requested before the current tile is
+    computed, and a tile is stored by a fixed, fully unrolled sequence of
+    16-byte buffer stores whose out-of-range lanes the hardware drops (the
+    last tile is partial).  With that fixed count the
+    compiler's wait for the next rows (issued before the stores) does not wait
+    for the stores to drain, so the stores of tile i overlap the arithmetic of
+    tile i + 1.  Requires an odd feature count (the tile is staged with row
+    pitch F) and a 16-byte aligned ``B`` (the host uses the generic kernel
+    otherwise).
+    """
+    out_dtype = out_dtype or dtype
+    if dtype == "f32" and out_dtype != "f32":
+        raise ValueError("an f32 plan writes f32 features")
+    real = "double" if dtype == "f64" else "float"
+    outt = "double" if out_dtype == "f64" else "float"
+    vec = 4 if out_dtype == "f32" else 2
+    F, Wd = plan.feature_count, plan.a_width
+    if F % 2 == 0:
+        raise ValueError("the persistent kernel stages rows with pitch F, which must be odd")
+    pitch = F
+    nodes = plan.nodes
+    out = []
+    w = out.append
+    w("// generated by ye3t_amd.ace.codegen (persistent) -- do not edit (compiled with hipRTC)")
+    w(f"#define REAL {real}")
+    w(f"#define OUT {outt}")
+    w("typedef unsigned v4u __attribute__((ext_vector_type(4)));")
+    w("typedef unsigned v2u __attribute__((ext_vector_type(2)));")
+    w(f"extern \"C\" __global__ __launch_bounds__(64) void {kernel_name}(")
+    w("    const REAL* __restrict__ A, long samples, OUT* __restrict__ B) {")
+    w(f"  __shared__ __attribute__((aligned(16))) OUT st[64 * {pitch}];")
+    w("  const int lane = threadIdx.x;")
+    w("  const long tiles = (samples + 63) / 64;")
+    w("  long tile = blockIdx.x;")
+    w("  if (tile >= tiles) return;")
+    w("  long srow = tile * 64 + lane;")
+    w("  srow = srow < samples ? srow : samples - 1;")
+    for c in range(Wd):
+        w(f"  REAL a{c} = A[srow * {Wd}L + {c}];")
+    w("  for (;;) {")
+    w("    const long next = tile + gridDim.x;")
+    w("    long nrow = next * 64 + lane;")
+    w("    nrow = nrow < samples ? nrow : samples - 1;")
+    for c in range(Wd):
+        w(f"    const REAL n{c} = A[nrow * {Wd}L + {c}];")
+    w("    {")
+    emitted = set()
+    for f, (root, comp) in enumerate(plan.outputs):
+        _emit_node_code(w, nodes, root, emitted, dtype, lambda c: f"a{c}")
+        w(f"      st[lane * {pitch} + {f}] = (OUT)v{root}_{comp};")
+    w("    }")
+    w("    __syncthreads();")
+    # fixed unrolled store of the [rows, F] tile (a contiguous block of B)
+    # through a buffer resource sized to the tile: every lane stores on every
+    # instruction (no branches, so the store count is known to the compiler)
+    # and the hardware drops the stores of lanes past the tile's data
+    total_full = 64 * F
+    nv_full = total_full // vec
+    iters = -(-nv_full // 64)
+    esize = 8 if out_dtype == "f64" else 4
+    w("    const long s0 = tile * 64;")
+    w("    const long rem = samples - s0;")
+    w("    const int rows = rem < 64 ? (int)rem : 64;")
+    w(f"    const int total = rows * {F};")
+    w(f"    const int nv = total / {vec};")
+    w(f"    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)(B + s0 * {F}L), (short)0, "
+      f"total * {esize}, 0x00020000);")
+    w("    const v4u* __restrict__ srcv = (const v4u*)st;")
+    for k in range(iters):
+        w(f"    {{ const int j = lane + {64 * k}; "
+          f"__builtin_amdgcn_raw_buffer_store_b128(srcv[j < nv ? j : 0], rb, j < nv ? j * 16 : 0x7ffffff0, 0, 0); }}")
+    if out_dtype == "f64":
+        w(f"    {{ const int j = nv * {vec} + lane; __builtin_amdgcn_raw_buffer_store_b64("
+          f"__builtin_bit_cast(v2u, st[j < total ? j : 0]), rb, j < total ? j * {esize} : 0x7ffffff0, 0, 0); }}")
+    else:
+        w(f"    {{ const int j = nv * {vec} + lane; __builtin_amdgcn_raw_buffer_store_b32("
+          f"__builtin_bit_cast(unsigned, st[j < total ? j : 0]), rb, j < total ? j * {esize} : 0x7ffffff0, 0, 0); }}")
+    w("    __syncthreads();")
+    w("    if (next >= tiles) break;")
+    w("    tile = next;")
+    for c in range(Wd):
+        w(f"    a{c} = n{c};")
+    w("  }")
+    w("}")
+    source = "\n".join(out) + "\n"
+    meta = {"kernel": kernel_name, "chunks": 1, "rows": 64, "persistent": True, "feature_count": F,
+            "a_width": Wd, "dtype": dtype, "out_dtype": out_dtype,
+            "hash": hashlib.sha256(source.encode()).hexdigest()[:16]}
+    return source, meta
+
+
+def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generated", out_dtype=None, rows=None):
     """Return ``(source, meta)`` for a specialised product kernel.
 
     ``dtype`` is the type of ``A`` and of the arithmetic, ``out_dtype`` (default
-    the same; "f32" with an "f64" plan) that of ``B``.
+    the same; "f32" with an "f64" plan) that of ``B``.  ``rows`` (<= 64,
+    default :func:`tile_rows`) is the number of samples a 64-lane workgroup
+    produces; lanes past it idle.
     """
     out_dtype = out_dtype or dtype
     if dtype == "f32" and out_dtype != "f32":
@@ -95,18 +267,21 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     w(f"extern \"C\" __global__ __launch_bounds__(64) void {kernel_name}(")
     w("    const REAL* __restrict__ A, long samples, OUT* __restrict__ B) {")
     single = len(chunks) == 1
+    R = tile_rows(F, out_dtype, rows) if single else 64
+    if not 1 <= R <= 64:
+        raise ValueError("rows per tile must be in [1, 64]")
     pitch = F if F % 2 else F + 1  # odd row pitch of the staged tile
     if single:
-        w(f"  __shared__ __attribute__((aligned(16))) OUT st[64 * {pitch}];")
+        w(f"  __shared__ __attribute__((aligned(16))) OUT st[{R} * {pitch}];")
     else:
         w(f"  __shared__ OUT st[{GROUP}][65];")
     w("  const int lane = threadIdx.x;")
-    w("  const long s0 = (long)blockIdx.x * 64;")
+    w(f"  const long s0 = (long)blockIdx.x * {R};")
     w("  const long s = s0 + lane;")
-    w("  const bool valid = s < samples;")
+    w(f"  const bool valid = lane < {R} && s < samples;")
     w(f"  const REAL* __restrict__ a = A + (valid ? s : 0) * {plan.a_width}L;")
     w("  const long rem = samples - s0;")
-    w("  const int rows = rem < 64 ? (int)rem : 64;")
+    w(f"  const int rows = rem < {R} ? (int)rem : {R};")
     w("  switch (blockIdx.y) {")
     for ci, (first, last, members) in enumerate(chunks):
         w(f"  case {ci}: {{")
@@ -157,9 +332,12 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
             for f in range(first, last):
                 root, comp = plan.outputs[f]
                 emit(root)
-                w(f"    st[lane * {pitch} + {f}] = (OUT)v{root}_{comp};")
+                stmt = f"st[lane * {pitch} + {f}] = (OUT)v{root}_{comp};"
+                w(f"    {stmt}" if R == 64 else f"    if (lane < {R}) {stmt}")
             w("    __syncthreads();")
-            _emit_tile_store(w, F, pitch, out_dtype)
+            # 16-byte stores need every tile's block of B 16-byte aligned
+            out_elem = 8 if out_dtype == "f64" else 4
+            _emit_tile_store(w, F, pitch, out_dtype, vector=(R * F * out_elem) % 16 == 0)
             w("    break;")
             w("  }")
             continue
@@ -182,6 +360,6 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     w("  }")
     w("}")
     source = "\n".join(out) + "\n"
-    meta = {"kernel": kernel_name, "chunks": len(chunks), "feature_count": F, "a_width": plan.a_width,
+    meta = {"kernel": kernel_name, "chunks": len(chunks), "rows": R, "feature_count": F, "a_width": plan.a_width,
             "dtype": dtype, "out_dtype": out_dtype, "hash": hashlib.sha256(source.encode()).hexdigest()[:16]}
     return source, meta

@@ -5,6 +5,8 @@ device program, and the stage-1 parameters.  Inputs stay resident in HBM;
 ``forward`` launches exactly two kernels on the current stream.
 """
 
+import os
+
 import numpy as np
 
 from ye3t_amd.ace.plan import ProductPlan
@@ -65,7 +67,15 @@ class ACEPipeline:
         if use_gen:
             from ye3t_amd.ace.codegen import generate
 
-            source, meta = generate(self.plan, self.accumulate, max_live, out_dtype=dtype)
+            from ye3t_amd.ace.codegen import generate_persistent
+
+            rows = os.environ.get("YE3T_PRODUCT_ROWS")  # samples per workgroup (tuning; default by LDS fit)
+            persistent = os.environ.get("YE3T_PRODUCT_PERSISTENT", "1") != "0"
+            if persistent and max_live is None and self.plan.feature_count % 2 and rows is None:
+                source, meta = generate_persistent(self.plan, self.accumulate, out_dtype=dtype)
+            else:
+                source, meta = generate(self.plan, self.accumulate, max_live, out_dtype=dtype,
+                                        rows=int(rows) if rows else None)
             self.handle.attach_generated(source, meta)
             self.kernel = "generated"
 

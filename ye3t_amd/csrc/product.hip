@@ -38,6 +38,8 @@ struct ye3t_hip_product_plan {
   hipModule_t module;
   hipFunction_t generated;
   int64_t generated_chunks;
+  int64_t generated_rows;  // samples per workgroup tile of the generated kernel
+  int64_t generated_max_grid;  // persistent kernel: workgroups resident at once (0: not persistent)
   int use_interpreter;
 };
 
@@ -347,10 +349,12 @@ int ye3t_hip_rtc_compile(const char* source, const char* name, const char* arch,
 void ye3t_hip_free(void* ptr) { std::free(ptr); }
 
 int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* p, const void* code, int64_t size,
-                                           const char* kernel_name, int64_t chunk_count) {
+                                           const char* kernel_name, int64_t chunk_count, int64_t rows_per_tile,
+                                           int persistent) {
   clear_error();
   YE3T_REQUIRE(p && code && size > 0 && kernel_name, "NULL argument");
   YE3T_REQUIRE(chunk_count >= 1 && chunk_count <= 65535, "bad generated chunk count");
+  YE3T_REQUIRE(rows_per_tile >= 1 && rows_per_tile <= kLanes, "rows_per_tile must be in [1, 64]");
   int prev = 0;
   YE3T_CHECK_HIP(hipGetDevice(&prev));
   YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
@@ -365,6 +369,15 @@ int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* p, const void*
   p->module = module;
   p->generated = fn;
   p->generated_chunks = chunk_count;
+  p->generated_rows = rows_per_tile;
+  p->generated_max_grid = 0;
+  if (persistent) {
+    YE3T_REQUIRE(chunk_count == 1 && rows_per_tile == kLanes, "a persistent kernel has one chunk of 64-row tiles");
+    int per_cu = 0, cus = 0;
+    YE3T_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kLanes, 0));
+    YE3T_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device));
+    p->generated_max_grid = int64_t(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  }
   p->use_interpreter = 0;
   return YE3T_OK;
 }
@@ -395,13 +408,18 @@ int ye3t_hip_product_forward(const ye3t_hip_product_plan* p, const void* A, int6
   if (samples == 0) return YE3T_OK;
   YE3T_REQUIRE(A && B, "NULL input or output");
   const int64_t tiles = (samples + kLanes - 1) / kLanes;
-  if (p->generated && !p->use_interpreter) {
-    YE3T_REQUIRE(tiles <= int64_t(0x7FFFFFFF), "too many samples for one launch");
+  // the persistent generated kernel stores 16-byte vectors: a misaligned B runs the generic kernel
+  const bool generated_ok =
+      p->generated && !p->use_interpreter && (p->generated_max_grid == 0 || reinterpret_cast<uintptr_t>(B) % 16 == 0);
+  if (generated_ok) {
+    int64_t gtiles = (samples + p->generated_rows - 1) / p->generated_rows;
+    YE3T_REQUIRE(gtiles <= int64_t(0x7FFFFFFF), "too many samples for one launch");
+    if (p->generated_max_grid > 0 && gtiles > p->generated_max_grid) gtiles = p->generated_max_grid;
     long s_arg = long(samples);
     const void* a_arg = A;
     void* b_arg = B;
     void* args[] = {&a_arg, &s_arg, &b_arg};
-    YE3T_CHECK_HIP(hipModuleLaunchKernel(p->generated, unsigned(tiles), unsigned(p->generated_chunks), 1, kLanes, 1,
+    YE3T_CHECK_HIP(hipModuleLaunchKernel(p->generated, unsigned(gtiles), unsigned(p->generated_chunks), 1, kLanes, 1,
                                          1, 0, as_stream(stream), args, nullptr));
     return YE3T_OK;
   }
