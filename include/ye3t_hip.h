@@ -186,11 +186,12 @@ void ye3t_hip_free(void* ptr);
  * produces.  `persistent` != 0: a one-chunk kernel whose workgroups loop over
  * 64-row tiles; it is launched with at most as many workgroups as the device
  * holds at once and needs a 16-byte aligned B (else the generic kernel runs).
- * The kernel signature is (const T* A, long samples, U* B), T = the plan's
- * dtype, U = its out_dtype. */
+ * `threads_per_block` (a multiple of 64) is the workgroup size the kernel was
+ * generated for.  The kernel signature is (const T* A, long samples, U* B),
+ * T = the plan's dtype, U = its out_dtype. */
 int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* plan, const void* code, int64_t size,
                                            const char* kernel_name, int64_t chunk_count, int64_t rows_per_tile,
-                                           int persistent);
+                                           int persistent, int threads_per_block);
 
 /* Select which kernel product_forward launches: 0 = generated (if attached),
  * 1 = generic interpreter. */

@@ -335,14 +335,18 @@ def test_fp64_mfma_density_random_csr(gpu, monkeypatch, mode, shape, storage, wa
     assert not np.any(outs["1"][empty])
 
 
+@pytest.mark.parametrize("waves", ["1", "2"])
 @pytest.mark.parametrize("accumulate", ["f32", "f64"])
-def test_persistent_generated_kernel_tiles_and_misaligned_output(gpu, accumulate):
+def test_persistent_generated_kernel_tiles_and_misaligned_output(gpu, monkeypatch, accumulate, waves):
     """Persistent plan-specialised kernel: partial last tiles, more tiles than resident
-    workgroups, and an output view that is not 16-byte aligned (generic kernel runs)."""
-    flush(f"persistent generated kernel, accumulate {accumulate}")
+    workgroups, and an output view that is not 16-byte aligned (generic kernel runs);
+    one or two waves per tile."""
+    flush(f"persistent generated kernel, accumulate {accumulate}, waves {waves}")
     import torch
 
+    monkeypatch.setenv("YE3T_PRODUCT_WAVES", waves)
     pipe = ACEPipeline(W.config(4).feature_spec, "f32", kernel="generated", accumulate=accumulate)
+    assert pipe.handle.generated["threads"] == 64 * int(waves)
     assert pipe.handle.generated.get("persistent")
     real = torch.float64 if accumulate == "f64" else torch.float32
     for samples in (1, 64, 65, 4097, 200003):

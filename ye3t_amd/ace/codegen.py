@@ -145,7 +145,26 @@ def _emit_node_code(w, nodes, n, emitted, dtype, src, lit=None):
         w(f"      const REAL v{n}_{c} = {chains[0]};")
 
 
-def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_product_generated"):
+def _split_outputs(plan, parts):
+    """Contiguous output ranges of about equal arithmetic (terms of the nodes
+    each range computes, shared nodes counted in every range that needs them)."""
+    nodes = plan.nodes
+
+    def cost(nset):
+        return sum(len(nodes[n].get("terms", ())) + nodes[n]["dim"] for n in nset)
+
+    total = cost(set().union(*(_closure(nodes, r, set()) for r, _ in plan.outputs)))
+    bounds, cur, first = [], set(), 0
+    for f, (root, _c) in enumerate(plan.outputs):
+        cur |= _closure(nodes, root, set())
+        if len(bounds) < parts - 1 and cost(cur) >= total / parts and f + 1 < len(plan.outputs):
+            bounds.append((first, f + 1))
+            cur, first = set(), f + 1
+    bounds.append((first, len(plan.outputs)))
+    return bounds
+
+
+def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_product_generated", waves=1):
     """Persistent variant of the single-chunk kernel: a workgroup loops over
     64-sample tiles ``blockIdx.x, blockIdx.x + gridDim.x, ...``.
 
@@ -158,6 +177,10 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
     tile i + 1.  Requires an odd feature count (the tile is staged with row
     pitch F) and a 16-byte aligned ``B`` (the host uses the generic kernel
     otherwise).
+
+    ``waves`` > 1: a workgroup of ``64 * waves`` threads shares the tile; wave
+    w computes the w-th of ``waves`` contiguous output ranges of about equal
+    arithmetic (fewer live values per wave), and all threads store the tile.
     """
     out_dtype = out_dtype or dtype
     if dtype == "f32" and out_dtype != "f32":
@@ -177,10 +200,12 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
     w(f"#define OUT {outt}")
     w("typedef unsigned v4u __attribute__((ext_vector_type(4)));")
     w("typedef unsigned v2u __attribute__((ext_vector_type(2)));")
-    w(f"extern \"C\" __global__ __launch_bounds__(64) void {kernel_name}(")
+    threads = 64 * waves
+    w(f"extern \"C\" __global__ __launch_bounds__({threads}) void {kernel_name}(")
     w("    const REAL* __restrict__ A, long samples, OUT* __restrict__ B) {")
     w(f"  __shared__ __attribute__((aligned(16))) OUT st[64 * {pitch}];")
-    w("  const int lane = threadIdx.x;")
+    w("  const int lane = threadIdx.x & 63;")
+    w("  const int wv = threadIdx.x >> 6;")
     w("  const long tiles = (samples + 63) / 64;")
     w("  long tile = blockIdx.x;")
     w("  if (tile >= tiles) return;")
@@ -194,12 +219,14 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
     w("    nrow = nrow < samples ? nrow : samples - 1;")
     for c in range(Wd):
         w(f"    const REAL n{c} = A[nrow * {Wd}L + {c}];")
-    w("    {")
-    emitted = set()
-    for f, (root, comp) in enumerate(plan.outputs):
-        _emit_node_code(w, nodes, root, emitted, dtype, lambda c: f"a{c}")
-        w(f"      st[lane * {pitch} + {f}] = (OUT)v{root}_{comp};")
-    w("    }")
+    for g, (f0, f1) in enumerate(_split_outputs(plan, waves)):
+        w(f"    if (wv == {g}) {{" if waves > 1 else "    {")
+        emitted = set()
+        for f in range(f0, f1):
+            root, comp = plan.outputs[f]
+            _emit_node_code(w, nodes, root, emitted, dtype, lambda c: f"a{c}")
+            w(f"      st[lane * {pitch} + {f}] = (OUT)v{root}_{comp};")
+        w("    }")
     w("    __syncthreads();")
     # fixed unrolled store of the [rows, F] tile (a contiguous block of B)
     # through a buffer resource sized to the tile: every lane stores on every
@@ -207,7 +234,7 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
     # and the hardware drops the stores of lanes past the tile's data
     total_full = 64 * F
     nv_full = total_full // vec
-    iters = -(-nv_full // 64)
+    iters = -(-nv_full // threads)
     esize = 8 if out_dtype == "f64" else 4
     w("    const long s0 = tile * 64;")
     w("    const long rem = samples - s0;")
@@ -218,13 +245,13 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
       f"total * {esize}, 0x00020000);")
     w("    const v4u* __restrict__ srcv = (const v4u*)st;")
     for k in range(iters):
-        w(f"    {{ const int j = lane + {64 * k}; "
+        w(f"    {{ const int j = threadIdx.x + {threads * k}; "
           f"__builtin_amdgcn_raw_buffer_store_b128(srcv[j < nv ? j : 0], rb, j < nv ? j * 16 : 0x7ffffff0, 0, 0); }}")
     if out_dtype == "f64":
-        w(f"    {{ const int j = nv * {vec} + lane; __builtin_amdgcn_raw_buffer_store_b64("
+        w(f"    {{ const int j = nv * {vec} + (int)threadIdx.x; __builtin_amdgcn_raw_buffer_store_b64("
           f"__builtin_bit_cast(v2u, st[j < total ? j : 0]), rb, j < total ? j * {esize} : 0x7ffffff0, 0, 0); }}")
     else:
-        w(f"    {{ const int j = nv * {vec} + lane; __builtin_amdgcn_raw_buffer_store_b32("
+        w(f"    {{ const int j = nv * {vec} + (int)threadIdx.x; __builtin_amdgcn_raw_buffer_store_b32("
           f"__builtin_bit_cast(unsigned, st[j < total ? j : 0]), rb, j < total ? j * {esize} : 0x7ffffff0, 0, 0); }}")
     w("    __syncthreads();")
     w("    if (next >= tiles) break;")
@@ -234,7 +261,8 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
     w("  }")
     w("}")
     source = "\n".join(out) + "\n"
-    meta = {"kernel": kernel_name, "chunks": 1, "rows": 64, "persistent": True, "feature_count": F,
+    meta = {"kernel": kernel_name, "chunks": 1, "rows": 64, "persistent": True, "threads": threads,
+            "feature_count": F,
             "a_width": Wd, "dtype": dtype, "out_dtype": out_dtype,
             "hash": hashlib.sha256(source.encode()).hexdigest()[:16]}
     return source, meta

@@ -71,8 +71,12 @@ class ACEPipeline:
 
             rows = os.environ.get("YE3T_PRODUCT_ROWS")  # samples per workgroup (tuning; default by LDS fit)
             persistent = os.environ.get("YE3T_PRODUCT_PERSISTENT", "1") != "0"
+            waves = os.environ.get("YE3T_PRODUCT_WAVES")  # waves sharing a tile (tuning)
             if persistent and max_live is None and self.plan.feature_count % 2 and rows is None:
-                source, meta = generate_persistent(self.plan, self.accumulate, out_dtype=dtype)
+                # two waves share each tile: each computes half the outputs, with
+                # half the live values (fp64 config 4: 170 -> 144 us)
+                source, meta = generate_persistent(self.plan, self.accumulate, out_dtype=dtype,
+                                                   waves=int(waves) if waves else 2)
             else:
                 source, meta = generate(self.plan, self.accumulate, max_live, out_dtype=dtype,
                                         rows=int(rows) if rows else None)

@@ -39,6 +39,7 @@ struct ye3t_hip_product_plan {
   hipFunction_t generated;
   int64_t generated_chunks;
   int64_t generated_rows;  // samples per workgroup tile of the generated kernel
+  int generated_threads;   // threads per workgroup of the generated kernel
   int64_t generated_max_grid;  // persistent kernel: workgroups resident at once (0: not persistent)
   int use_interpreter;
 };
@@ -350,11 +351,13 @@ void ye3t_hip_free(void* ptr) { std::free(ptr); }
 
 int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* p, const void* code, int64_t size,
                                            const char* kernel_name, int64_t chunk_count, int64_t rows_per_tile,
-                                           int persistent) {
+                                           int persistent, int threads_per_block) {
   clear_error();
   YE3T_REQUIRE(p && code && size > 0 && kernel_name, "NULL argument");
   YE3T_REQUIRE(chunk_count >= 1 && chunk_count <= 65535, "bad generated chunk count");
   YE3T_REQUIRE(rows_per_tile >= 1 && rows_per_tile <= kLanes, "rows_per_tile must be in [1, 64]");
+  YE3T_REQUIRE(threads_per_block >= kLanes && threads_per_block <= 1024 && threads_per_block % kLanes == 0,
+               "threads_per_block must be a multiple of 64 in [64, 1024]");
   int prev = 0;
   YE3T_CHECK_HIP(hipGetDevice(&prev));
   YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
@@ -370,11 +373,12 @@ int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* p, const void*
   p->generated = fn;
   p->generated_chunks = chunk_count;
   p->generated_rows = rows_per_tile;
+  p->generated_threads = threads_per_block;
   p->generated_max_grid = 0;
   if (persistent) {
     YE3T_REQUIRE(chunk_count == 1 && rows_per_tile == kLanes, "a persistent kernel has one chunk of 64-row tiles");
     int per_cu = 0, cus = 0;
-    YE3T_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kLanes, 0));
+    YE3T_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads_per_block, 0));
     YE3T_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device));
     p->generated_max_grid = int64_t(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
   }
@@ -419,7 +423,8 @@ int ye3t_hip_product_forward(const ye3t_hip_product_plan* p, const void* A, int6
     const void* a_arg = A;
     void* b_arg = B;
     void* args[] = {&a_arg, &s_arg, &b_arg};
-    YE3T_CHECK_HIP(hipModuleLaunchKernel(p->generated, unsigned(gtiles), unsigned(p->generated_chunks), 1, kLanes, 1,
+    YE3T_CHECK_HIP(hipModuleLaunchKernel(p->generated, unsigned(gtiles), unsigned(p->generated_chunks), 1,
+                                         unsigned(p->generated_threads), 1,
                                          1, 0, as_stream(stream), args, nullptr));
     return YE3T_OK;
   }

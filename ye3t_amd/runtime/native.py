@@ -80,7 +80,8 @@ def lib():
                                        ctypes.POINTER(_i64)]
     L.ye3t_hip_free.argtypes = [_vp]
     L.ye3t_hip_free.restype = None
-    L.ye3t_hip_product_plan_attach_generated.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, _i64, _i64, ctypes.c_int]
+    L.ye3t_hip_product_plan_attach_generated.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, _i64, _i64, ctypes.c_int,
+                                                         ctypes.c_int]
     L.ye3t_hip_product_plan_select.argtypes = [_vp, ctypes.c_int]
     version = L.ye3t_hip_abi_version()
     if version != ABI_VERSION:
@@ -367,7 +368,8 @@ class ProductPlanHandle:
         _check(lib().ye3t_hip_product_plan_attach_generated(self._handle, self._code, len(blob),
                                                             meta["kernel"].encode(), int(meta["chunks"]),
                                                             int(meta.get("rows", 64)),
-                                                            1 if meta.get("persistent") else 0),
+                                                            1 if meta.get("persistent") else 0,
+                                                            int(meta.get("threads", 64))),
                "ye3t_hip_product_plan_attach_generated")
         self.generated = meta
 
