@@ -59,6 +59,16 @@ struct Density64Params {
   double* __restrict__ A;
 };
 
+// offsets[i] through the constant address space: a scalar load (the CSR
+// offsets are read-only for the kernel's lifetime), so it is counted by
+// lgkmcnt and never waits for the vector stores of A
+__device__ inline int64_t offset_at(const int64_t* offsets, int64_t i) {
+  return ((const __attribute__((address_space(4))) int64_t*)(offsets))[i];
+}
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
+__device__ inline void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 __device__ inline int64_t readlane64(int64_t v, int idx) {
   const int lo = __builtin_amdgcn_readlane(int(uint32_t(uint64_t(v))), idx);
   const int hi = __builtin_amdgcn_readlane(int(uint32_t(uint64_t(v) >> 32)), idx);
@@ -91,26 +101,6 @@ __device__ inline void radial_row64(double r, const P& p, double* out, int strid
   }
 }
 
-// CSR offsets of a wave's contiguous atom range, read 64 at a time: lane q
-// holds offsets[win + q].  Windows are reloaded (wave-uniformly) as the walk
-// passes their end.
-struct OffsetWindow {
-  const int64_t* __restrict__ offsets;
-  int64_t a_end;  // last atom of the range + 1; offsets[a_end] is the range's edge end
-  int64_t win;
-  int64_t off;
-  int lane;
-  __device__ void load(int64_t base) {
-    win = base;
-    off = (lane <= a_end - base) ? offsets[base + lane] : 0;
-  }
-  // offsets[atom] for atom in [win, a_end]
-  __device__ int64_t at(int64_t atom) {
-    if (atom - win > 63) load(atom);
-    return readlane64(off, int(atom - win));
-  }
-};
-
 template <int MODE, typename In, int LMAX, int NMAX, int C>
 __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<In> p, NormTable nt) {
   constexpr int NR = NMAX + 1;
@@ -128,8 +118,6 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
   const int64_t a_begin = int64_t(blockIdx.x) * p.N / p.waves;
   const int64_t a_end = (int64_t(blockIdx.x) + 1) * p.N / p.waves;
   if (a_begin >= a_end) return;
-  OffsetWindow ow{p.offsets, a_end, 0, 0, lane};
-  ow.load(a_begin);
   // padding rows / columns of the tiles stay zero
   for (int q = lane; q < RT * 16 * kPitch64; q += 64) Wt[q] = 0.0;
   for (int q = lane; q < CT * 16 * kPitch64; q += 64) Yt[q] = 0.0;
@@ -137,7 +125,7 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
     for (int q = lane; q < C * NR; q += 64) Mx[q] = double(p.mix[q]);
   }
   __syncthreads();
-  const int64_t e_begin = ow.at(a_begin), e_end = p.offsets[a_end];
+  const int64_t e_begin = offset_at(p.offsets, a_begin), e_end = offset_at(p.offsets, a_end);
   double* __restrict__ Aw = p.A;
 
   // k-blocks whose operands are read from LDS in one batch
@@ -153,7 +141,7 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
   };
   zero_acc();
   int64_t a = a_begin;  // current atom (wave-uniform)
-  int64_t lo = e_begin, hi = ow.at(a_begin + 1);
+  int64_t lo = e_begin, hi = offset_at(p.offsets, a_begin + 1);
 
   auto store_atom = [&](int64_t atom) {
     double* __restrict__ dst = Aw + atom * (ROWS * LW);
@@ -196,13 +184,13 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
     const int cnt = int((e_end - t0) < 64 ? (e_end - t0) : 64);
     // requests for the following chunks; lanes past the wave's last edge
     // re-read that edge (unconditional loads keep the requests in flight)
+    const int64_t e2 = (t0 + 128 + lane) < e_end ? (t0 + 128 + lane) : (e_end - 1);
+    const int64_t nb2 = MODE == 2 ? p.nbr[e2] : 0;
     const int64_t e1 = (t0 + 64 + lane) < e_end ? (t0 + 64 + lane) : (e_end - 1);
     const In nvx = p.vec[3 * e1], nvy = p.vec[3 * e1 + 1], nvz = p.vec[3 * e1 + 2];
     In nh[HC];
 #pragma unroll
     for (int c = 0; c < HC; ++c) nh[c] = MODE == 2 ? p.feats[nb1 * C + c] : In(0);
-    const int64_t e2 = (t0 + 128 + lane) < e_end ? (t0 + 128 + lane) : (e_end - 1);
-    const int64_t nb2 = MODE == 2 ? p.nbr[e2] : 0;
 
     // ---- phase 1: basis and row weights of this lane's edge, in fp64
     if (lane < cnt) {
@@ -234,6 +222,11 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
 #pragma unroll
       for (int q = 0; q < ROWS; ++q) Wt[q * kPitch64 + lane] = 0.0;
     }
+    // The next chunk's loads were issued before this chunk's phase 1: wait for
+    // them here, before phase 2 issues this chunk's stores.  Loads and stores
+    // share one in-order counter, so a wait placed after the stores (where the
+    // compiler would put it) also waits for the stores to drain.
+    wait_vmem_all();
     __syncthreads();  // one wave: orders the LDS tile writes before the operand reads
 
     // ---- phase 2: per-atom MFMA accumulation over k-blocks of 4 edges.  The
@@ -275,7 +268,7 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
             more = a < a_end;
             if (more) {
               lo = hi;
-              hi = ow.at(a + 1);
+              hi = offset_at(p.offsets, a + 1);
               more = lo < kend;  // the next atom has edges in this k-block
             }
           }
@@ -327,8 +320,6 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_mix_kernel(Density64Par
   const int64_t a_begin = int64_t(blockIdx.x) * p.N / p.waves;
   const int64_t a_end = (int64_t(blockIdx.x) + 1) * p.N / p.waves;
   if (a_begin >= a_end) return;
-  OffsetWindow ow{p.offsets, a_end, 0, 0, lane};
-  ow.load(a_begin);
   for (int q = lane; q < 16 * P; q += 64) Gt[q] = 0.0;
   for (int q = lane; q < CT * 16 * P; q += 64) Yt[q] = 0.0;
   // B operand of the mix: mix^T[n = 4 ks + kq][c = cc]
@@ -339,13 +330,13 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_mix_kernel(Density64Par
     mixB[ks] = n < NR ? double(p.mix[cc * NR + n]) : 0.0;
   }
   __syncthreads();
-  const int64_t e_begin = ow.at(a_begin), e_end = p.offsets[a_end];
+  const int64_t e_begin = offset_at(p.offsets, a_begin), e_end = offset_at(p.offsets, a_end);
 
   mfma_d4 acc[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) acc[ct] = mfma_d4{0.0, 0.0, 0.0, 0.0};
   int64_t a = a_begin;
-  int64_t lo = e_begin, hi = ow.at(a_begin + 1);
+  int64_t lo = e_begin, hi = offset_at(p.offsets, a_begin + 1);
   auto store_atom = [&](int64_t atom) {
     double* __restrict__ dst = p.A + atom * (C * LW);
 #pragma unroll
@@ -454,7 +445,7 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_mix_kernel(Density64Par
         ++a;
         if (a >= a_end) break;
         lo = hi;
-        hi = ow.at(a + 1);
+        hi = offset_at(p.offsets, a + 1);
         if (lo >= kend) break;  // the next atom starts in a later k-block
       }
     }
