@@ -315,8 +315,10 @@ def test_fp64_mfma_density_random_csr(gpu, monkeypatch, mode, shape, storage, wa
     N = inp["atom_count"]
     ref = oracle.ace_density(rounded_inputs(inp, storage)).reshape(N, -1)
     outs = {}
-    kernels = {"1": ("1", "1"), "0": ("0", "1")}  # fp64 MFMA kernels / VALU kernel
+    # (YE3T_DENSITY_MFMA64, YE3T_DENSITY_MIX_MFMA): fp64 MFMA kernel (default) / VALU kernel
+    kernels = {"mfma64": ("1", "2"), "valu": ("0", "2")}
     if mode == "features":
+        kernels["mix-lds"] = ("1", "1")  # radial mix on the matrix cores, W staged in LDS
         kernels["mix-on-valu"] = ("1", "0")  # MFMA accumulation with the radial mix on VALU
     for mfma, (flag64, flagmix) in kernels.items():
         monkeypatch.setenv("YE3T_DENSITY_MFMA64", flag64)
@@ -328,11 +330,16 @@ def test_fp64_mfma_density_random_csr(gpu, monkeypatch, mode, shape, storage, wa
             radial_mix=dev.get("radial_mix"), out_dtype=torch.float64)
         outs[mfma] = A.cpu().numpy().reshape(N, -1)
         err = column_rel_error(outs[mfma], ref)
-        flush(f"  mfma64={mfma} err {err:.3e}")
+        flush(f"  mfma64={mfma} ({native.last_density_kernel()}) err {err:.3e}")
+        if mfma == "mfma64":
+            expect = "ace_density_mfma64_channel_kernel" if mode == "features" else "ace_density_mfma64_kernel"
+            assert native.last_density_kernel() == expect
         assert err < TOL["f64"]
     # empty atoms are exact zeros
     empty = np.diff(inp["row_offsets"]) == 0
-    assert not np.any(outs["1"][empty])
+    for key in ("mfma64", "mix-lds", "mix-on-valu"):
+        if key in outs:
+            assert not np.any(outs[key][empty])
 
 
 @pytest.mark.parametrize("waves", ["1", "2"])

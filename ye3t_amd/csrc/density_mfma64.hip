@@ -69,6 +69,12 @@ __device__ inline int64_t offset_at(const int64_t* offsets, int64_t i) {
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 __device__ inline void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+__device__ inline int64_t uniform64(int64_t v) {
+  const int lo = __builtin_amdgcn_readfirstlane(int(uint32_t(uint64_t(v))));
+  const int hi = __builtin_amdgcn_readfirstlane(int(uint32_t(uint64_t(v) >> 32)));
+  return int64_t((uint64_t(uint32_t(hi)) << 32) | uint64_t(uint32_t(lo)));
+}
+
 __device__ inline int64_t readlane64(int64_t v, int idx) {
   const int lo = __builtin_amdgcn_readlane(int(uint32_t(uint64_t(v))), idx);
   const int hi = __builtin_amdgcn_readlane(int(uint32_t(uint64_t(v) >> 32)), idx);
@@ -461,6 +467,178 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_mix_kernel(Density64Par
   for (; a < a_end; ++a) store_atom(a);
 }
 
+// MODE 2 at C = 16 channels, n_max = 8, l_max = 3 (one 16 x 16 density tile
+// per atom) with both products on the matrix cores and W never stored:
+//   phase 1  lane = edge, branch-free: real SH Y_lm (16) and the radial values
+//            g_1..g_8 in fp64 -> LDS ([lm][edge], [n - 1][edge]); the
+//            neighbour feature row -> LDS ([c][perm(edge)]), zero for padding
+//            lanes and for edges beyond the cutoff (whose g_n are all zero).
+//   phase 2  per 16-edge tile t: R[e][c] = mix[c][0] + sum_{n=1..8} g_n(e) mix[c][n]
+//            is two MFMAs, the constant g_0 = 1 entering as the accumulator's
+//            initial value.  Lane l then holds R[16 t + 4 v + l / 16][l % 16],
+//            which times h[e][c] is the A operand W[c][e] of k-block 4 t + v
+//            of the density product.  Atoms are walked with wave-relative
+//            32-bit edge indices and scalar compares; only a k-block that
+//            straddles an atom boundary is masked per lane.
+template <typename In>
+__global__ __launch_bounds__(64) void ace_density_mfma64_channel_kernel(Density64Params<In> p, NormTable nt) {
+  constexpr int C = 16, NR = 9, LMAX = 3, LW = 16;
+  constexpr int YP = 65;                         // pitch (doubles) of Yt and Gt, odd
+  constexpr int HP = sizeof(In) == 4 ? 68 : 66;  // pitch (elements) of Ht: rows 16-byte aligned
+  typedef In in4 __attribute__((ext_vector_type(4)));
+  __shared__ double Yt[LW * YP];
+  __shared__ double Gt[8 * YP];
+  __shared__ __attribute__((aligned(16))) In Ht[C * HP];
+
+  const int lane = threadIdx.x;
+  const int kq = lane >> 4, cc = lane & 15;
+  // edge 16 t + 4 v + k of a chunk sits at column 16 t + 4 k + v of Ht, so
+  // lane (k = kq, c = cc) reads its four feature values of tile t as one word
+  const int hcol = (lane & ~15) | ((lane & 3) << 2) | ((lane >> 2) & 3);
+  // wave-uniform atom range (kept in scalar registers)
+  const int64_t a_begin = uniform64(int64_t(blockIdx.x) * p.N / p.waves);
+  const int64_t a_end = uniform64((int64_t(blockIdx.x) + 1) * p.N / p.waves);
+  if (a_begin >= a_end) return;
+  // stale tile entries must stay finite (they meet zero weights)
+  for (int q = lane; q < LW * YP; q += 64) Yt[q] = 0.0;
+  for (int q = lane; q < 8 * YP; q += 64) Gt[q] = 0.0;
+  for (int q = lane; q < C * HP; q += 64) Ht[q] = In(0);
+  // B operands of the mix: mix^T[n = 1 + 4 s + kq][c = cc]; g_0 = 1 adds mix[c][0]
+  const double mix0 = double(p.mix[cc * NR]);
+  const double mixB0 = double(p.mix[cc * NR + 1 + kq]);
+  const double mixB1 = double(p.mix[cc * NR + 5 + kq]);
+  __syncthreads();
+  const int64_t e_begin = offset_at(p.offsets, a_begin), e_end = offset_at(p.offsets, a_end);
+  const int span = int(e_end - e_begin);  // edges of this wave (< 2^31, checked by the host)
+
+  mfma_d4 acc[2] = {mfma_d4{0.0, 0.0, 0.0, 0.0}, mfma_d4{0.0, 0.0, 0.0, 0.0}};
+  // current atom a_begin + a and its edges [lo, hi), all wave-relative (32-bit
+  // scalar compares; the host keeps the edge count below 2^31)
+  const int na = int(a_end - a_begin);
+  int a = 0;
+  int lo = 0, hi = int(offset_at(p.offsets, a_begin + 1) - e_begin);
+  double* __restrict__ Aw = p.A + a_begin * (C * LW) + lane;
+  auto store_atom = [&](int atom) {
+    double* __restrict__ dst = Aw + int64_t(atom) * (C * LW);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) dst[64 * v] = acc[0][v] + acc[1][v];  // row c = kq + 4 v, column lm = cc
+  };
+  // next atom: its edge range, or an empty range past the wave's edges
+  auto next_atom = [&]() {
+    store_atom(a);
+    acc[0] = mfma_d4{0.0, 0.0, 0.0, 0.0};
+    acc[1] = mfma_d4{0.0, 0.0, 0.0, 0.0};
+    ++a;
+    lo = hi;
+    hi = a < na ? int(offset_at(p.offsets, a_begin + a + 1) - e_begin) : 0x7fffffff;
+  };
+  auto clamp_edge = [&](int64_t e) { return e < e_end ? e : e_end - 1; };
+
+  // Software pipeline: on entry to chunk i the lane holds the vector and the
+  // feature row of its edge of chunk i and the neighbour index of its edge of
+  // chunk i + 1 (lanes past the last edge re-read that edge).
+  In vx = In(0), vy = In(0), vz = In(0);
+  In h[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) h[c] = In(0);
+  int64_t nb1 = 0;
+  if (span > 0) {
+    const int64_t e = clamp_edge(e_begin + lane);
+    vx = p.vec[3 * e];
+    vy = p.vec[3 * e + 1];
+    vz = p.vec[3 * e + 2];
+    const int64_t nb = p.nbr[e];
+#pragma unroll
+    for (int c = 0; c < C; ++c) h[c] = p.feats[nb * C + c];
+    nb1 = p.nbr[clamp_edge(e_begin + 64 + lane)];
+  }
+
+  for (int c0 = 0; c0 < span; c0 += 64) {
+    const int cnt = span - c0 < 64 ? span - c0 : 64;
+    const int64_t t0 = e_begin + c0;
+    const int64_t nb2 = p.nbr[clamp_edge(t0 + 128 + lane)];
+    const int64_t e1 = clamp_edge(t0 + 64 + lane);
+    const In nvx = p.vec[3 * e1], nvy = p.vec[3 * e1 + 1], nvz = p.vec[3 * e1 + 2];
+    In nh[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) nh[c] = p.feats[nb1 * C + c];
+
+    // ---- phase 1 (every lane; padding lanes hold a copy of the last edge)
+    {
+      const double x = double(vx), y = double(vy), z = double(vz);
+      const double r = sqrt(x * x + y * y + z * z);
+      const double sr = r > p.eps ? r : p.eps;
+      const double inv = 1.0 / sr;
+      real_sph_row<double, double>(x * inv, y * inv, z * inv, LMAX, nt, Yt + lane, YP);
+      const double s = r / p.cutoff;
+      const bool live = lane < cnt && !(s > 1.0);
+      const double sc = s > 1.0 ? 1.0 : s;
+      const double env = 1.0 + cospi(sc);
+      const double xc = 1.0 - 2.0 * expm1(-p.lambda * (sc - 1.0)) / p.den;
+      Gt[lane] = 0.5 * env;
+      double tm = 1.0, tn = xc;
+#pragma unroll
+      for (int n = 2; n < NR; ++n) {
+        const double t2 = 2.0 * xc * tn - tm;
+        Gt[(n - 1) * YP + lane] = 0.25 * (1.0 - t2) * env;
+        tm = tn;
+        tn = t2;
+      }
+#pragma unroll
+      for (int c = 0; c < C; ++c) Ht[c * HP + hcol] = live ? h[c] : In(0);
+    }
+    // The next chunk's loads were issued before phase 1: wait for them here,
+    // before phase 2 issues stores (loads and stores share one in-order counter).
+    wait_vmem_all();
+    __syncthreads();  // one wave: orders the LDS tile writes before the operand reads
+
+    // ---- phase 2.  All operands of the chunk are read at once (columns past
+    // cnt hold finite stale values that are never used), the four tiles' mix
+    // products run as independent chains, and consecutive k-blocks alternate
+    // between two accumulators.
+    const int nkb = (cnt + 3) >> 2;
+    double yv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) yv[j] = Yt[cc * YP + 4 * j + kq];
+    mfma_d4 R[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      R[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(Gt[kq * YP + 16 * t + cc], mixB0,
+                                                  mfma_d4{mix0, mix0, mix0, mix0}, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      R[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(Gt[(4 + kq) * YP + 16 * t + cc], mixB1, R[t], 0, 0, 0);
+    in4 h4[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) h4[t] = *reinterpret_cast<const in4*>(Ht + cc * HP + 16 * t + 4 * kq);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (j < nkb) {
+        const double w = R[j >> 2][j & 3] * double(h4[j >> 2][j & 3]);
+        const int ke = c0 + 4 * j + 4, er = ke - 4 + kq;
+        for (;;) {
+          // this lane's edge belongs to the current atom
+          const double wm = unsigned(er - lo) < unsigned(hi - lo) ? w : 0.0;
+          acc[j & 1] = __builtin_amdgcn_mfma_f64_16x16x4f64(wm, yv[j], acc[j & 1], 0, 0, 0);
+          if (hi > ke) break;  // the atom continues in a later k-block
+          next_atom();
+          if (a >= na || lo >= ke) break;  // the next atom starts in a later k-block
+        }
+      }
+    }
+    __syncthreads();  // operand reads done before the next chunk's tile writes
+
+    vx = nvx;
+    vy = nvy;
+    vz = nvz;
+#pragma unroll
+    for (int c = 0; c < C; ++c) h[c] = nh[c];
+    nb1 = nb2;
+  }
+  // atoms after the last edge (no edges of their own) get zero rows
+  for (; a < na; ++a) store_atom(a);
+}
+
 static int env_int64(const char* name, int fallback) {
   const char* v = std::getenv(name);
   return (v && *v) ? std::atoi(v) : fallback;
@@ -531,6 +709,28 @@ int launch64_mix(const ye3t_density_args* a, void* A, hipStream_t stream) {
   return check_launch("ace_density_mfma64_mix_kernel");
 }
 
+template <typename In>
+int launch64_channel(const ye3t_density_args* a, void* A, hipStream_t stream) {
+  Density64Params<In> p;
+  p.N = a->atom_count;
+  p.offsets = a->row_offsets;
+  p.nbr = a->neighbors;
+  p.vec = static_cast<const In*>(a->edge_vectors);
+  p.feats = static_cast<const In*>(a->node_features);
+  p.mix = static_cast<const In*>(a->radial_mix);
+  p.cutoff = a->cutoff > 2.220446049250313e-16 ? a->cutoff : 2.220446049250313e-16;
+  p.lambda = a->lambda;
+  p.den = std::expm1(a->lambda);
+  p.eps = a->epsilon;
+  p.A = static_cast<double*>(A);
+  const int64_t grid = density_waves(p.N, reinterpret_cast<const void*>(&ace_density_mfma64_channel_kernel<In>));
+  p.waves = grid;
+  hipLaunchKernelGGL((ace_density_mfma64_channel_kernel<In>), dim3(unsigned(grid)), dim3(64), 0, stream, p,
+                     norm_table());
+  set_density_kernel("ace_density_mfma64_channel_kernel");
+  return check_launch("ace_density_mfma64_channel_kernel");
+}
+
 // fp64 densities of the compiled shapes; YE3T_EUNSUPPORTED (nothing launched)
 // for the others, which run on the VALU kernel.
 template <typename In>
@@ -541,8 +741,12 @@ int launch_density_mfma64(const ye3t_density_args* a, void* A, hipStream_t strea
   if (a->node_features) {
     // neighbour indices are read as 32-bit values by the mix kernel
     if (L == 3 && Nm == 8 && a->channel_count == 16 && a->atom_count < (int64_t(1) << 31)) {
-      // radial mix on the matrix cores (opt-in: measured even with the VALU mix)
-      if (env_int64("YE3T_DENSITY_MIX_MFMA", 0)) return launch64_mix<In, 3, 8>(a, A, stream);
+      // YE3T_DENSITY_MIX_MFMA: 2 = both products on the matrix cores with W in
+      // registers (default; wave-relative edge indices need E < 2^31),
+      // 1 = mix on the matrix cores with W staged in LDS, 0 = mix on the VALU
+      const int variant = int(env_int64("YE3T_DENSITY_MIX_MFMA", 2));
+      if (variant == 2 && a->edge_count < (int64_t(1) << 31)) return launch64_channel<In>(a, A, stream);
+      if (variant == 1) return launch64_mix<In, 3, 8>(a, A, stream);
       return launch64<2, In, 3, 8, 16>(a, A, stream);
     }
     return YE3T_EUNSUPPORTED;
