@@ -316,10 +316,9 @@ def test_fp64_mfma_density_random_csr(gpu, monkeypatch, mode, shape, storage, wa
     ref = oracle.ace_density(rounded_inputs(inp, storage)).reshape(N, -1)
     outs = {}
     # (YE3T_DENSITY_MFMA64, YE3T_DENSITY_MIX_MFMA): fp64 MFMA kernel (default) / VALU kernel
-    kernels = {"mfma64": ("1", "2"), "valu": ("0", "2")}
+    kernels = {"mfma64": ("1", "1"), "valu": ("0", "1")}
     if mode == "features":
-        kernels["mix-lds"] = ("1", "1")  # radial mix on the matrix cores, W staged in LDS
-        kernels["mix-on-valu"] = ("1", "0")  # MFMA accumulation with the radial mix on VALU
+        kernels["mix-on-valu"] = ("1", "0")  # generic MFMA kernel with the radial mix on VALU
     for mfma, (flag64, flagmix) in kernels.items():
         monkeypatch.setenv("YE3T_DENSITY_MFMA64", flag64)
         monkeypatch.setenv("YE3T_DENSITY_MIX_MFMA", flagmix)
@@ -337,7 +336,7 @@ def test_fp64_mfma_density_random_csr(gpu, monkeypatch, mode, shape, storage, wa
         assert err < TOL["f64"]
     # empty atoms are exact zeros
     empty = np.diff(inp["row_offsets"]) == 0
-    for key in ("mfma64", "mix-lds", "mix-on-valu"):
+    for key in ("mfma64", "mix-on-valu"):
         if key in outs:
             assert not np.any(outs[key][empty])
 

@@ -28,6 +28,9 @@
 // Rows: MODE 0 -- one channel, rows are radial indices n, w_n(e) = g_n(e);
 //       MODE 2 -- node features with a per-channel radial mix, rows are
 //                 channels c, w_c(e) = h[nbr_e, c] * sum_n mix[c, n] g_n(e).
+// MODE 2 at 16 channels, n_max = 8, l_max = 3 runs on its own kernel
+// (ace_density_mfma64_channel_kernel) that also puts the radial mix on the
+// matrix cores and keeps W in registers.
 #include <cmath>
 #include <cstdlib>
 
@@ -294,179 +297,6 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
   for (; a < a_end; ++a) store_atom(a);
 }
 
-// MODE 2 (node features with a per-channel radial mix, C = 16 rows) with the
-// radial mix on the matrix cores as well.  Per chunk of 64 edges:
-//   phase 1  lane = edge: real SH and radial basis g_n in fp64 -> LDS
-//            ([lm][edge], [n][edge]); the lane's neighbour feature row
-//            h[nbr_e, :] -> LDS ([c][edge], columns permuted as below);
-//   phase 2  per 16-edge tile t, the mix  Wr[e][c] = sum_n g_n(e) mix[c][n]
-//            is one MFMA chain over n (A = G from LDS, B = mix^T in
-//            registers); lane l then holds Wr[16t + l/16 + 4v][l%16], scales
-//            it by h and writes W^T[c][e] over the tile's (consumed) columns
-//            of G; the density product then runs over k-blocks of 4 edges
-//            with both operands from LDS, as in the generic kernel.
-template <typename In, int LMAX, int NMAX>
-__global__ __launch_bounds__(64) void ace_density_mfma64_mix_kernel(Density64Params<In> p, NormTable nt) {
-  constexpr int C = 16;
-  constexpr int NR = NMAX + 1;
-  constexpr int KS = (NR + 3) / 4;  // k-steps of the mix product
-  static_assert(4 * KS <= 16, "radial basis must fit the 16 rows of the G/W tile");
-  constexpr int LW = (LMAX + 1) * (LMAX + 1);
-  constexpr int CT = (LW + 15) / 16;
-  constexpr int P = 65;  // LDS pitch: reads stay below column 64
-  __shared__ double Gt[16 * P];           // g_n (rows n < NR), then W^T (rows c)
-  __shared__ double Yt[CT * 16 * P];
-  __shared__ In Ht[C * P];                // h[nbr_e][c] at column perm(e)
-
-  const int lane = threadIdx.x;
-  const int kq = lane >> 4, cc = lane & 15;
-  // edge e = 16 t + 4 v + k is kept at column 16 t + 4 k + v of Ht, so lane
-  // (k = kq, c = cc) reads its four values of tile t as one 16-byte word
-  const int hcol = (lane & ~15) | ((lane & 3) << 2) | ((lane >> 2) & 3);
-  const int64_t a_begin = int64_t(blockIdx.x) * p.N / p.waves;
-  const int64_t a_end = (int64_t(blockIdx.x) + 1) * p.N / p.waves;
-  if (a_begin >= a_end) return;
-  for (int q = lane; q < 16 * P; q += 64) Gt[q] = 0.0;
-  for (int q = lane; q < CT * 16 * P; q += 64) Yt[q] = 0.0;
-  // B operand of the mix: mix^T[n = 4 ks + kq][c = cc]
-  double mixB[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    const int n = 4 * ks + kq;
-    mixB[ks] = n < NR ? double(p.mix[cc * NR + n]) : 0.0;
-  }
-  __syncthreads();
-  const int64_t e_begin = offset_at(p.offsets, a_begin), e_end = offset_at(p.offsets, a_end);
-
-  mfma_d4 acc[CT];
-#pragma unroll
-  for (int ct = 0; ct < CT; ++ct) acc[ct] = mfma_d4{0.0, 0.0, 0.0, 0.0};
-  int64_t a = a_begin;
-  int64_t lo = e_begin, hi = offset_at(p.offsets, a_begin + 1);
-  auto store_atom = [&](int64_t atom) {
-    double* __restrict__ dst = p.A + atom * (C * LW);
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = kq + 4 * v, col = ct * 16 + cc;
-        if (LW % 16 == 0 || col < LW) dst[row * LW + col] = acc[ct][v];
-      }
-  };
-  auto clamp_edge = [&](int64_t e) { return e < e_end ? e : e_end - 1; };
-
-  // Software pipeline: on entry to chunk i the lane holds the vector and the
-  // feature row of its edge of chunk i and the neighbour index of its edge of
-  // chunk i + 1 (lanes past the last edge re-read that edge).
-  In vx = In(0), vy = In(0), vz = In(0);
-  In h[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) h[c] = In(0);
-  int64_t nb1 = 0;
-  if (e_begin < e_end) {
-    const int64_t e = clamp_edge(e_begin + lane);
-    vx = p.vec[3 * e];
-    vy = p.vec[3 * e + 1];
-    vz = p.vec[3 * e + 2];
-    const int64_t nb = p.nbr[e];
-#pragma unroll
-    for (int c = 0; c < C; ++c) h[c] = p.feats[nb * C + c];
-    nb1 = p.nbr[clamp_edge(e_begin + 64 + lane)];
-  }
-
-  for (int64_t t0 = e_begin; t0 < e_end; t0 += 64) {
-    const int cnt = int((e_end - t0) < 64 ? (e_end - t0) : 64);
-    const int64_t e1 = clamp_edge(t0 + 64 + lane);
-    const In nvx = p.vec[3 * e1], nvy = p.vec[3 * e1 + 1], nvz = p.vec[3 * e1 + 2];
-    In nh[C];
-#pragma unroll
-    for (int c = 0; c < C; ++c) nh[c] = p.feats[nb1 * C + c];
-    const int64_t nb2 = p.nbr[clamp_edge(t0 + 128 + lane)];
-
-    // ---- phase 1
-    if (lane < cnt) {
-      const double x = double(vx), y = double(vy), z = double(vz);
-      const double r = sqrt(x * x + y * y + z * z);
-      const double sr = r > p.eps ? r : p.eps;
-      const double inv = 1.0 / sr;
-      real_sph_row<double, double>(x * inv, y * inv, z * inv, LMAX, nt, Yt + lane, P);
-      radial_row64<NMAX>(r, p, Gt + lane, P);
-#pragma unroll
-      for (int c = 0; c < C; ++c) Ht[c * P + hcol] = h[c];
-    } else {
-#pragma unroll
-      for (int q = 0; q < LW; ++q) Yt[q * P + lane] = 0.0;
-#pragma unroll
-      for (int q = 0; q < NR; ++q) Gt[q * P + lane] = 0.0;
-#pragma unroll
-      for (int c = 0; c < C; ++c) Ht[c * P + hcol] = In(0);
-    }
-#pragma unroll
-    for (int q = NR; q < 4 * KS; ++q) Gt[q * P + lane] = 0.0;  // rows the mix k-steps pad with
-    __syncthreads();  // one wave: orders the LDS tile writes before the operand reads
-
-    // ---- phase 2a: W^T[c][e] = h[e][c] * sum_n mix[c][n] g_n(e), tile by tile
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if (16 * t < cnt) {
-        mfma_d4 D = mfma_d4{0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          D = __builtin_amdgcn_mfma_f64_16x16x4f64(Gt[(4 * ks + kq) * P + 16 * t + cc], mixB[ks], D, 0, 0, 0);
-        const In* hp = Ht + cc * P + 16 * t + 4 * kq;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) Gt[cc * P + 16 * t + 4 * v + kq] = D[v] * double(hp[v]);
-      }
-    }
-    __syncthreads();
-
-    // ---- phase 2b: per-atom MFMA accumulation over k-blocks of 4 edges; the
-    // operands of k-block j + 1 are read before k-block j's MFMAs
-    const int nkb = (cnt + 3) >> 2;
-    double wn = Gt[cc * P + kq];
-    double yn[CT];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) yn[ct] = Yt[(ct * 16 + cc) * P + kq];
-    for (int j = 0; j < nkb; ++j) {
-      const double wv = wn;
-      double yv[CT];
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) yv[ct] = yn[ct];
-      if (j + 1 < nkb) {
-        const int el1 = 4 * j + 4 + kq;
-        wn = Gt[cc * P + el1];
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) yn[ct] = Yt[(ct * 16 + cc) * P + el1];
-      }
-      const int64_t e = t0 + 4 * j + kq;
-      const int64_t kend = t0 + 4 * j + 4;
-      for (;;) {
-        const double w = (e >= lo && e < hi) ? wv : 0.0;
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) acc[ct] = __builtin_amdgcn_mfma_f64_16x16x4f64(w, yv[ct], acc[ct], 0, 0, 0);
-        if (hi > kend) break;  // the atom continues in a later k-block
-        store_atom(a);
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) acc[ct] = mfma_d4{0.0, 0.0, 0.0, 0.0};
-        ++a;
-        if (a >= a_end) break;
-        lo = hi;
-        hi = offset_at(p.offsets, a + 1);
-        if (lo >= kend) break;  // the next atom starts in a later k-block
-      }
-    }
-    __syncthreads();  // operand reads done before the next chunk's tile writes
-
-    vx = nvx;
-    vy = nvy;
-    vz = nvz;
-#pragma unroll
-    for (int c = 0; c < C; ++c) h[c] = nh[c];
-    nb1 = nb2;
-  }
-  for (; a < a_end; ++a) store_atom(a);
-}
-
 // MODE 2 at C = 16 channels, n_max = 8, l_max = 3 (one 16 x 16 density tile
 // per atom) with both products on the matrix cores and W never stored:
 //   phase 1  lane = edge, branch-free: real SH Y_lm (16) and the radial values
@@ -511,7 +341,9 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_channel_kernel(Density6
   const int64_t e_begin = offset_at(p.offsets, a_begin), e_end = offset_at(p.offsets, a_end);
   const int span = int(e_end - e_begin);  // edges of this wave (< 2^31, checked by the host)
 
-  mfma_d4 acc[2] = {mfma_d4{0.0, 0.0, 0.0, 0.0}, mfma_d4{0.0, 0.0, 0.0, 0.0}};
+  // one accumulator: a dependent fp64 MFMA issues as soon as the matrix core
+  // is free (its latency equals its issue interval)
+  mfma_d4 acc = mfma_d4{0.0, 0.0, 0.0, 0.0};
   // current atom a_begin + a and its edges [lo, hi), all wave-relative (32-bit
   // scalar compares; the host keeps the edge count below 2^31)
   const int na = int(a_end - a_begin);
@@ -521,13 +353,12 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_channel_kernel(Density6
   auto store_atom = [&](int atom) {
     double* __restrict__ dst = Aw + int64_t(atom) * (C * LW);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) dst[64 * v] = acc[0][v] + acc[1][v];  // row c = kq + 4 v, column lm = cc
+    for (int v = 0; v < 4; ++v) dst[64 * v] = acc[v];  // row c = kq + 4 v, column lm = cc
   };
   // next atom: its edge range, or an empty range past the wave's edges
   auto next_atom = [&]() {
     store_atom(a);
-    acc[0] = mfma_d4{0.0, 0.0, 0.0, 0.0};
-    acc[1] = mfma_d4{0.0, 0.0, 0.0, 0.0};
+    acc = mfma_d4{0.0, 0.0, 0.0, 0.0};
     ++a;
     lo = hi;
     hi = a < na ? int(offset_at(p.offsets, a_begin + a + 1) - e_begin) : 0x7fffffff;
@@ -593,9 +424,8 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_channel_kernel(Density6
     __syncthreads();  // one wave: orders the LDS tile writes before the operand reads
 
     // ---- phase 2.  All operands of the chunk are read at once (columns past
-    // cnt hold finite stale values that are never used), the four tiles' mix
-    // products run as independent chains, and consecutive k-blocks alternate
-    // between two accumulators.
+    // cnt hold finite stale values that are never used) and the four tiles'
+    // mix products are issued before the density MFMAs that consume them.
     const int nkb = (cnt + 3) >> 2;
     double yv[16];
 #pragma unroll
@@ -619,7 +449,7 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_channel_kernel(Density6
         for (;;) {
           // this lane's edge belongs to the current atom
           const double wm = unsigned(er - lo) < unsigned(hi - lo) ? w : 0.0;
-          acc[j & 1] = __builtin_amdgcn_mfma_f64_16x16x4f64(wm, yv[j], acc[j & 1], 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f64_16x16x4f64(wm, yv[j], acc, 0, 0, 0);
           if (hi > ke) break;  // the atom continues in a later k-block
           next_atom();
           if (a >= na || lo >= ke) break;  // the next atom starts in a later k-block
@@ -660,8 +490,6 @@ static int64_t density_waves(int64_t atoms, const void* kernel) {
   return atoms < waves ? (atoms > 0 ? atoms : 1) : waves;
 }
 
-template <typename In, int LMAX, int NMAX>
-int launch64_mix(const ye3t_density_args* a, void* A, hipStream_t stream);
 
 template <int MODE, typename In, int LMAX, int NMAX, int C>
 int launch64(const ye3t_density_args* a, void* A, hipStream_t stream) {
@@ -687,27 +515,6 @@ int launch64(const ye3t_density_args* a, void* A, hipStream_t stream) {
   return check_launch("ace_density_mfma64_kernel");
 }
 
-template <typename In, int LMAX, int NMAX>
-int launch64_mix(const ye3t_density_args* a, void* A, hipStream_t stream) {
-  Density64Params<In> p;
-  p.N = a->atom_count;
-  p.offsets = a->row_offsets;
-  p.nbr = a->neighbors;
-  p.vec = static_cast<const In*>(a->edge_vectors);
-  p.feats = static_cast<const In*>(a->node_features);
-  p.mix = static_cast<const In*>(a->radial_mix);
-  p.cutoff = a->cutoff > 2.220446049250313e-16 ? a->cutoff : 2.220446049250313e-16;
-  p.lambda = a->lambda;
-  p.den = std::expm1(a->lambda);
-  p.eps = a->epsilon;
-  p.A = static_cast<double*>(A);
-  const int64_t grid = density_waves(p.N, reinterpret_cast<const void*>(&ace_density_mfma64_mix_kernel<In, LMAX, NMAX>));
-  p.waves = grid;
-  hipLaunchKernelGGL((ace_density_mfma64_mix_kernel<In, LMAX, NMAX>), dim3(unsigned(grid)), dim3(64), 0, stream, p,
-                     norm_table());
-  set_density_kernel("ace_density_mfma64_mix_kernel");
-  return check_launch("ace_density_mfma64_mix_kernel");
-}
 
 template <typename In>
 int launch64_channel(const ye3t_density_args* a, void* A, hipStream_t stream) {
@@ -731,6 +538,7 @@ int launch64_channel(const ye3t_density_args* a, void* A, hipStream_t stream) {
   return check_launch("ace_density_mfma64_channel_kernel");
 }
 
+
 // fp64 densities of the compiled shapes; YE3T_EUNSUPPORTED (nothing launched)
 // for the others, which run on the VALU kernel.
 template <typename In>
@@ -741,12 +549,11 @@ int launch_density_mfma64(const ye3t_density_args* a, void* A, hipStream_t strea
   if (a->node_features) {
     // neighbour indices are read as 32-bit values by the mix kernel
     if (L == 3 && Nm == 8 && a->channel_count == 16 && a->atom_count < (int64_t(1) << 31)) {
-      // YE3T_DENSITY_MIX_MFMA: 2 = both products on the matrix cores with W in
-      // registers (default; wave-relative edge indices need E < 2^31),
-      // 1 = mix on the matrix cores with W staged in LDS, 0 = mix on the VALU
-      const int variant = int(env_int64("YE3T_DENSITY_MIX_MFMA", 2));
-      if (variant == 2 && a->edge_count < (int64_t(1) << 31)) return launch64_channel<In>(a, A, stream);
-      if (variant == 1) return launch64_mix<In, 3, 8>(a, A, stream);
+      // both products on the matrix cores with W in registers (wave-relative
+      // edge indices need E < 2^31); YE3T_DENSITY_MIX_MFMA=0 selects the
+      // generic kernel with the radial mix on the VALU
+      if (env_int64("YE3T_DENSITY_MIX_MFMA", 1) != 0 && a->edge_count < (int64_t(1) << 31))
+        return launch64_channel<In>(a, A, stream);
       return launch64<2, In, 3, 8, 16>(a, A, stream);
     }
     return YE3T_EUNSUPPORTED;
