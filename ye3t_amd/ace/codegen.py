@@ -164,7 +164,8 @@ def _split_outputs(plan, parts):
     return bounds
 
 
-def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_product_generated", waves=1):
+def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_product_generated", waves=1,
+                        store_policy=0):
     """Persistent variant of the single-chunk kernel: a workgroup loops over
     64-sample tiles ``blockIdx.x, blockIdx.x + gridDim.x, ...``.
 
@@ -181,6 +182,9 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
     ``waves`` > 1: a workgroup of ``64 * waves`` threads shares the tile; wave
     w computes the w-th of ``waves`` contiguous output ranges of about equal
     arithmetic (fewer live values per wave), and all threads store the tile.
+
+    ``store_policy``: cache-policy bits of the B stores (gfx950 buffer-store
+    ``aux``: 1 = sc0, 2 = nt, 16 = sc1).
     """
     out_dtype = out_dtype or dtype
     if dtype == "f32" and out_dtype != "f32":
@@ -246,13 +250,16 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
     w("    const v4u* __restrict__ srcv = (const v4u*)st;")
     for k in range(iters):
         w(f"    {{ const int j = threadIdx.x + {threads * k}; "
-          f"__builtin_amdgcn_raw_buffer_store_b128(srcv[j < nv ? j : 0], rb, j < nv ? j * 16 : 0x7ffffff0, 0, 0); }}")
+          f"__builtin_amdgcn_raw_buffer_store_b128(srcv[j < nv ? j : 0], rb, j < nv ? j * 16 : 0x7ffffff0, 0, "
+          f"{int(store_policy)}); }}")
     if out_dtype == "f64":
         w(f"    {{ const int j = nv * {vec} + (int)threadIdx.x; __builtin_amdgcn_raw_buffer_store_b64("
-          f"__builtin_bit_cast(v2u, st[j < total ? j : 0]), rb, j < total ? j * {esize} : 0x7ffffff0, 0, 0); }}")
+          f"__builtin_bit_cast(v2u, st[j < total ? j : 0]), rb, j < total ? j * {esize} : 0x7ffffff0, 0, "
+          f"{int(store_policy)}); }}")
     else:
         w(f"    {{ const int j = nv * {vec} + (int)threadIdx.x; __builtin_amdgcn_raw_buffer_store_b32("
-          f"__builtin_bit_cast(unsigned, st[j < total ? j : 0]), rb, j < total ? j * {esize} : 0x7ffffff0, 0, 0); }}")
+          f"__builtin_bit_cast(unsigned, st[j < total ? j : 0]), rb, j < total ? j * {esize} : 0x7ffffff0, 0, "
+          f"{int(store_policy)}); }}")
     w("    __syncthreads();")
     w("    if (next >= tiles) break;")
     w("    tile = next;")

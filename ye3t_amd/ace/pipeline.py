@@ -75,8 +75,13 @@ class ACEPipeline:
             if persistent and max_live is None and self.plan.feature_count % 2 and rows is None:
                 # two waves share each tile: each computes half the outputs, with
                 # half the live values (fp64 config 4: 170 -> 144 us)
+                # B is written once and not re-read by this pipeline: non-temporal
+                # stores (policy 2) keep it from evicting the next step's inputs and
+                # the density from the last-level cache (config 4: ~7 us per step)
+                policy = os.environ.get("YE3T_PRODUCT_STORE_POLICY")  # cache-policy bits (tuning)
                 source, meta = generate_persistent(self.plan, self.accumulate, out_dtype=dtype,
-                                                   waves=int(waves) if waves else 2)
+                                                   waves=int(waves) if waves else 2,
+                                                   store_policy=int(policy) if policy else 2)
             else:
                 source, meta = generate(self.plan, self.accumulate, max_live, out_dtype=dtype,
                                         rows=int(rows) if rows else None)
