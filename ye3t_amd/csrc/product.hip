@@ -381,6 +381,9 @@ int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* p, const void*
     YE3T_CHECK_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads_per_block, 0));
     YE3T_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device));
     p->generated_max_grid = int64_t(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    // YE3T_PRODUCT_GRID overrides the resident-workgroup count (tuning)
+    const char* g = std::getenv("YE3T_PRODUCT_GRID");
+    if (g && *g && std::atoll(g) > 0) p->generated_max_grid = std::atoll(g);
   }
   p->use_interpreter = 0;
   return YE3T_OK;
