@@ -96,6 +96,83 @@ def cpu_baseline(cfg, pipe, target_seconds=10.0):
                       f"stage2 {s2:.2f}s (OpenMP over samples, {threads} threads)"}
 
 
+def _time_kernel(fn, steps, warmup):
+    """Mean wall time per call of ``fn`` (device-resident inputs, K back-to-back calls)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def bench_op(args, cfg):
+    """One widened op on the configuration's shapes (see ``--op``)."""
+    import numpy as np
+    import torch
+
+    from ye3t_amd.ace.pipeline import ACEPipeline, to_device_inputs
+    from ye3t_amd.ace.program import program_stats
+    from ye3t_amd.runtime import density_accumulate_adjoint, native
+
+    d = cfg.density
+    dtype = args.dtype or cfg.dtypes[0]
+    accumulate = args.accumulate or (cfg.accumulate if dtype == "f32" else None) or dtype
+    workload = f"config{cfg.config_id}-{cfg.name}"
+    line = {"op": args.op, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "data": "synthetic",
+            "config": {"workload": workload}}
+    if args.op == "linear_readout":
+        pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots, kernel=args.kernel, accumulate=accumulate)
+        A = pipe.density(to_device_inputs(cfg.density.generate(), dtype, "cuda"))
+        rows = A.reshape(-1, pipe.plan.a_width)
+        S = int(rows.shape[0])
+        w = torch.as_tensor(np.random.default_rng(3).normal(size=pipe.feature_count), device="cuda")
+        out = torch.empty((S,), dtype=torch.float64 if dtype == "f64" else torch.float32, device="cuda")
+        pipe.linear(rows, w, 0.5, out=out)  # compiles and attaches the fused kernel; validates the arguments
+        if pipe.last_linear_backend == "fused_generated":
+            wk = w.to(torch.float64 if accumulate == "f64" else torch.float32).contiguous()
+            t = _time_kernel(lambda: pipe.handle.linear(rows, wk, 0.5, out=out), args.steps, args.warmup)
+        else:
+            t = _time_kernel(lambda: pipe.linear(rows, w, 0.5, out=out), args.steps, args.warmup)
+        a_elem = 8 if accumulate == "f64" else 4
+        nbytes = S * pipe.plan.a_width * a_elem + S * out.element_size() + pipe.feature_count * a_elem
+        st = program_stats(pipe.program)
+        flops = S * (st["factor_reads"] + st["terms"] + 2 * pipe.feature_count)
+        line.update({
+            "metric": "readout samples/s", "value": S / t, "unit": "samples/s", "higher_is_better": True,
+            "us_per_call": t * 1e6, "dtype": accumulate, "storage_dtype": dtype, "backend": pipe.last_linear_backend,
+            "roofline": {"bound": "hbm", "achieved": nbytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": nbytes},
+            "fp64_arithmetic": {"algorithmic_flops": flops, "achieved_tflops": flops / t / 1e12,
+                                "peak_tflops": 78.6, "frac": flops / t / 1e12 / 78.6},
+            "samples": S, "features_per_sample": pipe.feature_count})
+        line["config"].update({"samples": S, "features": pipe.feature_count})
+    else:
+        inp = cfg.density.generate()
+        N = d.atom_count
+        C = d.channel_count * d.radial_rows * (d.l_max + 1) ** 2
+        tdt = torch.float64 if accumulate == "f64" else torch.float32
+        adj = torch.as_tensor(np.random.default_rng(4).normal(size=(N, C)), dtype=tdt, device="cuda")
+        centers = torch.as_tensor(inp["centers"], device="cuda")
+        E = int(centers.shape[0])
+        density_accumulate_adjoint(adj, centers)  # validates the centres once (a host-side range check)
+        t = _time_kernel(lambda: native.density_accumulate_adjoint(adj, centers), args.steps, args.warmup)
+        elem = adj.element_size()
+        nbytes = E * C * elem + E * 8 + N * C * elem
+        line.update({
+            "metric": "edge-adjoint GB/s", "value": nbytes / t / 1e9, "unit": "GB/s", "higher_is_better": True,
+            "us_per_call": t * 1e6, "dtype": accumulate,
+            "roofline": {"bound": "hbm", "achieved": nbytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": nbytes},
+            "note": "timed through the C-ABI binding; the Python wrapper's centre range check ran once"})
+        line["config"].update({"edges": E, "atoms": N, "channels": C})
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,6 +185,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--kernel", default="auto", choices=["auto", "generated", "interpreter"])
+    ap.add_argument("--op", default="pipeline", choices=["pipeline", "linear_readout", "density_accumulate_adjoint"],
+                    help="pipeline: the headline step (stage 1 + stage 2); the others time one widened op "
+                         "on the config's shapes and print its own JSON line")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the timed region, negate B into a new tensor once (a plain elementwise copy "
                          "kernel of known size, for calibrating FETCH_SIZE / WRITE_SIZE counters)")
@@ -126,6 +206,9 @@ def main():
     from ye3t_amd.runtime import native
 
     cfg = W.config(args.config)
+    if args.op != "pipeline":
+        print(json.dumps(bench_op(args, cfg)))
+        return
     dtype = args.dtype or cfg.dtypes[0]
     accumulate = args.accumulate or (cfg.accumulate if dtype == "f32" else None) or dtype
     elem = 8 if dtype == "f64" else 4

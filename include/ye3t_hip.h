@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 44 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 46 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -81,6 +81,17 @@ int ye3t_hip_real_sph_table(int dtype, const void* edge_vectors, int64_t edge_co
 int ye3t_hip_density_accumulate_csr(int dtype, const void* edge_values, const int64_t* row_offsets,
                                     int64_t atom_count, int64_t channel_count, void* out,
                                     ye3t_stream_t stream);
+
+/* edge_adjoint[e, c] = atomic_adjoint[centers[e], c] for e < edge_count, c <
+ * channel_count: the adjoint of density accumulation (a gather of centre rows;
+ * any edge order).  centers[e] must lie in [0, atom_count) (checked by the
+ * caller; the kernel clamps out-of-range indices instead of faulting).
+ * Replaces ye3t_runtime::density_accumulate_adjoint (schema
+ * execution_plan_torch.cpp:7288, CUDA kernel execution_plan_cuda.cu:9241-9260,
+ * launcher :13890-13921; CPU core ye3t_runtime_core.cpp:1704-1715). */
+int ye3t_hip_density_accumulate_adjoint(int dtype, const void* atomic_adjoint, const int64_t* centers,
+                                        int64_t edge_count, int64_t channel_count, int64_t atom_count,
+                                        void* edge_adjoint, ye3t_stream_t stream);
 
 /* Fused stage 1: A[i, c, r, lm] = sum_{e in row i} w_c(e) R_r(|v_e|) Y_lm(v_e/|v_e|).
  * One pass over edges: radial basis and real SH in registers, per-atom CSR
@@ -193,7 +204,30 @@ int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* plan, const vo
                                            const char* kernel_name, int64_t chunk_count, int64_t rows_per_tile,
                                            int persistent, int threads_per_block);
 
-/* Select which kernel product_forward launches: 0 = generated (if attached),
+/* Attach a plan-specialised fused linear readout kernel (code object of
+ * ye3t_amd/ace/codegen.py:generate_readout compiled with ye3t_hip_rtc_compile).
+ * Kernel signature (const T* A, long samples, U* out, const T* W, T bias), T =
+ * the plan's dtype, U = its out_dtype; launched persistent with at most as many
+ * workgroups of `threads_per_block` threads as the device holds at once. */
+int ye3t_hip_product_plan_attach_readout(ye3t_hip_product_plan* plan, const void* code, int64_t size,
+                                         const char* kernel_name, int threads_per_block);
+
+/* out[s] = bias + sum_k B[s, k] weight[k] without materialising B (B = the
+ * plan's features of A[s]); out has the plan's out_dtype, weight [feature_count]
+ * the plan's dtype.  YE3T_EUNSUPPORTED when no readout kernel is attached (the
+ * caller then materialises B and uses ye3t_hip_rows_dot).  Replaces
+ * ye3t_runtime::factorized_angular_linear (schema execution_plan_torch.cpp:7713,
+ * CUDA execution_plan_cuda.cu:8957; readout semantics execution_plan.py:13832-13850). */
+int ye3t_hip_product_linear_forward(const ye3t_hip_product_plan* plan, const void* A, int64_t samples,
+                                    const void* weight, double bias, void* out, ye3t_stream_t stream);
+
+/* out[s] = bias + sum_k B[s, k] weight[k] for a materialised B[samples, F]
+ * (fp64 accumulation, fixed reduction order).  The reference's materialised
+ * readout `features @ weight + bias` (execution_plan.py:13838-13845). */
+int ye3t_hip_rows_dot(int dtype, const void* B, int64_t samples, int64_t F, const void* weight, double bias,
+                      void* out, ye3t_stream_t stream);
+
+/* Select which kernel product_forward launches/* Select which kernel product_forward launches: 0 = generated (if attached),
  * 1 = generic interpreter. */
 int ye3t_hip_product_plan_select(ye3t_hip_product_plan* plan, int use_interpreter);
 

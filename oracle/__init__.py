@@ -42,6 +42,7 @@ def lib():
         L.oracle_radial_table.argtypes = [_d, _d, _d, _I, _I, _d, _d]
         L.oracle_real_sph_table.argtypes = [_d, _I, _I, ctypes.c_double, _d, _d]
         L.oracle_density_accumulate.argtypes = [_d, _i64, _I, _I, _I, _d]
+        L.oracle_density_accumulate_adjoint.argtypes = [_d, _i64, _I, _I, _d]
         L.oracle_ace_density.argtypes = [_I, _I, _i64, _i64, _d, _i32, _d, _d, _I, _I, _I,
                                          ctypes.c_double, ctypes.c_double, ctypes.c_double, _d]
         L.oracle_symmetric_power_monomial.argtypes = [_d, _I, _I, _i64, _i64, _d, _I, _d]
@@ -63,6 +64,8 @@ def ref_lib():
         _REF.ref_radial_table.argtypes = [_d, _d, _d, _I, _I, _d, _d]
         _REF.ref_real_sph_table.argtypes = [_d, _I, _I, ctypes.c_double, _d, _d]
         _REF.ref_density_accumulate.argtypes = [_d, _i64, _I, _I, _I, _d]
+        if hasattr(_REF, "ref_density_accumulate_adjoint"):
+            _REF.ref_density_accumulate_adjoint.argtypes = [_d, _i64, _I, _I, _d]
         _REF.ref_symmetric_power_monomial.argtypes = [_d, _I, _I, _i64, _i64, _d, _I, _I, _d]
     return _REF
 
@@ -119,6 +122,20 @@ def density_accumulate(edge_values, centers, atom_count, *, use_reference=False)
     out = np.zeros((atom_count, C))
     f = ref_lib().ref_density_accumulate if use_reference else lib().oracle_density_accumulate
     f(_p(ev), _p(centers, _i64), E, C, atom_count, _p(out))
+    return out
+
+
+def density_accumulate_adjoint(atomic_adjoint, centers, *, use_reference=False):
+    """``edge_adjoint[e] = atomic_adjoint[centers[e]]`` (the adjoint of :func:`density_accumulate`)."""
+    adj = _f64(atomic_adjoint)
+    N, C = adj.shape
+    centers = _i64a(centers)
+    if centers.size and (centers.min() < 0 or centers.max() >= N):
+        raise ValueError("center index out of range")
+    E = centers.shape[0]
+    out = np.zeros((E, C))
+    f = ref_lib().ref_density_accumulate_adjoint if use_reference else lib().oracle_density_accumulate_adjoint
+    f(_p(adj), _p(centers, _i64), E, C, _p(out))
     return out
 
 
@@ -186,3 +203,9 @@ def ace_product_flat(A, plan_arrays):
         _p(_i64a(pa["column_offsets"]), _i64), _p(_f64(pa["term_coeffs"])),
         _p(np.ascontiguousarray(pa["term_refs"], dtype=np.int32), _i32), _p(out))
     return out
+
+
+def linear_readout(features, weight, bias):
+    """``features @ weight + bias`` -- the reference's materialised readout
+    (``execution_plan.py:13838-13845``), in fp64."""
+    return _f64(features) @ _f64(weight) + float(bias)

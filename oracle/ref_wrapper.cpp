@@ -17,6 +17,10 @@ void ref_density_accumulate(const double* ev, const int64_t* centers, int64_t e,
                             double* out) {
   ye3t::runtime::density_accumulate_forward<double>(ev, centers, e, c, n, out);
 }
+void ref_density_accumulate_adjoint(const double* adj, const int64_t* centers, int64_t e, int64_t c,
+                                    double* out) {
+  ye3t::runtime::density_accumulate_adjoint<double>(adj, centers, e, c, out);
+}
 void ref_symmetric_power_monomial(const double* in, int64_t batch, int64_t in_dim, const int64_t* counts,
                                   const int64_t* offsets, const double* values, int64_t terms,
                                   int64_t out_dim, double* out) {

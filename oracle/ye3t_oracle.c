@@ -201,6 +201,17 @@ void oracle_density_accumulate(const double* edge_values, const int64_t* centers
   }
 }
 
+/* Gather of centre-row adjoints to edge rows, edge_adjoint[e, :] =
+ * atomic_adjoint[centers[e], :] (ye3t_runtime_core.cpp:1704-1715). */
+void oracle_density_accumulate_adjoint(const double* atomic_adjoint, const int64_t* centers, int64_t edge_count,
+                                       int64_t channel_count, double* edge_adjoint) {
+  for (int64_t e = 0; e < edge_count; ++e) {
+    const double* src = atomic_adjoint + centers[e] * channel_count;
+    double* dst = edge_adjoint + e * channel_count;
+    for (int64_t c = 0; c < channel_count; ++c) dst[c] = src[c];
+  }
+}
+
 /* Stage 1 composed the reference way: radial table, real SH table, edge
  * product edge[e, (c, n, lm)] = w_c(e) * R_n(e) * Y_lm(e) (the semantics of
  * scheduled_radial_angular_channels, ye3t_runtime_core.cpp:1550-1604), then

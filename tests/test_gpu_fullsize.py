@@ -37,6 +37,25 @@ def test_config4_full_size_fp32_parity(gpu):
     assert errB < TOL["f32"]
 
 
+def test_config4_full_size_fused_linear_readout(gpu):
+    """The fused readout over all 800 000 samples against B_ref @ w + bias."""
+    flush("config 4 full size, fused linear readout")
+    import torch
+
+    cfg = W.config(4)
+    inp = cfg.density.generate()
+    pipe = ACEPipeline(cfg.feature_spec, "f32", accumulate=cfg.accumulate)
+    A = pipe.density(to_device_inputs(inp, "f32", gpu))
+    w = np.random.default_rng(77).normal(size=pipe.feature_count)
+    got = pipe.linear(A.reshape(-1, pipe.plan.a_width), torch.as_tensor(w, device=gpu), -2.0)
+    assert pipe.last_linear_backend == "fused_generated"
+    A_ref = oracle.ace_density(rounded_inputs(inp, "f32")).reshape(-1, pipe.plan.a_width)
+    ref = oracle.linear_readout(oracle.ace_product_flat(A_ref, pipe.plan.flat_arrays()), w, -2.0)
+    err = float(np.max(np.abs(got.cpu().double().numpy() - ref))) / float(np.sqrt(np.mean(ref * ref)))
+    flush(f"  err {err:.3e}")
+    assert err < TOL["f32"]
+
+
 def test_config4_full_size_rotation_covariance_fp64(gpu):
     flush("config 4 full size, rotation covariance of every L block (fp64)")
     import torch

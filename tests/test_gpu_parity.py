@@ -72,6 +72,37 @@ def test_density_accumulate_unsorted(gpu):
         density_accumulate(torch.as_tensor(ev, device=gpu), torch.as_tensor(centers + 100, device=gpu), N)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "f64"])
+@pytest.mark.parametrize("C", [1, 3, 16, 33])
+def test_density_accumulate_adjoint(gpu, dtype, C):
+    """Gather of centre-row adjoints: bit-exact copy of the oracle, transpose of density_accumulate."""
+    flush(f"density_accumulate_adjoint {dtype} C={C}")
+    import torch
+
+    from ye3t_amd.runtime import density_accumulate, density_accumulate_adjoint
+
+    rng = np.random.default_rng(100 + C)
+    E, N = 5000, 700
+    tdt = torch.float64 if dtype == "f64" else torch.float32
+    adj = torch.as_tensor(rng.normal(size=(N, C)), dtype=tdt)
+    centers = rng.integers(0, N - 50, E)  # unsorted; the last atoms own no edges
+    got = density_accumulate_adjoint(adj.to(gpu), torch.as_tensor(centers, device=gpu))
+    ref = oracle.density_accumulate_adjoint(adj.double().numpy(), centers)
+    assert got.dtype == tdt and tuple(got.shape) == (E, C)
+    assert np.array_equal(got.cpu().double().numpy(), ref)
+    # <accumulate(x), y> = <x, adjoint(y)> on the device pair
+    x = torch.as_tensor(rng.normal(size=(E, C)), dtype=torch.float64, device=gpu)
+    y = adj.double().to(gpu)
+    cen = torch.as_tensor(centers, device=gpu)
+    lhs = float((density_accumulate(x, cen, N) * y).sum())
+    rhs = float((x * density_accumulate_adjoint(y, cen)).sum())
+    assert abs(lhs - rhs) <= 1e-10 * max(1.0, abs(lhs))
+    empty = density_accumulate_adjoint(adj.to(gpu), torch.zeros(0, dtype=torch.int64, device=gpu))
+    assert tuple(empty.shape) == (0, C)
+    with pytest.raises(RuntimeError, match="out of range"):
+        density_accumulate_adjoint(adj.to(gpu), torch.as_tensor(centers + N, device=gpu))
+
+
 def _ragged_workload(dtype_mode):
     """Atoms with 0, 1, 63, 64, 65 and 130 neighbours (empty rows and multi-tile rows)."""
     rng = np.random.default_rng(13)
@@ -237,6 +268,59 @@ def test_end_to_end_small(gpu, cid, dtype, atoms):
     err = column_rel_error(B.cpu().numpy(), B_ref)
     flush(f"  err {err:.3e}")
     assert err < TOL[dtype]
+
+
+@pytest.mark.parametrize("cid,dtype,atoms", [(4, "f32", 257), (2, "f64", 129)])
+def test_linear_readout(gpu, cid, dtype, atoms):
+    """Fused (generated plans) and block-materialised (interpreted plans) readouts vs B_ref @ w + bias."""
+    flush(f"linear readout config {cid} {dtype} atoms={atoms}")
+    import torch
+
+    cfg = W.config(cid, atom_count=atoms)
+    inp = cfg.density.generate()
+    pipe = ACEPipeline(cfg.feature_spec, dtype, accumulate=cfg.accumulate if dtype == "f32" else None)
+    A = pipe.density(to_device_inputs(inp, dtype, gpu))
+    rows = A.reshape(-1, pipe.plan.a_width)
+    F = pipe.feature_count
+    rng = np.random.default_rng(40 + cid)
+    w = rng.normal(size=F)
+    got = pipe.linear(rows, torch.as_tensor(w, device=gpu), 0.37)
+    backend = pipe.last_linear_backend
+    flush(f"  backend {backend}")
+    assert backend == ("fused_generated" if pipe.kernel == "generated" else "materialized_blocks")
+    A_ref = oracle.ace_density(rounded_inputs(inp, dtype)).reshape(-1, pipe.plan.a_width)
+    ref = oracle.linear_readout(oracle.ace_product_flat(A_ref, pipe.plan.flat_arrays()), w, 0.37)
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    err = float(np.max(np.abs(got.cpu().double().numpy() - ref))) / rms
+    flush(f"  err {err:.3e}")
+    assert err < TOL[dtype]
+    # small sample blocks on the materialised path agree with one block
+    if backend == "materialized_blocks":
+        again = pipe.linear(rows, torch.as_tensor(w, device=gpu), 0.37, block_bytes=F * 8 * 37)
+        assert torch.equal(again, got)
+    # a one-hot weight reads one feature column exactly
+    B = pipe.product(rows)
+    for k in (0, F // 2, F - 1):
+        e = np.zeros(F)
+        e[k] = 1.0
+        col = pipe.linear(rows, torch.as_tensor(e, device=gpu), 0.0)
+        assert torch.equal(col, B[:, k])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f64"])
+def test_rows_dot(gpu, dtype):
+    flush(f"rows_dot {dtype}")
+    import torch
+
+    tdt = torch.float64 if dtype == "f64" else torch.float32
+    rng = np.random.default_rng(9)
+    for S, F in ((1, 1), (7, 161), (1001, 3273), (5, 0)):
+        B = torch.as_tensor(rng.normal(size=(S, F)), dtype=tdt)
+        w = torch.as_tensor(rng.normal(size=F), dtype=tdt)
+        got = native.rows_dot(B.to(gpu), w.to(gpu), -1.5).cpu().double().numpy()
+        ref = oracle.linear_readout(B.double().numpy(), w.double().numpy(), -1.5)
+        scale = max(1.0, float(np.sqrt(np.mean(ref * ref))))
+        assert np.max(np.abs(got - ref)) / scale < (1e-13 if dtype == "f64" else 1e-6)
 
 
 @pytest.mark.parametrize("kernel", ["interpreter", "generated"])

@@ -139,6 +139,26 @@ def test_density_against_index_add_and_reference():
         assert np.array_equal(out, oracle.density_accumulate(ev, centers, N, use_reference=True))
 
 
+def test_density_adjoint_is_the_gather_and_the_transpose():
+    rng = np.random.default_rng(5)
+    E, C, N = 400, 9, 50
+    adj = rng.normal(size=(N, C))
+    centers = rng.integers(0, N, E)
+    out = oracle.density_accumulate_adjoint(adj, centers)
+    assert np.array_equal(out, adj[centers])
+    # <accumulate(x), y> = <x, adjoint(y)>: the gather is the transpose of the scatter-add
+    x = rng.normal(size=(E, C))
+    lhs = np.sum(oracle.density_accumulate(x, centers, N) * adj)
+    rhs = np.sum(x * out)
+    assert abs(lhs - rhs) <= 1e-12 * max(1.0, abs(lhs))
+    assert oracle.density_accumulate_adjoint(adj, np.zeros(0, dtype=np.int64)).shape == (0, C)
+    with pytest.raises(ValueError):
+        oracle.density_accumulate_adjoint(adj, centers + N)
+    ref = oracle.ref_lib()
+    if ref is not None and hasattr(ref, "ref_density_accumulate_adjoint"):
+        assert np.array_equal(out, oracle.density_accumulate_adjoint(adj, centers, use_reference=True))
+
+
 def test_ace_density_is_the_reference_chain_and_rotation_covariant():
     from ye3t_amd.ace import workloads as W
 
@@ -217,3 +237,16 @@ def test_config4_features_rotate_by_wigner_d():
         cols = slice(first, first + 2 * L + 1)
         np.testing.assert_allclose(B1[:, cols], B0[:, cols] @ wigner_real(R, L).T, rtol=1e-9,
                                    atol=1e-9 * np.abs(B0[:, cols]).max())
+
+
+def test_linear_readout_selects_columns_and_is_linear():
+    rng = np.random.default_rng(8)
+    B = rng.normal(size=(50, 7))
+    for k in range(7):
+        e = np.zeros(7)
+        e[k] = 1.0
+        assert np.array_equal(oracle.linear_readout(B, e, 0.0), B[:, k])
+    w1, w2 = rng.normal(size=7), rng.normal(size=7)
+    lhs = oracle.linear_readout(B, w1 + w2, 0.5)
+    rhs = oracle.linear_readout(B, w1, 0.25) + oracle.linear_readout(B, w2, 0.25)
+    np.testing.assert_allclose(lhs, rhs, rtol=1e-13, atol=1e-13)

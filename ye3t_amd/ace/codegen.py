@@ -275,6 +275,82 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
     return source, meta
 
 
+def generate_readout(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_product_readout", waves=2):
+    """Fused linear readout ``out[s] = bias + sum_f W[f] B[s, f]`` without
+    materialising B: the persistent tile loop of :func:`generate_persistent`
+    (64 samples per tile, next tile's rows prefetched, ``waves`` waves sharing a
+    tile over contiguous output ranges), where each wave folds its outputs into
+    one fp-``dtype`` sum per sample as they are computed, in output order.  The
+    wave sums and the bias are added in a fixed order (deterministic); one
+    value per sample is stored.
+
+    Kernel signature: ``(const REAL* A, long samples, OUT* out, const REAL* W, REAL bias)``.
+    Counterpart of the reference's fused ``factorized_angular_linear``
+    (``execution_plan_cuda.cu:8957``; readout semantics ``execution_plan.py:13832-13850``).
+    """
+    out_dtype = out_dtype or dtype
+    if dtype == "f32" and out_dtype != "f32":
+        raise ValueError("an f32 plan writes f32 values")
+    real = "double" if dtype == "f64" else "float"
+    outt = "double" if out_dtype == "f64" else "float"
+    fma = "fma" if dtype == "f64" else "fmaf"
+    Wd = plan.a_width
+    nodes = plan.nodes
+    out = []
+    w = out.append
+    w("// generated by ye3t_amd.ace.codegen (fused linear readout) -- do not edit (compiled with hipRTC)")
+    w(f"#define REAL {real}")
+    w(f"#define OUT {outt}")
+    threads = 64 * waves
+    w(f"extern \"C\" __global__ __launch_bounds__({threads}) void {kernel_name}(")
+    w("    const REAL* __restrict__ A, long samples, OUT* __restrict__ out, const REAL* __restrict__ W, REAL bias) {")
+    w(f"  __shared__ REAL part[{waves}][64];")
+    w("  const int lane = threadIdx.x & 63;")
+    w("  const int wv = threadIdx.x >> 6;")
+    w("  const long tiles = (samples + 63) / 64;")
+    w("  long tile = blockIdx.x;")
+    w("  if (tile >= tiles) return;")
+    w("  long srow = tile * 64 + lane;")
+    w("  srow = srow < samples ? srow : samples - 1;")
+    for c in range(Wd):
+        w(f"  REAL a{c} = A[srow * {Wd}L + {c}];")
+    w("  for (;;) {")
+    w("    const long next = tile + gridDim.x;")
+    w("    long nrow = next * 64 + lane;")
+    w("    nrow = nrow < samples ? nrow : samples - 1;")
+    for c in range(Wd):
+        w(f"    const REAL n{c} = A[nrow * {Wd}L + {c}];")
+    for g, (f0, f1) in enumerate(_split_outputs(plan, waves)):
+        w(f"    if (wv == {g}) {{" if waves > 1 else "    {")
+        w("      REAL acc = (REAL)0;")
+        emitted = set()
+        for f in range(f0, f1):
+            root, comp = plan.outputs[f]
+            _emit_node_code(w, nodes, root, emitted, dtype, lambda c: f"a{c}")
+            w(f"      acc = {fma}(W[{f}], v{root}_{comp}, acc);")
+        w(f"      part[{g}][lane] = acc;")
+        w("    }")
+    w("    __syncthreads();")
+    w("    if (wv == 0) {")
+    w("      REAL r = bias;")
+    for g in range(waves):
+        w(f"      r += part[{g}][lane];")
+    w("      const long s = tile * 64 + lane;")
+    w("      if (s < samples) out[s] = (OUT)r;")
+    w("    }")
+    w("    __syncthreads();")
+    w("    if (next >= tiles) break;")
+    w("    tile = next;")
+    for c in range(Wd):
+        w(f"    a{c} = n{c};")
+    w("  }")
+    w("}")
+    src = "\n".join(out) + "\n"
+    meta = {"kernel": kernel_name, "threads": threads, "feature_count": plan.feature_count, "a_width": Wd,
+            "dtype": dtype, "out_dtype": out_dtype, "hash": hashlib.sha256(src.encode()).hexdigest()[:16]}
+    return src, meta
+
+
 def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generated", out_dtype=None, rows=None):
     """Return ``(source, meta)`` for a specialised product kernel.
 

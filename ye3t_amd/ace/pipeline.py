@@ -107,6 +107,47 @@ class ACEPipeline:
     def product(self, A_rows, out=None):
         return self.handle.forward(A_rows, out=out)
 
+    def linear(self, A_rows, weight, bias=0.0, out=None, block_bytes=1 << 30):
+        """Linear readout ``out[s] = bias + sum_k B[s, k] weight[k]`` (reference
+        ``factorized_angular_linear``, ``execution_plan.py:13793-13850``).
+
+        Plans with a generated product kernel use a fused, plan-specialised
+        readout kernel that never stores B (compiled on first use).  Larger
+        plans materialise B in sample blocks of at most ``block_bytes`` and
+        reduce each row with ``rows_dot`` (the reference's materialised path).
+        ``last_linear_backend`` records which ran.
+        """
+        import torch
+
+        F = self.plan.feature_count
+        weight = torch.as_tensor(weight, device=A_rows.device)
+        if weight.ndim != 1 or int(weight.shape[0]) != F:
+            raise ValueError(f"weight must be a vector of the {F} features")
+        S = int(A_rows.shape[0])
+        out_t = torch.float64 if self.dtype == "f64" else torch.float32
+        if out is None:
+            out = torch.empty((S,), dtype=out_t, device=A_rows.device)
+        if self.kernel == "generated":
+            if getattr(self.handle, "readout", None) is None:
+                from ye3t_amd.ace.codegen import generate_readout
+
+                source, meta = generate_readout(self.plan, self.accumulate, out_dtype=self.dtype)
+                self.handle.attach_readout(source, meta)
+            w = weight.to(torch.float64 if self.accumulate == "f64" else torch.float32).contiguous()
+            self.last_linear_backend = "fused_generated"
+            return self.handle.linear(A_rows, w, float(bias), out=out)
+        w = weight.to(out_t).contiguous()
+        elem = 8 if self.dtype == "f64" else 4
+        blk = max(1, min(S, int(block_bytes) // (F * elem)))
+        B = torch.empty((min(blk, S), F), dtype=out_t, device=A_rows.device)
+        for s0 in range(0, S, blk):
+            s1 = min(S, s0 + blk)
+            Bb = B[: s1 - s0]
+            self.handle.forward(A_rows[s0:s1], out=Bb)
+            native.rows_dot(Bb, w, float(bias), out=out[s0:s1])
+        self.last_linear_backend = "materialized_blocks"
+        return out
+
     def forward(self, dev_inp, channelwise=False, A_out=None, B_out=None):
         A = self.density(dev_inp, out=A_out)
         rows = A.reshape(-1, self.plan.a_width) if channelwise else A.reshape(A.shape[0], -1)

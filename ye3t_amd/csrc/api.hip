@@ -192,6 +192,25 @@ __global__ __launch_bounds__(256) void density_csr_kernel(const Real* __restrict
   }
 }
 
+// Gather of centre-row adjoints to edge rows: thread per (edge, vector of
+// channels), V a 16-byte vector when the rows allow it.  Consecutive threads
+// walk one row, so both the centre-row reads and the edge-row writes are
+// contiguous.  Centres are validated by the caller; an index outside
+// [0, N) is clamped so that no access leaves the array.
+template <typename V>
+__global__ __launch_bounds__(256) void density_adjoint_kernel(const V* __restrict__ adj,
+                                                              const int64_t* __restrict__ centers, int64_t E,
+                                                              int64_t CV, int64_t N, V* __restrict__ out) {
+  const int64_t total = E * CV;
+  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t e = idx / CV, c = idx - e * CV;
+    int64_t i = centers[e];
+    i = i < 0 ? 0 : (i >= N ? N - 1 : i);
+    out[idx] = adj[i * CV + c];
+  }
+}
+
 inline unsigned grid_for(int64_t work, int threads) {
   int64_t g = (work + threads - 1) / threads;
   if (g < 1) g = 1;
@@ -285,6 +304,32 @@ int ye3t_hip_density_accumulate_csr(int dtype, const void* ev, const int64_t* of
     return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);
   }
   return check_launch("density_csr_kernel");
+}
+
+int ye3t_hip_density_accumulate_adjoint(int dtype, const void* adj, const int64_t* centers, int64_t E, int64_t C,
+                                        int64_t N, void* out, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(E >= 0 && C >= 0 && N >= 0, "negative size");
+  if (E * C == 0) return YE3T_OK;
+  YE3T_REQUIRE(N >= 1, "edges need at least one atom");
+  YE3T_REQUIRE(adj && centers && out, "NULL input or output");
+  const size_t elem = dtype == YE3T_F64 ? 8 : 4;
+  YE3T_REQUIRE(dtype == YE3T_F64 || dtype == YE3T_F32, "unsupported dtype %d", dtype);
+  const bool vec = (size_t(C) * elem) % 16 == 0 && reinterpret_cast<uintptr_t>(adj) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  const hipStream_t s = as_stream(stream);
+  if (vec) {
+    const int64_t CV = int64_t(size_t(C) * elem / 16);
+    hipLaunchKernelGGL(density_adjoint_kernel<float4>, dim3(grid_for(E * CV, 256)), dim3(256), 0, s,
+                       (const float4*)adj, centers, E, CV, N, (float4*)out);
+  } else if (dtype == YE3T_F64) {
+    hipLaunchKernelGGL(density_adjoint_kernel<double>, dim3(grid_for(E * C, 256)), dim3(256), 0, s,
+                       (const double*)adj, centers, E, C, N, (double*)out);
+  } else {
+    hipLaunchKernelGGL(density_adjoint_kernel<float>, dim3(grid_for(E * C, 256)), dim3(256), 0, s,
+                       (const float*)adj, centers, E, C, N, (float*)out);
+  }
+  return check_launch("density_adjoint_kernel");
 }
 
 }  // extern "C"

@@ -42,6 +42,11 @@ struct ye3t_hip_product_plan {
   int generated_threads;   // threads per workgroup of the generated kernel
   int64_t generated_max_grid;  // persistent kernel: workgroups resident at once (0: not persistent)
   int use_interpreter;
+  // plan-specialised fused linear readout (optional)
+  hipModule_t readout_module;
+  hipFunction_t readout;
+  int readout_threads;
+  int64_t readout_max_grid;  // workgroups resident at once
 };
 
 namespace ye3t {
@@ -127,6 +132,25 @@ __global__ __launch_bounds__(kLanes) void product_kernel(
     const int r = idx / nf;
     const int c = idx - r * nf;
     B[(s0 + r) * F + c0 + c] = Out(ws[int(out_slots[o0 + c]) * kPad + r]);
+  }
+}
+
+// out[s] = bias + sum_k B[s, k] w[k]: one wave per row (grid-stride over rows),
+// lanes stride over k with fp64 partial sums, then a fixed butterfly over the
+// 64 lanes, so the result does not depend on timing.
+template <typename Real>
+__global__ __launch_bounds__(256) void rows_dot_kernel(const Real* __restrict__ B, int64_t samples, int64_t F,
+                                                       const Real* __restrict__ w, double bias,
+                                                       Real* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = int64_t(gridDim.x) * (blockDim.x >> 6);
+  for (int64_t s = int64_t(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6); s < samples; s += waves) {
+    const Real* __restrict__ row = B + s * F;
+    double acc = 0.0;
+    for (int64_t k = lane; k < F; k += 64) acc = fma(double(row[k]), double(w[k]), acc);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) out[s] = Real(bias + acc);
   }
 }
 
@@ -227,6 +251,7 @@ void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* p) {
   (void)hipFree(p->out_off);
   (void)hipFree(p->first_col);
   if (p->module) (void)hipModuleUnload(p->module);
+  if (p->readout_module) (void)hipModuleUnload(p->readout_module);
   (void)hipSetDevice(prev);
   delete p;
 }
@@ -451,6 +476,79 @@ int ye3t_hip_product_forward(const ye3t_hip_product_plan* p, const void* A, int6
                        p->chunk_count);
   }
   return check_launch("product_kernel");
+}
+
+int ye3t_hip_product_plan_attach_readout(ye3t_hip_product_plan* p, const void* code, int64_t size,
+                                         const char* kernel_name, int threads_per_block) {
+  clear_error();
+  YE3T_REQUIRE(p && code && size > 0 && kernel_name, "NULL argument");
+  YE3T_REQUIRE(threads_per_block >= kLanes && threads_per_block <= 1024 && threads_per_block % kLanes == 0,
+               "threads_per_block must be a multiple of 64 in [64, 1024]");
+  int prev = 0;
+  YE3T_CHECK_HIP(hipGetDevice(&prev));
+  YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
+  hipModule_t module;
+  YE3T_CHECK_HIP(hipModuleLoadData(&module, code));
+  hipFunction_t fn;
+  if (hipModuleGetFunction(&fn, module, kernel_name) != hipSuccess) {
+    (void)hipModuleUnload(module);
+    return set_error(YE3T_EINVAL, "kernel %s not found in code object", kernel_name);
+  }
+  int per_cu = 0, cus = 0;
+  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads_per_block, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device) != hipSuccess) {
+    (void)hipModuleUnload(module);
+    return set_error(YE3T_ELAUNCH, "occupancy query failed for %s", kernel_name);
+  }
+  if (p->readout_module) (void)hipModuleUnload(p->readout_module);
+  p->readout_module = module;
+  p->readout = fn;
+  p->readout_threads = threads_per_block;
+  p->readout_max_grid = int64_t(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  return YE3T_OK;
+}
+
+int ye3t_hip_product_linear_forward(const ye3t_hip_product_plan* p, const void* A, int64_t samples,
+                                    const void* weight, double bias, void* out, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(p != nullptr, "NULL plan");
+  YE3T_REQUIRE(samples >= 0, "negative sample count");
+  if (!p->readout) return set_error(YE3T_EUNSUPPORTED, "no fused readout kernel attached to this plan");
+  if (samples == 0) return YE3T_OK;
+  YE3T_REQUIRE(A && weight && out, "NULL input, weight or output");
+  int64_t grid = (samples + kLanes - 1) / kLanes;
+  if (grid > p->readout_max_grid) grid = p->readout_max_grid;
+  long s_arg = long(samples);
+  const void* a_arg = A;
+  void* o_arg = out;
+  const void* w_arg = weight;
+  double bias64 = bias;
+  float bias32 = float(bias);
+  void* args[] = {&a_arg, &s_arg, &o_arg, &w_arg,
+                  p->dtype == YE3T_F64 ? static_cast<void*>(&bias64) : static_cast<void*>(&bias32)};
+  YE3T_CHECK_HIP(hipModuleLaunchKernel(p->readout, unsigned(grid), 1, 1, unsigned(p->readout_threads), 1, 1, 0,
+                                       as_stream(stream), args, nullptr));
+  return YE3T_OK;
+}
+
+int ye3t_hip_rows_dot(int dtype, const void* B, int64_t samples, int64_t F, const void* weight, double bias,
+                      void* out, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(samples >= 0 && F >= 0, "negative size");
+  if (samples == 0) return YE3T_OK;
+  YE3T_REQUIRE(out && (F == 0 || (B && weight)), "NULL input, weight or output");
+  int64_t grid = (samples + 3) / 4;  // four waves (rows) per 256-thread workgroup
+  if (grid > (1 << 20)) grid = 1 << 20;
+  if (dtype == YE3T_F64) {
+    hipLaunchKernelGGL(rows_dot_kernel<double>, dim3(unsigned(grid)), dim3(256), 0, as_stream(stream),
+                       (const double*)B, samples, F, (const double*)weight, bias, (double*)out);
+  } else if (dtype == YE3T_F32) {
+    hipLaunchKernelGGL(rows_dot_kernel<float>, dim3(unsigned(grid)), dim3(256), 0, as_stream(stream),
+                       (const float*)B, samples, F, (const float*)weight, bias, (float*)out);
+  } else {
+    return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);
+  }
+  return check_launch("rows_dot_kernel");
 }
 
 int ye3t_hip_evaluate_factorized_schedule(int dtype, const void* bv, int64_t batch, int64_t basis, int64_t blocks,

@@ -16,6 +16,7 @@ HIP_OPERATIONS = (
     "cheb_exp_cos_radial_table_with_derivative",
     "spherical_harmonics_table_with_derivative",
     "density_accumulate",
+    "density_accumulate_adjoint",
     "ace_density_forward",
     "symmetric_power_monomial",
     "evaluate_factorized_schedule",
@@ -92,6 +93,27 @@ def density_accumulate(edge_values, centers, atom_count, *, backend="auto"):
     offsets = torch.zeros(atom_count + 1, dtype=torch.int64, device=values.device)
     offsets[1:] = torch.cumsum(counts, 0)
     return native.density_accumulate_csr(values, offsets, atom_count)
+
+
+def density_accumulate_adjoint(atomic_adjoint, centers, *, backend="auto"):
+    """Gather centre-row adjoints to edge rows (reference ``execution_plan.py:7987-8049``).
+
+    ``edge_adjoint[e] = atomic_adjoint[centers[e]]``; the adjoint of
+    :func:`density_accumulate`.  Any edge order; deterministic (a copy).
+    """
+    import torch
+
+    _backend(backend, {"auto", "native", "deterministic"})
+    atomic_adjoint = torch.as_tensor(atomic_adjoint)
+    _require_device(atomic_adjoint, "density_accumulate_adjoint")
+    centers = torch.as_tensor(centers, dtype=torch.int64, device=atomic_adjoint.device)
+    if atomic_adjoint.ndim != 2 or centers.ndim != 1:
+        raise ValueError("atomic_adjoint must be [N, C] and centers [E]")
+    if centers.numel():
+        lo, hi = int(centers.min()), int(centers.max())
+        if lo < 0 or hi >= int(atomic_adjoint.shape[0]):
+            raise RuntimeError("density_accumulate_adjoint center index out of range")
+    return native.density_accumulate_adjoint(atomic_adjoint.contiguous(), centers.contiguous())
 
 
 def symmetric_power_monomial_contraction(input, monomial_counts, output_offsets, monomial_values, *,

@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 44
+ABI_VERSION = 46
 _LIB = None
 
 F32, F64 = 0, 1
@@ -66,6 +66,7 @@ def lib():
     L.ye3t_hip_radial_table.argtypes = [ctypes.c_int, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp]
     L.ye3t_hip_real_sph_table.argtypes = [ctypes.c_int, _vp, _i64, _i64, ctypes.c_double, _vp, _vp, _vp]
     L.ye3t_hip_density_accumulate_csr.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _vp]
+    L.ye3t_hip_density_accumulate_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _i64, _vp, _vp]
     L.ye3t_hip_ace_density_forward.argtypes = [ctypes.POINTER(DensityArgs), _vp, _vp]
     L.ye3t_hip_symmetric_power_monomial.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp]
     L.ye3t_hip_evaluate_factorized_schedule.argtypes = [ctypes.c_int, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp,
@@ -83,6 +84,9 @@ def lib():
     L.ye3t_hip_product_plan_attach_generated.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, _i64, _i64, ctypes.c_int,
                                                          ctypes.c_int]
     L.ye3t_hip_product_plan_select.argtypes = [_vp, ctypes.c_int]
+    L.ye3t_hip_product_plan_attach_readout.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, ctypes.c_int]
+    L.ye3t_hip_product_linear_forward.argtypes = [_vp, _vp, _i64, _vp, ctypes.c_double, _vp, _vp]
+    L.ye3t_hip_rows_dot.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, ctypes.c_double, _vp, _vp]
     version = L.ye3t_hip_abi_version()
     if version != ABI_VERSION:
         raise RuntimeError(f"ye3t_hip ABI {version} does not match the bindings ({ABI_VERSION})")
@@ -97,6 +101,8 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_product_plan_create", "ye3t_hip_product_plan_destroy", "ye3t_hip_product_forward",
     "ye3t_hip_product_launch_info", "ye3t_hip_rtc_compile", "ye3t_hip_free",
     "ye3t_hip_product_plan_attach_generated", "ye3t_hip_product_plan_select", "ye3t_hip_last_density_kernel",
+    "ye3t_hip_density_accumulate_adjoint", "ye3t_hip_product_plan_attach_readout", "ye3t_hip_product_linear_forward",
+    "ye3t_hip_rows_dot",
 )
 
 
@@ -184,6 +190,21 @@ def density_accumulate_csr(edge_values, row_offsets, atom_count):
     _check(lib().ye3t_hip_density_accumulate_csr(_dtype_code(edge_values), _dev(edge_values, "edge_values"),
                                                  _dev(row_offsets, "row_offsets"), int(atom_count), C,
                                                  _dev(out, "out"), _stream()), "ye3t_hip_density_accumulate_csr")
+    return out
+
+
+def density_accumulate_adjoint(atomic_adjoint, centers):
+    """``edge_adjoint[e] = atomic_adjoint[centers[e]]``; centres must lie in ``[0, N)``."""
+    import torch
+
+    if atomic_adjoint.ndim != 2 or centers.ndim != 1 or centers.dtype != torch.int64:
+        raise ValueError("atomic_adjoint must be [N, C] and centers int64 [E]")
+    N, C = (int(x) for x in atomic_adjoint.shape)
+    E = int(centers.shape[0])
+    out = torch.empty((E, C), dtype=atomic_adjoint.dtype, device=atomic_adjoint.device)
+    _check(lib().ye3t_hip_density_accumulate_adjoint(_dtype_code(atomic_adjoint), _dev(atomic_adjoint, "atomic_adjoint"),
+                                                     _dev(centers, "centers"), E, C, N, _dev(out, "out"), _stream()),
+           "ye3t_hip_density_accumulate_adjoint")
     return out
 
 
@@ -400,3 +421,52 @@ class ProductPlanHandle:
         _check(lib().ye3t_hip_product_forward(self._handle, _dev(A, "A"), S, _dev(out, "B"), _stream()),
                "ye3t_hip_product_forward")
         return out
+
+    def attach_readout(self, source, meta):
+        """Compile and attach a fused linear readout kernel (``codegen.generate_readout``)."""
+        if meta["feature_count"] != self.feature_count or meta["a_width"] != self.program["a_width"]:
+            raise ValueError("readout kernel does not match this plan")
+        if meta["dtype"] != self.dtype or meta.get("out_dtype", meta["dtype"]) != self.out_dtype:
+            raise ValueError("readout kernel dtypes do not match this plan")
+        blob = rtc_compile(source)
+        self._readout_code = ctypes.create_string_buffer(blob, len(blob))
+        _check(lib().ye3t_hip_product_plan_attach_readout(self._handle, self._readout_code, len(blob),
+                                                          meta["kernel"].encode(), int(meta["threads"])),
+               "ye3t_hip_product_plan_attach_readout")
+        self.readout = meta
+
+    def linear(self, A, weight, bias, out=None):
+        """``out[s] = bias + sum_k B[s, k] weight[k]`` with the attached fused kernel (B never stored)."""
+        import torch
+
+        if A.ndim != 2 or int(A.shape[1]) != int(self.program["a_width"]):
+            raise ValueError(f"A must be [samples, {self.program['a_width']}]")
+        want = torch.float64 if self.dtype == "f64" else torch.float32
+        if A.dtype != want or weight.dtype != want or tuple(weight.shape) != (self.feature_count,):
+            raise ValueError(f"A and weight [{self.feature_count}] must be {want} for this plan")
+        out_t = torch.float64 if self.out_dtype == "f64" else torch.float32
+        S = int(A.shape[0])
+        if out is None:
+            out = torch.empty((S,), dtype=out_t, device=A.device)
+        elif tuple(out.shape) != (S,) or out.dtype != out_t:
+            raise ValueError("out has the wrong shape or dtype")
+        _check(lib().ye3t_hip_product_linear_forward(self._handle, _dev(A, "A"), S, _dev(weight, "weight"),
+                                                     float(bias), _dev(out, "out"), _stream()),
+               "ye3t_hip_product_linear_forward")
+        return out
+
+
+def rows_dot(B, weight, bias, out=None):
+    """``out[s] = bias + sum_k B[s, k] weight[k]`` over a materialised B (fp64 sums, fixed order)."""
+    import torch
+
+    if B.ndim != 2 or weight.ndim != 1 or int(weight.shape[0]) != int(B.shape[1]) or weight.dtype != B.dtype:
+        raise ValueError("B must be [S, F] and weight [F] of the same dtype")
+    S, F = (int(x) for x in B.shape)
+    if out is None:
+        out = torch.empty((S,), dtype=B.dtype, device=B.device)
+    elif tuple(out.shape) != (S,) or out.dtype != B.dtype:
+        raise ValueError("out has the wrong shape or dtype")
+    _check(lib().ye3t_hip_rows_dot(_dtype_code(B), _dev(B, "B"), S, F, _dev(weight, "weight"), float(bias),
+                                   _dev(out, "out"), _stream()), "ye3t_hip_rows_dot")
+    return out
