@@ -192,22 +192,32 @@ __global__ __launch_bounds__(256) void density_csr_kernel(const Real* __restrict
   }
 }
 
-// Gather of centre-row adjoints to edge rows: thread per (edge, vector of
-// channels), V a 16-byte vector when the rows allow it.  Consecutive threads
-// walk one row, so both the centre-row reads and the edge-row writes are
-// contiguous.  Centres are validated by the caller; an index outside
-// [0, N) is clamped so that no access leaves the array.
+// Gather of centre-row adjoints to edge rows.  A workgroup of 256 threads
+// copies whole edge rows: 256 / CV rows at a time when a row is at most 256
+// vectors (V = 16 bytes when the rows allow it), else one row in a loop;
+// indices within the group are 32-bit.  The output is streamed with
+// non-temporal stores (written once, not re-read here).  Centres are validated
+// by the caller; an index outside [0, N) is clamped so that no access leaves
+// the array.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <typename V>
 __global__ __launch_bounds__(256) void density_adjoint_kernel(const V* __restrict__ adj,
                                                               const int64_t* __restrict__ centers, int64_t E,
-                                                              int64_t CV, int64_t N, V* __restrict__ out) {
-  const int64_t total = E * CV;
-  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t e = idx / CV, c = idx - e * CV;
-    int64_t i = centers[e];
-    i = i < 0 ? 0 : (i >= N ? N - 1 : i);
-    out[idx] = adj[i * CV + c];
+                                                              int CV, int64_t N, V* __restrict__ out) {
+  const int epb = CV >= 256 ? 1 : 256 / CV;  // edge rows per pass of the workgroup
+  const int span = epb * CV;
+  for (int64_t e0 = int64_t(blockIdx.x) * epb; e0 < E; e0 += int64_t(gridDim.x) * epb) {
+    for (int t = threadIdx.x; t < span; t += 256) {
+      const int de = t / CV;
+      const int c = t - de * CV;
+      const int64_t e = e0 + de;
+      if (e < E) {
+        int64_t i = centers[e];
+        i = i < 0 ? 0 : (i >= N ? N - 1 : i);
+        __builtin_nontemporal_store(adj[i * CV + c], out + e * CV + c);
+      }
+    }
   }
 }
 
@@ -318,16 +328,19 @@ int ye3t_hip_density_accumulate_adjoint(int dtype, const void* adj, const int64_
   const bool vec = (size_t(C) * elem) % 16 == 0 && reinterpret_cast<uintptr_t>(adj) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(out) % 16 == 0;
   const hipStream_t s = as_stream(stream);
+  const int64_t CV = vec ? int64_t(size_t(C) * elem / 16) : C;
+  YE3T_REQUIRE(CV < (int64_t(1) << 30), "channel_count too large");
+  const int64_t epb = CV >= 256 ? 1 : 256 / CV;
+  const unsigned grid = grid_for((E + epb - 1) / epb, 1);
   if (vec) {
-    const int64_t CV = int64_t(size_t(C) * elem / 16);
-    hipLaunchKernelGGL(density_adjoint_kernel<float4>, dim3(grid_for(E * CV, 256)), dim3(256), 0, s,
-                       (const float4*)adj, centers, E, CV, N, (float4*)out);
+    hipLaunchKernelGGL(density_adjoint_kernel<f32x4>, dim3(grid), dim3(256), 0, s, (const f32x4*)adj, centers, E,
+                       int(CV), N, (f32x4*)out);
   } else if (dtype == YE3T_F64) {
-    hipLaunchKernelGGL(density_adjoint_kernel<double>, dim3(grid_for(E * C, 256)), dim3(256), 0, s,
-                       (const double*)adj, centers, E, C, N, (double*)out);
+    hipLaunchKernelGGL(density_adjoint_kernel<double>, dim3(grid), dim3(256), 0, s, (const double*)adj, centers, E,
+                       int(CV), N, (double*)out);
   } else {
-    hipLaunchKernelGGL(density_adjoint_kernel<float>, dim3(grid_for(E * C, 256)), dim3(256), 0, s,
-                       (const float*)adj, centers, E, C, N, (float*)out);
+    hipLaunchKernelGGL(density_adjoint_kernel<float>, dim3(grid), dim3(256), 0, s, (const float*)adj, centers, E,
+                       int(CV), N, (float*)out);
   }
   return check_launch("density_adjoint_kernel");
 }
