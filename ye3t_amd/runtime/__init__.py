@@ -21,6 +21,7 @@ HIP_OPERATIONS = (
     "symmetric_power_monomial",
     "evaluate_factorized_schedule",
     "ace_product_forward",
+    "factorized_angular_linear",
 )
 
 
