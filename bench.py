@@ -151,6 +151,25 @@ def bench_op(args, cfg):
                                 "peak_tflops": 78.6, "frac": flops / t / 1e12 / 78.6},
             "samples": S, "features_per_sample": pipe.feature_count})
         line["config"].update({"samples": S, "features": pipe.feature_count})
+    elif args.op == "product_adjoint":
+        pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots, kernel=args.kernel, accumulate=accumulate)
+        A = pipe.density(to_device_inputs(cfg.density.generate(), dtype, "cuda"))
+        rows = A.reshape(-1, pipe.plan.a_width)
+        S = int(rows.shape[0])
+        g_t = torch.float64 if dtype == "f64" else torch.float32
+        gB = torch.as_tensor(np.random.default_rng(6).normal(size=(S, pipe.feature_count)), dtype=g_t,
+                             device="cuda")
+        gA = torch.empty_like(rows)
+        pipe.product_adjoint(rows, gB, out=gA)  # compiles and attaches the adjoint kernel
+        t = _time_kernel(lambda: pipe.handle.adjoint(rows, gB, out=gA), args.steps, args.warmup)
+        nbytes = S * pipe.plan.a_width * rows.element_size() * 2 + S * pipe.feature_count * gB.element_size()
+        line.update({
+            "metric": "adjoint samples/s", "value": S / t, "unit": "samples/s", "higher_is_better": True,
+            "us_per_call": t * 1e6, "dtype": accumulate, "storage_dtype": dtype,
+            "roofline": {"bound": "hbm", "achieved": nbytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": nbytes},
+            "samples": S, "features_per_sample": pipe.feature_count})
+        line["config"].update({"samples": S, "features": pipe.feature_count})
     else:
         inp = cfg.density.generate()
         N = d.atom_count
@@ -185,7 +204,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--kernel", default="auto", choices=["auto", "generated", "interpreter"])
-    ap.add_argument("--op", default="pipeline", choices=["pipeline", "linear_readout", "density_accumulate_adjoint"],
+    ap.add_argument("--op", default="pipeline",
+                    choices=["pipeline", "linear_readout", "density_accumulate_adjoint", "product_adjoint"],
                     help="pipeline: the headline step (stage 1 + stage 2); the others time one widened op "
                          "on the config's shapes and print its own JSON line")
     ap.add_argument("--copy-probe", action="store_true",

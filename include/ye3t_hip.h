@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 46 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 47 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -221,7 +221,22 @@ int ye3t_hip_product_plan_attach_readout(ye3t_hip_product_plan* plan, const void
 int ye3t_hip_product_linear_forward(const ye3t_hip_product_plan* plan, const void* A, int64_t samples,
                                     const void* weight, double bias, void* out, ye3t_stream_t stream);
 
-/* out[s] = bias + sum_k B[s, k] weight[k] for a materialised B[samples, F]
+/* Attach a plan-specialised adjoint kernel (ye3t_amd/ace/codegen.py:
+ * generate_adjoint compiled with ye3t_hip_rtc_compile), signature
+ * (const T* A, const G* gB, long samples, T* gA), T = the plan's dtype, G = that
+ * of the feature gradients (the plan's out_dtype). */
+int ye3t_hip_product_plan_attach_adjoint(ye3t_hip_product_plan* plan, const void* code, int64_t size,
+                                         const char* kernel_name, int threads_per_block);
+
+/* gA[s] = J(A[s])^T gB[s]: the density gradient of a feature gradient gB
+ * [samples, feature_count] through the plan's product (forward values
+ * recomputed).  YE3T_EUNSUPPORTED when no adjoint kernel is attached.
+ * Replaces ye3t_runtime::factorized_angular_adjoint (execution_plan_cuda.cu:6361,
+ * CPU core ye3t_runtime_core.h:1431-1456) for ACE plans. */
+int ye3t_hip_product_adjoint(const ye3t_hip_product_plan* plan, const void* A, const void* gB, int64_t samples,
+                             void* gA, ye3t_stream_t stream);
+
+/* out[s] = bias + sum_k B[s, k] weight[k] for a materialised B[samples, F]/* out[s] = bias + sum_k B[s, k] weight[k] for a materialised B[samples, F]
  * (fp64 accumulation, fixed reduction order).  The reference's materialised
  * readout `features @ weight + bias` (execution_plan.py:13838-13845). */
 int ye3t_hip_rows_dot(int dtype, const void* B, int64_t samples, int64_t F, const void* weight, double bias,

@@ -48,6 +48,7 @@ def lib():
         L.oracle_symmetric_power_monomial.argtypes = [_d, _I, _I, _i64, _i64, _d, _I, _d]
         L.oracle_evaluate_componentwise.argtypes = [_d, _i64, _i64, _i64, _d, _d, _I, _I, _I, _I, _I]
         L.oracle_ace_product_flat.argtypes = [_d, _I, _I, _I, _i64, _d, _i32, _I, _i64, _d, _i32, _d]
+        L.oracle_ace_product_flat_adjoint.argtypes = [_d, _d, _I, _I, _I, _i64, _d, _i32, _I, _i64, _d, _i32, _d]
         L.oracle_max_threads.restype = ctypes.c_int
         L.oracle_set_threads.argtypes = [ctypes.c_int]
     return _LIB
@@ -209,3 +210,19 @@ def linear_readout(features, weight, bias):
     """``features @ weight + bias`` -- the reference's materialised readout
     (``execution_plan.py:13838-13845``), in fp64."""
     return _f64(features) @ _f64(weight) + float(bias)
+
+
+def ace_product_flat_adjoint(A, gB, plan_arrays):
+    """``gA[s] = J(A[s])^T gB[s]`` for the flat product (reverse mode of :func:`ace_product_flat`)."""
+    A = _f64(A)
+    S, W = A.shape
+    pa = plan_arrays
+    K = pa["column_offsets"].shape[0] - 1
+    gB = _f64(gB).reshape(S, K)
+    out = np.zeros((S, W))
+    lib().oracle_ace_product_flat_adjoint(
+        _p(A), _p(gB), S, W, int(pa["value_count"]), _p(_i64a(pa["value_offsets"]), _i64),
+        _p(_f64(pa["value_coeffs"])), _p(np.ascontiguousarray(pa["value_factors"], dtype=np.int32), _i32), K,
+        _p(_i64a(pa["column_offsets"]), _i64), _p(_f64(pa["term_coeffs"])),
+        _p(np.ascontiguousarray(pa["term_refs"], dtype=np.int32), _i32), _p(out))
+    return out

@@ -364,3 +364,70 @@ void oracle_ace_product_flat(const double* A, int64_t samples, int64_t a_width,
     free(vals);
   }
 }
+
+/* Reverse mode of oracle_ace_product_flat: gA[s] = J(A[s])^T gB[s], where
+ * B = f(A) is the flat form above (a polynomial of total degree <= 4 in A).
+ * Each term's product rule is expanded factor by factor (the counterpart of
+ * factorized_angular_adjoint, ye3t_runtime_core.h:1431-1456). */
+void oracle_ace_product_flat_adjoint(const double* A, const double* gB, int64_t samples, int64_t a_width,
+                                     int64_t value_count, const int64_t* value_offsets, const double* value_coeffs,
+                                     const int32_t* value_factors, int64_t column_count,
+                                     const int64_t* column_offsets, const double* term_coeffs,
+                                     const int32_t* term_refs, double* gA) {
+#pragma omp parallel
+  {
+    const size_t nv = (size_t)(value_count > 0 ? value_count : 1);
+    double* vals = (double*)malloc(nv * sizeof(double));
+    double* gv = (double*)malloc(nv * sizeof(double));
+#pragma omp for schedule(static)
+    for (int64_t s = 0; s < samples; ++s) {
+      const double* row = A + s * a_width;
+      const double* g = gB + s * column_count;
+      double* out = gA + s * a_width;
+      for (int64_t v = 0; v < value_count; ++v) {
+        double acc = 0.0;
+        for (int64_t t = value_offsets[v]; t < value_offsets[v + 1]; ++t) {
+          double m = value_coeffs[t];
+          for (int q = 0; q < 4; ++q) {
+            const int32_t f = value_factors[t * 4 + q];
+            if (f >= 0) m *= row[f];
+          }
+          acc += m;
+        }
+        vals[v] = acc;
+        gv[v] = 0.0;
+      }
+      for (int64_t c = 0; c < column_count; ++c) {
+        for (int64_t t = column_offsets[c]; t < column_offsets[c + 1]; ++t) {
+          for (int q = 0; q < 4; ++q) {
+            const int32_t r = term_refs[t * 4 + q];
+            if (r < 0) continue;
+            double m = term_coeffs[t] * g[c];
+            for (int q2 = 0; q2 < 4; ++q2) {
+              const int32_t r2 = term_refs[t * 4 + q2];
+              if (q2 != q && r2 >= 0) m *= vals[r2];
+            }
+            gv[r] += m;
+          }
+        }
+      }
+      for (int64_t k = 0; k < a_width; ++k) out[k] = 0.0;
+      for (int64_t v = 0; v < value_count; ++v) {
+        for (int64_t t = value_offsets[v]; t < value_offsets[v + 1]; ++t) {
+          for (int q = 0; q < 4; ++q) {
+            const int32_t f = value_factors[t * 4 + q];
+            if (f < 0) continue;
+            double m = value_coeffs[t] * gv[v];
+            for (int q2 = 0; q2 < 4; ++q2) {
+              const int32_t f2 = value_factors[t * 4 + q2];
+              if (q2 != q && f2 >= 0) m *= row[f2];
+            }
+            out[f] += m;
+          }
+        }
+      }
+    }
+    free(vals);
+    free(gv);
+  }
+}

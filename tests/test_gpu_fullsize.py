@@ -56,6 +56,23 @@ def test_config4_full_size_fused_linear_readout(gpu):
     assert err < TOL["f32"]
 
 
+def test_config4_full_size_product_adjoint(gpu):
+    """dL/dA over all 800 000 samples of the benchmark density against the oracle's reverse mode."""
+    flush("config 4 full size, product adjoint")
+    import torch
+
+    cfg = W.config(4)
+    pipe = ACEPipeline(cfg.feature_spec, "f32", accumulate=cfg.accumulate)
+    A = pipe.density(to_device_inputs(cfg.density.generate(), "f32", gpu)).reshape(-1, pipe.plan.a_width)
+    gB = torch.as_tensor(np.random.default_rng(78).normal(size=(A.shape[0], pipe.feature_count)),
+                         dtype=torch.float32, device=gpu)
+    gA = pipe.product_adjoint(A, gB)
+    ref = oracle.ace_product_flat_adjoint(A.cpu().numpy(), gB.cpu().double().numpy(), pipe.plan.flat_arrays())
+    err = column_rel_error(gA.cpu().numpy(), ref)
+    flush(f"  err {err:.3e}")
+    assert err < 1e-12
+
+
 def test_config4_full_size_rotation_covariance_fp64(gpu):
     flush("config 4 full size, rotation covariance of every L block (fp64)")
     import torch

@@ -250,3 +250,30 @@ def test_linear_readout_selects_columns_and_is_linear():
     lhs = oracle.linear_readout(B, w1 + w2, 0.5)
     rhs = oracle.linear_readout(B, w1, 0.25) + oracle.linear_readout(B, w2, 0.25)
     np.testing.assert_allclose(lhs, rhs, rtol=1e-13, atol=1e-13)
+
+
+def test_product_adjoint_matches_the_exact_directional_derivative():
+    """<gB, f'(A) d> = <f'(A)^T gB, d>, with f'(A) d taken from five forward
+    evaluations: B(A + t d) is a polynomial of degree <= 4 in t, for which the
+    central stencil (f(-2) - 8 f(-1) + 8 f(1) - f(2)) / 12 is exact."""
+    from ye3t_amd.ace import workloads as W
+    from ye3t_amd.ace.plan import ProductPlan
+
+    rng = np.random.default_rng(21)
+    for cid in (4, 2):
+        plan = ProductPlan(W.config(cid).feature_spec)
+        arrays = plan.flat_arrays()
+        A = rng.normal(size=(6, plan.a_width))
+        d = rng.normal(size=A.shape)
+        gB = rng.normal(size=(6, plan.feature_count))
+        f = {t: oracle.ace_product_flat(A + t * d, arrays) for t in (-2, -1, 1, 2)}
+        jd = (f[-2] - 8 * f[-1] + 8 * f[1] - f[2]) / 12.0
+        gA = oracle.ace_product_flat_adjoint(A, gB, arrays)
+        lhs = np.sum(gB * jd, axis=1)
+        rhs = np.sum(gA * d, axis=1)
+        np.testing.assert_allclose(lhs, rhs, rtol=1e-9, atol=1e-9 * np.max(np.abs(lhs)))
+        # columns of A no feature depends on have zero gradient
+        used = np.zeros(plan.a_width, dtype=bool)
+        vf = np.asarray(arrays["value_factors"])
+        used[vf[vf >= 0]] = True
+        assert not np.any(gA[:, ~used])

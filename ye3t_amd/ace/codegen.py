@@ -351,6 +351,118 @@ def generate_readout(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_produc
     return src, meta
 
 
+def generate_adjoint(plan, dtype="f64", grad_dtype=None, kernel_name="ye3t_product_adjoint", waves=2):
+    """Reverse mode of the product: ``gA[s] = J(A[s])^T gB[s]`` (counterpart of
+    the reference's ``factorized_angular_adjoint``, ``execution_plan_cuda.cu:6361``;
+    CPU core ``ye3t_runtime_core.h:1431-1456``).
+
+    Persistent over 64-sample tiles.  The tile's output gradients (``gB``, of
+    ``grad_dtype``, default ``dtype``) are loaded into LDS with contiguous loads.
+    The adjoint is linear in gB, so wave w handles the w-th of ``waves`` output
+    ranges: it recomputes the forward values its range depends on, then sweeps
+    the nodes in reverse creation order (dependencies are created first)
+    accumulating node adjoints with the product rule, and leaves its partial
+    density gradient in LDS.  The partials are added in wave order (fixed) and
+    the ``[rows, a_width]`` block of gA is stored with contiguous stores.
+
+    Kernel signature: ``(const REAL* A, const GT* gB, long samples, REAL* gA)``.
+    """
+    grad_dtype = grad_dtype or dtype
+    if dtype == "f32" and grad_dtype != "f32":
+        raise ValueError("an f32 plan takes f32 gradients")
+    real = "double" if dtype == "f64" else "float"
+    gt = "double" if grad_dtype == "f64" else "float"
+    fma = "fma" if dtype == "f64" else "fmaf"
+    F, Wd = plan.feature_count, plan.a_width
+    pitch = F if F % 2 else F + 1
+    nodes = plan.nodes
+    out = []
+    w = out.append
+    w("// generated by ye3t_amd.ace.codegen (product adjoint) -- do not edit (compiled with hipRTC)")
+    w(f"#define REAL {real}")
+    w(f"#define GT {gt}")
+    threads = 64 * waves
+    w(f"extern \"C\" __global__ __launch_bounds__({threads}) void {kernel_name}(")
+    w("    const REAL* __restrict__ A, const GT* __restrict__ gB, long samples, REAL* __restrict__ gA) {")
+    w(f"  __shared__ GT gt[64 * {pitch}];")
+    w(f"  __shared__ REAL gp[{waves}][{Wd}][64];")
+    w("  const int lane = threadIdx.x & 63;")
+    w("  const int wv = threadIdx.x >> 6;")
+    w("  const long tiles = (samples + 63) / 64;")
+    w("  for (long tile = blockIdx.x; tile < tiles; tile += gridDim.x) {")
+    w("    const long s0 = tile * 64;")
+    w("    const int rows = samples - s0 < 64 ? (int)(samples - s0) : 64;")
+    w(f"    for (int i = threadIdx.x; i < rows * {F}; i += {threads}) {{")
+    w(f"      const int r = i / {F};")
+    w(f"      gt[r * {pitch} + (i - r * {F})] = gB[s0 * {F}L + i];")
+    w("    }")
+    w("    const long srow = s0 + (lane < rows ? lane : rows - 1);")
+    for c in range(Wd):
+        w(f"    const REAL a{c} = A[srow * {Wd}L + {c}];")
+    w("    __syncthreads();")
+    for g, (f0, f1) in enumerate(_split_outputs(plan, waves)):
+        w(f"    if (wv == {g}) {{" if waves > 1 else "    {")
+        roots = sorted({plan.outputs[f][0] for f in range(f0, f1)})
+        needed = set()
+        for r in roots:
+            _closure(nodes, r, needed)
+        emitted = set()
+        for r in roots:
+            for d in nodes[r]["deps"]:
+                _emit_node_code(w, nodes, d, emitted, dtype, lambda c: f"a{c}")
+        # adjoint accumulators: output components start from the gradient tile
+        init = {}
+        for f in range(f0, f1):
+            root, comp = plan.outputs[f]
+            init[(root, comp)] = f"(REAL)gt[lane * {pitch} + {f}]"
+        for n in sorted(needed):
+            for c in range(nodes[n]["dim"]):
+                w(f"      REAL g{n}_{c} = {init.get((n, c), '(REAL)0')};")
+        for n in sorted(needed, reverse=True):
+            nd = nodes[n]
+            if nd["kind"] == "leaf":
+                continue
+            if nd["kind"] == "pair":
+                da, db = nd["deps"]
+                for oc, value, (i, j) in nd["terms"]:
+                    cg = f"({_lit(value, dtype)} * g{n}_{oc})"
+                    w(f"      g{da}_{i} = {fma}({cg}, v{db}_{j}, g{da}_{i});")
+                    w(f"      g{db}_{j} = {fma}({cg}, v{da}_{i}, g{db}_{j});")
+            else:
+                srcn = nd["deps"][0]
+                for oc, value, factors in nd["terms"]:
+                    cg = f"({_lit(value, dtype)} * g{n}_{oc})"
+                    for m, q in enumerate(factors):
+                        rest = [f"v{srcn}_{x}" for k2, x in enumerate(factors) if k2 != m]
+                        prod = " * ".join(rest) if rest else "(REAL)1"
+                        w(f"      g{srcn}_{q} = {fma}({cg}, {prod}, g{srcn}_{q});")
+        touched = {}
+        for n in sorted(needed):
+            nd = nodes[n]
+            if nd["kind"] == "leaf":
+                for c in range(nd["dim"]):
+                    touched[nd["a_offset"] + c] = f"g{n}_{c}"
+        for col in range(Wd):
+            w(f"      gp[{g}][{col}][lane] = {touched.get(col, '(REAL)0')};")
+        w("    }")
+    w("    __syncthreads();")
+    w(f"    for (int i = threadIdx.x; i < rows * {Wd}; i += {threads}) {{")
+    w(f"      const int r = i / {Wd};")
+    w(f"      const int col = i - r * {Wd};")
+    w("      REAL v = gp[0][col][r];")
+    for g in range(1, waves):
+        w(f"      v += gp[{g}][col][r];")
+    w(f"      gA[s0 * {Wd}L + i] = v;")
+    w("    }")
+    w("    __syncthreads();")
+    w("  }")
+    w("}")
+    src = "\n".join(out) + "\n"
+    meta = {"kernel": kernel_name, "threads": threads, "feature_count": F, "a_width": Wd, "dtype": dtype,
+            "grad_dtype": grad_dtype, "hash": hashlib.sha256(src.encode()).hexdigest()[:16]}
+    return src, meta
+
+
 def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generated", out_dtype=None, rows=None):
     """Return ``(source, meta)`` for a specialised product kernel.
 

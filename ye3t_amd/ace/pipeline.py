@@ -107,6 +107,21 @@ class ACEPipeline:
     def product(self, A_rows, out=None):
         return self.handle.forward(A_rows, out=out)
 
+    def product_adjoint(self, A_rows, gB, out=None):
+        """Density gradient ``gA[s] = J(A[s])^T gB[s]`` of a feature gradient
+        (reference ``factorized_angular_adjoint``), with a plan-specialised
+        kernel compiled on first use.  Plans too large for generated code raise
+        ``NotImplementedError`` (no device adjoint for them yet)."""
+        if self.kernel != "generated":
+            raise NotImplementedError("the device adjoint needs a plan small enough for a generated kernel "
+                                      f"({self.plan.feature_count} features here)")
+        if getattr(self.handle, "adjoint_kernel", None) is None:
+            from ye3t_amd.ace.codegen import generate_adjoint
+
+            source, meta = generate_adjoint(self.plan, self.accumulate, grad_dtype=self.dtype)
+            self.handle.attach_adjoint(source, meta)
+        return self.handle.adjoint(A_rows, gB, out=out)
+
     def linear(self, A_rows, weight, bias=0.0, out=None, block_bytes=1 << 30):
         """Linear readout ``out[s] = bias + sum_k B[s, k] weight[k]`` (reference
         ``factorized_angular_linear``, ``execution_plan.py:13793-13850``).

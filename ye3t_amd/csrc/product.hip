@@ -47,6 +47,11 @@ struct ye3t_hip_product_plan {
   hipFunction_t readout;
   int readout_threads;
   int64_t readout_max_grid;  // workgroups resident at once
+  // plan-specialised adjoint (optional)
+  hipModule_t adjoint_module;
+  hipFunction_t adjoint;
+  int adjoint_threads;
+  int64_t adjoint_max_grid;
 };
 
 namespace ye3t {
@@ -252,6 +257,7 @@ void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* p) {
   (void)hipFree(p->first_col);
   if (p->module) (void)hipModuleUnload(p->module);
   if (p->readout_module) (void)hipModuleUnload(p->readout_module);
+  if (p->adjoint_module) (void)hipModuleUnload(p->adjoint_module);
   (void)hipSetDevice(prev);
   delete p;
 }
@@ -478,33 +484,85 @@ int ye3t_hip_product_forward(const ye3t_hip_product_plan* p, const void* A, int6
   return check_launch("product_kernel");
 }
 
+namespace {
+// Load `kernel_name` from a code object for a persistent launch: the module,
+// the function and the number of workgroups of `threads` the device holds at once.
+int load_persistent(const ye3t_hip_product_plan* p, const void* code, const char* kernel_name, int threads,
+                    hipModule_t* module, hipFunction_t* fn, int64_t* max_grid) {
+  int prev = 0;
+  YE3T_CHECK_HIP(hipGetDevice(&prev));
+  YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
+  YE3T_CHECK_HIP(hipModuleLoadData(module, code));
+  if (hipModuleGetFunction(fn, *module, kernel_name) != hipSuccess) {
+    (void)hipModuleUnload(*module);
+    return set_error(YE3T_EINVAL, "kernel %s not found in code object", kernel_name);
+  }
+  int per_cu = 0, cus = 0;
+  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, *fn, threads, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device) != hipSuccess) {
+    (void)hipModuleUnload(*module);
+    return set_error(YE3T_ELAUNCH, "occupancy query failed for %s", kernel_name);
+  }
+  *max_grid = int64_t(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  return YE3T_OK;
+}
+}  // namespace
+
 int ye3t_hip_product_plan_attach_readout(ye3t_hip_product_plan* p, const void* code, int64_t size,
                                          const char* kernel_name, int threads_per_block) {
   clear_error();
   YE3T_REQUIRE(p && code && size > 0 && kernel_name, "NULL argument");
   YE3T_REQUIRE(threads_per_block >= kLanes && threads_per_block <= 1024 && threads_per_block % kLanes == 0,
                "threads_per_block must be a multiple of 64 in [64, 1024]");
-  int prev = 0;
-  YE3T_CHECK_HIP(hipGetDevice(&prev));
-  YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
   hipModule_t module;
-  YE3T_CHECK_HIP(hipModuleLoadData(&module, code));
   hipFunction_t fn;
-  if (hipModuleGetFunction(&fn, module, kernel_name) != hipSuccess) {
-    (void)hipModuleUnload(module);
-    return set_error(YE3T_EINVAL, "kernel %s not found in code object", kernel_name);
-  }
-  int per_cu = 0, cus = 0;
-  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads_per_block, 0) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device) != hipSuccess) {
-    (void)hipModuleUnload(module);
-    return set_error(YE3T_ELAUNCH, "occupancy query failed for %s", kernel_name);
-  }
+  int64_t max_grid = 0;
+  const int rc = load_persistent(p, code, kernel_name, threads_per_block, &module, &fn, &max_grid);
+  if (rc != YE3T_OK) return rc;
   if (p->readout_module) (void)hipModuleUnload(p->readout_module);
   p->readout_module = module;
   p->readout = fn;
   p->readout_threads = threads_per_block;
-  p->readout_max_grid = int64_t(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  p->readout_max_grid = max_grid;
+  return YE3T_OK;
+}
+
+int ye3t_hip_product_plan_attach_adjoint(ye3t_hip_product_plan* p, const void* code, int64_t size,
+                                         const char* kernel_name, int threads_per_block) {
+  clear_error();
+  YE3T_REQUIRE(p && code && size > 0 && kernel_name, "NULL argument");
+  YE3T_REQUIRE(threads_per_block >= kLanes && threads_per_block <= 1024 && threads_per_block % kLanes == 0,
+               "threads_per_block must be a multiple of 64 in [64, 1024]");
+  hipModule_t module;
+  hipFunction_t fn;
+  int64_t max_grid = 0;
+  const int rc = load_persistent(p, code, kernel_name, threads_per_block, &module, &fn, &max_grid);
+  if (rc != YE3T_OK) return rc;
+  if (p->adjoint_module) (void)hipModuleUnload(p->adjoint_module);
+  p->adjoint_module = module;
+  p->adjoint = fn;
+  p->adjoint_threads = threads_per_block;
+  p->adjoint_max_grid = max_grid;
+  return YE3T_OK;
+}
+
+int ye3t_hip_product_adjoint(const ye3t_hip_product_plan* p, const void* A, const void* gB, int64_t samples,
+                             void* gA, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(p != nullptr, "NULL plan");
+  YE3T_REQUIRE(samples >= 0, "negative sample count");
+  if (!p->adjoint) return set_error(YE3T_EUNSUPPORTED, "no adjoint kernel attached to this plan");
+  if (samples == 0) return YE3T_OK;
+  YE3T_REQUIRE(A && gB && gA, "NULL input, gradient or output");
+  int64_t grid = (samples + kLanes - 1) / kLanes;
+  if (grid > p->adjoint_max_grid) grid = p->adjoint_max_grid;
+  long s_arg = long(samples);
+  const void* a_arg = A;
+  const void* g_arg = gB;
+  void* o_arg = gA;
+  void* args[] = {&a_arg, &g_arg, &s_arg, &o_arg};
+  YE3T_CHECK_HIP(hipModuleLaunchKernel(p->adjoint, unsigned(grid), 1, 1, unsigned(p->adjoint_threads), 1, 1, 0,
+                                       as_stream(stream), args, nullptr));
   return YE3T_OK;
 }
 

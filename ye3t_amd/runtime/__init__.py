@@ -22,6 +22,7 @@ HIP_OPERATIONS = (
     "evaluate_factorized_schedule",
     "ace_product_forward",
     "factorized_angular_linear",
+    "factorized_angular_adjoint",
 )
 
 

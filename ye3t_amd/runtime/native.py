@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 46
+ABI_VERSION = 47
 _LIB = None
 
 F32, F64 = 0, 1
@@ -87,6 +87,8 @@ def lib():
     L.ye3t_hip_product_plan_attach_readout.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, ctypes.c_int]
     L.ye3t_hip_product_linear_forward.argtypes = [_vp, _vp, _i64, _vp, ctypes.c_double, _vp, _vp]
     L.ye3t_hip_rows_dot.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, ctypes.c_double, _vp, _vp]
+    L.ye3t_hip_product_plan_attach_adjoint.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, ctypes.c_int]
+    L.ye3t_hip_product_adjoint.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
     version = L.ye3t_hip_abi_version()
     if version != ABI_VERSION:
         raise RuntimeError(f"ye3t_hip ABI {version} does not match the bindings ({ABI_VERSION})")
@@ -102,7 +104,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_product_launch_info", "ye3t_hip_rtc_compile", "ye3t_hip_free",
     "ye3t_hip_product_plan_attach_generated", "ye3t_hip_product_plan_select", "ye3t_hip_last_density_kernel",
     "ye3t_hip_density_accumulate_adjoint", "ye3t_hip_product_plan_attach_readout", "ye3t_hip_product_linear_forward",
-    "ye3t_hip_rows_dot",
+    "ye3t_hip_rows_dot", "ye3t_hip_product_plan_attach_adjoint", "ye3t_hip_product_adjoint",
 )
 
 
@@ -434,6 +436,39 @@ class ProductPlanHandle:
                                                           meta["kernel"].encode(), int(meta["threads"])),
                "ye3t_hip_product_plan_attach_readout")
         self.readout = meta
+
+    def attach_adjoint(self, source, meta):
+        """Compile and attach a plan-specialised adjoint kernel (``codegen.generate_adjoint``)."""
+        if meta["feature_count"] != self.feature_count or meta["a_width"] != self.program["a_width"]:
+            raise ValueError("adjoint kernel does not match this plan")
+        if meta["dtype"] != self.dtype or meta.get("grad_dtype", meta["dtype"]) != self.out_dtype:
+            raise ValueError("adjoint kernel dtypes do not match this plan")
+        blob = rtc_compile(source)
+        self._adjoint_code = ctypes.create_string_buffer(blob, len(blob))
+        _check(lib().ye3t_hip_product_plan_attach_adjoint(self._handle, self._adjoint_code, len(blob),
+                                                          meta["kernel"].encode(), int(meta["threads"])),
+               "ye3t_hip_product_plan_attach_adjoint")
+        self.adjoint_kernel = meta
+
+    def adjoint(self, A, gB, out=None):
+        """``gA[s] = J(A[s])^T gB[s]`` with the attached adjoint kernel (forward values recomputed)."""
+        import torch
+
+        W = int(self.program["a_width"])
+        a_t = torch.float64 if self.dtype == "f64" else torch.float32
+        g_t = torch.float64 if self.out_dtype == "f64" else torch.float32
+        if A.ndim != 2 or int(A.shape[1]) != W or A.dtype != a_t:
+            raise ValueError(f"A must be [samples, {W}] of {a_t}")
+        S = int(A.shape[0])
+        if tuple(gB.shape) != (S, self.feature_count) or gB.dtype != g_t:
+            raise ValueError(f"gB must be [{S}, {self.feature_count}] of {g_t}")
+        if out is None:
+            out = torch.empty((S, W), dtype=a_t, device=A.device)
+        elif tuple(out.shape) != (S, W) or out.dtype != a_t:
+            raise ValueError("out has the wrong shape or dtype")
+        _check(lib().ye3t_hip_product_adjoint(self._handle, _dev(A, "A"), _dev(gB.contiguous(), "gB"), S,
+                                              _dev(out, "gA"), _stream()), "ye3t_hip_product_adjoint")
+        return out
 
     def linear(self, A, weight, bias, out=None):
         """``out[s] = bias + sum_k B[s, k] weight[k]`` with the attached fused kernel (B never stored)."""
