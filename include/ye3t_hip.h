@@ -229,8 +229,8 @@ int ye3t_hip_product_plan_attach_adjoint(ye3t_hip_product_plan* plan, const void
                                          const char* kernel_name, int threads_per_block);
 
 /* gA[s] = J(A[s])^T gB[s]: the density gradient of a feature gradient gB
- * [samples, feature_count] through the plan's product (forward values
- * recomputed).  YE3T_EUNSUPPORTED when no adjoint kernel is attached.
+ * [samples, feature_count] (16-byte aligned) through the plan's product
+ * (forward values recomputed).  YE3T_EUNSUPPORTED when no adjoint kernel is attached.
  * Replaces ye3t_runtime::factorized_angular_adjoint (execution_plan_cuda.cu:6361,
  * CPU core ye3t_runtime_core.h:1431-1456) for ACE plans. */
 int ye3t_hip_product_adjoint(const ye3t_hip_product_plan* plan, const void* A, const void* gB, int64_t samples,

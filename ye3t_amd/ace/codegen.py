@@ -357,7 +357,8 @@ def generate_adjoint(plan, dtype="f64", grad_dtype=None, kernel_name="ye3t_produ
     CPU core ``ye3t_runtime_core.h:1431-1456``).
 
     Persistent over 64-sample tiles.  The tile's output gradients (``gB``, of
-    ``grad_dtype``, default ``dtype``) are loaded into LDS with contiguous loads.
+    ``grad_dtype``, default ``dtype``; 16-byte aligned) are loaded into LDS with
+    contiguous 16-byte loads, all issued before the first LDS write.
     The adjoint is linear in gB, so wave w handles the w-th of ``waves`` output
     ranges: it recomputes the forward values its range depends on, then sweeps
     the nodes in reverse creation order (dependencies are created first)
@@ -384,7 +385,7 @@ def generate_adjoint(plan, dtype="f64", grad_dtype=None, kernel_name="ye3t_produ
     threads = 64 * waves
     w(f"extern \"C\" __global__ __launch_bounds__({threads}) void {kernel_name}(")
     w("    const REAL* __restrict__ A, const GT* __restrict__ gB, long samples, REAL* __restrict__ gA) {")
-    w(f"  __shared__ GT gt[64 * {pitch}];")
+    w(f"  __shared__ __attribute__((aligned(16))) GT gt[64 * {pitch}];")
     w(f"  __shared__ REAL gp[{waves}][{Wd}][64];")
     w("  const int lane = threadIdx.x & 63;")
     w("  const int wv = threadIdx.x >> 6;")
@@ -392,10 +393,27 @@ def generate_adjoint(plan, dtype="f64", grad_dtype=None, kernel_name="ye3t_produ
     w("  for (long tile = blockIdx.x; tile < tiles; tile += gridDim.x) {")
     w("    const long s0 = tile * 64;")
     w("    const int rows = samples - s0 < 64 ? (int)(samples - s0) : 64;")
-    w(f"    for (int i = threadIdx.x; i < rows * {F}; i += {threads}) {{")
-    w(f"      const int r = i / {F};")
-    w(f"      gt[r * {pitch} + (i - r * {F})] = gB[s0 * {F}L + i];")
-    w("    }")
+    if pitch == F:
+        # the LDS tile is the contiguous [rows, F] block of gB: every 16-byte
+        # load of the block is issued before the first LDS write (one memory
+        # latency per tile), then a scalar tail for a partial tile
+        ve = 16 // (8 if grad_dtype == "f64" else 4)
+        vt = "double" if grad_dtype == "f64" else "float"
+        iters = -(-(64 * F // ve) // threads)
+        w(f"    typedef {vt} gv __attribute__((ext_vector_type({ve})));")
+        w(f"    const int nv = rows * {F} / {ve};")
+        w(f"    const gv* __restrict__ src = (const gv*)(gB + s0 * {F}L);")
+        for k in range(iters):
+            w(f"    const int j{k} = threadIdx.x + {threads * k};")
+            w(f"    const gv t{k} = src[j{k} < nv ? j{k} : 0];")
+        for k in range(iters):
+            w(f"    if (j{k} < nv) ((gv*)gt)[j{k}] = t{k};")
+        w(f"    for (int i = nv * {ve} + (int)threadIdx.x; i < rows * {F}; i += {threads}) gt[i] = gB[s0 * {F}L + i];")
+    else:
+        w(f"    for (int i = threadIdx.x; i < rows * {F}; i += {threads}) {{")
+        w(f"      const int r = i / {F};")
+        w(f"      gt[r * {pitch} + (i - r * {F})] = gB[s0 * {F}L + i];")
+        w("    }")
     w("    const long srow = s0 + (lane < rows ? lane : rows - 1);")
     for c in range(Wd):
         w(f"    const REAL a{c} = A[srow * {Wd}L + {c}];")

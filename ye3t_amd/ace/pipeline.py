@@ -118,7 +118,9 @@ class ACEPipeline:
         if getattr(self.handle, "adjoint_kernel", None) is None:
             from ye3t_amd.ace.codegen import generate_adjoint
 
-            source, meta = generate_adjoint(self.plan, self.accumulate, grad_dtype=self.dtype)
+            waves = os.environ.get("YE3T_ADJOINT_WAVES")  # waves sharing a tile (tuning)
+            source, meta = generate_adjoint(self.plan, self.accumulate, grad_dtype=self.dtype,
+                                            waves=int(waves) if waves else 2)
             self.handle.attach_adjoint(source, meta)
         return self.handle.adjoint(A_rows, gB, out=out)
 

@@ -554,6 +554,7 @@ int ye3t_hip_product_adjoint(const ye3t_hip_product_plan* p, const void* A, cons
   if (!p->adjoint) return set_error(YE3T_EUNSUPPORTED, "no adjoint kernel attached to this plan");
   if (samples == 0) return YE3T_OK;
   YE3T_REQUIRE(A && gB && gA, "NULL input, gradient or output");
+  YE3T_REQUIRE(reinterpret_cast<uintptr_t>(gB) % 16 == 0, "gB must be 16-byte aligned (tiles load 16-byte words)");
   int64_t grid = (samples + kLanes - 1) / kLanes;
   if (grid > p->adjoint_max_grid) grid = p->adjoint_max_grid;
   long s_arg = long(samples);
