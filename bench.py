@@ -170,6 +170,58 @@ def bench_op(args, cfg):
                          "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": nbytes},
             "samples": S, "features_per_sample": pipe.feature_count})
         line["config"].update({"samples": S, "features": pipe.feature_count})
+    elif args.op == "neighbor_list":
+        import ctypes
+
+        # uniform random positions at the config's atom count and cutoff; box
+        # edge chosen for a number density of 0.05 per unit volume (26 neighbours
+        # inside the box at cutoff 5, about 24 with the open faces)
+        N = d.atom_count
+        box = (N / 0.05) ** (1.0 / 3.0)
+        cutoff = float(d.radius)
+        npdt, tdt = (np.float64, torch.float64) if dtype == "f64" else (np.float32, torch.float32)
+        pos_np = np.random.default_rng(5).uniform(0.0, box, size=(N, 3)).astype(npdt)
+        pos = torch.as_tensor(pos_np, device="cuda")
+        nl = native.neighbor_list(pos, cutoff)  # validates the arguments; sizes the outputs
+        E = int(nl["edge_sources"].shape[0])
+        grid = native.cell_grid(pos_np.min(0), pos_np.max(0), cutoff, N)
+        L = native.lib()
+        ws_bytes = int(L.ye3t_hip_neighbor_workspace_bytes(N, ctypes.byref(grid)))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+        offs = torch.empty(N + 1, dtype=torch.int64, device="cuda")
+        cen, nbr, vec = (torch.empty_like(nl[k]) for k in ("edge_targets", "edge_sources", "edge_vectors"))
+        code = native.F64 if dtype == "f64" else native.F32
+        stream = native._stream()
+
+        def count():
+            native._check(L.ye3t_hip_neighbor_count(code, pos.data_ptr(), N, ctypes.byref(grid), cutoff,
+                                                    ws.data_ptr(), ws_bytes, offs.data_ptr(), stream), "count")
+
+        def fill():
+            native._check(L.ye3t_hip_neighbor_fill(code, N, ctypes.byref(grid), cutoff,
+                                                   ws.data_ptr(), ws_bytes, offs.data_ptr(), E, cen.data_ptr(),
+                                                   nbr.data_ptr(), vec.data_ptr(), stream), "fill")
+
+        count()
+        fill()
+        torch.cuda.synchronize()
+        assert torch.equal(offs, nl["target_offsets"]) and torch.equal(nbr, nl["edge_sources"])
+        t_count = _time_kernel(count, args.steps, args.warmup)
+        t_fill = _time_kernel(fill, args.steps, args.warmup)
+        t_build = _time_kernel(lambda: native.neighbor_list(pos, cutoff, grid=grid), args.steps, args.warmup)
+        elem = pos.element_size()
+        nbytes = N * 3 * elem + (N + 1) * 8 + E * (8 + 8 + 3 * elem)
+        t = t_count + t_fill
+        line.update({
+            "metric": "neighbour-list atoms/s", "value": N / t_build, "unit": "atoms/s", "higher_is_better": True,
+            "us_per_call": t_build * 1e6, "us_count_pass": t_count * 1e6, "us_fill_pass": t_fill * 1e6,
+            "dtype": dtype,
+            "roofline": {"bound": "hbm", "achieved": nbytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": nbytes,
+                         "time": "count + fill passes, back to back"},
+            "note": "us_per_call: the whole build through the Python binding, including its host "
+                    "synchronisation on the edge count and the output allocations"})
+        line["config"].update({"atoms": N, "edges": E, "cutoff": cutoff, "box_edge": box})
     else:
         inp = cfg.density.generate()
         N = d.atom_count
@@ -205,7 +257,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--kernel", default="auto", choices=["auto", "generated", "interpreter"])
     ap.add_argument("--op", default="pipeline",
-                    choices=["pipeline", "linear_readout", "density_accumulate_adjoint", "product_adjoint"],
+                    choices=["pipeline", "linear_readout", "density_accumulate_adjoint", "product_adjoint",
+                             "neighbor_list"],
                     help="pipeline: the headline step (stage 1 + stage 2); the others time one widened op "
                          "on the config's shapes and print its own JSON line")
     ap.add_argument("--copy-probe", action="store_true",

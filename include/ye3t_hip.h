@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 47 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 48 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -236,13 +236,49 @@ int ye3t_hip_product_plan_attach_adjoint(ye3t_hip_product_plan* plan, const void
 int ye3t_hip_product_adjoint(const ye3t_hip_product_plan* plan, const void* A, const void* gB, int64_t samples,
                              void* gA, ye3t_stream_t stream);
 
-/* out[s] = bias + sum_k B[s, k] weight[k] for a materialised B[samples, F]/* out[s] = bias + sum_k B[s, k] weight[k] for a materialised B[samples, F]
+/* out[s] = bias + sum_k B[s, k] weight[k] for a materialised B[samples, F]
  * (fp64 accumulation, fixed reduction order).  The reference's materialised
  * readout `features @ weight + bias` (execution_plan.py:13838-13845). */
 int ye3t_hip_rows_dot(int dtype, const void* B, int64_t samples, int64_t F, const void* weight, double bias,
                       void* out, ye3t_stream_t stream);
 
-/* Select which kernel product_forward launches/* Select which kernel product_forward launches: 0 = generated (if attached),
+/* Cell grid of the neighbour-list builder: dims[a] cells of edge cell_edge per
+ * axis from origin (1 <= dims[a] <= 2^24, fewer than 2^31 - 1 cells in all).
+ * Atoms outside the grid are clamped into its border cells, which is correct
+ * for any grid and fast when the grid covers the atoms. */
+typedef struct {
+  double origin[3];
+  double cell_edge; /* >= cutoff * (1 + 1e-9) */
+  int64_t dims[3];
+} ye3t_cell_grid;
+
+/* Device workspace bytes of a neighbour-list build (-1 on invalid input). */
+int64_t ye3t_hip_neighbor_workspace_bytes(int64_t atom_count, const ye3t_cell_grid* grid);
+
+/* Neighbour list, pass 1 of 2.  Bins positions[atom_count, 3] into the grid
+ * (kept in the workspace) and writes row_offsets[atom_count + 1]: row i holds
+ * the j != i with |r_j - r_i| < cutoff, decided in fp64 with each operation
+ * rounded on its own; the edge count is row_offsets[atom_count].  Open
+ * boundaries.  No neighbour builder exists in the reference: this produces the
+ * CSR that its density inputs take (centers, execution_plan.py:7913-7984;
+ * ye3t_runtime_core.h:294-301) in the order prepare_carrier_scatter_segments
+ * gives edges keyed (target, source) (execution_plan.py:9316-9434). */
+int ye3t_hip_neighbor_count(int dtype, const void* positions, int64_t atom_count, const ye3t_cell_grid* grid,
+                            double cutoff, void* workspace, int64_t workspace_bytes, int64_t* row_offsets,
+                            ye3t_stream_t stream);
+
+/* Neighbour list, pass 2 of 2, with the dtype, grid, cutoff, workspace and
+ * row_offsets of pass 1 (the workspace holds the positions in cell order):
+ * edge e in [row_offsets[i], row_offsets[i + 1]) gets centers[e] = i,
+ * neighbors[e] = j ascending within the row, edge_vectors[e] = r_j - r_i
+ * (computed in dtype).  Edges at or beyond edge_capacity are not written; a
+ * row cut by it holds its smallest neighbours. */
+int ye3t_hip_neighbor_fill(int dtype, int64_t atom_count, const ye3t_cell_grid* grid, double cutoff,
+                           const void* workspace, int64_t workspace_bytes, const int64_t* row_offsets,
+                           int64_t edge_capacity, int64_t* centers, int64_t* neighbors, void* edge_vectors,
+                           ye3t_stream_t stream);
+
+/* Select which kernel product_forward launches: 0 = generated (if attached),
  * 1 = generic interpreter. */
 int ye3t_hip_product_plan_select(ye3t_hip_product_plan* plan, int use_interpreter);
 

@@ -226,3 +226,28 @@ def ace_product_flat_adjoint(A, gB, plan_arrays):
         _p(_i64a(pa["column_offsets"]), _i64), _p(_f64(pa["term_coeffs"])),
         _p(np.ascontiguousarray(pa["term_refs"], dtype=np.int32), _i32), _p(out))
     return out
+
+
+def neighbor_list(positions, cutoff):
+    """Brute-force neighbour CSR (``oracle_neighbor_list``): dict with
+    ``target_offsets``, ``edge_targets``, ``edge_sources``, ``edge_vectors``
+    (the last in the positions' dtype)."""
+    L = lib()
+    pos = np.ascontiguousarray(positions)
+    if pos.dtype not in (np.float32, np.float64) or pos.ndim != 2 or pos.shape[1] != 3:
+        raise ValueError("positions must be float32/float64 [N, 3]")
+    n = int(pos.shape[0])
+    is_f32 = int(pos.dtype == np.float32)
+    offsets = np.zeros(n + 1, dtype=np.int64)
+    vp = ctypes.c_void_p
+    L.oracle_neighbor_list.argtypes = [vp, ctypes.c_int, _I, ctypes.c_double, vp, vp, vp, vp]
+    L.oracle_neighbor_list(pos.ctypes.data, is_f32, n, float(cutoff), offsets.ctypes.data, None, None, None)
+    e = int(offsets[-1])
+    centers = np.empty(e, dtype=np.int64)
+    nbrs = np.empty(e, dtype=np.int64)
+    vecs = np.empty((e, 3), dtype=np.float64)
+    if e:
+        L.oracle_neighbor_list(pos.ctypes.data, is_f32, n, float(cutoff), offsets.ctypes.data, centers.ctypes.data,
+                               nbrs.ctypes.data, vecs.ctypes.data)
+    return {"target_offsets": offsets, "edge_targets": centers, "edge_sources": nbrs,
+            "edge_vectors": vecs.astype(pos.dtype)}

@@ -431,3 +431,55 @@ void oracle_ace_product_flat_adjoint(const double* A, const double* gB, int64_t 
     free(gv);
   }
 }
+
+/* Brute-force neighbour list (the reference has no builder).  Row i holds the
+ * j != i, ascending, with |r_j - r_i|^2 < cutoff^2, each fp64 operation
+ * rounded on its own: ((dx*dx + dy*dy) + dz*dz) with d = r_j - r_i.  That is
+ * the CSR the density inputs take (centers, execution_plan.py:7913-7984) in the
+ * order prepare_carrier_scatter_segments gives edges keyed target*N + source
+ * (execution_plan.py:9316-9434).  positions are float (is_f32) or double; edge
+ * vectors r_j - r_i are computed in that type and returned widened to double.
+ * Pass 1 (centers == NULL) writes row_offsets[N + 1]; pass 2 fills the edges. */
+static double pos_at(const void* pos, int is_f32, int64_t k) {
+  return is_f32 ? (double)((const float*)pos)[k] : ((const double*)pos)[k];
+}
+
+void oracle_neighbor_list(const void* pos, int is_f32, int64_t n, double cutoff, int64_t* row_offsets,
+                          int64_t* centers, int64_t* neighbors, double* vectors) {
+  const double rc2 = cutoff * cutoff;
+  const int fill = centers != NULL;
+#pragma omp parallel for schedule(dynamic, 16)
+  for (int64_t i = 0; i < n; ++i) {
+    const double xi = pos_at(pos, is_f32, 3 * i), yi = pos_at(pos, is_f32, 3 * i + 1),
+                 zi = pos_at(pos, is_f32, 3 * i + 2);
+    int64_t e = fill ? row_offsets[i] : 0;
+    for (int64_t j = 0; j < n; ++j) {
+      if (j == i) continue;
+      const double xj = pos_at(pos, is_f32, 3 * j), yj = pos_at(pos, is_f32, 3 * j + 1),
+                   zj = pos_at(pos, is_f32, 3 * j + 2);
+      const double dx = xj - xi, dy = yj - yi, dz = zj - zi;  /* built with -ffp-contract=off */
+      const double d2 = (dx * dx + dy * dy) + dz * dz;
+      if (!(d2 < rc2)) continue;
+      if (fill) {
+        centers[e] = i;
+        neighbors[e] = j;
+        if (is_f32) {
+          const float* p = (const float*)pos;
+          vectors[3 * e] = (double)(float)(p[3 * j] - p[3 * i]);
+          vectors[3 * e + 1] = (double)(float)(p[3 * j + 1] - p[3 * i + 1]);
+          vectors[3 * e + 2] = (double)(float)(p[3 * j + 2] - p[3 * i + 2]);
+        } else {
+          vectors[3 * e] = xj - xi;
+          vectors[3 * e + 1] = yj - yi;
+          vectors[3 * e + 2] = zj - zi;
+        }
+      }
+      ++e;
+    }
+    if (!fill) row_offsets[i + 1] = e;
+  }
+  if (!fill) {
+    row_offsets[0] = 0;
+    for (int64_t i = 0; i < n; ++i) row_offsets[i + 1] += row_offsets[i];
+  }
+}

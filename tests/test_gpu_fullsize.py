@@ -96,3 +96,66 @@ def test_config4_full_size_rotation_covariance_fp64(gpu):
     err = column_rel_error(B1, expected)
     flush(f"  covariance err {err:.3e}")
     assert err < 1e-10  # fitted D^L carries ~1e-13 of least-squares error
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f64"])
+def test_config4_full_size_neighbor_list(gpu, dtype):
+    """50 000 uniform random atoms at config 4's cutoff (about 24 neighbours
+    each): the device list equals the brute-force oracle bit for bit, and is
+    symmetric (j in row i iff i in row j) with antisymmetric vectors."""
+    flush(f"config 4 full size neighbour list {dtype}")
+    import torch
+
+    from ye3t_amd.runtime import neighbor_list
+
+    d = W.config(4).density
+    N, cutoff = d.atom_count, float(d.radius)
+    box = (N / 0.05) ** (1.0 / 3.0)
+    pos = np.random.default_rng(5).uniform(0.0, box, size=(N, 3)).astype(np.float64 if dtype == "f64" else
+                                                                          np.float32)
+    got = neighbor_list(torch.as_tensor(pos, device=gpu), cutoff)
+    ref = oracle.neighbor_list(pos, cutoff)
+    E = len(ref["edge_sources"])
+    flush(f"  {E} edges ({E / N:.1f} per atom)")
+    assert E > 20 * N
+    for key in ("target_offsets", "edge_targets", "edge_sources", "edge_vectors"):
+        assert np.array_equal(got[key].cpu().numpy(), ref[key]), key
+    tgt, src = ref["edge_targets"], ref["edge_sources"]
+    fwd = tgt * N + src
+    rev = src * N + tgt
+    pos_of = np.searchsorted(fwd, rev)
+    assert np.array_equal(fwd[pos_of], rev)
+    assert np.array_equal(ref["edge_vectors"][pos_of], -ref["edge_vectors"])
+
+
+def test_neighbor_list_three_level_scans(gpu):
+    """4.3 M atoms on about 9 M cells: both device scans (cell starts and row
+    offsets) take three levels.  Row lengths equal those of an independent k-d
+    tree, rows are ascending, and sampled rows equal the tree's sets."""
+    flush("neighbour list, 4.3 M atoms (three-level scans)")
+    import torch
+    from scipy.spatial import cKDTree
+
+    from ye3t_amd.runtime import native, neighbor_list
+
+    N, cutoff = 4_300_000, 1.0
+    box = (N / (2.0 / (4.0 / 3.0 * np.pi))) ** (1.0 / 3.0)  # about 2 neighbours per atom
+    pos = np.random.default_rng(13).uniform(0.0, box, size=(N, 3))
+    grid = native.cell_grid(pos.min(0), pos.max(0), cutoff, N)
+    cells = grid.dims[0] * grid.dims[1] * grid.dims[2]
+    assert cells > 2048 * 2048 and N > 2048 * 2048
+    got = neighbor_list(torch.as_tensor(pos, device=gpu), cutoff)
+    offs = got["target_offsets"].cpu().numpy()
+    src = got["edge_sources"].cpu().numpy()
+    pairs = cKDTree(pos).query_pairs(cutoff, output_type="ndarray")
+    counts = np.bincount(pairs.ravel(), minlength=N)
+    flush(f"  {cells} cells, {len(src)} edges")
+    assert np.array_equal(np.diff(offs), counts) and offs[0] == 0
+    tgt = np.repeat(np.arange(N), counts)
+    assert np.array_equal(got["edge_targets"].cpu().numpy(), tgt)
+    same_row = tgt[1:] == tgt[:-1]
+    assert np.all(src[1:][same_row] > src[:-1][same_row])
+    tree = cKDTree(pos)
+    for i in np.random.default_rng(14).integers(0, N, 200):
+        want = sorted(j for j in tree.query_ball_point(pos[i], cutoff) if j != i)
+        assert src[offs[i]:offs[i + 1]].tolist() == want

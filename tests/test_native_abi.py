@@ -58,3 +58,36 @@ def test_plan_validation_rejects_bad_program():
             break
     with pytest.raises(RuntimeError, match="bad operand"):
         native.ProductPlanHandle(bad)
+
+
+def test_neighbor_list_arguments_are_checked_on_the_host():
+    L = native.lib()
+    grid = native.cell_grid([0.0, 0.0, 0.0], [10.0, 10.0, 10.0], 2.0, 100)
+    need = L.ye3t_hip_neighbor_workspace_bytes(100, ctypes.byref(grid))
+    assert need > 0
+    # a cutoff above the cell edge, a short workspace and a bad dtype fail before any launch
+    assert L.ye3t_hip_neighbor_count(1, None, 100, ctypes.byref(grid), 2.5, None, need, None, None) == -1
+    assert b"cutoff" in L.ye3t_hip_last_error()
+    assert L.ye3t_hip_neighbor_count(1, None, 100, ctypes.byref(grid), 2.0, ctypes.c_void_p(256), need - 1,
+                                     ctypes.c_void_p(256), None) == -1
+    assert b"workspace" in L.ye3t_hip_last_error()
+    assert L.ye3t_hip_neighbor_count(9, ctypes.c_void_p(256), 100, ctypes.byref(grid), 2.0, ctypes.c_void_p(256),
+                                     need, ctypes.c_void_p(256), None) == -3
+    bad = native.CellGrid()
+    bad.cell_edge = 1.0
+    bad.dims[0], bad.dims[1], bad.dims[2] = 1, 0, 1
+    assert L.ye3t_hip_neighbor_workspace_bytes(10, ctypes.byref(bad)) == -1
+
+
+def test_cell_grid_sizes():
+    g = native.cell_grid([0.0, 0.0, 0.0], [100.0, 100.0, 100.0], 5.0, 50000)
+    assert list(g.dims) == [20, 20, 20] and g.cell_edge >= 5.0 * (1 + 1e-9)
+    # sparse atoms far apart: the grid is widened to at most max(4 N, 64) cells
+    g = native.cell_grid([0.0, 0.0, 0.0], [1e6, 1.0, 1.0], 5.0, 10)
+    assert g.dims[0] * g.dims[1] * g.dims[2] <= 64 and g.dims[0] * g.cell_edge > 1e6
+    g = native.cell_grid([0.0] * 3, [0.0] * 3, 1.0, 0)
+    assert list(g.dims) == [1, 1, 1]
+    with pytest.raises(ValueError):
+        native.cell_grid([0.0, float("nan"), 0.0], [1.0, 1.0, 1.0], 1.0, 4)
+    with pytest.raises(ValueError):
+        native.cell_grid([0.0] * 3, [1.0] * 3, 0.0, 4)

@@ -277,3 +277,58 @@ def test_product_adjoint_matches_the_exact_directional_derivative():
         vf = np.asarray(arrays["value_factors"])
         used[vf[vf >= 0]] = True
         assert not np.any(gA[:, ~used])
+
+
+def _reference_segment_order(targets, sources, node_count):
+    """numpy restatement of the edge order of prepare_carrier_scatter_segments
+    (execution_plan.py:9316-9434): stable argsort of target * N + source."""
+    return np.argsort(targets * node_count + sources, kind="stable")
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_neighbor_list_against_kdtree_and_the_segment_convention(dtype):
+    from scipy.spatial import cKDTree
+
+    rng = np.random.default_rng(11)
+    pos = rng.uniform(-7.0, 13.0, size=(1500, 3)).astype(dtype)
+    cutoff = 2.7
+    nl = oracle.neighbor_list(pos, cutoff)
+    offs, tgt, src, vec = nl["target_offsets"], nl["edge_targets"], nl["edge_sources"], nl["edge_vectors"]
+    # the pair set of an independent implementation (both directions)
+    pairs = cKDTree(pos.astype(np.float64)).query_pairs(cutoff, output_type="ndarray")
+    both = np.concatenate([pairs, pairs[:, ::-1]])
+    assert len(tgt) == len(both) > 0
+    order = _reference_segment_order(both[:, 0], both[:, 1], len(pos))
+    np.testing.assert_array_equal(tgt, both[order, 0])
+    np.testing.assert_array_equal(src, both[order, 1])
+    # already in the reference's order: its stable argsort is the identity
+    np.testing.assert_array_equal(_reference_segment_order(tgt, src, len(pos)), np.arange(len(tgt)))
+    np.testing.assert_array_equal(offs, np.concatenate([[0], np.cumsum(np.bincount(tgt, minlength=len(pos)))]))
+    # r_j - r_i, one rounding in the positions' type
+    np.testing.assert_array_equal(vec, pos[src] - pos[tgt])
+    assert vec.dtype == dtype
+
+
+def test_neighbor_list_lattice_closed_forms_and_strict_cutoff():
+    n = 6
+    g = np.arange(n, dtype=np.float64)
+    pos = np.stack(np.meshgrid(g, g, g, indexing="ij"), -1).reshape(-1, 3)
+    # spacing 1 exactly: r < 1 excludes every lattice bond, r < 1.5 keeps the
+    # 3 n^2 (n-1) axis bonds, r < 1.45 vs 1.42 brackets the face diagonals sqrt(2)
+    assert oracle.neighbor_list(pos, 1.0)["target_offsets"][-1] == 0
+    axis = 2 * 3 * n * n * (n - 1)
+    assert oracle.neighbor_list(pos, 1.0 + 1e-12)["target_offsets"][-1] == axis
+    assert oracle.neighbor_list(pos, 1.41)["target_offsets"][-1] == axis
+    face = 2 * 3 * 2 * n * (n - 1) ** 2
+    nl = oracle.neighbor_list(pos, 1.42)
+    assert nl["target_offsets"][-1] == axis + face
+    # an interior site has 6 + 12 neighbours
+    centre = (2 * n + 2) * n + 2
+    assert np.diff(nl["target_offsets"])[centre] == 18
+    # coincident atoms are neighbours of each other (distance 0 < cutoff)
+    same = np.zeros((5, 3))
+    nl = oracle.neighbor_list(same, 0.5)
+    assert nl["target_offsets"].tolist() == [0, 4, 8, 12, 16, 20]
+    assert nl["edge_sources"][:4].tolist() == [1, 2, 3, 4]
+    empty = oracle.neighbor_list(np.zeros((0, 3)), 1.0)
+    assert empty["target_offsets"].tolist() == [0] and len(empty["edge_sources"]) == 0

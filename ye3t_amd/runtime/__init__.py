@@ -23,6 +23,7 @@ HIP_OPERATIONS = (
     "ace_product_forward",
     "factorized_angular_linear",
     "factorized_angular_adjoint",
+    "neighbor_list",
 )
 
 
@@ -116,6 +117,26 @@ def density_accumulate_adjoint(atomic_adjoint, centers, *, backend="auto"):
         if lo < 0 or hi >= int(atomic_adjoint.shape[0]):
             raise RuntimeError("density_accumulate_adjoint center index out of range")
     return native.density_accumulate_adjoint(atomic_adjoint.contiguous(), centers.contiguous())
+
+
+def neighbor_list(positions, cutoff, *, backend="auto"):
+    """Neighbour CSR built on the device (open boundaries).
+
+    Row i holds the j != i with ``|r_j - r_i| < cutoff`` (fp64 test, each
+    operation rounded on its own), j ascending: the (target, source) order
+    that ``prepare_carrier_scatter_segments`` (reference
+    ``execution_plan.py:9316-9434``) gives, so its ``edge_order`` of this
+    output is the identity.  Returns ``target_offsets [N+1]``,
+    ``edge_targets`` (centres), ``edge_sources`` (neighbours) and
+    ``edge_vectors = r_j - r_i`` in the positions' dtype -- the CSR, centres
+    and vectors the density ops take.  The reference has no builder.
+    """
+    import torch
+
+    _backend(backend, {"auto", "native"})
+    positions = torch.as_tensor(positions)
+    _require_device(positions, "neighbor_list")
+    return native.neighbor_list(positions.contiguous(), float(cutoff))
 
 
 def symmetric_power_monomial_contraction(input, monomial_counts, output_offsets, monomial_values, *,

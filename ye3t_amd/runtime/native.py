@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 47
+ABI_VERSION = 48
 _LIB = None
 
 F32, F64 = 0, 1
@@ -35,6 +35,10 @@ class ProductPlanDesc(ctypes.Structure):
                 ("chunk_out_offsets", _vp), ("chunk_first_column", _vp), ("words", _vp), ("word_count", _i64),
                 ("coeffs", _vp), ("coeff_count", _i64), ("out_slots", _vp), ("out_slot_count", _i64),
                 ("out_dtype", ctypes.c_int)]
+
+
+class CellGrid(ctypes.Structure):
+    _fields_ = [("origin", ctypes.c_double * 3), ("cell_edge", ctypes.c_double), ("dims", _i64 * 3)]
 
 
 class Caps(ctypes.Structure):
@@ -89,6 +93,12 @@ def lib():
     L.ye3t_hip_rows_dot.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, ctypes.c_double, _vp, _vp]
     L.ye3t_hip_product_plan_attach_adjoint.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, ctypes.c_int]
     L.ye3t_hip_product_adjoint.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
+    L.ye3t_hip_neighbor_workspace_bytes.argtypes = [_i64, ctypes.POINTER(CellGrid)]
+    L.ye3t_hip_neighbor_workspace_bytes.restype = _i64
+    L.ye3t_hip_neighbor_count.argtypes = [ctypes.c_int, _vp, _i64, ctypes.POINTER(CellGrid), ctypes.c_double, _vp,
+                                          _i64, _vp, _vp]
+    L.ye3t_hip_neighbor_fill.argtypes = [ctypes.c_int, _i64, ctypes.POINTER(CellGrid), ctypes.c_double, _vp, _i64,
+                                         _vp, _i64, _vp, _vp, _vp, _vp]
     version = L.ye3t_hip_abi_version()
     if version != ABI_VERSION:
         raise RuntimeError(f"ye3t_hip ABI {version} does not match the bindings ({ABI_VERSION})")
@@ -105,6 +115,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_product_plan_attach_generated", "ye3t_hip_product_plan_select", "ye3t_hip_last_density_kernel",
     "ye3t_hip_density_accumulate_adjoint", "ye3t_hip_product_plan_attach_readout", "ye3t_hip_product_linear_forward",
     "ye3t_hip_rows_dot", "ye3t_hip_product_plan_attach_adjoint", "ye3t_hip_product_adjoint",
+    "ye3t_hip_neighbor_workspace_bytes", "ye3t_hip_neighbor_count", "ye3t_hip_neighbor_fill",
 )
 
 
@@ -505,3 +516,75 @@ def rows_dot(B, weight, bias, out=None):
     _check(lib().ye3t_hip_rows_dot(_dtype_code(B), _dev(B, "B"), S, F, _dev(weight, "weight"), float(bias),
                                    _dev(out, "out"), _stream()), "ye3t_hip_rows_dot")
     return out
+
+
+MAX_GRID_DIM = 1 << 24
+
+
+def cell_grid(lower, upper, cutoff, atom_count):
+    """Cell grid covering the box ``[lower, upper]`` with cells a little wider
+    than ``cutoff`` (the builder requires ``cell_edge >= cutoff (1 + 1e-9)``),
+    widened further so that there are at most ``max(4 N, 64)`` cells."""
+    import math
+
+    cutoff = float(cutoff)
+    if not (cutoff > 0.0 and math.isfinite(cutoff)):
+        raise ValueError("cutoff must be positive and finite")
+    lower = [float(x) for x in lower]
+    upper = [float(x) for x in upper]
+    if not all(math.isfinite(x) for x in lower + upper):
+        raise ValueError("positions must be finite")
+    span = [max(hi - lo, 0.0) for lo, hi in zip(lower, upper)]
+    edge = cutoff * (1.0 + 1e-6)
+    limit = max(4 * int(atom_count), 64)
+    while True:
+        dims = [min(MAX_GRID_DIM, int(s / edge) + 1) for s in span]
+        if dims[0] * dims[1] * dims[2] <= limit:
+            break
+        edge *= max(1.05, (dims[0] * dims[1] * dims[2] / limit) ** (1.0 / 3.0))
+    grid = CellGrid()
+    for a in range(3):
+        grid.origin[a] = lower[a]
+        grid.dims[a] = dims[a]
+    grid.cell_edge = edge
+    return grid
+
+
+def neighbor_list(positions, cutoff, grid=None):
+    """Neighbour CSR of ``positions [N, 3]`` (open boundaries): row i holds the
+    j != i with ``|r_j - r_i| < cutoff`` in ascending j.  Two passes with one
+    host synchronisation between them (the edge count sizes the outputs)."""
+    import torch
+
+    if positions.ndim != 2 or positions.shape[1] != 3:
+        raise ValueError("positions must be [N, 3]")
+    N = int(positions.shape[0])
+    dev = positions.device
+    if grid is None:
+        if N:
+            lo, hi = torch.aminmax(positions, dim=0)
+            lo, hi = lo.double().cpu().tolist(), hi.double().cpu().tolist()
+        else:
+            lo = hi = [0.0, 0.0, 0.0]
+        grid = cell_grid(lo, hi, cutoff, N)
+    L = lib()
+    ws_bytes = int(L.ye3t_hip_neighbor_workspace_bytes(N, ctypes.byref(grid)))
+    if ws_bytes < 0:
+        _check(-1, "ye3t_hip_neighbor_workspace_bytes")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    offsets = torch.empty(N + 1, dtype=torch.int64, device=dev)
+    code = _dtype_code(positions)
+    pos = _dev(positions, "positions")
+    _check(L.ye3t_hip_neighbor_count(code, pos, N, ctypes.byref(grid), float(cutoff), _dev(ws, "workspace"),
+                                     ws_bytes, _dev(offsets, "row_offsets"), _stream()), "ye3t_hip_neighbor_count")
+    E = int(offsets[N])
+    centers = torch.empty(E, dtype=torch.int64, device=dev)
+    nbrs = torch.empty(E, dtype=torch.int64, device=dev)
+    vecs = torch.empty((E, 3), dtype=positions.dtype, device=dev)
+    if E:
+        _check(L.ye3t_hip_neighbor_fill(code, N, ctypes.byref(grid), float(cutoff), _dev(ws, "workspace"),
+                                        ws_bytes, _dev(offsets, "row_offsets"), E, _dev(centers, "centers"),
+                                        _dev(nbrs, "neighbors"), _dev(vecs, "edge_vectors"), _stream()),
+               "ye3t_hip_neighbor_fill")
+    return {"schema": "ye3t_amd_neighbor_csr_v1", "target_offsets": offsets, "edge_targets": centers,
+            "edge_sources": nbrs, "edge_vectors": vecs, "node_count": N, "cutoff": float(cutoff)}
