@@ -136,10 +136,16 @@ __global__ void clear_cells_kernel(int32_t* __restrict__ cell_start, int64_t cel
   if (blockIdx.x == 0 && threadIdx.x == 0 && row0 != nullptr) row0[0] = 0;
 }
 
-template <typename T>
-__device__ inline int cell_coord(T x, double o, double inv, int n) {
-  const double u = floor(__dmul_rn(__dsub_rn(double(x), o), inv));
+__device__ inline int cell_coord(double x, double o, double inv, int n) {
+  const double u = floor(__dmul_rn(__dsub_rn(x, o), inv));
   return !(u >= 0.0) ? 0 : (u >= double(n) ? n - 1 : int(u));  // NaN -> cell 0
+}
+
+__device__ inline int32_t cell_of_point(double x, double y, double z, const CellGrid& g) {
+  const int cx = cell_coord(x, g.origin[0], g.inv_cell, g.dims[0]);
+  const int cy = cell_coord(y, g.origin[1], g.inv_cell, g.dims[1]);
+  const int cz = cell_coord(z, g.origin[2], g.inv_cell, g.dims[2]);
+  return (cx * g.dims[1] + cy) * g.dims[2] + cz;
 }
 
 template <typename T>
@@ -149,10 +155,7 @@ __global__ __launch_bounds__(256) void bin_atoms_kernel(const T* __restrict__ po
   const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= N) return;
   const int32_t i = int32_t(t);
-  const int cx = cell_coord(pos[3 * int64_t(i)], g.origin[0], g.inv_cell, g.dims[0]);
-  const int cy = cell_coord(pos[3 * int64_t(i) + 1], g.origin[1], g.inv_cell, g.dims[1]);
-  const int cz = cell_coord(pos[3 * int64_t(i) + 2], g.origin[2], g.inv_cell, g.dims[2]);
-  const int32_t c = (cx * g.dims[1] + cy) * g.dims[2] + cz;
+  const int32_t c = cell_of_point(double(pos[3 * t]), double(pos[3 * t + 1]), double(pos[3 * t + 2]), g);
   cell_of[i] = c;
   slot[i] = atomicAdd(cell_start + c + 1, 1);
 }
@@ -220,39 +223,6 @@ __device__ inline int32_t candidate(int32_t v, const int32_t* k0, const int32_t*
   return k;
 }
 
-__device__ inline int64_t wave_atom() {
-  return int64_t(blockIdx.x) * (kRowThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-}
-
-// row_offsets[i + 1] = number of neighbours of i (one wave per atom)
-__global__ __launch_bounds__(kRowThreads) void neighbor_count_kernel(const Pos4* __restrict__ spos, int32_t N,
-                                                                     CellGrid g, const int32_t* __restrict__ cell_start,
-                                                                     const int32_t* __restrict__ cell_of,
-                                                                     const int32_t* __restrict__ order, double rc2,
-                                                                     int64_t* __restrict__ row_offsets) {
-  const int64_t t = wave_atom();
-  if (t >= N) return;
-  const int lane = threadIdx.x & 63;
-  const int32_t i = order[t];
-  const Pos4 pi = spos[t];
-  int32_t k0[9], pre[10];
-  cell_columns(cell_of[i], g, cell_start, k0, pre);
-  int64_t n = 0;
-  for (int32_t v0 = 0; v0 < pre[9]; v0 += 64) {
-    const int32_t v = v0 + lane;
-    bool hit = false;
-    if (v < pre[9]) {
-      const int32_t k = candidate(v, k0, pre);
-      if (k != t) {
-        const Pos4 pj = spos[k];
-        hit = within(pi.x, pi.y, pi.z, pj.x, pj.y, pj.z, rc2);
-      }
-    }
-    n += __popcll(__ballot(hit));
-  }
-  if (lane == 0) row_offsets[i + 1] = n;
-}
-
 template <typename T>
 __device__ inline void write_edge(int64_t e, int32_t i, int32_t j, const Pos4& pj, const Pos4& pi,
                                   int64_t* __restrict__ centers, int64_t* __restrict__ nbr, T* __restrict__ vec) {
@@ -264,91 +234,170 @@ __device__ inline void write_edge(int64_t e, int32_t i, int32_t j, const Pos4& p
   vec[3 * e + 2] = T(pj.z) - T(pi.z);
 }
 
-// Row i at row_offsets[i], ascending (one wave per atom).  Entries at or
-// beyond edge_capacity are not written; a row cut by the capacity holds its
-// smallest neighbours.
-template <typename T>
-__global__ __launch_bounds__(kRowThreads) void neighbor_fill_kernel(
+// Rows of kGroup consecutive cell-ordered atoms per wave: neighbouring atoms
+// mostly share a cell, so the wave reuses the cell's column ranges and keeps
+// the first kCached * 64 candidate positions in registers across them.
+constexpr int kGroup = 4;
+constexpr int kCached = 4;
+
+// FILL = false: row_offsets[i + 1] = number of neighbours of i.
+// FILL = true: row i at row_offsets[i], ascending; entries at or beyond
+// edge_capacity are not written and a row cut by it holds its smallest
+// neighbours.  Rows up to kRowCap entries are collected in LDS and each hit is
+// written at its rank; longer rows are built by one lane in global memory.
+template <bool FILL, typename T>
+__global__ __launch_bounds__(kRowThreads) void neighbor_rows_kernel(
     const Pos4* __restrict__ spos, int32_t N, CellGrid g, const int32_t* __restrict__ cell_start,
-    const int32_t* __restrict__ cell_of, const int32_t* __restrict__ order, double rc2,
-    const int64_t* __restrict__ row_offsets, int64_t edge_capacity, int64_t* __restrict__ centers,
-    int64_t* __restrict__ nbr, T* __restrict__ vec) {
-  __shared__ int32_t row_j[kRowThreads / 64][kRowCap];
-  __shared__ int32_t row_k[kRowThreads / 64][kRowCap];
-  const int64_t t = wave_atom();
-  if (t >= N) return;
+    const int32_t* __restrict__ order, double rc2, int64_t* __restrict__ row_offsets, int64_t edge_capacity,
+    int64_t* __restrict__ centers, int64_t* __restrict__ nbr, T* __restrict__ vec) {
+  // per wave: the hits of a row as (j, k) in arrival order, then k at its rank
+  __shared__ int32_t row_j[FILL ? kRowThreads / 64 : 1][FILL ? kRowCap : 1];
+  __shared__ int32_t row_k[FILL ? kRowThreads / 64 : 1][FILL ? kRowCap : 1];
+  __shared__ int32_t out_k[FILL ? kRowThreads / 64 : 1][FILL ? kRowCap : 1];
+  const int64_t t0 = (int64_t(blockIdx.x) * (kRowThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) *
+                     kGroup;
+  if (t0 >= N) return;
+  const int64_t t1 = t0 + kGroup < N ? t0 + kGroup : N;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int32_t i = order[t];
-  const Pos4 pi = spos[t];
-  const int64_t base = row_offsets[i];
-  const int64_t stop = row_offsets[i + 1];
-  const int64_t end = stop < edge_capacity ? stop : edge_capacity;
-  const int64_t len = (base >= 0 && end > base) ? end - base : 0;
-  if (len == 0) return;
+  const int wave = FILL ? (threadIdx.x >> 6) : 0;
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  int32_t cell = -1;
   int32_t k0[9], pre[10];
-  cell_columns(cell_of[i], g, cell_start, k0, pre);
-  if (stop - base <= kRowCap) {
+  double cx[kCached], cy[kCached], cz[kCached];
+  int32_t ck[kCached], cj[kCached];
+  // the group's atoms and row bounds, loaded ahead of the per-atom work
+  int32_t gi[kGroup];
+  int64_t gb[kGroup], gs[kGroup];
+#pragma unroll
+  for (int a = 0; a < kGroup; ++a) {
+    gi[a] = order[t0 + a < t1 ? t0 + a : t0];
+    if (FILL) {
+      gb[a] = row_offsets[gi[a]];
+      gs[a] = row_offsets[gi[a] + 1];
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < kGroup; ++a) {
+    const int64_t t = t0 + a;
+    if (t >= t1) break;
+    const Pos4 pi = spos[t];
+    const int32_t c = cell_of_point(pi.x, pi.y, pi.z, g);
+    if (c != cell) {  // uniform: a new cell's columns and cached candidates
+      cell = c;
+      cell_columns(c, g, cell_start, k0, pre);
+#pragma unroll
+      for (int r = 0; r < kCached; ++r) {
+        const int32_t v = r * 64 + lane;
+        ck[r] = v < pre[9] ? candidate(v, k0, pre) : -1;
+        const Pos4 pj = spos[ck[r] < 0 ? 0 : ck[r]];
+        cx[r] = pj.x;
+        cy[r] = pj.y;
+        cz[r] = pj.z;
+        if (FILL) cj[r] = order[ck[r] < 0 ? 0 : ck[r]];
+      }
+    }
+    const int32_t i = gi[a];
+    const int32_t total = pre[9];
+    int64_t base = 0, len = 0;
+    if (FILL) {
+      base = gb[a];
+      const int64_t stop = gs[a];
+      const int64_t end = stop < edge_capacity ? stop : edge_capacity;
+      len = (base >= 0 && end > base) ? end - base : 0;
+      if (len == 0) continue;
+      if (stop - base > kRowCap) {
+        // a long row: lane 0 inserts each hit, keyed (j << 32) | k, into the
+        // sorted prefix nbr[base, base + min(n, len)); the key orders by j
+        if (lane == 0) {
+          int64_t n = 0;
+          int64_t* r = nbr + base;
+          for (int32_t v = 0; v < total; ++v) {
+            const int32_t k = candidate(v, k0, pre);
+            if (k == t) continue;
+            const Pos4 pj = spos[k];
+            if (!within(pi.x, pi.y, pi.z, pj.x, pj.y, pj.z, rc2)) continue;
+            const int64_t key = (int64_t(order[k]) << 32) | int64_t(k);
+            int64_t b = (n < len ? n : len) - 1;
+            if (n < len || key < r[len - 1]) {
+              if (n >= len) --b;  // full: the largest entry drops out
+              while (b >= 0 && r[b] > key) {
+                r[b + 1] = r[b];
+                --b;
+              }
+              r[b + 1] = key;
+            }
+            ++n;
+          }
+          const int64_t written = n < len ? n : len;
+          for (int64_t a = 0; a < written; ++a) {
+            const int64_t key = r[a];
+            write_edge(base + a, i, int32_t(key >> 32), spos[int32_t(key & 0xffffffff)], pi, centers, nbr, vec);
+          }
+        }
+        continue;
+      }
+    }
     int32_t n = 0;
-    const uint64_t below = (uint64_t(1) << lane) - 1;
-    for (int32_t v0 = 0; v0 < pre[9]; v0 += 64) {
+    auto take = [&](bool hit, int32_t j, int32_t k) {
+      const uint64_t mask = __ballot(hit);
+      if (FILL) {
+        const int32_t slot = n + __popcll(mask & below);
+        if (hit && slot < kRowCap) {
+          row_j[wave][slot] = j;
+          row_k[wave][slot] = k;
+        }
+      }
+      n += __popcll(mask);
+    };
+#pragma unroll
+    for (int r = 0; r < kCached; ++r) {
+      const bool hit = r * 64 < total && ck[r] >= 0 && ck[r] != t &&
+                       within(pi.x, pi.y, pi.z, cx[r], cy[r], cz[r], rc2);
+      take(hit, FILL ? cj[r] : 0, ck[r]);
+    }
+    for (int32_t v0 = kCached * 64; v0 < total; v0 += 64) {
       const int32_t v = v0 + lane;
       bool hit = false;
       int32_t k = 0;
-      if (v < pre[9]) {
+      if (v < total) {
         k = candidate(v, k0, pre);
         if (k != t) {
           const Pos4 pj = spos[k];
           hit = within(pi.x, pi.y, pi.z, pj.x, pj.y, pj.z, rc2);
         }
       }
-      const uint64_t mask = __ballot(hit);
-      const int32_t slot = n + __popcll(mask & below);
-      if (hit && slot < kRowCap) {
-        row_j[wave][slot] = order[k];
-        row_k[wave][slot] = k;
-      }
-      n += __popcll(mask);
+      take(hit, FILL && hit ? order[k] : 0, k);
+    }
+    if (!FILL) {
+      if (lane == 0) row_offsets[i + 1] = n;
+      continue;
     }
     // the row's LDS entries were written by other lanes of this wave
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // rank of each hit = number of smaller j (j is unique): a permutation of [0, held)
     const int32_t held = n < kRowCap ? n : kRowCap;
     for (int32_t e = lane; e < held; e += 64) {
       const int32_t j = row_j[wave][e];
       int32_t rank = 0;
       for (int32_t q = 0; q < held; ++q) rank += row_j[wave][q] < j;
-      if (rank < len) write_edge(base + rank, i, j, spos[row_k[wave][e]], pi, centers, nbr, vec);
+      out_k[wave][rank] = row_k[wave][e];
     }
-    return;
-  }
-  // a long row: lane 0 inserts each hit, keyed (j << 32) | k, into the sorted
-  // prefix nbr[base, base + min(n, len)); the key orders by j (j is unique)
-  if (lane != 0) return;
-  int64_t n = 0;
-  int64_t* r = nbr + base;
-  for (int32_t v = 0; v < pre[9]; ++v) {
-    const int32_t k = candidate(v, k0, pre);
-    if (k == t) continue;
-    const Pos4 pj = spos[k];
-    if (!within(pi.x, pi.y, pi.z, pj.x, pj.y, pj.z, rc2)) continue;
-    const int64_t key = (int64_t(order[k]) << 32) | int64_t(k);
-    int64_t b = (n < len ? n : len) - 1;
-    if (n < len || key < r[len - 1]) {
-      if (n >= len) --b;  // full: the largest entry drops out
-      while (b >= 0 && r[b] > key) {
-        r[b + 1] = r[b];
-        --b;
-      }
-      r[b + 1] = key;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the row in order: consecutive lanes write consecutive edges
+    const int32_t count = held < len ? held : int32_t(len);
+    for (int32_t e = lane; e < count; e += 64) {
+      const uint32_t kk = uint32_t(out_k[wave][e]);
+      const int32_t k = kk < uint32_t(N) ? int32_t(kk) : 0;  // always a permutation; clamped regardless
+      write_edge(base + e, i, order[k], spos[k], pi, centers, nbr, vec);
     }
-    ++n;
-  }
-  const int64_t written = n < len ? n : len;
-  for (int64_t a = 0; a < written; ++a) {
-    const int64_t key = r[a];
-    write_edge(base + a, i, int32_t(key >> 32), spos[int32_t(key & 0xffffffff)], pi, centers, nbr, vec);
+    // every lane has read the row before the next atom overwrites it
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 
@@ -413,6 +462,13 @@ CellGrid device_grid(const ye3t_cell_grid* grid) {
   return g;
 }
 
+// blocks of the row kernels: kRowThreads / 64 waves of kGroup atoms each
+unsigned row_blocks(int64_t n) {
+  const int64_t per = int64_t(kRowThreads / 64) * kGroup;
+  const int64_t b = (n + per - 1) / per;
+  return unsigned(b < 1 ? 1 : b);
+}
+
 unsigned blocks_for(int64_t n, int threads) {
   const int64_t b = (n + threads - 1) / threads;
   return unsigned(b < 1 ? 1 : b);
@@ -435,10 +491,10 @@ int count_rows(const T* pos, int32_t N, const ye3t_cell_grid* grid, double cutof
   hipLaunchKernelGGL(place_atoms_kernel<T>, dim3(blocks_for(N, 256)), dim3(256), 0, s, pos, N,
                      (const int32_t*)w.cell_start, (const int32_t*)w.cell_of, (const int32_t*)w.slot, w.order, w.spos);
   if ((rc = check_launch("place_atoms_kernel")) != YE3T_OK) return rc;
-  hipLaunchKernelGGL(neighbor_count_kernel, dim3(blocks_for(N, kRowThreads / 64)), dim3(kRowThreads), 0, s,
-                     (const Pos4*)w.spos, N, g, (const int32_t*)w.cell_start, (const int32_t*)w.cell_of,
-                     (const int32_t*)w.order, cutoff * cutoff, row_offsets);
-  if ((rc = check_launch("neighbor_count_kernel")) != YE3T_OK) return rc;
+  hipLaunchKernelGGL((neighbor_rows_kernel<false, T>), dim3(row_blocks(N)), dim3(kRowThreads), 0, s,
+                     (const Pos4*)w.spos, N, g, (const int32_t*)w.cell_start, (const int32_t*)w.order,
+                     cutoff * cutoff, row_offsets, int64_t(0), (int64_t*)nullptr, (int64_t*)nullptr, (T*)nullptr);
+  if ((rc = check_launch("neighbor_rows_kernel")) != YE3T_OK) return rc;
   return scan_inclusive<int64_t>(row_offsets + 1, N, w.partials, s);
 }
 
@@ -447,11 +503,11 @@ int fill_rows(int32_t N, const ye3t_cell_grid* grid, double cutoff, const Worksp
               const int64_t* row_offsets, int64_t edge_capacity, int64_t* centers, int64_t* neighbors, T* vec,
               hipStream_t s) {
   if (N == 0) return YE3T_OK;
-  hipLaunchKernelGGL(neighbor_fill_kernel<T>, dim3(blocks_for(N, kRowThreads / 64)), dim3(kRowThreads), 0, s,
+  hipLaunchKernelGGL((neighbor_rows_kernel<true, T>), dim3(row_blocks(N)), dim3(kRowThreads), 0, s,
                      (const Pos4*)w.spos, N, device_grid(grid), (const int32_t*)w.cell_start,
-                     (const int32_t*)w.cell_of, (const int32_t*)w.order, cutoff * cutoff, row_offsets, edge_capacity,
+                     (const int32_t*)w.order, cutoff * cutoff, const_cast<int64_t*>(row_offsets), edge_capacity,
                      centers, neighbors, vec);
-  return check_launch("neighbor_fill_kernel");
+  return check_launch("neighbor_rows_kernel");
 }
 
 }  // namespace
