@@ -328,7 +328,13 @@ def main():
     s2 = float(np.mean([b.elapsed_time(c) for _, b, c in ev])) * 1e-3
     ms_per_step = wall / args.steps * 1e3
     b1, b2 = algorithmic_bytes(cfg, pipe.plan, elem, a_elem)
-    k2 = "ye3t_product_generated" if pipe.kernel == "generated" else "product_kernel"
+    if pipe.kernel == "generated":
+        k2 = "ye3t_product_generated"
+    elif pipe.handle.uses_stream:
+        # the stage-2 time includes the column-major copy of the density it reads
+        k2 = "transpose_kernel+product_stream_kernel" if pipe._columns else "product_stream_kernel"
+    else:
+        k2 = "product_kernel"
     features = rows.shape[0] * pipe.feature_count
     value = features / (wall / args.steps)
     stats = program_stats(pipe.program)

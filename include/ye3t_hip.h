@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 48 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 49 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -278,9 +278,32 @@ int ye3t_hip_neighbor_fill(int dtype, int64_t atom_count, const ye3t_cell_grid* 
                            int64_t edge_capacity, int64_t* centers, int64_t* neighbors, void* edge_vectors,
                            ye3t_stream_t stream);
 
+/* At[c * ld + r] = A[r * cols + c] for r < rows, c < cols, and At[c * ld + r]
+ * = 0 for rows <= r < ld: the column-major density of
+ * ye3t_hip_product_forward_columns.  No reference counterpart (a layout step
+ * of this backend). */
+int ye3t_hip_transpose(int dtype, const void* A, int64_t rows, int64_t cols, void* At, int64_t ld,
+                       ye3t_stream_t stream);
+
+/* ye3t_hip_product_forward on a column-major density At [a_width, ld]
+ * (element (s, col) at At[col * ld + s]; ld >= samples rounded up to 64):
+ * the interpreter reads each density column of 64 samples as one contiguous
+ * block.  For plans run by the term-stream interpreter (workspace byte offsets
+ * within 16 bits); YE3T_EINVAL otherwise.  Same results as
+ * ye3t_hip_product_forward on the row-major density.  Replaces the same
+ * reference ops as ye3t_hip_product_forward. */
+int ye3t_hip_product_forward_columns(const ye3t_hip_product_plan* plan, const void* At, int64_t ld,
+                                     int64_t samples, void* B, ye3t_stream_t stream);
+
 /* Select which kernel product_forward launches: 0 = generated (if attached),
  * 1 = generic interpreter. */
 int ye3t_hip_product_plan_select(ye3t_hip_product_plan* plan, int use_interpreter);
+
+/* 1 if the plan's interpreter is the term stream (LDS-staged records; the
+ * plan also accepts ye3t_hip_product_forward_columns), 0 for the program-word
+ * interpreter (workspaces too wide for the stream's 16-bit offsets or 64 KB of
+ * LDS).  No reference counterpart. */
+int ye3t_hip_product_plan_uses_stream(const ye3t_hip_product_plan* plan);
 
 /* Kernel name/launch geometry of the last product_forward (for profiling). */
 int ye3t_hip_product_launch_info(const ye3t_hip_product_plan* plan, int64_t samples, int64_t* grid,

@@ -234,6 +234,42 @@ def test_product_kernel_vs_flat_oracle(gpu, cid, dtype, samples, max_slots, kern
     assert np.array_equal(B, pipe.product(A_dev).cpu().numpy())
 
 
+@pytest.mark.parametrize("cid,dtype,samples,max_slots", [
+    (2, "f64", 200, None), (3, "f32", 100, None), (3, "f64", 70, None), (4, "f32", 130, 48), (4, "f64", 1, None),
+    (4, "f64", 129, 120)])
+def test_interpreter_column_major_density(gpu, cid, dtype, samples, max_slots):
+    """The term-stream interpreter on a column-major density (``transpose`` +
+    ``forward_columns``) equals its row-major run bit for bit and the oracle
+    within tolerance; a workspace too wide for 16-bit offsets keeps the word
+    interpreter and refuses the column-major entry point."""
+    flush(f"product columns config {cid} {dtype} samples={samples} slots={max_slots}")
+    import torch
+
+    spec = _species_rank4_spec() if cid == 3 else W.config(cid).feature_spec
+    pipe = ACEPipeline(spec, dtype, max_slots, kernel="interpreter")
+    A = np.random.default_rng(15).normal(size=(samples, pipe.plan.a_width))
+    A_dev = _t(A, dtype, gpu)
+    At = native.transpose(A_dev)
+    assert At.shape[1] % 64 == 0 and At.shape[1] >= samples
+    assert torch.equal(At[:, :samples], A_dev.t()) and bool((At[:, samples:] == 0).all())
+    B_rows = pipe.product(A_dev)
+    elem = 8 if dtype == "f64" else 4
+    # the stream needs the workspace plus the staged program within 64 KB of LDS:
+    # the default workspaces (48 fp64 / 96 fp32 slots) always take it
+    if (pipe.program["workspace_slots"] + 2) * 64 * elem <= 32 * 1024:
+        assert pipe.handle.uses_stream
+    if not pipe.handle.uses_stream:
+        with pytest.raises(RuntimeError, match="term stream"):
+            pipe.handle.forward_columns(At, samples)
+    else:
+        B_cols = pipe.handle.forward_columns(At, samples)
+        assert torch.equal(B_cols, B_rows)
+    ref = oracle.ace_product_flat(A_dev.double().cpu().numpy(), pipe.plan.flat_arrays())
+    err = column_rel_error(B_rows.cpu().numpy(), ref)
+    flush(f"  err {err:.3e}")
+    assert err < TOL[dtype]
+
+
 def test_generated_and_interpreter_agree_on_config4(gpu):
     flush("generated vs interpreter, config 4 full sample count")
     import torch

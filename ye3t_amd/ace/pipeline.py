@@ -59,6 +59,8 @@ class ACEPipeline:
         self.plan = plan if plan is not None else ProductPlan(feature_spec)
         self.program = compile_program(self.plan, self.accumulate, max_slots)
         self.handle = native.ProductPlanHandle(self.program, out_dtype=dtype)
+        self._columns = os.environ.get("YE3T_PRODUCT_COLUMNS", "1") != "0"
+        self._At = None  # (key, column-major density buffer) of the interpreter path
         terms = sum(len(nd.get("terms", ())) for nd in self.plan.nodes)
         use_gen = kernel == "generated" or (kernel == "auto" and terms <= GENERATED_MAX_TERMS)
         if kernel not in {"auto", "generated", "interpreter"}:
@@ -105,6 +107,20 @@ class ACEPipeline:
             out_dtype=torch.float64 if self.accumulate == "f64" else torch.float32)
 
     def product(self, A_rows, out=None):
+        """B-features of the density rows.  Interpreter plans read a column-major
+        copy of the density (each density column of 64 samples is one contiguous
+        block for the interpreter's loads); ``YE3T_PRODUCT_COLUMNS=0`` reads the
+        rows directly."""
+        if self.kernel == "interpreter" and self.handle.uses_stream and self._columns:
+            S = int(A_rows.shape[0])
+            ld = (S + 63) // 64 * 64
+            key = (int(A_rows.shape[1]), ld, A_rows.dtype, A_rows.device)
+            if self._At is None or self._At[0] != key:
+                import torch
+
+                self._At = (key, torch.empty((key[0], ld), dtype=A_rows.dtype, device=A_rows.device))
+            At = native.transpose(A_rows.contiguous(), out=self._At[1], ld=ld)
+            return self.handle.forward_columns(At, S, out=out)
         return self.handle.forward(A_rows, out=out)
 
     def product_adjoint(self, A_rows, gB, out=None):

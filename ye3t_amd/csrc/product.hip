@@ -1,6 +1,8 @@
 // Stage 2 -- ACE B-features from the density on gfx950.
 //
-// (a) product_kernel: executes a compiled product plan.  The plan is a DAG of
+// (a) product_stream_kernel (the default interpreter) and product_kernel (the
+//     program-word interpreter it replaces where its workspace fits): execute
+//     a compiled product plan.  The plan is a DAG of
 //     leaf loads, symmetric-block monomials and real CG pair couplings, shared
 //     across labels and contents (intermediate couplings computed once per
 //     sample).  One wave (64 lanes) processes 64 samples, lane = sample; the
@@ -13,6 +15,7 @@
 //     reference's flat schedule evaluator and symmetric-power contraction.
 #include <hip/hiprtc.h>
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
@@ -52,6 +55,17 @@ struct ye3t_hip_product_plan {
   hipFunction_t adjoint;
   int adjoint_threads;
   int64_t adjoint_max_grid;
+  // term stream of the interpreter (built from `words` at creation; absent when
+  // the workspace's byte offsets do not fit 16 bits)
+  uint4* recs;         // 16-byte records, each chunk padded to a multiple of 4
+  uint32_t* flags;     // flag word of each record
+  int64_t* rec_off;    // [chunks+1], in records
+  uint2* loads;        // (LDS byte offset, density column), each chunk padded to a multiple of 8
+  int64_t* load_off;   // [chunks+1], in loads
+  int use_stream;
+  uint32_t stream_layout[6];  // StreamLayout of the stream kernel (byte offsets in its LDS)
+  int64_t stream_lds;         // LDS bytes of the stream kernel
+  int64_t stream_tiles;  // tiles per workgroup of the stream kernel (0: by size; YE3T_STREAM_TILES)
 };
 
 namespace ye3t {
@@ -137,6 +151,251 @@ __global__ __launch_bounds__(kLanes) void product_kernel(
     const int r = idx / nf;
     const int c = idx - r * nf;
     B[(s0 + r) * F + c0 + c] = Out(ws[int(out_slots[o0 + c]) * kPad + r]);
+  }
+}
+
+// Term-stream interpreter.  The program words of a chunk are decoded on the
+// host into one 16-byte record per factor pair and a flag word beside it:
+//   record = (LDS byte offset of factor a, of factor b, coefficient: fp64 as
+//             low and high word, fp32 in the third word)
+//   flag   = flags | LDS byte offset of the destination << 16
+// A plain record accumulates acc += c * (a * b); kFlush then stores acc at the
+// destination and restarts it.  Terms of three or four factors take two
+// records: kChain keeps p = a * b, the next record (kChained) multiplies
+// (p * a) * b.  One-factor terms read b from a slot holding 1.  Each chunk's
+// records are padded to a multiple of kGroup with c = 0 terms, and its density
+// loads to a multiple of 8 with loads into a sink slot, so the unrolled loops
+// need no bounds tests.  No record of an aligned group of kGroup reads a slot
+// that an earlier record of the group flushes (the encoder pads with c = 0
+// terms to start a new group), so a group's factors are all read before its
+// stores.
+//
+// A workgroup is one wave that runs one chunk over tiles_per_group
+// consecutive 64-sample tiles (lane = sample).  The chunk's records, flags,
+// density-load list and output slots are staged in LDS once; records are read
+// back with broadcast LDS reads, which return in order, so the next group's
+// records are in flight while the current group computes.  The workspace is
+// [slot][64] values (slots + 2 for the constant 1 and the sink).  The next
+// tile's density values are loaded into registers while the current tile's
+// terms run.  The density is read row-major (A[s * lda + col]) or column-major
+// (A[col * lda + s]: one contiguous 64-sample block per column).
+#ifndef YE3T_STREAM_GROUP
+#define YE3T_STREAM_GROUP 8
+#endif
+constexpr uint32_t kFlush = 1, kChain = 2, kChained = 4;
+constexpr int kPrefetch = 32;  // density loads per tile held in registers ahead of time
+constexpr int kGroup = YE3T_STREAM_GROUP;  // records per hazard-free group (a multiple of 4)
+
+template <typename Real>
+__device__ inline Real record_coeff(const uint4& r) {
+  if constexpr (sizeof(Real) == 8) {
+    return __hiloint2double(int(r.w), int(r.z));
+  } else {
+    return __uint_as_float(r.z);
+  }
+}
+
+template <typename Real>
+__device__ inline Real& lds_at(unsigned char* base, uint32_t off) {
+  return *reinterpret_cast<Real*>(base + off);
+}
+
+struct StreamLayout {
+  uint32_t ws_bytes;    // workspace: (slots + 2) * 64 * elem
+  uint32_t rec_at;      // records (16 B each)
+  uint32_t flag_at;     // flag words
+  uint32_t load_at;     // (dst offset, column) pairs
+  uint32_t out_at;      // output slot byte offsets
+  uint32_t one_off;     // workspace byte offset of the slot holding 1
+};
+
+template <typename Real, typename Out, bool COLUMNS>
+__global__ __launch_bounds__(kLanes) void product_stream_kernel(
+    const Real* __restrict__ A, int64_t lda, int64_t samples, Out* __restrict__ B, int64_t F,
+    const uint4* __restrict__ recs, const uint32_t* __restrict__ flags, const int64_t* __restrict__ rec_off,
+    const uint2* __restrict__ loads, const int64_t* __restrict__ load_off, const uint16_t* __restrict__ out_slots,
+    const int64_t* __restrict__ out_off, const int64_t* __restrict__ first_col, int64_t chunks,
+    StreamLayout lay, int64_t tiles_per_group) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int lane = threadIdx.x;
+  const int64_t group = blockIdx.x / chunks;
+  const int64_t chunk = blockIdx.x - group * chunks;
+  const int64_t tiles = (samples + kLanes - 1) / kLanes;
+  const int64_t tile0 = group * tiles_per_group;
+  const int64_t tile_end = tile0 + tiles_per_group < tiles ? tile0 + tiles_per_group : tiles;
+  unsigned char* wsb = smem_raw + lane * sizeof(Real);
+  uint4* lrec = reinterpret_cast<uint4*>(smem_raw + lay.rec_at);
+  uint32_t* lflag = reinterpret_cast<uint32_t*>(smem_raw + lay.flag_at);
+  uint4* lload = reinterpret_cast<uint4*>(smem_raw + lay.load_at);
+  uint32_t* lout = reinterpret_cast<uint32_t*>(smem_raw + lay.out_at);
+
+  // stage the chunk's program in LDS
+  const int64_t r0 = rec_off[chunk];
+  const int nr = int(rec_off[chunk + 1] - r0);
+  const int64_t l0 = load_off[chunk];
+  const int nl = int(load_off[chunk + 1] - l0);
+  const int64_t o0 = out_off[chunk];
+  const int nf = int(out_off[chunk + 1] - o0);
+  for (int i = lane; i < nr; i += kLanes) {
+    lrec[i] = recs[r0 + i];
+    lflag[i] = flags[r0 + i];
+  }
+  // load entry i: (dst byte offset, element offset of its column: col * lda
+  // column-major, col row-major) so a tile's load address is one add
+  for (int i = lane; i < nl; i += kLanes) {
+    const uint2 e = loads[l0 + i];
+    const uint64_t eo = COLUMNS ? uint64_t(e.y) * uint64_t(lda) : uint64_t(e.y);
+    lload[i] = make_uint4(e.x, 0u, uint32_t(eo), uint32_t(eo >> 32));
+  }
+  for (int i = lane; i < nf; i += kLanes) lout[i] = uint32_t(out_slots[o0 + i]) * (kLanes * sizeof(Real));
+  lds_at<Real>(wsb, lay.one_off) = Real(1);
+  __syncthreads();
+  const int64_t c0 = first_col[chunk];
+  const float inv_nf = 1.0f / float(nf > 0 ? nf : 1);
+  const int npre = nl < kPrefetch ? nl : kPrefetch;
+
+  auto tile_src = [&](int64_t tile) {
+    const int64_t s = tile * kLanes + lane;
+    return COLUMNS ? A + s : A + (s < samples ? s : 0) * lda;
+  };
+  auto entry_off = [&](int i) {
+    const uint4 e = lload[i];
+    return int64_t((uint64_t(e.w) << 32) | e.z);
+  };
+  // density values of one tile for the first npre loads (into registers)
+  auto fetch = [&](int64_t tile, Real* v) {
+    const Real* __restrict__ src = tile_src(tile);
+#pragma unroll
+    for (int u = 0; u < kPrefetch; u += 8) {
+      if (u < npre) {
+#pragma unroll
+        for (int w = 0; w < 8; ++w) v[u + w] = src[entry_off(u + w)];
+      }
+    }
+  };
+  Real pre[kPrefetch];
+  if (tile0 < tile_end) fetch(tile0, pre);
+
+  for (int64_t tile = tile0; tile < tile_end; ++tile) {
+    const int64_t s0 = tile * kLanes;
+    // the prefetched values, then any loads beyond them
+#pragma unroll
+    for (int u = 0; u < kPrefetch; u += 8) {
+      if (u < npre) {
+#pragma unroll
+        for (int w = 0; w < 8; ++w) lds_at<Real>(wsb, lload[u + w].x) = pre[u + w];
+      }
+    }
+    if (nl > kPrefetch) {
+      const Real* __restrict__ src = tile_src(tile);
+      for (int q = kPrefetch; q < nl; q += 8) {
+        Real v[8];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) v[w] = src[entry_off(q + w)];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) lds_at<Real>(wsb, lload[q + w].x) = v[w];
+      }
+    }
+    if (tile + 1 < tile_end) fetch(tile + 1, pre);
+
+    // the term stream, kGroup records at a time; each group's records and flags
+    // are read one group ahead (the program region of LDS is not written here)
+    Real acc = Real(0), p = Real(1);
+    uint4 fw_next[kGroup / 4];
+    uint4 r_next[kGroup];
+#pragma unroll
+    for (int u = 0; u < kGroup / 4; ++u) fw_next[u] = *reinterpret_cast<const uint4*>(lflag + 4 * u);
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) r_next[u] = lrec[u];
+    for (int q = 0; q < nr; q += kGroup) {
+      uint32_t f[kGroup];
+#pragma unroll
+      for (int u = 0; u < kGroup / 4; ++u) {
+        f[4 * u] = uint32_t(__builtin_amdgcn_readfirstlane(int(fw_next[u].x)));
+        f[4 * u + 1] = uint32_t(__builtin_amdgcn_readfirstlane(int(fw_next[u].y)));
+        f[4 * u + 2] = uint32_t(__builtin_amdgcn_readfirstlane(int(fw_next[u].z)));
+        f[4 * u + 3] = uint32_t(__builtin_amdgcn_readfirstlane(int(fw_next[u].w)));
+      }
+      uint4 r[kGroup];
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) r[u] = r_next[u];
+      const int qn = q + kGroup < nr ? q + kGroup : q;
+#pragma unroll
+      for (int u = 0; u < kGroup / 4; ++u) fw_next[u] = *reinterpret_cast<const uint4*>(lflag + qn + 4 * u);
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) r_next[u] = lrec[qn + u];
+      // no record of a group reads a slot flushed earlier in the group: all its
+      // factors are read before any of its stores
+      Real a[kGroup], b[kGroup];
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        a[u] = lds_at<Real>(wsb, r[u].x);
+        b[u] = lds_at<Real>(wsb, r[u].y);
+      }
+      uint32_t any = 0;
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) any |= f[u];
+      if ((any & (kChain | kChained)) == 0) {
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) {
+          acc = d_fma(record_coeff<Real>(r[u]), a[u] * b[u], acc);
+          if (f[u] & kFlush) {
+            lds_at<Real>(wsb, f[u] >> 16) = acc;
+            acc = Real(0);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) {
+          if (f[u] & kChain) {
+            p = a[u] * b[u];
+            continue;
+          }
+          const Real t = (f[u] & kChained) ? (p * a[u]) * b[u] : a[u] * b[u];
+          acc = d_fma(record_coeff<Real>(r[u]), t, acc);
+          if (f[u] & kFlush) {
+            lds_at<Real>(wsb, f[u] >> 16) = acc;
+            acc = Real(0);
+          }
+        }
+      }
+    }
+    // transposed write-out of the chunk's [rows, nf] block: consecutive lanes
+    // take consecutive columns of a row, so a store covers a few row segments
+    // (a few cache lines) rather than one line per lane
+    {
+      const int rows = (samples - s0) < kLanes ? int(samples - s0) : kLanes;
+      const int total = rows * nf;
+      for (int idx = lane; idx < total; idx += kLanes) {
+        // (idx + 1/2) / nf lies at least 1/(2 nf) from an integer: the float quotient truncates exactly
+        const int r = int((float(idx) + 0.5f) * inv_nf);
+        const int c = idx - r * nf;
+        B[(s0 + r) * F + c0 + c] = Out(lds_at<Real>(smem_raw + r * sizeof(Real), lout[c]));
+      }
+    }
+    // the next tile's values overwrite slots this write-out reads (one wave:
+    // LDS operations complete in order; this keeps the compiler from moving them)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+}
+
+// At[c * ld + r] = A[r * cols + c] through 64 x 64 LDS tiles.
+template <typename Real>
+__global__ __launch_bounds__(256) void transpose_kernel(const Real* __restrict__ A, int64_t rows, int64_t cols,
+                                                        Real* __restrict__ At, int64_t ld) {
+  __shared__ Real t[64][65];
+  const int64_t r0 = int64_t(blockIdx.y) * 64, c0 = int64_t(blockIdx.x) * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int k = ty; k < 64; k += 4) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    t[k][tx] = (r < rows && c < cols) ? A[r * cols + c] : Real(0);
+  }
+  __syncthreads();
+  for (int k = ty; k < 64; k += 4) {
+    const int64_t c = c0 + k, r = r0 + tx;
+    if (c < cols && r < ld) At[c * ld + r] = t[tx][k];
   }
 }
 
@@ -234,7 +493,161 @@ int upload(T** dst, const T* src, int64_t count) {
 
 size_t product_lds_bytes(const ye3t_hip_product_plan* p) {
   const size_t elem = p->dtype == YE3T_F64 ? 8 : 4;
-  return size_t(p->slots) * kPad * elem;
+  return p->use_stream ? size_t(p->stream_lds) : size_t(p->slots) * kPad * elem;
+}
+
+// Decode validated program words into the term stream of product_stream_kernel
+// (workspace pitch 64 values; slots `slots` and `slots + 1` hold 1 and the
+// padding loads) and lay out its LDS.  Returns false when the workspace's byte
+// offsets do not fit the flag words' 16 bits or the LDS exceeds 64 KB.
+bool build_stream(const ye3t_product_plan_desc* d, std::vector<uint4>& recs, std::vector<uint32_t>& flags,
+                  std::vector<int64_t>& rec_off, std::vector<uint2>& loads, std::vector<int64_t>& load_off,
+                  StreamLayout& lay, int64_t& lds_bytes) {
+  const uint32_t elem = d->dtype == YE3T_F64 ? 8 : 4;
+  const uint32_t pitch = uint32_t(kLanes) * elem;
+  if ((uint64_t(d->workspace_slots) + 2) * pitch > 0x10000u) return false;
+  const uint32_t one = uint32_t(d->workspace_slots) * pitch, sink = one + pitch;
+  auto off = [&](uint32_t slot) { return slot * pitch; };
+  auto record = [&](uint32_t a, uint32_t b, int64_t ci) {
+    uint4 r = make_uint4(a, b, 0, 0);
+    if (ci < 0) return r;
+    if (elem == 8) {
+      uint64_t bits;
+      std::memcpy(&bits, static_cast<const double*>(d->coeffs) + ci, 8);
+      r.z = uint32_t(bits);
+      r.w = uint32_t(bits >> 32);
+    } else {
+      std::memcpy(&r.z, static_cast<const float*>(d->coeffs) + ci, 4);
+    }
+    return r;
+  };
+  rec_off.assign(1, 0);
+  load_off.assign(1, 0);
+  const uint4 nop = make_uint4(one, one, 0, 0);  // acc += 0 * 1 * 1
+  uint32_t flushed[kGroup];  // destinations flushed so far in the current group
+  int nflushed = 0;
+  auto pad_group = [&]() {
+    while ((int64_t(recs.size()) - rec_off.back()) % kGroup) {
+      recs.push_back(nop);
+      flags.push_back(0);
+    }
+  };
+  // append a record; start a new group first if it reads a slot flushed earlier in this one
+  auto emit = [&](const uint4& r, uint32_t flag) {
+    bool hazard = false;
+    for (int k = 0; k < nflushed; ++k) hazard |= (flushed[k] == r.x || flushed[k] == r.y);
+    if (hazard) pad_group();
+    if ((int64_t(recs.size()) - rec_off.back()) % kGroup == 0) nflushed = 0;
+    recs.push_back(r);
+    flags.push_back(flag);
+    if (flag & kFlush) flushed[nflushed++] = flag >> 16;
+  };
+  int64_t max_recs = 0, max_loads = 0, max_out = 0;
+  for (int64_t c = 0; c < d->chunk_count; ++c) {
+    nflushed = 0;
+    int64_t wpos = d->chunk_word_offsets[c];
+    const int64_t wend = d->chunk_word_offsets[c + 1];
+    int64_t cpos = d->chunk_coeff_offsets[c];
+    while (wpos < wend) {
+      const uint32_t h = d->words[wpos];
+      const uint32_t op = h >> 28, n = h & 0x00FFFFFFu;
+      if (op == OP_LOAD) {
+        for (uint32_t i = 0; i < n; ++i) {
+          const uint32_t t = d->words[wpos + 1 + i];
+          loads.push_back(make_uint2(off(t >> 16), t & 0xFFFFu));
+        }
+        wpos += 1 + n;
+        continue;
+      }
+      const uint32_t dst = off(d->words[wpos + 1]);
+      const uint32_t* tw = d->words + wpos + 2;
+      if (n == 0) emit(nop, kFlush | (dst << 16));  // an empty sum stores 0
+      for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t flush = (i + 1 == n) ? (kFlush | (dst << 16)) : 0;
+        if (op == OP_ACC1) {
+          emit(record(off(tw[i] & 0xFFFFu), one, cpos + i), flush);
+        } else if (op == OP_ACC2) {
+          emit(record(off(tw[i] & 0xFFFFu), off(tw[i] >> 16), cpos + i), flush);
+        } else {
+          const uint32_t t0 = tw[2 * i], t1 = tw[2 * i + 1];
+          emit(record(off(t0 & 0xFFFFu), off(t0 >> 16), -1), kChain);
+          emit(record(off(t1 & 0xFFFFu), op == OP_ACC4 ? off(t1 >> 16) : one, cpos + i), kChained | flush);
+        }
+      }
+      wpos += 2 + int64_t((op == OP_ACC3 || op == OP_ACC4) ? 2 : 1) * n;
+      cpos += n;
+    }
+    pad_group();
+    while ((int64_t(loads.size()) - load_off.back()) % 8) loads.push_back(make_uint2(sink, 0));
+    max_recs = std::max<int64_t>(max_recs, int64_t(recs.size()) - rec_off.back());
+    max_loads = std::max<int64_t>(max_loads, int64_t(loads.size()) - load_off.back());
+    max_out = std::max<int64_t>(max_out, d->chunk_out_offsets[c + 1] - d->chunk_out_offsets[c]);
+    rec_off.push_back(int64_t(recs.size()));
+    load_off.push_back(int64_t(loads.size()));
+  }
+  if (recs.empty()) {
+    recs.push_back(nop);
+    flags.push_back(0);
+  }
+  if (loads.empty()) loads.push_back(make_uint2(sink, 0));
+  auto up16 = [](int64_t b) { return (b + 15) & ~int64_t(15); };
+  int64_t at = up16((int64_t(d->workspace_slots) + 2) * pitch);
+  lay.ws_bytes = uint32_t(at);
+  lay.rec_at = uint32_t(at);
+  at = up16(at + 16 * max_recs);
+  lay.flag_at = uint32_t(at);
+  at = up16(at + 4 * max_recs);
+  lay.load_at = uint32_t(at);
+  at = up16(at + 16 * max_loads);
+  lay.out_at = uint32_t(at);
+  at = up16(at + 4 * max_out);
+  lay.one_off = one;
+  lds_bytes = at;
+  return at <= 64 * 1024;
+}
+
+// tiles per workgroup of the stream kernel: the most (up to 16) that still
+// leaves about 8 workgroups per workgroup slot of the device
+int64_t stream_tiles_per_group(const ye3t_hip_product_plan* p, int64_t tiles) {
+  int64_t per = p->stream_tiles;
+  if (per <= 0) {
+    per = 1;
+    while (per < 16 && (tiles + 2 * per - 1) / (2 * per) * p->chunk_count >= 8 * 256 * 6) per *= 2;
+  }
+  return per;
+}
+
+template <bool COLUMNS>
+int launch_stream(const ye3t_hip_product_plan* p, const void* A, int64_t lda, int64_t samples, void* B,
+                  ye3t_stream_t stream) {
+  const int64_t tiles = (samples + kLanes - 1) / kLanes;
+  const int64_t per = stream_tiles_per_group(p, tiles);
+  const int64_t groups = (tiles + per - 1) / per;
+  const int64_t grid = groups * p->chunk_count;
+  YE3T_REQUIRE(grid <= int64_t(0x7FFFFFFF), "too many samples for one launch");
+  const size_t lds = size_t(p->stream_lds);
+  StreamLayout lay;
+  lay.ws_bytes = p->stream_layout[0];
+  lay.rec_at = p->stream_layout[1];
+  lay.flag_at = p->stream_layout[2];
+  lay.load_at = p->stream_layout[3];
+  lay.out_at = p->stream_layout[4];
+  lay.one_off = p->stream_layout[5];
+  const hipStream_t s = as_stream(stream);
+  if (p->dtype == YE3T_F64 && p->out_dtype == YE3T_F64) {
+    hipLaunchKernelGGL((product_stream_kernel<double, double, COLUMNS>), dim3(unsigned(grid)), dim3(kLanes), lds, s,
+                       (const double*)A, lda, samples, (double*)B, p->feature_count, p->recs, p->flags, p->rec_off,
+                       p->loads, p->load_off, p->out_slots, p->out_off, p->first_col, p->chunk_count, lay, per);
+  } else if (p->dtype == YE3T_F64) {
+    hipLaunchKernelGGL((product_stream_kernel<double, float, COLUMNS>), dim3(unsigned(grid)), dim3(kLanes), lds, s,
+                       (const double*)A, lda, samples, (float*)B, p->feature_count, p->recs, p->flags, p->rec_off,
+                       p->loads, p->load_off, p->out_slots, p->out_off, p->first_col, p->chunk_count, lay, per);
+  } else {
+    hipLaunchKernelGGL((product_stream_kernel<float, float, COLUMNS>), dim3(unsigned(grid)), dim3(kLanes), lds, s,
+                       (const float*)A, lda, samples, (float*)B, p->feature_count, p->recs, p->flags, p->rec_off,
+                       p->loads, p->load_off, p->out_slots, p->out_off, p->first_col, p->chunk_count, lay, per);
+  }
+  return check_launch("product_stream_kernel");
 }
 
 }  // namespace ye3t
@@ -242,6 +655,40 @@ size_t product_lds_bytes(const ye3t_hip_product_plan* p) {
 using namespace ye3t;
 
 extern "C" {
+
+int ye3t_hip_transpose(int dtype, const void* A, int64_t rows, int64_t cols, void* At, int64_t ld,
+                       ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(rows >= 0 && cols >= 0 && ld >= rows, "bad transpose shape");
+  if (cols == 0 || ld == 0) return YE3T_OK;
+  YE3T_REQUIRE(A != nullptr || rows == 0, "NULL input");
+  YE3T_REQUIRE(At != nullptr, "NULL output");
+  const int64_t gx = (cols + 63) / 64, gy = (ld + 63) / 64;
+  YE3T_REQUIRE(gx <= 0x7FFFFFFF && gy <= 65535, "transpose too large for one launch");
+  const dim3 grid = dim3(unsigned(gx), unsigned(gy), 1u);
+  if (dtype == YE3T_F64) {
+    hipLaunchKernelGGL(transpose_kernel<double>, grid, dim3(256), 0, as_stream(stream), (const double*)A, rows, cols,
+                       (double*)At, ld);
+  } else if (dtype == YE3T_F32) {
+    hipLaunchKernelGGL(transpose_kernel<float>, grid, dim3(256), 0, as_stream(stream), (const float*)A, rows, cols,
+                       (float*)At, ld);
+  } else {
+    return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);
+  }
+  return check_launch("transpose_kernel");
+}
+
+int ye3t_hip_product_forward_columns(const ye3t_hip_product_plan* p, const void* At, int64_t ld, int64_t samples,
+                                     void* B, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(p != nullptr, "NULL plan");
+  YE3T_REQUIRE(samples >= 0, "negative sample count");
+  if (samples == 0) return YE3T_OK;
+  YE3T_REQUIRE(At && B, "NULL input or output");
+  YE3T_REQUIRE(p->use_stream, "this plan has no term stream (workspace too large); use ye3t_hip_product_forward");
+  YE3T_REQUIRE(ld >= (samples + kLanes - 1) / kLanes * kLanes, "ld must cover whole 64-sample tiles");
+  return launch_stream<true>(p, At, ld, samples, B, stream);
+}
 
 void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* p) {
   if (!p) return;
@@ -255,6 +702,11 @@ void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* p) {
   (void)hipFree(p->coeff_off);
   (void)hipFree(p->out_off);
   (void)hipFree(p->first_col);
+  (void)hipFree(p->recs);
+  (void)hipFree(p->flags);
+  (void)hipFree(p->rec_off);
+  (void)hipFree(p->loads);
+  (void)hipFree(p->load_off);
   if (p->module) (void)hipModuleUnload(p->module);
   if (p->readout_module) (void)hipModuleUnload(p->readout_module);
   if (p->adjoint_module) (void)hipModuleUnload(p->adjoint_module);
@@ -338,6 +790,30 @@ int ye3t_hip_product_plan_create(const ye3t_product_plan_desc* d, ye3t_hip_produ
       (rc = upload(&p->first_col, d->chunk_first_column, C)) != YE3T_OK) {
     ye3t_hip_product_plan_destroy(p);
     return rc;
+  }
+  // the term-stream interpreter; YE3T_PRODUCT_STREAM=0 keeps the word interpreter (comparisons)
+  const char* env = std::getenv("YE3T_PRODUCT_STREAM");
+  std::vector<uint4> recs;
+  std::vector<uint32_t> flags;
+  std::vector<uint2> loads;
+  std::vector<int64_t> rec_off, load_off;
+  StreamLayout lay{};
+  int64_t stream_lds = 0;
+  if (!(env && env[0] == '0') && build_stream(d, recs, flags, rec_off, loads, load_off, lay, stream_lds)) {
+    if ((rc = upload(&p->recs, recs.data(), int64_t(recs.size()))) != YE3T_OK ||
+        (rc = upload(&p->flags, flags.data(), int64_t(flags.size()))) != YE3T_OK ||
+        (rc = upload(&p->rec_off, rec_off.data(), C + 1)) != YE3T_OK ||
+        (rc = upload(&p->loads, loads.data(), int64_t(loads.size()))) != YE3T_OK ||
+        (rc = upload(&p->load_off, load_off.data(), C + 1)) != YE3T_OK) {
+      ye3t_hip_product_plan_destroy(p);
+      return rc;
+    }
+    const uint32_t fields[6] = {lay.ws_bytes, lay.rec_at, lay.flag_at, lay.load_at, lay.out_at, lay.one_off};
+    std::memcpy(p->stream_layout, fields, sizeof(fields));
+    p->stream_lds = stream_lds;
+    p->use_stream = 1;
+    const char* per = std::getenv("YE3T_STREAM_TILES");
+    p->stream_tiles = per ? std::atoll(per) : 0;
   }
   *out = p;
   return YE3T_OK;
@@ -428,11 +904,14 @@ int ye3t_hip_product_plan_select(ye3t_hip_product_plan* p, int use_interpreter) 
   return YE3T_OK;
 }
 
+int ye3t_hip_product_plan_uses_stream(const ye3t_hip_product_plan* p) { return p && p->use_stream ? 1 : 0; }
+
 int ye3t_hip_product_launch_info(const ye3t_hip_product_plan* p, int64_t samples, int64_t* grid, int64_t* block,
                                  int64_t* lds) {
   YE3T_REQUIRE(p != nullptr, "NULL plan");
   const int64_t tiles = (samples + kLanes - 1) / kLanes;
-  if (grid) *grid = tiles * p->chunk_count;
+  const int64_t per = p->use_stream ? stream_tiles_per_group(p, tiles) : 1;
+  if (grid) *grid = (tiles + per - 1) / per * p->chunk_count;
   if (block) *block = kLanes;
   if (lds) *lds = int64_t(product_lds_bytes(p));
   return YE3T_OK;
@@ -465,6 +944,7 @@ int ye3t_hip_product_forward(const ye3t_hip_product_plan* p, const void* A, int6
   const int64_t grid = tiles * p->chunk_count;
   YE3T_REQUIRE(grid <= int64_t(0x7FFFFFFF), "too many samples for one launch");
   const size_t lds = product_lds_bytes(p);
+  if (p->use_stream) return launch_stream<false>(p, A, p->a_width, samples, B, stream);
   if (p->dtype == YE3T_F64 && p->out_dtype == YE3T_F64) {
     hipLaunchKernelGGL((product_kernel<double, double>), dim3(unsigned(grid)), dim3(kLanes), lds, as_stream(stream),
                        (const double*)A, samples, p->a_width, (double*)B, p->feature_count, p->words, p->word_off,

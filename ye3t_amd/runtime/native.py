@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 48
+ABI_VERSION = 49
 _LIB = None
 
 F32, F64 = 0, 1
@@ -93,6 +93,9 @@ def lib():
     L.ye3t_hip_rows_dot.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, ctypes.c_double, _vp, _vp]
     L.ye3t_hip_product_plan_attach_adjoint.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, ctypes.c_int]
     L.ye3t_hip_product_adjoint.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
+    L.ye3t_hip_transpose.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _i64, _vp]
+    L.ye3t_hip_product_forward_columns.argtypes = [_vp, _vp, _i64, _i64, _vp, _vp]
+    L.ye3t_hip_product_plan_uses_stream.argtypes = [_vp]
     L.ye3t_hip_neighbor_workspace_bytes.argtypes = [_i64, ctypes.POINTER(CellGrid)]
     L.ye3t_hip_neighbor_workspace_bytes.restype = _i64
     L.ye3t_hip_neighbor_count.argtypes = [ctypes.c_int, _vp, _i64, ctypes.POINTER(CellGrid), ctypes.c_double, _vp,
@@ -116,6 +119,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_density_accumulate_adjoint", "ye3t_hip_product_plan_attach_readout", "ye3t_hip_product_linear_forward",
     "ye3t_hip_rows_dot", "ye3t_hip_product_plan_attach_adjoint", "ye3t_hip_product_adjoint",
     "ye3t_hip_neighbor_workspace_bytes", "ye3t_hip_neighbor_count", "ye3t_hip_neighbor_fill",
+    "ye3t_hip_transpose", "ye3t_hip_product_forward_columns", "ye3t_hip_product_plan_uses_stream",
 )
 
 
@@ -435,6 +439,31 @@ class ProductPlanHandle:
                "ye3t_hip_product_forward")
         return out
 
+    @property
+    def uses_stream(self):
+        """True when the plan's interpreter is the term stream (see ``forward_columns``)."""
+        return bool(lib().ye3t_hip_product_plan_uses_stream(self._handle))
+
+    def forward_columns(self, At, samples, out=None):
+        """The product on a column-major density ``At [a_width, ld]`` (``ld`` a
+        multiple of 64 covering ``samples``), as :func:`transpose` writes it."""
+        import torch
+
+        if At.ndim != 2 or int(At.shape[0]) != int(self.program["a_width"]):
+            raise ValueError(f"At must be [{self.program['a_width']}, ld]")
+        want = torch.float64 if self.dtype == "f64" else torch.float32
+        if At.dtype != want:
+            raise ValueError(f"At must be {want} for this plan")
+        S, ld = int(samples), int(At.shape[1])
+        out_t = torch.float64 if self.out_dtype == "f64" else torch.float32
+        if out is None:
+            out = torch.empty((S, self.feature_count), dtype=out_t, device=At.device)
+        elif tuple(out.shape) != (S, self.feature_count) or out.dtype != out_t:
+            raise ValueError("out has the wrong shape or dtype")
+        _check(lib().ye3t_hip_product_forward_columns(self._handle, _dev(At, "At"), ld, S, _dev(out, "B"),
+                                                      _stream()), "ye3t_hip_product_forward_columns")
+        return out
+
     def attach_readout(self, source, meta):
         """Compile and attach a fused linear readout kernel (``codegen.generate_readout``)."""
         if meta["feature_count"] != self.feature_count or meta["a_width"] != self.program["a_width"]:
@@ -588,3 +617,21 @@ def neighbor_list(positions, cutoff, grid=None):
                "ye3t_hip_neighbor_fill")
     return {"schema": "ye3t_amd_neighbor_csr_v1", "target_offsets": offsets, "edge_targets": centers,
             "edge_sources": nbrs, "edge_vectors": vecs, "node_count": N, "cutoff": float(cutoff)}
+
+
+def transpose(A, out=None, ld=None):
+    """Column-major copy ``At [cols, ld]`` of ``A [rows, cols]`` (``ld`` defaults to
+    ``rows`` rounded up to 64; the rows past ``rows`` are zero)."""
+    import torch
+
+    if A.ndim != 2:
+        raise ValueError("A must be 2-D")
+    rows, cols = (int(x) for x in A.shape)
+    ld = int(ld) if ld is not None else (rows + 63) // 64 * 64
+    if out is None:
+        out = torch.empty((cols, ld), dtype=A.dtype, device=A.device)
+    elif tuple(out.shape) != (cols, ld) or out.dtype != A.dtype:
+        raise ValueError("out has the wrong shape or dtype")
+    _check(lib().ye3t_hip_transpose(_dtype_code(A), _dev(A, "A"), rows, cols, _dev(out, "At"), ld, _stream()),
+           "ye3t_hip_transpose")
+    return out
