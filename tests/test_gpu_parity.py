@@ -526,3 +526,22 @@ def test_persistent_generated_kernel_tiles_and_misaligned_output(gpu, monkeypatc
             assert err < (1e-5 if accumulate == "f64" else TOL["f32"])
         # the generic kernel on the misaligned view agrees with the persistent kernel
         assert column_rel_error(got_mis, got.astype(np.float64)) < (1e-6 if accumulate == "f64" else 1e-5)
+
+
+@pytest.mark.parametrize("cid,dtype,samples", [(4, "f32", 300), (2, "f64", 150)])
+def test_pipeline_from_a_saved_plan(gpu, tmp_path, cid, dtype, samples):
+    """A plan written to disk and loaded back runs to the same bits (generated
+    kernel for config 4, term-stream interpreter for config 2)."""
+    flush(f"saved plan config {cid} {dtype}")
+    import torch
+
+    from ye3t_amd.ace import plan_io
+
+    spec = W.config(cid).feature_spec
+    pipe = ACEPipeline(spec, dtype)
+    path = tmp_path / "plan.json"
+    plan_io.save_plan(pipe.plan, path)
+    loaded = ACEPipeline(spec, dtype, plan=plan_io.load_plan(path))
+    assert loaded.kernel == pipe.kernel
+    A = _t(np.random.default_rng(16).normal(size=(samples, pipe.plan.a_width)), dtype, gpu)
+    assert torch.equal(loaded.product(A), pipe.product(A))
