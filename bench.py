@@ -161,7 +161,15 @@ def bench_op(args, cfg):
                              device="cuda")
         gA = torch.empty_like(rows)
         pipe.product_adjoint(rows, gB, out=gA)  # compiles and attaches the adjoint kernel
-        t = _time_kernel(lambda: pipe.handle.adjoint(rows, gB, out=gA), args.steps, args.warmup)
+        if pipe.last_adjoint_backend == "generated":
+            t = _time_kernel(lambda: pipe.handle.adjoint(rows, gB, out=gA), args.steps, args.warmup)
+        else:
+            # the term stream's reverse mode on the column-major density (the copy is
+            # the forward's; timed here: clearing the partial sums, the kernel, the sum)
+            At = native.transpose(rows)
+            t = _time_kernel(lambda: pipe._adjoint_handle.adjoint_stream(At, gB, samples=S, columns=True, out=gA),
+                             args.steps, args.warmup)
+        line["backend"] = pipe.last_adjoint_backend
         nbytes = S * pipe.plan.a_width * rows.element_size() * 2 + S * pipe.feature_count * gB.element_size()
         line.update({
             "metric": "adjoint samples/s", "value": S / t, "unit": "samples/s", "higher_is_better": True,

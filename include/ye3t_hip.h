@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 49 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 50 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -298,6 +298,24 @@ int ye3t_hip_product_forward_columns(const ye3t_hip_product_plan* plan, const vo
 /* Select which kernel product_forward launches: 0 = generated (if attached),
  * 1 = generic interpreter. */
 int ye3t_hip_product_plan_select(ye3t_hip_product_plan* plan, int use_interpreter);
+
+/* Device workspace bytes of ye3t_hip_product_adjoint_stream for `samples`
+ * samples (0 for plans without a term stream; -1 on invalid input). */
+int64_t ye3t_hip_product_adjoint_workspace_bytes(const ye3t_hip_product_plan* plan, int64_t samples);
+
+/* gA[s] = J(A[s])^T gB[s] (row-major gA [samples, a_width]) for plans run by
+ * the term-stream interpreter: the product's reverse mode with forward values
+ * recomputed, deterministic (per-group partial sums added in a fixed order,
+ * no atomics).  A is row-major (columns = 0, lda = a_width) or column-major
+ * (columns = 1, lda >= samples rounded up to 64); gB [samples, feature_count]
+ * in the plan's output dtype.  The workspace (ye3t_hip_product_adjoint_
+ * workspace_bytes) is cleared by the call.  Replaces
+ * ye3t_runtime::factorized_angular_adjoint (execution_plan_cuda.cu:6361, CPU
+ * core ye3t_runtime_core.h:1431-1456) for ACE plans too large for generated
+ * code. */
+int ye3t_hip_product_adjoint_stream(const ye3t_hip_product_plan* plan, const void* A, int64_t lda, int columns,
+                                    const void* gB, int64_t samples, void* workspace, int64_t workspace_bytes,
+                                    void* gA, ye3t_stream_t stream);
 
 /* 1 if the plan's interpreter is the term stream (LDS-staged records; the
  * plan also accepts ye3t_hip_product_forward_columns), 0 for the program-word

@@ -367,11 +367,43 @@ def test_product_adjoint(gpu, dtype, accumulate, tol):
     assert torch.equal(pipe.product_adjoint(A.to(gpu), 2 * gB.to(gpu)), 2 * gA)
 
 
-def test_product_adjoint_needs_a_generated_plan(gpu):
+@pytest.mark.parametrize("cid,dtype,accumulate,samples,tol", [
+    (2, "f64", "f64", 150, 1e-12), (3, "f64", "f64", 70, 1e-12), (3, "f32", "f32", 70, 2e-5),
+    (4, "f32", "f64", 4112, 1e-12), (4, "f32", "f32", 1000, 2e-5)])
+def test_stream_product_adjoint(gpu, cid, dtype, accumulate, samples, tol):
+    """gA = J(A)^T gB by the term stream's reverse mode (interpreter plans) vs the
+    oracle's reverse mode; row-major and column-major densities give the same
+    bits, doubling gB doubles gA exactly, and a rerun gives the same bits."""
+    flush(f"stream adjoint config {cid} storage {dtype} accumulate {accumulate} samples {samples}")
     import torch
 
-    pipe = ACEPipeline(W.config(2).feature_spec, "f64")
-    assert pipe.kernel == "interpreter"
+    spec = _species_rank4_spec() if cid == 3 else W.config(cid).feature_spec
+    pipe = ACEPipeline(spec, dtype, kernel="interpreter", accumulate=accumulate)
+    rng = np.random.default_rng(41 + cid)
+    a_t = torch.float64 if accumulate == "f64" else torch.float32
+    g_t = torch.float64 if dtype == "f64" else torch.float32
+    A = torch.as_tensor(rng.normal(size=(samples, pipe.plan.a_width)), dtype=a_t).to(gpu)
+    gB = torch.as_tensor(rng.normal(size=(samples, pipe.feature_count)), dtype=g_t).to(gpu)
+    gA = pipe.product_adjoint(A, gB)
+    assert pipe.last_adjoint_backend == "stream"
+    assert gA.dtype == a_t and tuple(gA.shape) == (samples, pipe.plan.a_width)
+    ref = oracle.ace_product_flat_adjoint(A.double().cpu().numpy(), gB.double().cpu().numpy(),
+                                          pipe.plan.flat_arrays())
+    err = column_rel_error(gA.cpu().double().numpy(), ref)
+    flush(f"  err {err:.3e}")
+    assert err < tol
+    assert torch.equal(pipe._adjoint_handle.adjoint_stream(A, gB), gA)  # row-major density
+    assert torch.equal(pipe.product_adjoint(A, 2 * gB), 2 * gA)
+    assert torch.equal(pipe.product_adjoint(A, gB), gA)
+
+
+def test_product_adjoint_needs_a_term_stream(gpu, monkeypatch):
+    """A workspace too wide for the term stream has no device adjoint."""
+    import torch
+
+    monkeypatch.setenv("YE3T_ADJOINT_SLOTS", "120")
+    pipe = ACEPipeline(W.config(4).feature_spec, "f64", 120, kernel="interpreter")
+    assert not pipe.handle.uses_stream
     A = torch.zeros((3, pipe.plan.a_width), dtype=torch.float64, device=gpu)
     with pytest.raises(NotImplementedError):
         pipe.product_adjoint(A, torch.zeros((3, pipe.feature_count), dtype=torch.float64, device=gpu))

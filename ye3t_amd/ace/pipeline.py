@@ -61,6 +61,7 @@ class ACEPipeline:
         self.handle = native.ProductPlanHandle(self.program, out_dtype=dtype)
         self._columns = os.environ.get("YE3T_PRODUCT_COLUMNS", "1") != "0"
         self._At = None  # (key, column-major density buffer) of the interpreter path
+        self._adjoint_handle = None  # program of the interpreter plans' reverse mode
         terms = sum(len(nd.get("terms", ())) for nd in self.plan.nodes)
         use_gen = kernel == "generated" or (kernel == "auto" and terms <= GENERATED_MAX_TERMS)
         if kernel not in {"auto", "generated", "interpreter"}:
@@ -125,12 +126,35 @@ class ACEPipeline:
 
     def product_adjoint(self, A_rows, gB, out=None):
         """Density gradient ``gA[s] = J(A[s])^T gB[s]`` of a feature gradient
-        (reference ``factorized_angular_adjoint``), with a plan-specialised
-        kernel compiled on first use.  Plans too large for generated code raise
-        ``NotImplementedError`` (no device adjoint for them yet)."""
+        (reference ``factorized_angular_adjoint``).  Generated plans use a
+        plan-specialised kernel compiled on first use; interpreter plans use the
+        term stream's reverse mode on the column-major density.  Plans whose
+        workspace is too wide for the term stream raise ``NotImplementedError``."""
+        self.last_adjoint_backend = None
         if self.kernel != "generated":
-            raise NotImplementedError("the device adjoint needs a plan small enough for a generated kernel "
-                                      f"({self.plan.feature_count} features here)")
+            if self._adjoint_handle is None:
+                # the forward's program; YE3T_ADJOINT_SLOTS compiles one with a narrower
+                # workspace (the reverse mode keeps values and gradients in LDS; tuning)
+                slots = os.environ.get("YE3T_ADJOINT_SLOTS")
+                if slots is None:
+                    self._adjoint_handle = self.handle
+                else:
+                    program = compile_program(self.plan, self.accumulate, int(slots))
+                    self._adjoint_handle = native.ProductPlanHandle(program, out_dtype=self.dtype)
+            if not self._adjoint_handle.uses_stream:
+                raise NotImplementedError("no device adjoint for a plan without a term stream "
+                                          f"(workspace of {self.program['workspace_slots']} slots)")
+            S = int(A_rows.shape[0])
+            ld = (S + 63) // 64 * 64
+            key = (int(A_rows.shape[1]), ld, A_rows.dtype, A_rows.device)
+            if self._At is None or self._At[0] != key:
+                import torch
+
+                self._At = (key, torch.empty((key[0], ld), dtype=A_rows.dtype, device=A_rows.device))
+            At = native.transpose(A_rows.contiguous(), out=self._At[1], ld=ld)
+            self.last_adjoint_backend = "stream"
+            return self._adjoint_handle.adjoint_stream(At, gB, samples=S, columns=True, out=out)
+        self.last_adjoint_backend = "generated"
         if getattr(self.handle, "adjoint_kernel", None) is None:
             from ye3t_amd.ace.codegen import generate_adjoint
 

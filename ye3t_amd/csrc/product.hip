@@ -381,6 +381,153 @@ __global__ __launch_bounds__(kLanes) void product_stream_kernel(
   }
 }
 
+// Reverse mode of the term stream: gA[s] = J(A[s])^T gB[s] for plans run by
+// the stream interpreter.  Workgroup (tile, group) runs the chunks
+// [group * chunks / groups, (group + 1) * chunks / groups) of one 64-sample
+// tile.  Per chunk: stage the program, load the density values and replay
+// the stream forward (every node value stays in its slot), seed a gradient
+// workspace with the chunk's feature gradients, then sweep the records
+// backwards:
+//   plain record  acc += c a b:      G[a] += c g b,  G[b] += c g a
+//   chained pair  p = a1 b1; acc += c (p a2) b2:
+//                 G[a2] += c g p b2, G[b2] += c g p a2,
+//                 G[a1] += c g a2 b2 b1, G[b1] += c g a2 b2 a1
+// with g = G[destination], read when the sweep meets the record that flushed
+// it (its last term).  The density gradients of the chunk's loads are added
+// into this workgroup's own block of P[group][col][s]; gA is the sum of the
+// groups in a fixed order (stream_adjoint_reduce_kernel), so no atomics and
+// the same bits every run.
+template <typename Real, typename G, bool COLUMNS>
+__global__ __launch_bounds__(kLanes) void product_stream_adjoint_kernel(
+    const Real* __restrict__ A, int64_t lda, int64_t samples, const G* __restrict__ gB, int64_t F,
+    const uint4* __restrict__ recs, const uint32_t* __restrict__ flags, const int64_t* __restrict__ rec_off,
+    const uint2* __restrict__ loads, const int64_t* __restrict__ load_off, const uint16_t* __restrict__ out_slots,
+    const int64_t* __restrict__ out_off, const int64_t* __restrict__ first_col, int64_t chunks, int64_t groups,
+    StreamLayout lay, Real* __restrict__ P, int64_t a_width, int64_t ldp) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int lane = threadIdx.x;
+  const int64_t tile = blockIdx.x / groups;
+  const int64_t group = blockIdx.x - tile * groups;
+  const int64_t s = tile * kLanes + lane;
+  const bool valid = s < samples;
+  unsigned char* wsb = smem_raw + lane * sizeof(Real);                  // values
+  unsigned char* gsb = smem_raw + lay.ws_bytes + lane * sizeof(Real);   // gradients
+  unsigned char* prog = smem_raw + lay.ws_bytes;                        // program region, past the gradients
+  uint4* lrec = reinterpret_cast<uint4*>(prog + lay.rec_at);
+  uint32_t* lflag = reinterpret_cast<uint32_t*>(prog + lay.flag_at);
+  uint2* lload = reinterpret_cast<uint2*>(prog + lay.load_at);
+  uint32_t* lout = reinterpret_cast<uint32_t*>(prog + lay.out_at);
+  const uint32_t pitch = kLanes * sizeof(Real);
+  const uint32_t sink = lay.one_off + pitch;
+  const uint32_t ws_slots = lay.one_off / pitch + 2;
+  Real* __restrict__ Pg = P + group * a_width * ldp + s;
+  const Real* __restrict__ src = COLUMNS ? A + s : A + (valid ? s : 0) * lda;
+  const int64_t c_begin = group * chunks / groups, c_end = (group + 1) * chunks / groups;
+
+  for (int64_t chunk = c_begin; chunk < c_end; ++chunk) {
+    const int64_t r0 = rec_off[chunk];
+    const int nr = int(rec_off[chunk + 1] - r0);
+    const int64_t l0 = load_off[chunk];
+    const int nl = int(load_off[chunk + 1] - l0);
+    const int64_t o0 = out_off[chunk];
+    const int nf = int(out_off[chunk + 1] - o0);
+    __syncthreads();  // the previous chunk is done with the program region
+    for (int i = lane; i < nr; i += kLanes) {
+      lrec[i] = recs[r0 + i];
+      lflag[i] = flags[r0 + i];
+    }
+    for (int i = lane; i < nl; i += kLanes) lload[i] = loads[l0 + i];
+    for (int i = lane; i < nf; i += kLanes) lout[i] = uint32_t(out_slots[o0 + i]) * pitch;
+    __syncthreads();
+    lds_at<Real>(wsb, lay.one_off) = Real(1);
+    for (int q = 0; q < nl; ++q) {
+      const uint2 e = lload[q];
+      lds_at<Real>(wsb, e.x) = COLUMNS ? src[int64_t(e.y) * lda] : src[e.y];
+    }
+    // forward replay
+    Real acc = Real(0), p = Real(1);
+    for (int q = 0; q < nr; ++q) {
+      const uint32_t f = lflag[q];
+      const uint4 r = lrec[q];
+      const Real a = lds_at<Real>(wsb, r.x), b = lds_at<Real>(wsb, r.y);
+      if (f & kChain) {
+        p = a * b;
+        continue;
+      }
+      const Real t = (f & kChained) ? (p * a) * b : a * b;
+      acc = d_fma(record_coeff<Real>(r), t, acc);
+      if (f & kFlush) {
+        lds_at<Real>(wsb, f >> 16) = acc;
+        acc = Real(0);
+      }
+    }
+    // gradient workspace: zero, then the chunk's feature gradients
+    for (uint32_t k = 0; k < ws_slots; ++k) lds_at<Real>(gsb, k * pitch) = Real(0);
+    const int64_t c0 = first_col[chunk];
+    for (int c = 0; c < nf; ++c) {
+      const Real gv = valid ? Real(gB[s * F + c0 + c]) : Real(0);
+      lds_at<Real>(gsb, lout[c]) += gv;
+    }
+    // reverse sweep
+    Real g = Real(0);
+    for (int q = nr - 1; q >= 0; --q) {
+      const uint32_t f = lflag[q];
+      if (f & kChain) continue;  // consumed with its chained partner
+      if (f & kFlush) g = lds_at<Real>(gsb, f >> 16);
+      const uint4 r = lrec[q];
+      const Real a = lds_at<Real>(wsb, r.x), b = lds_at<Real>(wsb, r.y);
+      const Real cg = record_coeff<Real>(r) * g;
+      if (f & kChained) {
+        const uint4 rc = lrec[q - 1];  // the chain record precedes its partner
+        const Real a1 = lds_at<Real>(wsb, rc.x), b1 = lds_at<Real>(wsb, rc.y);
+        const Real pp = a1 * b1, ab = a * b;
+        lds_at<Real>(gsb, r.x) += cg * pp * b;
+        lds_at<Real>(gsb, r.y) += cg * pp * a;
+        lds_at<Real>(gsb, rc.x) += cg * ab * b1;
+        lds_at<Real>(gsb, rc.y) += cg * ab * a1;
+      } else {
+        lds_at<Real>(gsb, r.x) += cg * b;
+        lds_at<Real>(gsb, r.y) += cg * a;
+      }
+    }
+    // density gradients of this chunk into the group's block
+    for (int q = 0; q < nl; ++q) {
+      const uint2 e = lload[q];
+      if (e.x == sink) continue;
+      Pg[int64_t(e.y) * ldp] += lds_at<Real>(gsb, e.x);
+    }
+  }
+}
+
+// gA[s * a_width + col] = sum over groups g (in order) of P[g][col][s], through
+// 64 x 64 LDS tiles (P is column-major, gA row-major).
+template <typename Real>
+__global__ __launch_bounds__(256) void stream_adjoint_reduce_kernel(const Real* __restrict__ P, int64_t groups,
+                                                                    int64_t a_width, int64_t ldp, int64_t samples,
+                                                                    Real* __restrict__ gA) {
+  __shared__ Real t[64][65];
+  const int64_t c0 = int64_t(blockIdx.x) * 64, s0 = int64_t(blockIdx.y) * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int k = ty; k < 64; k += 4) {
+    const int64_t col = c0 + k, s = s0 + tx;
+    Real v = Real(0);
+    if (col < a_width && s < ldp)
+      for (int64_t g = 0; g < groups; ++g) v += P[(g * a_width + col) * ldp + s];
+    t[k][tx] = v;
+  }
+  __syncthreads();
+  for (int k = ty; k < 64; k += 4) {
+    const int64_t s = s0 + k, col = c0 + tx;
+    if (s < samples && col < a_width) gA[s * a_width + col] = t[tx][k];
+  }
+}
+
+template <typename Real>
+__global__ __launch_bounds__(256) void fill_zero_kernel(Real* __restrict__ x, int64_t n) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+    x[i] = Real(0);
+}
+
 // At[c * ld + r] = A[r * cols + c] through 64 x 64 LDS tiles.
 template <typename Real>
 __global__ __launch_bounds__(256) void transpose_kernel(const Real* __restrict__ A, int64_t rows, int64_t cols,
@@ -569,9 +716,17 @@ bool build_stream(const ye3t_product_plan_desc* d, std::vector<uint4>& recs, std
         } else if (op == OP_ACC2) {
           emit(record(off(tw[i] & 0xFFFFu), off(tw[i] >> 16), cpos + i), flush);
         } else {
+          // the pair stays adjacent (the adjoint reads the chain record just
+          // before its partner): any hazard padding goes before both
           const uint32_t t0 = tw[2 * i], t1 = tw[2 * i + 1];
-          emit(record(off(t0 & 0xFFFFu), off(t0 >> 16), -1), kChain);
-          emit(record(off(t1 & 0xFFFFu), op == OP_ACC4 ? off(t1 >> 16) : one, cpos + i), kChained | flush);
+          const uint4 rc = record(off(t0 & 0xFFFFu), off(t0 >> 16), -1);
+          const uint4 rd = record(off(t1 & 0xFFFFu), op == OP_ACC4 ? off(t1 >> 16) : one, cpos + i);
+          bool hazard = false;
+          for (int k = 0; k < nflushed; ++k)
+            hazard |= (flushed[k] == rc.x || flushed[k] == rc.y || flushed[k] == rd.x || flushed[k] == rd.y);
+          if (hazard) pad_group();
+          emit(rc, kChain);
+          emit(rd, kChained | flush);
         }
       }
       wpos += 2 + int64_t((op == OP_ACC3 || op == OP_ACC4) ? 2 : 1) * n;
@@ -650,11 +805,110 @@ int launch_stream(const ye3t_hip_product_plan* p, const void* A, int64_t lda, in
   return check_launch("product_stream_kernel");
 }
 
+// Groups of chunks per tile for the stream adjoint (enough workgroups to fill
+// the device, partial blocks within 4 GiB) and the partial blocks' bytes.
+int64_t stream_adjoint_groups(const ye3t_hip_product_plan* p, int64_t samples, int64_t* bytes) {
+  const int64_t tiles = (samples + kLanes - 1) / kLanes;
+  const int64_t ldp = tiles * kLanes;
+  const int64_t per_group = p->a_width * ldp * (p->dtype == YE3T_F64 ? 8 : 4);
+  int64_t groups = (8 * 256 * 6 + tiles - 1) / tiles;
+  if (groups > p->chunk_count) groups = p->chunk_count;
+  const int64_t cap = int64_t(4) << 30;
+  if (groups * per_group > cap) groups = cap / per_group;
+  if (groups < 1) groups = 1;
+  if (bytes) *bytes = groups * per_group;
+  return groups;
+}
+
+template <bool COLUMNS>
+int launch_stream_adjoint(const ye3t_hip_product_plan* p, const void* A, int64_t lda, const void* gB,
+                          int64_t samples, void* P, int64_t groups, void* gA, hipStream_t s) {
+  const int64_t tiles = (samples + kLanes - 1) / kLanes;
+  const int64_t ldp = tiles * kLanes;
+  const size_t elem = p->dtype == YE3T_F64 ? 8 : 4;
+  const int64_t nP = groups * p->a_width * ldp;
+  const unsigned fill_grid = unsigned(std::min<int64_t>((nP + 255) / 256, 65536));
+  StreamLayout lay;
+  lay.ws_bytes = p->stream_layout[0];
+  lay.rec_at = p->stream_layout[1];
+  lay.flag_at = p->stream_layout[2];
+  lay.load_at = p->stream_layout[3];
+  lay.out_at = p->stream_layout[4];
+  lay.one_off = p->stream_layout[5];
+  const size_t lds = size_t(p->stream_lds) + lay.ws_bytes;
+  const int64_t grid = tiles * groups;
+  YE3T_REQUIRE(grid <= int64_t(0x7FFFFFFF), "too many samples for one launch");
+  const dim3 rgrid = dim3(unsigned((p->a_width + 63) / 64), unsigned((samples + 63) / 64), 1u);
+  YE3T_REQUIRE((samples + 63) / 64 <= 65535, "too many samples for one launch");
+  if (p->dtype == YE3T_F64) {
+    hipLaunchKernelGGL(fill_zero_kernel<double>, dim3(fill_grid), dim3(256), 0, s, (double*)P, nP);
+    if (p->out_dtype == YE3T_F64)
+      hipLaunchKernelGGL((product_stream_adjoint_kernel<double, double, COLUMNS>), dim3(unsigned(grid)), dim3(kLanes),
+                         lds, s, (const double*)A, lda, samples, (const double*)gB, p->feature_count, p->recs,
+                         p->flags, p->rec_off, p->loads, p->load_off, p->out_slots, p->out_off, p->first_col,
+                         p->chunk_count, groups, lay, (double*)P, p->a_width, ldp);
+    else
+      hipLaunchKernelGGL((product_stream_adjoint_kernel<double, float, COLUMNS>), dim3(unsigned(grid)), dim3(kLanes),
+                         lds, s, (const double*)A, lda, samples, (const float*)gB, p->feature_count, p->recs,
+                         p->flags, p->rec_off, p->loads, p->load_off, p->out_slots, p->out_off, p->first_col,
+                         p->chunk_count, groups, lay, (double*)P, p->a_width, ldp);
+    hipLaunchKernelGGL(stream_adjoint_reduce_kernel<double>, rgrid, dim3(256), 0, s, (const double*)P, groups,
+                       p->a_width, ldp, samples, (double*)gA);
+  } else {
+    hipLaunchKernelGGL(fill_zero_kernel<float>, dim3(fill_grid), dim3(256), 0, s, (float*)P, nP);
+    hipLaunchKernelGGL((product_stream_adjoint_kernel<float, float, COLUMNS>), dim3(unsigned(grid)), dim3(kLanes),
+                       lds, s, (const float*)A, lda, samples, (const float*)gB, p->feature_count, p->recs,
+                       p->flags, p->rec_off, p->loads, p->load_off, p->out_slots, p->out_off, p->first_col,
+                       p->chunk_count, groups, lay, (float*)P, p->a_width, ldp);
+    hipLaunchKernelGGL(stream_adjoint_reduce_kernel<float>, rgrid, dim3(256), 0, s, (const float*)P, groups,
+                       p->a_width, ldp, samples, (float*)gA);
+  }
+  (void)elem;
+  return check_launch("product_stream_adjoint_kernel");
+}
+
 }  // namespace ye3t
 
 using namespace ye3t;
 
 extern "C" {
+
+int64_t ye3t_hip_product_adjoint_workspace_bytes(const ye3t_hip_product_plan* p, int64_t samples) {
+  clear_error();
+  if (!p || samples < 0) {
+    set_error(YE3T_EINVAL, "NULL plan or negative sample count");
+    return -1;
+  }
+  if (!p->use_stream || samples == 0) return 0;
+  int64_t bytes = 0;
+  stream_adjoint_groups(p, samples, &bytes);
+  return bytes;
+}
+
+int ye3t_hip_product_adjoint_stream(const ye3t_hip_product_plan* p, const void* A, int64_t lda, int columns,
+                                    const void* gB, int64_t samples, void* workspace, int64_t workspace_bytes,
+                                    void* gA, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(p != nullptr, "NULL plan");
+  YE3T_REQUIRE(samples >= 0, "negative sample count");
+  if (samples == 0) return YE3T_OK;
+  YE3T_REQUIRE(p->use_stream, "this plan has no term stream (workspace too large)");
+  YE3T_REQUIRE(A && gB && gA, "NULL input or output");
+  const int64_t tiles = (samples + kLanes - 1) / kLanes;
+  if (columns) {
+    YE3T_REQUIRE(lda >= tiles * kLanes, "lda must cover whole 64-sample tiles");
+  } else {
+    YE3T_REQUIRE(lda == p->a_width, "a row-major density has lda == a_width");
+  }
+  int64_t need = 0;
+  const int64_t groups = stream_adjoint_groups(p, samples, &need);
+  YE3T_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace of %lld bytes needed", (long long)need);
+  YE3T_REQUIRE(p->stream_lds + int64_t(p->stream_layout[0]) <= 64 * 1024,
+               "the adjoint's values, gradients and program exceed 64 KB of LDS");
+  const hipStream_t s = as_stream(stream);
+  return columns ? launch_stream_adjoint<true>(p, A, lda, gB, samples, workspace, groups, gA, s)
+                 : launch_stream_adjoint<false>(p, A, lda, gB, samples, workspace, groups, gA, s);
+}
 
 int ye3t_hip_transpose(int dtype, const void* A, int64_t rows, int64_t cols, void* At, int64_t ld,
                        ye3t_stream_t stream) {

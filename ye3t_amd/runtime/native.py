@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 49
+ABI_VERSION = 50
 _LIB = None
 
 F32, F64 = 0, 1
@@ -96,6 +96,9 @@ def lib():
     L.ye3t_hip_transpose.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _i64, _vp]
     L.ye3t_hip_product_forward_columns.argtypes = [_vp, _vp, _i64, _i64, _vp, _vp]
     L.ye3t_hip_product_plan_uses_stream.argtypes = [_vp]
+    L.ye3t_hip_product_adjoint_workspace_bytes.argtypes = [_vp, _i64]
+    L.ye3t_hip_product_adjoint_workspace_bytes.restype = _i64
+    L.ye3t_hip_product_adjoint_stream.argtypes = [_vp, _vp, _i64, ctypes.c_int, _vp, _i64, _vp, _i64, _vp, _vp]
     L.ye3t_hip_neighbor_workspace_bytes.argtypes = [_i64, ctypes.POINTER(CellGrid)]
     L.ye3t_hip_neighbor_workspace_bytes.restype = _i64
     L.ye3t_hip_neighbor_count.argtypes = [ctypes.c_int, _vp, _i64, ctypes.POINTER(CellGrid), ctypes.c_double, _vp,
@@ -120,6 +123,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_rows_dot", "ye3t_hip_product_plan_attach_adjoint", "ye3t_hip_product_adjoint",
     "ye3t_hip_neighbor_workspace_bytes", "ye3t_hip_neighbor_count", "ye3t_hip_neighbor_fill",
     "ye3t_hip_transpose", "ye3t_hip_product_forward_columns", "ye3t_hip_product_plan_uses_stream",
+    "ye3t_hip_product_adjoint_workspace_bytes", "ye3t_hip_product_adjoint_stream",
 )
 
 
@@ -462,6 +466,41 @@ class ProductPlanHandle:
             raise ValueError("out has the wrong shape or dtype")
         _check(lib().ye3t_hip_product_forward_columns(self._handle, _dev(At, "At"), ld, S, _dev(out, "B"),
                                                       _stream()), "ye3t_hip_product_forward_columns")
+        return out
+
+    def adjoint_stream(self, A, gB, samples=None, columns=False, out=None):
+        """``gA[s] = J(A[s])^T gB[s]`` by the term-stream interpreter's reverse mode:
+        ``A`` row-major ``[samples, a_width]`` or, with ``columns``, column-major
+        ``[a_width, ld]``; returns row-major ``gA`` in the plan's dtype."""
+        import torch
+
+        want = torch.float64 if self.dtype == "f64" else torch.float32
+        g_t = torch.float64 if self.out_dtype == "f64" else torch.float32
+        W = int(self.program["a_width"])
+        if A.dtype != want:
+            raise ValueError(f"A must be {want} for this plan")
+        if columns:
+            if A.ndim != 2 or int(A.shape[0]) != W:
+                raise ValueError(f"A must be [{W}, ld]")
+            S, lda = int(samples), int(A.shape[1])
+        else:
+            if A.ndim != 2 or int(A.shape[1]) != W:
+                raise ValueError(f"A must be [samples, {W}]")
+            S, lda = int(A.shape[0]), W
+        if gB.dtype != g_t or tuple(gB.shape) != (S, self.feature_count):
+            raise ValueError(f"gB must be {g_t} [{S}, {self.feature_count}]")
+        if out is None:
+            out = torch.empty((S, W), dtype=want, device=A.device)
+        elif tuple(out.shape) != (S, W) or out.dtype != want:
+            raise ValueError("out has the wrong shape or dtype")
+        L = lib()
+        nbytes = int(L.ye3t_hip_product_adjoint_workspace_bytes(self._handle, S))
+        if nbytes < 0:
+            _check(-1, "ye3t_hip_product_adjoint_workspace_bytes")
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=A.device)
+        _check(L.ye3t_hip_product_adjoint_stream(self._handle, _dev(A, "A"), lda, 1 if columns else 0,
+                                                 _dev(gB, "gB"), S, _dev(ws, "workspace"), nbytes, _dev(out, "gA"),
+                                                 _stream()), "ye3t_hip_product_adjoint_stream")
         return out
 
     def attach_readout(self, source, meta):
