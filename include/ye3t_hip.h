@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 50 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 51 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -298,6 +298,20 @@ int ye3t_hip_product_forward_columns(const ye3t_hip_product_plan* plan, const vo
 /* Select which kernel product_forward launches: 0 = generated (if attached),
  * 1 = generic interpreter. */
 int ye3t_hip_product_plan_select(ye3t_hip_product_plan* plan, int use_interpreter);
+
+/* Host only (no device work): the term stream a plan description would run.
+ * counts[3] = (records, loads, chunks), all 0 when the plan gets no term
+ * stream.  Called with NULL arrays first to size them, then with
+ * recs[4 * records] (factor a LDS byte offset, factor b, coefficient words),
+ * flags[records] (flags | destination byte offset << 16; flags 1 = flush,
+ * 2 = chain, 4 = chained), rec_off[chunks + 1], loads[2 * loads] (LDS byte
+ * offset, density column), load_off[chunks + 1] and layout[8] (workspace
+ * bytes, record, flag, load and output-slot offsets, byte offset of the slot
+ * holding 1, LDS bytes, records per group).  For inspection and tests; no
+ * reference counterpart. */
+int ye3t_hip_product_stream_encode(const ye3t_product_plan_desc* desc, int64_t* counts, uint32_t* recs,
+                                   uint32_t* flags, int64_t* rec_off, uint32_t* loads, int64_t* load_off,
+                                   int64_t* layout);
 
 /* Device workspace bytes of ye3t_hip_product_adjoint_stream for `samples`
  * samples (0 for plans without a term stream; -1 on invalid input). */

@@ -867,11 +867,105 @@ int launch_stream_adjoint(const ye3t_hip_product_plan* p, const void* A, int64_t
   return check_launch("product_stream_adjoint_kernel");
 }
 
+// Host-side validation of every index a plan's kernels will use.
+int validate_plan_desc(const ye3t_product_plan_desc* d) {
+  YE3T_REQUIRE(d != nullptr, "NULL plan description");
+  YE3T_REQUIRE(d->dtype == YE3T_F32 || d->dtype == YE3T_F64, "unsupported dtype %d", d->dtype);
+  const int out_dtype = d->out_dtype < 0 ? d->dtype : d->out_dtype;
+  YE3T_REQUIRE(out_dtype == d->dtype || (d->dtype == YE3T_F64 && out_dtype == YE3T_F32),
+               "unsupported output dtype %d for a plan of dtype %d", d->out_dtype, d->dtype);
+  (void)out_dtype;
+  YE3T_REQUIRE(d->chunk_count >= 1 && d->a_width >= 1 && d->a_width <= 65536 && d->feature_count >= 1,
+               "bad plan sizes");
+  YE3T_REQUIRE(d->workspace_slots >= 1 && d->workspace_slots <= 65535, "bad workspace size");
+  const size_t elem = d->dtype == YE3T_F64 ? 8 : 4;
+  const size_t lds = size_t(d->workspace_slots) * kPad * elem;
+  YE3T_REQUIRE(lds <= 64 * 1024, "plan workspace needs %zu bytes of LDS (limit 65536)", lds);
+  // host-side validation of every index the kernel will use
+  const int64_t C = d->chunk_count;
+  YE3T_REQUIRE(d->chunk_word_offsets[0] == 0 && d->chunk_word_offsets[C] == d->word_count, "word offsets");
+  YE3T_REQUIRE(d->chunk_coeff_offsets[0] == 0 && d->chunk_coeff_offsets[C] == d->coeff_count, "coeff offsets");
+  YE3T_REQUIRE(d->chunk_out_offsets[0] == 0 && d->chunk_out_offsets[C] == d->out_slot_count, "out offsets");
+  for (int64_t c = 0; c < C; ++c) {
+    int64_t wpos = d->chunk_word_offsets[c];
+    const int64_t wend = d->chunk_word_offsets[c + 1];
+    int64_t cpos = d->chunk_coeff_offsets[c];
+    YE3T_REQUIRE(wpos <= wend, "word offsets not monotone");
+    while (wpos < wend) {
+      const uint32_t h = d->words[wpos];
+      const uint32_t op = h >> 28, n = h & 0x00FFFFFFu;
+      if (op == OP_LOAD) {
+        YE3T_REQUIRE(wpos + 1 + int64_t(n) <= wend, "chunk %lld: LOAD overruns", (long long)c);
+        for (uint32_t i = 0; i < n; ++i) {
+          const uint32_t t = d->words[wpos + 1 + i];
+          YE3T_REQUIRE(int64_t(t >> 16) < d->workspace_slots && int64_t(t & 0xFFFFu) < d->a_width,
+                       "chunk %lld: LOAD index out of range", (long long)c);
+        }
+        wpos += 1 + n;
+        continue;
+      }
+      YE3T_REQUIRE(op >= OP_ACC1 && op <= OP_ACC4, "chunk %lld: bad opcode %u", (long long)c, op);
+      const int per = (op == OP_ACC3 || op == OP_ACC4) ? 2 : 1;
+      YE3T_REQUIRE(wpos + 2 + int64_t(per) * n <= wend, "chunk %lld: op overruns", (long long)c);
+      YE3T_REQUIRE(int64_t(d->words[wpos + 1]) < d->workspace_slots, "chunk %lld: bad dst", (long long)c);
+      for (uint32_t i = 0; i < per * n; ++i) {
+        const uint32_t t = d->words[wpos + 2 + i];
+        const bool hi_used = !(op == OP_ACC1) && !(op == OP_ACC3 && (i % 2) == 1);
+        YE3T_REQUIRE(int64_t(t & 0xFFFFu) < d->workspace_slots, "chunk %lld: bad operand", (long long)c);
+        if (hi_used) YE3T_REQUIRE(int64_t(t >> 16) < d->workspace_slots, "chunk %lld: bad operand", (long long)c);
+      }
+      wpos += 2 + int64_t(per) * n;
+      cpos += n;
+    }
+    YE3T_REQUIRE(cpos == d->chunk_coeff_offsets[c + 1], "chunk %lld: coefficient count mismatch", (long long)c);
+    const int64_t o0 = d->chunk_out_offsets[c], o1 = d->chunk_out_offsets[c + 1];
+    YE3T_REQUIRE(d->chunk_first_column[c] >= 0 && d->chunk_first_column[c] + (o1 - o0) <= d->feature_count,
+                 "chunk %lld: output columns out of range", (long long)c);
+    for (int64_t o = o0; o < o1; ++o)
+      YE3T_REQUIRE(int64_t(d->out_slots[o]) < d->workspace_slots, "chunk %lld: bad out slot", (long long)c);
+  }
+  return YE3T_OK;
+}
+
 }  // namespace ye3t
 
 using namespace ye3t;
 
 extern "C" {
+
+int ye3t_hip_product_stream_encode(const ye3t_product_plan_desc* d, int64_t* counts, uint32_t* recs,
+                                   uint32_t* flags, int64_t* rec_off, uint32_t* loads, int64_t* load_off,
+                                   int64_t* layout) {
+  clear_error();
+  YE3T_REQUIRE(counts != nullptr, "NULL counts");
+  int rc = validate_plan_desc(d);
+  if (rc != YE3T_OK) return rc;
+  std::vector<uint4> r;
+  std::vector<uint32_t> f;
+  std::vector<uint2> l;
+  std::vector<int64_t> ro, lo;
+  StreamLayout lay{};
+  int64_t lds = 0;
+  if (!build_stream(d, r, f, ro, l, lo, lay, lds)) {
+    counts[0] = counts[1] = counts[2] = 0;
+    return YE3T_OK;  // no term stream for this plan
+  }
+  // the arrays keep one padding record / load when a plan has none
+  const int64_t nrec = ro.back(), nload = lo.back();
+  counts[0] = nrec;
+  counts[1] = nload;
+  counts[2] = d->chunk_count;
+  if (recs) std::memcpy(recs, r.data(), sizeof(uint4) * size_t(nrec));
+  if (flags) std::memcpy(flags, f.data(), sizeof(uint32_t) * size_t(nrec));
+  if (rec_off) std::memcpy(rec_off, ro.data(), sizeof(int64_t) * ro.size());
+  if (loads) std::memcpy(loads, l.data(), sizeof(uint2) * size_t(nload));
+  if (load_off) std::memcpy(load_off, lo.data(), sizeof(int64_t) * lo.size());
+  if (layout) {
+    const int64_t v[8] = {lay.ws_bytes, lay.rec_at, lay.flag_at, lay.load_at, lay.out_at, lay.one_off, lds, kGroup};
+    std::memcpy(layout, v, sizeof(v));
+  }
+  return YE3T_OK;
+}
 
 int64_t ye3t_hip_product_adjoint_workspace_bytes(const ye3t_hip_product_plan* p, int64_t samples) {
   clear_error();
@@ -972,59 +1066,13 @@ int ye3t_hip_product_plan_create(const ye3t_product_plan_desc* d, ye3t_hip_produ
   clear_error();
   YE3T_REQUIRE(d && out, "NULL plan description or output");
   *out = nullptr;
-  YE3T_REQUIRE(d->dtype == YE3T_F32 || d->dtype == YE3T_F64, "unsupported dtype %d", d->dtype);
-  const int out_dtype = d->out_dtype < 0 ? d->dtype : d->out_dtype;
-  YE3T_REQUIRE(out_dtype == d->dtype || (d->dtype == YE3T_F64 && out_dtype == YE3T_F32),
-               "unsupported output dtype %d for a plan of dtype %d", d->out_dtype, d->dtype);
-  YE3T_REQUIRE(d->chunk_count >= 1 && d->a_width >= 1 && d->a_width <= 65536 && d->feature_count >= 1,
-               "bad plan sizes");
-  YE3T_REQUIRE(d->workspace_slots >= 1 && d->workspace_slots <= 65535, "bad workspace size");
-  const size_t elem = d->dtype == YE3T_F64 ? 8 : 4;
-  const size_t lds = size_t(d->workspace_slots) * kPad * elem;
-  YE3T_REQUIRE(lds <= 64 * 1024, "plan workspace needs %zu bytes of LDS (limit 65536)", lds);
-  // host-side validation of every index the kernel will use
-  const int64_t C = d->chunk_count;
-  YE3T_REQUIRE(d->chunk_word_offsets[0] == 0 && d->chunk_word_offsets[C] == d->word_count, "word offsets");
-  YE3T_REQUIRE(d->chunk_coeff_offsets[0] == 0 && d->chunk_coeff_offsets[C] == d->coeff_count, "coeff offsets");
-  YE3T_REQUIRE(d->chunk_out_offsets[0] == 0 && d->chunk_out_offsets[C] == d->out_slot_count, "out offsets");
-  for (int64_t c = 0; c < C; ++c) {
-    int64_t wpos = d->chunk_word_offsets[c];
-    const int64_t wend = d->chunk_word_offsets[c + 1];
-    int64_t cpos = d->chunk_coeff_offsets[c];
-    YE3T_REQUIRE(wpos <= wend, "word offsets not monotone");
-    while (wpos < wend) {
-      const uint32_t h = d->words[wpos];
-      const uint32_t op = h >> 28, n = h & 0x00FFFFFFu;
-      if (op == OP_LOAD) {
-        YE3T_REQUIRE(wpos + 1 + int64_t(n) <= wend, "chunk %lld: LOAD overruns", (long long)c);
-        for (uint32_t i = 0; i < n; ++i) {
-          const uint32_t t = d->words[wpos + 1 + i];
-          YE3T_REQUIRE(int64_t(t >> 16) < d->workspace_slots && int64_t(t & 0xFFFFu) < d->a_width,
-                       "chunk %lld: LOAD index out of range", (long long)c);
-        }
-        wpos += 1 + n;
-        continue;
-      }
-      YE3T_REQUIRE(op >= OP_ACC1 && op <= OP_ACC4, "chunk %lld: bad opcode %u", (long long)c, op);
-      const int per = (op == OP_ACC3 || op == OP_ACC4) ? 2 : 1;
-      YE3T_REQUIRE(wpos + 2 + int64_t(per) * n <= wend, "chunk %lld: op overruns", (long long)c);
-      YE3T_REQUIRE(int64_t(d->words[wpos + 1]) < d->workspace_slots, "chunk %lld: bad dst", (long long)c);
-      for (uint32_t i = 0; i < per * n; ++i) {
-        const uint32_t t = d->words[wpos + 2 + i];
-        const bool hi_used = !(op == OP_ACC1) && !(op == OP_ACC3 && (i % 2) == 1);
-        YE3T_REQUIRE(int64_t(t & 0xFFFFu) < d->workspace_slots, "chunk %lld: bad operand", (long long)c);
-        if (hi_used) YE3T_REQUIRE(int64_t(t >> 16) < d->workspace_slots, "chunk %lld: bad operand", (long long)c);
-      }
-      wpos += 2 + int64_t(per) * n;
-      cpos += n;
-    }
-    YE3T_REQUIRE(cpos == d->chunk_coeff_offsets[c + 1], "chunk %lld: coefficient count mismatch", (long long)c);
-    const int64_t o0 = d->chunk_out_offsets[c], o1 = d->chunk_out_offsets[c + 1];
-    YE3T_REQUIRE(d->chunk_first_column[c] >= 0 && d->chunk_first_column[c] + (o1 - o0) <= d->feature_count,
-                 "chunk %lld: output columns out of range", (long long)c);
-    for (int64_t o = o0; o < o1; ++o)
-      YE3T_REQUIRE(int64_t(d->out_slots[o]) < d->workspace_slots, "chunk %lld: bad out slot", (long long)c);
+  {
+    const int rc = validate_plan_desc(d);
+    if (rc != YE3T_OK) return rc;
   }
+  const int out_dtype = d->out_dtype < 0 ? d->dtype : d->out_dtype;
+  const size_t elem = d->dtype == YE3T_F64 ? 8 : 4;
+  const int64_t C = d->chunk_count;
   auto* p = new ye3t_hip_product_plan();
   p->dtype = d->dtype;
   p->out_dtype = out_dtype;

@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 50
+ABI_VERSION = 51
 _LIB = None
 
 F32, F64 = 0, 1
@@ -96,6 +96,7 @@ def lib():
     L.ye3t_hip_transpose.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _i64, _vp]
     L.ye3t_hip_product_forward_columns.argtypes = [_vp, _vp, _i64, _i64, _vp, _vp]
     L.ye3t_hip_product_plan_uses_stream.argtypes = [_vp]
+    L.ye3t_hip_product_stream_encode.argtypes = [ctypes.POINTER(ProductPlanDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     L.ye3t_hip_product_adjoint_workspace_bytes.argtypes = [_vp, _i64]
     L.ye3t_hip_product_adjoint_workspace_bytes.restype = _i64
     L.ye3t_hip_product_adjoint_stream.argtypes = [_vp, _vp, _i64, ctypes.c_int, _vp, _i64, _vp, _i64, _vp, _vp]
@@ -123,7 +124,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_rows_dot", "ye3t_hip_product_plan_attach_adjoint", "ye3t_hip_product_adjoint",
     "ye3t_hip_neighbor_workspace_bytes", "ye3t_hip_neighbor_count", "ye3t_hip_neighbor_fill",
     "ye3t_hip_transpose", "ye3t_hip_product_forward_columns", "ye3t_hip_product_plan_uses_stream",
-    "ye3t_hip_product_adjoint_workspace_bytes", "ye3t_hip_product_adjoint_stream",
+    "ye3t_hip_product_adjoint_workspace_bytes", "ye3t_hip_product_adjoint_stream", "ye3t_hip_product_stream_encode",
 )
 
 
@@ -357,6 +358,53 @@ def rtc_compile(source, name="ye3t_generated.hip", arch="gfx950"):
     return blob
 
 
+def _plan_desc(program, out_dtype):
+    """``ye3t_product_plan_desc`` of a compiled program and the arrays it points into."""
+    keep = {k: np.ascontiguousarray(v) for k, v in program.items() if isinstance(v, np.ndarray)}
+
+    def ptr(name):
+        return ctypes.c_void_p(keep[name].ctypes.data) if keep[name].size else None
+
+    desc = ProductPlanDesc(
+        dtype=F64 if program["dtype"] == "f64" else F32, a_width=program["a_width"],
+        feature_count=program["feature_count"], chunk_count=program["chunk_count"],
+        workspace_slots=program["workspace_slots"], chunk_word_offsets=ptr("chunk_word_offsets"),
+        chunk_coeff_offsets=ptr("chunk_coeff_offsets"), chunk_out_offsets=ptr("chunk_out_offsets"),
+        chunk_first_column=ptr("chunk_first_column"), words=ptr("words"), word_count=int(keep["words"].size),
+        coeffs=ptr("coeffs"), coeff_count=int(keep["coeffs"].size), out_slots=ptr("out_slots"),
+        out_slot_count=int(keep["out_slots"].size), out_dtype=F64 if out_dtype == "f64" else F32)
+    return desc, keep
+
+
+def stream_encode(program):
+    """The term stream the device interpreter would run for ``program`` (host
+    only): dict of records ``[R, 4]`` uint32, flags ``[R]``, rec_off, loads
+    ``[L, 2]``, load_off and layout; ``None`` when the plan gets no term stream."""
+    L = lib()
+    desc, keep = _plan_desc(program, program["dtype"])
+    counts = np.zeros(3, dtype=np.int64)
+    vp = ctypes.c_void_p
+    _check(L.ye3t_hip_product_stream_encode(ctypes.byref(desc), vp(counts.ctypes.data), None, None, None, None,
+                                            None, None), "ye3t_hip_product_stream_encode")
+    nrec, nload, chunks = (int(x) for x in counts)
+    if chunks == 0:
+        return None
+    recs = np.zeros((nrec, 4), dtype=np.uint32)
+    flags = np.zeros(nrec, dtype=np.uint32)
+    rec_off = np.zeros(chunks + 1, dtype=np.int64)
+    loads = np.zeros((nload, 2), dtype=np.uint32)
+    load_off = np.zeros(chunks + 1, dtype=np.int64)
+    layout = np.zeros(8, dtype=np.int64)
+    _check(L.ye3t_hip_product_stream_encode(ctypes.byref(desc), vp(counts.ctypes.data), vp(recs.ctypes.data),
+                                            vp(flags.ctypes.data), vp(rec_off.ctypes.data), vp(loads.ctypes.data),
+                                            vp(load_off.ctypes.data), vp(layout.ctypes.data)),
+           "ye3t_hip_product_stream_encode")
+    del keep
+    names = ("ws_bytes", "rec_at", "flag_at", "load_at", "out_at", "one_off", "lds_bytes", "group")
+    return {"records": recs, "flags": flags, "rec_off": rec_off, "loads": loads, "load_off": load_off,
+            "layout": dict(zip(names, (int(x) for x in layout)))}
+
+
 class ProductPlanHandle:
     """Device-resident compiled product program (owns a ``ye3t_hip_product_plan``).
 
@@ -370,20 +418,7 @@ class ProductPlanHandle:
         self.out_dtype = out_dtype or self.dtype
         if self.out_dtype not in ("f32", "f64") or (self.dtype == "f32" and self.out_dtype == "f64"):
             raise ValueError(f"unsupported output dtype {self.out_dtype!r} for a {self.dtype} plan")
-        self._keep = {k: np.ascontiguousarray(v) for k, v in program.items() if isinstance(v, np.ndarray)}
-        k = self._keep
-
-        def ptr(name):
-            return ctypes.c_void_p(k[name].ctypes.data) if k[name].size else None
-
-        desc = ProductPlanDesc(
-            dtype=F64 if self.dtype == "f64" else F32, a_width=program["a_width"],
-            feature_count=program["feature_count"], chunk_count=program["chunk_count"],
-            workspace_slots=program["workspace_slots"], chunk_word_offsets=ptr("chunk_word_offsets"),
-            chunk_coeff_offsets=ptr("chunk_coeff_offsets"), chunk_out_offsets=ptr("chunk_out_offsets"),
-            chunk_first_column=ptr("chunk_first_column"), words=ptr("words"), word_count=int(k["words"].size),
-            coeffs=ptr("coeffs"), coeff_count=int(k["coeffs"].size), out_slots=ptr("out_slots"),
-            out_slot_count=int(k["out_slots"].size), out_dtype=F64 if self.out_dtype == "f64" else F32)
+        desc, self._keep = _plan_desc(program, self.out_dtype)
         handle = ctypes.c_void_p()
         _check(lib().ye3t_hip_product_plan_create(ctypes.byref(desc), ctypes.byref(handle)),
                "ye3t_hip_product_plan_create")
