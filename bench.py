@@ -96,12 +96,19 @@ def cpu_baseline(cfg, pipe, target_seconds=10.0):
                       f"stage2 {s2:.2f}s (OpenMP over samples, {threads} threads)"}
 
 
-def _time_kernel(fn, steps, warmup):
-    """Mean wall time per call of ``fn`` (device-resident inputs, K back-to-back calls)."""
+def _time_kernel(fn, steps, warmup, min_warmup_s=0.25):
+    """Mean wall time per call of ``fn`` (device-resident inputs, K back-to-back
+    calls), after ``warmup`` calls and at least ``min_warmup_s`` of them (the
+    GPU's clocks ramp up over the first ~0.1 s of work)."""
     import torch
 
-    for _ in range(warmup):
+    t0 = time.perf_counter()
+    done = 0
+    while done < warmup or time.perf_counter() - t0 < min_warmup_s:
         fn()
+        done += 1
+        if done % 16 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -255,8 +262,10 @@ def bench_op(args, cfg):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    # the GPU reaches its steady clocks only after ~0.1 s of work: 5 warmup steps
+    # time the ramp (config 4: 0.207 ms per step after 5, 0.171 ms after 200)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--config", type=int, default=4)
     ap.add_argument("--dtype", default=None, help="storage type of inputs and B-features (f32 / f64)")
     ap.add_argument("--accumulate", default=None, help="type of A and of the arithmetic (default per config)")
