@@ -200,6 +200,13 @@ __device__ inline Real& lds_at(unsigned char* base, uint32_t off) {
   return *reinterpret_cast<Real*>(base + off);
 }
 
+// LDS[base + off] += v as an LDS atomic add without return (ds_add_f32 /
+// ds_add_f64): the wave does not wait for a read-modify-write round trip
+template <typename Real>
+__device__ inline void lds_add(unsigned char* base, uint32_t off, Real v) {
+  __hip_atomic_fetch_add(reinterpret_cast<Real*>(base + off), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 struct StreamLayout {
   uint32_t ws_bytes;    // workspace: (slots + 2) * 64 * elem
   uint32_t rec_at;      // records (16 B each)
@@ -397,6 +404,10 @@ __global__ __launch_bounds__(kLanes) void product_stream_kernel(
 // into this workgroup's own block of P[group][col][s]; gA is the sum of the
 // groups in a fixed order (stream_adjoint_reduce_kernel), so no atomics and
 // the same bits every run.
+// global loads (density values, partial-block entries) in flight per batch
+// (16 measured slower than 8 at configs 2 and 3)
+constexpr int kAdjBatch = 8;
+
 template <typename Real, typename G, bool COLUMNS>
 __global__ __launch_bounds__(kLanes) void product_stream_adjoint_kernel(
     const Real* __restrict__ A, int64_t lda, int64_t samples, const G* __restrict__ gB, int64_t F,
@@ -440,61 +451,122 @@ __global__ __launch_bounds__(kLanes) void product_stream_adjoint_kernel(
     for (int i = lane; i < nf; i += kLanes) lout[i] = uint32_t(out_slots[o0 + i]) * pitch;
     __syncthreads();
     lds_at<Real>(wsb, lay.one_off) = Real(1);
-    for (int q = 0; q < nl; ++q) {
-      const uint2 e = lload[q];
-      lds_at<Real>(wsb, e.x) = COLUMNS ? src[int64_t(e.y) * lda] : src[e.y];
+    // density values, kAdjBatch loads in flight (nl is a multiple of 8;
+    // padding entries read a valid column into the sink slot)
+    for (int q = 0; q < nl; q += kAdjBatch) {
+      uint2 e[kAdjBatch];
+      Real v[kAdjBatch];
+#pragma unroll
+      for (int w = 0; w < kAdjBatch; ++w) e[w] = q + w < nl ? lload[q + w] : make_uint2(sink, 0u);
+#pragma unroll
+      for (int w = 0; w < kAdjBatch; ++w) v[w] = COLUMNS ? src[int64_t(e[w].y) * lda] : src[e[w].y];
+#pragma unroll
+      for (int w = 0; w < kAdjBatch; ++w) lds_at<Real>(wsb, e[w].x) = v[w];
     }
-    // forward replay
+    // forward replay, kGroup records at a time: no record of a group reads a
+    // slot flushed earlier in the group, so all its factors are read first
     Real acc = Real(0), p = Real(1);
-    for (int q = 0; q < nr; ++q) {
-      const uint32_t f = lflag[q];
-      const uint4 r = lrec[q];
-      const Real a = lds_at<Real>(wsb, r.x), b = lds_at<Real>(wsb, r.y);
-      if (f & kChain) {
-        p = a * b;
-        continue;
+    for (int q0 = 0; q0 < nr; q0 += kGroup) {
+      uint32_t f[kGroup];
+      uint4 r[kGroup];
+      Real a[kGroup], b[kGroup];
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        f[u] = uint32_t(__builtin_amdgcn_readfirstlane(int(lflag[q0 + u])));
+        r[u] = lrec[q0 + u];
       }
-      const Real t = (f & kChained) ? (p * a) * b : a * b;
-      acc = d_fma(record_coeff<Real>(r), t, acc);
-      if (f & kFlush) {
-        lds_at<Real>(wsb, f >> 16) = acc;
-        acc = Real(0);
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        a[u] = lds_at<Real>(wsb, r[u].x);
+        b[u] = lds_at<Real>(wsb, r[u].y);
+      }
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        if (f[u] & kChain) {
+          p = a[u] * b[u];
+          continue;
+        }
+        const Real t = (f[u] & kChained) ? (p * a[u]) * b[u] : a[u] * b[u];
+        acc = d_fma(record_coeff<Real>(r[u]), t, acc);
+        if (f[u] & kFlush) {
+          lds_at<Real>(wsb, f[u] >> 16) = acc;
+          acc = Real(0);
+        }
       }
     }
     // gradient workspace: zero, then the chunk's feature gradients
     for (uint32_t k = 0; k < ws_slots; ++k) lds_at<Real>(gsb, k * pitch) = Real(0);
     const int64_t c0 = first_col[chunk];
-    for (int c = 0; c < nf; ++c) {
-      const Real gv = valid ? Real(gB[s * F + c0 + c]) : Real(0);
-      lds_at<Real>(gsb, lout[c]) += gv;
+    for (int c = 0; c < nf; c += 8) {
+      Real gv[8];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) gv[w] = (valid && c + w < nf) ? Real(gB[s * F + c0 + c + w]) : Real(0);
+#pragma unroll
+      for (int w = 0; w < 8; ++w)
+        if (c + w < nf) lds_add<Real>(gsb, lout[c + w], gv[w]);
     }
-    // reverse sweep
+    // reverse sweep, a group at a time.  The node values are not written here,
+    // so a group's factors are read at once; gradients are added by LDS atomic
+    // adds without return (each lane owns its column, and one wave's LDS
+    // operations take effect in order, so a later read of g sees every add
+    // before it and the sums are the same every run).
     Real g = Real(0);
-    for (int q = nr - 1; q >= 0; --q) {
-      const uint32_t f = lflag[q];
-      if (f & kChain) continue;  // consumed with its chained partner
-      if (f & kFlush) g = lds_at<Real>(gsb, f >> 16);
-      const uint4 r = lrec[q];
-      const Real a = lds_at<Real>(wsb, r.x), b = lds_at<Real>(wsb, r.y);
-      const Real cg = record_coeff<Real>(r) * g;
-      if (f & kChained) {
-        const uint4 rc = lrec[q - 1];  // the chain record precedes its partner
-        const Real a1 = lds_at<Real>(wsb, rc.x), b1 = lds_at<Real>(wsb, rc.y);
-        const Real pp = a1 * b1, ab = a * b;
-        lds_at<Real>(gsb, r.x) += cg * pp * b;
-        lds_at<Real>(gsb, r.y) += cg * pp * a;
-        lds_at<Real>(gsb, rc.x) += cg * ab * b1;
-        lds_at<Real>(gsb, rc.y) += cg * ab * a1;
-      } else {
-        lds_at<Real>(gsb, r.x) += cg * b;
-        lds_at<Real>(gsb, r.y) += cg * a;
+    for (int q0 = nr - kGroup; q0 >= 0; q0 -= kGroup) {
+      uint32_t f[kGroup];
+      uint4 r[kGroup];
+      Real a[kGroup], b[kGroup];
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        f[u] = uint32_t(__builtin_amdgcn_readfirstlane(int(lflag[q0 + u])));
+        r[u] = lrec[q0 + u];
+      }
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        a[u] = lds_at<Real>(wsb, r[u].x);
+        b[u] = lds_at<Real>(wsb, r[u].y);
+      }
+#pragma unroll
+      for (int u = kGroup - 1; u >= 0; --u) {
+        if (f[u] & kChain) continue;  // consumed with its chained partner
+        if (f[u] & kFlush) g = lds_at<Real>(gsb, f[u] >> 16);
+        const Real cg = record_coeff<Real>(r[u]) * g;
+        if (f[u] & kChained) {
+          // the chain record precedes its partner, in this group or at the
+          // end of the previous one
+          const uint4 rc = u > 0 ? r[u > 0 ? u - 1 : 0] : lrec[q0 - 1];
+          const Real a1 = u > 0 ? a[u > 0 ? u - 1 : 0] : lds_at<Real>(wsb, rc.x);
+          const Real b1 = u > 0 ? b[u > 0 ? u - 1 : 0] : lds_at<Real>(wsb, rc.y);
+          const Real pp = a1 * b1, ab = a[u] * b[u];
+          lds_add<Real>(gsb, r[u].x, cg * pp * b[u]);
+          lds_add<Real>(gsb, r[u].y, cg * pp * a[u]);
+          lds_add<Real>(gsb, rc.x, cg * ab * b1);
+          lds_add<Real>(gsb, rc.y, cg * ab * a1);
+        } else {
+          lds_add<Real>(gsb, r[u].x, cg * b[u]);
+          lds_add<Real>(gsb, r[u].y, cg * a[u]);
+        }
       }
     }
-    // density gradients of this chunk into the group's block
-    for (int q = 0; q < nl; ++q) {
-      const uint2 e = lload[q];
-      if (e.x == sink) continue;
-      Pg[int64_t(e.y) * ldp] += lds_at<Real>(gsb, e.x);
+    // density gradients of this chunk into the group's block, eight at a
+    // time (the encoder loads a column at most once per chunk, so the eight
+    // read-modify-writes touch distinct entries)
+    for (int q = 0; q < nl; q += kAdjBatch) {
+      uint32_t slot[kAdjBatch], col[kAdjBatch];
+      Real sum[kAdjBatch];
+#pragma unroll
+      for (int w = 0; w < kAdjBatch; ++w) {
+        const uint2 e = q + w < nl ? lload[q + w] : make_uint2(sink, 0u);
+        slot[w] = uint32_t(__builtin_amdgcn_readfirstlane(int(e.x)));
+        col[w] = uint32_t(__builtin_amdgcn_readfirstlane(int(e.y)));
+      }
+      // padding entries read column 0 and the sink slot, and store nothing
+#pragma unroll
+      for (int w = 0; w < kAdjBatch; ++w) sum[w] = Pg[int64_t(col[w]) * ldp];
+#pragma unroll
+      for (int w = 0; w < kAdjBatch; ++w) sum[w] += lds_at<Real>(gsb, slot[w]);
+#pragma unroll
+      for (int w = 0; w < kAdjBatch; ++w)
+        if (slot[w] != sink) Pg[int64_t(col[w]) * ldp] = sum[w];
     }
   }
 }
@@ -733,6 +805,14 @@ bool build_stream(const ye3t_product_plan_desc* d, std::vector<uint4>& recs, std
       cpos += n;
     }
     pad_group();
+    {
+      // the adjoint adds a chunk's density gradients eight loads at a time:
+      // a density column is loaded at most once per chunk
+      std::vector<uint32_t> cols;
+      for (int64_t i = load_off.back(); i < int64_t(loads.size()); ++i) cols.push_back(loads[size_t(i)].y);
+      std::sort(cols.begin(), cols.end());
+      if (std::adjacent_find(cols.begin(), cols.end()) != cols.end()) return false;
+    }
     while ((int64_t(loads.size()) - load_off.back()) % 8) loads.push_back(make_uint2(sink, 0));
     max_recs = std::max<int64_t>(max_recs, int64_t(recs.size()) - rec_off.back());
     max_loads = std::max<int64_t>(max_loads, int64_t(loads.size()) - load_off.back());
