@@ -583,8 +583,20 @@ __global__ __launch_bounds__(256) void stream_adjoint_reduce_kernel(const Real* 
   for (int k = ty; k < 64; k += 4) {
     const int64_t col = c0 + k, s = s0 + tx;
     Real v = Real(0);
-    if (col < a_width && s < ldp)
-      for (int64_t g = 0; g < groups; ++g) v += P[(g * a_width + col) * ldp + s];
+    if (col < a_width && s < ldp) {
+      // eight groups' loads in flight, added in group order
+      const Real* __restrict__ src = P + col * ldp + s;
+      const int64_t gstride = a_width * ldp;
+      int64_t g = 0;
+      for (; g + 8 <= groups; g += 8) {
+        Real x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = src[(g + u) * gstride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v += x[u];
+      }
+      for (; g < groups; ++g) v += src[g * gstride];
+    }
     t[k][tx] = v;
   }
   __syncthreads();
@@ -891,7 +903,9 @@ int64_t stream_adjoint_groups(const ye3t_hip_product_plan* p, int64_t samples, i
   const int64_t tiles = (samples + kLanes - 1) / kLanes;
   const int64_t ldp = tiles * kLanes;
   const int64_t per_group = p->a_width * ldp * (p->dtype == YE3T_F64 ? 8 : 4);
-  int64_t groups = (8 * 256 * 6 + tiles - 1) / tiles;
+  const char* wg = std::getenv("YE3T_ADJOINT_WORKGROUPS");
+  const int64_t target = (wg && *wg && std::atoll(wg) > 0) ? std::atoll(wg) : 8 * 256 * 6;
+  int64_t groups = (target + tiles - 1) / tiles;
   if (groups > p->chunk_count) groups = p->chunk_count;
   const int64_t cap = int64_t(4) << 30;
   if (groups * per_group > cap) groups = cap / per_group;
