@@ -402,8 +402,9 @@ __global__ __launch_bounds__(kLanes) void product_stream_kernel(
 // with g = G[destination], read when the sweep meets the record that flushed
 // it (its last term).  The density gradients of the chunk's loads are added
 // into this workgroup's own block of P[group][col][s]; gA is the sum of the
-// groups in a fixed order (stream_adjoint_reduce_kernel), so no atomics and
-// the same bits every run.
+// groups in a fixed order (stream_adjoint_reduce_kernel), so no global atomics
+// and the same bits every run (the sweep's LDS atomic adds touch only the
+// adding lane's own column, in program order).
 // global loads (density values, partial-block entries) in flight per batch
 // (16 measured slower than 8 at configs 2 and 3)
 constexpr int kAdjBatch = 8;
