@@ -180,3 +180,22 @@ def test_wide_workspaces_get_no_stream():
     prog = compile_program(plan, "f64", 120)
     assert (prog["workspace_slots"] + 2) * 64 * 8 > 56 * 1024
     assert native.stream_encode(prog) is None
+
+
+def test_a_chunk_that_loads_a_column_twice_gets_no_stream():
+    """The reverse mode adds a chunk's density gradients eight loads at a time,
+    which needs each density column loaded at most once per chunk: the encoder
+    refuses a program that breaks this (the plan then runs the word interpreter)."""
+    plan = ProductPlan(W.config(2).feature_spec)
+    prog = compile_program(plan, "f64")
+    assert native.stream_encode(prog) is not None
+    words = prog["words"].copy()
+    w0 = int(prog["chunk_word_offsets"][0])
+    assert words[w0] >> 28 == 1  # the chunk opens with its LOAD block
+    n = int(words[w0] & 0xFFFFFF)
+    assert n >= 2
+    first_col = int(words[w0 + 1]) & 0xFFFF
+    # the second load keeps its slot but reads the first load's column
+    words[w0 + 2] = (int(words[w0 + 2]) & 0xFFFF0000) | first_col
+    bad = dict(prog, words=words)
+    assert native.stream_encode(bad) is None
