@@ -322,11 +322,21 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # Per-kernel durations come from HIP events on one timed step in ten: an
+    # event record drains the queue between the two kernels (config 4: 0.167 ms
+    # per step with events on every step, 0.156 ms without), so the other
+    # steps run as a caller would run them.
+    every = 10 if args.steps >= 20 else 1
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+           torch.cuda.Event(enable_timing=True)) for _ in range(0, args.steps, every)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for e0, e1, e2 in ev:
+    for i in range(args.steps):
+        if i % every:
+            pipe.density(dev, out=A)
+            pipe.product(rows, out=B)
+            continue
+        e0, e1, e2 = ev[i // every]
         e0.record()
         pipe.density(dev, out=A)
         e1.record()
@@ -382,7 +392,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": b2 / s2 / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": b2 / s2 / 1e9 / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": k2,
-                     "algorithmic_bytes": b2, "avg_kernel_us": s2 * 1e6},
+                     "algorithmic_bytes": b2, "avg_kernel_us": s2 * 1e6, "event_steps": len(ev)},
         "stage1": {"kernel": k1, "avg_kernel_us": s1 * 1e6, "algorithmic_bytes": b1,
                    "achieved_gbs": b1 / s1 / 1e9, "frac": b1 / s1 / 1e9 / HBM_PEAK_GBS,
                    "traffic": traffic1, "traffic_source": traffic1_src},
