@@ -231,22 +231,20 @@ __global__ __launch_bounds__(kLanes) void product_stream_kernel(
   const int64_t tile0 = group * tiles_per_group;
   const int64_t tile_end = tile0 + tiles_per_group < tiles ? tile0 + tiles_per_group : tiles;
   unsigned char* wsb = smem_raw + lane * sizeof(Real);
-  uint4* lrec = reinterpret_cast<uint4*>(smem_raw + lay.rec_at);
-  uint32_t* lflag = reinterpret_cast<uint32_t*>(smem_raw + lay.flag_at);
   uint4* lload = reinterpret_cast<uint4*>(smem_raw + lay.load_at);
   uint32_t* lout = reinterpret_cast<uint32_t*>(smem_raw + lay.out_at);
 
-  // stage the chunk's program in LDS
+  // stage the chunk's loads and output slots in LDS; its records and flags are
+  // wave-uniform and are read through the scalar cache (no LDS for them)
   const int64_t r0 = rec_off[chunk];
   const int nr = int(rec_off[chunk + 1] - r0);
   const int64_t l0 = load_off[chunk];
   const int nl = int(load_off[chunk + 1] - l0);
   const int64_t o0 = out_off[chunk];
   const int nf = int(out_off[chunk + 1] - o0);
-  for (int i = lane; i < nr; i += kLanes) {
-    lrec[i] = recs[r0 + i];
-    lflag[i] = flags[r0 + i];
-  }
+  typedef const __attribute__((address_space(4))) uint32_t* scalar_u32;
+  const scalar_u32 grec = (scalar_u32)(const void*)(recs + r0);
+  const scalar_u32 gflag = (scalar_u32)(const void*)(flags + r0);
   // load entry i: (dst byte offset, element offset of its column: col * lda
   // column-major, col row-major) so a tile's load address is one add
   for (int i = lane; i < nl; i += kLanes) {
@@ -306,31 +304,27 @@ __global__ __launch_bounds__(kLanes) void product_stream_kernel(
     if (tile + 1 < tile_end) fetch(tile + 1, pre);
 
     // the term stream, kGroup records at a time; each group's records and flags
-    // are read one group ahead (the program region of LDS is not written here)
+    // are read (scalar loads) one group ahead
     Real acc = Real(0), p = Real(1);
-    uint4 fw_next[kGroup / 4];
+    uint32_t fw_next[kGroup];
     uint4 r_next[kGroup];
+    auto read_group = [&](int q) {
 #pragma unroll
-    for (int u = 0; u < kGroup / 4; ++u) fw_next[u] = *reinterpret_cast<const uint4*>(lflag + 4 * u);
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) r_next[u] = lrec[u];
+      for (int u = 0; u < kGroup; ++u) {
+        fw_next[u] = gflag[q + u];
+        r_next[u] = make_uint4(grec[4 * (q + u)], grec[4 * (q + u) + 1], grec[4 * (q + u) + 2], grec[4 * (q + u) + 3]);
+      }
+    };
+    read_group(0);
     for (int q = 0; q < nr; q += kGroup) {
       uint32_t f[kGroup];
-#pragma unroll
-      for (int u = 0; u < kGroup / 4; ++u) {
-        f[4 * u] = uint32_t(__builtin_amdgcn_readfirstlane(int(fw_next[u].x)));
-        f[4 * u + 1] = uint32_t(__builtin_amdgcn_readfirstlane(int(fw_next[u].y)));
-        f[4 * u + 2] = uint32_t(__builtin_amdgcn_readfirstlane(int(fw_next[u].z)));
-        f[4 * u + 3] = uint32_t(__builtin_amdgcn_readfirstlane(int(fw_next[u].w)));
-      }
       uint4 r[kGroup];
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) r[u] = r_next[u];
-      const int qn = q + kGroup < nr ? q + kGroup : q;
-#pragma unroll
-      for (int u = 0; u < kGroup / 4; ++u) fw_next[u] = *reinterpret_cast<const uint4*>(lflag + qn + 4 * u);
-#pragma unroll
-      for (int u = 0; u < kGroup; ++u) r_next[u] = lrec[qn + u];
+      for (int u = 0; u < kGroup; ++u) {
+        f[u] = fw_next[u];
+        r[u] = r_next[u];
+      }
+      read_group(q + kGroup < nr ? q + kGroup : q);
       // no record of a group reads a slot flushed earlier in the group: all its
       // factors are read before any of its stores
       Real a[kGroup], b[kGroup];
@@ -725,7 +719,7 @@ int upload(T** dst, const T* src, int64_t count) {
 
 size_t product_lds_bytes(const ye3t_hip_product_plan* p) {
   const size_t elem = p->dtype == YE3T_F64 ? 8 : 4;
-  return p->use_stream ? size_t(p->stream_lds) : size_t(p->slots) * kPad * elem;
+  return p->use_stream ? size_t(p->stream_layout[1]) : size_t(p->slots) * kPad * elem;
 }
 
 // Decode validated program words into the term stream of product_stream_kernel
@@ -841,14 +835,16 @@ bool build_stream(const ye3t_product_plan_desc* d, std::vector<uint4>& recs, std
   auto up16 = [](int64_t b) { return (b + 15) & ~int64_t(15); };
   int64_t at = up16((int64_t(d->workspace_slots) + 2) * pitch);
   lay.ws_bytes = uint32_t(at);
-  lay.rec_at = uint32_t(at);
-  at = up16(at + 16 * max_recs);
-  lay.flag_at = uint32_t(at);
-  at = up16(at + 4 * max_recs);
   lay.load_at = uint32_t(at);
   at = up16(at + 16 * max_loads);
   lay.out_at = uint32_t(at);
   at = up16(at + 4 * max_out);
+  // records and flags last: the forward kernel reads them through the scalar
+  // cache and allocates LDS only below rec_at; the reverse mode stages them
+  lay.rec_at = uint32_t(at);
+  at = up16(at + 16 * max_recs);
+  lay.flag_at = uint32_t(at);
+  at = up16(at + 4 * max_recs);
   lay.one_off = one;
   lds_bytes = at;
   return at <= 64 * 1024;
@@ -873,7 +869,7 @@ int launch_stream(const ye3t_hip_product_plan* p, const void* A, int64_t lda, in
   const int64_t groups = (tiles + per - 1) / per;
   const int64_t grid = groups * p->chunk_count;
   YE3T_REQUIRE(grid <= int64_t(0x7FFFFFFF), "too many samples for one launch");
-  const size_t lds = size_t(p->stream_lds);
+  const size_t lds = size_t(p->stream_layout[1]);  // up to rec_at: records and flags stay in global memory
   StreamLayout lay;
   lay.ws_bytes = p->stream_layout[0];
   lay.rec_at = p->stream_layout[1];
