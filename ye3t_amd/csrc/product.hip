@@ -419,8 +419,6 @@ __global__ __launch_bounds__(kLanes) void product_stream_adjoint_kernel(
   unsigned char* wsb = smem_raw + lane * sizeof(Real);                  // values
   unsigned char* gsb = smem_raw + lay.ws_bytes + lane * sizeof(Real);   // gradients
   unsigned char* prog = smem_raw + lay.ws_bytes;                        // program region, past the gradients
-  uint4* lrec = reinterpret_cast<uint4*>(prog + lay.rec_at);
-  uint32_t* lflag = reinterpret_cast<uint32_t*>(prog + lay.flag_at);
   uint2* lload = reinterpret_cast<uint2*>(prog + lay.load_at);
   uint32_t* lout = reinterpret_cast<uint32_t*>(prog + lay.out_at);
   const uint32_t pitch = kLanes * sizeof(Real);
@@ -438,10 +436,11 @@ __global__ __launch_bounds__(kLanes) void product_stream_adjoint_kernel(
     const int64_t o0 = out_off[chunk];
     const int nf = int(out_off[chunk + 1] - o0);
     __syncthreads();  // the previous chunk is done with the program region
-    for (int i = lane; i < nr; i += kLanes) {
-      lrec[i] = recs[r0 + i];
-      lflag[i] = flags[r0 + i];
-    }
+    // records and flags are wave-uniform: read through the scalar cache
+    typedef const __attribute__((address_space(4))) uint32_t* scalar_u32;
+    const scalar_u32 grec = (scalar_u32)(const void*)(recs + r0);
+    const scalar_u32 gflag = (scalar_u32)(const void*)(flags + r0);
+    auto rec_at = [&](int q) { return make_uint4(grec[4 * q], grec[4 * q + 1], grec[4 * q + 2], grec[4 * q + 3]); };
     for (int i = lane; i < nl; i += kLanes) lload[i] = loads[l0 + i];
     for (int i = lane; i < nf; i += kLanes) lout[i] = uint32_t(out_slots[o0 + i]) * pitch;
     __syncthreads();
@@ -467,8 +466,8 @@ __global__ __launch_bounds__(kLanes) void product_stream_adjoint_kernel(
       Real a[kGroup], b[kGroup];
 #pragma unroll
       for (int u = 0; u < kGroup; ++u) {
-        f[u] = uint32_t(__builtin_amdgcn_readfirstlane(int(lflag[q0 + u])));
-        r[u] = lrec[q0 + u];
+        f[u] = gflag[q0 + u];
+        r[u] = rec_at(q0 + u);
       }
 #pragma unroll
       for (int u = 0; u < kGroup; ++u) {
@@ -512,8 +511,8 @@ __global__ __launch_bounds__(kLanes) void product_stream_adjoint_kernel(
       Real a[kGroup], b[kGroup];
 #pragma unroll
       for (int u = 0; u < kGroup; ++u) {
-        f[u] = uint32_t(__builtin_amdgcn_readfirstlane(int(lflag[q0 + u])));
-        r[u] = lrec[q0 + u];
+        f[u] = gflag[q0 + u];
+        r[u] = rec_at(q0 + u);
       }
 #pragma unroll
       for (int u = 0; u < kGroup; ++u) {
@@ -528,7 +527,7 @@ __global__ __launch_bounds__(kLanes) void product_stream_adjoint_kernel(
         if (f[u] & kChained) {
           // the chain record precedes its partner, in this group or at the
           // end of the previous one
-          const uint4 rc = u > 0 ? r[u > 0 ? u - 1 : 0] : lrec[q0 - 1];
+          const uint4 rc = u > 0 ? r[u > 0 ? u - 1 : 0] : rec_at(q0 - 1);
           const Real a1 = u > 0 ? a[u > 0 ? u - 1 : 0] : lds_at<Real>(wsb, rc.x);
           const Real b1 = u > 0 ? b[u > 0 ? u - 1 : 0] : lds_at<Real>(wsb, rc.y);
           const Real pp = a1 * b1, ab = a[u] * b[u];
@@ -926,7 +925,8 @@ int launch_stream_adjoint(const ye3t_hip_product_plan* p, const void* A, int64_t
   lay.load_at = p->stream_layout[3];
   lay.out_at = p->stream_layout[4];
   lay.one_off = p->stream_layout[5];
-  const size_t lds = size_t(p->stream_lds) + lay.ws_bytes;
+  // values, gradients, loads and output slots (records and flags stay in global memory)
+  const size_t lds = size_t(p->stream_layout[1]) + lay.ws_bytes;
   const int64_t grid = tiles * groups;
   YE3T_REQUIRE(grid <= int64_t(0x7FFFFFFF), "too many samples for one launch");
   const dim3 rgrid = dim3(unsigned((p->a_width + 63) / 64), unsigned((samples + 63) / 64), 1u);
@@ -1088,8 +1088,8 @@ int ye3t_hip_product_adjoint_stream(const ye3t_hip_product_plan* p, const void* 
   int64_t need = 0;
   const int64_t groups = stream_adjoint_groups(p, samples, &need);
   YE3T_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace of %lld bytes needed", (long long)need);
-  YE3T_REQUIRE(p->stream_lds + int64_t(p->stream_layout[0]) <= 64 * 1024,
-               "the adjoint's values, gradients and program exceed 64 KB of LDS");
+  YE3T_REQUIRE(int64_t(p->stream_layout[1]) + int64_t(p->stream_layout[0]) <= 64 * 1024,
+               "the adjoint's values, gradients, loads and output slots exceed 64 KB of LDS");
   const hipStream_t s = as_stream(stream);
   return columns ? launch_stream_adjoint<true>(p, A, lda, gB, samples, workspace, groups, gA, s)
                  : launch_stream_adjoint<false>(p, A, lda, gB, samples, workspace, groups, gA, s);
