@@ -22,16 +22,37 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 
 
-def algorithmic_bytes(cfg, plan, elem, a_elem):
-    """Compulsory traffic per launch (each input read once, each output written once).
+def algorithmic_bytes(cfg, plan, s):
+    """Compulsory traffic per launch as the survey's measurement contract defines
+    it: every input read once, every output written once, at the
+    configuration's storage element size ``s`` (4 for fp32 configurations,
+    also for the density), with 4-byte CSR offsets and neighbour indices:
 
-    ``elem``: bytes of an input / B-feature value; ``a_elem``: bytes of a density value.
+      stage 1: E (3 s + 4) + (N + 1) 4 + [E 4 species | N C_in s node features] + N a_row s
+      stage 2: samples a_width s + samples F s
     """
     d = cfg.density
     N, K = d.atom_count, d.neighbors_per_atom
     E = N * K
-    C = d.channel_count
-    a_row = C * d.radial_rows * (d.l_max + 1) ** 2
+    a_row = d.channel_count * d.radial_rows * (d.l_max + 1) ** 2
+    stage1 = E * (3 * s + 4) + (N + 1) * 4 + N * a_row * s
+    if d.node_channels:
+        stage1 += N * d.node_channels * s
+    if d.species_count:
+        stage1 += E * 4
+    samples = cfg.samples()
+    stage2 = samples * plan.a_width * s + samples * plan.feature_count * s
+    return stage1, stage2
+
+
+def as_built_bytes(cfg, plan, elem, a_elem):
+    """The same compulsory traffic for the buffers as this build lays them out:
+    int64 CSR offsets and neighbour indices (the reference's index type), the
+    radial-mix table, and the density at its stored element size ``a_elem``."""
+    d = cfg.density
+    N, K = d.atom_count, d.neighbors_per_atom
+    E = N * K
+    a_row = d.channel_count * d.radial_rows * (d.l_max + 1) ** 2
     stage1 = E * (3 * elem + 8) + (N + 1) * 8 + N * a_row * a_elem
     if d.node_channels:
         stage1 += N * d.node_channels * elem + d.node_channels * (d.n_max + 1) * elem
@@ -65,10 +86,44 @@ def counter_traffic(kernel, workload, dtype):
     return None, None
 
 
+def host_facts():
+    """CPU model, logical CPUs, the CPUs this process may run on and OMP_NUM_THREADS."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": affinity,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+def cpu_calibration():
+    """Restatement-over-reference time ratios measured in the development
+    container (the reference's own CPU core compiled from its sources; it is
+    never shipped to the GPU box), from the committed summary's
+    ``calibration:`` lines."""
+    path = os.path.join(ROOT, "profiles", "cpu_baseline_calibration.md")
+    out = {}
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        for line in fh:
+            if line.startswith("calibration:"):
+                kv = dict(item.split("=", 1) for item in line[len("calibration:"):].split())
+                out[kv.pop("op")] = {k: (float(v) if k.endswith(("ratio", "_s")) else v) for k, v in kv.items()}
+    return {"source": os.path.relpath(path, ROOT), "ops": out} if out else None
+
+
 def cpu_baseline(cfg, pipe, target_seconds=10.0):
     """The C oracle (restatement of the reference CPU path) on a bounded sample."""
-    import numpy as np
-
     import oracle
 
     threads = oracle.max_threads()
@@ -90,26 +145,42 @@ def cpu_baseline(cfg, pipe, target_seconds=10.0):
     s1, s2 = run(atoms)
     per_atom_features = cfg.samples() // cfg.density.atom_count * pipe.plan.feature_count
     total = s1 + s2
-    return {"value": atoms * per_atom_features / total, "unit": "B-features/s", "cores": threads,
-            "kind": "port", "atoms_per_s": atoms / total,
-            "sample": f"{atoms} atoms of the same workload; stage1 {s1:.2f}s (serial edge loop, as the reference), "
-                      f"stage2 {s2:.2f}s (OpenMP over samples, {threads} threads)"}
+    out = {"value": atoms * per_atom_features / total, "unit": "B-features/s", "cores": threads,
+           "kind": "port", "atoms_per_s": atoms / total,
+           "sample": f"{atoms} atoms of the same workload; stage1 {s1:.2f}s (serial edge loop, as the reference), "
+                     f"stage2 {s2:.2f}s (OpenMP over samples, {threads} threads)"}
+    out.update(host_facts())
+    out["calibration"] = cpu_calibration()
+    return out
 
 
-def _time_kernel(fn, steps, warmup, min_warmup_s=0.25):
-    """Mean wall time per call of ``fn`` (device-resident inputs, K back-to-back
-    calls), after ``warmup`` calls and at least ``min_warmup_s`` of them (the
-    GPU's clocks ramp up over the first ~0.1 s of work)."""
+def warm_up(fn, warmup, min_seconds):
+    """Run ``fn`` at least ``warmup`` times and for at least ``min_seconds``
+    (the GPU reaches its steady clocks only after ~0.1 s of work); returns
+    ``(calls, seconds)`` actually spent."""
     import torch
 
     t0 = time.perf_counter()
     done = 0
-    while done < warmup or time.perf_counter() - t0 < min_warmup_s:
+    while done < warmup or time.perf_counter() - t0 < min_seconds:
         fn()
         done += 1
         if done % 16 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
+    return done, time.perf_counter() - t0
+
+
+MIN_WARMUP_S = 0.5
+
+
+def _time_kernel(fn, steps, warmup, min_warmup_s=MIN_WARMUP_S):
+    """Mean wall time per call of ``fn`` (device-resident inputs, K back-to-back
+    calls), after ``warmup`` calls and at least ``min_warmup_s`` of them (the
+    GPU's clocks ramp up over the first ~0.1 s of work)."""
+    import torch
+
+    warm_up(fn, warmup, min_warmup_s)
     t0 = time.perf_counter()
     for _ in range(steps):
         fn()
@@ -129,11 +200,13 @@ def bench_op(args, cfg):
     d = cfg.density
     dtype = args.dtype or cfg.dtypes[0]
     accumulate = args.accumulate or (cfg.accumulate if dtype == "f32" else None) or dtype
+    density = args.density or (cfg.density_dtype if dtype == "f32" and accumulate == cfg.accumulate else None) or accumulate
     workload = f"config{cfg.config_id}-{cfg.name}"
     line = {"op": args.op, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "data": "synthetic",
             "config": {"workload": workload}}
     if args.op == "linear_readout":
-        pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots, kernel=args.kernel, accumulate=accumulate)
+        pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots, kernel=args.kernel, accumulate=accumulate,
+                           density=density)
         A = pipe.density(to_device_inputs(cfg.density.generate(), dtype, "cuda"))
         rows = A.reshape(-1, pipe.plan.a_width)
         S = int(rows.shape[0])
@@ -145,8 +218,8 @@ def bench_op(args, cfg):
             t = _time_kernel(lambda: pipe.handle.linear(rows, wk, 0.5, out=out), args.steps, args.warmup)
         else:
             t = _time_kernel(lambda: pipe.linear(rows, w, 0.5, out=out), args.steps, args.warmup)
-        a_elem = 8 if accumulate == "f64" else 4
-        nbytes = S * pipe.plan.a_width * a_elem + S * out.element_size() + pipe.feature_count * a_elem
+        nbytes = S * pipe.plan.a_width * rows.element_size() + S * out.element_size() + \
+            pipe.feature_count * (8 if accumulate == "f64" else 4)
         st = program_stats(pipe.program)
         flops = S * (st["factor_reads"] + st["terms"] + 2 * pipe.feature_count)
         line.update({
@@ -159,7 +232,8 @@ def bench_op(args, cfg):
             "samples": S, "features_per_sample": pipe.feature_count})
         line["config"].update({"samples": S, "features": pipe.feature_count})
     elif args.op == "product_adjoint":
-        pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots, kernel=args.kernel, accumulate=accumulate)
+        pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots, kernel=args.kernel, accumulate=accumulate,
+                           density=density)
         A = pipe.density(to_device_inputs(cfg.density.generate(), dtype, "cuda"))
         rows = A.reshape(-1, pipe.plan.a_width)
         S = int(rows.shape[0])
@@ -262,13 +336,16 @@ def bench_op(args, cfg):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # the GPU reaches its steady clocks only after ~0.1 s of work: 5 warmup steps
-    # time the ramp (config 4: 0.207 ms per step after 5, 0.171 ms after 200)
+    # the warmup also lasts at least MIN_WARMUP_S seconds whatever --warmup says
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=1000)
+    ap.add_argument("--min-warmup-s", type=float, default=MIN_WARMUP_S,
+                    help="least warmup time in seconds (counter-collection runs, whose dispatches are "
+                         "serialised, pass 0)")
     ap.add_argument("--config", type=int, default=4)
     ap.add_argument("--dtype", default=None, help="storage type of inputs and B-features (f32 / f64)")
-    ap.add_argument("--accumulate", default=None, help="type of A and of the arithmetic (default per config)")
+    ap.add_argument("--accumulate", default=None, help="type of the arithmetic (default per config)")
+    ap.add_argument("--density", default=None, help="storage type of A (default per config)")
     ap.add_argument("--max-slots", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -301,27 +378,32 @@ def main():
         return
     dtype = args.dtype or cfg.dtypes[0]
     accumulate = args.accumulate or (cfg.accumulate if dtype == "f32" else None) or dtype
+    density = args.density or (cfg.density_dtype if dtype == "f32" and accumulate == cfg.accumulate else None) or accumulate
     elem = 8 if dtype == "f64" else 4
-    a_elem = 8 if accumulate == "f64" else 4
+    a_elem = 8 if density == "f64" else 4
     t_build = time.perf_counter()
-    pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots, kernel=args.kernel, accumulate=accumulate)
+    pipe = ACEPipeline(cfg.feature_spec, dtype, args.max_slots, kernel=args.kernel, accumulate=accumulate,
+                       density=density)
     t_build = time.perf_counter() - t_build
     inp = cfg.density.generate()
     dev = to_device_inputs(inp, dtype, "cuda")
     d = cfg.density
     A = torch.empty((d.atom_count, d.channel_count, d.radial_rows, (d.l_max + 1) ** 2),
-                    dtype=torch.float64 if accumulate == "f64" else torch.float32, device="cuda")
+                    dtype=torch.float64 if density == "f64" else torch.float32, device="cuda")
     rows = A.reshape(-1, pipe.plan.a_width)
     B = torch.empty((rows.shape[0], pipe.feature_count),
                     dtype=torch.float64 if dtype == "f64" else torch.float32, device="cuda")
 
+    pipe.density(dev, out=A)  # validates the CSR and neighbour indices once
+
     def step():
-        pipe.density(dev, out=A)
+        pipe.density(dev, out=A, validate=False)
         pipe.product(rows, out=B)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    # at least --warmup steps and at least MIN_WARMUP_S seconds of them: the
+    # GPU reaches its steady clocks only after ~0.1 s of work (config 4 with 5
+    # warmup steps: 0.207 ms per step; after 1 000: 0.157 ms)
+    warm_steps, warm_s = warm_up(step, args.warmup, args.min_warmup_s)
     # Per-kernel durations come from HIP events on one timed step in ten: an
     # event record drains the queue between the two kernels (config 4: 0.167 ms
     # per step with events on every step, 0.156 ms without), so the other
@@ -333,12 +415,12 @@ def main():
     t0 = time.perf_counter()
     for i in range(args.steps):
         if i % every:
-            pipe.density(dev, out=A)
+            pipe.density(dev, out=A, validate=False)
             pipe.product(rows, out=B)
             continue
         e0, e1, e2 = ev[i // every]
         e0.record()
-        pipe.density(dev, out=A)
+        pipe.density(dev, out=A, validate=False)
         e1.record()
         pipe.product(rows, out=B)
         e2.record()
@@ -354,7 +436,8 @@ def main():
     s1 = float(np.mean([a.elapsed_time(b) for a, b, _ in ev])) * 1e-3
     s2 = float(np.mean([b.elapsed_time(c) for _, b, c in ev])) * 1e-3
     ms_per_step = wall / args.steps * 1e3
-    b1, b2 = algorithmic_bytes(cfg, pipe.plan, elem, a_elem)
+    b1, b2 = algorithmic_bytes(cfg, pipe.plan, elem)
+    c1, c2 = as_built_bytes(cfg, pipe.plan, elem, a_elem)
     if pipe.kernel == "generated":
         k2 = "ye3t_product_generated"
     elif pipe.handle.uses_stream:
@@ -366,9 +449,10 @@ def main():
     value = features / (wall / args.steps)
     stats = program_stats(pipe.program)
     workload = f"config{cfg.config_id}-{cfg.name}"
-    traffic, traffic_src = counter_traffic(k2, workload, accumulate)
+    prec = f"{accumulate}-{density}A"  # arithmetic and density storage of the counter summaries
+    traffic, traffic_src = counter_traffic(k2, workload, prec)
     k1 = native.last_density_kernel()
-    traffic1, traffic1_src = counter_traffic(k1, workload, accumulate)
+    traffic1, traffic1_src = counter_traffic(k1, workload, prec)
     line = {
         "metric": "B-features/sec (atoms/s) on 1 MI355X; achieved HBM GB/s vs peak",
         "value": value,
@@ -376,12 +460,15 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": warm_steps,
+        "warmup_s": warm_s,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": accumulate,
         "storage_dtype": dtype,
+        "density_dtype": density,
         "data": "synthetic (seeded counter RNG, BASELINE.json configuration shapes)",
         "config": {"workload": workload, "atoms": d.atom_count,
                    "neighbors_per_atom": d.neighbors_per_atom, "channels": d.channel_count,
@@ -391,14 +478,20 @@ def main():
         "atoms_per_s": d.atom_count / (wall / args.steps),
         "roofline": {"bound": "hbm", "achieved": b2 / s2 / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": b2 / s2 / 1e9 / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
-                     "kernel": k2,
-                     "algorithmic_bytes": b2, "avg_kernel_us": s2 * 1e6, "event_steps": len(ev)},
+                     "kernel": k2, "algorithmic_bytes": b2, "algorithmic_bytes_as_built": c2,
+                     "frac_as_built": c2 / s2 / 1e9 / HBM_PEAK_GBS,
+                     "avg_kernel_us": s2 * 1e6, "event_steps": len(ev)},
         "stage1": {"kernel": k1, "avg_kernel_us": s1 * 1e6, "algorithmic_bytes": b1,
                    "achieved_gbs": b1 / s1 / 1e9, "frac": b1 / s1 / 1e9 / HBM_PEAK_GBS,
+                   "algorithmic_bytes_as_built": c1, "frac_as_built": c1 / s1 / 1e9 / HBM_PEAK_GBS,
                    "traffic": traffic1, "traffic_source": traffic1_src},
         "stage2": {"kernel": k2, "avg_kernel_us": s2 * 1e6, "algorithmic_bytes": b2,
                    "achieved_gbs": b2 / s2 / 1e9, "frac": b2 / s2 / 1e9 / HBM_PEAK_GBS,
+                   "algorithmic_bytes_as_built": c2, "frac_as_built": c2 / s2 / 1e9 / HBM_PEAK_GBS,
                    "program": stats, "plan_compile_s": t_build, "product_kernel": pipe.kernel},
+        "bytes_note": "algorithmic_bytes: the survey's compulsory-traffic formula at the configuration's "
+                      "storage element size with 4-byte indices; _as_built: int64 indices and the density at "
+                      "its stored size",
     }
     if copy_bytes is not None:
         line["copy_probe_bytes"] = copy_bytes

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 51 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 52 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -39,6 +39,15 @@ enum ye3t_status {
 /* Library ABI version; replaces core_abi_version() of the reference's pybind
  * module (ye3t/runtime/csrc/execution_plan_torch.cpp:7924-7934). */
 int ye3t_hip_abi_version(void);
+
+/* 1 when a HIP device is visible to this process, else 0: the counterpart of
+ * has_cuda() of the reference's pybind module (execution_plan_torch.cpp:7924-7934,
+ * consumed by native_execution_plan_capabilities, execution_plan.py:6118). */
+int ye3t_hip_has_hip(void);
+
+/* 0: this library has no CPU kernels (the reference's CPU runtime serves CPU
+ * tensors); counterpart of has_cpu() (execution_plan_torch.cpp:7924-7934). */
+int ye3t_hip_has_cpu(void);
 
 /* Thread-local message of the last failed call ("" if none). */
 const char* ye3t_hip_last_error(void);
@@ -117,6 +126,10 @@ typedef struct {
   double epsilon;
   int out_dtype;                /* dtype of A and of the accumulation; -1 = dtype.  YE3T_F64 with
                                    dtype YE3T_F32 keeps fp32 inputs but an fp64 density */
+  int accumulate_dtype;         /* arithmetic of the density; -1 = out_dtype.  YE3T_F64 with an
+                                   fp32 out_dtype accumulates in fp64 (matrix cores) and rounds A
+                                   once to fp32 at the store (fp64-MFMA shapes only, else
+                                   YE3T_EUNSUPPORTED) */
 } ye3t_density_args;
 
 /* A has shape [N, C, R, (l_max+1)^2] with R = 1 when radial_mix is set, else n_max+1. */
@@ -168,6 +181,11 @@ typedef struct {
   int64_t out_slot_count;
   int out_dtype;                /* dtype of B; -1 = dtype.  A and the arithmetic use dtype, so an
                                    fp64 plan may write fp32 features (rounded once, at the store) */
+  int in_dtype;                 /* dtype of the density A; -1 = dtype.  YE3T_F32 with an fp64 plan
+                                   reads fp32 density rows into fp64 arithmetic; such plans run
+                                   their attached generated kernels only (forward, readout,
+                                   adjoint with an fp32 gA); the interpreters return
+                                   YE3T_EUNSUPPORTED for them */
 } ye3t_product_plan_desc;
 
 typedef struct ye3t_hip_product_plan ye3t_hip_product_plan;

@@ -17,6 +17,19 @@ def column_rel_error(got, ref):
     return float(err.max()) if err.size else 0.0
 
 
+def fp32_rounding_ratio(got, ref):
+    """Largest elementwise ``|got - ref| / (2^-24 |ref| + 1e-13 RMS(column))``
+    of fp32 values ``got`` against fp64 ``ref``: at most 1 when each value of
+    ``got`` is ``ref`` rounded once to fp32 (half an ulp, 2^-24 relative) after
+    fp64 arithmetic (the second term covers fp64 rounding where a value cancels
+    far below its column's scale)."""
+    got = np.asarray(got, dtype=np.float64).reshape(ref.shape[0], -1)
+    ref = np.asarray(ref, dtype=np.float64).reshape(ref.shape[0], -1)
+    rms = np.sqrt(np.mean(ref * ref, axis=0))
+    bound = 2.0 ** -24 * np.abs(ref) + 1e-13 * np.where(rms > 0, rms, 1.0)
+    return float(np.max(np.abs(got - ref) / bound)) if ref.size else 0.0
+
+
 def rounded_inputs(inp, dtype):
     """Inputs as the device sees them: float arrays rounded to the compute dtype."""
     if dtype == "f64":

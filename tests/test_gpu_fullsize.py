@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests._util import TOL, column_rel_error, flush, rotation, rounded_inputs, wigner_real
+from tests._util import TOL, column_rel_error, flush, fp32_rounding_ratio, rotation, rounded_inputs, wigner_real
 from ye3t_amd.ace import workloads as W
 from ye3t_amd.ace.pipeline import ACEPipeline, to_device_inputs
 
@@ -21,11 +21,12 @@ pytestmark = pytest.mark.gpu
 
 
 def test_config4_full_size_fp32_parity(gpu):
-    """fp32 inputs and features with the configuration's fp64 intermediates."""
+    """fp32 inputs, density and features with the configuration's fp64
+    arithmetic (the density is accumulated in fp64 and rounded once)."""
     flush("config 4 full size, fp32 storage vs fp64 oracle")
     cfg = W.config(4)
     inp = cfg.density.generate()
-    pipe = ACEPipeline(cfg.feature_spec, "f32", accumulate=cfg.accumulate)
+    pipe = ACEPipeline(cfg.feature_spec, "f32", accumulate=cfg.accumulate, density=cfg.density_dtype)
     A, B = pipe.forward(to_device_inputs(inp, "f32", gpu), channelwise=True)
     A_ref = oracle.ace_density(rounded_inputs(inp, "f32"))
     N = cfg.density.atom_count
@@ -44,7 +45,7 @@ def test_config4_full_size_fused_linear_readout(gpu):
 
     cfg = W.config(4)
     inp = cfg.density.generate()
-    pipe = ACEPipeline(cfg.feature_spec, "f32", accumulate=cfg.accumulate)
+    pipe = ACEPipeline(cfg.feature_spec, "f32", accumulate=cfg.accumulate, density=cfg.density_dtype)
     A = pipe.density(to_device_inputs(inp, "f32", gpu))
     w = np.random.default_rng(77).normal(size=pipe.feature_count)
     got = pipe.linear(A.reshape(-1, pipe.plan.a_width), torch.as_tensor(w, device=gpu), -2.0)
@@ -62,15 +63,24 @@ def test_config4_full_size_product_adjoint(gpu):
     import torch
 
     cfg = W.config(4)
-    pipe = ACEPipeline(cfg.feature_spec, "f32", accumulate=cfg.accumulate)
+    pipe = ACEPipeline(cfg.feature_spec, "f32", accumulate=cfg.accumulate, density=cfg.density_dtype)
     A = pipe.density(to_device_inputs(cfg.density.generate(), "f32", gpu)).reshape(-1, pipe.plan.a_width)
     gB = torch.as_tensor(np.random.default_rng(78).normal(size=(A.shape[0], pipe.feature_count)),
                          dtype=torch.float32, device=gpu)
     gA = pipe.product_adjoint(A, gB)
-    ref = oracle.ace_product_flat_adjoint(A.cpu().numpy(), gB.cpu().double().numpy(), pipe.plan.flat_arrays())
-    err = column_rel_error(gA.cpu().numpy(), ref)
-    flush(f"  err {err:.3e}")
-    assert err < 1e-12
+    ref = oracle.ace_product_flat_adjoint(A.cpu().double().numpy(), gB.cpu().double().numpy(),
+                                          pipe.plan.flat_arrays())
+    got = gA.cpu().double().numpy()
+    if pipe.density_dtype == "f64":
+        err = column_rel_error(got, ref)
+        flush(f"  err {err:.3e}")
+        assert err < 1e-12
+    else:
+        # fp64 arithmetic, gA stored in the density's fp32: each value is the
+        # oracle's rounded once (within half an fp32 ulp, 2^-24 relative)
+        ratio = fp32_rounding_ratio(got, ref)
+        flush(f"  error / fp32 rounding bound {ratio:.3f}")
+        assert ratio <= 1.0
 
 
 def test_config4_full_size_rotation_covariance_fp64(gpu):

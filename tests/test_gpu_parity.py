@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests._util import TOL, column_rel_error, flush, rounded_inputs
+from tests._util import TOL, column_rel_error, flush, fp32_rounding_ratio, rounded_inputs
 from ye3t_amd.ace import workloads as W
 from ye3t_amd.ace.pipeline import ACEPipeline, to_device_inputs
 from ye3t_amd.ace.plan import ProductPlan
@@ -254,8 +254,9 @@ def test_interpreter_column_major_density(gpu, cid, dtype, samples, max_slots):
     assert torch.equal(At[:, :samples], A_dev.t()) and bool((At[:, samples:] == 0).all())
     B_rows = pipe.product(A_dev)
     elem = 8 if dtype == "f64" else 4
-    # the stream needs the workspace plus the staged program within 64 KB of LDS:
-    # the default workspaces (48 fp64 / 96 fp32 slots) always take it
+    # the stream needs the workspace plus the staged density loads and output
+    # slots within 64 KB of LDS: the default workspaces (48 fp64 / 96 fp32
+    # slots) always take it
     if (pipe.program["workspace_slots"] + 2) * 64 * elem <= 32 * 1024:
         assert pipe.handle.uses_stream
     if not pipe.handle.uses_stream:
@@ -294,8 +295,10 @@ def test_end_to_end_small(gpu, cid, dtype, atoms):
     flush(f"end to end config {cid} {dtype} atoms={atoms}")
     cfg = W.config(cid, atom_count=atoms)
     inp = cfg.density.generate()
-    pipe = ACEPipeline(cfg.feature_spec, dtype, accumulate=cfg.accumulate if dtype == "f32" else None)
-    flush(f"  plan built: {pipe.feature_count} features, kernel {pipe.kernel}, accumulate {pipe.accumulate}")
+    pipe = ACEPipeline(cfg.feature_spec, dtype, accumulate=cfg.accumulate if dtype == "f32" else None,
+                       density=cfg.density_dtype if dtype == "f32" else None)
+    flush(f"  plan built: {pipe.feature_count} features, kernel {pipe.kernel}, accumulate {pipe.accumulate}, "
+          f"density {pipe.density_dtype}")
     A, B = pipe.forward(to_device_inputs(inp, dtype, gpu), channelwise=cfg.channelwise)
     A_ref = oracle.ace_density(rounded_inputs(inp, dtype))
     assert column_rel_error(A.cpu().numpy().reshape(atoms, -1), A_ref.reshape(atoms, -1)) < TOL[dtype]
@@ -314,7 +317,8 @@ def test_linear_readout(gpu, cid, dtype, atoms):
 
     cfg = W.config(cid, atom_count=atoms)
     inp = cfg.density.generate()
-    pipe = ACEPipeline(cfg.feature_spec, dtype, accumulate=cfg.accumulate if dtype == "f32" else None)
+    pipe = ACEPipeline(cfg.feature_spec, dtype, accumulate=cfg.accumulate if dtype == "f32" else None,
+                       density=cfg.density_dtype if dtype == "f32" else None)
     A = pipe.density(to_device_inputs(inp, dtype, gpu))
     rows = A.reshape(-1, pipe.plan.a_width)
     F = pipe.feature_count
@@ -343,26 +347,34 @@ def test_linear_readout(gpu, cid, dtype, atoms):
         assert torch.equal(col, B[:, k])
 
 
-@pytest.mark.parametrize("dtype,accumulate,tol", [("f32", "f64", 1e-12), ("f64", "f64", 1e-12),
-                                                  ("f32", "f32", 2e-5)])
-def test_product_adjoint(gpu, dtype, accumulate, tol):
-    """gA = J(A)^T gB from the generated adjoint kernel vs the oracle's reverse mode (config 4 plan)."""
-    flush(f"product adjoint storage {dtype} accumulate {accumulate}")
+@pytest.mark.parametrize("dtype,accumulate,density,tol", [
+    ("f32", "f64", "f64", 1e-12), ("f64", "f64", "f64", 1e-12), ("f32", "f32", "f32", 2e-5),
+    ("f32", "f64", "f32", None)])
+def test_product_adjoint(gpu, dtype, accumulate, density, tol):
+    """gA = J(A)^T gB from the generated adjoint kernel vs the oracle's reverse
+    mode (config 4 plan).  With an fp32 density and fp64 arithmetic (tol None),
+    each gA value is the oracle's rounded once to fp32."""
+    flush(f"product adjoint storage {dtype} accumulate {accumulate} density {density}")
     import torch
 
-    pipe = ACEPipeline(W.config(4).feature_spec, dtype, accumulate=accumulate)
+    pipe = ACEPipeline(W.config(4).feature_spec, dtype, accumulate=accumulate, density=density)
     rng = np.random.default_rng(31)
     S = 4112  # 64 full tiles and a partial one
-    a_t = torch.float64 if accumulate == "f64" else torch.float32
+    a_t = torch.float64 if density == "f64" else torch.float32
     g_t = torch.float64 if dtype == "f64" else torch.float32
     A = torch.as_tensor(rng.normal(size=(S, pipe.plan.a_width)), dtype=a_t)
     gB = torch.as_tensor(rng.normal(size=(S, pipe.feature_count)), dtype=g_t)
     gA = pipe.product_adjoint(A.to(gpu), gB.to(gpu))
     assert gA.dtype == a_t and tuple(gA.shape) == (S, pipe.plan.a_width)
     ref = oracle.ace_product_flat_adjoint(A.double().numpy(), gB.double().numpy(), pipe.plan.flat_arrays())
-    err = column_rel_error(gA.cpu().double().numpy(), ref)
-    flush(f"  err {err:.3e}")
-    assert err < tol
+    if tol is None:
+        ratio = fp32_rounding_ratio(gA.cpu().double().numpy(), ref)
+        flush(f"  error / fp32 rounding bound {ratio:.3f}")
+        assert ratio <= 1.0
+    else:
+        err = column_rel_error(gA.cpu().double().numpy(), ref)
+        flush(f"  err {err:.3e}")
+        assert err < tol
     # linear in the feature gradient: doubling gB doubles every intermediate exactly
     assert torch.equal(pipe.product_adjoint(A.to(gpu), 2 * gB.to(gpu)), 2 * gA)
 
@@ -398,15 +410,23 @@ def test_stream_product_adjoint(gpu, cid, dtype, accumulate, samples, tol):
 
 
 def test_product_adjoint_needs_a_term_stream(gpu, monkeypatch):
-    """A workspace too wide for the term stream has no device adjoint."""
+    """A workspace too wide for the term stream has no device adjoint; one whose
+    forward stream fits 64 KB of LDS but whose reverse mode (values and
+    gradients) does not is refused by the library before any launch."""
     import torch
 
-    monkeypatch.setenv("YE3T_ADJOINT_SLOTS", "120")
-    pipe = ACEPipeline(W.config(4).feature_spec, "f64", 120, kernel="interpreter")
+    monkeypatch.setenv("YE3T_ADJOINT_SLOTS", "130")
+    pipe = ACEPipeline(W.config(4).feature_spec, "f64", 130, kernel="interpreter")
     assert not pipe.handle.uses_stream
     A = torch.zeros((3, pipe.plan.a_width), dtype=torch.float64, device=gpu)
+    gB = torch.zeros((3, pipe.feature_count), dtype=torch.float64, device=gpu)
     with pytest.raises(NotImplementedError):
-        pipe.product_adjoint(A, torch.zeros((3, pipe.feature_count), dtype=torch.float64, device=gpu))
+        pipe.product_adjoint(A, gB)
+    monkeypatch.setenv("YE3T_ADJOINT_SLOTS", "120")
+    pipe = ACEPipeline(W.config(4).feature_spec, "f64", 120, kernel="interpreter")
+    assert pipe.handle.uses_stream  # records take no LDS: the forward stream fits
+    with pytest.raises(RuntimeError, match="64 KB"):
+        pipe.product_adjoint(A, gB)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f64"])
@@ -527,6 +547,95 @@ def test_fp64_mfma_density_random_csr(gpu, monkeypatch, mode, shape, storage, wa
             assert not np.any(outs[key][empty])
 
 
+@pytest.mark.parametrize("mode,shape", [("features", (8, 3)), ("single", (8, 3)), ("single", (12, 6))])
+def test_fp32_density_accumulated_in_fp64(gpu, mode, shape):
+    """accumulate_dtype=f64 with an fp32 A: the fp64 matrix-core accumulation
+    rounded once, i.e. exactly the fp64 density's values rounded to fp32."""
+    flush(f"fp32 density accumulated in fp64, {mode} n_max,l_max={shape}")
+    import torch
+
+    inp = _random_csr_workload(mode, 301, 150, 32, n_max=shape[0], l_max=shape[1])
+    dev = to_device_inputs(inp, "f32", gpu)
+    N = inp["atom_count"]
+    kw = dict(atom_count=N, channel_count=inp["channel_count"], n_max=inp["n_max"], l_max=inp["l_max"],
+              cutoff=inp["cutoff"], lam=inp["lambda"], epsilon=inp["epsilon"],
+              node_features=dev.get("node_features"), radial_mix=dev.get("radial_mix"))
+    A64 = native.ace_density_forward(dev["edge_vectors"], dev["row_offsets"], dev["neighbors"],
+                                     out_dtype=torch.float64, **kw)
+    A32 = native.ace_density_forward(dev["edge_vectors"], dev["row_offsets"], dev["neighbors"],
+                                     out_dtype=torch.float32, accumulate_dtype=torch.float64, **kw)
+    assert A32.dtype == torch.float32
+    assert torch.equal(A32, A64.to(torch.float32))
+    ref = oracle.ace_density(rounded_inputs(inp, "f32")).reshape(N, -1)
+    assert column_rel_error(A32.cpu().numpy().reshape(N, -1), ref) < 1e-6
+
+
+def test_fp32_density_accumulated_in_fp64_needs_an_mfma_shape(gpu):
+    """Species densities have no fp64 matrix-core kernel: the mixed precision is refused."""
+    import torch
+
+    inp = _ragged_workload("species")
+    dev = to_device_inputs(inp, "f32", gpu)
+    with pytest.raises(RuntimeError, match="fp64 matrix-core shapes"):
+        native.ace_density_forward(
+            dev["edge_vectors"], dev["row_offsets"], dev["neighbors"], atom_count=inp["atom_count"],
+            channel_count=inp["channel_count"], n_max=inp["n_max"], l_max=inp["l_max"], cutoff=inp["cutoff"],
+            lam=inp["lambda"], species=dev["species"], out_dtype=torch.float32, accumulate_dtype=torch.float64)
+
+
+def test_density_rejects_bad_indices_before_launch(gpu):
+    """Out-of-range neighbours and inconsistent CSR offsets raise on the host."""
+    import torch
+
+    inp = _random_csr_workload("features", 50, 20, 33)
+    dev = to_device_inputs(inp, "f32", gpu)
+    kw = dict(atom_count=50, channel_count=16, n_max=8, l_max=3, cutoff=5.0, lam=W.LAMBDA,
+              node_features=dev["node_features"], radial_mix=dev["radial_mix"])
+    bad = dev["neighbors"].clone()
+    bad[-1] = 50
+    with pytest.raises(ValueError, match="neighbor index"):
+        native.ace_density_forward(dev["edge_vectors"], dev["row_offsets"], bad, **kw)
+    offs = dev["row_offsets"].clone()
+    offs[-1] -= 1
+    with pytest.raises(ValueError, match="row_offsets"):
+        native.ace_density_forward(dev["edge_vectors"], offs, dev["neighbors"], **kw)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("cid,dtype", [(2, "f64"), (3, "f32")])
+def test_stream_multi_tile_workgroups(gpu, monkeypatch, cid, dtype):
+    """Four 64-sample tiles per stream workgroup (the per-tile record re-read and
+    the next-tile density prefetch), five tiles with a partial last one:
+    row-major, column-major and the oracle agree, and the reverse mode matches
+    the oracle's and reruns to the same bits."""
+    flush(f"stream with 4 tiles per workgroup, config {cid} {dtype}")
+    import torch
+
+    monkeypatch.setenv("YE3T_STREAM_TILES", "4")
+    spec = _species_rank4_spec() if cid == 3 else W.config(cid).feature_spec
+    pipe = ACEPipeline(spec, dtype, kernel="interpreter")
+    assert pipe.handle.uses_stream
+    samples = 4 * 64 + 37
+    A = _t(np.random.default_rng(17).normal(size=(samples, pipe.plan.a_width)), dtype, gpu)
+    B_rows = pipe.handle.forward(A)
+    B_cols = pipe.product(A)  # column-major density
+    assert torch.equal(B_rows, B_cols)
+    ref = oracle.ace_product_flat(A.double().cpu().numpy(), pipe.plan.flat_arrays())
+    err = column_rel_error(B_rows.cpu().numpy(), ref)
+    flush(f"  forward err {err:.3e}")
+    assert err < TOL[dtype]
+    g_t = torch.float64 if dtype == "f64" else torch.float32
+    gB = torch.as_tensor(np.random.default_rng(18).normal(size=(samples, pipe.feature_count)), dtype=g_t,
+                         device=gpu)
+    gA = pipe.product_adjoint(A, gB)
+    gref = oracle.ace_product_flat_adjoint(A.double().cpu().numpy(), gB.double().cpu().numpy(),
+                                           pipe.plan.flat_arrays())
+    err = column_rel_error(gA.cpu().double().numpy(), gref)
+    flush(f"  adjoint err {err:.3e}")
+    assert err < TOL[dtype]
+    assert torch.equal(pipe.product_adjoint(A, gB), gA)
+
+
 @pytest.mark.parametrize("waves", ["1", "2"])
 @pytest.mark.parametrize("accumulate", ["f32", "f64"])
 def test_persistent_generated_kernel_tiles_and_misaligned_output(gpu, monkeypatch, accumulate, waves):
@@ -541,6 +650,42 @@ def test_persistent_generated_kernel_tiles_and_misaligned_output(gpu, monkeypatc
     assert pipe.handle.generated["threads"] == 64 * int(waves)
     assert pipe.handle.generated.get("persistent")
     real = torch.float64 if accumulate == "f64" else torch.float32
+    _check_persistent_tiles(gpu, pipe, real, accumulate)
+
+
+@pytest.mark.parametrize("samples", [1, 65, 4097, 200003])
+def test_fp32_density_with_fp64_arithmetic(gpu, samples):
+    """An fp32 density read into fp64 arithmetic by the persistent generated
+    kernel (config 4's mode): equals the fp64 plan on the same fp32 values to
+    the fp32 rounding of B, and the generic kernels refuse such a plan."""
+    flush(f"fp32 density, fp64 arithmetic, samples {samples}")
+    import torch
+
+    spec = W.config(4).feature_spec
+    mixed = ACEPipeline(spec, "f32", accumulate="f64", density="f32")
+    wide = ACEPipeline(spec, "f32", accumulate="f64")
+    assert mixed.kernel == "generated" and mixed.handle.generated["in_dtype"] == "f32"
+    A32 = torch.as_tensor(np.random.default_rng(samples).normal(size=(samples, mixed.plan.a_width)),
+                          dtype=torch.float32, device=gpu)
+    B_mixed = mixed.product(A32)
+    B_wide = wide.product(A32.double())
+    assert torch.equal(B_mixed, B_wide)  # same fp64 arithmetic on the same values
+    if samples <= 4097:
+        ref = oracle.ace_product_flat(A32.double().cpu().numpy(), mixed.plan.flat_arrays())
+        assert column_rel_error(B_mixed.cpu().numpy(), ref) < 1e-5
+    # the word and stream interpreters read densities of the plan's dtype only
+    mixed.handle.select(use_interpreter=True)
+    with pytest.raises(RuntimeError, match="generated kernel only"):
+        mixed.product(A32)
+    mixed.handle.select(use_interpreter=False)
+    flat = torch.empty(samples * mixed.feature_count + 1, dtype=torch.float32, device=gpu)
+    with pytest.raises(RuntimeError, match="generated kernel only"):
+        mixed.product(A32, out=flat[1:].view(samples, mixed.feature_count))  # misaligned B: no persistent kernel
+
+
+def _check_persistent_tiles(gpu, pipe, real, accumulate):
+    import torch
+
     for samples in (1, 64, 65, 4097, 200003):
         A = torch.as_tensor(np.random.default_rng(samples).normal(size=(samples, pipe.plan.a_width)), dtype=real,
                             device=gpu)

@@ -1,0 +1,105 @@
+"""Host-side behaviour of the ``ye3t.runtime`` mirror (no GPU work).
+
+* the capability report keeps the reference's keys and reports operations
+  under the reference's names (``execution_plan.py:6118-6850``);
+* index inputs of the fused density are range-checked before any launch;
+* ``backend="reference"`` is a known value that this device branch refuses
+  explicitly.
+"""
+
+import pytest
+import torch
+
+from ye3t_amd import runtime
+from ye3t_amd.runtime import native
+
+# keys of the reference report that consumers test (execution_plan.py:6316-6662)
+REFERENCE_KEYS = ("schema", "torch_independent_core_source", "prebuilt_extension", "cpu", "cuda",
+                  "cuda_operations", "cuda_density_auto_min_work_items", "segmented_factorized_angular",
+                  "heterogeneous_factorized_roots", "triton_available", "triton_cuda_available",
+                  "triton_operations", "core_abi_version", "factorized_workspace_metadata", "dtypes",
+                  "analysis_orientation", "operations")
+
+# operation names of the reference report's ``operations`` tuple for the ops
+# this backend implements (execution_plan.py:6662-6850)
+REFERENCE_NAMES = {"cheb_exp_cos_radial_table_with_derivative", "real_spherical_harmonics_table_with_derivative",
+                   "density_accumulate", "density_accumulate_adjoint", "symmetric_power_monomial"}
+
+
+def test_capability_report_keys_and_names():
+    report = runtime.native_execution_plan_capabilities()
+    for key in REFERENCE_KEYS:
+        assert key in report, key
+    assert report["schema"] == "ye3t_execution_plan_v1"
+    assert report["cuda"] is False and report["cuda_operations"] == ()
+    assert report["core_abi_version"] == native.ABI_VERSION >= report["minimum_core_abi_version"] == 42
+    assert report["analysis_orientation"] == "conjugate_transpose"
+    assert REFERENCE_NAMES <= set(report["operations"])
+    # the reference names its SH table op with the real_ prefix
+    assert "spherical_harmonics_table_with_derivative" not in report["operations"]
+    assert len(set(report["operations"])) == len(report["operations"])
+    # no GPU in this environment: the HIP capability is off and lists nothing
+    if not torch.cuda.is_available():
+        assert report["hip"] is False and report["hip_operations"] == ()
+        assert "hip_device" not in report
+
+
+def test_has_hip_and_has_cpu_are_exported():
+    lib = native.lib()
+    assert lib.ye3t_hip_has_cpu() == 0
+    assert hasattr(lib, "ye3t_hip_has_hip")
+
+
+def _csr(N=5, K=3):
+    offs = torch.arange(N + 1, dtype=torch.int64) * K
+    nbr = (torch.arange(N * K, dtype=torch.int64) * 7) % N
+    return offs, nbr
+
+
+def test_density_csr_validation_accepts_good_input():
+    offs, nbr = _csr()
+    species = torch.tensor([0, 1, 2, 3, 1], dtype=torch.int32)
+    assert runtime.validate_density_csr(offs, nbr, 5, 15, species=species, species_count=4)
+    # atoms without edges and an empty edge list are fine
+    assert runtime.validate_density_csr(torch.zeros(4, dtype=torch.int64), None, 3, 0)
+
+
+@pytest.mark.parametrize("case", ["first", "last", "decreasing", "nbr_high", "nbr_negative", "species_high",
+                                  "species_dtype", "offsets_dtype", "offsets_shape"])
+def test_density_csr_validation_rejects_bad_input(case):
+    offs, nbr = _csr()
+    species = torch.tensor([0, 1, 2, 3, 1], dtype=torch.int32)
+    N, E = 5, 15
+    if case == "first":
+        offs = offs + 1
+    elif case == "last":
+        offs = offs.clone()
+        offs[-1] = E - 1
+    elif case == "decreasing":
+        offs = offs.clone()
+        offs[2] = offs[3] + 1
+    elif case == "nbr_high":
+        nbr = nbr.clone()
+        nbr[4] = N
+    elif case == "nbr_negative":
+        nbr = nbr.clone()
+        nbr[0] = -1
+    elif case == "species_high":
+        species = species.clone()
+        species[2] = 4
+    elif case == "species_dtype":
+        species = species.to(torch.int64)
+    elif case == "offsets_dtype":
+        offs = offs.to(torch.int32)
+    elif case == "offsets_shape":
+        offs = offs[:-1]
+    with pytest.raises(ValueError):
+        runtime.validate_density_csr(offs, nbr, N, E, species=species, species_count=4)
+
+
+def test_backend_reference_is_refused_explicitly():
+    x = torch.zeros(3, dtype=torch.float64)
+    with pytest.raises(NotImplementedError, match="reference"):
+        runtime.cheb_exp_cos_radial_table_with_derivative(x, x, x, 2, backend="reference")
+    with pytest.raises(ValueError, match="backend"):
+        runtime.cheb_exp_cos_radial_table_with_derivative(x, x, x, 2, backend="triton")

@@ -177,9 +177,24 @@ def test_stream_reverse_sweep_matches_the_oracle(case):
 
 def test_wide_workspaces_get_no_stream():
     plan = ProductPlan(W.config(4).feature_spec)
-    prog = compile_program(plan, "f64", 120)
-    assert (prog["workspace_slots"] + 2) * 64 * 8 > 56 * 1024
+    prog = compile_program(plan, "f64", 130)
+    # 125 + 2 fp64 slots (63.5 KB) plus the staged density loads and output
+    # slots of the widest chunk exceed 64 KB of LDS
+    assert prog["workspace_slots"] == 125
     assert native.stream_encode(prog) is None
+
+
+def test_records_take_no_lds():
+    """Records and flags are read through the scalar cache, so only the
+    workspace, the density-load list and the output slots must fit 64 KB: a
+    120-slot fp64 workspace (61 KB) still gets a term stream."""
+    plan = ProductPlan(W.config(4).feature_spec)
+    prog = compile_program(plan, "f64", 120)
+    st = native.stream_encode(prog)
+    assert st is not None
+    lay = st["layout"]
+    assert lay["rec_at"] == lay["flag_at"] == lay["lds_bytes"] <= 64 * 1024
+    assert lay["lds_bytes"] < lay["ws_bytes"] + 16 * len(st["records"])
 
 
 def test_a_chunk_that_loads_a_column_twice_gets_no_stream():

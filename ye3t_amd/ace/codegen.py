@@ -22,6 +22,18 @@ GROUP = 32  # output columns staged per flush
 CHAINS = 4  # independent partial sums per output component (persistent kernel)
 
 
+def _ctype(dtype):
+    return "double" if dtype == "f64" else "float"
+
+
+def _check_in_dtype(dtype, in_dtype):
+    """Density storage type of a kernel whose arithmetic is ``dtype``."""
+    in_dtype = in_dtype or dtype
+    if in_dtype not in ("f32", "f64") or (dtype == "f32" and in_dtype == "f64"):
+        raise ValueError(f"unsupported density dtype {in_dtype!r} for {dtype} arithmetic")
+    return in_dtype
+
+
 def _lit(value, dtype):
     if dtype == "f64":
         return repr(float(value))
@@ -165,7 +177,7 @@ def _split_outputs(plan, parts):
 
 
 def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_product_generated", waves=1,
-                        store_policy=0):
+                        store_policy=0, in_dtype=None):
     """Persistent variant of the single-chunk kernel: a workgroup loops over
     64-sample tiles ``blockIdx.x, blockIdx.x + gridDim.x, ...``.
 
@@ -185,8 +197,12 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
 
     ``store_policy``: cache-policy bits of the B stores (gfx950 buffer-store
     ``aux``: 1 = sc0, 2 = nt, 16 = sc1).
+
+    ``in_dtype`` (default ``dtype``): type of the density rows; "f32" with an
+    "f64" plan converts each value to fp64 as it is loaded.
     """
     out_dtype = out_dtype or dtype
+    in_dtype = _check_in_dtype(dtype, in_dtype)
     if dtype == "f32" and out_dtype != "f32":
         raise ValueError("an f32 plan writes f32 features")
     real = "double" if dtype == "f64" else "float"
@@ -202,11 +218,12 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
     w("// generated by ye3t_amd.ace.codegen (persistent) -- do not edit (compiled with hipRTC)")
     w(f"#define REAL {real}")
     w(f"#define OUT {outt}")
+    w(f"#define AIN {_ctype(in_dtype)}")
     w("typedef unsigned v4u __attribute__((ext_vector_type(4)));")
     w("typedef unsigned v2u __attribute__((ext_vector_type(2)));")
     threads = 64 * waves
     w(f"extern \"C\" __global__ __launch_bounds__({threads}) void {kernel_name}(")
-    w("    const REAL* __restrict__ A, long samples, OUT* __restrict__ B) {")
+    w("    const AIN* __restrict__ A, long samples, OUT* __restrict__ B) {")
     w(f"  __shared__ __attribute__((aligned(16))) OUT st[64 * {pitch}];")
     w("  const int lane = threadIdx.x & 63;")
     w("  const int wv = threadIdx.x >> 6;")
@@ -216,13 +233,13 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
     w("  long srow = tile * 64 + lane;")
     w("  srow = srow < samples ? srow : samples - 1;")
     for c in range(Wd):
-        w(f"  REAL a{c} = A[srow * {Wd}L + {c}];")
+        w(f"  REAL a{c} = (REAL)A[srow * {Wd}L + {c}];")
     w("  for (;;) {")
     w("    const long next = tile + gridDim.x;")
     w("    long nrow = next * 64 + lane;")
     w("    nrow = nrow < samples ? nrow : samples - 1;")
     for c in range(Wd):
-        w(f"    const REAL n{c} = A[nrow * {Wd}L + {c}];")
+        w(f"    const AIN n{c} = A[nrow * {Wd}L + {c}];")
     for g, (f0, f1) in enumerate(_split_outputs(plan, waves)):
         w(f"    if (wv == {g}) {{" if waves > 1 else "    {")
         emitted = set()
@@ -264,18 +281,19 @@ def generate_persistent(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_pro
     w("    if (next >= tiles) break;")
     w("    tile = next;")
     for c in range(Wd):
-        w(f"    a{c} = n{c};")
+        w(f"    a{c} = (REAL)n{c};")
     w("  }")
     w("}")
     source = "\n".join(out) + "\n"
     meta = {"kernel": kernel_name, "chunks": 1, "rows": 64, "persistent": True, "threads": threads,
             "feature_count": F,
-            "a_width": Wd, "dtype": dtype, "out_dtype": out_dtype,
+            "a_width": Wd, "dtype": dtype, "out_dtype": out_dtype, "in_dtype": in_dtype,
             "hash": hashlib.sha256(source.encode()).hexdigest()[:16]}
     return source, meta
 
 
-def generate_readout(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_product_readout", waves=2):
+def generate_readout(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_product_readout", waves=2,
+                     in_dtype=None):
     """Fused linear readout ``out[s] = bias + sum_f W[f] B[s, f]`` without
     materialising B: the persistent tile loop of :func:`generate_persistent`
     (64 samples per tile, next tile's rows prefetched, ``waves`` waves sharing a
@@ -284,11 +302,13 @@ def generate_readout(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_produc
     wave sums and the bias are added in a fixed order (deterministic); one
     value per sample is stored.
 
-    Kernel signature: ``(const REAL* A, long samples, OUT* out, const REAL* W, REAL bias)``.
+    Kernel signature: ``(const AIN* A, long samples, OUT* out, const REAL* W, REAL bias)``
+    (``AIN`` = ``in_dtype``, default ``dtype``).
     Counterpart of the reference's fused ``factorized_angular_linear``
     (``execution_plan_cuda.cu:8957``; readout semantics ``execution_plan.py:13832-13850``).
     """
     out_dtype = out_dtype or dtype
+    in_dtype = _check_in_dtype(dtype, in_dtype)
     if dtype == "f32" and out_dtype != "f32":
         raise ValueError("an f32 plan writes f32 values")
     real = "double" if dtype == "f64" else "float"
@@ -301,9 +321,10 @@ def generate_readout(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_produc
     w("// generated by ye3t_amd.ace.codegen (fused linear readout) -- do not edit (compiled with hipRTC)")
     w(f"#define REAL {real}")
     w(f"#define OUT {outt}")
+    w(f"#define AIN {_ctype(in_dtype)}")
     threads = 64 * waves
     w(f"extern \"C\" __global__ __launch_bounds__({threads}) void {kernel_name}(")
-    w("    const REAL* __restrict__ A, long samples, OUT* __restrict__ out, const REAL* __restrict__ W, REAL bias) {")
+    w("    const AIN* __restrict__ A, long samples, OUT* __restrict__ out, const REAL* __restrict__ W, REAL bias) {")
     w(f"  __shared__ REAL part[{waves}][64];")
     w("  const int lane = threadIdx.x & 63;")
     w("  const int wv = threadIdx.x >> 6;")
@@ -313,13 +334,13 @@ def generate_readout(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_produc
     w("  long srow = tile * 64 + lane;")
     w("  srow = srow < samples ? srow : samples - 1;")
     for c in range(Wd):
-        w(f"  REAL a{c} = A[srow * {Wd}L + {c}];")
+        w(f"  REAL a{c} = (REAL)A[srow * {Wd}L + {c}];")
     w("  for (;;) {")
     w("    const long next = tile + gridDim.x;")
     w("    long nrow = next * 64 + lane;")
     w("    nrow = nrow < samples ? nrow : samples - 1;")
     for c in range(Wd):
-        w(f"    const REAL n{c} = A[nrow * {Wd}L + {c}];")
+        w(f"    const AIN n{c} = A[nrow * {Wd}L + {c}];")
     for g, (f0, f1) in enumerate(_split_outputs(plan, waves)):
         w(f"    if (wv == {g}) {{" if waves > 1 else "    {")
         w("      REAL acc = (REAL)0;")
@@ -342,16 +363,18 @@ def generate_readout(plan, dtype="f32", out_dtype=None, kernel_name="ye3t_produc
     w("    if (next >= tiles) break;")
     w("    tile = next;")
     for c in range(Wd):
-        w(f"    a{c} = n{c};")
+        w(f"    a{c} = (REAL)n{c};")
     w("  }")
     w("}")
     src = "\n".join(out) + "\n"
     meta = {"kernel": kernel_name, "threads": threads, "feature_count": plan.feature_count, "a_width": Wd,
-            "dtype": dtype, "out_dtype": out_dtype, "hash": hashlib.sha256(src.encode()).hexdigest()[:16]}
+            "dtype": dtype, "out_dtype": out_dtype, "in_dtype": in_dtype,
+            "hash": hashlib.sha256(src.encode()).hexdigest()[:16]}
     return src, meta
 
 
-def generate_adjoint(plan, dtype="f64", grad_dtype=None, kernel_name="ye3t_product_adjoint", waves=2):
+def generate_adjoint(plan, dtype="f64", grad_dtype=None, kernel_name="ye3t_product_adjoint", waves=2,
+                     in_dtype=None):
     """Reverse mode of the product: ``gA[s] = J(A[s])^T gB[s]`` (counterpart of
     the reference's ``factorized_angular_adjoint``, ``execution_plan_cuda.cu:6361``;
     CPU core ``ye3t_runtime_core.h:1431-1456``).
@@ -366,9 +389,12 @@ def generate_adjoint(plan, dtype="f64", grad_dtype=None, kernel_name="ye3t_produ
     density gradient in LDS.  The partials are added in wave order (fixed) and
     the ``[rows, a_width]`` block of gA is stored with contiguous stores.
 
-    Kernel signature: ``(const REAL* A, const GT* gB, long samples, REAL* gA)``.
+    Kernel signature: ``(const AIN* A, const GT* gB, long samples, AIN* gA)``:
+    the density and its gradient have the type ``in_dtype`` (default ``dtype``);
+    the arithmetic is ``dtype``.
     """
     grad_dtype = grad_dtype or dtype
+    in_dtype = _check_in_dtype(dtype, in_dtype)
     if dtype == "f32" and grad_dtype != "f32":
         raise ValueError("an f32 plan takes f32 gradients")
     real = "double" if dtype == "f64" else "float"
@@ -382,9 +408,10 @@ def generate_adjoint(plan, dtype="f64", grad_dtype=None, kernel_name="ye3t_produ
     w("// generated by ye3t_amd.ace.codegen (product adjoint) -- do not edit (compiled with hipRTC)")
     w(f"#define REAL {real}")
     w(f"#define GT {gt}")
+    w(f"#define AIN {_ctype(in_dtype)}")
     threads = 64 * waves
     w(f"extern \"C\" __global__ __launch_bounds__({threads}) void {kernel_name}(")
-    w("    const REAL* __restrict__ A, const GT* __restrict__ gB, long samples, REAL* __restrict__ gA) {")
+    w("    const AIN* __restrict__ A, const GT* __restrict__ gB, long samples, AIN* __restrict__ gA) {")
     w(f"  __shared__ __attribute__((aligned(16))) GT gt[64 * {pitch}];")
     w(f"  __shared__ REAL gp[{waves}][{Wd}][64];")
     w("  const int lane = threadIdx.x & 63;")
@@ -416,7 +443,7 @@ def generate_adjoint(plan, dtype="f64", grad_dtype=None, kernel_name="ye3t_produ
         w("    }")
     w("    const long srow = s0 + (lane < rows ? lane : rows - 1);")
     for c in range(Wd):
-        w(f"    const REAL a{c} = A[srow * {Wd}L + {c}];")
+        w(f"    const REAL a{c} = (REAL)A[srow * {Wd}L + {c}];")
     w("    __syncthreads();")
     for g, (f0, f1) in enumerate(_split_outputs(plan, waves)):
         w(f"    if (wv == {g}) {{" if waves > 1 else "    {")
@@ -470,26 +497,29 @@ def generate_adjoint(plan, dtype="f64", grad_dtype=None, kernel_name="ye3t_produ
     w("      REAL v = gp[0][col][r];")
     for g in range(1, waves):
         w(f"      v += gp[{g}][col][r];")
-    w(f"      gA[s0 * {Wd}L + i] = v;")
+    w(f"      gA[s0 * {Wd}L + i] = (AIN)v;")
     w("    }")
     w("    __syncthreads();")
     w("  }")
     w("}")
     src = "\n".join(out) + "\n"
     meta = {"kernel": kernel_name, "threads": threads, "feature_count": F, "a_width": Wd, "dtype": dtype,
-            "grad_dtype": grad_dtype, "hash": hashlib.sha256(src.encode()).hexdigest()[:16]}
+            "grad_dtype": grad_dtype, "in_dtype": in_dtype, "hash": hashlib.sha256(src.encode()).hexdigest()[:16]}
     return src, meta
 
 
-def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generated", out_dtype=None, rows=None):
+def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generated", out_dtype=None, rows=None,
+             in_dtype=None):
     """Return ``(source, meta)`` for a specialised product kernel.
 
     ``dtype`` is the type of ``A`` and of the arithmetic, ``out_dtype`` (default
     the same; "f32" with an "f64" plan) that of ``B``.  ``rows`` (<= 64,
     default :func:`tile_rows`) is the number of samples a 64-lane workgroup
-    produces; lanes past it idle.
+    produces; lanes past it idle.  ``in_dtype`` (default ``dtype``) is the
+    storage type of ``A`` ("f32" with an "f64" plan: converted as loaded).
     """
     out_dtype = out_dtype or dtype
+    in_dtype = _check_in_dtype(dtype, in_dtype)
     if dtype == "f32" and out_dtype != "f32":
         raise ValueError("an f32 plan writes f32 features")
     real = "double" if dtype == "f64" else "float"
@@ -505,8 +535,9 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     w("// generated by ye3t_amd.ace.codegen -- do not edit (compiled with hipRTC)")
     w(f"#define REAL {real}")
     w(f"#define OUT {outt}")
+    w(f"#define AIN {_ctype(in_dtype)}")
     w(f"extern \"C\" __global__ __launch_bounds__(64) void {kernel_name}(")
-    w("    const REAL* __restrict__ A, long samples, OUT* __restrict__ B) {")
+    w("    const AIN* __restrict__ A, long samples, OUT* __restrict__ B) {")
     single = len(chunks) == 1
     R = tile_rows(F, out_dtype, rows) if single else 64
     if not 1 <= R <= 64:
@@ -520,7 +551,7 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     w(f"  const long s0 = (long)blockIdx.x * {R};")
     w("  const long s = s0 + lane;")
     w(f"  const bool valid = lane < {R} && s < samples;")
-    w(f"  const REAL* __restrict__ a = A + (valid ? s : 0) * {plan.a_width}L;")
+    w(f"  const AIN* __restrict__ a = A + (valid ? s : 0) * {plan.a_width}L;")
     w("  const long rem = samples - s0;")
     w(f"  const int rows = rem < {R} ? (int)rem : {R};")
     w("  switch (blockIdx.y) {")
@@ -537,7 +568,7 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
             emitted.add(n)
             if nd["kind"] == "leaf":
                 for c in range(nd["dim"]):
-                    w(f"    const REAL v{n}_{c} = valid ? a[{nd['a_offset'] + c}] : (REAL)0;")
+                    w(f"    const REAL v{n}_{c} = valid ? (REAL)a[{nd['a_offset'] + c}] : (REAL)0;")
                 return
             per = [[] for _ in range(nd["dim"])]
             if nd["kind"] == "sym":
@@ -602,5 +633,6 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     w("}")
     source = "\n".join(out) + "\n"
     meta = {"kernel": kernel_name, "chunks": len(chunks), "rows": R, "feature_count": F, "a_width": plan.a_width,
-            "dtype": dtype, "out_dtype": out_dtype, "hash": hashlib.sha256(source.encode()).hexdigest()[:16]}
+            "dtype": dtype, "out_dtype": out_dtype, "in_dtype": in_dtype,
+            "hash": hashlib.sha256(source.encode()).hexdigest()[:16]}
     return source, meta

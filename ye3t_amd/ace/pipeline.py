@@ -40,32 +40,44 @@ GENERATED_MAX_TERMS = 5000
 class ACEPipeline:
     """``dtype``: storage type of the inputs and of the B-features.
 
-    ``accumulate``: type of the density ``A`` and of all arithmetic (default:
-    ``dtype``).  "f64" with ``dtype="f32"`` keeps fp32 inputs and outputs but
-    carries the density and the CG products in fp64, for plans whose features
-    cancel too strongly for fp32 intermediates.
+    ``accumulate``: type of all arithmetic, and of the density ``A`` unless
+    ``density`` says otherwise (default: ``dtype``).  "f64" with
+    ``dtype="f32"`` keeps fp32 inputs and outputs but carries the density and
+    the CG products in fp64, for plans whose features cancel too strongly for
+    fp32 intermediates.
+
+    ``density``: storage type of ``A`` (default: ``accumulate``).  "f32" with
+    ``accumulate="f64"`` accumulates the density in fp64, rounds each value
+    once to fp32 for storage (half the density bytes) and converts it back to
+    fp64 for the product; this needs a plan with a generated product kernel.
 
     ``kernel``: "auto" (generated kernel when the plan is small enough),
     "generated" or "interpreter" (the generic table-driven product kernel)."""
 
     def __init__(self, feature_spec, dtype="f32", max_slots=None, plan=None, kernel="auto", max_live=None,
-                 accumulate=None):
+                 accumulate=None, density=None):
         self.spec = feature_spec
         self.dtype = dtype
         self.accumulate = accumulate or dtype
+        self.density_dtype = density or self.accumulate
         if dtype not in ("f32", "f64") or self.accumulate not in ("f32", "f64") or (
                 dtype == "f64" and self.accumulate == "f32"):
             raise ValueError(f"unsupported precision: dtype {dtype!r}, accumulate {accumulate!r}")
+        if self.density_dtype not in ("f32", "f64") or (self.accumulate == "f32" and self.density_dtype == "f64"):
+            raise ValueError(f"unsupported density dtype {density!r} for {self.accumulate} arithmetic")
+        if kernel not in {"auto", "generated", "interpreter"}:
+            raise ValueError(f"unknown product kernel {kernel!r}")
         self.plan = plan if plan is not None else ProductPlan(feature_spec)
+        terms = sum(len(nd.get("terms", ())) for nd in self.plan.nodes)
+        use_gen = kernel == "generated" or (kernel == "auto" and terms <= GENERATED_MAX_TERMS)
+        if self.density_dtype != self.accumulate and not use_gen:
+            raise ValueError(f"a {self.density_dtype} density with {self.accumulate} arithmetic needs a generated "
+                             f"product kernel (plans of at most {GENERATED_MAX_TERMS} terms)")
         self.program = compile_program(self.plan, self.accumulate, max_slots)
-        self.handle = native.ProductPlanHandle(self.program, out_dtype=dtype)
+        self.handle = native.ProductPlanHandle(self.program, out_dtype=dtype, in_dtype=self.density_dtype)
         self._columns = os.environ.get("YE3T_PRODUCT_COLUMNS", "1") != "0"
         self._At = None  # (key, column-major density buffer) of the interpreter path
         self._adjoint_handle = None  # program of the interpreter plans' reverse mode
-        terms = sum(len(nd.get("terms", ())) for nd in self.plan.nodes)
-        use_gen = kernel == "generated" or (kernel == "auto" and terms <= GENERATED_MAX_TERMS)
-        if kernel not in {"auto", "generated", "interpreter"}:
-            raise ValueError(f"unknown product kernel {kernel!r}")
         self.kernel = "interpreter"
         if use_gen:
             from ye3t_amd.ace.codegen import generate
@@ -84,10 +96,11 @@ class ACEPipeline:
                 policy = os.environ.get("YE3T_PRODUCT_STORE_POLICY")  # cache-policy bits (tuning)
                 source, meta = generate_persistent(self.plan, self.accumulate, out_dtype=dtype,
                                                    waves=int(waves) if waves else 2,
-                                                   store_policy=int(policy) if policy else 2)
+                                                   store_policy=int(policy) if policy else 2,
+                                                   in_dtype=self.density_dtype)
             else:
                 source, meta = generate(self.plan, self.accumulate, max_live, out_dtype=dtype,
-                                        rows=int(rows) if rows else None)
+                                        rows=int(rows) if rows else None, in_dtype=self.density_dtype)
             self.handle.attach_generated(source, meta)
             self.kernel = "generated"
 
@@ -95,7 +108,10 @@ class ACEPipeline:
     def feature_count(self):
         return self.plan.feature_count
 
-    def density(self, dev_inp, out=None):
+    def density(self, dev_inp, out=None, validate=True):
+        """Stage 1.  ``validate`` range-checks the CSR offsets and the neighbour
+        and species indices before the launch (a caller that reuses validated
+        inputs, such as a timing loop, may skip it)."""
         import torch
 
         return native.ace_density_forward(
@@ -105,7 +121,8 @@ class ACEPipeline:
             lam=float(dev_inp["lambda"]), epsilon=float(dev_inp.get("epsilon", 1e-12)),
             species=dev_inp.get("species"), node_features=dev_inp.get("node_features"),
             radial_mix=dev_inp.get("radial_mix"), out=out,
-            out_dtype=torch.float64 if self.accumulate == "f64" else torch.float32)
+            out_dtype=torch.float64 if self.density_dtype == "f64" else torch.float32,
+            accumulate_dtype=torch.float64 if self.accumulate == "f64" else torch.float32, validate=validate)
 
     def product(self, A_rows, out=None):
         """B-features of the density rows.  Interpreter plans read a column-major
@@ -160,7 +177,7 @@ class ACEPipeline:
 
             waves = os.environ.get("YE3T_ADJOINT_WAVES")  # waves sharing a tile (tuning)
             source, meta = generate_adjoint(self.plan, self.accumulate, grad_dtype=self.dtype,
-                                            waves=int(waves) if waves else 2)
+                                            waves=int(waves) if waves else 2, in_dtype=self.density_dtype)
             self.handle.attach_adjoint(source, meta)
         return self.handle.adjoint(A_rows, gB, out=out)
 
@@ -188,7 +205,8 @@ class ACEPipeline:
             if getattr(self.handle, "readout", None) is None:
                 from ye3t_amd.ace.codegen import generate_readout
 
-                source, meta = generate_readout(self.plan, self.accumulate, out_dtype=self.dtype)
+                source, meta = generate_readout(self.plan, self.accumulate, out_dtype=self.dtype,
+                                                in_dtype=self.density_dtype)
                 self.handle.attach_readout(source, meta)
             w = weight.to(torch.float64 if self.accumulate == "f64" else torch.float32).contiguous()
             self.last_linear_backend = "fused_generated"
@@ -205,8 +223,8 @@ class ACEPipeline:
         self.last_linear_backend = "materialized_blocks"
         return out
 
-    def forward(self, dev_inp, channelwise=False, A_out=None, B_out=None):
-        A = self.density(dev_inp, out=A_out)
+    def forward(self, dev_inp, channelwise=False, A_out=None, B_out=None, validate=True):
+        A = self.density(dev_inp, out=A_out, validate=validate)
         rows = A.reshape(-1, self.plan.a_width) if channelwise else A.reshape(A.shape[0], -1)
         if rows.shape[1] != self.plan.a_width:
             raise ValueError(f"density row width {rows.shape[1]} != plan width {self.plan.a_width}")

@@ -132,7 +132,8 @@ class Config:
     feature_spec: ACEFeatureSpec = None
     dtypes: tuple = ("f64",)
     channelwise: bool = False       # samples are (atom, channel) rows of A
-    accumulate: str = None          # type of A and of the arithmetic (None: the storage dtype)
+    accumulate: str = None          # type of the arithmetic (None: the storage dtype)
+    density_dtype: str = None       # storage type of A (None: the arithmetic type)
     note: str = ""
 
     def samples(self):
@@ -157,10 +158,11 @@ def config(config_id, *, atom_count=None):
     if config_id == 4:
         d = DensityWorkload(atom_count or 50000, 24, 5.0, 0.8, 8, 3, node_channels=16, config_id=4)
         spec = ACEFeatureSpec(channel_count=1, l_max=3, nu_max=3, nu_min=3, targets=(0, 1, 2))
-        # fp32 storage, fp64 intermediates: over the full 800 000 samples a density
-        # accumulated in fp32 leaves 4.8e-5 column error in B (fp64 A: 5e-6)
+        # fp32 storage, fp64 arithmetic: over the full 800 000 samples a density
+        # accumulated in fp32 leaves 4.8e-5 column error in B, while an fp64
+        # accumulation rounded once to an fp32 density leaves 1.3e-5 (fp64 A: 5e-6)
         return Config(4, "equivariant-message-couplings", d, spec, ("f32",), channelwise=True,
-                      accumulate="f64")
+                      accumulate="f64", density_dtype="f32")
     if config_id == 5:
         d = DensityWorkload(atom_count or 200000, 48, 5.5, 0.8, 12, 6, species_count=8, config_id=5)
         spec = ACEFeatureSpec(channel_count=104, l_max=6, nu_max=4, targets=(0, 1, 2), parity="any",

@@ -236,6 +236,17 @@ extern "C" {
 
 int ye3t_hip_abi_version(void) { return YE3T_HIP_ABI_VERSION; }
 
+int ye3t_hip_has_hip(void) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return count > 0 ? 1 : 0;
+}
+
+int ye3t_hip_has_cpu(void) { return 0; }
+
 const char* ye3t_hip_last_error(void) { return g_last_error.c_str(); }
 
 const char* ye3t_hip_last_density_kernel(void) { return g_last_density_kernel; }

@@ -302,7 +302,7 @@ int launch_mode(const ye3t_density_args* a, void* A, hipStream_t s) {
 }
 
 int launch_density_mfma(const ye3t_density_args* a, void* A, hipStream_t stream);
-template <typename In>
+template <typename In, typename Out>
 int launch_density_mfma64(const ye3t_density_args* a, void* A, hipStream_t stream);
 
 template <typename Real, typename In>
@@ -314,7 +314,7 @@ int dispatch_density(const ye3t_density_args* a, void* A, hipStream_t s) {
     clear_error();
   } else {
     // so do fp64 densities of the compiled shapes (fp64 MFMA)
-    const int rc = launch_density_mfma64<In>(a, A, s);
+    const int rc = launch_density_mfma64<In, double>(a, A, s);
     if (rc != YE3T_EUNSUPPORTED) return rc;
     clear_error();
   }
@@ -344,8 +344,19 @@ extern "C" int ye3t_hip_ace_density_forward(const ye3t_density_args* a, void* A,
   YE3T_REQUIRE(a->edge_count == 0 || (a->edge_vectors && (a->neighbors || (!a->species && !a->node_features))),
                "NULL edge arrays");
   const int out_dtype = a->out_dtype < 0 ? a->dtype : a->out_dtype;
-  if (a->dtype == YE3T_F64 && out_dtype == YE3T_F64) return dispatch_density<double, double>(a, A, as_stream(stream));
-  if (a->dtype == YE3T_F32 && out_dtype == YE3T_F32) return dispatch_density<float, float>(a, A, as_stream(stream));
-  if (a->dtype == YE3T_F32 && out_dtype == YE3T_F64) return dispatch_density<double, float>(a, A, as_stream(stream));
-  return set_error(YE3T_EDTYPE, "unsupported dtype pair (inputs %d, density %d)", a->dtype, out_dtype);
+  const int acc_dtype = a->accumulate_dtype < 0 ? out_dtype : a->accumulate_dtype;
+  if (acc_dtype == out_dtype) {
+    if (a->dtype == YE3T_F64 && out_dtype == YE3T_F64) return dispatch_density<double, double>(a, A, as_stream(stream));
+    if (a->dtype == YE3T_F32 && out_dtype == YE3T_F32) return dispatch_density<float, float>(a, A, as_stream(stream));
+    if (a->dtype == YE3T_F32 && out_dtype == YE3T_F64) return dispatch_density<double, float>(a, A, as_stream(stream));
+  } else if (a->dtype == YE3T_F32 && out_dtype == YE3T_F32 && acc_dtype == YE3T_F64) {
+    // fp64 accumulation rounded once to an fp32 density: the fp64 matrix-core kernels
+    const int rc = launch_density_mfma64<float, float>(a, A, as_stream(stream));
+    if (rc != YE3T_EUNSUPPORTED) return rc;
+    return set_error(YE3T_EUNSUPPORTED,
+                     "an fp32 density accumulated in fp64 is built for the fp64 matrix-core shapes only "
+                     "(node features at 16 channels, n_max 8, l_max 3; single channel at (3, 8), (4, 10), (6, 12))");
+  }
+  return set_error(YE3T_EDTYPE, "unsupported dtype combination (inputs %d, density %d, accumulation %d)", a->dtype,
+                   out_dtype, acc_dtype);
 }

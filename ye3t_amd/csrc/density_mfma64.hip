@@ -53,7 +53,7 @@ typedef double mfma_d4 __attribute__((ext_vector_type(4)));
 // so 16 lanes reading one column of 16 rows hit 16 distinct bank pairs
 constexpr int kPitch64 = 67;
 
-template <typename In>
+template <typename In, typename Out>
 struct Density64Params {
   int64_t N;
   const int64_t* __restrict__ offsets;
@@ -66,7 +66,7 @@ struct Density64Params {
   double lambda;
   double den;                    // expm1(lambda)
   double eps;
-  double* __restrict__ A;
+  Out* __restrict__ A;           // fp64, or fp32 rounded once from the fp64 accumulators
 };
 
 // offsets[i] through the constant address space: a scalar load (the CSR
@@ -117,8 +117,8 @@ __device__ inline void radial_row64(double r, const P& p, double* out, int strid
   }
 }
 
-template <int MODE, typename In, int LMAX, int NMAX, int C>
-__global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<In> p, NormTable nt) {
+template <int MODE, typename In, typename Out, int LMAX, int NMAX, int C>
+__global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<In, Out> p, NormTable nt) {
   constexpr int NR = NMAX + 1;
   constexpr int LW = (LMAX + 1) * (LMAX + 1);
   constexpr int ROWS = MODE == 2 ? C : NR;
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
   }
   __syncthreads();
   const int64_t e_begin = offset_at(p.offsets, a_begin), e_end = offset_at(p.offsets, a_end);
-  double* __restrict__ Aw = p.A;
+  Out* __restrict__ Aw = p.A;
 
   // k-blocks whose operands are read from LDS in one batch
   constexpr int KB = (RT + CT <= 2) ? 16 : ((RT + CT <= 5) ? 8 : 4);
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
   int64_t lo = e_begin, hi = offset_at(p.offsets, a_begin + 1);
 
   auto store_atom = [&](int64_t atom) {
-    double* __restrict__ dst = Aw + atom * (ROWS * LW);
+    Out* __restrict__ dst = Aw + atom * (ROWS * LW);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
         for (int v = 0; v < 4; ++v) {
           const int row = rt * 16 + kq + 4 * v, col = ct * 16 + cc;
           if ((ROWS % 16 == 0 || row < ROWS) && (LW % 16 == 0 || col < LW))
-            dst[row * LW + col] = acc[0][rt][ct][v] + acc[1][rt][ct][v];
+            dst[row * LW + col] = Out(acc[0][rt][ct][v] + acc[1][rt][ct][v]);
         }
   };
   auto in_chunk = [&](int64_t t) { return t < e_end && lane < e_end - t; };
@@ -317,8 +317,8 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
 //            of the density product.  Atoms are walked with wave-relative
 //            32-bit edge indices and scalar compares; only a k-block that
 //            straddles an atom boundary is masked per lane.
-template <typename In>
-__global__ __launch_bounds__(64) void ace_density_mfma64_channel_kernel(Density64Params<In> p, NormTable nt) {
+template <typename In, typename Out>
+__global__ __launch_bounds__(64) void ace_density_mfma64_channel_kernel(Density64Params<In, Out> p, NormTable nt) {
   constexpr int C = 16, NR = 9, LMAX = 3, LW = 16;
   constexpr int YP = 65;                         // pitch (doubles) of Yt and Gt, odd
   constexpr int HP = sizeof(In) == 4 ? 68 : 66;  // pitch (elements) of Ht: rows 16-byte aligned
@@ -356,11 +356,11 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_channel_kernel(Density6
   const int na = int(a_end - a_begin);
   int a = 0;
   int lo = 0, hi = int(offset_at(p.offsets, a_begin + 1) - e_begin);
-  double* __restrict__ Aw = p.A + a_begin * (C * LW) + lane;
+  Out* __restrict__ Aw = p.A + a_begin * (C * LW) + lane;
   auto store_atom = [&](int atom) {
-    double* __restrict__ dst = Aw + int64_t(atom) * (C * LW);
+    Out* __restrict__ dst = Aw + int64_t(atom) * (C * LW);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) dst[64 * v] = acc[v];  // row c = kq + 4 v, column lm = cc
+    for (int v = 0; v < 4; ++v) dst[64 * v] = Out(acc[v]);  // row c = kq + 4 v, column lm = cc
   };
   // next atom: its edge range, or an empty range past the wave's edges
   auto next_atom = [&]() {
@@ -504,9 +504,9 @@ static int64_t density_waves(int64_t atoms, const void* kernel) {
 }
 
 
-template <int MODE, typename In, int LMAX, int NMAX, int C>
+template <int MODE, typename In, typename Out, int LMAX, int NMAX, int C>
 int launch64(const ye3t_density_args* a, void* A, hipStream_t stream) {
-  Density64Params<In> p;
+  Density64Params<In, Out> p;
   p.N = a->atom_count;
   p.offsets = a->row_offsets;
   p.nbr = a->neighbors;
@@ -517,21 +517,21 @@ int launch64(const ye3t_density_args* a, void* A, hipStream_t stream) {
   p.lambda = a->lambda;
   p.den = std::expm1(a->lambda);
   p.eps = a->epsilon;
-  p.A = static_cast<double*>(A);
+  p.A = static_cast<Out*>(A);
   // about three 64-edge chunks per wave
   const int64_t grid =
-      density_waves(p.N, reinterpret_cast<const void*>(&ace_density_mfma64_kernel<MODE, In, LMAX, NMAX, C>));
+      density_waves(p.N, reinterpret_cast<const void*>(&ace_density_mfma64_kernel<MODE, In, Out, LMAX, NMAX, C>));
   p.waves = grid;
-  hipLaunchKernelGGL((ace_density_mfma64_kernel<MODE, In, LMAX, NMAX, C>), dim3(unsigned(grid)), dim3(64), 0,
+  hipLaunchKernelGGL((ace_density_mfma64_kernel<MODE, In, Out, LMAX, NMAX, C>), dim3(unsigned(grid)), dim3(64), 0,
                      stream, p, norm_table());
   set_density_kernel("ace_density_mfma64_kernel");
   return check_launch("ace_density_mfma64_kernel");
 }
 
 
-template <typename In>
+template <typename In, typename Out>
 int launch64_channel(const ye3t_density_args* a, void* A, hipStream_t stream) {
-  Density64Params<In> p;
+  Density64Params<In, Out> p;
   p.N = a->atom_count;
   p.offsets = a->row_offsets;
   p.nbr = a->neighbors;
@@ -542,19 +542,21 @@ int launch64_channel(const ye3t_density_args* a, void* A, hipStream_t stream) {
   p.lambda = a->lambda;
   p.den = std::expm1(a->lambda);
   p.eps = a->epsilon;
-  p.A = static_cast<double*>(A);
-  const int64_t grid = density_waves(p.N, reinterpret_cast<const void*>(&ace_density_mfma64_channel_kernel<In>));
+  p.A = static_cast<Out*>(A);
+  const int64_t grid =
+      density_waves(p.N, reinterpret_cast<const void*>(&ace_density_mfma64_channel_kernel<In, Out>));
   p.waves = grid;
-  hipLaunchKernelGGL((ace_density_mfma64_channel_kernel<In>), dim3(unsigned(grid)), dim3(64), 0, stream, p,
+  hipLaunchKernelGGL((ace_density_mfma64_channel_kernel<In, Out>), dim3(unsigned(grid)), dim3(64), 0, stream, p,
                      norm_table());
   set_density_kernel("ace_density_mfma64_channel_kernel");
   return check_launch("ace_density_mfma64_channel_kernel");
 }
 
 
-// fp64 densities of the compiled shapes; YE3T_EUNSUPPORTED (nothing launched)
-// for the others, which run on the VALU kernel.
-template <typename In>
+// Densities accumulated in fp64 for the compiled shapes, stored as Out (fp64,
+// or fp32 rounded once from the fp64 accumulators); YE3T_EUNSUPPORTED (nothing
+// launched) for the others, which run on the VALU kernel.
+template <typename In, typename Out>
 int launch_density_mfma64(const ye3t_density_args* a, void* A, hipStream_t stream) {
   if (a->species) return YE3T_EUNSUPPORTED;
   if (env_int64("YE3T_DENSITY_MFMA64", 1) == 0) return YE3T_EUNSUPPORTED;
@@ -566,19 +568,20 @@ int launch_density_mfma64(const ye3t_density_args* a, void* A, hipStream_t strea
       // edge indices need E < 2^31); YE3T_DENSITY_MIX_MFMA=0 selects the
       // generic kernel with the radial mix on the VALU
       if (env_int64("YE3T_DENSITY_MIX_MFMA", 1) != 0 && a->edge_count < (int64_t(1) << 31))
-        return launch64_channel<In>(a, A, stream);
-      return launch64<2, In, 3, 8, 16>(a, A, stream);
+        return launch64_channel<In, Out>(a, A, stream);
+      return launch64<2, In, Out, 3, 8, 16>(a, A, stream);
     }
     return YE3T_EUNSUPPORTED;
   }
   if (a->channel_count != 1) return YE3T_EUNSUPPORTED;
-  if (L == 3 && Nm == 8) return launch64<0, In, 3, 8, 1>(a, A, stream);
-  if (L == 4 && Nm == 10) return launch64<0, In, 4, 10, 1>(a, A, stream);
-  if (L == 6 && Nm == 12) return launch64<0, In, 6, 12, 1>(a, A, stream);
+  if (L == 3 && Nm == 8) return launch64<0, In, Out, 3, 8, 1>(a, A, stream);
+  if (L == 4 && Nm == 10) return launch64<0, In, Out, 4, 10, 1>(a, A, stream);
+  if (L == 6 && Nm == 12) return launch64<0, In, Out, 6, 12, 1>(a, A, stream);
   return YE3T_EUNSUPPORTED;
 }
 
-template int launch_density_mfma64<float>(const ye3t_density_args*, void*, hipStream_t);
-template int launch_density_mfma64<double>(const ye3t_density_args*, void*, hipStream_t);
+template int launch_density_mfma64<float, double>(const ye3t_density_args*, void*, hipStream_t);
+template int launch_density_mfma64<double, double>(const ye3t_density_args*, void*, hipStream_t);
+template int launch_density_mfma64<float, float>(const ye3t_density_args*, void*, hipStream_t);
 
 }  // namespace ye3t

@@ -23,8 +23,9 @@
 #include "common.h"
 
 struct ye3t_hip_product_plan {
-  int dtype;      // A, coefficients and arithmetic
+  int dtype;      // coefficients and arithmetic (and A unless in_dtype differs)
   int out_dtype;  // B
+  int in_dtype;   // A (fp32 rows into fp64 arithmetic: generated kernels only)
   int64_t a_width;
   int64_t feature_count;
   int64_t chunk_count;
@@ -171,10 +172,10 @@ __global__ __launch_bounds__(kLanes) void product_kernel(
 // stores.
 //
 // A workgroup is one wave that runs one chunk over tiles_per_group
-// consecutive 64-sample tiles (lane = sample).  The chunk's records, flags,
-// density-load list and output slots are staged in LDS once; records are read
-// back with broadcast LDS reads, which return in order, so the next group's
-// records are in flight while the current group computes.  The workspace is
+// consecutive 64-sample tiles (lane = sample).  The chunk's density-load list
+// and output slots are staged in LDS once; its records and flags are
+// wave-uniform and read with scalar loads, one group ahead, so the next
+// group's records are in flight while the current group computes.  The workspace is
 // [slot][64] values (slots + 2 for the constant 1 and the sink).  The next
 // tile's density values are loaded into registers while the current tile's
 // terms run.  The density is read row-major (A[s * lda + col]) or column-major
@@ -209,8 +210,8 @@ __device__ inline void lds_add(unsigned char* base, uint32_t off, Real v) {
 
 struct StreamLayout {
   uint32_t ws_bytes;    // workspace: (slots + 2) * 64 * elem
-  uint32_t rec_at;      // records (16 B each)
-  uint32_t flag_at;     // flag words
+  uint32_t rec_at;      // end of the LDS-resident part (records stay in global memory)
+  uint32_t flag_at;     // == rec_at (flag words stay in global memory)
   uint32_t load_at;     // (dst offset, column) pairs
   uint32_t out_at;      // output slot byte offsets
   uint32_t one_off;     // workspace byte offset of the slot holding 1
@@ -838,14 +839,13 @@ bool build_stream(const ye3t_product_plan_desc* d, std::vector<uint4>& recs, std
   at = up16(at + 16 * max_loads);
   lay.out_at = uint32_t(at);
   at = up16(at + 4 * max_out);
-  // records and flags last: the forward kernel reads them through the scalar
-  // cache and allocates LDS only below rec_at; the reverse mode stages them
+  // records and flags stay in global memory (both kernels read them through
+  // the scalar cache): rec_at and flag_at mark the end of the LDS a wave uses
   lay.rec_at = uint32_t(at);
-  at = up16(at + 16 * max_recs);
   lay.flag_at = uint32_t(at);
-  at = up16(at + 4 * max_recs);
   lay.one_off = one;
   lds_bytes = at;
+  (void)max_recs;
   return at <= 64 * 1024;
 }
 
@@ -965,7 +965,11 @@ int validate_plan_desc(const ye3t_product_plan_desc* d) {
   const int out_dtype = d->out_dtype < 0 ? d->dtype : d->out_dtype;
   YE3T_REQUIRE(out_dtype == d->dtype || (d->dtype == YE3T_F64 && out_dtype == YE3T_F32),
                "unsupported output dtype %d for a plan of dtype %d", d->out_dtype, d->dtype);
+  const int in_dtype = d->in_dtype < 0 ? d->dtype : d->in_dtype;
+  YE3T_REQUIRE(in_dtype == d->dtype || (d->dtype == YE3T_F64 && in_dtype == YE3T_F32),
+               "unsupported density dtype %d for a plan of dtype %d", d->in_dtype, d->dtype);
   (void)out_dtype;
+  (void)in_dtype;
   YE3T_REQUIRE(d->chunk_count >= 1 && d->a_width >= 1 && d->a_width <= 65536 && d->feature_count >= 1,
                "bad plan sizes");
   YE3T_REQUIRE(d->workspace_slots >= 1 && d->workspace_slots <= 65535, "bad workspace size");
@@ -1078,6 +1082,8 @@ int ye3t_hip_product_adjoint_stream(const ye3t_hip_product_plan* p, const void* 
   YE3T_REQUIRE(samples >= 0, "negative sample count");
   if (samples == 0) return YE3T_OK;
   YE3T_REQUIRE(p->use_stream, "this plan has no term stream (workspace too large)");
+  if (p->in_dtype != p->dtype)
+    return set_error(YE3T_EUNSUPPORTED, "the term stream reads densities of the plan's dtype only");
   YE3T_REQUIRE(A && gB && gA, "NULL input or output");
   const int64_t tiles = (samples + kLanes - 1) / kLanes;
   if (columns) {
@@ -1125,6 +1131,8 @@ int ye3t_hip_product_forward_columns(const ye3t_hip_product_plan* p, const void*
   if (samples == 0) return YE3T_OK;
   YE3T_REQUIRE(At && B, "NULL input or output");
   YE3T_REQUIRE(p->use_stream, "this plan has no term stream (workspace too large); use ye3t_hip_product_forward");
+  if (p->in_dtype != p->dtype)
+    return set_error(YE3T_EUNSUPPORTED, "the term stream reads densities of the plan's dtype only");
   YE3T_REQUIRE(ld >= (samples + kLanes - 1) / kLanes * kLanes, "ld must cover whole 64-sample tiles");
   return launch_stream<true>(p, At, ld, samples, B, stream);
 }
@@ -1167,6 +1175,7 @@ int ye3t_hip_product_plan_create(const ye3t_product_plan_desc* d, ye3t_hip_produ
   auto* p = new ye3t_hip_product_plan();
   p->dtype = d->dtype;
   p->out_dtype = out_dtype;
+  p->in_dtype = d->in_dtype < 0 ? d->dtype : d->in_dtype;
   p->a_width = d->a_width;
   p->feature_count = d->feature_count;
   p->chunk_count = C;
@@ -1334,6 +1343,10 @@ int ye3t_hip_product_forward(const ye3t_hip_product_plan* p, const void* A, int6
                                          1, 0, as_stream(stream), args, nullptr));
     return YE3T_OK;
   }
+  if (p->in_dtype != p->dtype)
+    return set_error(YE3T_EUNSUPPORTED,
+                     "an fp32 density with fp64 arithmetic runs on an attached generated kernel only "
+                     "(and, for a persistent one, a 16-byte aligned B)");
   const int64_t grid = tiles * p->chunk_count;
   YE3T_REQUIRE(grid <= int64_t(0x7FFFFFFF), "too many samples for one launch");
   const size_t lds = product_lds_bytes(p);

@@ -12,19 +12,26 @@ import os
 from ye3t_amd.runtime import native
 
 _NATIVE_EXECUTION_PLAN_ABI = 42
-HIP_OPERATIONS = (
+
+# Operations this library runs on the device, under the reference's operation
+# names (the ``operations`` tuple of ``native_execution_plan_capabilities``,
+# reference ``execution_plan.py:6662-6850``), then this backend's fused ops.
+REFERENCE_OPERATIONS = (
     "cheb_exp_cos_radial_table_with_derivative",
-    "spherical_harmonics_table_with_derivative",
+    "real_spherical_harmonics_table_with_derivative",
     "density_accumulate",
     "density_accumulate_adjoint",
-    "ace_density_forward",
     "symmetric_power_monomial",
-    "evaluate_factorized_schedule",
+)
+FUSED_OPERATIONS = (
+    "ace_density_forward",
     "ace_product_forward",
-    "factorized_angular_linear",
-    "factorized_angular_adjoint",
+    "ace_product_adjoint",
+    "ace_product_linear",
+    "evaluate_factorized_schedule",
     "neighbor_list",
 )
+HIP_OPERATIONS = REFERENCE_OPERATIONS + FUSED_OPERATIONS
 
 
 def _require_device(t, name):
@@ -34,9 +41,16 @@ def _require_device(t, name):
 
 
 def _backend(backend, allowed):
+    """Validate a reference ``backend=`` argument.  ``"reference"`` (the
+    reference's pure-Torch implementation) is a known value that this device
+    branch does not carry: it raises ``NotImplementedError`` naming the
+    reference's own runtime instead of running anything else."""
     backend = str(backend)
+    if backend == "reference":
+        raise NotImplementedError("backend='reference' selects the reference's Torch implementation "
+                                  "(ye3t.runtime); ye3t_amd runs the native HIP branch only")
     if backend not in allowed:
-        raise ValueError(f"backend must be one of {sorted(allowed)}")
+        raise ValueError(f"backend must be one of {sorted(allowed | {'reference'})}")
     return backend
 
 
@@ -66,6 +80,40 @@ def spherical_harmonics_table_with_derivative(edge_vectors, maximum_angular_mome
         raise ValueError("maximum_angular_momentum must be non-negative")
     _require_device(edge_vectors, "spherical_harmonics_table_with_derivative")
     return native.real_sph_table(edge_vectors.contiguous(), maximum_angular_momentum, epsilon)
+
+
+def validate_density_csr(row_offsets, neighbors, atom_count, edge_count, *, species=None, species_count=None):
+    """Host-side range checks of the fused density's index inputs (any device).
+
+    ``row_offsets`` must be int64 ``[N+1]``, start at 0, be non-decreasing and
+    end at ``edge_count``; ``neighbors`` int64 ``[E]`` in ``[0, N)``;
+    ``species`` int32 ``[N]`` in ``[0, species_count)``.  The kernels gather
+    through these indices without bounds checks, as the reference's do after
+    its own ``TORCH_CHECK`` guards (``execution_plan_cuda.cu:37-197``), so bad
+    indices raise here before any launch.  Each check reduces on the tensor's
+    device and reads one scalar back.
+    """
+    import torch
+
+    atom_count, edge_count = int(atom_count), int(edge_count)
+    if row_offsets.dtype != torch.int64 or tuple(row_offsets.shape) != (atom_count + 1,):
+        raise ValueError(f"row_offsets must be int64 [{atom_count + 1}]")
+    first, last = int(row_offsets[0]), int(row_offsets[-1])
+    if first != 0 or last != edge_count:
+        raise ValueError(f"row_offsets must run from 0 to the edge count {edge_count} (got {first} .. {last})")
+    if atom_count > 0 and bool((row_offsets[1:] < row_offsets[:-1]).any()):
+        raise ValueError("row_offsets must be non-decreasing (edges sorted by centre)")
+    if neighbors is not None:
+        if neighbors.dtype != torch.int64 or tuple(neighbors.shape) != (edge_count,):
+            raise ValueError(f"neighbors must be int64 [{edge_count}]")
+        if edge_count and (int(neighbors.min()) < 0 or int(neighbors.max()) >= atom_count):
+            raise ValueError(f"neighbor index out of range [0, {atom_count})")
+    if species is not None:
+        if species.dtype != torch.int32 or tuple(species.shape) != (atom_count,):
+            raise ValueError(f"species must be int32 [{atom_count}]")
+        if atom_count and (int(species.min()) < 0 or int(species.max()) >= int(species_count)):
+            raise ValueError(f"species index out of range [0, {int(species_count)})")
+    return True
 
 
 def density_accumulate(edge_values, centers, atom_count, *, backend="auto"):
@@ -148,11 +196,20 @@ def symmetric_power_monomial_contraction(input, monomial_counts, output_offsets,
 
 
 def native_execution_plan_capabilities():
-    """Capability report (reference ``execution_plan.py:6118-6850``) with the HIP capability."""
+    """Capability report (reference ``execution_plan.py:6118-6850``) with the HIP capability.
+
+    Keys the reference's consumers test keep their meaning: ``cuda`` and
+    ``cuda_operations`` are False / empty (this library has no CUDA branch),
+    ``operations`` lists what runs natively under the reference's names, and
+    ``hip`` / ``hip_operations`` carry the new capability (``has_hip()`` of
+    the library, the counterpart of the reference's ``has_cuda()``).
+    """
     import torch
 
     available = native.available()
-    has_hip = bool(available and torch.version.hip is not None and torch.cuda.is_available())
+    has_hip = bool(available and torch.version.hip is not None and torch.cuda.is_available()
+                   and native.has_hip())
+    ops = HIP_OPERATIONS if available else ()
     report = {
         "schema": "ye3t_execution_plan_v1",
         "torch_independent_core_source": True,
@@ -161,14 +218,22 @@ def native_execution_plan_capabilities():
         "cuda": False,
         "cuda_operations": (),
         "hip": has_hip,
-        "hip_operations": HIP_OPERATIONS if available else (),
+        "hip_operations": ops if has_hip else (),
         "hip_arch": "gfx950",
+        "cuda_density_auto_min_work_items": None,
+        "hip_density_reduction": "csr_segment_deterministic",
+        "segmented_factorized_angular": False,
+        "heterogeneous_factorized_roots": False,
+        "triton_available": False,
+        "triton_cuda_available": False,
+        "triton_operations": (),
         "core_abi_version": native.ABI_VERSION if available else None,
         "minimum_core_abi_version": _NATIVE_EXECUTION_PLAN_ABI,
+        "factorized_workspace_metadata": "compiler_host_scalar_no_device_read",
         "dtypes": ("float32", "float64"),
         "analysis_orientation": "conjugate_transpose",
+        "operations": ops,
         "density_reduction": "csr_segment_deterministic",
-        "triton_available": False,
         "library_path": native.library_path(),
     }
     if has_hip:

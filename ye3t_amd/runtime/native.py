@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 51
+ABI_VERSION = 52
 _LIB = None
 
 F32, F64 = 0, 1
@@ -26,7 +26,8 @@ class DensityArgs(ctypes.Structure):
                 ("row_offsets", _vp), ("neighbors", _vp), ("edge_vectors", _vp), ("species", _vp),
                 ("node_features", _vp), ("radial_mix", _vp), ("channel_count", _i64),
                 ("max_radial_index", _i64), ("max_angular", _i64), ("cutoff", ctypes.c_double),
-                ("lambda_", ctypes.c_double), ("epsilon", ctypes.c_double), ("out_dtype", ctypes.c_int)]
+                ("lambda_", ctypes.c_double), ("epsilon", ctypes.c_double), ("out_dtype", ctypes.c_int),
+                ("accumulate_dtype", ctypes.c_int)]
 
 
 class ProductPlanDesc(ctypes.Structure):
@@ -34,7 +35,7 @@ class ProductPlanDesc(ctypes.Structure):
                 ("workspace_slots", _i64), ("chunk_word_offsets", _vp), ("chunk_coeff_offsets", _vp),
                 ("chunk_out_offsets", _vp), ("chunk_first_column", _vp), ("words", _vp), ("word_count", _i64),
                 ("coeffs", _vp), ("coeff_count", _i64), ("out_slots", _vp), ("out_slot_count", _i64),
-                ("out_dtype", ctypes.c_int)]
+                ("out_dtype", ctypes.c_int), ("in_dtype", ctypes.c_int)]
 
 
 class CellGrid(ctypes.Structure):
@@ -64,6 +65,8 @@ def lib():
         raise RuntimeError(f"ye3t_amd HIP library not built: {LIB_PATH} is missing (run __graft_entry__.build())")
     L = ctypes.CDLL(LIB_PATH)
     L.ye3t_hip_abi_version.restype = ctypes.c_int
+    L.ye3t_hip_has_hip.restype = ctypes.c_int
+    L.ye3t_hip_has_cpu.restype = ctypes.c_int
     L.ye3t_hip_last_error.restype = ctypes.c_char_p
     L.ye3t_hip_last_density_kernel.restype = ctypes.c_char_p
     L.ye3t_hip_device_caps.argtypes = [ctypes.c_int, ctypes.POINTER(Caps)]
@@ -114,7 +117,7 @@ def lib():
 
 
 EXPORTED_SYMBOLS = (
-    "ye3t_hip_abi_version", "ye3t_hip_last_error", "ye3t_hip_device_caps", "ye3t_hip_radial_table",
+    "ye3t_hip_abi_version", "ye3t_hip_has_hip", "ye3t_hip_has_cpu", "ye3t_hip_last_error", "ye3t_hip_device_caps", "ye3t_hip_radial_table",
     "ye3t_hip_real_sph_table", "ye3t_hip_density_accumulate_csr", "ye3t_hip_ace_density_forward",
     "ye3t_hip_symmetric_power_monomial", "ye3t_hip_evaluate_factorized_schedule",
     "ye3t_hip_product_plan_create", "ye3t_hip_product_plan_destroy", "ye3t_hip_product_forward",
@@ -160,6 +163,11 @@ def _dev(t, name):
 
 def _opt(t, name):
     return None if t is None else _dev(t, name)
+
+
+def has_hip():
+    """The library's ``ye3t_hip_has_hip()``: a HIP device is visible."""
+    return bool(lib().ye3t_hip_has_hip())
 
 
 def device_caps(device=0):
@@ -232,12 +240,17 @@ def density_accumulate_adjoint(atomic_adjoint, centers):
 
 def ace_density_forward(edge_vectors, row_offsets, neighbors, *, atom_count, channel_count, n_max, l_max, cutoff,
                         lam, epsilon=1e-12, species=None, node_features=None, radial_mix=None, out=None,
-                        out_dtype=None):
+                        out_dtype=None, accumulate_dtype=None, validate=True):
     """Fused stage 1; returns ``A[N, C, R, (l_max+1)^2]``.
 
     ``out_dtype`` (a torch dtype, default: that of the inputs) is the type of
-    ``A`` and of the accumulation; float64 with float32 inputs gives an fp64
-    density of fp32 data.
+    ``A``; float64 with float32 inputs gives an fp64 density of fp32 data.
+    ``accumulate_dtype`` (default: ``out_dtype``) is the type of the
+    accumulation: float64 with a float32 ``A`` accumulates in fp64 and rounds
+    each density value once to fp32.  ``validate`` range-checks the CSR
+    offsets, neighbour and species indices first (one device reduction and a
+    scalar read-back each); a caller that has already validated these inputs
+    may skip it.
     """
     import torch
 
@@ -254,6 +267,17 @@ def ace_density_forward(edge_vectors, row_offsets, neighbors, *, atom_count, cha
         raise ValueError("neighbors must be int64")
     if species is not None and species.dtype != torch.int32:
         raise ValueError("species must be int32")
+    if edge_vectors.ndim != 2 or edge_vectors.shape[1] != 3:
+        raise ValueError("edge_vectors must be [E, 3]")
+    if validate:
+        from ye3t_amd.runtime import validate_density_csr
+
+        validate_density_csr(row_offsets, neighbors, atom_count, int(edge_vectors.shape[0]), species=species,
+                             species_count=channel_count)
+    if node_features is not None and tuple(node_features.shape) != (atom_count, channel_count):
+        raise ValueError(f"node_features must be [{atom_count}, {channel_count}]")
+    if radial_mix is not None and tuple(radial_mix.shape) != (channel_count, n_max + 1):
+        raise ValueError(f"radial_mix must be [{channel_count}, {n_max + 1}]")
     for t, n in ((node_features, "node_features"), (radial_mix, "radial_mix")):
         if t is not None and t.dtype != edge_vectors.dtype:
             raise ValueError(f"{n} must have dtype {edge_vectors.dtype}")
@@ -263,7 +287,8 @@ def ace_density_forward(edge_vectors, row_offsets, neighbors, *, atom_count, cha
         edge_vectors=_dev(edge_vectors, "edge_vectors"), species=_opt(species, "species"),
         node_features=_opt(node_features, "node_features"), radial_mix=_opt(radial_mix, "radial_mix"),
         channel_count=int(channel_count), max_radial_index=int(n_max), max_angular=int(l_max),
-        cutoff=float(cutoff), lambda_=float(lam), epsilon=float(epsilon), out_dtype=_dtype_code(out))
+        cutoff=float(cutoff), lambda_=float(lam), epsilon=float(epsilon), out_dtype=_dtype_code(out),
+        accumulate_dtype=-1 if accumulate_dtype is None else (F64 if accumulate_dtype == torch.float64 else F32))
     _check(lib().ye3t_hip_ace_density_forward(ctypes.byref(args), _dev(out, "A"), _stream()),
            "ye3t_hip_ace_density_forward")
     return out
@@ -358,7 +383,7 @@ def rtc_compile(source, name="ye3t_generated.hip", arch="gfx950"):
     return blob
 
 
-def _plan_desc(program, out_dtype):
+def _plan_desc(program, out_dtype, in_dtype=None):
     """``ye3t_product_plan_desc`` of a compiled program and the arrays it points into."""
     keep = {k: np.ascontiguousarray(v) for k, v in program.items() if isinstance(v, np.ndarray)}
 
@@ -372,7 +397,8 @@ def _plan_desc(program, out_dtype):
         chunk_coeff_offsets=ptr("chunk_coeff_offsets"), chunk_out_offsets=ptr("chunk_out_offsets"),
         chunk_first_column=ptr("chunk_first_column"), words=ptr("words"), word_count=int(keep["words"].size),
         coeffs=ptr("coeffs"), coeff_count=int(keep["coeffs"].size), out_slots=ptr("out_slots"),
-        out_slot_count=int(keep["out_slots"].size), out_dtype=F64 if out_dtype == "f64" else F32)
+        out_slot_count=int(keep["out_slots"].size), out_dtype=F64 if out_dtype == "f64" else F32,
+        in_dtype=-1 if in_dtype is None else (F64 if in_dtype == "f64" else F32))
     return desc, keep
 
 
@@ -408,17 +434,22 @@ def stream_encode(program):
 class ProductPlanHandle:
     """Device-resident compiled product program (owns a ``ye3t_hip_product_plan``).
 
-    ``A`` and the arithmetic use the program's dtype; ``out_dtype`` ("f32" or
-    "f64", default: the same) is the type of the B-features.
+    The arithmetic uses the program's dtype; ``out_dtype`` ("f32" or "f64",
+    default: the same) is the type of the B-features and ``in_dtype`` (default:
+    the program's dtype) that of the density rows.  An "f32" density with an
+    "f64" program runs on attached generated kernels only.
     """
 
-    def __init__(self, program, out_dtype=None):
+    def __init__(self, program, out_dtype=None, in_dtype=None):
         self.program = program
         self.dtype = program["dtype"]
         self.out_dtype = out_dtype or self.dtype
+        self.in_dtype = in_dtype or self.dtype
         if self.out_dtype not in ("f32", "f64") or (self.dtype == "f32" and self.out_dtype == "f64"):
             raise ValueError(f"unsupported output dtype {self.out_dtype!r} for a {self.dtype} plan")
-        desc, self._keep = _plan_desc(program, self.out_dtype)
+        if self.in_dtype not in ("f32", "f64") or (self.dtype == "f32" and self.in_dtype == "f64"):
+            raise ValueError(f"unsupported density dtype {self.in_dtype!r} for a {self.dtype} plan")
+        desc, self._keep = _plan_desc(program, self.out_dtype, self.in_dtype)
         handle = ctypes.c_void_p()
         _check(lib().ye3t_hip_product_plan_create(ctypes.byref(desc), ctypes.byref(handle)),
                "ye3t_hip_product_plan_create")
@@ -438,7 +469,8 @@ class ProductPlanHandle:
         """Compile and attach a plan-specialised kernel (``ye3t_amd.ace.codegen``)."""
         if meta["feature_count"] != self.feature_count or meta["a_width"] != self.program["a_width"]:
             raise ValueError("generated kernel does not match this plan")
-        if meta["dtype"] != self.dtype or meta.get("out_dtype", meta["dtype"]) != self.out_dtype:
+        if meta["dtype"] != self.dtype or meta.get("out_dtype", meta["dtype"]) != self.out_dtype or \
+                meta.get("in_dtype", meta["dtype"]) != self.in_dtype:
             raise ValueError("generated kernel dtypes do not match this plan")
         blob = rtc_compile(source)
         self._code = ctypes.create_string_buffer(blob, len(blob))
@@ -465,7 +497,7 @@ class ProductPlanHandle:
 
         if A.ndim != 2 or int(A.shape[1]) != int(self.program["a_width"]):
             raise ValueError(f"A must be [samples, {self.program['a_width']}]")
-        want = torch.float64 if self.dtype == "f64" else torch.float32
+        want = torch.float64 if self.in_dtype == "f64" else torch.float32
         if A.dtype != want:
             raise ValueError(f"A must be {want} for this plan")
         out_t = torch.float64 if self.out_dtype == "f64" else torch.float32
@@ -542,7 +574,8 @@ class ProductPlanHandle:
         """Compile and attach a fused linear readout kernel (``codegen.generate_readout``)."""
         if meta["feature_count"] != self.feature_count or meta["a_width"] != self.program["a_width"]:
             raise ValueError("readout kernel does not match this plan")
-        if meta["dtype"] != self.dtype or meta.get("out_dtype", meta["dtype"]) != self.out_dtype:
+        if meta["dtype"] != self.dtype or meta.get("out_dtype", meta["dtype"]) != self.out_dtype or \
+                meta.get("in_dtype", meta["dtype"]) != self.in_dtype:
             raise ValueError("readout kernel dtypes do not match this plan")
         blob = rtc_compile(source)
         self._readout_code = ctypes.create_string_buffer(blob, len(blob))
@@ -555,7 +588,8 @@ class ProductPlanHandle:
         """Compile and attach a plan-specialised adjoint kernel (``codegen.generate_adjoint``)."""
         if meta["feature_count"] != self.feature_count or meta["a_width"] != self.program["a_width"]:
             raise ValueError("adjoint kernel does not match this plan")
-        if meta["dtype"] != self.dtype or meta.get("grad_dtype", meta["dtype"]) != self.out_dtype:
+        if meta["dtype"] != self.dtype or meta.get("grad_dtype", meta["dtype"]) != self.out_dtype or \
+                meta.get("in_dtype", meta["dtype"]) != self.in_dtype:
             raise ValueError("adjoint kernel dtypes do not match this plan")
         blob = rtc_compile(source)
         self._adjoint_code = ctypes.create_string_buffer(blob, len(blob))
@@ -569,7 +603,7 @@ class ProductPlanHandle:
         import torch
 
         W = int(self.program["a_width"])
-        a_t = torch.float64 if self.dtype == "f64" else torch.float32
+        a_t = torch.float64 if self.in_dtype == "f64" else torch.float32
         g_t = torch.float64 if self.out_dtype == "f64" else torch.float32
         if A.ndim != 2 or int(A.shape[1]) != W or A.dtype != a_t:
             raise ValueError(f"A must be [samples, {W}] of {a_t}")
@@ -591,8 +625,9 @@ class ProductPlanHandle:
         if A.ndim != 2 or int(A.shape[1]) != int(self.program["a_width"]):
             raise ValueError(f"A must be [samples, {self.program['a_width']}]")
         want = torch.float64 if self.dtype == "f64" else torch.float32
-        if A.dtype != want or weight.dtype != want or tuple(weight.shape) != (self.feature_count,):
-            raise ValueError(f"A and weight [{self.feature_count}] must be {want} for this plan")
+        a_t = torch.float64 if self.in_dtype == "f64" else torch.float32
+        if A.dtype != a_t or weight.dtype != want or tuple(weight.shape) != (self.feature_count,):
+            raise ValueError(f"A must be {a_t} and weight [{self.feature_count}] {want} for this plan")
         out_t = torch.float64 if self.out_dtype == "f64" else torch.float32
         S = int(A.shape[0])
         if out is None:
