@@ -349,6 +349,21 @@ int ye3t_hip_product_adjoint_stream(const ye3t_hip_product_plan* plan, const voi
                                     const void* gB, int64_t samples, void* workspace, int64_t workspace_bytes,
                                     void* gA, ye3t_stream_t stream);
 
+/* ye3t_hip_product_adjoint_stream without a workspace argument and without
+ * any allocation: the per-group partial gradients live in a static device
+ * array of 64 MiB (one per device the library runs on, held until the process
+ * ends), cleared by the call with a fill kernel.  Fewer groups than the
+ * workspace form may be used, so sums are grouped differently (same values to
+ * rounding).  YE3T_EUNSUPPORTED when one group's partials exceed 64 MiB
+ * (a_width * samples rounded up to 64 * element size).  Calls that overlap on
+ * one device (other streams or threads) share the array and race.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under stream capture, tight serving loops, allocation-free
+ * harnesses). */
+int ye3t_hip_product_adjoint_stream_noalloc(const ye3t_hip_product_plan* plan, const void* A, int64_t lda,
+                                            int columns, const void* gB, int64_t samples, void* gA,
+                                            ye3t_stream_t stream);
+
 /* 1 if the plan's interpreter is the term stream (LDS-staged records; the
  * plan also accepts ye3t_hip_product_forward_columns), 0 for the program-word
  * interpreter (workspaces too wide for the stream's 16-bit offsets or 64 KB of

@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -895,7 +896,10 @@ int launch_stream(const ye3t_hip_product_plan* p, const void* A, int64_t lda, in
 
 // Groups of chunks per tile for the stream adjoint (enough workgroups to fill
 // the device, partial blocks within 4 GiB) and the partial blocks' bytes.
-int64_t stream_adjoint_groups(const ye3t_hip_product_plan* p, int64_t samples, int64_t* bytes) {
+// `cap` bounds the partial blocks' bytes.  When one group alone exceeds it the
+// result is one group, or 0 with `strict` (a cap that cannot grow).
+int64_t stream_adjoint_groups(const ye3t_hip_product_plan* p, int64_t samples, int64_t* bytes,
+                              int64_t cap = int64_t(4) << 30, bool strict = false) {
   const int64_t tiles = (samples + kLanes - 1) / kLanes;
   const int64_t ldp = tiles * kLanes;
   const int64_t per_group = p->a_width * ldp * (p->dtype == YE3T_F64 ? 8 : 4);
@@ -903,9 +907,8 @@ int64_t stream_adjoint_groups(const ye3t_hip_product_plan* p, int64_t samples, i
   const int64_t target = (wg && *wg && std::atoll(wg) > 0) ? std::atoll(wg) : 8 * 256 * 6;
   int64_t groups = (target + tiles - 1) / tiles;
   if (groups > p->chunk_count) groups = p->chunk_count;
-  const int64_t cap = int64_t(4) << 30;
   if (groups * per_group > cap) groups = cap / per_group;
-  if (groups < 1) groups = 1;
+  if (groups < 1) groups = (strict && per_group > cap) ? 0 : 1;
   if (bytes) *bytes = groups * per_group;
   return groups;
 }
@@ -1022,6 +1025,36 @@ int validate_plan_desc(const ye3t_product_plan_desc* d) {
   return YE3T_OK;
 }
 
+// Scratch of ye3t_hip_product_adjoint_stream_noalloc: the per-group partial
+// density gradients live in this file-scope device array instead of a
+// caller's or the library's allocation.  Each device the library runs on
+// holds its own copy until the process ends.  Host code never uses the
+// array's name as an address: the device address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+constexpr int64_t kNoAllocScratchBytes = int64_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on device `dev` (the current device).
+int scratch_address(int dev, void** out) {
+  YE3T_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "device %d beyond the scratch table", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_address[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      return set_error(YE3T_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                       hipGetErrorString(e));
+    }
+    g_scratch_address[dev] = ptr;
+  }
+  *out = g_scratch_address[dev];
+  return YE3T_OK;
+}
+
 }  // namespace ye3t
 
 using namespace ye3t;
@@ -1099,6 +1132,47 @@ int ye3t_hip_product_adjoint_stream(const ye3t_hip_product_plan* p, const void* 
   const hipStream_t s = as_stream(stream);
   return columns ? launch_stream_adjoint<true>(p, A, lda, gB, samples, workspace, groups, gA, s)
                  : launch_stream_adjoint<false>(p, A, lda, gB, samples, workspace, groups, gA, s);
+}
+
+int ye3t_hip_product_adjoint_stream_noalloc(const ye3t_hip_product_plan* p, const void* A, int64_t lda,
+                                            int columns, const void* gB, int64_t samples, void* gA,
+                                            ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(p != nullptr, "NULL plan");
+  YE3T_REQUIRE(samples >= 0, "negative sample count");
+  if (samples == 0) return YE3T_OK;
+  YE3T_REQUIRE(p->use_stream, "this plan has no term stream (workspace too large)");
+  if (p->in_dtype != p->dtype)
+    return set_error(YE3T_EUNSUPPORTED, "the term stream reads densities of the plan's dtype only");
+  YE3T_REQUIRE(A && gB && gA, "NULL input or output");
+  const int64_t tiles = (samples + kLanes - 1) / kLanes;
+  if (columns) {
+    YE3T_REQUIRE(lda >= tiles * kLanes, "lda must cover whole 64-sample tiles");
+  } else {
+    YE3T_REQUIRE(lda == p->a_width, "a row-major density has lda == a_width");
+  }
+  YE3T_REQUIRE(int64_t(p->stream_layout[1]) + int64_t(p->stream_layout[0]) <= 64 * 1024,
+               "the adjoint's values, gradients, loads and output slots exceed 64 KB of LDS");
+  int dev = 0;
+  YE3T_CHECK_HIP(hipGetDevice(&dev));
+  YE3T_REQUIRE(dev == p->device, "call on the plan's device");
+  int64_t need = 0;
+  const int64_t groups = stream_adjoint_groups(p, samples, &need, kNoAllocScratchBytes, true);
+  if (groups < 1) {
+    const int64_t one = p->a_width * tiles * kLanes * (p->dtype == YE3T_F64 ? 8 : 4);
+    return set_error(YE3T_EUNSUPPORTED,
+                     "%lld samples need %lld bytes of partial gradients; the static scratch holds %lld "
+                     "(at most %lld samples of this plan)",
+                     (long long)samples, (long long)one, (long long)kNoAllocScratchBytes,
+                     (long long)(kNoAllocScratchBytes / (p->a_width * (p->dtype == YE3T_F64 ? 8 : 4)) / kLanes *
+                                 kLanes));
+  }
+  void* P = nullptr;
+  const int rc = scratch_address(dev, &P);
+  if (rc != YE3T_OK) return rc;
+  const hipStream_t s = as_stream(stream);
+  return columns ? launch_stream_adjoint<true>(p, A, lda, gB, samples, P, groups, gA, s)
+                 : launch_stream_adjoint<false>(p, A, lda, gB, samples, P, groups, gA, s);
 }
 
 int ye3t_hip_transpose(int dtype, const void* A, int64_t rows, int64_t cols, void* At, int64_t ld,

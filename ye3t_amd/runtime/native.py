@@ -103,6 +103,7 @@ def lib():
     L.ye3t_hip_product_adjoint_workspace_bytes.argtypes = [_vp, _i64]
     L.ye3t_hip_product_adjoint_workspace_bytes.restype = _i64
     L.ye3t_hip_product_adjoint_stream.argtypes = [_vp, _vp, _i64, ctypes.c_int, _vp, _i64, _vp, _i64, _vp, _vp]
+    L.ye3t_hip_product_adjoint_stream_noalloc.argtypes = [_vp, _vp, _i64, ctypes.c_int, _vp, _i64, _vp, _vp]
     L.ye3t_hip_neighbor_workspace_bytes.argtypes = [_i64, ctypes.POINTER(CellGrid)]
     L.ye3t_hip_neighbor_workspace_bytes.restype = _i64
     L.ye3t_hip_neighbor_count.argtypes = [ctypes.c_int, _vp, _i64, ctypes.POINTER(CellGrid), ctypes.c_double, _vp,
@@ -128,6 +129,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_neighbor_workspace_bytes", "ye3t_hip_neighbor_count", "ye3t_hip_neighbor_fill",
     "ye3t_hip_transpose", "ye3t_hip_product_forward_columns", "ye3t_hip_product_plan_uses_stream",
     "ye3t_hip_product_adjoint_workspace_bytes", "ye3t_hip_product_adjoint_stream", "ye3t_hip_product_stream_encode",
+    "ye3t_hip_product_adjoint_stream_noalloc",
 )
 
 
@@ -568,6 +570,34 @@ class ProductPlanHandle:
         _check(L.ye3t_hip_product_adjoint_stream(self._handle, _dev(A, "A"), lda, 1 if columns else 0,
                                                  _dev(gB, "gB"), S, _dev(ws, "workspace"), nbytes, _dev(out, "gA"),
                                                  _stream()), "ye3t_hip_product_adjoint_stream")
+        return out
+
+    def adjoint_stream_noalloc(self, A, gB, out, samples=None, columns=False):
+        """:meth:`adjoint_stream` through the library's allocation-free entry
+        point (partial gradients in its static device scratch; ``out`` must be
+        given).  Calls that overlap on one device race on that scratch."""
+        import torch
+
+        want = torch.float64 if self.dtype == "f64" else torch.float32
+        g_t = torch.float64 if self.out_dtype == "f64" else torch.float32
+        W = int(self.program["a_width"])
+        if A.dtype != want:
+            raise ValueError(f"A must be {want} for this plan")
+        if columns:
+            if A.ndim != 2 or int(A.shape[0]) != W:
+                raise ValueError(f"A must be [{W}, ld]")
+            S, lda = int(samples), int(A.shape[1])
+        else:
+            if A.ndim != 2 or int(A.shape[1]) != W:
+                raise ValueError(f"A must be [samples, {W}]")
+            S, lda = int(A.shape[0]), W
+        if gB.dtype != g_t or tuple(gB.shape) != (S, self.feature_count):
+            raise ValueError(f"gB must be {g_t} [{S}, {self.feature_count}]")
+        if tuple(out.shape) != (S, W) or out.dtype != want:
+            raise ValueError("out has the wrong shape or dtype")
+        _check(lib().ye3t_hip_product_adjoint_stream_noalloc(self._handle, _dev(A, "A"), lda, 1 if columns else 0,
+                                                             _dev(gB, "gB"), S, _dev(out, "gA"), _stream()),
+               "ye3t_hip_product_adjoint_stream_noalloc")
         return out
 
     def attach_readout(self, source, meta):
