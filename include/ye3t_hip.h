@@ -25,7 +25,7 @@ extern "C" {
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
-enum ye3t_dtype { YE3T_F32 = 0, YE3T_F64 = 1 };
+enum ye3t_dtype { YE3T_F32 = 0, YE3T_F64 = 1, YE3T_C64 = 2, YE3T_C128 = 3 /* complex: (re, im) pairs */ };
 
 enum ye3t_status {
   YE3T_OK = 0,
@@ -330,6 +330,92 @@ int ye3t_hip_product_plan_select(ye3t_hip_product_plan* plan, int use_interprete
 int ye3t_hip_product_stream_encode(const ye3t_product_plan_desc* desc, int64_t* counts, uint32_t* recs,
                                    uint32_t* flags, int64_t* rec_off, uint32_t* loads, int64_t* load_off,
                                    int64_t* layout);
+
+/* ---- General factorized-angular DAG (the reference's factorized_angular op) ---- */
+
+/* Host tables of one factorized-angular DAG, exactly the arguments of the
+ * reference op factorized_angular(packed_slots, node_offsets, node_dimensions,
+ * node_leaf_offsets, node_left, node_right, node_coefficient_offsets,
+ * coefficient_rows, coefficient_columns, coefficient_values, root_nodes,
+ * projection_values, source_dimension, workspace_dimension, output_dimension)
+ * (schema execution_plan_torch.cpp:7586-7594), with the counts of its vectors.
+ * Nodes are in topological order; a leaf node copies node_dimensions values
+ * of the input slot from node_leaf_offsets; a merge node accumulates
+ * out[column] += conj(value) * left[row / dim(right)] * right[row % dim(right)]
+ * over its coefficient range; every root is projected onto all P =
+ * projection_count / source_dimension projection columns (the reference's
+ * uniform root metadata, execution_plan_torch.cpp:205-250). */
+typedef struct {
+  int dtype;                               /* YE3T_F32, YE3T_F64, YE3T_C64 or YE3T_C128 */
+  int64_t node_count;
+  const int64_t* node_offsets;             /* host [node_count] */
+  const int64_t* node_dimensions;          /* host [node_count] */
+  const int64_t* node_leaf_offsets;        /* host [node_count], -1 for merge nodes */
+  const int64_t* node_left;                /* host [node_count] */
+  const int64_t* node_right;               /* host [node_count] */
+  const int64_t* node_coefficient_offsets; /* host [node_count + 1] */
+  int64_t coefficient_count;
+  const int64_t* coefficient_rows;         /* host [coefficient_count] */
+  const int64_t* coefficient_columns;      /* host [coefficient_count] */
+  const void* coefficient_values;          /* host [coefficient_count] of dtype */
+  int64_t root_count;
+  const int64_t* root_nodes;               /* host [root_count] */
+  int64_t projection_count;
+  const void* projection_values;           /* host [source_dimension * P] of dtype */
+  int64_t source_dimension;
+  int64_t input_dimension;                 /* values per source slot (packed width / source_dimension) */
+  int64_t workspace_dimension;             /* node_offsets[-1] + node_dimensions[-1] */
+  int64_t output_dimension;                /* root_count * P * dim(root) */
+} ye3t_factorized_angular_desc;
+
+typedef struct ye3t_hip_factorized_angular_plan ye3t_hip_factorized_angular_plan;
+
+/* Validates the tables on the host (the reference op's TORCH_CHECKs, plus every
+ * index the kernels use) and copies them to the current device (synchronous).
+ * Counterpart of the reference module's plan buffers (execution_plan.py:12918-13151). */
+int ye3t_hip_factorized_angular_plan_create(const ye3t_factorized_angular_desc* desc,
+                                            ye3t_hip_factorized_angular_plan** out);
+void ye3t_hip_factorized_angular_plan_destroy(ye3t_hip_factorized_angular_plan* plan);
+
+/* info[7] = (dtype, source_dimension, input_dimension, workspace_dimension,
+ * output_dimension, projection columns P, root dimension). */
+int ye3t_hip_factorized_angular_plan_info(const ye3t_hip_factorized_angular_plan* plan, int64_t* info);
+
+/* output[batch, output_dimension] from packed_slots[batch, source_dimension *
+ * input_dimension].  Replaces the CUDA branch of ye3t_runtime::factorized_angular
+ * (kernel execution_plan_cuda.cu:6228-6358, launcher :11488-11672; CPU core
+ * ye3t_runtime_core.cpp:5667-5769).  The per-sample workspace lives in LDS;
+ * YE3T_EUNSUPPORTED when one sample's workspace exceeds 64 KB. */
+int ye3t_hip_factorized_angular_forward(const ye3t_hip_factorized_angular_plan* plan, const void* packed_slots,
+                                        int64_t batch, void* output, ye3t_stream_t stream);
+
+/* packed_slots_adjoint[batch, S * input_dimension]: the conjugate-transpose
+ * (analysis) adjoint of an output adjoint, forward values recomputed.
+ * Replaces ye3t_runtime::factorized_angular_adjoint (execution_plan_cuda.cu:6361;
+ * CPU core ye3t_runtime_core.cpp:6481-6643). */
+int ye3t_hip_factorized_angular_adjoint(const ye3t_hip_factorized_angular_plan* plan, const void* output_adjoint,
+                                        const void* packed_slots, int64_t batch, void* packed_slots_adjoint,
+                                        ye3t_stream_t stream);
+
+/* output[b] = bias + sum_k features[b, k] weight[k] without storing the
+ * features (weight [output_dimension] on the device, bias one host value of
+ * dtype).  Replaces ye3t_runtime::factorized_angular_linear (execution_plan_cuda.cu:8957;
+ * CPU core ye3t_runtime_core.cpp:7144-7234). */
+int ye3t_hip_factorized_angular_linear_forward(const ye3t_hip_factorized_angular_plan* plan, const void* packed_slots,
+                                               int64_t batch, const void* weight, const void* bias, void* output,
+                                               ye3t_stream_t stream);
+
+/* Adjoint of the linear readout for output_adjoint[batch]: packed_slots_adjoint,
+ * weight_adjoint[output_dimension] = sum_b g[b] conj(features[b]) and
+ * bias_adjoint = sum_b g[b] (device, summed over the batch in order).
+ * `features` is a caller-provided [batch, output_dimension] device buffer the
+ * call fills with the forward features.  Replaces
+ * ye3t_runtime::factorized_angular_linear_adjoint (CPU core
+ * ye3t_runtime_core.cpp:7237-7399). */
+int ye3t_hip_factorized_angular_linear_adjoint(const ye3t_hip_factorized_angular_plan* plan,
+                                               const void* output_adjoint, const void* packed_slots, int64_t batch,
+                                               const void* weight, void* features, void* packed_slots_adjoint,
+                                               void* weight_adjoint, void* bias_adjoint, ye3t_stream_t stream);
 
 /* Device workspace bytes of ye3t_hip_product_adjoint_stream for `samples`
  * samples (0 for plans without a term stream; -1 on invalid input). */

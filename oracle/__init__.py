@@ -251,3 +251,232 @@ def neighbor_list(positions, cutoff):
                                nbrs.ctypes.data, vecs.ctypes.data)
     return {"target_offsets": offsets, "edge_targets": centers, "edge_sources": nbrs,
             "edge_vectors": vecs.astype(pos.dtype)}
+
+
+# ---- factorized angular DAG (ye3t_oracle_dag.c) ------------------------------
+
+FA_TABLE_KEYS = ("node_offsets", "node_dimensions", "node_leaf_offsets", "node_left", "node_right",
+                 "node_coefficient_offsets", "coefficient_rows", "coefficient_columns")
+
+
+def _fa_args(tables, complex_data):
+    """ctypes arguments of the DAG tables (dict of arrays) and the arrays kept alive."""
+    keep = {k: _i64a(tables[k]) for k in FA_TABLE_KEYS + ("root_nodes",)}
+    ctype = np.complex128 if complex_data else np.float64
+    keep["coefficient_values"] = np.ascontiguousarray(tables["coefficient_values"], dtype=ctype)
+    keep["projection_values"] = np.ascontiguousarray(tables["projection_values"], dtype=ctype)
+    return keep
+
+
+def _vp(a):
+    return ctypes.c_void_p(a.ctypes.data) if a is not None and a.size else None
+
+
+def _fa_dims(packed, tables, source_dimension):
+    nodes = int(len(tables["node_offsets"]))
+    S = int(source_dimension)
+    width = int(packed.shape[1])
+    proj = np.asarray(tables["projection_values"]).reshape(-1)
+    P = proj.shape[0] // S
+    roots = np.asarray(tables["root_nodes"]).reshape(-1)
+    rdim = int(np.asarray(tables["node_dimensions"])[roots[0]])
+    W = int(tables["node_offsets"][-1] + tables["node_dimensions"][-1])
+    return nodes, S, width // S, P, len(roots), rdim, W
+
+
+def _fa_fn(name, complex_data, use_reference):
+    suffix = "c128" if complex_data else "f64"
+    if use_reference:
+        fn = getattr(ref_lib(), f"ref_{name}_{suffix}")
+    else:
+        fn = getattr(lib(), f"oracle_{name}_{suffix}")
+    fn.restype = None
+    return fn
+
+
+def factorized_angular(packed_slots, tables, source_dimension, *, use_reference=False):
+    """``factorized_angular_forward`` (ye3t_runtime_core.cpp:5667-5769) with the
+    Torch op's uniform root metadata; returns ``[batch, roots * P * root_dim]``."""
+    cplx = np.iscomplexobj(packed_slots) or np.iscomplexobj(tables["coefficient_values"]) or \
+        np.iscomplexobj(tables["projection_values"])
+    dt = np.complex128 if cplx else np.float64
+    x = np.ascontiguousarray(packed_slots, dtype=dt)
+    B = int(x.shape[0])
+    nodes, S, D, P, R, rdim, W = _fa_dims(x, tables, source_dimension)
+    out_dim = R * P * rdim
+    k = _fa_args(tables, cplx)
+    out = np.zeros((B, out_dim), dtype=dt)
+    ws = np.zeros(max(W, 1), dtype=dt)
+    I = ctypes.c_int64
+    args = [_vp(x), I(B), I(D), I(S)] + [_vp(k[n]) for n in FA_TABLE_KEYS[:6]] + [I(nodes)] + \
+        [_vp(k["coefficient_rows"]), _vp(k["coefficient_columns"]), _vp(k["coefficient_values"]),
+         _vp(k["root_nodes"]), I(R), _vp(k["projection_values"]), I(P), I(out_dim)]
+    if not use_reference:
+        args.append(_vp(ws))
+    args.append(_vp(out))
+    _fa_fn("factorized_angular", cplx, use_reference)(*args)
+    return out
+
+
+def factorized_angular_adjoint(output_adjoint, packed_slots, tables, source_dimension, *, use_reference=False):
+    """``factorized_angular_adjoint`` (ye3t_runtime_core.cpp:6481-6643): the
+    packed-slot gradient ``[batch, S * input_dim]`` of an output adjoint."""
+    cplx = np.iscomplexobj(packed_slots) or np.iscomplexobj(output_adjoint) or \
+        np.iscomplexobj(tables["coefficient_values"]) or np.iscomplexobj(tables["projection_values"])
+    dt = np.complex128 if cplx else np.float64
+    x = np.ascontiguousarray(packed_slots, dtype=dt)
+    g = np.ascontiguousarray(output_adjoint, dtype=dt)
+    B = int(x.shape[0])
+    nodes, S, D, P, R, rdim, W = _fa_dims(x, tables, source_dimension)
+    out_dim = R * P * rdim
+    k = _fa_args(tables, cplx)
+    out = np.zeros((B, S * D), dtype=dt)
+    ws = np.zeros(max(W, 1), dtype=dt)
+    wa = np.zeros(max(W, 1), dtype=dt)
+    I = ctypes.c_int64
+    args = [_vp(g), _vp(x), I(B), I(D), I(S)] + [_vp(k[n]) for n in FA_TABLE_KEYS[:6]] + [I(nodes)] + \
+        [_vp(k["coefficient_rows"]), _vp(k["coefficient_columns"]), _vp(k["coefficient_values"]),
+         _vp(k["root_nodes"]), I(R), _vp(k["projection_values"]), I(P), I(out_dim)]
+    if not use_reference:
+        args += [_vp(ws), _vp(wa)]
+    args.append(_vp(out))
+    _fa_fn("factorized_angular_adjoint", cplx, use_reference)(*args)
+    return out
+
+
+def factorized_angular_linear(packed_slots, tables, source_dimension, weight, bias, *, use_reference=False):
+    """``factorized_angular_linear_forward`` (ye3t_runtime_core.cpp:7144-7234):
+    ``bias + features @ weight`` per sample, accumulated in the reference's order."""
+    cplx = any(np.iscomplexobj(a) for a in (packed_slots, weight, tables["coefficient_values"],
+                                            tables["projection_values"])) or isinstance(bias, complex)
+    dt = np.complex128 if cplx else np.float64
+    x = np.ascontiguousarray(packed_slots, dtype=dt)
+    B = int(x.shape[0])
+    nodes, S, D, P, R, rdim, W = _fa_dims(x, tables, source_dimension)
+    k = _fa_args(tables, cplx)
+    w = np.ascontiguousarray(weight, dtype=dt)
+    b = np.array([bias], dtype=dt)
+    out = np.zeros(B, dtype=dt)
+    ws = np.zeros(max(W, 1), dtype=dt)
+    I = ctypes.c_int64
+    args = [_vp(x), I(B), I(D), I(S)] + [_vp(k[n]) for n in FA_TABLE_KEYS[:6]] + [I(nodes)] + \
+        [_vp(k["coefficient_rows"]), _vp(k["coefficient_columns"]), _vp(k["coefficient_values"]),
+         _vp(k["root_nodes"]), I(R), _vp(k["projection_values"]), I(P), _vp(w)]
+    if use_reference:
+        args += [_vp(b), _vp(out)]
+    else:
+        # the C restatement takes the bias by value
+        fn = _fa_fn("factorized_angular_linear", cplx, False)
+        if cplx:
+            class _C(ctypes.Structure):
+                _fields_ = [("re", ctypes.c_double), ("im", ctypes.c_double)]
+            fn.argtypes = None
+            args += [_C(b[0].real, b[0].imag), _vp(ws), _vp(out)]
+        else:
+            args += [ctypes.c_double(float(b[0])), _vp(ws), _vp(out)]
+        fn(*args)
+        return out
+    _fa_fn("factorized_angular_linear", cplx, True)(*args)
+    return out
+
+
+def factorized_angular_linear_adjoint(output_adjoint, packed_slots, tables, source_dimension, weight, *,
+                                      use_reference=False):
+    """``factorized_angular_linear_adjoint`` (ye3t_runtime_core.cpp:7237-7399):
+    ``(packed_slots_adjoint, weight_adjoint, bias_adjoint)``."""
+    cplx = any(np.iscomplexobj(a) for a in (packed_slots, weight, output_adjoint, tables["coefficient_values"],
+                                            tables["projection_values"]))
+    dt = np.complex128 if cplx else np.float64
+    x = np.ascontiguousarray(packed_slots, dtype=dt)
+    g = np.ascontiguousarray(output_adjoint, dtype=dt)
+    B = int(x.shape[0])
+    nodes, S, D, P, R, rdim, W = _fa_dims(x, tables, source_dimension)
+    k = _fa_args(tables, cplx)
+    w = np.ascontiguousarray(weight, dtype=dt)
+    gx = np.zeros((B, S * D), dtype=dt)
+    gw = np.zeros(R * P * rdim, dtype=dt)
+    gb = np.zeros(1, dtype=dt)
+    ws = np.zeros(max(W, 1), dtype=dt)
+    wa = np.zeros(max(W, 1), dtype=dt)
+    I = ctypes.c_int64
+    args = [_vp(g), _vp(x), I(B), I(D), I(S)] + [_vp(k[n]) for n in FA_TABLE_KEYS[:6]] + [I(nodes)] + \
+        [_vp(k["coefficient_rows"]), _vp(k["coefficient_columns"]), _vp(k["coefficient_values"]),
+         _vp(k["root_nodes"]), I(R), _vp(k["projection_values"]), I(P), _vp(w)]
+    if not use_reference:
+        args += [_vp(ws), _vp(wa)]
+    args += [_vp(gx), _vp(gw), _vp(gb)]
+    _fa_fn("factorized_angular_linear_adjoint", cplx, use_reference)(*args)
+    return gx, gw, gb[0]
+
+
+# ---- symmetric-power monomial adjoint and shared monomials -------------------
+
+def symmetric_power_monomial_adjoint(output_adjoint, inp, monomial_counts, output_indices, monomial_values,
+                                     output_dimension, *, use_reference=False):
+    """``symmetric_power_monomial_adjoint`` (ye3t_runtime_core.cpp:5318-5389)."""
+    x = _f64(inp)
+    B, D = x.shape
+    g = _f64(output_adjoint).reshape(B, int(output_dimension))
+    counts = _i64a(monomial_counts)
+    idx = _i64a(output_indices)
+    vals = _f64(monomial_values)
+    out = np.zeros((B, D))
+    fn = ref_lib().ref_symmetric_power_monomial_adjoint if use_reference else \
+        lib().oracle_symmetric_power_monomial_adjoint
+    fn.restype = None
+    I = ctypes.c_int64
+    fn(_vp(g), _vp(x), I(B), I(D), _vp(counts), _vp(idx), _vp(vals), I(vals.shape[0]), I(int(output_dimension)),
+       _vp(out))
+    return out
+
+
+def symmetric_power_shared_monomial(inp, monomial_counts, output_offsets, coefficient_terms, coefficient_values,
+                                    *, use_reference=False):
+    """``symmetric_power_shared_monomial_forward`` (ye3t_runtime_core.cpp:5392-5440)."""
+    x = _f64(inp)
+    B, D = x.shape
+    counts = _i64a(monomial_counts)
+    M = counts.shape[0]
+    offs = _i64a(output_offsets)
+    terms = _i64a(coefficient_terms)
+    vals = _f64(coefficient_values)
+    O = offs.shape[0] - 1
+    out = np.zeros((B, O))
+    I = ctypes.c_int64
+    if use_reference:
+        fn = ref_lib().ref_symmetric_power_shared_monomial
+        fn.restype = None
+        fn(_vp(x), I(B), I(D), _vp(counts), I(M), _vp(offs), _vp(terms), _vp(vals), I(vals.shape[0]), I(O), _vp(out))
+    else:
+        fn = lib().oracle_symmetric_power_shared_monomial
+        fn.restype = None
+        ws = np.zeros(max(M, 1))
+        fn(_vp(x), I(B), I(D), _vp(counts), I(M), _vp(offs), _vp(terms), _vp(vals), I(O), _vp(ws), _vp(out))
+    return out
+
+
+def symmetric_power_shared_monomial_adjoint(output_adjoint, inp, monomial_counts, output_offsets,
+                                            coefficient_terms, coefficient_values, *, use_reference=False):
+    """``symmetric_power_shared_monomial_adjoint`` (ye3t_runtime_core.cpp:5442-5540)."""
+    x = _f64(inp)
+    B, D = x.shape
+    counts = _i64a(monomial_counts)
+    M = counts.shape[0]
+    offs = _i64a(output_offsets)
+    terms = _i64a(coefficient_terms)
+    vals = _f64(coefficient_values)
+    O = offs.shape[0] - 1
+    g = _f64(output_adjoint).reshape(B, O)
+    out = np.zeros((B, D))
+    I = ctypes.c_int64
+    if use_reference:
+        fn = ref_lib().ref_symmetric_power_shared_monomial_adjoint
+        fn.restype = None
+        fn(_vp(g), _vp(x), I(B), I(D), _vp(counts), I(M), _vp(offs), _vp(terms), _vp(vals), I(vals.shape[0]), I(O),
+           _vp(out))
+    else:
+        fn = lib().oracle_symmetric_power_shared_monomial_adjoint
+        fn.restype = None
+        ws = np.zeros(max(M, 1))
+        fn(_vp(g), _vp(x), I(B), I(D), _vp(counts), I(M), _vp(offs), _vp(terms), _vp(vals), I(O), _vp(ws), _vp(out))
+    return out

@@ -2,8 +2,43 @@
 // compiled from the reference sources in place by oracle/Makefile into
 // oracle/_ref/.  Used to validate the C restatement and as a CPU baseline in
 // this container.  Never part of the product.
+#include <complex>
 #include <cstdint>
+#include <vector>
 #include "ye3t_runtime_core.h"
+
+namespace {
+// uniform root metadata of the Torch op (execution_plan_torch.cpp:205-250)
+struct Roots {
+  std::vector<int64_t> starts, dims, offsets;
+  Roots(int64_t root_count, int64_t proj_dim, int64_t root_dim)
+      : starts(root_count, 0), dims(root_count, proj_dim), offsets(root_count) {
+    for (int64_t r = 0; r < root_count; ++r) offsets[r] = r * proj_dim * root_dim;
+  }
+};
+
+template <typename T>
+void fa_forward(const T* packed, int64_t batch, int64_t in_dim, int64_t src_dim, const int64_t* noff,
+                const int64_t* ndim, const int64_t* nleaf, const int64_t* nl, const int64_t* nr, const int64_t* ncoef,
+                int64_t nodes, const int64_t* rows, const int64_t* cols, const T* coef, const int64_t* roots,
+                int64_t root_count, const T* proj, int64_t proj_dim, int64_t out_dim, T* out) {
+  Roots m(root_count, proj_dim, ndim[roots[0]]);
+  ye3t::runtime::factorized_angular_forward<T>(packed, batch, in_dim, src_dim, noff, ndim, nleaf, nl, nr, ncoef,
+                                              nodes, rows, cols, coef, roots, root_count, m.starts.data(),
+                                              m.dims.data(), m.offsets.data(), proj, proj_dim, out_dim, out);
+}
+
+template <typename T>
+void fa_adjoint(const T* gout, const T* packed, int64_t batch, int64_t in_dim, int64_t src_dim, const int64_t* noff,
+                const int64_t* ndim, const int64_t* nleaf, const int64_t* nl, const int64_t* nr, const int64_t* ncoef,
+                int64_t nodes, const int64_t* rows, const int64_t* cols, const T* coef, const int64_t* roots,
+                int64_t root_count, const T* proj, int64_t proj_dim, int64_t out_dim, T* gpacked) {
+  Roots m(root_count, proj_dim, ndim[roots[0]]);
+  ye3t::runtime::factorized_angular_adjoint<T>(gout, packed, batch, in_dim, src_dim, noff, ndim, nleaf, nl, nr, ncoef,
+                                              nodes, rows, cols, coef, roots, root_count, m.starts.data(),
+                                              m.dims.data(), m.offsets.data(), proj, proj_dim, out_dim, gpacked);
+}
+}  // namespace
 
 extern "C" {
 void ref_radial_table(const double* r, const double* c, const double* l, int64_t e, int64_t n,
@@ -27,4 +62,64 @@ void ref_symmetric_power_monomial(const double* in, int64_t batch, int64_t in_di
   ye3t::runtime::symmetric_power_monomial_forward<double>(in, batch, in_dim, counts, offsets, values, terms,
                                                           out_dim, out);
 }
+void ref_symmetric_power_monomial_adjoint(const double* gout, const double* in, int64_t batch, int64_t in_dim,
+                                          const int64_t* counts, const int64_t* out_index, const double* values,
+                                          int64_t terms, int64_t out_dim, double* gin) {
+  ye3t::runtime::symmetric_power_monomial_adjoint<double>(gout, in, batch, in_dim, counts, out_index, values, terms,
+                                                          out_dim, gin);
+}
+void ref_symmetric_power_shared_monomial(const double* in, int64_t batch, int64_t in_dim, const int64_t* counts,
+                                         int64_t monomials, const int64_t* out_off, const int64_t* terms,
+                                         const double* values, int64_t coef_count, int64_t out_dim, double* out) {
+  ye3t::runtime::symmetric_power_shared_monomial_forward<double>(in, batch, in_dim, counts, monomials, out_off,
+                                                                 terms, values, coef_count, out_dim, out);
+}
+void ref_symmetric_power_shared_monomial_adjoint(const double* gout, const double* in, int64_t batch,
+                                                 int64_t in_dim, const int64_t* counts, int64_t monomials,
+                                                 const int64_t* out_off, const int64_t* terms, const double* values,
+                                                 int64_t coef_count, int64_t out_dim, double* gin) {
+  ye3t::runtime::symmetric_power_shared_monomial_adjoint<double>(gout, in, batch, in_dim, counts, monomials, out_off,
+                                                                 terms, values, coef_count, out_dim, gin);
+}
+// factorized angular DAG: real (f64) and complex (c128, interleaved re/im)
+#define YE3T_REF_FA(SUFFIX, T)                                                                                    \
+  void ref_factorized_angular_##SUFFIX(const T* packed, int64_t batch, int64_t in_dim, int64_t src_dim,           \
+                                       const int64_t* noff, const int64_t* ndim, const int64_t* nleaf,            \
+                                       const int64_t* nl, const int64_t* nr, const int64_t* ncoef, int64_t nodes, \
+                                       const int64_t* rows, const int64_t* cols, const T* coef,                   \
+                                       const int64_t* roots, int64_t root_count, const T* proj, int64_t proj_dim, \
+                                       int64_t out_dim, T* out) {                                                 \
+    fa_forward<T>(packed, batch, in_dim, src_dim, noff, ndim, nleaf, nl, nr, ncoef, nodes, rows, cols, coef,     \
+                  roots, root_count, proj, proj_dim, out_dim, out);                                              \
+  }                                                                                                              \
+  void ref_factorized_angular_adjoint_##SUFFIX(                                                                  \
+      const T* gout, const T* packed, int64_t batch, int64_t in_dim, int64_t src_dim, const int64_t* noff,         \
+      const int64_t* ndim, const int64_t* nleaf, const int64_t* nl, const int64_t* nr, const int64_t* ncoef,       \
+      int64_t nodes, const int64_t* rows, const int64_t* cols, const T* coef, const int64_t* roots,              \
+      int64_t root_count, const T* proj, int64_t proj_dim, int64_t out_dim, T* gpacked) {                         \
+    fa_adjoint<T>(gout, packed, batch, in_dim, src_dim, noff, ndim, nleaf, nl, nr, ncoef, nodes, rows, cols, coef,\
+                  roots, root_count, proj, proj_dim, out_dim, gpacked);                                          \
+  }                                                                                                              \
+  void ref_factorized_angular_linear_##SUFFIX(                                                                   \
+      const T* packed, int64_t batch, int64_t in_dim, int64_t src_dim, const int64_t* noff, const int64_t* ndim,   \
+      const int64_t* nleaf, const int64_t* nl, const int64_t* nr, const int64_t* ncoef, int64_t nodes,            \
+      const int64_t* rows, const int64_t* cols, const T* coef, const int64_t* roots, int64_t root_count,          \
+      const T* proj, int64_t proj_dim, const T* weight, const T* bias, T* out) {                                  \
+    ye3t::runtime::factorized_angular_linear_forward<T>(packed, batch, in_dim, src_dim, noff, ndim, nleaf, nl, nr, \
+                                                        ncoef, nodes, rows, cols, coef, roots, root_count, proj,  \
+                                                        proj_dim, weight, *bias, out);                            \
+  }                                                                                                              \
+  void ref_factorized_angular_linear_adjoint_##SUFFIX(                                                           \
+      const T* gout, const T* packed, int64_t batch, int64_t in_dim, int64_t src_dim, const int64_t* noff,         \
+      const int64_t* ndim, const int64_t* nleaf, const int64_t* nl, const int64_t* nr, const int64_t* ncoef,       \
+      int64_t nodes, const int64_t* rows, const int64_t* cols, const T* coef, const int64_t* roots,              \
+      int64_t root_count, const T* proj, int64_t proj_dim, const T* weight, T* gpacked, T* gweight, T* gbias) {  \
+    ye3t::runtime::factorized_angular_linear_adjoint<T>(gout, packed, batch, in_dim, src_dim, noff, ndim, nleaf,  \
+                                                        nl, nr, ncoef, nodes, rows, cols, coef, roots,            \
+                                                        root_count, proj, proj_dim, weight, gpacked, gweight,     \
+                                                        gbias);                                                   \
+  }
+YE3T_REF_FA(f64, double)
+YE3T_REF_FA(c128, std::complex<double>)
+#undef YE3T_REF_FA
 }

@@ -22,6 +22,10 @@ REFERENCE_OPERATIONS = (
     "density_accumulate",
     "density_accumulate_adjoint",
     "symmetric_power_monomial",
+    "factorized_angular",
+    "factorized_angular_adjoint",
+    "factorized_angular_linear",
+    "factorized_angular_linear_adjoint",
 )
 FUSED_OPERATIONS = (
     "ace_density_forward",
@@ -230,7 +234,7 @@ def native_execution_plan_capabilities():
         "core_abi_version": native.ABI_VERSION if available else None,
         "minimum_core_abi_version": _NATIVE_EXECUTION_PLAN_ABI,
         "factorized_workspace_metadata": "compiler_host_scalar_no_device_read",
-        "dtypes": ("float32", "float64"),
+        "dtypes": ("float32", "float64", "complex64", "complex128"),
         "analysis_orientation": "conjugate_transpose",
         "operations": ops,
         "density_reduction": "csr_segment_deterministic",
@@ -240,6 +244,15 @@ def native_execution_plan_capabilities():
         caps = native.device_caps(torch.cuda.current_device())
         report["hip_device"] = caps
     return report
+
+
+def __getattr__(name):
+    # the factorized-angular op and module load torch, so they are imported on first use
+    if name in ("factorized_angular", "factorized_angular_linear", "YE3TFactorizedAngularModule"):
+        import importlib
+
+        return getattr(importlib.import_module("ye3t_amd.runtime.dag"), name)
+    raise AttributeError(name)
 
 
 def require_native():

@@ -1,0 +1,290 @@
+"""The reference's general factorized-angular DAG op on the HIP library.
+
+``factorized_angular`` and ``factorized_angular_linear`` take the reference
+op's arguments (schema ``execution_plan_torch.cpp:7586-7594`` and the linear
+readout's) and differentiate through the library's adjoint kernels
+(``ye3t_hip_factorized_angular_adjoint`` / ``_linear_adjoint``), which follow
+the reference's conjugate-transpose convention: the gradient Torch autograd
+returns for the reference's own Torch restatement.
+
+``YE3TFactorizedAngularModule`` mirrors the reference module
+(``ye3t/runtime/execution_plan.py:13550-13903``): it owns the DAG tables as
+buffers, packs per-slot inputs the same way and offers ``forward``,
+``linear_readout`` and ``runtime_report``.  It is built from explicit DAG
+tables (``from_tables``) or from a reference execution-plan document
+(:meth:`YE3TFactorizedAngularModule.from_execution_plan`).
+"""
+
+import hashlib
+
+import numpy as np
+import torch
+
+from ye3t_amd.runtime import native
+
+_PLANS = {}
+
+
+def _table_arrays(tables):
+    out = {}
+    for name in native.FA_TABLE_NAMES:
+        v = tables[name]
+        out[name] = v.detach().cpu().numpy() if hasattr(v, "detach") else np.asarray(v)
+    return out
+
+
+def plan_for(tables, source_dimension, input_dimension, workspace_dimension, output_dimension, dtype, device):
+    """The device plan of these tables (validated and uploaded once, cached by
+    content, dimensions, dtype and device)."""
+    arrays = _table_arrays(tables)
+    h = hashlib.sha256()
+    for name in native.FA_TABLE_NAMES:
+        a = np.ascontiguousarray(arrays[name])
+        h.update(name.encode())
+        h.update(str(a.dtype).encode())
+        h.update(a.tobytes())
+    key = (h.hexdigest(), int(source_dimension), int(input_dimension), int(workspace_dimension),
+           int(output_dimension), str(dtype), str(device))
+    plan = _PLANS.get(key)
+    if plan is None:
+        import torch
+
+        with torch.cuda.device(device):
+            plan = native.FactorizedAngularPlanHandle(arrays, source_dimension, input_dimension, workspace_dimension,
+                                                      output_dimension, dtype)
+        if len(_PLANS) > 64:
+            _PLANS.clear()
+        _PLANS[key] = plan
+    return plan
+
+
+def _autograd():
+    import torch
+
+    class _FactorizedAngular(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, packed, plan):
+            ctx.plan = plan
+            ctx.save_for_backward(packed)
+            return plan.forward(packed)
+
+        @staticmethod
+        def backward(ctx, grad):
+            (packed,) = ctx.saved_tensors
+            return ctx.plan.adjoint(grad.contiguous(), packed), None
+
+    class _FactorizedAngularLinear(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, packed, weight, bias, plan):
+            ctx.plan = plan
+            ctx.save_for_backward(packed, weight)
+            ctx.bias_shape = bias.shape
+            return plan.linear(packed, weight, bias.item())
+
+        @staticmethod
+        def backward(ctx, grad):
+            packed, weight = ctx.saved_tensors
+            gx, gw, gb = ctx.plan.linear_adjoint(grad.contiguous(), packed, weight)
+            return gx, gw.to(weight.dtype), gb.reshape(ctx.bias_shape), None
+
+    return _FactorizedAngular, _FactorizedAngularLinear
+
+
+_FN = None
+
+
+def _fns():
+    global _FN
+    if _FN is None:
+        _FN = _autograd()
+    return _FN
+
+
+def _check_device(packed):
+    if not packed.is_cuda:
+        raise NotImplementedError("factorized_angular: ye3t_amd implements the HIP device branch; CPU tensors are "
+                                  "served by the reference CPU runtime")
+
+
+def factorized_angular(packed_slots, node_offsets, node_dimensions, node_leaf_offsets, node_left, node_right,
+                       node_coefficient_offsets, coefficient_rows, coefficient_columns, coefficient_values,
+                       root_nodes, projection_values, source_dimension, workspace_dimension, output_dimension):
+    """``ye3t_runtime::factorized_angular`` (schema ``execution_plan_torch.cpp:7586-7594``):
+    ``[batch, output_dimension]`` features of ``packed_slots [batch,
+    source_dimension * input_dimension]``; differentiable (conjugate-transpose
+    adjoint)."""
+    _check_device(packed_slots)
+    S = int(source_dimension)
+    if S <= 0:
+        raise RuntimeError("source_dimension must be positive")
+    if packed_slots.ndim != 2 or int(packed_slots.shape[1]) % S:
+        raise RuntimeError("packed_slots width must be divisible by source_dimension")
+    tables = dict(zip(native.FA_TABLE_NAMES, (node_offsets, node_dimensions, node_leaf_offsets, node_left,
+                                              node_right, node_coefficient_offsets, coefficient_rows,
+                                              coefficient_columns, coefficient_values, root_nodes,
+                                              projection_values)))
+    plan = plan_for(tables, S, int(packed_slots.shape[1]) // S, workspace_dimension, output_dimension,
+                    packed_slots.dtype, packed_slots.device)
+    return _fns()[0].apply(packed_slots.contiguous(), plan)
+
+
+def factorized_angular_linear(packed_slots, node_offsets, node_dimensions, node_leaf_offsets, node_left, node_right,
+                              node_coefficient_offsets, coefficient_rows, coefficient_columns, coefficient_values,
+                              root_nodes, projection_values, source_dimension, workspace_dimension, weight, bias):
+    """``ye3t_runtime::factorized_angular_linear``: ``bias + features @ weight``
+    per sample without materialising the features; differentiable in the slots,
+    the weight and the bias."""
+    import torch
+
+    _check_device(packed_slots)
+    S = int(source_dimension)
+    if packed_slots.ndim != 2 or int(packed_slots.shape[1]) % S:
+        raise RuntimeError("packed_slots width must be divisible by source_dimension")
+    tables = dict(zip(native.FA_TABLE_NAMES, (node_offsets, node_dimensions, node_leaf_offsets, node_left,
+                                              node_right, node_coefficient_offsets, coefficient_rows,
+                                              coefficient_columns, coefficient_values, root_nodes,
+                                              projection_values)))
+    weight = torch.as_tensor(weight, device=packed_slots.device).to(packed_slots.dtype)
+    bias = torch.as_tensor(bias, device=packed_slots.device).to(packed_slots.dtype).reshape(())
+    plan = plan_for(tables, S, int(packed_slots.shape[1]) // S, workspace_dimension, int(weight.numel()),
+                    packed_slots.dtype, packed_slots.device)
+    return _fns()[1].apply(packed_slots.contiguous(), weight, bias, plan)
+
+
+def _torch():
+    return torch
+
+
+class YE3TFactorizedAngularModule(torch.nn.Module):
+    """Prepared factorized-angular DAG runtime (reference
+    ``execution_plan.py:13550-13903``).
+
+    Build it with :meth:`from_tables` (explicit DAG tables) or
+    :meth:`from_execution_plan` (a reference execution-plan document).
+    ``forward(slot_values)`` returns ``[..., roots * P, 2 L + 1]``;
+    ``linear_readout(slot_values, weight, bias)`` the fused readout.
+    """
+
+    def __init__(self, tables, *, input_Ls, source_dimension, output_L, backend="auto", dtype=None, device=None,
+                 plan_hash=None, plan_id=None):
+        torch = _torch()
+        super().__init__()
+        backend = str(backend)
+        if backend == "reference":
+            raise NotImplementedError("backend='reference' selects the reference's Torch implementation "
+                                      "(ye3t.runtime); ye3t_amd runs the native HIP branch only")
+        if backend not in {"auto", "native"}:
+            raise ValueError("backend must be 'auto', 'native', or 'reference'")
+        values = np.asarray(tables["coefficient_values"])
+        proj = np.asarray(tables["projection_values"])
+        if dtype is None:
+            dtype = torch.complex128 if (np.iscomplexobj(values) and np.any(values.imag != 0)) or \
+                (np.iscomplexobj(proj) and np.any(proj.imag != 0)) else torch.float64
+        device = torch.device("cuda" if device is None else device)
+        if device.type != "cuda":
+            raise NotImplementedError("YE3TFactorizedAngularModule: ye3t_amd implements the HIP device branch")
+        for name in native.FA_TABLE_NAMES:
+            v = np.asarray(tables[name])
+            t = torch.as_tensor(v, dtype=dtype if name in ("coefficient_values", "projection_values") else torch.int64,
+                                device=device)
+            self.register_buffer(name, t, persistent=False)
+        self.input_Ls = tuple(int(x) for x in input_Ls)
+        self.input_dimension = sum(2 * L + 1 for L in self.input_Ls)
+        self.source_dimension = int(source_dimension)
+        offs = np.asarray(tables["node_offsets"])
+        dims = np.asarray(tables["node_dimensions"])
+        self.workspace_dimension = int(offs[-1] + dims[-1])
+        self.magnetic_dimension = 2 * int(output_L) + 1
+        P = int(proj.size) // self.source_dimension
+        self.logical_channel_tableau_dimension = int(np.asarray(tables["root_nodes"]).size) * P
+        self.output_dimension = self.logical_channel_tableau_dimension * self.magnetic_dimension
+        self.plan_hash = None if plan_hash is None else str(plan_hash)
+        self.factorized_angular_plan_id = None if plan_id is None else str(plan_id)
+        self.requested_backend = backend
+        self.resolved_backend = "native_hip"
+        self.last_linear_readout_backend = None
+        self.analysis_orientation = "conjugate_transpose"
+        self._plan = plan_for(tables, self.source_dimension, self.input_dimension, self.workspace_dimension,
+                              self.output_dimension, dtype, device)
+
+    @classmethod
+    def from_tables(cls, tables, *, input_Ls, source_dimension, output_L, **kw):
+        return cls(tables, input_Ls=input_Ls, source_dimension=source_dimension, output_L=output_L, **kw)
+
+    @classmethod
+    def from_execution_plan(cls, execution_plan, factorized_angular_plan_id=None, backend="auto", dtype=None,
+                            device=None):
+        """The reference constructor's form: a reference execution-plan
+        document (``YE3TExecutionPlan.to_dict()`` JSON) and the id of one of
+        its factorized-angular plans."""
+        from ye3t_amd.runtime import execution_plan as ep
+
+        plan = execution_plan if isinstance(execution_plan, ep.ExecutionPlan) else \
+            ep.ExecutionPlan.from_dict(execution_plan)
+        tables, meta = plan.factorized_angular_buffers(factorized_angular_plan_id)
+        return cls(tables, input_Ls=meta["input_Ls"], source_dimension=meta["source_dimension"],
+                   output_L=meta["output_L"], backend=backend, dtype=dtype, device=device,
+                   plan_hash=plan.plan_hash, plan_id=meta["plan_id"])
+
+    def _packed_slots(self, slot_values):
+        """Reference ``_packed_slots`` (``execution_plan.py:13688-13734``)."""
+        torch = _torch()
+        slots = tuple(slot_values)
+        if len(slots) != len(self.input_Ls):
+            raise ValueError("slot tensor count does not match input_Ls")
+        if self.source_dimension == 1:
+            leading = tuple(slots[0].shape[:-1])
+        else:
+            if slots[0].ndim < 2:
+                raise ValueError("role-resolved slots require a source-coordinate axis")
+            leading = tuple(slots[0].shape[:-2])
+        work = []
+        for slot, L in zip(slots, self.input_Ls):
+            if int(slot.shape[-1]) != 2 * L + 1:
+                raise ValueError("slot magnetic dimension does not match input_Ls")
+            if self.source_dimension == 1:
+                if tuple(slot.shape[:-1]) != leading:
+                    raise ValueError("slot tensors must share leading dimensions")
+                slot = slot.unsqueeze(-2)
+            else:
+                if tuple(slot.shape[:-2]) != leading:
+                    raise ValueError("slot tensors must share leading dimensions")
+                if int(slot.shape[-2]) != self.source_dimension:
+                    raise ValueError("slot source axis does not match source assembly")
+            work.append(slot.to(dtype=self.coefficient_values.dtype, device=self.coefficient_values.device))
+        packed = torch.cat(tuple(work), dim=-1).reshape(-1, self.source_dimension * self.input_dimension)
+        return packed.contiguous(), leading
+
+    def forward(self, slot_values):
+        packed, leading = self._packed_slots(slot_values)
+        if int(packed.shape[0]) == 0:
+            out = packed[:, :1].expand(-1, self.output_dimension)
+        else:
+            out = _fns()[0].apply(packed, self._plan)
+        return out.reshape(leading + (self.logical_channel_tableau_dimension, self.magnetic_dimension))
+
+    def linear_readout(self, slot_values, weight, bias):
+        torch = _torch()
+        packed, leading = self._packed_slots(slot_values)
+        dt, dev = self.coefficient_values.dtype, self.coefficient_values.device
+        weight = torch.as_tensor(weight, dtype=dt, device=dev)
+        bias = torch.as_tensor(bias, dtype=dt, device=dev).reshape(())
+        if weight.ndim != 1 or int(weight.numel()) != self.output_dimension:
+            raise ValueError("weight must be a vector matching factorized output dimension")
+        if int(packed.shape[0]) == 0:
+            self.last_linear_readout_backend = "empty_batch"
+            return packed[:, 0].reshape(leading)
+        out = _fns()[1].apply(packed, weight, bias, self._plan)
+        self.last_linear_readout_backend = "native_fused_factorized_linear"
+        return out.reshape(leading)
+
+    def runtime_report(self):
+        return {
+            "backend": self.resolved_backend, "native": True, "operation": "factorized_angular_source_analysis",
+            "factorized_angular_plan_id": self.factorized_angular_plan_id, "plan_hash": self.plan_hash,
+            "input_Ls": tuple(self.input_Ls), "source_dimension": int(self.source_dimension),
+            "workspace_dimension": int(self.workspace_dimension), "runtime_device_scalar_metadata_reads": 0,
+            "root_path_count": int(self.root_nodes.numel()), "unique_node_count": int(self.node_offsets.numel()),
+            "last_linear_readout_backend": self.last_linear_readout_backend,
+            "analysis_orientation": self.analysis_orientation,
+        }

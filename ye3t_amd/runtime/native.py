@@ -38,6 +38,16 @@ class ProductPlanDesc(ctypes.Structure):
                 ("out_dtype", ctypes.c_int), ("in_dtype", ctypes.c_int)]
 
 
+class FactorizedAngularDesc(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int), ("node_count", _i64), ("node_offsets", _vp), ("node_dimensions", _vp),
+                ("node_leaf_offsets", _vp), ("node_left", _vp), ("node_right", _vp),
+                ("node_coefficient_offsets", _vp), ("coefficient_count", _i64), ("coefficient_rows", _vp),
+                ("coefficient_columns", _vp), ("coefficient_values", _vp), ("root_count", _i64),
+                ("root_nodes", _vp), ("projection_count", _i64), ("projection_values", _vp),
+                ("source_dimension", _i64), ("input_dimension", _i64), ("workspace_dimension", _i64),
+                ("output_dimension", _i64)]
+
+
 class CellGrid(ctypes.Structure):
     _fields_ = [("origin", ctypes.c_double * 3), ("cell_edge", ctypes.c_double), ("dims", _i64 * 3)]
 
@@ -104,6 +114,14 @@ def lib():
     L.ye3t_hip_product_adjoint_workspace_bytes.restype = _i64
     L.ye3t_hip_product_adjoint_stream.argtypes = [_vp, _vp, _i64, ctypes.c_int, _vp, _i64, _vp, _i64, _vp, _vp]
     L.ye3t_hip_product_adjoint_stream_noalloc.argtypes = [_vp, _vp, _i64, ctypes.c_int, _vp, _i64, _vp, _vp]
+    L.ye3t_hip_factorized_angular_plan_create.argtypes = [ctypes.POINTER(FactorizedAngularDesc), ctypes.POINTER(_vp)]
+    L.ye3t_hip_factorized_angular_plan_destroy.argtypes = [_vp]
+    L.ye3t_hip_factorized_angular_plan_destroy.restype = None
+    L.ye3t_hip_factorized_angular_plan_info.argtypes = [_vp, _vp]
+    L.ye3t_hip_factorized_angular_forward.argtypes = [_vp, _vp, _i64, _vp, _vp]
+    L.ye3t_hip_factorized_angular_adjoint.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
+    L.ye3t_hip_factorized_angular_linear_forward.argtypes = [_vp, _vp, _i64, _vp, _vp, _vp, _vp]
+    L.ye3t_hip_factorized_angular_linear_adjoint.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp]
     L.ye3t_hip_neighbor_workspace_bytes.argtypes = [_i64, ctypes.POINTER(CellGrid)]
     L.ye3t_hip_neighbor_workspace_bytes.restype = _i64
     L.ye3t_hip_neighbor_count.argtypes = [ctypes.c_int, _vp, _i64, ctypes.POINTER(CellGrid), ctypes.c_double, _vp,
@@ -129,7 +147,10 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_neighbor_workspace_bytes", "ye3t_hip_neighbor_count", "ye3t_hip_neighbor_fill",
     "ye3t_hip_transpose", "ye3t_hip_product_forward_columns", "ye3t_hip_product_plan_uses_stream",
     "ye3t_hip_product_adjoint_workspace_bytes", "ye3t_hip_product_adjoint_stream", "ye3t_hip_product_stream_encode",
-    "ye3t_hip_product_adjoint_stream_noalloc",
+    "ye3t_hip_product_adjoint_stream_noalloc", "ye3t_hip_factorized_angular_plan_create",
+    "ye3t_hip_factorized_angular_plan_destroy", "ye3t_hip_factorized_angular_plan_info",
+    "ye3t_hip_factorized_angular_forward", "ye3t_hip_factorized_angular_adjoint",
+    "ye3t_hip_factorized_angular_linear_forward", "ye3t_hip_factorized_angular_linear_adjoint",
 )
 
 
@@ -137,6 +158,9 @@ def _check(rc, what):
     if rc != 0:
         msg = lib().ye3t_hip_last_error().decode(errors="replace")
         raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+C64, C128 = 2, 3
 
 
 def _dtype_code(t):
@@ -147,6 +171,16 @@ def _dtype_code(t):
     if t.dtype == torch.float32:
         return F32
     raise TypeError(f"unsupported dtype {t.dtype}; expected float32 or float64")
+
+
+def _any_dtype_code(dtype):
+    """ABI code of a real or complex torch dtype."""
+    import torch
+
+    codes = {torch.float32: F32, torch.float64: F64, torch.complex64: C64, torch.complex128: C128}
+    if dtype not in codes:
+        raise TypeError(f"unsupported dtype {dtype}; expected float32, float64, complex64 or complex128")
+    return codes[dtype]
 
 
 def _stream():
@@ -774,3 +808,147 @@ def transpose(A, out=None, ld=None):
     _check(lib().ye3t_hip_transpose(_dtype_code(A), _dev(A, "A"), rows, cols, _dev(out, "At"), ld, _stream()),
            "ye3t_hip_transpose")
     return out
+
+
+FA_TABLE_NAMES = ("node_offsets", "node_dimensions", "node_leaf_offsets", "node_left", "node_right",
+                  "node_coefficient_offsets", "coefficient_rows", "coefficient_columns", "coefficient_values",
+                  "root_nodes", "projection_values")
+
+
+class FactorizedAngularPlanHandle:
+    """A validated, device-resident factorized-angular DAG
+    (``ye3t_hip_factorized_angular_plan``): the reference op's tables
+    (``execution_plan_torch.cpp:7586-7594``) in ``dtype`` (a torch real or
+    complex dtype)."""
+
+    def __init__(self, tables, source_dimension, input_dimension, workspace_dimension, output_dimension, dtype):
+        import torch
+
+        self.dtype = dtype
+        np_t = {torch.float32: np.float32, torch.float64: np.float64, torch.complex64: np.complex64,
+                torch.complex128: np.complex128}[dtype]
+        keep = {}
+        for name in FA_TABLE_NAMES[:8] + ("root_nodes",):
+            v = tables[name]
+            v = v.detach().cpu().numpy() if hasattr(v, "detach") else np.asarray(v)
+            keep[name] = np.ascontiguousarray(v.reshape(-1), dtype=np.int64)
+        for name in ("coefficient_values", "projection_values"):
+            v = tables[name]
+            v = v.detach().cpu().numpy() if hasattr(v, "detach") else np.asarray(v)
+            keep[name] = np.ascontiguousarray(v.reshape(-1).astype(np_t))
+        self._keep = keep
+
+        def ptr(name):
+            a = keep[name]
+            return ctypes.c_void_p(a.ctypes.data) if a.size else None
+
+        desc = FactorizedAngularDesc(
+            dtype=_any_dtype_code(dtype), node_count=int(keep["node_offsets"].size),
+            node_offsets=ptr("node_offsets"), node_dimensions=ptr("node_dimensions"),
+            node_leaf_offsets=ptr("node_leaf_offsets"), node_left=ptr("node_left"), node_right=ptr("node_right"),
+            node_coefficient_offsets=ptr("node_coefficient_offsets"),
+            coefficient_count=int(keep["coefficient_rows"].size), coefficient_rows=ptr("coefficient_rows"),
+            coefficient_columns=ptr("coefficient_columns"), coefficient_values=ptr("coefficient_values"),
+            root_count=int(keep["root_nodes"].size), root_nodes=ptr("root_nodes"),
+            projection_count=int(keep["projection_values"].size), projection_values=ptr("projection_values"),
+            source_dimension=int(source_dimension), input_dimension=int(input_dimension),
+            workspace_dimension=int(workspace_dimension), output_dimension=int(output_dimension))
+        if int(keep["coefficient_values"].size) != desc.coefficient_count or \
+                int(keep["coefficient_columns"].size) != desc.coefficient_count:
+            raise RuntimeError("factorized coefficient arrays must have equal length")
+        n = desc.node_count
+        for name in ("node_dimensions", "node_leaf_offsets", "node_left", "node_right"):
+            if int(keep[name].size) != n:
+                raise RuntimeError("factorized node arrays must have equal length")
+        if int(keep["node_coefficient_offsets"].size) != n + 1:
+            raise RuntimeError("node_coefficient_offsets must have node_count + 1 entries")
+        handle = ctypes.c_void_p()
+        _check(lib().ye3t_hip_factorized_angular_plan_create(ctypes.byref(desc), ctypes.byref(handle)),
+               "ye3t_hip_factorized_angular_plan_create")
+        self._handle = handle
+        self.source_dimension = int(source_dimension)
+        self.input_dimension = int(input_dimension)
+        self.workspace_dimension = int(workspace_dimension)
+        self.output_dimension = int(output_dimension)
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h is not None and h.value and _LIB is not None:
+            _LIB.ye3t_hip_factorized_angular_plan_destroy(h)
+            self._handle = None
+
+    def _packed(self, packed):
+        if not packed.is_cuda or packed.dtype != self.dtype or packed.ndim != 2 or \
+                int(packed.shape[1]) != self.source_dimension * self.input_dimension:
+            raise ValueError(f"packed_slots must be a {self.dtype} GPU tensor "
+                             f"[batch, {self.source_dimension * self.input_dimension}]")
+        return packed.contiguous()
+
+    def forward(self, packed):
+        import torch
+
+        packed = self._packed(packed)
+        B = int(packed.shape[0])
+        out = torch.empty((B, self.output_dimension), dtype=self.dtype, device=packed.device)
+        _check(lib().ye3t_hip_factorized_angular_forward(self._handle, _dev(packed, "packed_slots"), B,
+                                                         _dev(out, "output"), _stream()),
+               "ye3t_hip_factorized_angular_forward")
+        return out
+
+    def adjoint(self, output_adjoint, packed):
+        import torch
+
+        packed = self._packed(packed)
+        B = int(packed.shape[0])
+        g = output_adjoint.to(self.dtype).contiguous()
+        if tuple(g.shape) != (B, self.output_dimension):
+            raise ValueError(f"output_adjoint must be [{B}, {self.output_dimension}]")
+        out = torch.empty_like(packed)
+        _check(lib().ye3t_hip_factorized_angular_adjoint(self._handle, _dev(g, "output_adjoint"),
+                                                         _dev(packed, "packed_slots"), B, _dev(out, "adjoint"),
+                                                         _stream()), "ye3t_hip_factorized_angular_adjoint")
+        return out
+
+    def _bias(self, bias):
+        if self.dtype.is_complex:
+            b = complex(bias)
+            dt = np.complex64 if self.dtype == __import__("torch").complex64 else np.complex128
+        else:
+            b = float(bias)
+            dt = np.float32 if self.dtype == __import__("torch").float32 else np.float64
+        return np.array([b], dtype=dt)
+
+    def linear(self, packed, weight, bias):
+        import torch
+
+        packed = self._packed(packed)
+        B = int(packed.shape[0])
+        w = weight.to(device=packed.device, dtype=self.dtype).contiguous()
+        if tuple(w.shape) != (self.output_dimension,):
+            raise ValueError("weight must be a vector matching factorized output dimension")
+        b = self._bias(bias)
+        out = torch.empty((B,), dtype=self.dtype, device=packed.device)
+        _check(lib().ye3t_hip_factorized_angular_linear_forward(self._handle, _dev(packed, "packed_slots"), B,
+                                                                _dev(w, "weight"), ctypes.c_void_p(b.ctypes.data),
+                                                                _dev(out, "output"), _stream()),
+               "ye3t_hip_factorized_angular_linear_forward")
+        return out
+
+    def linear_adjoint(self, output_adjoint, packed, weight):
+        import torch
+
+        packed = self._packed(packed)
+        B = int(packed.shape[0])
+        g = output_adjoint.to(self.dtype).contiguous()
+        w = weight.to(device=packed.device, dtype=self.dtype).contiguous()
+        if tuple(g.shape) != (B,) or tuple(w.shape) != (self.output_dimension,):
+            raise ValueError("output_adjoint must be [batch] and weight [output_dimension]")
+        feats = torch.empty((B, self.output_dimension), dtype=self.dtype, device=packed.device)
+        gx = torch.empty_like(packed)
+        gw = torch.empty_like(w)
+        gb = torch.empty((), dtype=self.dtype, device=packed.device)
+        _check(lib().ye3t_hip_factorized_angular_linear_adjoint(
+            self._handle, _dev(g, "output_adjoint"), _dev(packed, "packed_slots"), B, _dev(w, "weight"),
+            _dev(feats, "features"), _dev(gx, "packed_adjoint"), _dev(gw, "weight_adjoint"),
+            ctypes.c_void_p(gb.data_ptr()), _stream()), "ye3t_hip_factorized_angular_linear_adjoint")
+        return gx, gw, gb
