@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 52 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 53 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -140,13 +140,48 @@ int ye3t_hip_ace_density_forward(const ye3t_density_args* args, void* A, ye3t_st
 const char* ye3t_hip_last_density_kernel(void);
 
 /* S[b, o] = sum_{t in [output_offsets[o], output_offsets[o+1])} monomial_values[t]
- *           * prod_c input[b, c]^monomial_counts[t, c].
+ *           * prod_c input[b, c]^monomial_counts[t, c]
+ * for input[batch, input_dim], monomial_counts[T, input_dim], output_offsets[O+1]
+ * and output_indices[T] (the output of each term, consistent with the offsets;
+ * the adjoint's gather index).  Device tables, validated by the caller.
  * Replaces the CUDA branch of ye3t_runtime::symmetric_power_monomial
- * (kernel execution_plan_cuda.cu:5229; CPU ye3t_runtime_core.cpp:5279-5315). */
+ * (schema execution_plan_torch.cpp:7528-7530; kernel execution_plan_cuda.cu:5229;
+ * CPU ye3t_runtime_core.cpp:5279-5315). */
 int ye3t_hip_symmetric_power_monomial(int dtype, const void* input, int64_t batch, int64_t input_dim,
                                       const int64_t* monomial_counts, const int64_t* output_offsets,
-                                      const void* monomial_values, int64_t output_dim, void* output,
-                                      ye3t_stream_t stream);
+                                      const int64_t* output_indices, const void* monomial_values, int64_t term_count,
+                                      int64_t output_dim, void* output, ye3t_stream_t stream);
+
+/* input_adjoint[b, c] of output_adjoint[batch, output_dim] through the grouped
+ * table: the reference's rule for zero factors (ye3t_runtime_core.cpp:5318-5389).
+ * Replaces ye3t_runtime::symmetric_power_monomial_adjoint (schema
+ * execution_plan_torch.cpp:7531-7534). */
+int ye3t_hip_symmetric_power_monomial_adjoint(int dtype, const void* output_adjoint, const void* input,
+                                              int64_t batch, int64_t input_dim, const int64_t* monomial_counts,
+                                              const int64_t* output_indices, const void* monomial_values,
+                                              int64_t term_count, int64_t output_dim, void* input_adjoint,
+                                              ye3t_stream_t stream);
+
+/* S[b, o] = sum_{k in [output_offsets[o], output_offsets[o+1])} coefficient_values[k]
+ *           * prod_c input[b, c]^monomial_counts[coefficient_terms[k], c]:
+ * outputs as sparse combinations of monomial_count unique monomials.
+ * Replaces ye3t_runtime::symmetric_power_shared_monomial (schema
+ * execution_plan_torch.cpp:7540-7544; CPU ye3t_runtime_core.cpp:5392-5440). */
+int ye3t_hip_symmetric_power_shared_monomial(int dtype, const void* input, int64_t batch, int64_t input_dim,
+                                             const int64_t* monomial_counts, int64_t monomial_count,
+                                             const int64_t* output_offsets, const int64_t* coefficient_terms,
+                                             const void* coefficient_values, int64_t coefficient_count,
+                                             int64_t output_dim, void* output, ye3t_stream_t stream);
+
+/* Adjoint of the shared form (ye3t_runtime_core.cpp:5442-5540).  Replaces
+ * ye3t_runtime::symmetric_power_shared_monomial_adjoint. */
+int ye3t_hip_symmetric_power_shared_monomial_adjoint(int dtype, const void* output_adjoint, const void* input,
+                                                     int64_t batch, int64_t input_dim,
+                                                     const int64_t* monomial_counts, int64_t monomial_count,
+                                                     const int64_t* output_offsets,
+                                                     const int64_t* coefficient_terms,
+                                                     const void* coefficient_values, int64_t coefficient_count,
+                                                     int64_t output_dim, void* input_adjoint, ye3t_stream_t stream);
 
 /* out[b, k] = sum_{t in k} coeffs[t] prod_blk block_values[b, label_k, blk, block_m_indices[t, blk]].
  * Device counterpart of evaluate_factorized_schedule_cpu

@@ -103,3 +103,23 @@ def test_backend_reference_is_refused_explicitly():
         runtime.cheb_exp_cos_radial_table_with_derivative(x, x, x, 2, backend="reference")
     with pytest.raises(ValueError, match="backend"):
         runtime.cheb_exp_cos_radial_table_with_derivative(x, x, x, 2, backend="triton")
+
+
+def test_monomial_table_checks():
+    import numpy as np
+
+    counts = np.array([[2, 0], [1, 1], [0, 2]])
+    offs = np.array([0, 1, 3])
+    idx = np.array([0, 1, 1])
+    vals = np.array([1.0, 2.0, 3.0])
+    native.check_monomial_table(2, counts, offs, idx, vals)
+    for bad in ({"idx": np.array([0, 0, 1])}, {"offs": np.array([0, 2, 2])}, {"counts": counts[:, :1]},
+                {"vals": vals[:2]}, {"counts": -counts}):
+        kw = {"counts": counts, "offs": offs, "idx": idx, "vals": vals, **bad}
+        with pytest.raises(ValueError):
+            native.check_monomial_table(2, kw["counts"], kw["offs"], kw["idx"], kw["vals"])
+    native.check_shared_table(2, counts, offs, np.array([0, 1, 2]), idx, vals)
+    with pytest.raises(ValueError, match="coefficient_terms"):
+        native.check_shared_table(2, counts, offs, np.array([0, 1, 3]), idx, vals)
+    with pytest.raises(ValueError, match="coefficient_outputs"):
+        native.check_shared_table(2, counts, offs, np.array([0, 1, 2]), np.array([1, 1, 1]), vals)

@@ -11,8 +11,8 @@
 //     transposed output read is bank-conflict free).  Output columns of a chunk
 //     are written through LDS so each store instruction covers contiguous
 //     columns of one row.
-// (b) evaluate_schedule_kernel / sym_monomial_kernel: device versions of the
-//     reference's flat schedule evaluator and symmetric-power contraction.
+// (b) evaluate_schedule_kernel: device version of the reference's flat
+//     schedule evaluator (the symmetric-power contractions are in monomial.hip).
 #include <hip/hiprtc.h>
 
 #include <algorithm>
@@ -662,38 +662,6 @@ __global__ __launch_bounds__(256) void evaluate_schedule_kernel(
       const int64_t* tm = midx + t * blocks;
       for (int64_t blk = 0; blk < blocks; ++blk) v *= base[blk * mdim + tm[blk]];
       acc += v;
-    }
-    out[idx] = acc;
-  }
-}
-
-template <typename Real>
-__device__ inline Real ipow(Real b, int64_t e) {
-  Real v = Real(1);
-  while (e > 0) {
-    if (e & 1) v *= b;
-    e >>= 1;
-    if (e > 0) b *= b;
-  }
-  return v;
-}
-
-template <typename Real>
-__global__ __launch_bounds__(256) void sym_monomial_kernel(const Real* __restrict__ x, int64_t batch, int64_t D,
-                                                           const int64_t* __restrict__ counts,
-                                                           const int64_t* __restrict__ offsets,
-                                                           const Real* __restrict__ values, int64_t O,
-                                                           Real* __restrict__ out) {
-  const int64_t total = batch * O;
-  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t b = idx / O, o = idx - (idx / O) * O;
-    const Real* row = x + b * D;
-    Real acc = Real(0);
-    for (int64_t t = offsets[o]; t < offsets[o + 1]; ++t) {
-      Real m = values[t];
-      for (int64_t c = 0; c < D; ++c) m *= ipow(row[c], counts[t * D + c]);
-      acc += m;
     }
     out[idx] = acc;
   }
@@ -1591,26 +1559,6 @@ int ye3t_hip_evaluate_factorized_schedule(int dtype, const void* bv, int64_t bat
     return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);
   }
   return check_launch("evaluate_schedule_kernel");
-}
-
-int ye3t_hip_symmetric_power_monomial(int dtype, const void* x, int64_t batch, int64_t D, const int64_t* counts,
-                                      const int64_t* offsets, const void* values, int64_t O, void* out,
-                                      ye3t_stream_t stream) {
-  clear_error();
-  YE3T_REQUIRE(batch >= 0 && D >= 0 && O >= 0, "negative size");
-  if (batch * O == 0) return YE3T_OK;
-  YE3T_REQUIRE(x && offsets && out, "NULL argument");
-  const unsigned grid = grid_1d(batch * O, 256);
-  if (dtype == YE3T_F64) {
-    hipLaunchKernelGGL(sym_monomial_kernel<double>, dim3(grid), dim3(256), 0, as_stream(stream), (const double*)x,
-                       batch, D, counts, offsets, (const double*)values, O, (double*)out);
-  } else if (dtype == YE3T_F32) {
-    hipLaunchKernelGGL(sym_monomial_kernel<float>, dim3(grid), dim3(256), 0, as_stream(stream), (const float*)x,
-                       batch, D, counts, offsets, (const float*)values, O, (float*)out);
-  } else {
-    return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);
-  }
-  return check_launch("sym_monomial_kernel");
 }
 
 }  // extern "C"

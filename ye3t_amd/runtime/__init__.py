@@ -22,6 +22,9 @@ REFERENCE_OPERATIONS = (
     "density_accumulate",
     "density_accumulate_adjoint",
     "symmetric_power_monomial",
+    "symmetric_power_monomial_adjoint",
+    "symmetric_power_shared_monomial",
+    "symmetric_power_shared_monomial_adjoint",
     "factorized_angular",
     "factorized_angular_adjoint",
     "factorized_angular_linear",
@@ -191,12 +194,82 @@ def neighbor_list(positions, cutoff, *, backend="auto"):
     return native.neighbor_list(positions.contiguous(), float(cutoff))
 
 
-def symmetric_power_monomial_contraction(input, monomial_counts, output_offsets, monomial_values, *,
+def _monomial_functions():
+    import torch
+
+    class _Grouped(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x, counts, offsets, indices, values):
+            ctx.save_for_backward(x)
+            ctx.table = (counts, offsets, indices, values)
+            return native.symmetric_power_monomial(x, counts, offsets, values, output_indices=indices)
+
+        @staticmethod
+        def backward(ctx, g):
+            (x,) = ctx.saved_tensors
+            counts, offsets, indices, values = ctx.table
+            return native.symmetric_power_monomial_adjoint(g.contiguous(), x, counts, indices, values,
+                                                           offsets), None, None, None, None
+
+    class _Shared(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x, counts, offsets, terms, outputs, values):
+            ctx.save_for_backward(x)
+            ctx.table = (counts, offsets, terms, outputs, values)
+            return native.symmetric_power_shared_monomial(x, counts, offsets, terms, outputs, values)
+
+        @staticmethod
+        def backward(ctx, g):
+            (x,) = ctx.saved_tensors
+            return (native.symmetric_power_shared_monomial_adjoint(g.contiguous(), x, *ctx.table),
+                    None, None, None, None, None)
+
+    return _Grouped, _Shared
+
+
+_MONOMIAL_FNS = None
+
+
+def _monomials():
+    global _MONOMIAL_FNS
+    if _MONOMIAL_FNS is None:
+        _MONOMIAL_FNS = _monomial_functions()
+    return _MONOMIAL_FNS
+
+
+def _feature_rows(input, name):
+    if input.ndim < 1:
+        raise ValueError("symmetric-power input requires a feature axis")
+    _require_device(input, name)
+    return input.reshape(-1, int(input.shape[-1])).contiguous()
+
+
+def symmetric_power_monomial_contraction(input, monomial_counts, output_offsets, output_indices, monomial_values, *,
                                          backend="auto"):
-    """Symmetric-power monomial table contraction (reference ``ye3t_runtime_core.cpp:5279-5315``)."""
+    """Compiler-grouped symmetric-power table contraction (reference
+    ``execution_plan.py:11998-12095``; core ``ye3t_runtime_core.cpp:5279-5315``).
+
+    ``S[..., o] = sum_{t in [output_offsets[o], output_offsets[o+1])} v_t prod_c input[..., c]^counts[t, c]``;
+    ``output_indices[t]`` names the output of term t.  Differentiable: the
+    backward is the library's monomial adjoint (``ye3t_runtime_core.cpp:5318-5389``).
+    """
     _backend(backend, {"auto", "native"})
-    _require_device(input, "symmetric_power_monomial_contraction")
-    return native.symmetric_power_monomial(input.contiguous(), monomial_counts, output_offsets, monomial_values)
+    flat = _feature_rows(input, "symmetric_power_monomial_contraction")
+    out = _monomials()[0].apply(flat, monomial_counts, output_offsets, output_indices, monomial_values)
+    return out.reshape(tuple(input.shape[:-1]) + (int(out.shape[-1]),))
+
+
+def symmetric_power_shared_monomial_contraction(input, monomial_counts, output_offsets, coefficient_terms,
+                                                coefficient_outputs, coefficient_values, *, backend="auto"):
+    """Shared-monomial symmetric-power contraction (reference
+    ``execution_plan.py:12502-12600``; core ``ye3t_runtime_core.cpp:5392-5440``):
+    outputs are sparse combinations of unique monomials.  Differentiable
+    (adjoint ``ye3t_runtime_core.cpp:5442-5540``)."""
+    _backend(backend, {"auto", "native"})
+    flat = _feature_rows(input, "symmetric_power_shared_monomial_contraction")
+    out = _monomials()[1].apply(flat, monomial_counts, output_offsets, coefficient_terms, coefficient_outputs,
+                                coefficient_values)
+    return out.reshape(tuple(input.shape[:-1]) + (int(out.shape[-1]),))
 
 
 def native_execution_plan_capabilities():

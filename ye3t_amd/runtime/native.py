@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 52
+ABI_VERSION = 53
 _LIB = None
 
 F32, F64 = 0, 1
@@ -85,7 +85,14 @@ def lib():
     L.ye3t_hip_density_accumulate_csr.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _vp]
     L.ye3t_hip_density_accumulate_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _i64, _vp, _vp]
     L.ye3t_hip_ace_density_forward.argtypes = [ctypes.POINTER(DensityArgs), _vp, _vp]
-    L.ye3t_hip_symmetric_power_monomial.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp]
+    L.ye3t_hip_symmetric_power_monomial.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
+                                                    _vp, _vp]
+    L.ye3t_hip_symmetric_power_monomial_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64,
+                                                            _i64, _vp, _vp]
+    L.ye3t_hip_symmetric_power_shared_monomial.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp,
+                                                           _i64, _i64, _vp, _vp]
+    L.ye3t_hip_symmetric_power_shared_monomial_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _i64, _vp,
+                                                                   _vp, _vp, _i64, _i64, _vp, _vp]
     L.ye3t_hip_evaluate_factorized_schedule.argtypes = [ctypes.c_int, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp,
                                                         _vp, _i64, _vp, _vp]
     L.ye3t_hip_product_plan_create.argtypes = [ctypes.POINTER(ProductPlanDesc), ctypes.POINTER(_vp)]
@@ -151,6 +158,8 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_factorized_angular_plan_destroy", "ye3t_hip_factorized_angular_plan_info",
     "ye3t_hip_factorized_angular_forward", "ye3t_hip_factorized_angular_adjoint",
     "ye3t_hip_factorized_angular_linear_forward", "ye3t_hip_factorized_angular_linear_adjoint",
+    "ye3t_hip_symmetric_power_monomial_adjoint", "ye3t_hip_symmetric_power_shared_monomial",
+    "ye3t_hip_symmetric_power_shared_monomial_adjoint",
 )
 
 
@@ -335,25 +344,153 @@ def last_density_kernel():
     return lib().ye3t_hip_last_density_kernel().decode()
 
 
-def symmetric_power_monomial(x, monomial_counts, output_offsets, monomial_values):
+def _host_i64(a):
+    return np.ascontiguousarray(np.asarray(a.detach().cpu() if hasattr(a, "detach") else a), dtype=np.int64)
+
+
+def _host_real(a):
+    return np.asarray(a.detach().cpu() if hasattr(a, "detach") else a)
+
+
+def check_monomial_table(D, monomial_counts, output_offsets, output_indices, monomial_values):
+    """Host checks of a grouped monomial table (the reference op's and core's
+    contract, execution_plan.py:11894-11940, execution_plan_torch.cpp): returns
+    the int64 host arrays."""
+    counts = _host_i64(monomial_counts)
+    offs = _host_i64(output_offsets).reshape(-1)
+    idx = _host_i64(output_indices).reshape(-1)
+    T = int(np.asarray(_host_real(monomial_values)).reshape(-1).shape[0])
+    if counts.ndim != 2 or int(counts.shape[1]) != int(D):
+        raise ValueError("monomial_counts must have shape [term, input_dimension]")
+    if int(idx.size) != int(counts.shape[0]):
+        raise ValueError("output_indices length must match the term count")
+    if T != int(counts.shape[0]):
+        raise ValueError("monomial_values length must match the term count")
+    if offs.size < 1:
+        raise ValueError("output_offsets must contain at least one entry")
+    O = int(offs.size) - 1
+    if offs[0] != 0 or offs[-1] != T or np.any(np.diff(offs) < 0):
+        raise ValueError("output_offsets must be a nondecreasing CSR over the terms")
+    if T and np.any(np.repeat(np.arange(O), np.diff(offs)) != idx):
+        raise ValueError("output_indices must agree with output_offsets")
+    if np.any(counts < 0):
+        raise ValueError("monomial_counts must be nonnegative")
+    return counts, offs, idx
+
+
+def check_shared_table(D, monomial_counts, output_offsets, coefficient_terms, coefficient_outputs,
+                       coefficient_values):
+    """Host checks of a shared monomial table (execution_plan.py:12100-12160,
+    execution_plan_torch.cpp:5820-5860); returns the int64 host arrays."""
+    counts = _host_i64(monomial_counts)
+    offs = _host_i64(output_offsets).reshape(-1)
+    terms = _host_i64(coefficient_terms).reshape(-1)
+    outs = _host_i64(coefficient_outputs).reshape(-1)
+    C = int(np.asarray(_host_real(coefficient_values)).reshape(-1).shape[0])
+    if counts.ndim != 2 or int(counts.shape[1]) != int(D):
+        raise ValueError("monomial_counts must have shape [monomial, input_dimension]")
+    if int(outs.size) != int(terms.size):
+        raise ValueError("coefficient_outputs length must match coefficient_terms")
+    if C != int(terms.size):
+        raise ValueError("coefficient_values length must match coefficient_terms")
+    if offs.size < 1:
+        raise ValueError("output_offsets must contain at least one entry")
+    O = int(offs.size) - 1
+    if offs[0] != 0 or offs[-1] != C or np.any(np.diff(offs) < 0):
+        raise ValueError("output_offsets must span the coefficient table")
+    if C and (terms.min() < 0 or terms.max() >= counts.shape[0]):
+        raise ValueError("coefficient_terms contains an invalid monomial")
+    if C and np.any(np.repeat(np.arange(O), np.diff(offs)) != outs):
+        raise ValueError("coefficient_outputs must agree with output_offsets")
+    if np.any(counts < 0):
+        raise ValueError("monomial_counts must be nonnegative")
+    return counts, offs, terms, outs
+
+
+def _dev_i64(a, device):
+    import torch
+
+    return torch.as_tensor(a, dtype=torch.int64, device=device).contiguous()
+
+
+def symmetric_power_monomial(x, monomial_counts, output_offsets, monomial_values, output_indices=None):
+    """Grouped monomial table on the device (``output_indices`` defaults to the
+    offsets' own term-to-output map)."""
     import torch
 
     B, D = (int(s) for s in x.shape)
-    T = int(monomial_values.shape[0])
-    counts = np.asarray(monomial_counts.cpu() if hasattr(monomial_counts, "cpu") else monomial_counts)
-    offs = np.asarray(output_offsets.cpu() if hasattr(output_offsets, "cpu") else output_offsets)
-    if counts.shape != (T, D) or offs.ndim != 1 or offs[0] != 0 or offs[-1] != T or np.any(np.diff(offs) < 0):
-        raise ValueError("invalid monomial table")
-    if np.any(counts < 0):
-        raise ValueError("negative monomial exponent")
-    O = int(offs.shape[0] - 1)
+    if output_indices is None:
+        offs = _host_i64(output_offsets).reshape(-1)
+        output_indices = np.repeat(np.arange(offs.size - 1), np.diff(offs))
+    counts, offs, idx = check_monomial_table(D, monomial_counts, output_offsets, output_indices, monomial_values)
+    T, O = int(counts.shape[0]), int(offs.size - 1)
     out = torch.empty((B, O), dtype=x.dtype, device=x.device)
-    dc = torch.as_tensor(counts, dtype=torch.int64, device=x.device).contiguous()
-    do = torch.as_tensor(offs, dtype=torch.int64, device=x.device).contiguous()
-    dv = monomial_values.to(device=x.device, dtype=x.dtype).contiguous()
+    dv = torch.as_tensor(_host_real(monomial_values), device=x.device).to(x.dtype).contiguous()
+    dc, do, di = _dev_i64(counts, x.device), _dev_i64(offs, x.device), _dev_i64(idx, x.device)
     _check(lib().ye3t_hip_symmetric_power_monomial(_dtype_code(x), _dev(x, "input"), B, D, _dev(dc, "counts"),
-                                                   _dev(do, "offsets"), _dev(dv, "values"), O, _dev(out, "out"),
-                                                   _stream()), "ye3t_hip_symmetric_power_monomial")
+                                                   _dev(do, "offsets"), _dev(di, "indices"), _dev(dv, "values"), T, O,
+                                                   _dev(out, "out"), _stream()), "ye3t_hip_symmetric_power_monomial")
+    return out
+
+
+def symmetric_power_monomial_adjoint(output_adjoint, x, monomial_counts, output_indices, monomial_values,
+                                     output_offsets):
+    import torch
+
+    B, D = (int(s) for s in x.shape)
+    counts, offs, idx = check_monomial_table(D, monomial_counts, output_offsets, output_indices, monomial_values)
+    T, O = int(counts.shape[0]), int(offs.size - 1)
+    g = output_adjoint.to(x.dtype).contiguous()
+    if tuple(g.shape) != (B, O):
+        raise ValueError(f"output_adjoint must be [{B}, {O}]")
+    out = torch.empty_like(x)
+    dv = torch.as_tensor(_host_real(monomial_values), device=x.device).to(x.dtype).contiguous()
+    dc, di = _dev_i64(counts, x.device), _dev_i64(idx, x.device)
+    _check(lib().ye3t_hip_symmetric_power_monomial_adjoint(_dtype_code(x), _dev(g, "output_adjoint"),
+                                                           _dev(x, "input"), B, D, _dev(dc, "counts"),
+                                                           _dev(di, "indices"), _dev(dv, "values"), T, O,
+                                                           _dev(out, "input_adjoint"), _stream()),
+           "ye3t_hip_symmetric_power_monomial_adjoint")
+    return out
+
+
+def symmetric_power_shared_monomial(x, monomial_counts, output_offsets, coefficient_terms, coefficient_outputs,
+                                    coefficient_values):
+    import torch
+
+    B, D = (int(s) for s in x.shape)
+    counts, offs, terms, _ = check_shared_table(D, monomial_counts, output_offsets, coefficient_terms,
+                                                coefficient_outputs, coefficient_values)
+    M, C, O = int(counts.shape[0]), int(terms.size), int(offs.size - 1)
+    out = torch.empty((B, O), dtype=x.dtype, device=x.device)
+    dv = torch.as_tensor(_host_real(coefficient_values), device=x.device).to(x.dtype).contiguous()
+    dc, do, dt = _dev_i64(counts, x.device), _dev_i64(offs, x.device), _dev_i64(terms, x.device)
+    _check(lib().ye3t_hip_symmetric_power_shared_monomial(_dtype_code(x), _dev(x, "input"), B, D,
+                                                          _dev(dc, "counts") if M else None, M, _dev(do, "offsets"),
+                                                          _dev(dt, "terms") if C else None,
+                                                          _dev(dv, "values") if C else None, C, O, _dev(out, "out"),
+                                                          _stream()), "ye3t_hip_symmetric_power_shared_monomial")
+    return out
+
+
+def symmetric_power_shared_monomial_adjoint(output_adjoint, x, monomial_counts, output_offsets, coefficient_terms,
+                                            coefficient_outputs, coefficient_values):
+    import torch
+
+    B, D = (int(s) for s in x.shape)
+    counts, offs, terms, _ = check_shared_table(D, monomial_counts, output_offsets, coefficient_terms,
+                                                coefficient_outputs, coefficient_values)
+    M, C, O = int(counts.shape[0]), int(terms.size), int(offs.size - 1)
+    g = output_adjoint.to(x.dtype).contiguous()
+    if tuple(g.shape) != (B, O):
+        raise ValueError(f"output_adjoint must be [{B}, {O}]")
+    out = torch.empty_like(x)
+    dv = torch.as_tensor(_host_real(coefficient_values), device=x.device).to(x.dtype).contiguous()
+    dc, do, dt = _dev_i64(counts, x.device), _dev_i64(offs, x.device), _dev_i64(terms, x.device)
+    _check(lib().ye3t_hip_symmetric_power_shared_monomial_adjoint(
+        _dtype_code(x), _dev(g, "output_adjoint"), _dev(x, "input"), B, D, _dev(dc, "counts") if M else None, M,
+        _dev(do, "offsets"), _dev(dt, "terms") if C else None, _dev(dv, "values") if C else None, C, O,
+        _dev(out, "input_adjoint"), _stream()), "ye3t_hip_symmetric_power_shared_monomial_adjoint")
     return out
 
 
