@@ -114,6 +114,13 @@ def real_to_complex_unitary(L):
 
     For ``m>0``: ``Y^c_{+m} = (-1)^m (Y^r_{+m} - i Y^r_{-m}) / sqrt 2`` and
     ``Y^c_{-m} = (Y^r_{+m} + i Y^r_{-m}) / sqrt 2``; ``Y^c_0 = Y^r_0``.
+
+    This is the ordering of the real spherical-harmonic tables (cosine-type
+    ``Re[(x+iy)^m]`` at index ``l+m``, ``ye3t_runtime_core.cpp:226-290`` and
+    ``runtime/execution_plan.py:6919-6962``), so a density built from those
+    tables is a real multiplet in this basis.  The reference's tesseral map
+    (``core/tesseral.py:13-24, 124-140``) stores the cosine type at ``l-m``
+    instead: its ``W_tess[m, a] = W[m, 2l-a]`` (see :func:`tesseral_unitary`).
     """
     L = int(L)
     W = np.zeros((2 * L + 1, 2 * L + 1), dtype=np.complex128)
@@ -125,6 +132,21 @@ def real_to_complex_unitary(L):
         W[L + m, L - m] = -sign * 1j * r
         W[L - m, L + m] = r
         W[L - m, L - m] = 1j * r
+    W.setflags(write=False)
+    return W
+
+
+@lru_cache(maxsize=None)
+def tesseral_unitary(L):
+    """The reference's tesseral-to-Condon--Shortley map (``core/tesseral.py:124-140``).
+
+    ``c_{-m} = (t_{l-m} + i t_{l+m}) / sqrt 2``, ``c_{+m} = (-1)^m (t_{l-m} - i t_{l+m}) / sqrt 2``,
+    ``c_0 = t_l`` -- the formula the reference's own test spells out
+    (``tests/test_numeric_structured_expansion.py:503-520``).  It is
+    :func:`real_to_complex_unitary` with the real index reversed.
+    """
+    L = int(L)
+    W = np.ascontiguousarray(real_to_complex_unitary(L)[:, ::-1])
     W.setflags(write=False)
     return W
 
@@ -161,6 +183,26 @@ def real_cg_tensor(left_L, right_L, output_L):
     real[np.abs(real) < 1e-15] = 0.0
     real.setflags(write=False)
     return real
+
+
+@lru_cache(maxsize=None)
+def tesseral_cg_entries(left_L, right_L, output_L, tol=1e-14):
+    """Real CG nonzeros ``(a, b, c, value)`` in the reference's tesseral ordering.
+
+    The table of ``_real_cg_entries_exact`` (``core/tesseral.py:48-82``, via
+    ``paired_cg.py:62-72``): the same lowering as :func:`real_cg_tensor` with
+    every index reversed (``a -> 2l-a``), sorted by ``(a, b, c)`` and filtered
+    at ``|value| > tol``.
+    """
+    T = real_cg_tensor(left_L, right_L, output_L)[::-1, ::-1, ::-1]
+    entries = []
+    for a in range(T.shape[0]):
+        for b in range(T.shape[1]):
+            for c in range(T.shape[2]):
+                v = float(T[a, b, c])
+                if abs(v) > tol:
+                    entries.append((a, b, c, v))
+    return tuple(entries)
 
 
 @lru_cache(maxsize=None)

@@ -383,3 +383,246 @@ def evaluate_factorized_schedule_torch(block_values, schedule, *, backend="auto"
         values = values * block_values[batch_index, term_label.unsqueeze(0), blk, m_idx[:, blk].unsqueeze(0)]
     out.index_add_(1, term_comp, values)
     return out
+
+
+# ------------------------------------------------------------ real tesseral
+@dataclass(eq=False)
+class RealFactorizedCoefficientSchedule:
+    """Real-tesseral inter-block CG schedule for collapsed ACE blocks.
+
+    Fields of the reference record (``ye3t/core/couplings.py:313-420``).  Block
+    and output components are real indices in the reference's tesseral ordering
+    (:func:`ye3t_amd.core.cg.tesseral_unitary`), so ``block_real_tuples`` index
+    the block values directly.
+    """
+
+    rank: int
+    block_count: int
+    L_R: int
+    n_tuple: tuple
+    l_tuple: tuple
+    tree_type: str
+    block_specs: tuple
+    angular_keys: tuple
+    basis_keys: tuple
+    component_indices: np.ndarray
+    component_label_index: np.ndarray
+    component_offsets: np.ndarray
+    block_real_tuples: np.ndarray
+    coeffs: np.ndarray
+    basis_convention: str = "real_tesseral"
+    permutation_sector: str = "trivial"
+    backend_provenance: str = "real_cg_direct"
+    complex_term_count: int = -1
+    fallback_reason: object = None
+    structured_labels: tuple = ()
+
+    @property
+    def basis_count(self):
+        return int(len(self.angular_keys))
+
+    @property
+    def component_count(self):
+        return int(len(self.component_label_index))
+
+    @property
+    def term_count(self):
+        return int(len(self.coeffs))
+
+    def component_terms(self, component_index):
+        start = int(self.component_offsets[int(component_index)])
+        stop = int(self.component_offsets[int(component_index) + 1])
+        return self.block_real_tuples[start:stop], self.coeffs[start:stop]
+
+    def block_L_by_label(self, *, dtype=np.int16):
+        values = [[int(s["Lambda"] if s["kind"] == "sym" else s["l"]) for s in specs]
+                  for specs in self.block_specs]
+        if not values:
+            return np.zeros((0, int(self.block_count)), dtype=dtype)
+        return np.asarray(values, dtype=dtype)
+
+    def metadata(self):
+        return {"basis_convention": str(self.basis_convention),
+                "permutation_sector": str(self.permutation_sector),
+                "backend_provenance": str(self.backend_provenance),
+                "term_count": int(self.term_count),
+                "complex_term_count": int(self.complex_term_count),
+                "fallback_reason": None if self.fallback_reason is None else str(self.fallback_reason)}
+
+    def flat_arrays(self):
+        """Runtime arrays of ``to_torch`` (``core/couplings.py:378-420``) as numpy;
+        ``block_m_indices`` are the real component indices themselves."""
+        offsets = np.asarray(self.component_offsets, dtype=np.int64)
+        term_component = np.repeat(np.arange(self.component_count, dtype=np.int64), np.diff(offsets))
+        label_index = np.asarray(self.component_label_index, dtype=np.int64)
+        term_label = label_index[term_component] if term_component.size else np.zeros(0, np.int64)
+        block_L = self.block_L_by_label(dtype=np.int64)
+        if self.term_count and self.block_count:
+            idx = np.asarray(self.block_real_tuples, dtype=np.int64)
+        else:
+            idx = np.zeros((0, int(self.block_count)), dtype=np.int64)
+        return {
+            "component_offsets": offsets,
+            "component_label_index": label_index,
+            "term_component_index": term_component,
+            "term_label_index": term_label,
+            "block_m_indices": np.ascontiguousarray(idx),
+            "coeffs": np.ascontiguousarray(self.coeffs, dtype=np.float64),
+            "max_block_m_dim": int(2 * int(block_L.max()) + 1) if block_L.size else 0,
+        }
+
+
+def _as_tuple(value):
+    if isinstance(value, (list, tuple)):
+        return tuple(_as_tuple(v) for v in value)
+    return value
+
+
+def structured_label_from_compact(compact):
+    """The structured label whose ``compact_label`` is ``compact`` (its ``count`` order)."""
+    compact = _as_tuple(compact)
+    n_seq, l_seq, internal = compact[0], compact[1], compact[2]
+    tree_type = compact[3] if len(compact) > 3 else "balanced"
+    target = int(internal[-1]) if internal else int(l_seq[0])
+    for lab in _basis.structured_labels_by_L(tuple(n_seq), tuple(l_seq), tree_type).get(target, ()):
+        if _basis.compact_label(lab, tree_type) == compact:
+            return lab
+    raise ValueError(f"Could not recover structured label for {compact!r}.")
+
+
+def _label_total_L(label):
+    return int(label[2] if label[0] == "leaf" else label[4] if label[0] == "sym" else label[3])
+
+
+_REAL_PATH_CACHE = {}
+
+
+def expand_real_path(label):
+    """Root component, block real tuples and coefficients of one structured label.
+
+    Reference ``_expand_block_real_path_arrays`` (``core/couplings.py:1339-1403``):
+    leaves and collapsed sym blocks are identities on their ``2L+1``
+    components; a node walks the tesseral CG nonzeros in ``(a, b, c)`` order
+    and, for each, pairs every left term ending in ``a`` with every right term
+    ending in ``b`` (left outer), keeping ``|product| > 1e-14``.
+    """
+    key = _basis.path_key(label)
+    cached = _REAL_PATH_CACHE.get(key)
+    if cached is not None:
+        return cached
+    if label[0] in ("leaf", "sym"):
+        dim = 2 * _label_total_L(label) + 1
+        idx = np.arange(dim, dtype=np.int16)
+        out = (idx, idx.reshape(dim, 1), np.ones(dim, dtype=np.float64))
+    else:
+        from ye3t_amd.core.cg import tesseral_cg_entries
+
+        l_out, l_tup, l_co = expand_real_path(label[1])
+        r_out, r_tup, r_co = expand_real_path(label[2])
+        width = l_tup.shape[1] + r_tup.shape[1]
+        entries = tesseral_cg_entries(_label_total_L(label[1]), _label_total_L(label[2]), int(label[3]))
+        outs, tups, cos = [], [], []
+        if entries and l_out.size and r_out.size:
+            l_by = {}
+            r_by = {}
+            for i, c in enumerate(l_out.tolist()):
+                l_by.setdefault(int(c), []).append(i)
+            for i, c in enumerate(r_out.tolist()):
+                r_by.setdefault(int(c), []).append(i)
+            for a, b, c, v in entries:
+                li, ri = l_by.get(a), r_by.get(b)
+                if not li or not ri:
+                    continue
+                fl = np.repeat(np.asarray(li, np.int64), len(ri))
+                fr = np.tile(np.asarray(ri, np.int64), len(li))
+                co = l_co[fl] * r_co[fr] * float(v)
+                keep = np.abs(co) > 1.0e-14
+                if not np.any(keep):
+                    continue
+                outs.append(np.full(int(np.count_nonzero(keep)), c, dtype=np.int16))
+                tups.append(np.concatenate((l_tup[fl], r_tup[fr]), axis=1)[keep])
+                cos.append(co[keep])
+        if outs:
+            out = (np.concatenate(outs).astype(np.int16), np.concatenate(tups).astype(np.int16),
+                   np.concatenate(cos))
+        else:
+            out = (np.zeros(0, np.int16), np.zeros((0, width), np.int16), np.zeros(0, np.float64))
+    _REAL_PATH_CACHE[key] = out
+    return out
+
+
+def generate_real_factorized_coefficient_schedule_for_labels(labels, component_indices=None, coeff_tol=1e-14, *,
+                                                             coeff_dtype=np.float64, real_index_dtype=np.int16):
+    """Real-tesseral factorized ACE schedule of compact labels.
+
+    Reference ``generate_real_factorized_coefficient_schedule_for_labels`` /
+    ``_real_factorized_schedule_from_structured_labels``
+    (``core/couplings.py:1818-1966``): assembled label-major, components in
+    ``component_indices`` order, terms in :func:`expand_real_path` order.
+    """
+    labels = [_as_tuple(lab) for lab in labels]
+    if not labels:
+        return RealFactorizedCoefficientSchedule(
+            rank=0, block_count=0, L_R=0, n_tuple=(), l_tuple=(), tree_type="balanced", block_specs=(),
+            angular_keys=(), basis_keys=(), component_indices=np.asarray([0], dtype=np.int64),
+            component_label_index=np.zeros(0, np.int64), component_offsets=np.zeros(1, np.int64),
+            block_real_tuples=np.zeros((0, 0), dtype=real_index_dtype), coeffs=np.zeros(0, dtype=coeff_dtype))
+    structured = [structured_label_from_compact(lab) for lab in labels]
+    first = labels[0]
+    tree_type = first[3] if len(first) > 3 else "balanced"
+    L_R = _label_total_L(structured[0])
+    rank = len(first[0])
+    if component_indices is None:
+        component_indices = range(0, 2 * L_R + 1)
+    component_indices = tuple(int(c) for c in component_indices)
+    for c in component_indices:
+        if c < 0 or c >= 2 * L_R + 1:
+            raise ValueError(f"Real component index {c} is outside V_{L_R}.")
+    for lab, s in zip(labels, structured):
+        if _label_total_L(s) != L_R:
+            raise ValueError("All labels must share one final L_R.")
+        if len(lab[0]) != rank:
+            raise ValueError("All labels must have the same rank.")
+    specs = tuple(_basis.block_specs(s) for s in structured)
+    block_count = len(specs[0])
+    comp_label, offsets, tup_chunks, co_chunks = [], [0], [], []
+    for label_index, s in enumerate(structured):
+        root, tuples, coeffs = expand_real_path(s)
+        for c in component_indices:
+            comp_label.append(label_index)
+            keep = root == c
+            if coeff_tol > 0.0:
+                keep = keep & (np.abs(coeffs) > float(coeff_tol))
+            count = int(np.count_nonzero(keep))
+            if count:
+                tup_chunks.append(tuples[keep])
+                co_chunks.append(coeffs[keep])
+            offsets.append(offsets[-1] + count)
+    block_real = (np.concatenate(tup_chunks).astype(real_index_dtype) if tup_chunks
+                  else np.zeros((0, block_count), dtype=real_index_dtype))
+    coeffs = (np.concatenate(co_chunks).astype(coeff_dtype) if co_chunks else np.zeros(0, dtype=coeff_dtype))
+    keys = []
+    for lab in labels:
+        basis_key = lab[4] if len(lab) == 5 else ()
+        keys.append((angular_key(lab[1], lab[2], tree_type, basis_key), tuple(basis_key)))
+    complex_terms = _schedule_from_structured(structured, L_R, tree_type, coeff_tol).term_count
+    return RealFactorizedCoefficientSchedule(
+        rank=rank, block_count=block_count, L_R=L_R, n_tuple=tuple(first[0]), l_tuple=tuple(first[1]),
+        tree_type=tree_type, block_specs=specs, angular_keys=tuple(k for k, _ in keys),
+        basis_keys=tuple(b for _, b in keys), component_indices=np.asarray(component_indices, dtype=np.int64),
+        component_label_index=np.asarray(comp_label, dtype=np.int64),
+        component_offsets=np.asarray(offsets, dtype=np.int64), block_real_tuples=block_real, coeffs=coeffs,
+        complex_term_count=int(complex_terms), structured_labels=tuple(structured))
+
+
+def evaluate_real_factorized_schedule_torch(block_values, schedule, *, backend="auto"):
+    """Evaluate a real-tesseral schedule (reference ``core/couplings.py:570-610``).
+
+    Same contract as :func:`evaluate_factorized_schedule_torch`; real block
+    values only.  ``"auto"`` runs the HIP kernel on a GPU tensor.
+    """
+    import torch
+
+    if torch.is_complex(block_values):
+        raise ValueError("Real factorized schedule evaluation requires real block values.")
+    return evaluate_factorized_schedule_torch(block_values, schedule, backend=backend)
