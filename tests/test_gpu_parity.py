@@ -535,6 +535,42 @@ def _random_csr_workload(mode, atoms, max_degree, seed, n_max=8, l_max=3, channe
     return inp
 
 
+@pytest.mark.parametrize("storage", ["f32", "f64"])
+def test_channel_density_aligned_rows_and_cutoff_ties(gpu, storage):
+    """The channel kernel's unmasked form (atom ends on k-block boundaries, with
+    empty atoms between some of them, which send those chunks to the masked
+    form) and edges at exactly the cutoff distance and one ulp either side of it."""
+    flush(f"channel density aligned rows and cutoff ties {storage}")
+    inp = _random_csr_workload("features", 400, 64, 77)
+    rng = np.random.default_rng(78)
+    counts = 4 * rng.integers(0, 17, 400)
+    counts[::7] = 24
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    E = int(offsets[-1])
+    vec = rng.normal(size=(E, 3))
+    vec = vec / np.linalg.norm(vec, axis=1, keepdims=True) * rng.uniform(0.8, 5.2, (E, 1))
+    ft = np.float32 if storage == "f32" else np.float64
+    c = ft(5.0)
+    for k, v in enumerate([(c, 0, 0), (0, -c, 0), (0, 0, c), (np.nextafter(c, ft(6)), 0, 0),
+                           (0, np.nextafter(c, ft(4)), 0), (0, 0, -np.nextafter(c, ft(6)))]):
+        vec[k::37] = np.asarray(v, dtype=np.float64)
+    inp.update(edge_count=E, row_offsets=offsets, centers=np.repeat(np.arange(400), counts),
+               neighbors=rng.integers(0, 400, E), edge_vectors=vec)
+    dev = to_device_inputs(inp, storage, gpu)
+    ref = oracle.ace_density(rounded_inputs(inp, storage)).reshape(400, -1)
+    import torch
+
+    A = native.ace_density_forward(
+        dev["edge_vectors"], dev["row_offsets"], dev["neighbors"], atom_count=400, channel_count=16, n_max=8,
+        l_max=3, cutoff=5.0, lam=inp["lambda"], epsilon=inp["epsilon"], node_features=dev["node_features"],
+        radial_mix=dev["radial_mix"], out_dtype=torch.float64)
+    assert native.last_density_kernel() == "ace_density_channel16_kernel"
+    err = column_rel_error(A.cpu().numpy().reshape(400, -1), ref)
+    flush(f"  err {err:.3e}")
+    assert err < TOL[storage]
+    assert np.all(A.cpu().numpy()[counts == 0] == 0)
+
+
 @pytest.mark.parametrize("waves", [None, "1", "5", "64"])
 @pytest.mark.parametrize("mode,shape", [("features", (8, 3)), ("single", (8, 3)), ("single", (10, 4)),
                                         ("single", (12, 6))])
@@ -567,7 +603,7 @@ def test_fp64_mfma_density_random_csr(gpu, monkeypatch, mode, shape, storage, wa
         err = column_rel_error(outs[mfma], ref)
         flush(f"  mfma64={mfma} ({native.last_density_kernel()}) err {err:.3e}")
         if mfma == "mfma64":
-            expect = "ace_density_mfma64_channel_kernel" if mode == "features" else "ace_density_mfma64_kernel"
+            expect = "ace_density_channel16_kernel" if mode == "features" else "ace_density_mfma64_kernel"
             assert native.last_density_kernel() == expect
         assert err < TOL["f64"]
     # empty atoms are exact zeros

@@ -29,16 +29,16 @@
 //       MODE 2 -- node features with a per-channel radial mix, rows are
 //                 channels c, w_c(e) = h[nbr_e, c] * sum_n mix[c, n] g_n(e).
 // MODE 2 at 16 channels, n_max = 8, l_max = 3 runs on its own kernel
-// (ace_density_mfma64_channel_kernel) that also puts the radial mix on the
-// matrix cores and keeps W in registers.
+// (ace_density_channel16_kernel) that also puts the radial mix on the matrix
+// cores and keeps W in registers.
 #include <cmath>
 #include <cstdlib>
 
 #include "common.h"
 
-// Issue priority of the channel kernel's MFMA phase (phase 1 runs at 0).  With
+// Issue priority of the channel kernel's MFMA phase (phase 1 runs at 0): with
 // two waves per SIMD, the wave feeding the matrix core goes first while the
-// other fills the gaps with its VALU basis math: 57.4 -> 55.7 us at config 4.
+// other fills the gaps with its VALU basis math.
 #ifndef YE3T_DENSITY_SETPRIO
 #define YE3T_DENSITY_SETPRIO 1
 #endif
@@ -67,6 +67,11 @@ struct Density64Params {
   double den;                    // expm1(lambda)
   double eps;
   Out* __restrict__ A;           // fp64, or fp32 rounded once from the fp64 accumulators
+  // host-side reciprocals of the channel kernel
+  double inv_cutoff;             // 1 / cutoff
+  double two_over_den;           // 2 / expm1(lambda)
+  double inv_eps;                // 1 / eps
+  double cutoff_tie;             // 8 ulp(cutoff): distances this close decide liveness exactly
 };
 
 // offsets[i] through the constant address space: a scalar load (the CSR
@@ -304,145 +309,282 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
   for (; a < a_end; ++a) store_atom(a);
 }
 
-// MODE 2 at C = 16 channels, n_max = 8, l_max = 3 (one 16 x 16 density tile
-// per atom) with both products on the matrix cores and W never stored:
-//   phase 1  lane = edge, branch-free: real SH Y_lm (16) and the radial values
-//            g_1..g_8 in fp64 -> LDS ([lm][edge], [n - 1][edge]); the
-//            neighbour feature row -> LDS ([c][perm(edge)]), zero for padding
-//            lanes and for edges beyond the cutoff (whose g_n are all zero).
-//   phase 2  per 16-edge tile t: R[e][c] = mix[c][0] + sum_{n=1..8} g_n(e) mix[c][n]
-//            is two MFMAs, the constant g_0 = 1 entering as the accumulator's
-//            initial value.  Lane l then holds R[16 t + 4 v + l / 16][l % 16],
-//            which times h[e][c] is the A operand W[c][e] of k-block 4 t + v
-//            of the density product.  Atoms are walked with wave-relative
-//            32-bit edge indices and scalar compares; only a k-block that
-//            straddles an atom boundary is masked per lane.
+// ---------------------------------------------------------------------------
+// Channel kernel: MODE 2 at C = 16 channels, n_max = 8, l_max = 3 (one 16 x 16
+// density tile per atom), both products on the matrix cores.
+//
+// Per chunk of 64 edges (lane = edge in phase 1):
+//   phase 1  the distance, the radial values g_1..g_8 -> LDS ([n - 1][edge]),
+//            the neighbour feature row -> LDS ([c][perm(edge)], zero for
+//            padding lanes and for edges beyond the cutoff, whose g_n are all
+//            zero);
+//   mix      R[e][c] = mix[c][0] + sum_{n=1..8} g_n(e) mix[c][n] as two MFMAs
+//            per 16-edge tile (the constant g_0 = 1 enters as the initial
+//            accumulator); lane l then holds R[16 t + 4 v + l / 16][l % 16],
+//            which times h[e][c] is the A operand W[c][e] of k-block 4 t + v;
+//            the harmonics are computed next, over the radial rows (LDS keeps
+//            one wave's reads and writes in order, so the MFMA operand reads
+//            see g), which keeps the wave at 12.6 KB of LDS;
+//   phase 2  one MFMA per k-block of four edges.  A full chunk whose atom ends
+//            all fall on k-block boundaries, with every atom holding at least
+//            one k-block, runs as 16 unmasked MFMAs with a scalar test for an
+//            atom end after each; any other chunk masks each k-block per lane
+//            by atom and splits the k-blocks that straddle an atom boundary.
+// Atom ends come from a vector window of 64 CSR offsets (v_readlane), so the
+// MFMA loop issues no scalar loads.  The next chunk's loads (two register
+// sets, alternating) are issued after one wait for everything issued a chunk
+// earlier, so the basis math never waits on loads still in flight; edge
+// vectors, neighbour indices and the density are streamed non-temporally.
+// The basis math is written for this shape: closed-form real harmonics of
+// degree <= 3 (the reference's polynomials, not simplified with |u| = 1),
+// 1/sqrt by v_rsq_f64 and two Newton steps, cos(pi s) and expm1 by Taylor
+// polynomials truncated below 1e-17; liveness at the cutoff is decided
+// exactly as the reference does (sqrt, then a division) for the distances
+// within a few ulps of it.
+namespace chan16 {
+// sqrt2 N_lm Q_l^m(z) prefactors, N_lm = sqrt((2l+1)/(4 pi) (l-m)!/(l+m)!)
+constexpr double kC00 = 0.28209479177387814;   // N_00
+constexpr double kC1 = 0.4886025119029199;     // N_10 = sqrt2 N_11
+constexpr double kN20 = 0.63078313050504;      // N_20
+constexpr double kK21 = 1.0925484305920792;    // sqrt2 N_21 * 3
+constexpr double kK22 = 0.5462742152960396;    // sqrt2 N_22 * 3
+constexpr double kN30 = 0.7463526651802308;    // N_30
+constexpr double kK31 = 0.30469719964297715;   // sqrt2 N_31
+constexpr double kK32 = 1.4453057213202771;    // sqrt2 N_32 * 15
+constexpr double kK33 = 0.5900435899266435;    // sqrt2 N_33 * 15
+// sin(pi u) / u = sum_k (-1)^k pi^(2k+1) / (2k+1)! u^(2k), |u| <= 1/2
+constexpr double kSinPi[11] = {3.141592653589793,       -5.16771278004997,       2.5501640398773455,
+                               -0.5992645293207921,     0.08214588661112823,     -0.0073704309457143504,
+                               0.00046630280576761255,  -2.1915353447830217e-05, 7.952054001475513e-07,
+                               -2.2948428997269873e-08, 5.392664662608129e-10};
+// expm1(r) / r = sum_k r^k / (k+1)!, |r| <= ln2 / 2
+constexpr double kExpm1[13] = {1.0,
+                               0.5,
+                               0.16666666666666666,
+                               0.041666666666666664,
+                               0.008333333333333333,
+                               0.001388888888888889,
+                               0.0001984126984126984,
+                               2.48015873015873e-05,
+                               2.7557319223985893e-06,
+                               2.755731922398589e-07,
+                               2.505210838544172e-08,
+                               2.08767569878681e-09,
+                               1.6059043836821613e-10};
+constexpr double kLn2Hi = 0.6931471805599453, kLn2Lo = 2.3190468138462996e-17, kLog2e = 1.4426950408889634;
+
+// Both polynomials read their coefficients from an LDS copy of the tables
+// (kCoef: kSinPi then kExpm1): fetched where they are used, they do not sit in
+// registers for the whole kernel as hoisted 64-bit constants would.
+constexpr int kCoef = 11 + 13;
+
+// cos(pi s) for s in [0, 1] as -sin(pi (s - 1/2))
+__device__ inline double cospi01(double s, const double* coef) {
+  const double u = s - 0.5, u2 = u * u;
+  double q = coef[10];
+#pragma unroll
+  for (int i = 9; i >= 0; --i) q = fma(q, u2, coef[i]);
+  return -u * q;
+}
+
+// expm1(t) = 2^k expm1(r) + (2^k - 1), t = k ln2 + r (Cody-Waite)
+__device__ inline double expm1_reduced(double t, const double* coef) {
+  const double k = rint(t * kLog2e);
+  double r = fma(-k, kLn2Hi, t);
+  r = fma(-k, kLn2Lo, r);
+  double q = coef[11 + 12];
+#pragma unroll
+  for (int i = 11; i >= 0; --i) q = fma(q, r, coef[11 + i]);
+  const double scale = ldexp(1.0, int(k));
+  return fma(scale, q * r, scale - 1.0);
+}
+
+// the 16 real harmonics of degree <= 3 (column-major in Y: Y[lm * YP])
+template <int YP>
+__device__ inline void sph3(double x, double y, double z, double* Y) {
+  const double zz = z * z, xy = x * y, d2 = fma(x, x, -y * y);  // Re, Im/2 of (x+iy)^2
+  Y[0] = kC00;
+  Y[1 * YP] = -kC1 * y;
+  Y[2 * YP] = kC1 * z;
+  Y[3 * YP] = kC1 * x;
+  Y[4 * YP] = -2.0 * kK22 * xy;
+  Y[5 * YP] = -kK21 * z * y;
+  Y[6 * YP] = kN20 * fma(1.5, zz, -0.5);
+  Y[7 * YP] = kK21 * z * x;
+  Y[8 * YP] = kK22 * d2;
+  const double q31 = kK31 * fma(7.5, zz, -1.5);
+  Y[9 * YP] = -kK33 * y * fma(3.0 * x, x, -y * y);
+  Y[10 * YP] = -2.0 * kK32 * z * xy;
+  Y[11 * YP] = -q31 * y;
+  Y[12 * YP] = kN30 * z * fma(2.5, zz, -1.5);
+  Y[13 * YP] = q31 * x;
+  Y[14 * YP] = kK32 * z * d2;
+  Y[15 * YP] = kK33 * x * fma(x, x, -3.0 * y * y);
+}
+}  // namespace chan16
+
 template <typename In, typename Out>
-__global__ __launch_bounds__(64) void ace_density_mfma64_channel_kernel(Density64Params<In, Out> p, NormTable nt) {
-  constexpr int C = 16, NR = 9, LMAX = 3, LW = 16;
+__global__ __launch_bounds__(64) void ace_density_channel16_kernel(Density64Params<In, Out> p) {
+  using namespace chan16;
+  constexpr int C = 16, NR = 9, LW = 16;
   constexpr int YP = 65;                         // pitch (doubles) of Yt and Gt, odd
   constexpr int HP = sizeof(In) == 4 ? 68 : 66;  // pitch (elements) of Ht: rows 16-byte aligned
   typedef In in4 __attribute__((ext_vector_type(4)));
+  // harmonics [lm][edge]; rows 0..7 first hold the radial values g_1..g_8
+  // [n - 1][edge] until the mix MFMAs have read them (LDS keeps one wave's
+  // reads and writes in order)
   __shared__ double Yt[LW * YP];
-  __shared__ double Gt[8 * YP];
-  __shared__ __attribute__((aligned(16))) In Ht[C * HP];
+  double* const Gt = Yt;
+  __shared__ __attribute__((aligned(16))) In Ht[C * HP];    // feature rows [c][perm(edge)]
+  __shared__ double coef[kCoef];
 
   const int lane = threadIdx.x;
   const int kq = lane >> 4, cc = lane & 15;
   // edge 16 t + 4 v + k of a chunk sits at column 16 t + 4 k + v of Ht, so
   // lane (k = kq, c = cc) reads its four feature values of tile t as one word
   const int hcol = (lane & ~15) | ((lane & 3) << 2) | ((lane >> 2) & 3);
-  // wave-uniform atom range (kept in scalar registers)
   const int64_t a_begin = uniform64(int64_t(blockIdx.x) * p.N / p.waves);
   const int64_t a_end = uniform64((int64_t(blockIdx.x) + 1) * p.N / p.waves);
   if (a_begin >= a_end) return;
-  // stale tile entries must stay finite (they meet zero weights)
   for (int q = lane; q < LW * YP; q += 64) Yt[q] = 0.0;
-  for (int q = lane; q < 8 * YP; q += 64) Gt[q] = 0.0;
   for (int q = lane; q < C * HP; q += 64) Ht[q] = In(0);
-  // B operands of the mix: mix^T[n = 1 + 4 s + kq][c = cc]; g_0 = 1 adds mix[c][0]
+  if (lane < 11) coef[lane] = kSinPi[lane];
+  if (lane < 13) coef[11 + lane] = kExpm1[lane];
   const double mix0 = double(p.mix[cc * NR]);
   const double mixB0 = double(p.mix[cc * NR + 1 + kq]);
   const double mixB1 = double(p.mix[cc * NR + 5 + kq]);
   __syncthreads();
   const int64_t e_begin = offset_at(p.offsets, a_begin), e_end = offset_at(p.offsets, a_end);
   const int span = int(e_end - e_begin);  // edges of this wave (< 2^31, checked by the host)
-
-  // one accumulator: a dependent fp64 MFMA issues as soon as the matrix core
-  // is free (its latency equals its issue interval)
-  mfma_d4 acc = mfma_d4{0.0, 0.0, 0.0, 0.0};
-  // current atom a_begin + a and its edges [lo, hi), all wave-relative (32-bit
-  // scalar compares; the host keeps the edge count below 2^31)
   const int na = int(a_end - a_begin);
-  int a = 0;
-  int lo = 0, hi = int(offset_at(p.offsets, a_begin + 1) - e_begin);
+
+  // end offsets (wave-relative) of atoms wb + lane, clamped to the wave's last
+  // atom: the low words of the CSR offsets suffice (the host keeps E < 2^31),
+  // and a one-word load leaves no dead half-register for a later write to wait on
+  const int* const off32 = reinterpret_cast<const int*>(p.offsets);
+  const int e_begin32 = int(e_begin);
+  auto window = [&](int wb) {
+    const int64_t i = a_begin + wb + 1 + lane;
+    return off32[2 * (i < a_end ? i : a_end)] - e_begin32;
+  };
+  int wb = 0;
+  int offw = window(0);
+
+  mfma_d4 acc = mfma_d4{0.0, 0.0, 0.0, 0.0};
+  int a = 0, lo = 0;
+  int hi = int(offset_at(p.offsets, a_begin + 1) - e_begin);
   Out* __restrict__ Aw = p.A + a_begin * (C * LW) + lane;
   auto store_atom = [&](int atom) {
     Out* __restrict__ dst = Aw + int64_t(atom) * (C * LW);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) dst[64 * v] = Out(acc[v]);  // row c = kq + 4 v, column lm = cc
+    for (int v = 0; v < 4; ++v) __builtin_nontemporal_store(Out(acc[v]), dst + 64 * v);  // row kq + 4v, column cc
   };
-  // next atom: its edge range, or an empty range past the wave's edges
   auto next_atom = [&]() {
     store_atom(a);
     acc = mfma_d4{0.0, 0.0, 0.0, 0.0};
     ++a;
     lo = hi;
-    hi = a < na ? int(offset_at(p.offsets, a_begin + a + 1) - e_begin) : 0x7fffffff;
+    if (a >= na) {
+      hi = 0x7fffffff;
+    } else if (a - wb < 64) {
+      hi = __builtin_amdgcn_readlane(offw, a - wb);
+    } else {
+      hi = int(offset_at(p.offsets, a_begin + a + 1) - e_begin);
+    }
   };
   auto clamp_edge = [&](int64_t e) { return e < e_end ? e : e_end - 1; };
 
-  // Software pipeline: on entry to chunk i the lane holds the vector and the
-  // feature row of its edge of chunk i and the neighbour index of its edge of
-  // chunk i + 1 (lanes past the last edge re-read that edge).
-  In vx = In(0), vy = In(0), vz = In(0);
-  In h[C];
+  // Software pipeline, two chunks per trip with two register sets: on entry
+  // to a chunk the lane holds the vector and the feature row of its edge of
+  // that chunk and the neighbour index of its edge of the next chunk.
+  In vxA = In(0), vyA = In(0), vzA = In(0), vxB = In(0), vyB = In(0), vzB = In(0);
+  in4 hA[4], hB[4];
 #pragma unroll
-  for (int c = 0; c < C; ++c) h[c] = In(0);
-  int64_t nb1 = 0;
+  for (int t = 0; t < 4; ++t) hA[t] = hB[t] = in4{In(0), In(0), In(0), In(0)};
+  int64_t nb = 0;
   if (span > 0) {
     const int64_t e = clamp_edge(e_begin + lane);
-    vx = p.vec[3 * e];
-    vy = p.vec[3 * e + 1];
-    vz = p.vec[3 * e + 2];
-    const int64_t nb = p.nbr[e];
+    vxA = __builtin_nontemporal_load(p.vec + 3 * e);
+    vyA = __builtin_nontemporal_load(p.vec + 3 * e + 1);
+    vzA = __builtin_nontemporal_load(p.vec + 3 * e + 2);
+    const in4* row = reinterpret_cast<const in4*>(p.feats + __builtin_nontemporal_load(p.nbr + e) * C);
 #pragma unroll
-    for (int c = 0; c < C; ++c) h[c] = p.feats[nb * C + c];
-    nb1 = p.nbr[clamp_edge(e_begin + 64 + lane)];
+    for (int t = 0; t < 4; ++t) hA[t] = row[t];
+    nb = __builtin_nontemporal_load(p.nbr + clamp_edge(e_begin + 64 + lane));
   }
 
-  for (int c0 = 0; c0 < span; c0 += 64) {
+  auto chunk = [&](const int c0, const In vx, const In vy, const In vz, const in4* h4, In& nvx, In& nvy, In& nvz,
+                   in4* nh4) {
     const int cnt = span - c0 < 64 ? span - c0 : 64;
     const int64_t t0 = e_begin + c0;
-    const int64_t nb2 = p.nbr[clamp_edge(t0 + 128 + lane)];
-    const int64_t e1 = clamp_edge(t0 + 64 + lane);
-    const In nvx = p.vec[3 * e1], nvy = p.vec[3 * e1 + 1], nvz = p.vec[3 * e1 + 2];
-    In nh[C];
+    // Everything issued before this point (this chunk's operands, loaded one
+    // chunk ago, and the previous chunk's stores) is complete by now: one wait
+    // here, before the next loads go out, spares the basis math below the
+    // waits for loads that are still in flight (the in-order counter cannot
+    // tell them apart once a variable number of stores sits in between).
+    wait_vmem_all();
+    // the next chunk's vector and feature row, the neighbour index one further,
+    // and the offsets window from the current atom on
+    {
+      const int64_t e1 = clamp_edge(t0 + 64 + lane);
+      nvx = __builtin_nontemporal_load(p.vec + 3 * e1);
+      nvy = __builtin_nontemporal_load(p.vec + 3 * e1 + 1);
+      nvz = __builtin_nontemporal_load(p.vec + 3 * e1 + 2);
+      const in4* row = reinterpret_cast<const in4*>(p.feats + nb * C);
 #pragma unroll
-    for (int c = 0; c < C; ++c) nh[c] = p.feats[nb1 * C + c];
+      for (int t = 0; t < 4; ++t) nh4[t] = row[t];
+      nb = __builtin_nontemporal_load(p.nbr + clamp_edge(t0 + 128 + lane));
+    }
+    const int wb_next = a;
+    const int offw_next = window(a);
 
-    // ---- phase 1 (every lane; padding lanes hold a copy of the last edge)
+    // ---- phase 1 (lane = edge): radial rows -> Gt and feature row -> Ht, then
+    // the mix MFMAs, then the harmonics over the radial rows
 #if YE3T_DENSITY_SETPRIO
     __builtin_amdgcn_s_setprio(0);
 #endif
+    const double x = double(vx), y = double(vy), z = double(vz);
+    double inv;
     {
-      const double x = double(vx), y = double(vy), z = double(vz);
-      const double r = sqrt(x * x + y * y + z * z);
-      const double sr = r > p.eps ? r : p.eps;
-      const double inv = 1.0 / sr;
-      real_sph_row<double, double>(x * inv, y * inv, z * inv, LMAX, nt, Yt + lane, YP);
-      const double s = r / p.cutoff;
-      const bool live = lane < cnt && !(s > 1.0);
-      const double sc = s > 1.0 ? 1.0 : s;
-      const double env = 1.0 + cospi(sc);
-      const double xc = 1.0 - 2.0 * expm1(-p.lambda * (sc - 1.0)) / p.den;
+      const double r2 = x * x + y * y + z * z;
+      const double r2c = r2 > 2.2250738585072014e-308 ? r2 : 2.2250738585072014e-308;
+      const double hr = 0.5 * r2c;
+      double rs = __builtin_amdgcn_rsq(r2c);
+      rs = rs * fma(-hr * rs, rs, 1.5);
+      rs = rs * fma(-hr * rs, rs, 1.5);
+      const double r = r2 * rs;  // sqrt(r2) within an ulp
+      inv = r >= p.eps ? rs : p.inv_eps;
+      bool over = r > p.cutoff;
+      // liveness exactly as the reference decides it (sqrt(r2) / cutoff > 1)
+      // for the rare distances within a few ulps of the cutoff
+      const bool tie = fabs(r - p.cutoff) <= p.cutoff_tie;
+      if (__ballot(tie) != 0) {
+        asm volatile("" ::: "memory");
+        if (tie) over = sqrt(r2) / p.cutoff > 1.0;
+      }
+      const bool live = lane < cnt && !over;
+      const double s = r * p.inv_cutoff;
+      const double sc = over ? 1.0 : (s < 1.0 ? s : 1.0);
+      const double env = 1.0 + cospi01(sc, coef);
+      const double xc = 1.0 - expm1_reduced(p.lambda * (1.0 - sc), coef) * p.two_over_den;
       Gt[lane] = 0.5 * env;
+      const double q = 0.25 * env, x2 = xc + xc;
       double tm = 1.0, tn = xc;
 #pragma unroll
       for (int n = 2; n < NR; ++n) {
-        const double t2 = 2.0 * xc * tn - tm;
-        Gt[(n - 1) * YP + lane] = 0.25 * (1.0 - t2) * env;
+        const double t2 = fma(x2, tn, -tm);
+        Gt[(n - 1) * YP + lane] = fma(-q, t2, q);
         tm = tn;
         tn = t2;
       }
 #pragma unroll
-      for (int c = 0; c < C; ++c) Ht[c * HP + hcol] = live ? h[c] : In(0);
-    }
-    // The next chunk's loads were issued before phase 1: wait for them here,
-    // before phase 2 issues stores (loads and stores share one in-order counter).
-    wait_vmem_all();
-    __syncthreads();  // one wave: orders the LDS tile writes before the operand reads
-
-    // ---- phase 2.  All operands of the chunk are read at once (columns past
-    // cnt hold finite stale values that are never used) and the four tiles'
-    // mix products are issued before the density MFMAs that consume them.
-#if YE3T_DENSITY_SETPRIO
-    __builtin_amdgcn_s_setprio(YE3T_DENSITY_SETPRIO);
-#endif
-    const int nkb = (cnt + 3) >> 2;
-    double yv[16];
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) yv[j] = Yt[cc * YP + 4 * j + kq];
+        for (int u = 0; u < 4; ++u) Ht[(4 * t + u) * HP + hcol] = live ? h4[t][u] : In(0);
+    }
+    __syncthreads();
+
+    // ---- radial mix on the matrix cores: lane l holds R[16 t + 4 v + l / 16][l % 16]
     mfma_d4 R[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -451,32 +593,74 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_channel_kernel(Density6
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       R[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(Gt[(4 + kq) * YP + 16 * t + cc], mixB1, R[t], 0, 0, 0);
-    in4 h4[4];
+    sph3<YP>(x * inv, y * inv, z * inv, Yt + lane);
+    __syncthreads();
+    // operands of the chunk's 16 k-blocks: B from Yt, A = W[c][e] = R[e][c] h[e][c]
+    double wv[16];
+    {
+      in4 hk[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) h4[t] = *reinterpret_cast<const in4*>(Ht + cc * HP + 16 * t + 4 * kq);
+      for (int t = 0; t < 4; ++t) hk[t] = *reinterpret_cast<const in4*>(Ht + cc * HP + 16 * t + 4 * kq);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if (j < nkb) {
-        const double w = R[j >> 2][j & 3] * double(h4[j >> 2][j & 3]);
-        const int ke = c0 + 4 * j + 4, er = ke - 4 + kq;
-        for (;;) {
-          // this lane's edge belongs to the current atom
-          const double wm = unsigned(er - lo) < unsigned(hi - lo) ? w : 0.0;
-          acc = __builtin_amdgcn_mfma_f64_16x16x4f64(wm, yv[j], acc, 0, 0, 0);
-          if (hi > ke) break;  // the atom continues in a later k-block
-          next_atom();
-          if (a >= na || lo >= ke) break;  // the next atom starts in a later k-block
+      for (int j = 0; j < 16; ++j) wv[j] = R[j >> 2][j & 3] * double(hk[j >> 2][j & 3]);
+    }
+
+    // ---- phase 2: one MFMA per k-block of four edges
+#if YE3T_DENSITY_SETPRIO
+    __builtin_amdgcn_s_setprio(YE3T_DENSITY_SETPRIO);
+#endif
+    // atoms without edges that end where this chunk starts
+    while (hi <= c0 && a < na) next_atom();
+    // fast form: a full chunk whose atom ends all fall on k-block boundaries,
+    // every atom inside it holding at least one k-block, all within the window
+    bool fast = false;
+    if (cnt == 64 && a - wb < 64 && __builtin_amdgcn_readlane(offw, 63) >= c0 + 64) {
+      const int d = a - wb;
+      const int prev = __shfl_up(offw, 1);
+      const int start = lane == d ? lo : prev;
+      const bool bad = lane >= d && offw > c0 && offw < c0 + 64 && ((offw & 3) != 0 || offw - start < 4);
+      fast = __ballot(bad) == 0;
+    }
+    // B operands are read from Yt one tile (four k-blocks) ahead of their MFMAs
+    double yq[2][4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) yq[0][v] = Yt[cc * YP + 4 * v + kq];
+    if (fast) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if ((j & 3) == 0 && j < 12) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) yq[((j >> 2) + 1) & 1][v] = Yt[cc * YP + 4 * (j + 4 + v) + kq];
+        }
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(wv[j], yq[(j >> 2) & 1][j & 3], acc, 0, 0, 0);
+        if (hi == c0 + 4 * j + 4) next_atom();
+      }
+    } else {
+      const int nkb = (cnt + 3) >> 2;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if (j < nkb) {
+          const int ke = c0 + 4 * j + 4, er = ke - 4 + kq;
+          const double yv = Yt[cc * YP + 4 * j + kq];
+          for (;;) {
+            const double wm = unsigned(er - lo) < unsigned(hi - lo) ? wv[j] : 0.0;
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(wm, yv, acc, 0, 0, 0);
+            if (hi > ke) break;  // the atom continues in a later k-block
+            next_atom();
+            if (a >= na || lo >= ke) break;  // the next atom starts in a later k-block
+          }
         }
       }
     }
     __syncthreads();  // operand reads done before the next chunk's tile writes
+    wb = wb_next;
+    offw = offw_next;
+  };
 
-    vx = nvx;
-    vy = nvy;
-    vz = nvz;
-#pragma unroll
-    for (int c = 0; c < C; ++c) h[c] = nh[c];
-    nb1 = nb2;
+  for (int c0 = 0; c0 < span; c0 += 128) {
+    chunk(c0, vxA, vyA, vzA, hA, vxB, vyB, vzB, hB);
+    if (c0 + 64 >= span) break;
+    chunk(c0 + 64, vxB, vyB, vzB, hB, vxA, vyA, vzA, hA);
   }
   // atoms after the last edge (no edges of their own) get zero rows
   for (; a < na; ++a) store_atom(a);
@@ -543,13 +727,15 @@ int launch64_channel(const ye3t_density_args* a, void* A, hipStream_t stream) {
   p.den = std::expm1(a->lambda);
   p.eps = a->epsilon;
   p.A = static_cast<Out*>(A);
-  const int64_t grid =
-      density_waves(p.N, reinterpret_cast<const void*>(&ace_density_mfma64_channel_kernel<In, Out>));
+  p.inv_cutoff = 1.0 / p.cutoff;
+  p.two_over_den = 2.0 / p.den;
+  p.inv_eps = 1.0 / p.eps;
+  p.cutoff_tie = 8.0 * (std::nextafter(p.cutoff, 2.0 * p.cutoff) - p.cutoff);
+  const int64_t grid = density_waves(p.N, reinterpret_cast<const void*>(&ace_density_channel16_kernel<In, Out>));
   p.waves = grid;
-  hipLaunchKernelGGL((ace_density_mfma64_channel_kernel<In, Out>), dim3(unsigned(grid)), dim3(64), 0, stream, p,
-                     norm_table());
-  set_density_kernel("ace_density_mfma64_channel_kernel");
-  return check_launch("ace_density_mfma64_channel_kernel");
+  hipLaunchKernelGGL((ace_density_channel16_kernel<In, Out>), dim3(unsigned(grid)), dim3(64), 0, stream, p);
+  set_density_kernel("ace_density_channel16_kernel");
+  return check_launch("ace_density_channel16_kernel");
 }
 
 
