@@ -65,7 +65,7 @@ struct ye3t_hip_product_plan {
   uint2* loads;        // (LDS byte offset, density column), each chunk padded to a multiple of 8
   int64_t* load_off;   // [chunks+1], in loads
   int use_stream;
-  uint32_t stream_layout[6];  // StreamLayout of the stream kernel (byte offsets in its LDS)
+  uint32_t stream_layout[7];  // StreamLayout of the stream kernel (byte offsets in its LDS)
   int64_t stream_lds;         // LDS bytes of the stream kernel
   int64_t stream_tiles;  // tiles per workgroup of the stream kernel (0: by size; YE3T_STREAM_TILES)
 };
@@ -209,6 +209,54 @@ __device__ inline void lds_add(unsigned char* base, uint32_t off, Real v) {
   __hip_atomic_fetch_add(reinterpret_cast<Real*>(base + off), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// One group of the term stream (kGroup == 8 records): two 64-byte record
+// blocks and one 32-byte flag block, each a single scalar load (a chunk's
+// records start at a multiple of 8 records, so every block is aligned).
+typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+typedef const __attribute__((address_space(4))) u32x16* StreamRec16;
+typedef const __attribute__((address_space(4))) u32x8* StreamFlag8;
+struct StreamGroup {
+  u32x16 lo, hi;
+  u32x8 f;
+};
+static_assert(kGroup == 8, "the wide scalar loads of a group assume 8 records");
+
+__device__ inline StreamGroup fetch_group(StreamRec16 rec16, StreamFlag8 flag8, int q) {
+  StreamGroup g;
+  g.lo = rec16[q / 4];
+  g.hi = rec16[q / 4 + 1];
+  g.f = flag8[q / 8];
+  return g;
+}
+
+// word k of record u of a group
+__device__ inline uint32_t group_word(const StreamGroup& g, int u, int k) {
+  return u < 4 ? g.lo[4 * u + k] : g.hi[4 * (u - 4) + k];
+}
+
+template <typename Real>
+__device__ inline Real group_coeff(const StreamGroup& g, int u) {
+  if constexpr (sizeof(Real) == 8) {
+    return __hiloint2double(int(group_word(g, u, 3)), int(group_word(g, u, 2)));
+  } else {
+    return __uint_as_float(group_word(g, u, 2));
+  }
+}
+
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt left at their maxima)
+__device__ inline void wait_lgkm_all() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Hardware dispatch places workgroup b on XCD b % 8.  Renumbered this way,
+// each XCD runs one contiguous range of logical blocks, in order: the chunks of
+// one sample group then run on one XCD, so their partial output cache lines
+// merge in one L2 and the density rows they share are read from it.
+__device__ inline int64_t xcd_contiguous(int64_t b, int64_t n) {
+  constexpr int64_t X = 8;
+  const int64_t q = n / X, r = n % X, x = b % X, i = b / X;
+  return x * q + (x < r ? x : r) + i;
+}
+
 struct StreamLayout {
   uint32_t ws_bytes;    // workspace: (slots + 2) * 64 * elem
   uint32_t rec_at;      // end of the LDS-resident part (records stay in global memory)
@@ -216,6 +264,7 @@ struct StreamLayout {
   uint32_t load_at;     // (dst offset, column) pairs
   uint32_t out_at;      // output slot byte offsets
   uint32_t one_off;     // workspace byte offset of the slot holding 1
+  uint32_t sink_off;    // workspace byte offset of the sink slot (padding loads, unflushed stores)
 };
 
 template <typename Real, typename Out, bool COLUMNS>
@@ -227,8 +276,9 @@ __global__ __launch_bounds__(kLanes) void product_stream_kernel(
     StreamLayout lay, int64_t tiles_per_group) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int lane = threadIdx.x;
-  const int64_t group = blockIdx.x / chunks;
-  const int64_t chunk = blockIdx.x - group * chunks;
+  const int64_t blk = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int64_t group = blk / chunks;
+  const int64_t chunk = blk - group * chunks;
   const int64_t tiles = (samples + kLanes - 1) / kLanes;
   const int64_t tile0 = group * tiles_per_group;
   const int64_t tile_end = tile0 + tiles_per_group < tiles ? tile0 + tiles_per_group : tiles;
@@ -244,9 +294,8 @@ __global__ __launch_bounds__(kLanes) void product_stream_kernel(
   const int nl = int(load_off[chunk + 1] - l0);
   const int64_t o0 = out_off[chunk];
   const int nf = int(out_off[chunk + 1] - o0);
-  typedef const __attribute__((address_space(4))) uint32_t* scalar_u32;
-  const scalar_u32 grec = (scalar_u32)(const void*)(recs + r0);
-  const scalar_u32 gflag = (scalar_u32)(const void*)(flags + r0);
+  const StreamRec16 grec16 = (StreamRec16)(const void*)(recs + r0);
+  const StreamFlag8 gflag8 = (StreamFlag8)(const void*)(flags + r0);
   // load entry i: (dst byte offset, element offset of its column: col * lda
   // column-major, col row-major) so a tile's load address is one add
   for (int i = lane; i < nl; i += kLanes) {
@@ -305,63 +354,64 @@ __global__ __launch_bounds__(kLanes) void product_stream_kernel(
     }
     if (tile + 1 < tile_end) fetch(tile + 1, pre);
 
-    // the term stream, kGroup records at a time; each group's records and flags
-    // are read (scalar loads) one group ahead
+    // the term stream, one group of 8 records at a time.  A group's records
+    // and flags are three wide scalar loads, issued right after the wait for
+    // the previous group's LDS operands (scalar and LDS reads share one
+    // counter, and scalar reads return out of order): they are in flight while
+    // that group computes, and no LDS wait has to wait for them.
     Real acc = Real(0), p = Real(1);
-    uint32_t fw_next[kGroup];
-    uint4 r_next[kGroup];
-    auto read_group = [&](int q) {
-#pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
-        fw_next[u] = gflag[q + u];
-        r_next[u] = make_uint4(grec[4 * (q + u)], grec[4 * (q + u) + 1], grec[4 * (q + u) + 2], grec[4 * (q + u) + 3]);
-      }
-    };
-    read_group(0);
-    for (int q = 0; q < nr; q += kGroup) {
-      uint32_t f[kGroup];
-      uint4 r[kGroup];
-#pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
-        f[u] = fw_next[u];
-        r[u] = r_next[u];
-      }
-      read_group(q + kGroup < nr ? q + kGroup : q);
-      // no record of a group reads a slot flushed earlier in the group: all its
-      // factors are read before any of its stores
+    StreamGroup ga = fetch_group(grec16, gflag8, 0), gb;
+    const int last = nr - kGroup;
+    auto run_group = [&](const StreamGroup& g, int qnext, StreamGroup& gn) {
       Real a[kGroup], b[kGroup];
 #pragma unroll
       for (int u = 0; u < kGroup; ++u) {
-        a[u] = lds_at<Real>(wsb, r[u].x);
-        b[u] = lds_at<Real>(wsb, r[u].y);
+        a[u] = lds_at<Real>(wsb, group_word(g, u, 0));
+        b[u] = lds_at<Real>(wsb, group_word(g, u, 1));
       }
+      wait_lgkm_all();
+      // branch-free records (one basic block per group, so the scalar loads
+      // above stay where they are): every record stores acc, to its
+      // destination when it flushes and to the sink slot otherwise, and a
+      // flush restarts acc by a multiply with 0
       uint32_t any = 0;
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) any |= f[u];
+      for (int u = 0; u < kGroup; ++u) any |= g.f[u];
+      // (the next group's loads are issued at the top of each branch: placed
+      // before the branch, the compiler sinks them below it)
       if ((any & (kChain | kChained)) == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        gn = fetch_group(grec16, gflag8, qnext);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < kGroup; ++u) {
-          acc = d_fma(record_coeff<Real>(r[u]), a[u] * b[u], acc);
-          if (f[u] & kFlush) {
-            lds_at<Real>(wsb, f[u] >> 16) = acc;
-            acc = Real(0);
-          }
+          const uint32_t fw = g.f[u];
+          acc = d_fma(group_coeff<Real>(g, u), a[u] * b[u], acc);
+          lds_at<Real>(wsb, (fw & kFlush) ? (fw >> 16) : lay.sink_off) = acc;
+          acc *= (fw & kFlush) ? Real(0) : Real(1);
         }
       } else {
+        // a kChain record (coefficient 0) sets p = a b, its kChained partner
+        // adds c (p a) b
+        __builtin_amdgcn_sched_barrier(0);
+        gn = fetch_group(grec16, gflag8, qnext);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < kGroup; ++u) {
-          if (f[u] & kChain) {
-            p = a[u] * b[u];
-            continue;
-          }
-          const Real t = (f[u] & kChained) ? (p * a[u]) * b[u] : a[u] * b[u];
-          acc = d_fma(record_coeff<Real>(r[u]), t, acc);
-          if (f[u] & kFlush) {
-            lds_at<Real>(wsb, f[u] >> 16) = acc;
-            acc = Real(0);
-          }
+          const uint32_t fw = g.f[u];
+          const Real ab = a[u] * b[u];
+          const Real t = (fw & kChained) ? (p * a[u]) * b[u] : ab;
+          acc = d_fma(group_coeff<Real>(g, u), t, acc);
+          p = (fw & kChain) ? ab : p;
+          lds_at<Real>(wsb, (fw & kFlush) ? (fw >> 16) : lay.sink_off) = acc;
+          acc *= (fw & kFlush) ? Real(0) : Real(1);
         }
       }
+    };
+    for (int q = 0; q < nr; q += 2 * kGroup) {
+      run_group(ga, q + kGroup < last ? q + kGroup : last, gb);
+      if (q + kGroup >= nr) break;
+      run_group(gb, q + 2 * kGroup < last ? q + 2 * kGroup : last, ga);
     }
     // transposed write-out of the chunk's [rows, nf] block: consecutive lanes
     // take consecutive columns of a row, so a store covers a few row segments
@@ -813,6 +863,7 @@ bool build_stream(const ye3t_product_plan_desc* d, std::vector<uint4>& recs, std
   lay.rec_at = uint32_t(at);
   lay.flag_at = uint32_t(at);
   lay.one_off = one;
+  lay.sink_off = sink;
   lds_bytes = at;
   (void)max_recs;
   return at <= 64 * 1024;
@@ -845,6 +896,7 @@ int launch_stream(const ye3t_hip_product_plan* p, const void* A, int64_t lda, in
   lay.load_at = p->stream_layout[3];
   lay.out_at = p->stream_layout[4];
   lay.one_off = p->stream_layout[5];
+  lay.sink_off = p->stream_layout[6];
   const hipStream_t s = as_stream(stream);
   if (p->dtype == YE3T_F64 && p->out_dtype == YE3T_F64) {
     hipLaunchKernelGGL((product_stream_kernel<double, double, COLUMNS>), dim3(unsigned(grid)), dim3(kLanes), lds, s,
@@ -896,6 +948,7 @@ int launch_stream_adjoint(const ye3t_hip_product_plan* p, const void* A, int64_t
   lay.load_at = p->stream_layout[3];
   lay.out_at = p->stream_layout[4];
   lay.one_off = p->stream_layout[5];
+  lay.sink_off = p->stream_layout[6];
   // values, gradients, loads and output slots (records and flags stay in global memory)
   const size_t lds = size_t(p->stream_layout[1]) + lay.ws_bytes;
   const int64_t grid = tiles * groups;
@@ -1252,7 +1305,8 @@ int ye3t_hip_product_plan_create(const ye3t_product_plan_desc* d, ye3t_hip_produ
       ye3t_hip_product_plan_destroy(p);
       return rc;
     }
-    const uint32_t fields[6] = {lay.ws_bytes, lay.rec_at, lay.flag_at, lay.load_at, lay.out_at, lay.one_off};
+    const uint32_t fields[7] = {lay.ws_bytes, lay.rec_at,  lay.flag_at, lay.load_at,
+                                lay.out_at,   lay.one_off, lay.sink_off};
     std::memcpy(p->stream_layout, fields, sizeof(fields));
     p->stream_lds = stream_lds;
     p->use_stream = 1;
