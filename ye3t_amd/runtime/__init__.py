@@ -325,6 +325,10 @@ def __getattr__(name):
         import importlib
 
         return getattr(importlib.import_module("ye3t_amd.runtime.dag"), name)
+    if name in ("ExecutionPlan", "YE3TExecutionPlan"):
+        from ye3t_amd.runtime.execution_plan import ExecutionPlan
+
+        return ExecutionPlan
     raise AttributeError(name)
 
 

@@ -11,8 +11,8 @@ returns for the reference's own Torch restatement.
 (``ye3t/runtime/execution_plan.py:13550-13903``): it owns the DAG tables as
 buffers, packs per-slot inputs the same way and offers ``forward``,
 ``linear_readout`` and ``runtime_report``.  It is built from explicit DAG
-tables (``from_tables``) or from a reference execution-plan document
-(:meth:`YE3TFactorizedAngularModule.from_execution_plan`).
+tables (``from_tables``) or, as the reference's constructor takes it, from an
+execution-plan document (``ye3t_amd.runtime.execution_plan.ExecutionPlan``).
 """
 
 import hashlib
@@ -159,14 +159,23 @@ class YE3TFactorizedAngularModule(torch.nn.Module):
     """Prepared factorized-angular DAG runtime (reference
     ``execution_plan.py:13550-13903``).
 
-    Build it with :meth:`from_tables` (explicit DAG tables) or
-    :meth:`from_execution_plan` (a reference execution-plan document).
-    ``forward(slot_values)`` returns ``[..., roots * P, 2 L + 1]``;
-    ``linear_readout(slot_values, weight, bias)`` the fused readout.
+    ``YE3TFactorizedAngularModule(execution_plan, factorized_angular_plan_id=None,
+    backend="auto", dtype=None, device=None)`` takes the reference constructor's
+    arguments: an execution-plan document (an :class:`ExecutionPlan` or its
+    ``to_dict()`` payload) and the id of one of its factorized-angular plans
+    (optional when the document holds exactly one).  ``dtype`` defaults to
+    complex128 when any synthesis coefficient has an imaginary part, else
+    float64, as in the reference.  :meth:`from_tables` builds one from explicit
+    DAG tables.  ``forward(slot_values)`` returns
+    ``[..., roots * P, 2 L + 1]``; ``linear_readout(slot_values, weight, bias)``
+    the fused readout ``features @ weight + bias``.  The module runs the HIP
+    branch only: ``device`` defaults to the current CUDA device and a CPU device
+    is refused.
     """
 
-    def __init__(self, tables, *, input_Ls, source_dimension, output_L, backend="auto", dtype=None, device=None,
-                 plan_hash=None, plan_id=None):
+    def __init__(self, execution_plan=None, factorized_angular_plan_id=None, backend="auto", dtype=None,
+                 device=None, *, tables=None, input_Ls=None, source_dimension=None, output_L=None, plan_hash=None,
+                 plan_id=None):
         torch = _torch()
         super().__init__()
         backend = str(backend)
@@ -175,6 +184,26 @@ class YE3TFactorizedAngularModule(torch.nn.Module):
                                       "(ye3t.runtime); ye3t_amd runs the native HIP branch only")
         if backend not in {"auto", "native"}:
             raise ValueError("backend must be 'auto', 'native', or 'reference'")
+        dense_elements = None
+        identity = {}
+        if execution_plan is not None:
+            if tables is not None:
+                raise ValueError("give an execution plan or explicit tables, not both")
+            from ye3t_amd.runtime import execution_plan as ep
+
+            plan = execution_plan if isinstance(execution_plan, ep.ExecutionPlan) else \
+                ep.ExecutionPlan.from_dict(execution_plan)
+            _, meta = plan.factorized_angular_buffers(factorized_angular_plan_id)
+            if dtype is None:
+                dtype = torch.complex128 if meta["coefficient_complex"] else torch.float64
+            tables, meta = plan.factorized_angular_buffers(factorized_angular_plan_id,
+                                                           complex_values=dtype.is_complex)
+            input_Ls, source_dimension, output_L = meta["input_Ls"], meta["source_dimension"], meta["output_L"]
+            plan_hash, plan_id = plan.plan_hash, meta["plan_id"]
+            dense_elements = meta["reference_dense_synthesis_element_count"]
+            identity = {k: meta[k] for k in ("node_operator_hashes", "node_subtree_hashes")}
+        elif tables is None:
+            raise ValueError("YE3TFactorizedAngularModule needs an execution plan or explicit tables")
         values = np.asarray(tables["coefficient_values"])
         proj = np.asarray(tables["projection_values"])
         if dtype is None:
@@ -183,6 +212,9 @@ class YE3TFactorizedAngularModule(torch.nn.Module):
         device = torch.device("cuda" if device is None else device)
         if device.type != "cuda":
             raise NotImplementedError("YE3TFactorizedAngularModule: ye3t_amd implements the HIP device branch")
+        if not dtype.is_complex:  # a real dtype keeps the real parts (reference execution_plan.py:11392-11397)
+            tables = {k: (np.asarray(v).real if k in ("coefficient_values", "projection_values") else v)
+                      for k, v in tables.items()}
         for name in native.FA_TABLE_NAMES:
             v = np.asarray(tables[name])
             t = torch.as_tensor(v, dtype=dtype if name in ("coefficient_values", "projection_values") else torch.int64,
@@ -198,6 +230,9 @@ class YE3TFactorizedAngularModule(torch.nn.Module):
         P = int(proj.size) // self.source_dimension
         self.logical_channel_tableau_dimension = int(np.asarray(tables["root_nodes"]).size) * P
         self.output_dimension = self.logical_channel_tableau_dimension * self.magnetic_dimension
+        self.reference_dense_synthesis_element_count = None if dense_elements is None else int(dense_elements)
+        self.node_operator_hashes = tuple(identity.get("node_operator_hashes", ()))
+        self.node_subtree_hashes = tuple(identity.get("node_subtree_hashes", ()))
         self.plan_hash = None if plan_hash is None else str(plan_hash)
         self.factorized_angular_plan_id = None if plan_id is None else str(plan_id)
         self.requested_backend = backend
@@ -209,22 +244,13 @@ class YE3TFactorizedAngularModule(torch.nn.Module):
 
     @classmethod
     def from_tables(cls, tables, *, input_Ls, source_dimension, output_L, **kw):
-        return cls(tables, input_Ls=input_Ls, source_dimension=source_dimension, output_L=output_L, **kw)
+        return cls(tables=tables, input_Ls=input_Ls, source_dimension=source_dimension, output_L=output_L, **kw)
 
     @classmethod
     def from_execution_plan(cls, execution_plan, factorized_angular_plan_id=None, backend="auto", dtype=None,
                             device=None):
-        """The reference constructor's form: a reference execution-plan
-        document (``YE3TExecutionPlan.to_dict()`` JSON) and the id of one of
-        its factorized-angular plans."""
-        from ye3t_amd.runtime import execution_plan as ep
-
-        plan = execution_plan if isinstance(execution_plan, ep.ExecutionPlan) else \
-            ep.ExecutionPlan.from_dict(execution_plan)
-        tables, meta = plan.factorized_angular_buffers(factorized_angular_plan_id)
-        return cls(tables, input_Ls=meta["input_Ls"], source_dimension=meta["source_dimension"],
-                   output_L=meta["output_L"], backend=backend, dtype=dtype, device=device,
-                   plan_hash=plan.plan_hash, plan_id=meta["plan_id"])
+        """Same as the constructor's reference form."""
+        return cls(execution_plan, factorized_angular_plan_id, backend=backend, dtype=dtype, device=device)
 
     def _packed_slots(self, slot_values):
         """Reference ``_packed_slots`` (``execution_plan.py:13688-13734``)."""
@@ -285,6 +311,11 @@ class YE3TFactorizedAngularModule(torch.nn.Module):
             "input_Ls": tuple(self.input_Ls), "source_dimension": int(self.source_dimension),
             "workspace_dimension": int(self.workspace_dimension), "runtime_device_scalar_metadata_reads": 0,
             "root_path_count": int(self.root_nodes.numel()), "unique_node_count": int(self.node_offsets.numel()),
+            "reference_dense_synthesis_materialized": False,
+            "reference_dense_synthesis_element_count": self.reference_dense_synthesis_element_count,
+            "reference_dense_synthesis_bytes": 0,
+            "per_forward_synthesis_table_reconstruction": False,
             "last_linear_readout_backend": self.last_linear_readout_backend,
+            "linear_readout_auto_policy": "fuse",
             "analysis_orientation": self.analysis_orientation,
         }
