@@ -452,6 +452,94 @@ int ye3t_hip_factorized_angular_linear_adjoint(const ye3t_hip_factorized_angular
                                                const void* weight, void* features, void* packed_slots_adjoint,
                                                void* weight_adjoint, void* bias_adjoint, ye3t_stream_t stream);
 
+/* ---- Segmented factorized-angular DAGs (several plans in one launch) ---- */
+
+/* Host tables of the reference op factorized_angular_segmented(packed_slots,
+ * segment_source_offsets, segment_input_offsets, segment_input_dimensions,
+ * segment_workspace_offsets, segment_workspace_dimensions, segment_node_offsets,
+ * segment_root_offsets, segment_projection_offsets, segment_projection_dimensions,
+ * segment_output_offsets, node_offsets, node_dimensions, node_leaf_offsets,
+ * node_left, node_right, node_coefficient_offsets, coefficient_rows,
+ * coefficient_columns, coefficient_values, root_nodes, root_projection_starts,
+ * root_projection_dimensions, root_output_offsets, projection_values,
+ * total_source_count, workspace_dimension, output_dimension)
+ * (schema execution_plan_torch.cpp:7666-7679), with the counts of its vectors
+ * and packed_input_dimension = packed_slots.size(1).  Segment k is one DAG over
+ * packed columns [segment_input_offsets[k], + S_k * segment_input_dimensions[k])
+ * and output columns [segment_output_offsets[k], segment_output_offsets[k + 1]);
+ * its node and root indices are local to its slices, node_coefficient_offsets
+ * index the concatenated coefficients, and root r projects onto columns
+ * [root_projection_starts[r], + root_projection_dimensions[r]) of the segment's
+ * [S_k x segment_projection_dimensions[k]] projection block into output block
+ * root_output_offsets[r] of the segment. */
+typedef struct {
+  int dtype; /* YE3T_F32, YE3T_F64, YE3T_C64 or YE3T_C128 */
+  int64_t segment_count;
+  const int64_t* segment_source_offsets;        /* [segment_count + 1] */
+  const int64_t* segment_input_offsets;         /* [segment_count] */
+  const int64_t* segment_input_dimensions;      /* [segment_count] */
+  const int64_t* segment_workspace_offsets;     /* [segment_count] */
+  const int64_t* segment_workspace_dimensions;  /* [segment_count] */
+  const int64_t* segment_node_offsets;          /* [segment_count + 1] */
+  const int64_t* segment_root_offsets;          /* [segment_count + 1] */
+  const int64_t* segment_projection_offsets;    /* [segment_count] */
+  const int64_t* segment_projection_dimensions; /* [segment_count] */
+  const int64_t* segment_output_offsets;        /* [segment_count + 1] */
+  int64_t node_count;
+  const int64_t* node_offsets;
+  const int64_t* node_dimensions;
+  const int64_t* node_leaf_offsets;
+  const int64_t* node_left;
+  const int64_t* node_right;
+  const int64_t* node_coefficient_offsets; /* [node_count + 1] */
+  int64_t coefficient_count;
+  const int64_t* coefficient_rows;
+  const int64_t* coefficient_columns;
+  const void* coefficient_values; /* [coefficient_count] of dtype */
+  int64_t root_count;
+  const int64_t* root_nodes;
+  const int64_t* root_projection_starts;
+  const int64_t* root_projection_dimensions;
+  const int64_t* root_output_offsets;
+  int64_t projection_count;
+  const void* projection_values; /* [projection_count] of dtype */
+  int64_t packed_input_dimension;
+  int64_t total_source_count;
+  int64_t workspace_dimension;
+  int64_t output_dimension;
+} ye3t_factorized_angular_segmented_desc;
+
+typedef struct ye3t_hip_factorized_angular_segmented_plan ye3t_hip_factorized_angular_segmented_plan;
+
+/* Validates the tables on the host (the reference op's checks,
+ * execution_plan_torch.cpp:434-726, plus every index the kernels use) and
+ * copies them to the current device (synchronous).  Counterpart of the
+ * reference's segmented group buffers (execution_plan.py:16632-16890). */
+int ye3t_hip_factorized_angular_segmented_plan_create(const ye3t_factorized_angular_segmented_desc* desc,
+                                                      ye3t_hip_factorized_angular_segmented_plan** out);
+void ye3t_hip_factorized_angular_segmented_plan_destroy(ye3t_hip_factorized_angular_segmented_plan* plan);
+
+/* info[6] = (dtype, segment_count, total_source_count, packed_input_dimension,
+ * workspace_dimension, output_dimension). */
+int ye3t_hip_factorized_angular_segmented_plan_info(const ye3t_hip_factorized_angular_segmented_plan* plan,
+                                                    int64_t* info);
+
+/* output[batch, output_dimension] from packed_slots[batch, packed_input_dimension],
+ * every segment in one launch (blocks of 64 samples by segment).  Replaces the
+ * CUDA branch of ye3t_runtime::factorized_angular_segmented
+ * (execution_plan_cuda.cu:13099; CPU core ye3t_runtime_core.cpp:6977-7021). */
+int ye3t_hip_factorized_angular_segmented_forward(const ye3t_hip_factorized_angular_segmented_plan* plan,
+                                                  const void* packed_slots, int64_t batch, void* output,
+                                                  ye3t_stream_t stream);
+
+/* packed_slots_adjoint[batch, packed_input_dimension] of an output adjoint
+ * (conjugate-transpose convention, forward values recomputed).  Replaces
+ * ye3t_runtime::factorized_angular_segmented_adjoint (schema
+ * execution_plan_torch.cpp:7681-7695; CPU core ye3t_runtime_core.cpp:7023-7070). */
+int ye3t_hip_factorized_angular_segmented_adjoint(const ye3t_hip_factorized_angular_segmented_plan* plan,
+                                                  const void* output_adjoint, const void* packed_slots, int64_t batch,
+                                                  void* packed_slots_adjoint, ye3t_stream_t stream);
+
 /* Device workspace bytes of ye3t_hip_product_adjoint_stream for `samples`
  * samples (0 for plans without a term stream; -1 on invalid input). */
 int64_t ye3t_hip_product_adjoint_workspace_bytes(const ye3t_hip_product_plan* plan, int64_t samples);

@@ -409,6 +409,73 @@ def factorized_angular_linear_adjoint(output_adjoint, packed_slots, tables, sour
     return gx, gw, gb[0]
 
 
+# segmented tables, in the reference op's argument order (execution_plan_torch.cpp:7666-7679)
+FA_SEGMENT_KEYS = ("segment_source_offsets", "segment_input_offsets", "segment_input_dimensions",
+                   "segment_workspace_offsets", "segment_workspace_dimensions", "segment_node_offsets",
+                   "segment_root_offsets", "segment_projection_offsets", "segment_projection_dimensions",
+                   "segment_output_offsets", "node_offsets", "node_dimensions", "node_leaf_offsets", "node_left",
+                   "node_right", "node_coefficient_offsets", "coefficient_rows", "coefficient_columns",
+                   "coefficient_values", "root_nodes", "root_projection_starts", "root_projection_dimensions",
+                   "root_output_offsets", "projection_values")
+
+
+def _fa_seg_args(seg, cplx, packed_dim, out_dim, batch):
+    keep = {k: _i64a(seg[k]) for k in FA_SEGMENT_KEYS if k not in ("coefficient_values", "projection_values")}
+    dt = np.complex128 if cplx else np.float64
+    keep["coefficient_values"] = np.ascontiguousarray(seg["coefficient_values"], dtype=dt)
+    keep["projection_values"] = np.ascontiguousarray(seg["projection_values"], dtype=dt)
+    I = ctypes.c_int64
+    nseg = int(keep["segment_input_offsets"].size)
+    args = [I(batch), I(packed_dim), I(nseg)] + [_vp(keep[k]) for k in (
+        "segment_source_offsets", "segment_input_offsets", "segment_input_dimensions", "segment_node_offsets",
+        "segment_root_offsets", "segment_projection_offsets", "segment_projection_dimensions",
+        "segment_output_offsets")] + [I(out_dim)] + [_vp(keep[k]) for k in (
+            "node_offsets", "node_dimensions", "node_leaf_offsets", "node_left", "node_right",
+            "node_coefficient_offsets", "coefficient_rows", "coefficient_columns", "coefficient_values",
+            "root_nodes", "root_projection_starts", "root_projection_dimensions", "root_output_offsets",
+            "projection_values")]
+    W = int(max(np.asarray(seg["segment_workspace_dimensions"]).max(), 1))
+    return keep, args, W
+
+
+def _seg_complex(seg, *arrays):
+    return any(np.iscomplexobj(a) for a in arrays) or np.iscomplexobj(seg["coefficient_values"]) or \
+        np.iscomplexobj(seg["projection_values"])
+
+
+def factorized_angular_segmented(packed_slots, seg, output_dimension, *, use_reference=False):
+    """``factorized_angular_segmented_forward`` (ye3t_runtime_core.cpp:6977-7021):
+    ``seg`` holds the op's segment, node, coefficient, root and projection
+    tables (:data:`FA_SEGMENT_KEYS`); returns ``[batch, output_dimension]``."""
+    cplx = _seg_complex(seg, packed_slots)
+    dt = np.complex128 if cplx else np.float64
+    x = np.ascontiguousarray(packed_slots, dtype=dt)
+    B, D = x.shape
+    out = np.zeros((B, int(output_dimension)), dtype=dt)
+    keep, args, W = _fa_seg_args(seg, cplx, D, int(output_dimension), B)
+    ws = np.zeros(W, dtype=dt)
+    args = [_vp(x)] + args + ([] if use_reference else [_vp(ws)]) + [_vp(out)]
+    _fa_fn("factorized_angular_segmented", cplx, use_reference)(*args)
+    return out
+
+
+def factorized_angular_segmented_adjoint(output_adjoint, packed_slots, seg, *, use_reference=False):
+    """``factorized_angular_segmented_adjoint`` (ye3t_runtime_core.cpp:7023-7070):
+    the packed-slot gradient ``[batch, packed width]``."""
+    cplx = _seg_complex(seg, packed_slots, output_adjoint)
+    dt = np.complex128 if cplx else np.float64
+    x = np.ascontiguousarray(packed_slots, dtype=dt)
+    g = np.ascontiguousarray(output_adjoint, dtype=dt)
+    B, D = x.shape
+    gx = np.zeros((B, D), dtype=dt)
+    keep, args, W = _fa_seg_args(seg, cplx, D, int(g.shape[1]), B)
+    ws = np.zeros(W, dtype=dt)
+    wa = np.zeros(W, dtype=dt)
+    args = [_vp(g), _vp(x)] + args + ([] if use_reference else [_vp(ws), _vp(wa)]) + [_vp(gx)]
+    _fa_fn("factorized_angular_segmented_adjoint", cplx, use_reference)(*args)
+    return gx
+
+
 # ---- symmetric-power monomial adjoint and shared monomials -------------------
 
 def symmetric_power_monomial_adjoint(output_adjoint, inp, monomial_counts, output_indices, monomial_values,

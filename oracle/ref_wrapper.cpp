@@ -122,4 +122,59 @@ void ref_symmetric_power_shared_monomial_adjoint(const double* gout, const doubl
 YE3T_REF_FA(f64, double)
 YE3T_REF_FA(c128, std::complex<double>)
 #undef YE3T_REF_FA
+
+// segmented DAGs (factorized_angular_segmented_forward / _adjoint), with the
+// argument order of the oracle's restatement (minus its scratch buffers)
+#define YE3T_REF_FA_SEG_ARGS(T)                                                                                   \
+  int64_t batch, int64_t packed_dim, int64_t seg_count, const int64_t *seg_src_off, const int64_t *seg_in_off,   \
+      const int64_t *seg_in_dim, const int64_t *seg_node_off, const int64_t *seg_root_off,                       \
+      const int64_t *seg_proj_off, const int64_t *seg_proj_dim, const int64_t *seg_out_off, int64_t out_dim,     \
+      const int64_t *noff, const int64_t *ndim, const int64_t *nleaf, const int64_t *nl, const int64_t *nr,      \
+      const int64_t *ncoef, const int64_t *rows, const int64_t *cols, const T *coef, const int64_t *roots,       \
+      const int64_t *rps, const int64_t *rpd, const int64_t *roo, const T *proj
+#define YE3T_REF_FA_SEG_VIEW(T)                                                                                   \
+  ye3t::runtime::FactorizedAngularSegmentedPlanView<T> v;                                                        \
+  v.segment_source_offsets = seg_src_off;                                                                        \
+  v.segment_input_offsets = seg_in_off;                                                                          \
+  v.segment_input_dimensions = seg_in_dim;                                                                       \
+  v.segment_workspace_offsets = nullptr;                                                                         \
+  v.segment_workspace_dimensions = nullptr;                                                                      \
+  v.segment_node_offsets = seg_node_off;                                                                         \
+  v.segment_root_offsets = seg_root_off;                                                                         \
+  v.segment_projection_offsets = seg_proj_off;                                                                   \
+  v.segment_projection_dimensions = seg_proj_dim;                                                                \
+  v.segment_output_offsets = seg_out_off;                                                                        \
+  v.node_offsets = noff;                                                                                         \
+  v.node_dimensions = ndim;                                                                                      \
+  v.node_leaf_offsets = nleaf;                                                                                   \
+  v.node_left = nl;                                                                                              \
+  v.node_right = nr;                                                                                             \
+  v.node_coefficient_offsets = ncoef;                                                                            \
+  v.coefficient_rows = rows;                                                                                     \
+  v.coefficient_columns = cols;                                                                                  \
+  v.coefficient_values = coef;                                                                                   \
+  v.root_nodes = roots;                                                                                          \
+  v.root_projection_starts = rps;                                                                                \
+  v.root_projection_dimensions = rpd;                                                                            \
+  v.root_output_offsets = roo;                                                                                   \
+  v.projection_values = proj;                                                                                    \
+  v.segment_count = seg_count;                                                                                   \
+  v.packed_input_dimension = packed_dim;                                                                         \
+  v.workspace_dimension = 0;                                                                                     \
+  v.output_dimension = out_dim;
+#define YE3T_REF_FA_SEG(SUFFIX, T)                                                                                \
+  void ref_factorized_angular_segmented_##SUFFIX(const T *packed, YE3T_REF_FA_SEG_ARGS(T), T *out) {             \
+    YE3T_REF_FA_SEG_VIEW(T)                                                                                      \
+    ye3t::runtime::factorized_angular_segmented_forward<T>(packed, batch, v, out);                               \
+  }                                                                                                              \
+  void ref_factorized_angular_segmented_adjoint_##SUFFIX(const T *gout, const T *packed, YE3T_REF_FA_SEG_ARGS(T), \
+                                                         T *gpacked) {                                           \
+    YE3T_REF_FA_SEG_VIEW(T)                                                                                      \
+    ye3t::runtime::factorized_angular_segmented_adjoint<T>(gout, packed, batch, v, gpacked);                     \
+  }
+YE3T_REF_FA_SEG(f64, double)
+YE3T_REF_FA_SEG(c128, std::complex<double>)
+#undef YE3T_REF_FA_SEG
+#undef YE3T_REF_FA_SEG_VIEW
+#undef YE3T_REF_FA_SEG_ARGS
 }

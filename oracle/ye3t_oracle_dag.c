@@ -234,6 +234,109 @@ FA_LINEAR(oracle_factorized_angular_linear_c128, double complex, conj_c)
 FA_LINEAR_ADJOINT(oracle_factorized_angular_linear_adjoint_f64, double, conj_r)
 FA_LINEAR_ADJOINT(oracle_factorized_angular_linear_adjoint_c128, double complex, conj_c)
 
+/* ---- segmented DAGs -------------------------------------------------------
+ * factorized_angular_segmented_forward / _adjoint (ye3t_runtime_core.cpp:
+ * 6977-7100): per sample, per segment, the general single-DAG forward (or
+ * adjoint) with explicit root metadata (root r of a segment projects onto
+ * projection columns [start, start + dim) of that segment's [S x P] block and
+ * writes at segment output offset + root_output_offsets[r]).  Node, root and
+ * root-metadata arrays are segment-local slices; node_coefficient_offsets
+ * index the concatenated coefficient arrays. */
+
+#define FA_SEG_ARGS(T)                                                                                        \
+  int64_t batch, int64_t packed_dim, int64_t seg_count, const int64_t* seg_src_off, const int64_t* seg_in_off,  \
+      const int64_t* seg_in_dim, const int64_t* seg_node_off, const int64_t* seg_root_off,                      \
+      const int64_t* seg_proj_off, const int64_t* seg_proj_dim, const int64_t* seg_out_off, int64_t out_dim,    \
+      const int64_t* all_node_offsets, const int64_t* all_node_dims, const int64_t* all_node_leaf,              \
+      const int64_t* all_node_left, const int64_t* all_node_right, const int64_t* all_node_coef_off,            \
+      const int64_t* rows, const int64_t* cols, const T* coef, const int64_t* all_roots,                        \
+      const int64_t* all_root_ps, const int64_t* all_root_pd, const int64_t* all_root_oo, const T* all_proj
+
+/* segment k's slices under the names FA_REPLAY / FA_SWEEP use */
+#define FA_SEG_BIND                                                                                           \
+  const int64_t n0 = seg_node_off[k], r0 = seg_root_off[k];                                                  \
+  const int64_t source_dim = seg_src_off[k + 1] - seg_src_off[k], input_dim = seg_in_dim[k];                  \
+  const int64_t node_count = seg_node_off[k + 1] - n0, root_count = seg_root_off[k + 1] - r0;               \
+  const int64_t *node_offsets = all_node_offsets + n0, *node_dims = all_node_dims + n0;                       \
+  const int64_t *node_leaf = all_node_leaf + n0, *node_left = all_node_left + n0;                             \
+  const int64_t *node_right = all_node_right + n0, *node_coef_off = all_node_coef_off + n0;                   \
+  const int64_t *roots = all_roots + r0, *root_ps = all_root_ps + r0, *root_pd = all_root_pd + r0;            \
+  const int64_t* root_oo = all_root_oo + r0;                                                                  \
+  const int64_t proj_dim = seg_proj_dim[k], seg_out = seg_out_off[k + 1] - seg_out_off[k];                    \
+  const int64_t W = node_offsets[node_count - 1] + node_dims[node_count - 1];                                 \
+  (void)W;
+
+#define FA_SEG_FORWARD(NAME, T, CONJ)                                                                        \
+  void NAME(const T* packed, FA_SEG_ARGS(T), T* ws, T* out) {                                                 \
+    for (int64_t b = 0; b < batch; ++b) {                                                                     \
+      for (int64_t k = 0; k < seg_count; ++k) {                                                               \
+        FA_SEG_BIND                                                                                           \
+        const T* proj = all_proj + seg_proj_off[k];                                                           \
+        T* orow = out + b * out_dim + seg_out_off[k];                                                         \
+        for (int64_t q = 0; q < seg_out; ++q) orow[q] = 0;                                                    \
+        for (int64_t s = 0; s < source_dim; ++s) {                                                            \
+          for (int64_t q = 0; q < W; ++q) ws[q] = 0;                                                          \
+          const T* in = packed + b * packed_dim + seg_in_off[k] + s * input_dim;                              \
+          for (int64_t n = 0; n < node_count; ++n) {                                                          \
+            T* o = ws + node_offsets[n];                                                                      \
+            if (node_leaf[n] >= 0) {                                                                          \
+              for (int64_t i = 0; i < node_dims[n]; ++i) o[i] = in[node_leaf[n] + i];                         \
+              continue;                                                                                       \
+            }                                                                                                 \
+            const T* l = ws + node_offsets[node_left[n]];                                                     \
+            const T* r = ws + node_offsets[node_right[n]];                                                    \
+            const int64_t rd = node_dims[node_right[n]];                                                      \
+            for (int64_t e = node_coef_off[n]; e < node_coef_off[n + 1]; ++e)                                 \
+              o[cols[e]] += CONJ(coef[e]) * l[rows[e] / rd] * r[rows[e] % rd];                                \
+          }                                                                                                   \
+          for (int64_t ri = 0; ri < root_count; ++ri) {                                                       \
+            const int64_t rn = roots[ri], rdim = node_dims[rn];                                               \
+            const T* rv = ws + node_offsets[rn];                                                              \
+            for (int64_t p = 0; p < root_pd[ri]; ++p) {                                                       \
+              T* blk = orow + root_oo[ri] + p * rdim;                                                         \
+              const T pv = proj[s * proj_dim + root_ps[ri] + p];                                              \
+              for (int64_t m = 0; m < rdim; ++m) blk[m] += rv[m] * pv;                                        \
+            }                                                                                                 \
+          }                                                                                                   \
+        }                                                                                                     \
+      }                                                                                                       \
+    }                                                                                                         \
+  }
+
+FA_SEG_FORWARD(oracle_factorized_angular_segmented_f64, double, conj_r)
+FA_SEG_FORWARD(oracle_factorized_angular_segmented_c128, double complex, conj_c)
+
+#define FA_SEG_ADJOINT(NAME, T, CONJ)                                                                        \
+  void NAME(const T* gout, const T* packed, FA_SEG_ARGS(T), T* ws, T* wa, T* gpacked) {                       \
+    for (int64_t b = 0; b < batch; ++b) {                                                                     \
+      for (int64_t k = 0; k < seg_count; ++k) {                                                               \
+        FA_SEG_BIND                                                                                           \
+        const T* proj = all_proj + seg_proj_off[k];                                                           \
+        const T* orow = gout + b * out_dim + seg_out_off[k];                                                  \
+        T* grow = gpacked + b * packed_dim + seg_in_off[k];                                                   \
+        for (int64_t q = 0; q < source_dim * input_dim; ++q) grow[q] = 0;                                     \
+        for (int64_t s = 0; s < source_dim; ++s) {                                                            \
+          const T* in = packed + b * packed_dim + seg_in_off[k] + s * input_dim;                              \
+          FA_REPLAY(T, CONJ)                                                                                  \
+          for (int64_t ri = 0; ri < root_count; ++ri) {                                                       \
+            const int64_t rn = roots[ri], rdim = node_dims[rn];                                               \
+            T* ra = wa + node_offsets[rn];                                                                    \
+            for (int64_t p = 0; p < root_pd[ri]; ++p) {                                                       \
+              const T* blk = orow + root_oo[ri] + p * rdim;                                                   \
+              const T pv = proj[s * proj_dim + root_ps[ri] + p];                                              \
+              for (int64_t m = 0; m < rdim; ++m) ra[m] += blk[m] * CONJ(pv);                                  \
+            }                                                                                                 \
+          }                                                                                                   \
+          T* gin = grow + s * input_dim;                                                                      \
+          FA_SWEEP(T, CONJ)                                                                                   \
+        }                                                                                                     \
+      }                                                                                                       \
+    }                                                                                                         \
+  }
+
+FA_SEG_ADJOINT(oracle_factorized_angular_segmented_adjoint_f64, double, conj_r)
+FA_SEG_ADJOINT(oracle_factorized_angular_segmented_adjoint_c128, double complex, conj_c)
+
 /* ---- symmetric-power monomials ------------------------------------------- */
 
 /* symmetric_power_monomial_adjoint (ye3t_runtime_core.cpp:5318-5389): per term,

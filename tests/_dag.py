@@ -78,3 +78,79 @@ def random_dag(seed, *, complex_data, leaves_L=(1, 2, 1, 0), sources=3, projecti
               "coefficient_values": np.array(vals, dtype=np.complex128 if complex_data else np.float64),
               "root_nodes": np.array(roots), "projection_values": proj}
     return tables, sources, running_in
+
+
+SEGMENT_KEYS = ("segment_source_offsets", "segment_input_offsets", "segment_input_dimensions",
+                "segment_workspace_offsets", "segment_workspace_dimensions", "segment_node_offsets",
+                "segment_root_offsets", "segment_projection_offsets", "segment_projection_dimensions",
+                "segment_output_offsets", "node_offsets", "node_dimensions", "node_leaf_offsets", "node_left",
+                "node_right", "node_coefficient_offsets", "coefficient_rows", "coefficient_columns",
+                "coefficient_values", "root_nodes", "root_projection_starts", "root_projection_dimensions",
+                "root_output_offsets", "projection_values")
+
+
+def random_segmented(seed, *, complex_data, count=3):
+    """Random segmented tables (the reference segmented op's layout): ``count``
+    random DAGs with their own source count, leaves and projection width; each
+    segment's roots are random nodes of any dimension, each projecting onto a
+    random interval of its segment's projection columns, their output blocks
+    laid out in a shuffled order.  Returns ``(tables, dims)`` with ``dims`` =
+    (packed_input_dimension, total_source_count, workspace_dimension,
+    output_dimension)."""
+    rng = np.random.default_rng(seed)
+    t = {k: [] for k in SEGMENT_KEYS}
+    for k in ("segment_source_offsets", "segment_node_offsets", "segment_root_offsets", "segment_output_offsets"):
+        t[k].append(0)
+    src = in_base = ws_base = proj_base = out_base = node_base = root_base = coef_base = 0
+    for k in range(count):
+        leaves = tuple(int(x) for x in rng.integers(0, 4, size=int(rng.integers(2, 5))))
+        S, P = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+        dag, S, D = random_dag(int(seed) * 100 + k, complex_data=complex_data, leaves_L=leaves, sources=S,
+                               projections=P, max_nodes=len(leaves) + int(rng.integers(2, 8)))
+        dims = np.asarray(dag["node_dimensions"])
+        N = int(dims.size)
+        W = int(dag["node_offsets"][-1] + dims[-1])
+        R = int(rng.integers(1, min(4, N) + 1))
+        roots = rng.choice(N, size=R, replace=False)
+        ps = rng.integers(0, P, size=R)
+        pd = np.array([int(rng.integers(1, P - a + 1)) for a in ps])
+        sizes = pd * dims[roots]
+        oo = np.zeros(R, dtype=np.int64)
+        cursor = 0
+        for r in rng.permutation(R):
+            oo[r] = cursor
+            cursor += int(sizes[r])
+        src += S
+        t["segment_source_offsets"].append(src)
+        t["segment_input_offsets"].append(in_base)
+        t["segment_input_dimensions"].append(D)
+        t["segment_workspace_offsets"].append(ws_base)
+        t["segment_workspace_dimensions"].append(W)
+        t["segment_projection_offsets"].append(proj_base)
+        t["segment_projection_dimensions"].append(P)
+        for n in ("node_offsets", "node_dimensions", "node_leaf_offsets", "node_left", "node_right"):
+            t[n].extend(int(v) for v in dag[n])
+        offs = [int(v) + coef_base for v in dag["node_coefficient_offsets"]]
+        t["node_coefficient_offsets"].extend(offs if k == 0 else offs[1:])
+        t["coefficient_rows"].extend(int(v) for v in dag["coefficient_rows"])
+        t["coefficient_columns"].extend(int(v) for v in dag["coefficient_columns"])
+        t["coefficient_values"].extend(dag["coefficient_values"])
+        t["root_nodes"].extend(int(v) for v in roots)
+        t["root_projection_starts"].extend(int(v) for v in ps)
+        t["root_projection_dimensions"].extend(int(v) for v in pd)
+        t["root_output_offsets"].extend(int(v) for v in oo)
+        t["projection_values"].extend(dag["projection_values"])
+        node_base += N
+        root_base += R
+        coef_base += len(dag["coefficient_values"])
+        proj_base += S * P
+        in_base += S * D
+        ws_base += S * W
+        out_base += cursor
+        t["segment_node_offsets"].append(node_base)
+        t["segment_root_offsets"].append(root_base)
+        t["segment_output_offsets"].append(out_base)
+    vdt = np.complex128 if complex_data else np.float64
+    tables = {k: np.asarray(v, dtype=vdt if k in ("coefficient_values", "projection_values") else np.int64)
+              for k, v in t.items()}
+    return tables, (in_base, src, ws_base, out_base)

@@ -29,6 +29,8 @@ REFERENCE_OPERATIONS = (
     "factorized_angular_adjoint",
     "factorized_angular_linear",
     "factorized_angular_linear_adjoint",
+    "factorized_angular_segmented",
+    "factorized_angular_segmented_adjoint",
 )
 FUSED_OPERATIONS = (
     "ace_density_forward",
@@ -299,7 +301,7 @@ def native_execution_plan_capabilities():
         "hip_arch": "gfx950",
         "cuda_density_auto_min_work_items": None,
         "hip_density_reduction": "csr_segment_deterministic",
-        "segmented_factorized_angular": False,
+        "segmented_factorized_angular": bool(available),
         "heterogeneous_factorized_roots": False,
         "triton_available": False,
         "triton_cuda_available": False,
@@ -321,7 +323,8 @@ def native_execution_plan_capabilities():
 
 def __getattr__(name):
     # the factorized-angular op and module load torch, so they are imported on first use
-    if name in ("factorized_angular", "factorized_angular_linear", "YE3TFactorizedAngularModule"):
+    if name in ("factorized_angular", "factorized_angular_linear", "factorized_angular_segmented",
+                "YE3TFactorizedAngularModule", "YE3TSegmentedFactorizedAngularModuleGroup"):
         import importlib
 
         return getattr(importlib.import_module("ye3t_amd.runtime.dag"), name)

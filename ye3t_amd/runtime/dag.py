@@ -25,37 +25,51 @@ from ye3t_amd.runtime import native
 _PLANS = {}
 
 
-def _table_arrays(tables):
+def _table_arrays(tables, names=native.FA_TABLE_NAMES):
     out = {}
-    for name in native.FA_TABLE_NAMES:
+    for name in names:
         v = tables[name]
         out[name] = v.detach().cpu().numpy() if hasattr(v, "detach") else np.asarray(v)
     return out
 
 
-def plan_for(tables, source_dimension, input_dimension, workspace_dimension, output_dimension, dtype, device):
-    """The device plan of these tables (validated and uploaded once, cached by
-    content, dimensions, dtype and device)."""
-    arrays = _table_arrays(tables)
+def _cached_plan(names, tables, dims, dtype, device, make):
+    arrays = _table_arrays(tables, names)
     h = hashlib.sha256()
-    for name in native.FA_TABLE_NAMES:
+    for name in names:
         a = np.ascontiguousarray(arrays[name])
         h.update(name.encode())
         h.update(str(a.dtype).encode())
+        h.update(str(a.shape).encode())
         h.update(a.tobytes())
-    key = (h.hexdigest(), int(source_dimension), int(input_dimension), int(workspace_dimension),
-           int(output_dimension), str(dtype), str(device))
+    key = (names, h.hexdigest(), tuple(int(d) for d in dims), str(dtype), str(device))
     plan = _PLANS.get(key)
     if plan is None:
         import torch
 
         with torch.cuda.device(device):
-            plan = native.FactorizedAngularPlanHandle(arrays, source_dimension, input_dimension, workspace_dimension,
-                                                      output_dimension, dtype)
+            plan = make(arrays)
         if len(_PLANS) > 64:
             _PLANS.clear()
         _PLANS[key] = plan
     return plan
+
+
+def plan_for(tables, source_dimension, input_dimension, workspace_dimension, output_dimension, dtype, device):
+    """The device plan of these tables (validated and uploaded once, cached by
+    content, dimensions, dtype and device)."""
+    dims = (source_dimension, input_dimension, workspace_dimension, output_dimension)
+    return _cached_plan(native.FA_TABLE_NAMES, tables, dims, dtype, device,
+                        lambda a: native.FactorizedAngularPlanHandle(a, *dims, dtype))
+
+
+def segmented_plan_for(tables, packed_input_dimension, total_source_count, workspace_dimension, output_dimension,
+                       dtype, device):
+    """The device plan of segmented tables (``native.SEGMENT_TABLE_NAMES``),
+    cached like :func:`plan_for`."""
+    dims = (packed_input_dimension, total_source_count, workspace_dimension, output_dimension)
+    return _cached_plan(native.SEGMENT_TABLE_NAMES, tables, dims, dtype, device,
+                        lambda a: native.FactorizedAngularSegmentedPlanHandle(a, *dims, dtype))
 
 
 def _autograd():
@@ -149,6 +163,100 @@ def factorized_angular_linear(packed_slots, node_offsets, node_dimensions, node_
     plan = plan_for(tables, S, int(packed_slots.shape[1]) // S, workspace_dimension, int(weight.numel()),
                     packed_slots.dtype, packed_slots.device)
     return _fns()[1].apply(packed_slots.contiguous(), weight, bias, plan)
+
+
+def factorized_angular_segmented(packed_slots, segment_source_offsets, segment_input_offsets,
+                                 segment_input_dimensions, segment_workspace_offsets, segment_workspace_dimensions,
+                                 segment_node_offsets, segment_root_offsets, segment_projection_offsets,
+                                 segment_projection_dimensions, segment_output_offsets, node_offsets, node_dimensions,
+                                 node_leaf_offsets, node_left, node_right, node_coefficient_offsets,
+                                 coefficient_rows, coefficient_columns, coefficient_values, root_nodes,
+                                 root_projection_starts, root_projection_dimensions, root_output_offsets,
+                                 projection_values, total_source_count, workspace_dimension, output_dimension):
+    """``ye3t_runtime::factorized_angular_segmented`` (schema
+    ``execution_plan_torch.cpp:7666-7679``): several factorized-angular DAGs
+    over disjoint column ranges of ``packed_slots`` in one launch;
+    ``[batch, output_dimension]``, differentiable (the segmented adjoint,
+    ``:7681-7695``)."""
+    _check_device(packed_slots)
+    if packed_slots.ndim != 2:
+        raise RuntimeError("packed_slots must be [batch, packed width]")
+    values = (segment_source_offsets, segment_input_offsets, segment_input_dimensions, segment_workspace_offsets,
+              segment_workspace_dimensions, segment_node_offsets, segment_root_offsets, segment_projection_offsets,
+              segment_projection_dimensions, segment_output_offsets, node_offsets, node_dimensions,
+              node_leaf_offsets, node_left, node_right, node_coefficient_offsets, coefficient_rows,
+              coefficient_columns, coefficient_values, root_nodes, root_projection_starts,
+              root_projection_dimensions, root_output_offsets, projection_values)
+    tables = dict(zip(native.SEGMENT_TABLE_NAMES, values))
+    plan = segmented_plan_for(tables, int(packed_slots.shape[1]), total_source_count, workspace_dimension,
+                              output_dimension, packed_slots.dtype, packed_slots.device)
+    return _fns()[0].apply(packed_slots.contiguous(), plan)
+
+
+def segmented_tables(members):
+    """Concatenated segmented tables of several DAGs, as the reference's
+    segmented group builds them (``execution_plan.py:16672-16884``): each
+    member (a :class:`YE3TFactorizedAngularModule`, or any object with its
+    table attributes and dimensions) becomes one segment with
+    the uniform root metadata (every root onto all of its P projection columns,
+    root ``r``'s block at ``r * P * (2 L + 1)``).  Returns ``(tables, dims)``,
+    ``dims`` = (packed_input_dimension, total_source_count,
+    workspace_dimension, output_dimension)."""
+    cols = {name: [] for name in native.SEGMENT_TABLE_NAMES}
+    src, node_base, root_base, coef_base, in_base, ws_base, proj_base, out_base = 0, 0, 0, 0, 0, 0, 0, 0
+    cols["segment_source_offsets"].append(0)
+    cols["segment_node_offsets"].append(0)
+    cols["segment_root_offsets"].append(0)
+    cols["segment_output_offsets"].append(0)
+    for k, m in enumerate(members):
+        arr = {}
+        for n in native.FA_TABLE_NAMES:
+            v = getattr(m, n)
+            arr[n] = v.detach().cpu().numpy() if hasattr(v, "detach") else np.asarray(v)
+        S, D, W = int(m.source_dimension), int(m.input_dimension), int(m.workspace_dimension)
+        if int(arr["projection_values"].size) % S:
+            raise ValueError("factorized projection table does not match source dimension")
+        P = int(arr["projection_values"].size) // S
+        R = int(arr["root_nodes"].size)
+        if R * P * int(m.magnetic_dimension) != int(m.output_dimension):
+            raise ValueError("segmented factorized output does not match roots")
+        src += S
+        cols["segment_source_offsets"].append(src)
+        cols["segment_input_offsets"].append(in_base)
+        cols["segment_input_dimensions"].append(D)
+        cols["segment_workspace_offsets"].append(ws_base)
+        cols["segment_workspace_dimensions"].append(W)
+        cols["segment_projection_offsets"].append(proj_base)
+        cols["segment_projection_dimensions"].append(P)
+        for n in ("node_offsets", "node_dimensions", "node_leaf_offsets", "node_left", "node_right"):
+            cols[n].append(arr[n])
+        offs = arr["node_coefficient_offsets"] + coef_base
+        cols["node_coefficient_offsets"].append(offs if k == 0 else offs[1:])
+        for n in ("coefficient_rows", "coefficient_columns", "coefficient_values", "root_nodes",
+                  "projection_values"):
+            cols[n].append(arr[n])
+        cols["root_projection_starts"].append(np.zeros(R, dtype=np.int64))
+        cols["root_projection_dimensions"].append(np.full(R, P, dtype=np.int64))
+        cols["root_output_offsets"].append(np.arange(R, dtype=np.int64) * P * int(m.magnetic_dimension))
+        node_base += int(arr["node_offsets"].size)
+        root_base += R
+        coef_base += int(arr["coefficient_values"].size)
+        proj_base += int(arr["projection_values"].size)
+        in_base += S * D
+        ws_base += S * W
+        out_base += int(m.output_dimension)
+        cols["segment_node_offsets"].append(node_base)
+        cols["segment_root_offsets"].append(root_base)
+        cols["segment_output_offsets"].append(out_base)
+    tables = {}
+    for n, parts in cols.items():
+        if n in ("coefficient_values", "projection_values"):
+            tables[n] = np.concatenate(parts)
+        elif parts and isinstance(parts[0], np.ndarray):
+            tables[n] = np.concatenate(parts).astype(np.int64)
+        else:
+            tables[n] = np.asarray(parts, dtype=np.int64)
+    return tables, (in_base, src, ws_base, out_base)
 
 
 def _torch():
@@ -318,4 +426,84 @@ class YE3TFactorizedAngularModule(torch.nn.Module):
             "last_linear_readout_backend": self.last_linear_readout_backend,
             "linear_readout_auto_policy": "fuse",
             "analysis_orientation": self.analysis_orientation,
+        }
+
+
+class YE3TSegmentedFactorizedAngularModuleGroup(torch.nn.Module):
+    """Several prepared factorized-angular plans evaluated by one segmented
+    launch (reference ``_YE3TSegmentedFactorizedAngularModuleGroup``,
+    ``execution_plan.py:16632-17100``).
+
+    ``forward(slot_values_by_plan)`` takes one slot tuple per member module
+    (shared leading shape) and returns one ``[..., roots * P, 2 L + 1]``
+    tensor per member; ``forward_packed`` returns the concatenated
+    ``[batch, output_dimension]`` rows."""
+
+    def __init__(self, modules, plan_indices=None, enable_native=True):
+        super().__init__()
+        modules = tuple(modules)
+        if not modules:
+            raise ValueError("segmented factorized group requires at least one plan")
+        plan_indices = tuple(range(len(modules))) if plan_indices is None else tuple(int(v) for v in plan_indices)
+        if len(plan_indices) != len(modules):
+            raise ValueError("segmented factorized plan indices must match modules")
+        first = modules[0]
+        if any(m.coefficient_values.dtype != first.coefficient_values.dtype or
+               m.coefficient_values.device != first.coefficient_values.device for m in modules[1:]):
+            raise ValueError("segmented factorized plans must share backend, dtype, and device")
+        if not enable_native:
+            raise NotImplementedError("ye3t_amd runs the native segmented launch only")
+        object.__setattr__(self, "_source_modules", modules)
+        self.plan_indices = plan_indices
+        tables, dims = segmented_tables(modules)
+        self.input_dimension, self.total_source_count, self.workspace_dimension, self.output_dimension = dims
+        self._tables = tables
+        dt, dev = first.coefficient_values.dtype, first.coefficient_values.device
+        self._plan = segmented_plan_for(tables, *dims, dt, dev)
+        starts = tables["segment_output_offsets"]
+        self.output_slices = tuple({"plan_index": int(i), "start": int(starts[k]), "stop": int(starts[k + 1]),
+                                    "logical_channel_tableau_dimension": int(m.logical_channel_tableau_dimension),
+                                    "magnetic_dimension": int(m.magnetic_dimension), "plan_hash": str(m.plan_hash)}
+                                   for k, (m, i) in enumerate(zip(modules, plan_indices)))
+        self.last_backend = None
+
+    def native_tables(self):
+        """The op's table arguments (numpy), in the reference schema's order."""
+        return tuple(self._tables[n] for n in native.SEGMENT_TABLE_NAMES)
+
+    def forward_packed(self, slot_values_by_plan):
+        slot_values_by_plan = tuple(tuple(v) for v in slot_values_by_plan)
+        if len(slot_values_by_plan) != len(self._source_modules):
+            raise ValueError("segmented factorized input count does not match plans")
+        packed, leading = [], []
+        for m, values in zip(self._source_modules, slot_values_by_plan):
+            p, lead = m._packed_slots(values)
+            packed.append(p)
+            leading.append(tuple(lead))
+        if any(s != leading[0] for s in leading[1:]):
+            raise ValueError("segmented factorized plans require matching leading shapes")
+        packed = _torch().cat(tuple(packed), dim=1).contiguous()
+        self.last_backend = "native_destination_segmented_factorized_angular"
+        if int(packed.shape[0]) == 0:
+            return packed.new_zeros((0, self.output_dimension))
+        return _fns()[0].apply(packed, self._plan)
+
+    def forward(self, slot_values_by_plan):
+        slot_values_by_plan = tuple(tuple(v) for v in slot_values_by_plan)
+        out = self.forward_packed(slot_values_by_plan)
+        first = slot_values_by_plan[0][0]
+        lead = tuple(first.shape[:-1] if int(self._source_modules[0].source_dimension) == 1 else first.shape[:-2])
+        return tuple(out[:, r["start"]:r["stop"]].reshape(lead + (r["logical_channel_tableau_dimension"],
+                                                                  r["magnetic_dimension"]))
+                     for r in self.output_slices)
+
+    def runtime_report(self):
+        return {
+            "runtime": "YE3TSegmentedFactorizedAngularModuleGroup",
+            "member_plan_count": len(self._source_modules), "member_plan_indices": tuple(self.plan_indices),
+            "member_plan_hashes": tuple(str(m.plan_hash) for m in self._source_modules),
+            "source_dimensions": tuple(int(m.source_dimension) for m in self._source_modules),
+            "total_source_count": int(self.total_source_count), "input_dimension": int(self.input_dimension),
+            "workspace_dimension": int(self.workspace_dimension), "output_dimension": int(self.output_dimension),
+            "native_enabled": True, "native_call_count": 1, "last_backend": self.last_backend,
         }

@@ -48,6 +48,26 @@ class FactorizedAngularDesc(ctypes.Structure):
                 ("output_dimension", _i64)]
 
 
+SEGMENT_TABLE_NAMES = ("segment_source_offsets", "segment_input_offsets", "segment_input_dimensions",
+                       "segment_workspace_offsets", "segment_workspace_dimensions", "segment_node_offsets",
+                       "segment_root_offsets", "segment_projection_offsets", "segment_projection_dimensions",
+                       "segment_output_offsets", "node_offsets", "node_dimensions", "node_leaf_offsets", "node_left",
+                       "node_right", "node_coefficient_offsets", "coefficient_rows", "coefficient_columns",
+                       "coefficient_values", "root_nodes", "root_projection_starts", "root_projection_dimensions",
+                       "root_output_offsets", "projection_values")
+
+
+class FactorizedAngularSegmentedDesc(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int), ("segment_count", _i64)] + \
+        [(n, _vp) for n in SEGMENT_TABLE_NAMES[:10]] + \
+        [("node_count", _i64)] + [(n, _vp) for n in SEGMENT_TABLE_NAMES[10:16]] + \
+        [("coefficient_count", _i64), ("coefficient_rows", _vp), ("coefficient_columns", _vp),
+         ("coefficient_values", _vp), ("root_count", _i64), ("root_nodes", _vp), ("root_projection_starts", _vp),
+         ("root_projection_dimensions", _vp), ("root_output_offsets", _vp), ("projection_count", _i64),
+         ("projection_values", _vp), ("packed_input_dimension", _i64), ("total_source_count", _i64),
+         ("workspace_dimension", _i64), ("output_dimension", _i64)]
+
+
 class CellGrid(ctypes.Structure):
     _fields_ = [("origin", ctypes.c_double * 3), ("cell_edge", ctypes.c_double), ("dims", _i64 * 3)]
 
@@ -129,6 +149,13 @@ def lib():
     L.ye3t_hip_factorized_angular_adjoint.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
     L.ye3t_hip_factorized_angular_linear_forward.argtypes = [_vp, _vp, _i64, _vp, _vp, _vp, _vp]
     L.ye3t_hip_factorized_angular_linear_adjoint.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp]
+    L.ye3t_hip_factorized_angular_segmented_plan_create.argtypes = [ctypes.POINTER(FactorizedAngularSegmentedDesc),
+                                                                    ctypes.POINTER(_vp)]
+    L.ye3t_hip_factorized_angular_segmented_plan_destroy.argtypes = [_vp]
+    L.ye3t_hip_factorized_angular_segmented_plan_destroy.restype = None
+    L.ye3t_hip_factorized_angular_segmented_plan_info.argtypes = [_vp, _vp]
+    L.ye3t_hip_factorized_angular_segmented_forward.argtypes = [_vp, _vp, _i64, _vp, _vp]
+    L.ye3t_hip_factorized_angular_segmented_adjoint.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
     L.ye3t_hip_neighbor_workspace_bytes.argtypes = [_i64, ctypes.POINTER(CellGrid)]
     L.ye3t_hip_neighbor_workspace_bytes.restype = _i64
     L.ye3t_hip_neighbor_count.argtypes = [ctypes.c_int, _vp, _i64, ctypes.POINTER(CellGrid), ctypes.c_double, _vp,
@@ -159,7 +186,9 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_factorized_angular_forward", "ye3t_hip_factorized_angular_adjoint",
     "ye3t_hip_factorized_angular_linear_forward", "ye3t_hip_factorized_angular_linear_adjoint",
     "ye3t_hip_symmetric_power_monomial_adjoint", "ye3t_hip_symmetric_power_shared_monomial",
-    "ye3t_hip_symmetric_power_shared_monomial_adjoint",
+    "ye3t_hip_symmetric_power_shared_monomial_adjoint", "ye3t_hip_factorized_angular_segmented_plan_create",
+    "ye3t_hip_factorized_angular_segmented_plan_destroy", "ye3t_hip_factorized_angular_segmented_plan_info",
+    "ye3t_hip_factorized_angular_segmented_forward", "ye3t_hip_factorized_angular_segmented_adjoint",
 )
 
 
@@ -1089,3 +1118,103 @@ class FactorizedAngularPlanHandle:
             _dev(feats, "features"), _dev(gx, "packed_adjoint"), _dev(gw, "weight_adjoint"),
             ctypes.c_void_p(gb.data_ptr()), _stream()), "ye3t_hip_factorized_angular_linear_adjoint")
         return gx, gw, gb
+
+
+class FactorizedAngularSegmentedPlanHandle:
+    """A validated, device-resident segmented factorized-angular plan
+    (``ye3t_hip_factorized_angular_segmented_plan``): the reference op's
+    segment, node, coefficient, root and projection tables
+    (``execution_plan_torch.cpp:7666-7679``) in ``dtype``."""
+
+    def __init__(self, tables, packed_input_dimension, total_source_count, workspace_dimension, output_dimension,
+                 dtype):
+        import torch
+
+        self.dtype = dtype
+        np_t = {torch.float32: np.float32, torch.float64: np.float64, torch.complex64: np.complex64,
+                torch.complex128: np.complex128}[dtype]
+        keep = {}
+        for name in SEGMENT_TABLE_NAMES:
+            v = tables[name]
+            v = v.detach().cpu().numpy() if hasattr(v, "detach") else np.asarray(v)
+            if name in ("coefficient_values", "projection_values"):
+                if np.iscomplexobj(v) and not np.iscomplexobj(np.empty(0, np_t)):
+                    v = v.real
+                keep[name] = np.ascontiguousarray(v.reshape(-1).astype(np_t))
+            else:
+                keep[name] = np.ascontiguousarray(v.reshape(-1), dtype=np.int64)
+        self._keep = keep
+        K = int(keep["segment_input_offsets"].size)
+        counts = {"segment_source_offsets": K + 1, "segment_node_offsets": K + 1, "segment_root_offsets": K + 1,
+                  "segment_output_offsets": K + 1}
+        for name in SEGMENT_TABLE_NAMES[:10]:
+            if int(keep[name].size) != counts.get(name, K):
+                raise RuntimeError("segmented boundary offsets must contain segment_count + 1 entries"
+                                   if name in counts else "segmented per-plan metadata must match segment count")
+        n = int(keep["node_offsets"].size)
+        for name in ("node_dimensions", "node_leaf_offsets", "node_left", "node_right"):
+            if int(keep[name].size) != n:
+                raise RuntimeError("segmented node metadata has inconsistent lengths")
+        if int(keep["node_coefficient_offsets"].size) != n + 1:
+            raise RuntimeError("segmented node metadata has inconsistent lengths")
+        e = int(keep["coefficient_rows"].size)
+        if int(keep["coefficient_columns"].size) != e or int(keep["coefficient_values"].size) != e:
+            raise RuntimeError("segmented coefficient arrays must have equal length")
+        r = int(keep["root_nodes"].size)
+        for name in ("root_projection_starts", "root_projection_dimensions", "root_output_offsets"):
+            if int(keep[name].size) != r:
+                raise RuntimeError("segmented root metadata has inconsistent lengths")
+
+        def ptr(name):
+            a = keep[name]
+            return ctypes.c_void_p(a.ctypes.data) if a.size else None
+
+        desc = FactorizedAngularSegmentedDesc(
+            dtype=_any_dtype_code(dtype), segment_count=K, node_count=n, coefficient_count=e, root_count=r,
+            projection_count=int(keep["projection_values"].size), packed_input_dimension=int(packed_input_dimension),
+            total_source_count=int(total_source_count), workspace_dimension=int(workspace_dimension),
+            output_dimension=int(output_dimension), **{name: ptr(name) for name in SEGMENT_TABLE_NAMES})
+        handle = ctypes.c_void_p()
+        _check(lib().ye3t_hip_factorized_angular_segmented_plan_create(ctypes.byref(desc), ctypes.byref(handle)),
+               "ye3t_hip_factorized_angular_segmented_plan_create")
+        self._handle = handle
+        self.packed_input_dimension = int(packed_input_dimension)
+        self.output_dimension = int(output_dimension)
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h is not None and h.value and _LIB is not None:
+            _LIB.ye3t_hip_factorized_angular_segmented_plan_destroy(h)
+            self._handle = None
+
+    def _packed(self, packed):
+        if not packed.is_cuda or packed.dtype != self.dtype or packed.ndim != 2 or \
+                int(packed.shape[1]) != self.packed_input_dimension:
+            raise ValueError(f"packed_slots must be a {self.dtype} GPU tensor [batch, {self.packed_input_dimension}]")
+        return packed.contiguous()
+
+    def forward(self, packed):
+        import torch
+
+        packed = self._packed(packed)
+        B = int(packed.shape[0])
+        out = torch.empty((B, self.output_dimension), dtype=self.dtype, device=packed.device)
+        _check(lib().ye3t_hip_factorized_angular_segmented_forward(self._handle, _dev(packed, "packed_slots"), B,
+                                                                   _dev(out, "output"), _stream()),
+               "ye3t_hip_factorized_angular_segmented_forward")
+        return out
+
+    def adjoint(self, output_adjoint, packed):
+        import torch
+
+        packed = self._packed(packed)
+        B = int(packed.shape[0])
+        g = output_adjoint.to(self.dtype).contiguous()
+        if tuple(g.shape) != (B, self.output_dimension):
+            raise ValueError(f"output_adjoint must be [{B}, {self.output_dimension}]")
+        out = torch.empty_like(packed)
+        _check(lib().ye3t_hip_factorized_angular_segmented_adjoint(self._handle, _dev(g, "output_adjoint"),
+                                                                   _dev(packed, "packed_slots"), B,
+                                                                   _dev(out, "adjoint"), _stream()),
+               "ye3t_hip_factorized_angular_segmented_adjoint")
+        return out
