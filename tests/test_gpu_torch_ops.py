@@ -1,0 +1,142 @@
+"""The ``ye3t_runtime`` Torch operators on the GPU through the shim.
+
+Each covered operator, called as the reference's Python calls it
+(``torch.ops.ye3t_runtime.<op>`` on device tensors), runs this library's
+kernels: its results equal the direct entry points' (the same kernels) and the
+oracle's, and ``torch.library.opcheck`` (schema, fake tensor, autograd
+registration, AOT dispatch) passes, as the reference's own operator tests
+require (``tests/test_execution_plan_native.py:6303-6350``).
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from tests._dag import KAT_OUTPUT, KAT_PACKED, KAT_SOURCES, KAT_TABLES, KAT_WORKSPACE, SEGMENT_KEYS, random_segmented
+from tests._util import TOL, column_rel_error, flush
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    import torch
+
+    from ye3t_amd.runtime import torch_ops
+
+    torch_ops.register()
+    return torch.ops.ye3t_runtime
+
+
+def _opcheck(op, args):
+    import torch
+
+    result = torch.library.opcheck(op, args, raise_exception=False)
+    assert all(v == "SUCCESS" for v in result.values()), result
+
+
+def _fa_args(dev, dt):
+    import torch
+
+    out = [torch.as_tensor(np.asarray(KAT_TABLES[n]), dtype=torch.int64, device=dev) for n in (
+        "node_offsets", "node_dimensions", "node_leaf_offsets", "node_left", "node_right",
+        "node_coefficient_offsets", "coefficient_rows", "coefficient_columns")]
+    out.append(torch.as_tensor(np.asarray(KAT_TABLES["coefficient_values"]), device=dev).to(dt))
+    out.append(torch.as_tensor(np.asarray(KAT_TABLES["root_nodes"]), dtype=torch.int64, device=dev))
+    out.append(torch.as_tensor(np.asarray(KAT_TABLES["projection_values"]), device=dev).to(dt))
+    return out
+
+
+def test_factorized_angular_operators(gpu):
+    flush("torch ops: factorized_angular / adjoint / linear (complex128)")
+    import torch
+
+    ops = _ops()
+    dt = torch.complex128
+    args = _fa_args(gpu, dt)
+    packed = torch.as_tensor(KAT_PACKED, dtype=dt, device=gpu)
+    out = ops.factorized_angular(packed, *args, KAT_SOURCES, KAT_WORKSPACE, KAT_OUTPUT)
+    ref = oracle.factorized_angular(KAT_PACKED.astype(np.complex128), KAT_TABLES, KAT_SOURCES)
+    assert np.max(np.abs(out.cpu().numpy() - ref)) <= 1e-12
+    _opcheck(ops.factorized_angular.default,
+             (packed.clone().requires_grad_(True), *args, KAT_SOURCES, KAT_WORKSPACE, KAT_OUTPUT))
+    g = torch.randn(out.shape, dtype=dt, device=gpu)
+    adj = ops.factorized_angular_adjoint(g, packed, *args, KAT_SOURCES, KAT_WORKSPACE)
+    assert np.max(np.abs(adj.cpu().numpy() - oracle.factorized_angular_adjoint(
+        g.cpu().numpy(), KAT_PACKED.astype(np.complex128), KAT_TABLES, KAT_SOURCES))) <= 1e-12
+    _opcheck(ops.factorized_angular_adjoint.default, (g, packed, *args, KAT_SOURCES, KAT_WORKSPACE))
+    w = torch.randn(KAT_OUTPUT, dtype=dt, device=gpu)
+    b = torch.tensor(0.25 - 0.5j, dtype=dt, device=gpu)
+    lin = ops.factorized_angular_linear(packed, *args, KAT_SOURCES, KAT_WORKSPACE, w, b)
+    torch.testing.assert_close(lin, out @ w + b, rtol=1e-12, atol=1e-12)
+    _opcheck(ops.factorized_angular_linear.default,
+             (packed.clone().requires_grad_(True), *args, KAT_SOURCES, KAT_WORKSPACE, w.clone().requires_grad_(True),
+              b.clone().requires_grad_(True)))
+
+
+@pytest.mark.parametrize("count", [1, 3])
+def test_segmented_and_heterogeneous_operators(gpu, count):
+    flush(f"torch ops: factorized_angular_segmented / heterogeneous ({count} segments)")
+    import torch
+
+    ops = _ops()
+    tables, (D, S, W, F) = random_segmented(20 + count, complex_data=False, count=count)
+    t = {k: torch.as_tensor(v, device=gpu) for k, v in tables.items()}
+    x = torch.randn(37, D, dtype=torch.float64, device=gpu)
+    seg_args = tuple(t[k] for k in SEGMENT_KEYS)
+    out = ops.factorized_angular_segmented(x, *seg_args, S, W, F)
+    ref = oracle.factorized_angular_segmented(x.cpu().numpy(), tables, F)
+    assert column_rel_error(out.cpu().numpy(), ref) < TOL["f64"]
+    _opcheck(ops.factorized_angular_segmented.default, (x.clone().requires_grad_(True), *seg_args, S, W, F))
+    if count == 1:
+        node = tuple(t[k] for k in ("node_offsets", "node_dimensions", "node_leaf_offsets", "node_left", "node_right",
+                                    "node_coefficient_offsets", "coefficient_rows", "coefficient_columns",
+                                    "coefficient_values", "root_nodes"))
+        het = node + (t["root_projection_starts"], t["root_projection_dimensions"], t["root_output_offsets"],
+                      t["projection_values"])
+        h = ops.factorized_angular_heterogeneous(x, *het, S, int(tables["segment_workspace_dimensions"][0]), F)
+        assert torch.equal(h, out)
+        _opcheck(ops.factorized_angular_heterogeneous.default,
+                 (x.clone().requires_grad_(True), *het, S, int(tables["segment_workspace_dimensions"][0]), F))
+
+
+def test_density_and_monomial_operators(gpu):
+    flush("torch ops: density_accumulate, monomials, radial and harmonic tables")
+    import torch
+
+    from ye3t_amd import runtime
+
+    ops = _ops()
+    rng = np.random.default_rng(3)
+    centers = torch.as_tensor(np.sort(rng.integers(0, 11, size=50)), device=gpu)
+    vals = torch.randn(50, 6, dtype=torch.float64, device=gpu)
+    acc = ops.density_accumulate(vals, centers, 11)
+    assert torch.equal(acc, runtime.density_accumulate(vals, centers, 11))
+    _opcheck(ops.density_accumulate.default, (vals.clone().requires_grad_(True), centers, 11))
+    _opcheck(ops.density_accumulate_adjoint.default, (acc.clone().requires_grad_(True), centers))
+    x = torch.randn(9, 3, dtype=torch.float64, device=gpu)
+    counts = torch.tensor([[2, 0, 0], [0, 1, 1], [1, 1, 0], [0, 0, 2]], dtype=torch.int64, device=gpu)
+    offsets = torch.tensor([0, 2, 4], dtype=torch.int64, device=gpu)
+    indices = torch.tensor([0, 0, 1, 1], dtype=torch.int64, device=gpu)
+    values = torch.tensor([0.75, -1.25, 0.5, -0.625], dtype=torch.float64, device=gpu)
+    mono = ops.symmetric_power_monomial(x, counts, offsets, indices, values)
+    assert torch.equal(mono, runtime.symmetric_power_monomial_contraction(x, counts, offsets, indices, values))
+    _opcheck(ops.symmetric_power_monomial.default, (x.clone().requires_grad_(True), counts, offsets, indices, values))
+    s_off = torch.tensor([0, 2, 4, 5], dtype=torch.int64, device=gpu)
+    terms = torch.tensor([0, 1, 1, 2, 0], dtype=torch.int64, device=gpu)
+    outs = torch.tensor([0, 0, 1, 1, 2], dtype=torch.int64, device=gpu)
+    cvals = torch.tensor([0.75, -1.25, 0.5, -0.625, 1.5], dtype=torch.float64, device=gpu)
+    shared = ops.symmetric_power_shared_monomial(x, counts, s_off, terms, outs, cvals)
+    assert torch.equal(shared, runtime.symmetric_power_shared_monomial_contraction(x, counts, s_off, terms, outs,
+                                                                                  cvals))
+    _opcheck(ops.symmetric_power_shared_monomial.default,
+             (x.clone().requires_grad_(True), counts, s_off, terms, outs, cvals))
+    r = torch.rand(40, dtype=torch.float64, device=gpu) * 4.5 + 0.3
+    c = torch.full_like(r, 5.0)
+    lam = torch.full_like(r, 1.5)
+    v, d = ops.cheb_exp_cos_radial_table_with_derivative(r, c, lam, 7)
+    v2, d2 = runtime.cheb_exp_cos_radial_table_with_derivative(r, c, lam, 7)
+    assert torch.equal(v, v2) and torch.equal(d, d2)
+    e = torch.randn(40, 3, dtype=torch.float64, device=gpu)
+    y, gy = ops.spherical_harmonics_table_with_derivative(e, 3, True, 1e-12)
+    y2, gy2 = runtime.spherical_harmonics_table_with_derivative(e, 3, real_output=True)
+    assert torch.equal(y, y2) and torch.equal(gy, gy2)

@@ -1,0 +1,97 @@
+"""The ``ye3t_runtime`` Torch operator shim on the CPU: registration, schemas, fake shapes.
+
+* every operator the shim covers exists after :func:`register` (idempotent);
+* its schema is the reference's, read from the reference's own registration
+  text where the reference tree is present (``execution_plan_torch.cpp``);
+* the fake implementations give the reference's output shapes and dtypes on
+  meta tensors;
+* CPU tensors reach no kernel of this library (Torch's dispatch error).
+"""
+
+import os
+import re
+
+import pytest
+import torch
+
+from ye3t_amd.runtime import torch_ops
+
+REF_TORCH_CPP = "/root/reference/ye3t/runtime/csrc/execution_plan_torch.cpp"
+
+
+def _ops():
+    torch_ops.register()
+    return torch.ops.ye3t_runtime
+
+
+def test_register_defines_every_covered_operator():
+    first = torch_ops.register()
+    assert torch_ops.register() == first
+    for name in torch_ops.SCHEMAS:
+        assert hasattr(_ops(), name), name
+    assert set(torch_ops.KERNELS) == set(torch_ops.SCHEMAS)
+    assert set(torch_ops.FAKES) == set(torch_ops.SCHEMAS)
+
+
+def _reference_schemas():
+    text = open(REF_TORCH_CPP).read()
+    out = {}
+    for m in re.finditer(r"library\.def\(\s*((?:\"[^\"]*\"\s*)+)\)", text):
+        schema = "".join(re.findall(r"\"([^\"]*)\"", m.group(1)))
+        name = schema.split("(", 1)[0]
+        out[name] = schema[len(name):]
+    return out
+
+
+@pytest.mark.skipif(not os.path.exists(REF_TORCH_CPP), reason="reference tree not present")
+def test_schemas_are_the_reference_registration():
+    ref = _reference_schemas()
+    norm = lambda s: re.sub(r"\s+", " ", s).replace("( ", "(").strip()  # noqa: E731
+    for name, schema in torch_ops.SCHEMAS.items():
+        assert name in ref, name
+        assert norm(schema) == norm(ref[name]), name
+    for name in torch_ops.SCHEMAS:
+        parsed = torch._C.parse_schema("ye3t_runtime::" + name + torch_ops.SCHEMAS[name])
+        assert str(_ops().__getattr__(name).default._schema) == str(parsed)
+
+
+def _m(*shape, dtype=torch.float64):
+    return torch.empty(shape, dtype=dtype, device="meta")
+
+
+def _i(n):
+    return torch.empty(n, dtype=torch.int64, device="meta")
+
+
+def test_fake_shapes_on_meta_tensors():
+    ops = _ops()
+    v, d = ops.cheb_exp_cos_radial_table_with_derivative(_m(7), _m(7), _m(7), 5)
+    assert v.shape == (7, 6) and d.shape == (7, 6)
+    v, g = ops.spherical_harmonics_table_with_derivative(_m(7, 3), 3, True, 1e-12)
+    assert v.shape == (7, 16) and g.shape == (7, 16, 3) and v.dtype == torch.float64
+    v, _ = ops.spherical_harmonics_table_with_derivative(_m(7, 3, dtype=torch.float32), 2, False, 1e-12)
+    assert v.dtype == torch.complex64 and v.shape == (7, 9)
+    assert ops.density_accumulate(_m(9, 4), _i(9), 3).shape == (3, 4)
+    assert ops.density_accumulate_adjoint(_m(3, 4), _i(9)).shape == (9, 4)
+    x = _m(5, 3)
+    assert ops.symmetric_power_monomial(x, _i(4), _i(6), _i(4), _m(4)).shape == (5, 5)
+    assert ops.symmetric_power_monomial_adjoint(_m(5, 5), x, _i(4), _i(6), _i(4), _m(4)).shape == (5, 3)
+    assert ops.symmetric_power_shared_monomial(x, _i(4), _i(3), _i(4), _i(4), _m(4)).shape == (5, 2)
+    fa = (_i(3), _i(3), _i(3), _i(3), _i(3), _i(4), _i(3), _i(3), _m(3), _i(1), _m(4))
+    p = _m(6, 12)
+    assert ops.factorized_angular(p, *fa, 2, 7, 2).shape == (6, 2)
+    assert ops.factorized_angular_adjoint(_m(6, 2), p, *fa, 2, 7).shape == (6, 12)
+    assert ops.factorized_angular_linear(p, *fa, 2, 7, _m(2), _m()).shape == (6,)
+    gx, gw, gb = ops.factorized_angular_linear_adjoint(_m(6), p, *fa, 2, 7, _m(2))
+    assert gx.shape == (6, 12) and gw.shape == (2,) and gb.shape == ()
+    het = fa[:10] + (_i(1), _i(1), _i(1), fa[10])
+    assert ops.factorized_angular_heterogeneous(p, *het, 2, 7, 3).shape == (6, 3)
+    seg = tuple(_i(2) for _ in range(10)) + fa[:10] + (_i(1), _i(1), _i(1), fa[10])
+    assert ops.factorized_angular_segmented(p, *seg, 2, 7, 5).shape == (6, 5)
+    assert ops.factorized_angular_segmented_adjoint(_m(6, 5), p, *seg, 2, 7).shape == (6, 12)
+
+
+def test_cpu_tensors_reach_no_kernel_here():
+    ops = _ops()
+    with pytest.raises(NotImplementedError, match="CPU"):
+        ops.density_accumulate(torch.zeros(3, 2, dtype=torch.float64), torch.zeros(3, dtype=torch.int64), 2)

@@ -29,6 +29,8 @@ REFERENCE_OPERATIONS = (
     "factorized_angular_adjoint",
     "factorized_angular_linear",
     "factorized_angular_linear_adjoint",
+    "factorized_angular_heterogeneous",
+    "factorized_angular_heterogeneous_adjoint",
     "factorized_angular_segmented",
     "factorized_angular_segmented_adjoint",
 )
@@ -302,7 +304,7 @@ def native_execution_plan_capabilities():
         "cuda_density_auto_min_work_items": None,
         "hip_density_reduction": "csr_segment_deterministic",
         "segmented_factorized_angular": bool(available),
-        "heterogeneous_factorized_roots": False,
+        "heterogeneous_factorized_roots": bool(available),
         "triton_available": False,
         "triton_cuda_available": False,
         "triton_operations": (),
