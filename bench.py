@@ -311,6 +311,33 @@ def bench_op(args, cfg):
             "note": "us_per_call: the whole build through the Python binding, including its host "
                     "synchronisation on the edge count and the output allocations"})
         line["config"].update({"atoms": N, "edges": E, "cutoff": cutoff, "box_edge": box})
+    elif args.op == "density_edge_gradient":
+        inp = cfg.density.generate()
+        dev = to_device_inputs(inp, dtype, "cuda")
+        N, E = d.atom_count, int(inp["edge_count"])
+        rows = d.radial_rows
+        shape = (N, d.channel_count, rows, (d.l_max + 1) ** 2)
+        gdt = torch.float64 if density == "f64" else torch.float32
+        gA = torch.as_tensor(np.random.default_rng(4).normal(size=shape), dtype=gdt, device="cuda")
+        kw = dict(atom_count=N, channel_count=d.channel_count, n_max=d.n_max, l_max=d.l_max, cutoff=inp["cutoff"],
+                  lam=inp["lambda"], epsilon=inp["epsilon"], species=dev.get("species"),
+                  node_features=dev.get("node_features"), radial_mix=dev.get("radial_mix"))
+        call = lambda v: native.ace_density_edge_gradient(gA, dev["edge_vectors"], dev["row_offsets"],  # noqa: E731
+                                                          dev["neighbors"], validate=v, **kw)
+        call(True)  # validates the CSR once
+        t = _time_kernel(lambda: call(False), args.steps, args.warmup)
+        elem = dev["edge_vectors"].element_size()
+        # per edge: its vector, neighbour index and gradient; per atom: its CSR offset, the
+        # adjoint row and (features) its feature row, each read once
+        feat = d.channel_count * elem if inp.get("node_features") is not None else 0
+        nbytes = E * (3 * elem + 8 + 3 * elem) + (N + 1) * 8 + gA.numel() * gA.element_size() + N * feat
+        line.update({
+            "metric": "force edges/s", "value": E / t, "unit": "edges/s", "higher_is_better": True,
+            "us_per_call": t * 1e6, "dtype": "f64", "storage_dtype": dtype, "adjoint_dtype": str(gdt)[6:],
+            "roofline": {"bound": "hbm", "achieved": nbytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": nbytes},
+            "note": "timed through the Python binding without its CSR validation (validated once)"})
+        line["config"].update({"edges": E, "atoms": N})
     else:
         inp = cfg.density.generate()
         N = d.atom_count
@@ -352,7 +379,7 @@ def main():
     ap.add_argument("--kernel", default="auto", choices=["auto", "generated", "interpreter"])
     ap.add_argument("--op", default="pipeline",
                     choices=["pipeline", "linear_readout", "density_accumulate_adjoint", "product_adjoint",
-                             "neighbor_list"],
+                             "neighbor_list", "density_edge_gradient"],
                     help="pipeline: the headline step (stage 1 + stage 2); the others time one widened op "
                          "on the config's shapes and print its own JSON line")
     ap.add_argument("--copy-probe", action="store_true",

@@ -139,6 +139,21 @@ int ye3t_hip_ace_density_forward(const ye3t_density_args* args, void* A, ye3t_st
  * launched ("" if none), for profiling.  No reference counterpart. */
 const char* ye3t_hip_last_density_kernel(void);
 
+/* Edge-vector gradient of the fused stage 1 (forces): edge_gradient[e, :] =
+ * d <density_adjoint, A> / d edge_vectors[e, :] for density_adjoint shaped like
+ * A ([N, C, R, (l_max+1)^2], dtype adjoint_dtype: YE3T_F64, or YE3T_F32 /
+ * YE3T_F64 with fp32 edge vectors) and edge_gradient [E, 3] in args->dtype;
+ * fp64 arithmetic, one lane per edge, no atomics.  The radial derivative's
+ * direction is v / max(|v|, epsilon), the unit vector of the harmonics.
+ * args->out_dtype and args->accumulate_dtype are ignored; n_max <= 15,
+ * l_max <= 8.  Replaces the reference's force path
+ * scheduled_radial_angular_channels_with_derivative (execution_plan.py:7675;
+ * schema execution_plan_torch.cpp:7267; CPU core ye3t_runtime_core.cpp:1550-1604)
+ * on the radial/harmonic derivative tables, followed by density_accumulate_adjoint
+ * (execution_plan_torch.cpp:7288) and the contraction with the edge adjoint. */
+int ye3t_hip_ace_density_edge_gradient(const ye3t_density_args* args, int adjoint_dtype, const void* density_adjoint,
+                                       void* edge_gradient, ye3t_stream_t stream);
+
 /* S[b, o] = sum_{t in [output_offsets[o], output_offsets[o+1])} monomial_values[t]
  *           * prod_c input[b, c]^monomial_counts[t, c]
  * for input[batch, input_dim], monomial_counts[T, input_dim], output_offsets[O+1]

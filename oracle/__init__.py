@@ -43,6 +43,8 @@ def lib():
         L.oracle_real_sph_table.argtypes = [_d, _I, _I, ctypes.c_double, _d, _d]
         L.oracle_density_accumulate.argtypes = [_d, _i64, _I, _I, _I, _d]
         L.oracle_density_accumulate_adjoint.argtypes = [_d, _i64, _I, _I, _d]
+        L.oracle_ace_density_edge_gradient.argtypes = [_I, _I, _i64, _i64, _d, _i32, _d, _d, _I, _I, _I,
+                                                       ctypes.c_double, ctypes.c_double, ctypes.c_double, _d, _d]
         L.oracle_ace_density.argtypes = [_I, _I, _i64, _i64, _d, _i32, _d, _d, _I, _I, _I,
                                          ctypes.c_double, ctypes.c_double, ctypes.c_double, _d]
         L.oracle_symmetric_power_monomial.argtypes = [_d, _I, _I, _i64, _i64, _d, _I, _d]
@@ -160,6 +162,34 @@ def ace_density(inp):
                              _p(fe) if fe is not None else None, _p(mx) if mx is not None else None,
                              C, n_max, l_max, float(inp["cutoff"]), float(inp["lambda"]),
                              float(inp.get("epsilon", 1e-12)), _p(out))
+    return out
+
+
+def ace_density_edge_gradient(inp, density_adjoint):
+    """Edge-vector gradient ``[E, 3]`` of ``<density_adjoint, A(edge_vectors)>``
+    for a stage-1 workload dict (``oracle_ace_density_edge_gradient``: the
+    reference's scheduled channel derivative, ye3t_runtime_core.cpp:1550-1604,
+    on the radial and harmonic derivative tables, contracted with the gathered
+    density adjoint)."""
+    N, E = int(inp["atom_count"]), int(inp["edge_count"])
+    centers = _i64a(inp["centers"])
+    neighbors = _i64a(inp["neighbors"])
+    vec = _f64(inp["edge_vectors"])
+    species = inp.get("species")
+    feats = inp.get("node_features")
+    mix = inp.get("radial_mix")
+    C, n_max, l_max = int(inp["channel_count"]), int(inp["n_max"]), int(inp["l_max"])
+    rows = 1 if mix is not None else n_max + 1
+    gA = _f64(density_adjoint).reshape(N, C * rows * (l_max + 1) ** 2)
+    out = np.zeros((E, 3))
+    sp = np.ascontiguousarray(species, dtype=np.int32) if species is not None else None
+    fe = _f64(feats) if feats is not None else None
+    mx = _f64(mix) if mix is not None else None
+    lib().oracle_ace_density_edge_gradient(N, E, _p(centers, _i64), _p(neighbors, _i64), _p(vec),
+                                           _p(sp, _i32) if sp is not None else None,
+                                           _p(fe) if fe is not None else None, _p(mx) if mx is not None else None,
+                                           C, n_max, l_max, float(inp["cutoff"]), float(inp["lambda"]),
+                                           float(inp.get("epsilon", 1e-12)), _p(gA), _p(out))
     return out
 
 

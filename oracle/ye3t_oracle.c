@@ -271,6 +271,76 @@ void oracle_ace_density(int64_t atom_count, int64_t edge_count, const int64_t* c
   free(edge_row); free(radii); free(cuts); free(lams); free(R); free(Y);
 }
 
+/* Edge-vector gradient of stage 1 composed the reference way: per edge e
+ * (centre i, neighbour j) and channel (c, r, k) the reference's scheduled
+ * channel derivative (ye3t_runtime_core.cpp:1550-1604)
+ *   d value / d v_e = w_c(j) (rad'_{c,r}(|v|) dir_e Y_k + rad_{c,r} dY_k / dv)
+ * with radial and harmonic tables from oracle_radial_table /
+ * oracle_real_sph_table (derivatives included), dir_e = v_e / max(|v_e|, eps)
+ * (the unit vector of the harmonics) and rad = R_r, or sum_q mix[c, q] R_q when
+ * radial_mix is set; contracted with the density adjoint gathered to the edge
+ * (density_accumulate_adjoint, ye3t_runtime_core.cpp:1704-1715):
+ *   grad[e, a] = sum_{c, r, k} adjoint[i, c, r, k] d value_{c,r,k} / d v_e[a]. */
+void oracle_ace_density_edge_gradient(int64_t atom_count, int64_t edge_count, const int64_t* centers,
+                                      const int64_t* neighbors, const double* edge_vectors, const int32_t* species,
+                                      const double* node_features, const double* radial_mix, int64_t channel_count,
+                                      int64_t n_max, int64_t l_max, double cutoff, double lambda, double epsilon,
+                                      const double* density_adjoint, double* grad) {
+  const int64_t nr = n_max + 1;
+  const int64_t lw = (l_max + 1) * (l_max + 1);
+  const int64_t rows = radial_mix ? 1 : nr;
+  const int64_t row = channel_count * rows * lw;
+  double* radii = (double*)malloc((size_t)edge_count * sizeof(double));
+  double* cuts = (double*)malloc((size_t)edge_count * sizeof(double));
+  double* lams = (double*)malloc((size_t)edge_count * sizeof(double));
+  double* R = (double*)malloc((size_t)(edge_count * nr) * sizeof(double));
+  double* dR = (double*)malloc((size_t)(edge_count * nr) * sizeof(double));
+  double* Y = (double*)malloc((size_t)(edge_count * lw) * sizeof(double));
+  double* dY = (double*)malloc((size_t)(edge_count * lw * 3) * sizeof(double));
+  for (int64_t e = 0; e < edge_count; ++e) {
+    const double* v = edge_vectors + 3 * e;
+    radii[e] = sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+    cuts[e] = cutoff; lams[e] = lambda;
+  }
+  (void)atom_count;
+  oracle_radial_table(radii, cuts, lams, edge_count, n_max, R, dR);
+  oracle_real_sph_table(edge_vectors, edge_count, l_max, epsilon, Y, dY);
+  for (int64_t e = 0; e < edge_count; ++e) {
+    const int64_t j = neighbors ? neighbors[e] : 0;
+    const double* adj = density_adjoint + centers[e] * row;
+    const double sr = radii[e] > epsilon ? radii[e] : epsilon;
+    double dir[3];
+    for (int a = 0; a < 3; ++a) dir[a] = edge_vectors[3 * e + a] / sr;
+    double g[3] = {0.0, 0.0, 0.0};
+    for (int64_t c = 0; c < channel_count; ++c) {
+      double w;
+      if (species) w = (species[j] == c) ? 1.0 : 0.0;
+      else if (node_features) w = node_features[j * channel_count + c];
+      else w = 1.0;
+      for (int64_t n = 0; n < rows; ++n) {
+        double rad, drad;
+        if (radial_mix) {
+          rad = 0.0; drad = 0.0;
+          for (int64_t q = 0; q < nr; ++q) {
+            rad += radial_mix[c * nr + q] * R[e * nr + q];
+            drad += radial_mix[c * nr + q] * dR[e * nr + q];
+          }
+        } else {
+          rad = R[e * nr + n];
+          drad = dR[e * nr + n];
+        }
+        for (int64_t k = 0; k < lw; ++k) {
+          const double ad = adj[(c * rows + n) * lw + k];
+          for (int a = 0; a < 3; ++a)
+            g[a] += ad * (w * (drad * dir[a] * Y[e * lw + k] + rad * dY[(e * lw + k) * 3 + a]));
+        }
+      }
+    }
+    for (int a = 0; a < 3; ++a) grad[3 * e + a] = g[a];
+  }
+  free(radii); free(cuts); free(lams); free(R); free(dR); free(Y); free(dY);
+}
+
 static double ipow(double b, int64_t e) {
   double v = 1.0;
   while (e > 0) { if (e & 1) v *= b; e >>= 1; if (e > 0) b *= b; }

@@ -74,16 +74,17 @@ const NormTable& norm_table();
 
 // Radial ChebExpCos values (and d/dr) for n = 0..n_max, same algebra as the
 // reference CPU core (ye3t_runtime_core.cpp:321-423) but one Chebyshev pass.
-// Value n goes to v[n * vs], its derivative to d[n].
+// Value n goes to v[n * vs], its derivative to d[n * ds].
 template <typename Real, bool WithDeriv, typename Out = Real>
-__device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max, Out* v, Out* d, int vs = 1) {
+__device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max, Out* v, Out* d, int vs = 1,
+                                      int ds = 1) {
   const Real pi = Real(3.141592653589793238462643383279502884);
   const Real rc = rc_in > Eps<Real>::value ? rc_in : Eps<Real>::value;
   const Real s = r / rc;
   if (s > Real(1)) {
     for (int n = 0; n <= n_max; ++n) {
       v[n * vs] = Out(0);
-      if (WithDeriv) d[n] = Out(0);
+      if (WithDeriv) d[n * ds] = Out(0);
     }
     return;
   }
@@ -95,7 +96,7 @@ __device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max,
   if (WithDeriv) d[0] = Out(0);
   if (n_max >= 1) {
     v[vs] = Out(Real(0.5) * (Real(1) + c));
-    if (WithDeriv) d[1] = Out(-Real(0.5) * pi * sn / rc);
+    if (WithDeriv) d[ds] = Out(-Real(0.5) * pi * sn / rc);
   }
   if (n_max >= 2) {
     const Real den = d_expm1(lam);
@@ -110,7 +111,7 @@ __device__ inline void cheb_exp_cos_row(Real r, Real rc_in, Real lam, int n_max,
       const Real t2 = Real(2) * x * t1 - t0;
       // derivative of T_n is n U_{n-1}; U_{n-1} is u1 here
       v[n * vs] = Out(Real(0.25) * (Real(1) - t2) * env);
-      if (WithDeriv) d[n] = Out(Real(0.25) * (-(Real(n) * u1) * dx * env + (Real(1) - t2) * denv));
+      if (WithDeriv) d[n * ds] = Out(Real(0.25) * (-(Real(n) * u1) * dx * env + (Real(1) - t2) * denv));
       t0 = t1;
       t1 = t2;
       const Real u2 = Real(2) * x * u1 - u0;

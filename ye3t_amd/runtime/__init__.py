@@ -36,6 +36,7 @@ REFERENCE_OPERATIONS = (
 )
 FUSED_OPERATIONS = (
     "ace_density_forward",
+    "ace_density_edge_gradient",
     "ace_product_forward",
     "ace_product_adjoint",
     "ace_product_linear",
@@ -176,6 +177,62 @@ def density_accumulate_adjoint(atomic_adjoint, centers, *, backend="auto"):
         if lo < 0 or hi >= int(atomic_adjoint.shape[0]):
             raise RuntimeError("density_accumulate_adjoint center index out of range")
     return native.density_accumulate_adjoint(atomic_adjoint.contiguous(), centers.contiguous())
+
+
+def _density_function():
+    import torch
+
+    class _Density(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, edge_vectors, row_offsets, neighbors, kw):
+            ctx.save_for_backward(edge_vectors, row_offsets, *(() if neighbors is None else (neighbors,)))
+            ctx.kw = kw
+            ctx.has_neighbors = neighbors is not None
+            return native.ace_density_forward(edge_vectors, row_offsets, neighbors, **kw)
+
+        @staticmethod
+        def backward(ctx, grad):
+            saved = ctx.saved_tensors
+            vec, offsets = saved[0], saved[1]
+            nbr = saved[2] if ctx.has_neighbors else None
+            kw = {k: v for k, v in ctx.kw.items() if k not in ("out_dtype", "accumulate_dtype", "out")}
+            g = grad.to(torch.float64 if grad.dtype == torch.float64 or vec.dtype == torch.float64 else grad.dtype)
+            return native.ace_density_edge_gradient(g, vec, offsets, nbr, validate=False, **kw), None, None, None
+
+    return _Density
+
+
+_DENSITY_FN = None
+
+
+def ace_density(edge_vectors, row_offsets, neighbors, *, atom_count, channel_count, n_max, l_max, cutoff, lam,
+                epsilon=1e-12, species=None, node_features=None, radial_mix=None, out_dtype=None,
+                accumulate_dtype=None):
+    """Fused stage 1 ``A[N, C, R, (l_max+1)^2]`` (``ye3t_hip_ace_density_forward``),
+    differentiable in ``edge_vectors``: the backward is the fused edge-vector
+    gradient (``ye3t_hip_ace_density_edge_gradient``), the force path of the
+    reference's chain (``scheduled_radial_angular_channels_with_derivative``,
+    ``execution_plan.py:7675``, then ``density_accumulate_adjoint``).
+    ``node_features`` and ``radial_mix`` are constants here (no gradient)."""
+    global _DENSITY_FN
+    _require_device(edge_vectors, "ace_density")
+    for t, n in ((node_features, "node_features"), (radial_mix, "radial_mix")):
+        if t is not None and t.requires_grad:
+            raise NotImplementedError(f"ace_density: no gradient with respect to {n}")
+    if _DENSITY_FN is None:
+        _DENSITY_FN = _density_function()
+    kw = dict(atom_count=int(atom_count), channel_count=int(channel_count), n_max=int(n_max), l_max=int(l_max),
+              cutoff=float(cutoff), lam=float(lam), epsilon=float(epsilon), species=species,
+              node_features=node_features, radial_mix=radial_mix, out_dtype=out_dtype,
+              accumulate_dtype=accumulate_dtype)
+    return _DENSITY_FN.apply(edge_vectors, row_offsets, neighbors, kw)
+
+
+def ace_density_edge_gradient(density_adjoint, edge_vectors, row_offsets, neighbors, **kw):
+    """Edge-vector gradient ``[E, 3]`` of ``<density_adjoint, A>`` for the fused
+    stage 1 (arguments as :func:`ace_density`)."""
+    _require_device(edge_vectors, "ace_density_edge_gradient")
+    return native.ace_density_edge_gradient(density_adjoint, edge_vectors, row_offsets, neighbors, **kw)
 
 
 def neighbor_list(positions, cutoff, *, backend="auto"):

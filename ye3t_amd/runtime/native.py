@@ -105,6 +105,7 @@ def lib():
     L.ye3t_hip_density_accumulate_csr.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _vp]
     L.ye3t_hip_density_accumulate_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _i64, _vp, _vp]
     L.ye3t_hip_ace_density_forward.argtypes = [ctypes.POINTER(DensityArgs), _vp, _vp]
+    L.ye3t_hip_ace_density_edge_gradient.argtypes = [ctypes.POINTER(DensityArgs), ctypes.c_int, _vp, _vp, _vp]
     L.ye3t_hip_symmetric_power_monomial.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
                                                     _vp, _vp]
     L.ye3t_hip_symmetric_power_monomial_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64,
@@ -189,6 +190,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_symmetric_power_shared_monomial_adjoint", "ye3t_hip_factorized_angular_segmented_plan_create",
     "ye3t_hip_factorized_angular_segmented_plan_destroy", "ye3t_hip_factorized_angular_segmented_plan_info",
     "ye3t_hip_factorized_angular_segmented_forward", "ye3t_hip_factorized_angular_segmented_adjoint",
+    "ye3t_hip_ace_density_edge_gradient",
 )
 
 
@@ -365,6 +367,59 @@ def ace_density_forward(edge_vectors, row_offsets, neighbors, *, atom_count, cha
         accumulate_dtype=-1 if accumulate_dtype is None else (F64 if accumulate_dtype == torch.float64 else F32))
     _check(lib().ye3t_hip_ace_density_forward(ctypes.byref(args), _dev(out, "A"), _stream()),
            "ye3t_hip_ace_density_forward")
+    return out
+
+
+def ace_density_edge_gradient(density_adjoint, edge_vectors, row_offsets, neighbors, *, atom_count, channel_count,
+                              n_max, l_max, cutoff, lam, epsilon=1e-12, species=None, node_features=None,
+                              radial_mix=None, validate=True):
+    """Edge-vector gradient ``[E, 3]`` of ``<density_adjoint, A(edge_vectors)>``
+    for the fused stage 1 with the same arguments as :func:`ace_density_forward`
+    (``ye3t_hip_ace_density_edge_gradient``).  ``density_adjoint`` has A's
+    shape; float64, or float32/float64 with float32 edge vectors.  The result
+    has the edge vectors' dtype."""
+    import torch
+
+    rows = 1 if radial_mix is not None else n_max + 1
+    shape = (atom_count, channel_count, rows, (l_max + 1) ** 2)
+    if tuple(density_adjoint.shape) != shape:
+        raise ValueError(f"density_adjoint must be {shape}")
+    if density_adjoint.dtype not in (torch.float32, torch.float64) or \
+            (density_adjoint.dtype == torch.float32 and edge_vectors.dtype == torch.float64):
+        raise ValueError("density_adjoint must be float64, or float32 with float32 edge vectors")
+    if row_offsets.dtype != torch.int64 or row_offsets.shape != (atom_count + 1,):
+        raise ValueError("row_offsets must be int64 [N+1]")
+    if edge_vectors.ndim != 2 or edge_vectors.shape[1] != 3:
+        raise ValueError("edge_vectors must be [E, 3]")
+    if neighbors is not None and neighbors.dtype != torch.int64:
+        raise ValueError("neighbors must be int64")
+    if species is not None and species.dtype != torch.int32:
+        raise ValueError("species must be int32")
+    if validate:
+        from ye3t_amd.runtime import validate_density_csr
+
+        validate_density_csr(row_offsets, neighbors, atom_count, int(edge_vectors.shape[0]), species=species,
+                             species_count=channel_count)
+    if node_features is not None and tuple(node_features.shape) != (atom_count, channel_count):
+        raise ValueError(f"node_features must be [{atom_count}, {channel_count}]")
+    if radial_mix is not None and tuple(radial_mix.shape) != (channel_count, n_max + 1):
+        raise ValueError(f"radial_mix must be [{channel_count}, {n_max + 1}]")
+    for t, n in ((node_features, "node_features"), (radial_mix, "radial_mix")):
+        if t is not None and t.dtype != edge_vectors.dtype:
+            raise ValueError(f"{n} must have dtype {edge_vectors.dtype}")
+    g = density_adjoint.contiguous()
+    vec = edge_vectors.contiguous()
+    out = torch.empty((int(vec.shape[0]), 3), dtype=vec.dtype, device=vec.device)
+    args = DensityArgs(
+        dtype=_dtype_code(edge_vectors), atom_count=int(atom_count), edge_count=int(edge_vectors.shape[0]),
+        row_offsets=_dev(row_offsets, "row_offsets"), neighbors=_opt(neighbors, "neighbors"),
+        edge_vectors=_dev(vec, "edge_vectors"), species=_opt(species, "species"),
+        node_features=_opt(node_features, "node_features"), radial_mix=_opt(radial_mix, "radial_mix"),
+        channel_count=int(channel_count), max_radial_index=int(n_max), max_angular=int(l_max),
+        cutoff=float(cutoff), lambda_=float(lam), epsilon=float(epsilon), out_dtype=-1, accumulate_dtype=-1)
+    _check(lib().ye3t_hip_ace_density_edge_gradient(ctypes.byref(args), _dtype_code(g), _dev(g, "density_adjoint"),
+                                                    _dev(out, "edge_gradient"), _stream()),
+           "ye3t_hip_ace_density_edge_gradient")
     return out
 
 
