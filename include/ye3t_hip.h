@@ -245,9 +245,12 @@ typedef struct ye3t_hip_product_plan ye3t_hip_product_plan;
 int ye3t_hip_product_plan_create(const ye3t_product_plan_desc* desc, ye3t_hip_product_plan** out);
 void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* plan);
 
-/* B[samples, feature_count] (out_dtype) from A[samples, a_width] (dtype).  Replaces the CUDA
- * factorized_angular forward (execution_plan_cuda.cu:6228-6358, launcher
- * :11488-11672; schema execution_plan_torch.cpp:7586-7594) for ACE products. */
+/* B[samples, feature_count] (out_dtype) from A[samples, a_width] (dtype) for a
+ * plan compiled by this backend (program words of ye3t_amd.ace.program).  It is
+ * the ACE-product form of the reference's factorized-angular forward
+ * (execution_plan_cuda.cu:6228-6358, launcher :11488-11672): one DAG for every
+ * content and target L of a configuration.  Callers holding the reference op's
+ * own DAG tables use ye3t_hip_factorized_angular_forward below. */
 int ye3t_hip_product_forward(const ye3t_hip_product_plan* plan, const void* A, int64_t samples, void* B,
                              ye3t_stream_t stream);
 
