@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 54 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 55 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -138,6 +138,19 @@ int ye3t_hip_ace_density_forward(const ye3t_density_args* args, void* A, ye3t_st
 /* Name of the kernel the last ye3t_hip_ace_density_forward call on this thread
  * launched ("" if none), for profiling.  No reference counterpart. */
 const char* ye3t_hip_last_density_kernel(void);
+
+/* Diagnostic, no reference counterpart: `workgroups` 64-thread workgroups each
+ * run `iterations` rounds of fp64 work -- mode 0: four independent
+ * v_mfma_f64_16x16x4f64 (8192 flops), 1: 64 fp64 FMAs per lane on 8 chains
+ * (8192 flops), 2: both in every wave, 3: the second half of the workgroups
+ * the MFMAs, the first half the FMAs -- and write one value per lane to
+ * out[workgroups * 64]: lane 0 of each wave its SIMD's identity
+ * ((XCC_ID << 32) | HW_ID, exact in a double), the others a sink value.
+ * At two workgroups per SIMD, mode 3 against modes 0 and 1 at one workgroup
+ * per SIMD shows whether a SIMD's matrix-core and vector fp64 work overlap
+ * (near the larger of the two) or take turns (near their sum), which bounds
+ * the fused density kernel. */
+int ye3t_hip_fp64_pipe_probe(int mode, int64_t workgroups, int iterations, double* out, ye3t_stream_t stream);
 
 /* Edge-vector gradient of the fused stage 1 (forces): edge_gradient[e, :] =
  * d <density_adjoint, A> / d edge_vectors[e, :] for density_adjoint shaped like

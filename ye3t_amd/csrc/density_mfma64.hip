@@ -327,9 +327,16 @@ __global__ __launch_bounds__(64) void ace_density_mfma64_kernel(Density64Params<
 //            see g), which keeps the wave at 12.6 KB of LDS;
 //   phase 2  one MFMA per k-block of four edges.  A full chunk whose atom ends
 //            all fall on k-block boundaries, with every atom holding at least
-//            one k-block, runs as 16 unmasked MFMAs with a scalar test for an
-//            atom end after each; any other chunk masks each k-block per lane
-//            by atom and splits the k-blocks that straddle an atom boundary.
+//            one k-block and at most P (4, or 2 for an fp64 density) atoms
+//            ending in it, runs as 16 unmasked MFMAs with a scalar test for an
+//            atom end after each; the rows of those atoms wait in registers
+//            and are stored at the start of the next chunk.  Any other chunk
+//            masks each k-block per lane by atom, splits the k-blocks that
+//            straddle an atom boundary and stores rows as atoms end.
+// On gfx950 the fp64 MFMAs and the fp64 VALU instructions of one SIMD take
+// turns on the same fp64 pipe (a wave of MFMAs and a wave of FMAs sharing a
+// SIMD take the sum of their separate times), so the basis math is not hidden
+// under the matrix-core phase: the kernel's bound is the sum of the two.
 // Atom ends come from a vector window of 64 CSR offsets (v_readlane), so the
 // MFMA loop issues no scalar loads.  The next chunk's loads (two register
 // sets, alternating) are issued after one wait for everything issued a chunk
@@ -493,6 +500,46 @@ __global__ __launch_bounds__(64) void ace_density_channel16_kernel(Density64Para
     }
   };
   auto clamp_edge = [&](int64_t e) { return e < e_end ? e : e_end - 1; };
+  // Rows of the atoms a fast chunk completes are held in registers and stored
+  // at the start of the next chunk, after its wait and ahead of its loads: the
+  // next wait then finds those stores issued a whole chunk earlier (loads and
+  // stores share one in-order counter).
+  constexpr int P = sizeof(Out) == 4 ? 4 : 2;
+  Out held[P][4];
+  int held_atom[P];
+  int nheld = 0;
+#pragma unroll
+  for (int s = 0; s < P; ++s) held_atom[s] = 0;
+  auto hold_atom = [&]() {
+#pragma unroll
+    for (int s = 0; s < P; ++s)
+      if (s == nheld) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) held[s][v] = Out(acc[v]);
+        held_atom[s] = a;
+      }
+    ++nheld;
+    acc = mfma_d4{0.0, 0.0, 0.0, 0.0};
+    ++a;
+    lo = hi;
+    if (a >= na) {
+      hi = 0x7fffffff;
+    } else if (a - wb < 64) {
+      hi = __builtin_amdgcn_readlane(offw, a - wb);
+    } else {
+      hi = int(offset_at(p.offsets, a_begin + a + 1) - e_begin);
+    }
+  };
+  auto flush = [&]() {
+#pragma unroll
+    for (int s = 0; s < P; ++s)
+      if (s < nheld) {
+        Out* __restrict__ dst = Aw + int64_t(held_atom[s]) * (C * LW);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) __builtin_nontemporal_store(held[s][v], dst + 64 * v);
+      }
+    nheld = 0;
+  };
 
   // Software pipeline, two chunks per trip with two register sets: on entry
   // to a chunk the lane holds the vector and the feature row of its edge of
@@ -523,6 +570,7 @@ __global__ __launch_bounds__(64) void ace_density_channel16_kernel(Density64Para
     // waits for loads that are still in flight (the in-order counter cannot
     // tell them apart once a variable number of stores sits in between).
     wait_vmem_all();
+    flush();
     // the next chunk's vector and feature row, the neighbour index one further,
     // and the offsets window from the current atom on
     {
@@ -618,8 +666,10 @@ __global__ __launch_bounds__(64) void ace_density_channel16_kernel(Density64Para
       const int d = a - wb;
       const int prev = __shfl_up(offw, 1);
       const int start = lane == d ? lo : prev;
-      const bool bad = lane >= d && offw > c0 && offw < c0 + 64 && ((offw & 3) != 0 || offw - start < 4);
-      fast = __ballot(bad) == 0;
+      const bool inside = lane >= d && wb + lane < na && offw > c0;
+      const bool bad = inside && offw < c0 + 64 && ((offw & 3) != 0 || offw - start < 4);
+      const bool ends = inside && offw <= c0 + 64;
+      fast = __ballot(bad) == 0 && __popcll(__ballot(ends)) <= P;
     }
     // B operands are read from Yt one tile (four k-blocks) ahead of their MFMAs
     double yq[2][4];
@@ -633,7 +683,7 @@ __global__ __launch_bounds__(64) void ace_density_channel16_kernel(Density64Para
           for (int v = 0; v < 4; ++v) yq[((j >> 2) + 1) & 1][v] = Yt[cc * YP + 4 * (j + 4 + v) + kq];
         }
         acc = __builtin_amdgcn_mfma_f64_16x16x4f64(wv[j], yq[(j >> 2) & 1][j & 3], acc, 0, 0, 0);
-        if (hi == c0 + 4 * j + 4) next_atom();
+        if (hi == c0 + 4 * j + 4) hold_atom();
       }
     } else {
       const int nkb = (cnt + 3) >> 2;
@@ -662,6 +712,7 @@ __global__ __launch_bounds__(64) void ace_density_channel16_kernel(Density64Para
     if (c0 + 64 >= span) break;
     chunk(c0 + 64, vxB, vyB, vzB, hB, vxA, vyA, vzA, hA);
   }
+  flush();
   // atoms after the last edge (no edges of their own) get zero rows
   for (; a < na; ++a) store_atom(a);
 }

@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 54
+ABI_VERSION = 55
 _LIB = None
 
 F32, F64 = 0, 1
@@ -106,6 +106,7 @@ def lib():
     L.ye3t_hip_density_accumulate_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _i64, _vp, _vp]
     L.ye3t_hip_ace_density_forward.argtypes = [ctypes.POINTER(DensityArgs), _vp, _vp]
     L.ye3t_hip_ace_density_edge_gradient.argtypes = [ctypes.POINTER(DensityArgs), ctypes.c_int, _vp, _vp, _vp]
+    L.ye3t_hip_fp64_pipe_probe.argtypes = [ctypes.c_int, _i64, ctypes.c_int, _vp, _vp]
     L.ye3t_hip_symmetric_power_monomial.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
                                                     _vp, _vp]
     L.ye3t_hip_symmetric_power_monomial_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64,
@@ -177,6 +178,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_product_plan_create", "ye3t_hip_product_plan_destroy", "ye3t_hip_product_forward",
     "ye3t_hip_product_launch_info", "ye3t_hip_rtc_compile", "ye3t_hip_free",
     "ye3t_hip_product_plan_attach_generated", "ye3t_hip_product_plan_select", "ye3t_hip_last_density_kernel",
+    "ye3t_hip_fp64_pipe_probe",
     "ye3t_hip_density_accumulate_adjoint", "ye3t_hip_product_plan_attach_readout", "ye3t_hip_product_linear_forward",
     "ye3t_hip_rows_dot", "ye3t_hip_product_plan_attach_adjoint", "ye3t_hip_product_adjoint",
     "ye3t_hip_neighbor_workspace_bytes", "ye3t_hip_neighbor_count", "ye3t_hip_neighbor_fill",
@@ -426,6 +428,19 @@ def ace_density_edge_gradient(density_adjoint, edge_vectors, row_offsets, neighb
 def last_density_kernel():
     """Kernel launched by the last ``ace_density_forward`` call on this thread."""
     return lib().ye3t_hip_last_density_kernel().decode()
+
+
+def fp64_pipe_probe(mode, workgroups, iterations, out):
+    """Launch the fp64 pipe probe (diagnostic, no reference counterpart) on
+    torch's current stream: mode 0 MFMAs, 1 FMAs, 2 both per wave, 3 split
+    between odd and even workgroups; ``out`` is a float64 device tensor of at
+    least ``workgroups * 64`` elements."""
+    import torch
+
+    if out.dtype != torch.float64 or out.numel() < workgroups * 64:
+        raise ValueError("out must be float64 with workgroups * 64 elements")
+    _check(lib().ye3t_hip_fp64_pipe_probe(int(mode), int(workgroups), int(iterations), _dev(out, "out"), _stream()),
+           "ye3t_hip_fp64_pipe_probe")
 
 
 def _host_i64(a):
