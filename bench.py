@@ -405,7 +405,7 @@ def main():
     ap.add_argument("--max-slots", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--kernel", default="auto", choices=["auto", "generated", "interpreter"])
+    ap.add_argument("--kernel", default="auto", choices=["auto", "generated", "parts", "interpreter"])
     ap.add_argument("--op", default="pipeline",
                     choices=["pipeline", "linear_readout", "density_accumulate_adjoint", "product_adjoint",
                              "neighbor_list", "density_edge_gradient", "fp64_pipe"],
@@ -496,6 +496,9 @@ def main():
     c1, c2 = as_built_bytes(cfg, pipe.plan, elem, a_elem)
     if pipe.kernel == "generated":
         k2 = "ye3t_product_generated"
+    elif pipe.kernel == "parts":
+        # the stage-2 time includes the column-major copy of the density the parts read
+        k2 = "transpose_kernel+ye3t_product_part" if pipe._columns else "ye3t_product_part"
     elif pipe.handle.uses_stream:
         # the stage-2 time includes the column-major copy of the density it reads
         k2 = "transpose_kernel+product_stream_kernel" if pipe._columns else "product_stream_kernel"

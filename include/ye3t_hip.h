@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 55 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 56 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -288,6 +288,25 @@ int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* plan, const vo
                                            const char* kernel_name, int64_t chunk_count, int64_t rows_per_tile,
                                            int persistent, int threads_per_block);
 
+/* Attach a plan-specialised kernel in `part_count` parts, for plans whose
+ * generated code is too large to compile as one kernel: part i is the code
+ * object codes[i] (sizes[i] bytes, from ye3t_hip_rtc_compile of
+ * ye3t_amd/ace/codegen.py:generate_parts output) with kernel kernel_names[i],
+ * which computes chunk_counts[i] consecutive output chunks of the plan.
+ * product_forward and product_forward_columns then launch the parts in order
+ * on their stream, each with 64 threads per workgroup and grid
+ * (ceil(samples / 64), chunk_counts[i]); the kernel signature is
+ * (const T* A, long samples, U* B, long row_stride, long col_stride), density
+ * value (s, k) at A[s * row_stride + k * col_stride]: (a_width, 1) for the
+ * row-major density, (1, ld) for its column-major copy.  Replaces earlier
+ * parts; a kernel attached with ye3t_hip_product_plan_attach_generated takes
+ * precedence in product_forward.  No
+ * reference counterpart (the reference runs such plans on its generic DAG
+ * executor, execution_plan_cuda.cu:11584-11589). */
+int ye3t_hip_product_plan_attach_generated_parts(ye3t_hip_product_plan* plan, int64_t part_count,
+                                                 const void* const* codes, const int64_t* sizes,
+                                                 const char* const* kernel_names, const int64_t* chunk_counts);
+
 /* Attach a plan-specialised fused linear readout kernel (code object of
  * ye3t_amd/ace/codegen.py:generate_readout compiled with ye3t_hip_rtc_compile).
  * Kernel signature (const T* A, long samples, U* out, const T* W, T bias), T =
@@ -372,15 +391,16 @@ int ye3t_hip_transpose(int dtype, const void* A, int64_t rows, int64_t cols, voi
 /* ye3t_hip_product_forward on a column-major density At [a_width, ld]
  * (element (s, col) at At[col * ld + s]; ld >= samples rounded up to 64):
  * the interpreter reads each density column of 64 samples as one contiguous
- * block.  For plans run by the term-stream interpreter (workspace byte offsets
- * within 16 bits); YE3T_EINVAL otherwise.  Same results as
+ * block.  For plans with generated parts attached, or run by the term-stream
+ * interpreter (workspace byte offsets within 16 bits); YE3T_EINVAL otherwise.
+ * Same results as
  * ye3t_hip_product_forward on the row-major density.  Replaces the same
  * reference ops as ye3t_hip_product_forward. */
 int ye3t_hip_product_forward_columns(const ye3t_hip_product_plan* plan, const void* At, int64_t ld,
                                      int64_t samples, void* B, ye3t_stream_t stream);
 
-/* Select which kernel product_forward launches: 0 = generated (if attached),
- * 1 = generic interpreter. */
+/* Select which kernel product_forward launches: 0 = generated (if attached,
+ * whole or in parts), 1 = generic interpreter. */
 int ye3t_hip_product_plan_select(ye3t_hip_product_plan* plan, int use_interpreter);
 
 /* Host only (no device work): the term stream a plan description would run.

@@ -245,7 +245,9 @@ def _species_rank4_spec():
     (4, "f32", 1000, None, "interpreter"), (4, "f64", 333, None, "interpreter"), (4, "f32", 63, 250, "interpreter"),
     (4, "f32", 130, 48, "interpreter"), (2, "f64", 200, None, "interpreter"), (3, "f32", 100, None, "interpreter"),
     (3, "f64", 70, None, "interpreter"), (4, "f32", 1000, None, "generated"), (4, "f64", 333, None, "generated"),
-    (4, "f32", 63, None, "generated"), (4, "f32", 65, None, "generated")])
+    (4, "f32", 63, None, "generated"), (4, "f32", 65, None, "generated"), (2, "f64", 200, None, "parts"),
+    (2, "f64", 65, None, "parts"), (3, "f32", 100, None, "parts"), (3, "f64", 70, None, "parts"),
+    (4, "f32", 1000, None, "parts"), (4, "f64", 1, None, "parts")])
 def test_product_kernel_vs_flat_oracle(gpu, cid, dtype, samples, max_slots, kernel):
     flush(f"product config {cid} {dtype} samples={samples} slots={max_slots} kernel={kernel}")
     import torch
@@ -299,6 +301,29 @@ def test_interpreter_column_major_density(gpu, cid, dtype, samples, max_slots):
     err = column_rel_error(B_rows.cpu().numpy(), ref)
     flush(f"  err {err:.3e}")
     assert err < TOL[dtype]
+
+
+def test_parts_and_interpreter_agree_on_config2(gpu):
+    """Config 2's full plan (16 810 terms) at its full 10 000 samples: the
+    generated kernel in parts (the default for this plan size) against the
+    term-stream interpreter, and against the flat oracle on a slice."""
+    flush("generated parts vs interpreter, config 2 full sample count")
+    import torch
+
+    cfg = W.config(2)
+    pipe = ACEPipeline(cfg.feature_spec, "f64")
+    assert pipe.kernel == "parts" and len(pipe.handle.generated_parts) > 1
+    A = torch.as_tensor(np.random.default_rng(21).normal(size=(10000, pipe.plan.a_width)), device=gpu)
+    B_parts = pipe.product(A)
+    pipe.handle.select(use_interpreter=True)
+    B_int = pipe.handle.forward(A)
+    pipe.handle.select(use_interpreter=False)
+    torch.cuda.synchronize()
+    err = column_rel_error(B_parts.cpu().numpy(), B_int.cpu().numpy())
+    flush(f"  parts vs interpreter {err:.3e}")
+    assert err < TOL["f64"]
+    ref = oracle.ace_product_flat(A[:96].cpu().numpy(), pipe.plan.flat_arrays())
+    assert column_rel_error(B_parts[:96].cpu().numpy(), ref) < TOL["f64"]
 
 
 def test_generated_and_interpreter_agree_on_config4(gpu):
@@ -475,7 +500,7 @@ def test_rows_dot(gpu, dtype):
         assert np.max(np.abs(got - ref)) / scale < (1e-13 if dtype == "f64" else 1e-6)
 
 
-@pytest.mark.parametrize("kernel", ["interpreter", "generated"])
+@pytest.mark.parametrize("kernel", ["interpreter", "generated", "parts"])
 def test_fp64_plan_with_fp32_features(gpu, kernel):
     """accumulate=f64 with f32 storage: only the final store rounds."""
     flush(f"mixed precision product, kernel {kernel}")

@@ -103,3 +103,30 @@ def test_rank_four_and_species_program():
     A = np.random.default_rng(2).normal(size=(9, plan.a_width))
     np.testing.assert_allclose(emulate(prog, A), oracle.ace_product_flat(A, plan.flat_arrays()),
                                rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("max_live,per", [(16, 1), (24, 3), (1 << 30, 4)])
+def test_generated_parts_cover_the_outputs_in_order(max_live, per):
+    """``codegen.generate_parts``: consecutive parts hand over at chunk
+    boundaries, cover every output once, and a part's kernel switches over its
+    own chunks and writes only its columns (never the whole-row tile store of
+    a one-chunk plan)."""
+    import re
+
+    from ye3t_amd.ace import codegen
+
+    plan = ProductPlan(W.config(4).feature_spec)
+    chunks = codegen._chunks(plan, max_live)
+    parts = codegen.generate_parts(plan, "f64", max_live=max_live, chunks_per_part=per, out_dtype="f32")
+    assert len(parts) == -(-len(chunks) // per)
+    assert sum(m["chunks"] for _, m in parts) == len(chunks)
+    first = 0
+    for k, (src, meta) in enumerate(parts):
+        assert meta["first_output"] == first and meta["kernel"] == "ye3t_product_part"
+        lo, hi = meta["first_output"], meta["last_output"]
+        assert (lo, hi) == (chunks[k * per][0], chunks[min(len(chunks), (k + 1) * per) - 1][1])
+        assert src.count("  case ") == meta["chunks"] and "switch (blockIdx.y)" in src
+        cols = [int(g) for g in re.findall(r"B\[\(s0 \+ r\) \* \d+L \+ (\d+) \+ c\]", src)]
+        assert cols and min(cols) == lo and max(cols) < hi
+        first = hi
+    assert first == plan.feature_count

@@ -509,7 +509,7 @@ def generate_adjoint(plan, dtype="f64", grad_dtype=None, kernel_name="ye3t_produ
 
 
 def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generated", out_dtype=None, rows=None,
-             in_dtype=None):
+             in_dtype=None, chunks=None, strided=False, group=GROUP):
     """Return ``(source, meta)`` for a specialised product kernel.
 
     ``dtype`` is the type of ``A`` and of the arithmetic, ``out_dtype`` (default
@@ -517,6 +517,12 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     default :func:`tile_rows`) is the number of samples a 64-lane workgroup
     produces; lanes past it idle.  ``in_dtype`` (default ``dtype``) is the
     storage type of ``A`` ("f32" with an "f64" plan: converted as loaded).
+    ``chunks`` (default: the plan's chunks at ``max_live``) restricts the
+    kernel to those output chunks, one per grid row, with 64-sample tiles
+    (see :func:`generate_parts`).  ``strided``: the kernel takes two more
+    arguments ``(row_stride, col_stride)`` and reads density value ``(s, k)``
+    at ``A[s * row_stride + k * col_stride]``, so one code object serves the
+    row-major density and its column-major copy.
     """
     out_dtype = out_dtype or dtype
     in_dtype = _check_in_dtype(dtype, in_dtype)
@@ -528,7 +534,10 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     if max_live is None:
         max_live = 1 << 30  # one chunk unless asked otherwise
     nodes = plan.nodes
-    chunks = _chunks(plan, max_live)
+    # a kernel restricted to given chunks always uses 64-row tiles and writes its columns only
+    single = chunks is None
+    if chunks is None:
+        chunks = _chunks(plan, max_live)
     F = plan.feature_count
     out = []
     w = out.append
@@ -537,8 +546,12 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     w(f"#define OUT {outt}")
     w(f"#define AIN {_ctype(in_dtype)}")
     w(f"extern \"C\" __global__ __launch_bounds__(64) void {kernel_name}(")
-    w("    const AIN* __restrict__ A, long samples, OUT* __restrict__ B) {")
-    single = len(chunks) == 1
+    if strided:
+        # density value (s, k) at A[s * row_stride + k * col_stride]: rows (a_width, 1) or columns (1, ld)
+        w("    const AIN* __restrict__ A, long samples, OUT* __restrict__ B, long row_stride, long col_stride) {")
+    else:
+        w("    const AIN* __restrict__ A, long samples, OUT* __restrict__ B) {")
+    single = single and len(chunks) == 1
     R = tile_rows(F, out_dtype, rows) if single else 64
     if not 1 <= R <= 64:
         raise ValueError("rows per tile must be in [1, 64]")
@@ -546,12 +559,15 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     if single:
         w(f"  __shared__ __attribute__((aligned(16))) OUT st[{R} * {pitch}];")
     else:
-        w(f"  __shared__ OUT st[{GROUP}][65];")
+        w(f"  __shared__ OUT st[{group}][65];")
     w("  const int lane = threadIdx.x;")
     w(f"  const long s0 = (long)blockIdx.x * {R};")
     w("  const long s = s0 + lane;")
     w(f"  const bool valid = lane < {R} && s < samples;")
-    w(f"  const AIN* __restrict__ a = A + (valid ? s : 0) * {plan.a_width}L;")
+    if strided:
+        w("  const AIN* __restrict__ a = A + (valid ? s : 0) * row_stride;")
+    else:
+        w(f"  const AIN* __restrict__ a = A + (valid ? s : 0) * {plan.a_width}L;")
     w("  const long rem = samples - s0;")
     w(f"  const int rows = rem < {R} ? (int)rem : {R};")
     w("  switch (blockIdx.y) {")
@@ -568,7 +584,8 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
             emitted.add(n)
             if nd["kind"] == "leaf":
                 for c in range(nd["dim"]):
-                    w(f"    const REAL v{n}_{c} = valid ? (REAL)a[{nd['a_offset'] + c}] : (REAL)0;")
+                    at = f"{nd['a_offset'] + c}L * col_stride" if strided else f"{nd['a_offset'] + c}"
+                    w(f"    const REAL v{n}_{c} = valid ? (REAL)a[{at}] : (REAL)0;")
                 return
             per = [[] for _ in range(nd["dim"])]
             if nd["kind"] == "sym":
@@ -600,6 +617,10 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
                     expr = f"{head} * ({inner})" if expr is None else f"{fma}({head}, {inner}, {expr})"
                 w(f"    const REAL v{n}_{c} = {expr};")
 
+        if strided:
+            # every density value of the chunk requested up front (independent loads in flight together)
+            for n in sorted((m for m in members if nodes[m]["kind"] == "leaf"), key=lambda m: nodes[m]["a_offset"]):
+                emit(n)
         if single:
             for f in range(first, last):
                 root, comp = plan.outputs[f]
@@ -613,8 +634,8 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
             w("    break;")
             w("  }")
             continue
-        for g0 in range(first, last, GROUP):
-            g1 = min(g0 + GROUP, last)
+        for g0 in range(first, last, group):
+            g1 = min(g0 + group, last)
             for f in range(g0, g1):
                 root, comp = plan.outputs[f]
                 emit(root)
@@ -633,6 +654,38 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     w("}")
     source = "\n".join(out) + "\n"
     meta = {"kernel": kernel_name, "chunks": len(chunks), "rows": R, "feature_count": F, "a_width": plan.a_width,
-            "dtype": dtype, "out_dtype": out_dtype, "in_dtype": in_dtype,
+            "dtype": dtype, "out_dtype": out_dtype, "in_dtype": in_dtype, "first_output": chunks[0][0],
+            "last_output": chunks[-1][1], "strided": bool(strided),
             "hash": hashlib.sha256(source.encode()).hexdigest()[:16]}
     return source, meta
+
+
+# node values per chunk of a generated part and chunks per part: config 2 (fp64)
+# measured 166 us at (400, 6) against 447 us at (96, 16) and 270 us at (256, 4);
+# larger chunks re-read fewer density columns and recompute fewer shared nodes
+PART_MAX_LIVE = 400
+PART_CHUNKS = 6
+
+
+def generate_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per_part=PART_CHUNKS, out_dtype=None,
+                   in_dtype=None, group=GROUP):
+    """``[(source, meta), ...]``: the plan's generated product kernel cut into
+    parts of ``chunks_per_part`` consecutive output chunks (each chunk holds
+    at most ``max_live`` node values), for plans whose code is too large for
+    one hipRTC module (compile time grows faster than the code: 221 s for
+    config 2's 16 810 terms as one kernel at 126 chunks, ~5 s per 6-chunk
+    part of 400-value chunks).  Part i
+    writes columns ``[meta["first_output"], meta["last_output"])`` of B; the
+    parts run in order (``ye3t_hip_product_plan_attach_generated_parts``) and
+    read the density through row and column strides (``strided``), so the
+    column-major copy the interpreter reads serves them too: a leaf of 64
+    samples is then one contiguous 512-byte load instead of 64 cache lines."""
+    if chunks_per_part < 1:
+        raise ValueError("chunks_per_part must be positive")
+    chunks = _chunks(plan, max_live)
+    parts = []
+    for i in range(0, len(chunks), chunks_per_part):
+        parts.append(generate(plan, dtype, max_live, kernel_name="ye3t_product_part", out_dtype=out_dtype,
+                              in_dtype=in_dtype, chunks=chunks[i:i + chunks_per_part], strided=True,
+                              group=group))
+    return parts

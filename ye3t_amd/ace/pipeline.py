@@ -35,6 +35,9 @@ def to_device_inputs(inp, dtype, device="cuda"):
 # plans up to this many DAG terms get a plan-specialised (generated) kernel;
 # larger plans run the generic interpreter (hipRTC time grows with code size)
 GENERATED_MAX_TERMS = 5000
+# plans up to this size run on a generated kernel in parts (one hipRTC module per
+# 16 chunks, compiled in parallel and cached); larger ones on the interpreter
+PARTS_MAX_TERMS = 200000
 
 
 class ACEPipeline:
@@ -51,8 +54,10 @@ class ACEPipeline:
     once to fp32 for storage (half the density bytes) and converts it back to
     fp64 for the product; this needs a plan with a generated product kernel.
 
-    ``kernel``: "auto" (generated kernel when the plan is small enough),
-    "generated" or "interpreter" (the generic table-driven product kernel)."""
+    ``kernel``: "auto" (a generated kernel when the plan has at most
+    ``GENERATED_MAX_TERMS`` terms, a generated kernel in parts up to
+    ``PARTS_MAX_TERMS``, else the interpreter), "generated", "parts" or
+    "interpreter" (the generic table-driven product kernel)."""
 
     def __init__(self, feature_spec, dtype="f32", max_slots=None, plan=None, kernel="auto", max_live=None,
                  accumulate=None, density=None):
@@ -65,14 +70,15 @@ class ACEPipeline:
             raise ValueError(f"unsupported precision: dtype {dtype!r}, accumulate {accumulate!r}")
         if self.density_dtype not in ("f32", "f64") or (self.accumulate == "f32" and self.density_dtype == "f64"):
             raise ValueError(f"unsupported density dtype {density!r} for {self.accumulate} arithmetic")
-        if kernel not in {"auto", "generated", "interpreter"}:
+        if kernel not in {"auto", "generated", "parts", "interpreter"}:
             raise ValueError(f"unknown product kernel {kernel!r}")
         self.plan = plan if plan is not None else ProductPlan(feature_spec)
         terms = sum(len(nd.get("terms", ())) for nd in self.plan.nodes)
         use_gen = kernel == "generated" or (kernel == "auto" and terms <= GENERATED_MAX_TERMS)
-        if self.density_dtype != self.accumulate and not use_gen:
+        use_parts = kernel == "parts" or (kernel == "auto" and not use_gen and terms <= PARTS_MAX_TERMS)
+        if self.density_dtype != self.accumulate and not (use_gen or use_parts):
             raise ValueError(f"a {self.density_dtype} density with {self.accumulate} arithmetic needs a generated "
-                             f"product kernel (plans of at most {GENERATED_MAX_TERMS} terms)")
+                             f"product kernel (plans of at most {PARTS_MAX_TERMS} terms)")
         self.program = compile_program(self.plan, self.accumulate, max_slots)
         self.handle = native.ProductPlanHandle(self.program, out_dtype=dtype, in_dtype=self.density_dtype)
         self._columns = os.environ.get("YE3T_PRODUCT_COLUMNS", "1") != "0"
@@ -103,6 +109,17 @@ class ACEPipeline:
                                         rows=int(rows) if rows else None, in_dtype=self.density_dtype)
             self.handle.attach_generated(source, meta)
             self.kernel = "generated"
+        elif use_parts:
+            from ye3t_amd.ace.codegen import PART_CHUNKS, PART_MAX_LIVE, generate_parts
+
+            # node values per chunk and chunks per part (tuning)
+            live = int(os.environ.get("YE3T_PARTS_MAX_LIVE", PART_MAX_LIVE))
+            per = int(os.environ.get("YE3T_PARTS_CHUNKS", PART_CHUNKS))
+            group = int(os.environ.get("YE3T_PARTS_GROUP", 32))  # output columns per staged store
+            self.handle.attach_generated_parts(generate_parts(self.plan, self.accumulate, max_live=live,
+                                                              chunks_per_part=per, out_dtype=dtype,
+                                                              in_dtype=self.density_dtype, group=group))
+            self.kernel = "parts"
 
     @property
     def feature_count(self):
@@ -125,11 +142,12 @@ class ACEPipeline:
             accumulate_dtype=torch.float64 if self.accumulate == "f64" else torch.float32, validate=validate)
 
     def product(self, A_rows, out=None):
-        """B-features of the density rows.  Interpreter plans read a column-major
-        copy of the density (each density column of 64 samples is one contiguous
-        block for the interpreter's loads); ``YE3T_PRODUCT_COLUMNS=0`` reads the
-        rows directly."""
-        if self.kernel == "interpreter" and self.handle.uses_stream and self._columns:
+        """B-features of the density rows.  Interpreter plans and generated
+        parts read a column-major copy of the density (each density column of
+        64 samples is one contiguous block for their loads);
+        ``YE3T_PRODUCT_COLUMNS=0`` reads the rows directly."""
+        columns = self.kernel == "parts" or (self.kernel == "interpreter" and self.handle.uses_stream)
+        if columns and self._columns:
             S = int(A_rows.shape[0])
             ld = (S + 63) // 64 * 64
             key = (int(A_rows.shape[1]), ld, A_rows.dtype, A_rows.device)

@@ -1,0 +1,63 @@
+"""Compile the generated product kernels of benchmark configurations ahead of use.
+
+Plans between ``GENERATED_MAX_TERMS`` and ``PARTS_MAX_TERMS`` terms run on a
+generated kernel in parts (``codegen.generate_parts``), one hipRTC module per
+16 chunks: about half a minute for config 2 and a few minutes for config 3 on
+8 cores.  hipRTC needs no GPU, so this runs on a build host; the code objects
+land in the JIT cache (``ye3t_amd/jit_cache`` unless ``YE3T_AMD_JIT_CACHE`` says
+otherwise), keyed by source hash, and travel with the tree.
+
+    python -m ye3t_amd.ace.prebuild            # configs 2 and 3, every dtype they are benchmarked in
+    python -m ye3t_amd.ace.prebuild 2 --dtype f64
+"""
+
+import argparse
+import os
+import sys
+import time
+from concurrent.futures import ThreadPoolExecutor
+
+
+def precisions(cfg, dtype):
+    """(accumulate, density) of ``dtype`` storage, as ``bench.py`` and the tests choose them."""
+    accumulate = (cfg.accumulate if dtype == "f32" else None) or dtype
+    density = (cfg.density_dtype if dtype == "f32" and accumulate == cfg.accumulate else None) or accumulate
+    return accumulate, density
+
+
+def prebuild(config_ids=(2, 3), dtypes=None, workers=None, log=print):
+    from ye3t_amd.ace import workloads as W
+    from ye3t_amd.ace.codegen import generate_parts
+    from ye3t_amd.ace.pipeline import GENERATED_MAX_TERMS, PARTS_MAX_TERMS
+    from ye3t_amd.ace.plan import ProductPlan
+    from ye3t_amd.runtime import native
+
+    workers = workers or min(16, os.cpu_count() or 1)
+    for cid in config_ids:
+        cfg = W.config(cid)
+        plan = ProductPlan(cfg.feature_spec)
+        terms = sum(len(nd.get("terms", ())) for nd in plan.nodes)
+        if not GENERATED_MAX_TERMS < terms <= PARTS_MAX_TERMS:
+            log(f"config {cid}: {terms} terms, not a parts plan; skipped")
+            continue
+        for dtype in dtypes or cfg.dtypes:
+            accumulate, density = precisions(cfg, dtype)
+            parts = generate_parts(plan, accumulate, out_dtype=dtype, in_dtype=density)
+            t0 = time.time()
+            with ThreadPoolExecutor(workers) as pool:
+                list(pool.map(lambda part: native.rtc_compile(part[0]), parts))
+            log(f"config {cid} {dtype} (arithmetic {accumulate}, density {density}): {len(parts)} parts "
+                f"in {time.time() - t0:.1f} s -> {native._jit_cache_dir()}")
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("configs", nargs="*", type=int, default=[2, 3])
+    ap.add_argument("--dtype", action="append", help="storage dtype (default: every dtype of the config)")
+    ap.add_argument("--workers", type=int, default=None)
+    args = ap.parse_args(argv)
+    prebuild(args.configs, args.dtype, args.workers)
+
+
+if __name__ == "__main__":
+    sys.exit(main())

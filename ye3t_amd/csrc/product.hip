@@ -46,6 +46,18 @@ struct ye3t_hip_product_plan {
   int64_t generated_rows;  // samples per workgroup tile of the generated kernel
   int generated_threads;   // threads per workgroup of the generated kernel
   int64_t generated_max_grid;  // persistent kernel: workgroups resident at once (0: not persistent)
+  // plan-specialised kernel in parts (plans too large for one module): part i
+  // computes part_chunks[i] consecutive chunks, one per grid row, 64-row tiles
+  int64_t part_count;
+  hipModule_t* part_modules;
+  hipFunction_t* part_fns;
+  int64_t* part_chunks;
+  // the parts run concurrently on part_lanes streams of the plan, forked from
+  // and joined back to the caller's stream with events (1: the caller's stream only)
+  int part_lanes;
+  hipStream_t part_streams[4];
+  hipEvent_t part_fork;
+  hipEvent_t part_join[4];
   int use_interpreter;
   // plan-specialised fused linear readout (optional)
   hipModule_t readout_module;
@@ -1218,6 +1230,36 @@ int ye3t_hip_transpose(int dtype, const void* A, int64_t rows, int64_t cols, voi
   return check_launch("transpose_kernel");
 }
 
+// the generated kernel in parts, in order: density value (s, k) at A[s * row_stride + k * col_stride]
+static int launch_parts(const ye3t_hip_product_plan* p, const void* A, int64_t row_stride, int64_t col_stride,
+                        int64_t samples, void* B, hipStream_t stream) {
+  const int64_t tiles = (samples + kLanes - 1) / kLanes;
+  YE3T_REQUIRE(tiles <= int64_t(0x7FFFFFFF), "too many samples for one launch");
+  long s_arg = long(samples), rs_arg = long(row_stride), cs_arg = long(col_stride);
+  const void* a_arg = A;
+  void* b_arg = B;
+  void* args[] = {&a_arg, &s_arg, &b_arg, &rs_arg, &cs_arg};
+  const int lanes = p->part_lanes;
+  if (lanes <= 1) {
+    for (int64_t i = 0; i < p->part_count; ++i)
+      YE3T_CHECK_HIP(hipModuleLaunchKernel(p->part_fns[i], unsigned(tiles), unsigned(p->part_chunks[i]), 1, kLanes,
+                                           1, 1, 0, stream, args, nullptr));
+    return YE3T_OK;
+  }
+  // fork: the plan's streams start after the caller's prior work; join: the
+  // caller's stream continues after every part
+  YE3T_CHECK_HIP(hipEventRecord(p->part_fork, stream));
+  for (int k = 0; k < lanes; ++k) YE3T_CHECK_HIP(hipStreamWaitEvent(p->part_streams[k], p->part_fork, 0));
+  for (int64_t i = 0; i < p->part_count; ++i)
+    YE3T_CHECK_HIP(hipModuleLaunchKernel(p->part_fns[i], unsigned(tiles), unsigned(p->part_chunks[i]), 1, kLanes,
+                                         1, 1, 0, p->part_streams[i % lanes], args, nullptr));
+  for (int k = 0; k < lanes; ++k) {
+    YE3T_CHECK_HIP(hipEventRecord(p->part_join[k], p->part_streams[k]));
+    YE3T_CHECK_HIP(hipStreamWaitEvent(stream, p->part_join[k], 0));
+  }
+  return YE3T_OK;
+}
+
 int ye3t_hip_product_forward_columns(const ye3t_hip_product_plan* p, const void* At, int64_t ld, int64_t samples,
                                      void* B, ye3t_stream_t stream) {
   clear_error();
@@ -1225,11 +1267,31 @@ int ye3t_hip_product_forward_columns(const ye3t_hip_product_plan* p, const void*
   YE3T_REQUIRE(samples >= 0, "negative sample count");
   if (samples == 0) return YE3T_OK;
   YE3T_REQUIRE(At && B, "NULL input or output");
+  YE3T_REQUIRE(ld >= samples, "ld must cover the samples");
+  if (p->part_count > 0 && !p->use_interpreter) return launch_parts(p, At, 1, ld, samples, B, as_stream(stream));
   YE3T_REQUIRE(p->use_stream, "this plan has no term stream (workspace too large); use ye3t_hip_product_forward");
   if (p->in_dtype != p->dtype)
     return set_error(YE3T_EUNSUPPORTED, "the term stream reads densities of the plan's dtype only");
   YE3T_REQUIRE(ld >= (samples + kLanes - 1) / kLanes * kLanes, "ld must cover whole 64-sample tiles");
   return launch_stream<true>(p, At, ld, samples, B, stream);
+}
+
+static void release_parts(ye3t_hip_product_plan* p) {
+  for (int k = 0; k < p->part_lanes; ++k) {
+    (void)hipStreamDestroy(p->part_streams[k]);
+    (void)hipEventDestroy(p->part_join[k]);
+  }
+  if (p->part_lanes > 0) (void)hipEventDestroy(p->part_fork);
+  p->part_lanes = 0;
+  for (int64_t i = 0; i < p->part_count; ++i)
+    if (p->part_modules[i]) (void)hipModuleUnload(p->part_modules[i]);
+  delete[] p->part_modules;
+  delete[] p->part_fns;
+  delete[] p->part_chunks;
+  p->part_modules = nullptr;
+  p->part_fns = nullptr;
+  p->part_chunks = nullptr;
+  p->part_count = 0;
 }
 
 void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* p) {
@@ -1252,6 +1314,7 @@ void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* p) {
   if (p->module) (void)hipModuleUnload(p->module);
   if (p->readout_module) (void)hipModuleUnload(p->readout_module);
   if (p->adjoint_module) (void)hipModuleUnload(p->adjoint_module);
+  release_parts(p);
   (void)hipSetDevice(prev);
   delete p;
 }
@@ -1394,10 +1457,66 @@ int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* p, const void*
   return YE3T_OK;
 }
 
+int ye3t_hip_product_plan_attach_generated_parts(ye3t_hip_product_plan* p, int64_t part_count,
+                                                 const void* const* codes, const int64_t* sizes,
+                                                 const char* const* kernel_names, const int64_t* chunk_counts) {
+  clear_error();
+  YE3T_REQUIRE(p && codes && sizes && kernel_names && chunk_counts, "NULL argument");
+  YE3T_REQUIRE(part_count >= 1 && part_count <= (int64_t(1) << 20), "part_count must be in [1, 2^20]");
+  int64_t total = 0;
+  for (int64_t i = 0; i < part_count; ++i) {
+    YE3T_REQUIRE(codes[i] && sizes[i] > 0 && kernel_names[i], "NULL or empty part %lld", (long long)i);
+    YE3T_REQUIRE(chunk_counts[i] >= 1 && chunk_counts[i] <= 65535, "bad chunk count of part %lld", (long long)i);
+    total += chunk_counts[i];
+  }
+  YE3T_REQUIRE(total <= (int64_t(1) << 31), "too many chunks");
+  int prev = 0;
+  YE3T_CHECK_HIP(hipGetDevice(&prev));
+  YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
+  auto* modules = new hipModule_t[size_t(part_count)]();
+  auto* fns = new hipFunction_t[size_t(part_count)]();
+  auto* chunks = new int64_t[size_t(part_count)];
+  for (int64_t i = 0; i < part_count; ++i) {
+    chunks[i] = chunk_counts[i];
+    hipError_t e = hipModuleLoadData(&modules[i], codes[i]);
+    if (e == hipSuccess && hipModuleGetFunction(&fns[i], modules[i], kernel_names[i]) != hipSuccess)
+      e = hipErrorNotFound;
+    if (e != hipSuccess) {
+      for (int64_t j = 0; j <= i; ++j)
+        if (modules[j]) (void)hipModuleUnload(modules[j]);
+      delete[] modules;
+      delete[] fns;
+      delete[] chunks;
+      return set_error(YE3T_EINVAL, "part %lld: code object not loadable or kernel %s not found", (long long)i,
+                       kernel_names[i]);
+    }
+  }
+  release_parts(p);
+  p->part_modules = modules;
+  p->part_fns = fns;
+  p->part_chunks = chunks;
+  p->part_count = part_count;
+  // concurrent streams for the parts (YE3T_PARTS_STREAMS, 1..4, default 4), at the default priority
+  int lanes = 4;
+  if (const char* e = std::getenv("YE3T_PARTS_STREAMS")) lanes = std::atoi(e);
+  lanes = lanes < 1 ? 1 : (lanes > 4 ? 4 : lanes);
+  if (lanes > part_count) lanes = int(part_count);
+  if (lanes > 1) {
+    YE3T_CHECK_HIP(hipEventCreateWithFlags(&p->part_fork, hipEventDisableTiming));
+    for (int k = 0; k < lanes; ++k) {
+      YE3T_CHECK_HIP(hipStreamCreateWithFlags(&p->part_streams[k], hipStreamNonBlocking));
+      YE3T_CHECK_HIP(hipEventCreateWithFlags(&p->part_join[k], hipEventDisableTiming));
+      p->part_lanes = k + 1;
+    }
+  }
+  p->use_interpreter = 0;
+  return YE3T_OK;
+}
+
 int ye3t_hip_product_plan_select(ye3t_hip_product_plan* p, int use_interpreter) {
   clear_error();
   YE3T_REQUIRE(p != nullptr, "NULL plan");
-  YE3T_REQUIRE(use_interpreter || p->generated, "no generated kernel attached");
+  YE3T_REQUIRE(use_interpreter || p->generated || p->part_count > 0, "no generated kernel attached");
   p->use_interpreter = use_interpreter ? 1 : 0;
   return YE3T_OK;
 }
@@ -1439,6 +1558,8 @@ int ye3t_hip_product_forward(const ye3t_hip_product_plan* p, const void* A, int6
                                          1, 0, as_stream(stream), args, nullptr));
     return YE3T_OK;
   }
+  if (p->part_count > 0 && !p->use_interpreter)
+    return launch_parts(p, A, p->a_width, 1, samples, B, as_stream(stream));
   if (p->in_dtype != p->dtype)
     return set_error(YE3T_EUNSUPPORTED,
                      "an fp32 density with fp64 arithmetic runs on an attached generated kernel only "

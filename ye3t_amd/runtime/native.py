@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 55
+ABI_VERSION = 56
 _LIB = None
 
 F32, F64 = 0, 1
@@ -130,6 +130,8 @@ def lib():
     L.ye3t_hip_product_plan_attach_generated.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, _i64, _i64, ctypes.c_int,
                                                          ctypes.c_int]
     L.ye3t_hip_product_plan_select.argtypes = [_vp, ctypes.c_int]
+    L.ye3t_hip_product_plan_attach_generated_parts.argtypes = [_vp, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_i64),
+                                                               ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i64)]
     L.ye3t_hip_product_plan_attach_readout.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, ctypes.c_int]
     L.ye3t_hip_product_linear_forward.argtypes = [_vp, _vp, _i64, _vp, ctypes.c_double, _vp, _vp]
     L.ye3t_hip_rows_dot.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, ctypes.c_double, _vp, _vp]
@@ -178,7 +180,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_product_plan_create", "ye3t_hip_product_plan_destroy", "ye3t_hip_product_forward",
     "ye3t_hip_product_launch_info", "ye3t_hip_rtc_compile", "ye3t_hip_free",
     "ye3t_hip_product_plan_attach_generated", "ye3t_hip_product_plan_select", "ye3t_hip_last_density_kernel",
-    "ye3t_hip_fp64_pipe_probe",
+    "ye3t_hip_fp64_pipe_probe", "ye3t_hip_product_plan_attach_generated_parts",
     "ye3t_hip_density_accumulate_adjoint", "ye3t_hip_product_plan_attach_readout", "ye3t_hip_product_linear_forward",
     "ye3t_hip_rows_dot", "ye3t_hip_product_plan_attach_adjoint", "ye3t_hip_product_adjoint",
     "ye3t_hip_neighbor_workspace_bytes", "ye3t_hip_neighbor_count", "ye3t_hip_neighbor_fill",
@@ -625,9 +627,19 @@ def evaluate_factorized_schedule(block_values, schedule):
 
 
 def _jit_cache_dir():
+    """Code objects of generated kernels, keyed by source hash: ``YE3T_AMD_JIT_CACHE``,
+    else ``jit_cache/`` beside this package (built ahead with
+    ``python -m ye3t_amd.ace.prebuild`` it travels with the tree), else a
+    temporary directory when the package directory is read-only."""
     import tempfile
 
-    path = os.environ.get("YE3T_AMD_JIT_CACHE") or os.path.join(tempfile.gettempdir(), "ye3t_amd_jit")
+    path = os.environ.get("YE3T_AMD_JIT_CACHE")
+    if not path:
+        path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "jit_cache")
+        try:
+            os.makedirs(path, exist_ok=True)
+        except OSError:
+            path = os.path.join(tempfile.gettempdir(), "ye3t_amd_jit")
     os.makedirs(path, exist_ok=True)
     return path
 
@@ -754,6 +766,36 @@ class ProductPlanHandle:
                "ye3t_hip_product_plan_attach_generated")
         self.generated = meta
 
+    def attach_generated_parts(self, parts, workers=None):
+        """Compile (hipRTC, in parallel threads, cached on disk) and attach a
+        plan-specialised kernel in parts (``ye3t_amd.ace.codegen.generate_parts``)."""
+        from concurrent.futures import ThreadPoolExecutor
+
+        first = 0
+        for _source, meta in parts:
+            if meta["feature_count"] != self.feature_count or meta["a_width"] != self.program["a_width"]:
+                raise ValueError("generated part does not match this plan")
+            if meta["dtype"] != self.dtype or meta.get("out_dtype", meta["dtype"]) != self.out_dtype or \
+                    meta.get("in_dtype", meta["dtype"]) != self.in_dtype:
+                raise ValueError("generated part dtypes do not match this plan")
+            if meta["first_output"] != first:
+                raise ValueError("generated parts must cover the outputs in order")
+            first = meta["last_output"]
+        if first != self.feature_count:
+            raise ValueError("generated parts do not cover every output")
+        workers = workers or min(16, os.cpu_count() or 1)
+        with ThreadPoolExecutor(max(1, workers)) as pool:
+            blobs = list(pool.map(lambda part: rtc_compile(part[0]), parts))
+        n = len(parts)
+        self._part_code = [ctypes.create_string_buffer(b, len(b)) for b in blobs]
+        codes = (_vp * n)(*[ctypes.cast(c, _vp) for c in self._part_code])
+        sizes = (_i64 * n)(*[len(b) for b in blobs])
+        names = (ctypes.c_char_p * n)(*[m["kernel"].encode() for _, m in parts])
+        chunks = (_i64 * n)(*[int(m["chunks"]) for _, m in parts])
+        _check(lib().ye3t_hip_product_plan_attach_generated_parts(self._handle, n, codes, sizes, names, chunks),
+               "ye3t_hip_product_plan_attach_generated_parts")
+        self.generated_parts = [m for _, m in parts]
+
     def select(self, use_interpreter):
         _check(lib().ye3t_hip_product_plan_select(self._handle, 1 if use_interpreter else 0),
                "ye3t_hip_product_plan_select")
@@ -794,7 +836,7 @@ class ProductPlanHandle:
 
         if At.ndim != 2 or int(At.shape[0]) != int(self.program["a_width"]):
             raise ValueError(f"At must be [{self.program['a_width']}, ld]")
-        want = torch.float64 if self.dtype == "f64" else torch.float32
+        want = torch.float64 if self.in_dtype == "f64" else torch.float32
         if At.dtype != want:
             raise ValueError(f"At must be {want} for this plan")
         S, ld = int(samples), int(At.shape[1])
