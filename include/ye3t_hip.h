@@ -294,8 +294,10 @@ int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* plan, const vo
  * ye3t_amd/ace/codegen.py:generate_parts output) with kernel kernel_names[i],
  * which computes chunk_counts[i] consecutive output chunks of the plan.
  * product_forward and product_forward_columns then launch the parts in order
- * on their stream, each with 64 threads per workgroup and grid
- * (ceil(samples / 64), chunk_counts[i]); the kernel signature is
+ * on their stream, each with 64 threads per workgroup and grid (ceil(samples
+ * / 64) rounded up to a multiple of 8, chunk_counts[i]) -- the kernel maps its
+ * linear workgroup id to (tile, chunk) so that each XCD takes one eighth of the
+ * tiles, and workgroups past the last tile return at once; the signature is
  * (const T* A, long samples, U* B, long row_stride, long col_stride), density
  * value (s, k) at A[s * row_stride + k * col_stride]: (a_width, 1) for the
  * row-major density, (1, ld) for its column-major copy.  Replaces earlier

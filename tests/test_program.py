@@ -109,8 +109,8 @@ def test_rank_four_and_species_program():
 def test_generated_parts_cover_the_outputs_in_order(max_live, per):
     """``codegen.generate_parts``: consecutive parts hand over at chunk
     boundaries, cover every output once, and a part's kernel switches over its
-    own chunks and writes only its columns (never the whole-row tile store of
-    a one-chunk plan)."""
+    own chunks (mapped from the linear workgroup id) and writes only its
+    columns (never the whole-row tile store of a one-chunk plan)."""
     import re
 
     from ye3t_amd.ace import codegen
@@ -125,7 +125,7 @@ def test_generated_parts_cover_the_outputs_in_order(max_live, per):
         assert meta["first_output"] == first and meta["kernel"] == "ye3t_product_part"
         lo, hi = meta["first_output"], meta["last_output"]
         assert (lo, hi) == (chunks[k * per][0], chunks[min(len(chunks), (k + 1) * per) - 1][1])
-        assert src.count("  case ") == meta["chunks"] and "switch (blockIdx.y)" in src
+        assert src.count("  case ") == meta["chunks"] and "switch (chunk)" in src
         cols = [int(g) for g in re.findall(r"B\[\(s0 \+ r\) \* \d+L \+ (\d+) \+ c\]", src)]
         assert cols and min(cols) == lo and max(cols) < hi
         first = hi

@@ -561,7 +561,18 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     else:
         w(f"  __shared__ OUT st[{group}][65];")
     w("  const int lane = threadIdx.x;")
-    w(f"  const long s0 = (long)blockIdx.x * {R};")
+    if strided:
+        # XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by
+        # linear id, so XCD x gets the tiles [x * per, (x + 1) * per) of every
+        # chunk and its L2 holds one eighth of the density (gridDim.x = 8 * per)
+        w("  const long wg = (long)blockIdx.y * gridDim.x + blockIdx.x;")
+        w("  const long per = gridDim.x >> 3, k = wg >> 3;")
+        w("  const long tile = (wg & 7) * per + k % per;")
+        w("  const int chunk = (int)(k / per);")
+        w(f"  const long s0 = tile * {R};")
+        w("  if (s0 >= samples) return;")
+    else:
+        w(f"  const long s0 = (long)blockIdx.x * {R};")
     w("  const long s = s0 + lane;")
     w(f"  const bool valid = lane < {R} && s < samples;")
     if strided:
@@ -570,7 +581,7 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
         w(f"  const AIN* __restrict__ a = A + (valid ? s : 0) * {plan.a_width}L;")
     w("  const long rem = samples - s0;")
     w(f"  const int rows = rem < {R} ? (int)rem : {R};")
-    w("  switch (blockIdx.y) {")
+    w("  switch (chunk) {" if strided else "  switch (blockIdx.y) {")
     for ci, (first, last, members) in enumerate(chunks):
         w(f"  case {ci}: {{")
         emitted = set()
@@ -584,8 +595,13 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
             emitted.add(n)
             if nd["kind"] == "leaf":
                 for c in range(nd["dim"]):
-                    at = f"{nd['a_offset'] + c}L * col_stride" if strided else f"{nd['a_offset'] + c}"
-                    w(f"    const REAL v{n}_{c} = valid ? (REAL)a[{at}] : (REAL)0;")
+                    if strided:
+                        # unconditional: lanes past the last sample read sample 0 (a valid
+                        # address) and their outputs are never stored; a select per load
+                        # would turn each into a branch that waits for its own data
+                        w(f"    const REAL v{n}_{c} = (REAL)a[{nd['a_offset'] + c}L * col_stride];")
+                    else:
+                        w(f"    const REAL v{n}_{c} = valid ? (REAL)a[{nd['a_offset'] + c}] : (REAL)0;")
                 return
             per = [[] for _ in range(nd["dim"])]
             if nd["kind"] == "sym":
@@ -661,10 +677,11 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
 
 
 # node values per chunk of a generated part and chunks per part: config 2 (fp64)
-# measured 166 us at (400, 6) against 447 us at (96, 16) and 270 us at (256, 4);
-# larger chunks re-read fewer density columns and recompute fewer shared nodes
+# measured 127 us at (400, 9), 135 us at (400, 6), 140 us at (300, 6), 162 us at
+# (500, 4) and 216 us at (800, 2); larger chunks re-read fewer density columns and
+# recompute fewer shared nodes until they spill
 PART_MAX_LIVE = 400
-PART_CHUNKS = 6
+PART_CHUNKS = 9
 
 
 def generate_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per_part=PART_CHUNKS, out_dtype=None,
@@ -673,7 +690,7 @@ def generate_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per_part=PA
     parts of ``chunks_per_part`` consecutive output chunks (each chunk holds
     at most ``max_live`` node values), for plans whose code is too large for
     one hipRTC module (compile time grows faster than the code: 221 s for
-    config 2's 16 810 terms as one kernel at 126 chunks, ~5 s per 6-chunk
+    config 2's 16 810 terms as one kernel at 126 chunks, ~5 s per 9-chunk
     part of 400-value chunks).  Part i
     writes columns ``[meta["first_output"], meta["last_output"])`` of B; the
     parts run in order (``ye3t_hip_product_plan_attach_generated_parts``) and

@@ -2,20 +2,22 @@
 
 Plans between ``GENERATED_MAX_TERMS`` and ``PARTS_MAX_TERMS`` terms run on a
 generated kernel in parts (``codegen.generate_parts``), one hipRTC module per
-16 chunks: about half a minute for config 2 and a few minutes for config 3 on
-8 cores.  hipRTC needs no GPU, so this runs on a build host; the code objects
-land in the JIT cache (``ye3t_amd/jit_cache`` unless ``YE3T_AMD_JIT_CACHE`` says
-otherwise), keyed by source hash, and travel with the tree.
+9 chunks.  hipRTC compiles one module at a time per process (~15 s for a
+config-3 part), so the parts are spread over worker processes.  hipRTC needs
+no GPU, so this runs on a build host; the code objects land in the JIT cache
+(``ye3t_amd/jit_cache`` unless ``YE3T_AMD_JIT_CACHE`` says otherwise), keyed by
+source hash, and travel with the tree.
 
     python -m ye3t_amd.ace.prebuild            # configs 2 and 3, every dtype they are benchmarked in
     python -m ye3t_amd.ace.prebuild 2 --dtype f64
 """
 
 import argparse
+import multiprocessing
 import os
 import sys
 import time
-from concurrent.futures import ThreadPoolExecutor
+from concurrent.futures import ProcessPoolExecutor
 
 
 def precisions(cfg, dtype):
@@ -23,6 +25,13 @@ def precisions(cfg, dtype):
     accumulate = (cfg.accumulate if dtype == "f32" else None) or dtype
     density = (cfg.density_dtype if dtype == "f32" and accumulate == cfg.accumulate else None) or accumulate
     return accumulate, density
+
+
+def _compile(source):
+    from ye3t_amd.runtime import native
+
+    native.rtc_compile(source)
+    return len(source)
 
 
 def prebuild(config_ids=(2, 3), dtypes=None, workers=None, log=print):
@@ -44,8 +53,9 @@ def prebuild(config_ids=(2, 3), dtypes=None, workers=None, log=print):
             accumulate, density = precisions(cfg, dtype)
             parts = generate_parts(plan, accumulate, out_dtype=dtype, in_dtype=density)
             t0 = time.time()
-            with ThreadPoolExecutor(workers) as pool:
-                list(pool.map(lambda part: native.rtc_compile(part[0]), parts))
+            # worker processes (spawned: nothing of this process is inherited) compile in parallel
+            with ProcessPoolExecutor(workers, mp_context=multiprocessing.get_context("spawn")) as pool:
+                list(pool.map(_compile, [part[0] for part in parts]))
             log(f"config {cid} {dtype} (arithmetic {accumulate}, density {density}): {len(parts)} parts "
                 f"in {time.time() - t0:.1f} s -> {native._jit_cache_dir()}")
 

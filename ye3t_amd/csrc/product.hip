@@ -1233,8 +1233,9 @@ int ye3t_hip_transpose(int dtype, const void* A, int64_t rows, int64_t cols, voi
 // the generated kernel in parts, in order: density value (s, k) at A[s * row_stride + k * col_stride]
 static int launch_parts(const ye3t_hip_product_plan* p, const void* A, int64_t row_stride, int64_t col_stride,
                         int64_t samples, void* B, hipStream_t stream) {
-  const int64_t tiles = (samples + kLanes - 1) / kLanes;
-  YE3T_REQUIRE(tiles <= int64_t(0x7FFFFFFF), "too many samples for one launch");
+  // a multiple of 8 tile columns: the parts deal tiles to XCDs by linear workgroup id
+  const int64_t tiles = ((samples + kLanes - 1) / kLanes + 7) & ~int64_t(7);
+  YE3T_REQUIRE(tiles <= int64_t(0x7FFFFFF8), "too many samples for one launch");
   long s_arg = long(samples), rs_arg = long(row_stride), cs_arg = long(col_stride);
   const void* a_arg = A;
   void* b_arg = B;
