@@ -595,13 +595,11 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
             emitted.add(n)
             if nd["kind"] == "leaf":
                 for c in range(nd["dim"]):
-                    if strided:
-                        # unconditional: lanes past the last sample read sample 0 (a valid
-                        # address) and their outputs are never stored; a select per load
-                        # would turn each into a branch that waits for its own data
-                        w(f"    const REAL v{n}_{c} = (REAL)a[{nd['a_offset'] + c}L * col_stride];")
-                    else:
-                        w(f"    const REAL v{n}_{c} = valid ? (REAL)a[{nd['a_offset'] + c}] : (REAL)0;")
+                    # unconditional: lanes past the last sample read sample 0 (a valid
+                    # address) and their outputs are never stored; a select per load
+                    # would turn each into a branch that waits for its own data
+                    at = f"{nd['a_offset'] + c}L * col_stride" if strided else f"{nd['a_offset'] + c}"
+                    w(f"    const REAL v{n}_{c} = (REAL)a[{at}];")
                 return
             per = [[] for _ in range(nd["dim"])]
             if nd["kind"] == "sym":
