@@ -244,6 +244,9 @@ def bench_op(args, cfg):
         pipe.product_adjoint(rows, gB, out=gA)  # compiles and attaches the adjoint kernel
         if pipe.last_adjoint_backend == "generated":
             t = _time_kernel(lambda: pipe.handle.adjoint(rows, gB, out=gA), args.steps, args.warmup)
+        elif pipe.last_adjoint_backend == "parts":
+            # the column-major copy, the parts on the plan's streams and the fixed-order reduction
+            t = _time_kernel(lambda: pipe.product_adjoint(rows, gB, out=gA), args.steps, args.warmup)
         else:
             # the term stream's reverse mode on the column-major density (the copy is
             # the forward's; timed here: clearing the partial sums, the kernel, the sum)

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 56 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 57 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -308,6 +308,38 @@ int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* plan, const vo
 int ye3t_hip_product_plan_attach_generated_parts(ye3t_hip_product_plan* plan, int64_t part_count,
                                                  const void* const* codes, const int64_t* sizes,
                                                  const char* const* kernel_names, const int64_t* chunk_counts);
+
+/* Reverse mode of a plan in parts (code objects of
+ * ye3t_amd/ace/codegen.py:generate_adjoint_parts, kernel signature
+ * (const T* A, const G* gB, long samples, R* P, long row_stride,
+ * long col_stride, long ldp), R = the plan's dtype, T = its density type, G =
+ * its out_dtype).  Each part writes partial density gradients of its chunks as
+ * rows of P [partial_rows, ldp]; column k of gA then sums P rows
+ * row_ids[col_off[k] .. col_off[k + 1]) in that order (host arrays, copied to
+ * the device; col_off has a_width + 1 entries).  No reference counterpart:
+ * the plan-specialised form of the reference's factorized_angular_adjoint
+ * (execution_plan_cuda.cu:6361) for the plans of
+ * ye3t_hip_product_plan_attach_generated_parts. */
+int ye3t_hip_product_plan_attach_adjoint_parts(ye3t_hip_product_plan* plan, int64_t part_count,
+                                               const void* const* codes, const int64_t* sizes,
+                                               const char* const* kernel_names, const int64_t* chunk_counts,
+                                               int64_t partial_rows, const int64_t* col_off, const int64_t* row_ids);
+
+/* Bytes of the partial buffer ye3t_hip_product_adjoint_parts needs for
+ * `samples` (partial_rows x samples rounded up to 64 x the plan's element
+ * size); 0 without adjoint parts, -1 on error. */
+int64_t ye3t_hip_product_adjoint_parts_workspace_bytes(const ye3t_hip_product_plan* plan, int64_t samples);
+
+/* gA[s] = J(A[s])^T gB[s] on the attached adjoint parts: A row-major
+ * [samples, a_width] (lda == a_width) or, with `columns`, column-major
+ * [a_width, lda] (lda >= samples); gB [samples, feature_count] of the plan's
+ * out_dtype; gA row-major in the density's type.  The parts run on the plan's
+ * streams (as the forward parts do), then one fixed-order reduction on
+ * `stream`; results do not depend on the launch schedule.  Replaces the same
+ * reference op as ye3t_hip_product_adjoint. */
+int ye3t_hip_product_adjoint_parts(const ye3t_hip_product_plan* plan, const void* A, int64_t lda, int columns,
+                                   const void* gB, int64_t samples, void* workspace, int64_t workspace_bytes,
+                                   void* gA, ye3t_stream_t stream);
 
 /* Attach a plan-specialised fused linear readout kernel (code object of
  * ye3t_amd/ace/codegen.py:generate_readout compiled with ye3t_hip_rtc_compile).

@@ -464,6 +464,45 @@ def test_stream_product_adjoint(gpu, cid, dtype, accumulate, samples, tol):
     assert torch.equal(pipe.product_adjoint(A, gB), gA)
 
 
+@pytest.mark.parametrize("cid,dtype,accumulate,samples,tol", [
+    (2, "f64", "f64", 150, 1e-12), (2, "f64", "f64", 1000, 1e-12), (3, "f64", "f64", 70, 1e-12),
+    (3, "f32", "f32", 70, 2e-5), (4, "f32", "f64", 4112, None), (4, "f64", "f64", 1, 1e-12)])
+def test_parts_product_adjoint(gpu, cid, dtype, accumulate, samples, tol):
+    """gA = J(A)^T gB by the generated reverse mode in parts (partial rows per
+    chunk, fixed-order reduction) vs the oracle's reverse mode; doubling gB
+    doubles gA exactly, a rerun and a run in several sample blocks give the
+    same bits.  With an fp32 density (tol None) each value is the oracle's
+    rounded once to fp32."""
+    flush(f"parts adjoint config {cid} storage {dtype} accumulate {accumulate} samples {samples}")
+    import torch
+
+    spec = _species_rank4_spec() if cid == 3 else W.config(cid).feature_spec
+    density = "f32" if tol is None else None
+    pipe = ACEPipeline(spec, dtype, kernel="parts", accumulate=accumulate, density=density)
+    rng = np.random.default_rng(51 + cid)
+    a_t = torch.float32 if density == "f32" or accumulate == "f32" else torch.float64
+    g_t = torch.float64 if dtype == "f64" else torch.float32
+    A = torch.as_tensor(rng.normal(size=(samples, pipe.plan.a_width)), dtype=a_t).to(gpu)
+    gB = torch.as_tensor(rng.normal(size=(samples, pipe.feature_count)), dtype=g_t).to(gpu)
+    gA = pipe.product_adjoint(A, gB)
+    assert pipe.last_adjoint_backend == "parts"
+    assert gA.dtype == a_t and tuple(gA.shape) == (samples, pipe.plan.a_width)
+    ref = oracle.ace_product_flat_adjoint(A.double().cpu().numpy(), gB.double().cpu().numpy(),
+                                          pipe.plan.flat_arrays())
+    if tol is None:
+        ratio = fp32_rounding_ratio(gA.cpu().double().numpy(), ref)
+        flush(f"  error / fp32 rounding bound {ratio:.3f}")
+        assert ratio <= 1.0
+    else:
+        err = column_rel_error(gA.cpu().double().numpy(), ref)
+        flush(f"  err {err:.3e}")
+        assert err < tol
+    assert torch.equal(pipe.product_adjoint(A, 2 * gB), 2 * gA)
+    assert torch.equal(pipe.product_adjoint(A, gB), gA)
+    blocked = pipe._adjoint_parts(A, gB, None, block_bytes=pipe._adjoint_rows * 8 * 64)
+    assert torch.equal(blocked, gA)
+
+
 def test_product_adjoint_needs_a_term_stream(gpu, monkeypatch):
     """A workspace too wide for the term stream has no device adjoint; one whose
     forward stream fits 64 KB of LDS but whose reverse mode (values and

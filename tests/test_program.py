@@ -130,3 +130,29 @@ def test_generated_parts_cover_the_outputs_in_order(max_live, per):
         assert cols and min(cols) == lo and max(cols) < hi
         first = hi
     assert first == plan.feature_count
+
+
+def test_adjoint_parts_reduction_map():
+    """``codegen.generate_adjoint_parts``: every partial row belongs to exactly
+    one density column, a column's rows come in chunk order, the parts' row
+    ranges tile the partial buffer, and each part writes exactly its rows."""
+    import re
+
+    from ye3t_amd.ace import codegen
+
+    plan = ProductPlan(W.config(4).feature_spec)
+    parts, red = codegen.generate_adjoint_parts(plan, "f64", max_live=24, chunks_per_part=2, grad_dtype="f32",
+                                                in_dtype="f32")
+    col_off, rows = red["col_off"], red["rows"]
+    assert len(col_off) == plan.a_width + 1 and col_off[0] == 0 and col_off[-1] == len(rows)
+    assert sorted(rows.tolist()) == list(range(red["partial_rows"]))
+    for k in range(plan.a_width):
+        seg = rows[col_off[k]:col_off[k + 1]]
+        assert np.all(np.diff(seg) > 0)
+    first = 0
+    for src, meta in parts:
+        assert meta["first_row"] == first
+        written = sorted(int(r) for r in re.findall(r"P\[(\d+)L \* ldp \+ s\]", src))
+        assert written == list(range(meta["first_row"], meta["last_row"]))
+        first = meta["last_row"]
+    assert first == red["partial_rows"]

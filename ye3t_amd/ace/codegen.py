@@ -704,3 +704,150 @@ def generate_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per_part=PA
                               in_dtype=in_dtype, chunks=chunks[i:i + chunks_per_part], strided=True,
                               group=group))
     return parts
+
+
+def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per_part=PART_CHUNKS, grad_dtype=None,
+                           in_dtype=None, group=GROUP):
+    """Reverse mode of a plan too large for one module, in parts:
+    ``gA[s] = J(A[s])^T gB[s]`` (counterpart of the reference's
+    ``factorized_angular_adjoint``, ``execution_plan_cuda.cu:6361``).
+
+    The chunks and parts are those of :func:`generate_parts`.  For each tile
+    of 64 samples a chunk recomputes the forward values its outputs depend on
+    (density read through row and column strides), loads its outputs'
+    gradients from ``gB`` (row segments staged through LDS, ``group`` columns
+    at a time), sweeps its nodes in reverse creation order and writes the
+    gradients of the density columns it touches as rows of a partial buffer
+    ``P`` (``P[row * ldp + s]``, one row per (chunk, touched column)).  A
+    reduction then sums, for each density column, its partial rows in chunk
+    order (fixed, so the result does not depend on scheduling).
+
+    Returns ``(parts, reduction)``: ``parts`` is ``[(source, meta), ...]`` with
+    kernel signature ``(const AIN* A, const GT* gB, long samples, REAL* P,
+    long row_stride, long col_stride, long ldp)``; ``reduction`` holds
+    ``partial_rows`` (rows of ``P``), ``col_off`` (``[a_width + 1]``) and
+    ``rows``: column ``k``'s partial rows are ``rows[col_off[k]:col_off[k + 1]]``.
+    """
+    import numpy as np
+
+    grad_dtype = grad_dtype or dtype
+    in_dtype = _check_in_dtype(dtype, in_dtype)
+    if dtype == "f32" and grad_dtype != "f32":
+        raise ValueError("an f32 plan takes f32 gradients")
+    if chunks_per_part < 1:
+        raise ValueError("chunks_per_part must be positive")
+    real = "double" if dtype == "f64" else "float"
+    gt = "double" if grad_dtype == "f64" else "float"
+    fma = "fma" if dtype == "f64" else "fmaf"
+    nodes = plan.nodes
+    F, Wd = plan.feature_count, plan.a_width
+    chunks = _chunks(plan, max_live)
+    touched = []
+    for _first, _last, members in chunks:
+        touched.append(sorted(nodes[n]["a_offset"] + c for n in members if nodes[n]["kind"] == "leaf"
+                              for c in range(nodes[n]["dim"])))
+    row_base = [0]
+    for cols in touched:
+        row_base.append(row_base[-1] + len(cols))
+    col_rows = [[] for _ in range(Wd)]
+    for ci, cols in enumerate(touched):
+        for j, k in enumerate(cols):
+            col_rows[k].append(row_base[ci] + j)
+    col_off = np.zeros(Wd + 1, dtype=np.int64)
+    col_off[1:] = np.cumsum([len(r) for r in col_rows])
+    rows = np.array([r for rs in col_rows for r in rs], dtype=np.int64)
+
+    parts = []
+    for p0 in range(0, len(chunks), chunks_per_part):
+        sub = list(range(p0, min(len(chunks), p0 + chunks_per_part)))
+        out = []
+        w = out.append
+        w("// generated by ye3t_amd.ace.codegen (product adjoint part) -- do not edit (compiled with hipRTC)")
+        w(f"#define REAL {real}")
+        w(f"#define GT {gt}")
+        w(f"#define AIN {_ctype(in_dtype)}")
+        w("extern \"C\" __global__ __launch_bounds__(64) void ye3t_product_adjoint_part(")
+        w("    const AIN* __restrict__ A, const GT* __restrict__ gB, long samples, REAL* __restrict__ P,")
+        w("    long row_stride, long col_stride, long ldp) {")
+        w(f"  __shared__ GT st[{group}][65];")
+        w("  const int lane = threadIdx.x;")
+        # the forward parts' XCD-aware (tile, chunk) order
+        w("  const long wg = (long)blockIdx.y * gridDim.x + blockIdx.x;")
+        w("  const long per = gridDim.x >> 3, k = wg >> 3;")
+        w("  const long tile = (wg & 7) * per + k % per;")
+        w("  const int chunk = (int)(k / per);")
+        w("  const long s0 = tile * 64;")
+        w("  if (s0 >= samples) return;")
+        w("  const long s = s0 + lane;")
+        w("  const AIN* __restrict__ a = A + (s < samples ? s : 0) * row_stride;")
+        w("  const long rem = samples - s0;")
+        w("  const int rows = rem < 64 ? (int)rem : 64;")
+        w("  switch (chunk) {")
+        for lc, ci in enumerate(sub):
+            first, last, members = chunks[ci]
+            w(f"  case {lc}: {{")
+            emitted = set()
+            # every density value of the chunk, unconditionally (lanes past the
+            # last sample read sample 0 and write only partial rows never summed)
+            for n in sorted((m for m in members if nodes[m]["kind"] == "leaf"), key=lambda m: nodes[m]["a_offset"]):
+                _emit_node_code(w, nodes, n, emitted, dtype, lambda c: f"(REAL)a[{c}L * col_stride]")
+            roots = sorted({plan.outputs[f][0] for f in range(first, last)})
+            needed = set()
+            for r in roots:
+                _closure(nodes, r, needed)
+            for r in roots:
+                for d in nodes[r]["deps"]:
+                    _emit_node_code(w, nodes, d, emitted, dtype, lambda c: f"(REAL)a[{c}L * col_stride]")
+            for n in sorted(needed):
+                for c in range(nodes[n]["dim"]):
+                    w(f"      REAL g{n}_{c} = (REAL)0;")
+            # the chunk's output gradients, `group` columns at a time
+            for g0 in range(first, last, group):
+                g1 = min(g0 + group, last)
+                width = g1 - g0
+                w("      __syncthreads();")
+                w(f"      for (int i = lane; i < rows * {width}; i += 64) {{")
+                w(f"        const int r = i / {width}, c = i - r * {width};")
+                w(f"        st[c][r] = gB[(s0 + r) * {F}L + {g0} + c];")
+                w("      }")
+                w("      __syncthreads();")
+                for f in range(g0, g1):
+                    root, comp = plan.outputs[f]
+                    w(f"      g{root}_{comp} += (REAL)st[{f - g0}][lane];")
+            for n in sorted(needed, reverse=True):
+                nd = nodes[n]
+                if nd["kind"] == "leaf":
+                    continue
+                if nd["kind"] == "pair":
+                    da, db = nd["deps"]
+                    for oc, value, (i, j) in nd["terms"]:
+                        cg = f"({_lit(value, dtype)} * g{n}_{oc})"
+                        w(f"      g{da}_{i} = {fma}({cg}, v{db}_{j}, g{da}_{i});")
+                        w(f"      g{db}_{j} = {fma}({cg}, v{da}_{i}, g{db}_{j});")
+                else:
+                    srcn = nd["deps"][0]
+                    for oc, value, factors in nd["terms"]:
+                        cg = f"({_lit(value, dtype)} * g{n}_{oc})"
+                        for m, q in enumerate(factors):
+                            rest = [f"v{srcn}_{x}" for k2, x in enumerate(factors) if k2 != m]
+                            prod = " * ".join(rest) if rest else "(REAL)1"
+                            w(f"      g{srcn}_{q} = {fma}({cg}, {prod}, g{srcn}_{q});")
+            leaf_of = {}
+            for n in needed:
+                if nodes[n]["kind"] == "leaf":
+                    for c in range(nodes[n]["dim"]):
+                        leaf_of[nodes[n]["a_offset"] + c] = f"g{n}_{c}"
+            for j, col in enumerate(touched[ci]):
+                w(f"      P[{row_base[ci] + j}L * ldp + s] = {leaf_of.get(col, '(REAL)0')};")
+            w("      break;")
+            w("  }")
+        w("  default: break;")
+        w("  }")
+        w("}")
+        source = "\n".join(out) + "\n"
+        meta = {"kernel": "ye3t_product_adjoint_part", "chunks": len(sub), "feature_count": F, "a_width": Wd,
+                "dtype": dtype, "grad_dtype": grad_dtype, "in_dtype": in_dtype,
+                "first_row": row_base[sub[0]], "last_row": row_base[sub[-1] + 1],
+                "hash": hashlib.sha256(source.encode()).hexdigest()[:16]}
+        parts.append((source, meta))
+    return parts, {"partial_rows": row_base[-1], "col_off": col_off, "rows": rows}

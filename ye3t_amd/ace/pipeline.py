@@ -36,8 +36,12 @@ def to_device_inputs(inp, dtype, device="cuda"):
 # larger plans run the generic interpreter (hipRTC time grows with code size)
 GENERATED_MAX_TERMS = 5000
 # plans up to this size run on a generated kernel in parts (one hipRTC module per
-# 16 chunks, compiled in parallel and cached); larger ones on the interpreter
+# 9 chunks, compiled once and cached); larger ones on the interpreter
 PARTS_MAX_TERMS = 200000
+# the reverse mode's parts: chunks of fewer node values (values and gradients are
+# live together; 128 compiles without spills at config 2) and chunks per part
+ADJOINT_PART_MAX_LIVE = 128
+ADJOINT_PART_CHUNKS = 8
 
 
 class ACEPipeline:
@@ -166,6 +170,8 @@ class ACEPipeline:
         term stream's reverse mode on the column-major density.  Plans whose
         workspace is too wide for the term stream raise ``NotImplementedError``."""
         self.last_adjoint_backend = None
+        if self.kernel == "parts":
+            return self._adjoint_parts(A_rows, gB, out)
         if self.kernel != "generated":
             if self._adjoint_handle is None:
                 # the forward's program; YE3T_ADJOINT_SLOTS compiles one with a narrower
@@ -198,6 +204,43 @@ class ACEPipeline:
                                             waves=int(waves) if waves else 2, in_dtype=self.density_dtype)
             self.handle.attach_adjoint(source, meta)
         return self.handle.adjoint(A_rows, gB, out=out)
+
+    def _adjoint_parts(self, A_rows, gB, out, block_bytes=2 << 30):
+        """Reverse mode of a parts plan: the plan-specialised adjoint in parts
+        (compiled on first use) on the column-major density, in sample blocks
+        whose partial buffer stays within ``block_bytes``."""
+        import torch
+
+        from ye3t_amd.ace.codegen import generate_adjoint_parts
+
+        if getattr(self.handle, "adjoint_part_meta", None) is None:
+            # smaller chunks than the forward's: values and gradients are live together (tuning)
+            live = int(os.environ.get("YE3T_ADJOINT_PARTS_MAX_LIVE", ADJOINT_PART_MAX_LIVE))
+            per = int(os.environ.get("YE3T_ADJOINT_PARTS_CHUNKS", ADJOINT_PART_CHUNKS))
+            parts, reduction = generate_adjoint_parts(self.plan, self.accumulate, max_live=live, chunks_per_part=per,
+                                                      grad_dtype=self.dtype, in_dtype=self.density_dtype)
+            self.handle.attach_adjoint_parts(parts, reduction)
+            self._adjoint_rows = int(reduction["partial_rows"])
+        S = int(A_rows.shape[0])
+        W = self.plan.a_width
+        a_t = torch.float64 if self.density_dtype == "f64" else torch.float32
+        if out is None:
+            out = torch.empty((S, W), dtype=a_t, device=A_rows.device)
+        if S == 0:
+            return out
+        ld = (S + 63) // 64 * 64
+        key = (W, ld, A_rows.dtype, A_rows.device)
+        if self._At is None or self._At[0] != key:
+            self._At = (key, torch.empty((W, ld), dtype=A_rows.dtype, device=A_rows.device))
+        At = native.transpose(A_rows.contiguous(), out=self._At[1], ld=ld)
+        elem = 8 if self.accumulate == "f64" else 4
+        blk = max(64, block_bytes // max(1, self._adjoint_rows * elem) // 64 * 64)
+        gB = gB.contiguous()
+        for s0 in range(0, S, blk):
+            s1 = min(S, s0 + blk)
+            self.handle.adjoint_parts(At[:, s0:], gB[s0:s1], samples=s1 - s0, columns=True, out=out[s0:s1])
+        self.last_adjoint_backend = "parts"
+        return out
 
     def linear(self, A_rows, weight, bias=0.0, out=None, block_bytes=1 << 30):
         """Linear readout ``out[s] = bias + sum_k B[s, k] weight[k]`` (reference

@@ -36,8 +36,9 @@ def _compile(source):
 
 def prebuild(config_ids=(2, 3), dtypes=None, workers=None, log=print):
     from ye3t_amd.ace import workloads as W
-    from ye3t_amd.ace.codegen import generate_parts
-    from ye3t_amd.ace.pipeline import GENERATED_MAX_TERMS, PARTS_MAX_TERMS
+    from ye3t_amd.ace.codegen import generate_adjoint_parts, generate_parts
+    from ye3t_amd.ace.pipeline import (ADJOINT_PART_CHUNKS, ADJOINT_PART_MAX_LIVE, GENERATED_MAX_TERMS,
+                                       PARTS_MAX_TERMS)
     from ye3t_amd.ace.plan import ProductPlan
     from ye3t_amd.runtime import native
 
@@ -52,12 +53,15 @@ def prebuild(config_ids=(2, 3), dtypes=None, workers=None, log=print):
         for dtype in dtypes or cfg.dtypes:
             accumulate, density = precisions(cfg, dtype)
             parts = generate_parts(plan, accumulate, out_dtype=dtype, in_dtype=density)
+            adjoint, _ = generate_adjoint_parts(plan, accumulate, max_live=ADJOINT_PART_MAX_LIVE,
+                                                chunks_per_part=ADJOINT_PART_CHUNKS, grad_dtype=dtype,
+                                                in_dtype=density)
             t0 = time.time()
             # worker processes (spawned: nothing of this process is inherited) compile in parallel
             with ProcessPoolExecutor(workers, mp_context=multiprocessing.get_context("spawn")) as pool:
-                list(pool.map(_compile, [part[0] for part in parts]))
-            log(f"config {cid} {dtype} (arithmetic {accumulate}, density {density}): {len(parts)} parts "
-                f"in {time.time() - t0:.1f} s -> {native._jit_cache_dir()}")
+                list(pool.map(_compile, [part[0] for part in parts + adjoint]))
+            log(f"config {cid} {dtype} (arithmetic {accumulate}, density {density}): {len(parts)} forward and "
+                f"{len(adjoint)} adjoint parts in {time.time() - t0:.1f} s -> {native._jit_cache_dir()}")
 
 
 def main(argv=None):

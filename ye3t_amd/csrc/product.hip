@@ -58,6 +58,16 @@ struct ye3t_hip_product_plan {
   hipStream_t part_streams[4];
   hipEvent_t part_fork;
   hipEvent_t part_join[4];
+  // plan-specialised reverse mode in parts: part i writes partial density
+  // gradients of adj_chunks[i] chunks as rows of P[adj_rows][ldp]; column k of gA
+  // sums P rows adj_row_ids[adj_col_off[k] .. adj_col_off[k + 1]) in that order
+  int64_t adj_count;
+  hipModule_t* adj_modules;
+  hipFunction_t* adj_fns;
+  int64_t* adj_chunks;
+  int64_t adj_rows;
+  int64_t* adj_col_off;  // device [a_width + 1]
+  int64_t* adj_row_ids;  // device [adj_col_off[a_width]]
   int use_interpreter;
   // plan-specialised fused linear readout (optional)
   hipModule_t readout_module;
@@ -1277,6 +1287,53 @@ int ye3t_hip_product_forward_columns(const ye3t_hip_product_plan* p, const void*
   return launch_stream<true>(p, At, ld, samples, B, stream);
 }
 
+extern "C++" {
+namespace ye3t {
+// gA[s, k] = sum of P[row * ldp + s] over column k's partial rows, in their
+// listed order: 256 threads per 64 samples x 64 columns, staged in LDS so the
+// row-major gA block is written in row segments
+template <typename Real, typename Out>
+__global__ __launch_bounds__(256) void adjoint_parts_reduce_kernel(const Real* __restrict__ P, int64_t ldp,
+                                                                   const int64_t* __restrict__ col_off,
+                                                                   const int64_t* __restrict__ row_ids, int64_t W,
+                                                                   int64_t samples, Out* __restrict__ gA) {
+  __shared__ Real tile[64][65];
+  const int lane = threadIdx.x & 63, cw = threadIdx.x >> 6;
+  const int64_t s0 = int64_t(blockIdx.x) * 64, k0 = int64_t(blockIdx.y) * 64;
+  const int rows = samples - s0 < 64 ? int(samples - s0) : 64;
+  const int cols = W - k0 < 64 ? int(W - k0) : 64;
+  for (int c = cw; c < cols; c += 4) {
+    Real v = Real(0);
+    const int64_t e = col_off[k0 + c + 1];
+    for (int64_t q = col_off[k0 + c]; q < e; ++q) v += P[row_ids[q] * ldp + s0 + lane];
+    tile[c][lane] = v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < rows * cols; i += 256) {
+    const int r = i / cols, c = i - r * cols;
+    gA[(s0 + r) * W + k0 + c] = Out(tile[c][r]);
+  }
+}
+}  // namespace ye3t
+}  // extern "C++"
+
+static void release_adjoint_parts(ye3t_hip_product_plan* p) {
+  for (int64_t i = 0; i < p->adj_count; ++i)
+    if (p->adj_modules[i]) (void)hipModuleUnload(p->adj_modules[i]);
+  delete[] p->adj_modules;
+  delete[] p->adj_fns;
+  delete[] p->adj_chunks;
+  (void)hipFree(p->adj_col_off);
+  (void)hipFree(p->adj_row_ids);
+  p->adj_modules = nullptr;
+  p->adj_fns = nullptr;
+  p->adj_chunks = nullptr;
+  p->adj_col_off = nullptr;
+  p->adj_row_ids = nullptr;
+  p->adj_count = 0;
+  p->adj_rows = 0;
+}
+
 static void release_parts(ye3t_hip_product_plan* p) {
   for (int k = 0; k < p->part_lanes; ++k) {
     (void)hipStreamDestroy(p->part_streams[k]);
@@ -1316,6 +1373,7 @@ void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* p) {
   if (p->readout_module) (void)hipModuleUnload(p->readout_module);
   if (p->adjoint_module) (void)hipModuleUnload(p->adjoint_module);
   release_parts(p);
+  release_adjoint_parts(p);
   (void)hipSetDevice(prev);
   delete p;
 }
@@ -1512,6 +1570,141 @@ int ye3t_hip_product_plan_attach_generated_parts(ye3t_hip_product_plan* p, int64
   }
   p->use_interpreter = 0;
   return YE3T_OK;
+}
+
+int ye3t_hip_product_plan_attach_adjoint_parts(ye3t_hip_product_plan* p, int64_t part_count,
+                                               const void* const* codes, const int64_t* sizes,
+                                               const char* const* kernel_names, const int64_t* chunk_counts,
+                                               int64_t partial_rows, const int64_t* col_off, const int64_t* row_ids) {
+  clear_error();
+  YE3T_REQUIRE(p && codes && sizes && kernel_names && chunk_counts && col_off, "NULL argument");
+  YE3T_REQUIRE(part_count >= 1 && part_count <= (int64_t(1) << 20), "part_count must be in [1, 2^20]");
+  YE3T_REQUIRE(partial_rows >= 0 && partial_rows < (int64_t(1) << 40), "bad partial row count");
+  const int64_t W = p->a_width;
+  YE3T_REQUIRE(col_off[0] == 0, "col_off[0] must be 0");
+  for (int64_t k = 0; k < W; ++k) YE3T_REQUIRE(col_off[k + 1] >= col_off[k], "col_off must be non-decreasing");
+  const int64_t nnz = col_off[W];
+  YE3T_REQUIRE(nnz == 0 || row_ids != nullptr, "NULL row_ids");
+  for (int64_t q = 0; q < nnz; ++q)
+    YE3T_REQUIRE(row_ids[q] >= 0 && row_ids[q] < partial_rows, "row id %lld out of range", (long long)q);
+  for (int64_t i = 0; i < part_count; ++i) {
+    YE3T_REQUIRE(codes[i] && sizes[i] > 0 && kernel_names[i], "NULL or empty part %lld", (long long)i);
+    YE3T_REQUIRE(chunk_counts[i] >= 1 && chunk_counts[i] <= 65535, "bad chunk count of part %lld", (long long)i);
+  }
+  int prev = 0;
+  YE3T_CHECK_HIP(hipGetDevice(&prev));
+  YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
+  int64_t* d_off = nullptr;
+  int64_t* d_ids = nullptr;
+  YE3T_CHECK_HIP(hipMalloc(&d_off, size_t(W + 1) * sizeof(int64_t)));
+  if (hipMalloc(&d_ids, size_t(nnz > 0 ? nnz : 1) * sizeof(int64_t)) != hipSuccess) {
+    (void)hipFree(d_off);
+    return set_error(YE3T_ENOMEM, "device allocation failed");
+  }
+  if (hipMemcpy(d_off, col_off, size_t(W + 1) * sizeof(int64_t), hipMemcpyHostToDevice) != hipSuccess ||
+      (nnz > 0 && hipMemcpy(d_ids, row_ids, size_t(nnz) * sizeof(int64_t), hipMemcpyHostToDevice) != hipSuccess)) {
+    (void)hipFree(d_off);
+    (void)hipFree(d_ids);
+    return set_error(YE3T_ELAUNCH, "copying the reduction map failed");
+  }
+  auto* modules = new hipModule_t[size_t(part_count)]();
+  auto* fns = new hipFunction_t[size_t(part_count)]();
+  auto* chunks = new int64_t[size_t(part_count)];
+  for (int64_t i = 0; i < part_count; ++i) {
+    chunks[i] = chunk_counts[i];
+    hipError_t e = hipModuleLoadData(&modules[i], codes[i]);
+    if (e == hipSuccess && hipModuleGetFunction(&fns[i], modules[i], kernel_names[i]) != hipSuccess)
+      e = hipErrorNotFound;
+    if (e != hipSuccess) {
+      for (int64_t j = 0; j <= i; ++j)
+        if (modules[j]) (void)hipModuleUnload(modules[j]);
+      delete[] modules;
+      delete[] fns;
+      delete[] chunks;
+      (void)hipFree(d_off);
+      (void)hipFree(d_ids);
+      return set_error(YE3T_EINVAL, "adjoint part %lld: code object not loadable or kernel %s not found",
+                       (long long)i, kernel_names[i]);
+    }
+  }
+  release_adjoint_parts(p);
+  p->adj_modules = modules;
+  p->adj_fns = fns;
+  p->adj_chunks = chunks;
+  p->adj_count = part_count;
+  p->adj_rows = partial_rows;
+  p->adj_col_off = d_off;
+  p->adj_row_ids = d_ids;
+  return YE3T_OK;
+}
+
+int64_t ye3t_hip_product_adjoint_parts_workspace_bytes(const ye3t_hip_product_plan* p, int64_t samples) {
+  clear_error();
+  if (!p || samples < 0) {
+    set_error(YE3T_EINVAL, "NULL plan or negative sample count");
+    return -1;
+  }
+  if (p->adj_count == 0 || samples == 0) return 0;
+  const int64_t ldp = (samples + kLanes - 1) / kLanes * kLanes;
+  return p->adj_rows * ldp * int64_t(p->dtype == YE3T_F64 ? 8 : 4);
+}
+
+int ye3t_hip_product_adjoint_parts(const ye3t_hip_product_plan* p, const void* A, int64_t lda, int columns,
+                                   const void* gB, int64_t samples, void* workspace, int64_t workspace_bytes,
+                                   void* gA, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(p != nullptr, "NULL plan");
+  YE3T_REQUIRE(samples >= 0, "negative sample count");
+  if (samples == 0) return YE3T_OK;
+  YE3T_REQUIRE(p->adj_count > 0, "no adjoint parts attached");
+  YE3T_REQUIRE(A && gB && gA, "NULL input or output");
+  const int64_t tiles = (samples + kLanes - 1) / kLanes;
+  if (columns) {
+    YE3T_REQUIRE(lda >= samples, "lda must cover the samples");
+  } else {
+    YE3T_REQUIRE(lda == p->a_width, "a row-major density has lda == a_width");
+  }
+  const int64_t ldp = tiles * kLanes;
+  const int64_t need = p->adj_rows * ldp * int64_t(p->dtype == YE3T_F64 ? 8 : 4);
+  YE3T_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace of %lld bytes needed", (long long)need);
+  const int64_t gx = (tiles + 7) & ~int64_t(7);  // the parts deal tiles to XCDs by linear workgroup id
+  YE3T_REQUIRE(gx <= int64_t(0x7FFFFFF8), "too many samples for one launch");
+  const hipStream_t s = as_stream(stream);
+  long s_arg = long(samples), rs_arg = long(columns ? 1 : p->a_width), cs_arg = long(columns ? lda : 1);
+  long ldp_arg = long(ldp);
+  const void* a_arg = A;
+  const void* g_arg = gB;
+  void* w_arg = workspace;
+  void* args[] = {&a_arg, &g_arg, &s_arg, &w_arg, &rs_arg, &cs_arg, &ldp_arg};
+  const int lanes = p->part_lanes;
+  if (lanes > 1) {
+    YE3T_CHECK_HIP(hipEventRecord(p->part_fork, s));
+    for (int k = 0; k < lanes; ++k) YE3T_CHECK_HIP(hipStreamWaitEvent(p->part_streams[k], p->part_fork, 0));
+  }
+  for (int64_t i = 0; i < p->adj_count; ++i)
+    YE3T_CHECK_HIP(hipModuleLaunchKernel(p->adj_fns[i], unsigned(gx), unsigned(p->adj_chunks[i]), 1, kLanes, 1, 1, 0,
+                                         lanes > 1 ? p->part_streams[i % lanes] : s, args, nullptr));
+  if (lanes > 1) {
+    for (int k = 0; k < lanes; ++k) {
+      YE3T_CHECK_HIP(hipEventRecord(p->part_join[k], p->part_streams[k]));
+      YE3T_CHECK_HIP(hipStreamWaitEvent(s, p->part_join[k], 0));
+    }
+  }
+  const dim3 grid = dim3(unsigned(tiles), unsigned((p->a_width + 63) / 64)), block = dim3(256);
+  if (p->dtype == YE3T_F64 && p->in_dtype == YE3T_F64) {
+    hipLaunchKernelGGL((adjoint_parts_reduce_kernel<double, double>), grid, block, 0, s,
+                       static_cast<const double*>(workspace), ldp, p->adj_col_off, p->adj_row_ids, p->a_width,
+                       samples, static_cast<double*>(gA));
+  } else if (p->dtype == YE3T_F64) {
+    hipLaunchKernelGGL((adjoint_parts_reduce_kernel<double, float>), grid, block, 0, s,
+                       static_cast<const double*>(workspace), ldp, p->adj_col_off, p->adj_row_ids, p->a_width,
+                       samples, static_cast<float*>(gA));
+  } else {
+    hipLaunchKernelGGL((adjoint_parts_reduce_kernel<float, float>), grid, block, 0, s,
+                       static_cast<const float*>(workspace), ldp, p->adj_col_off, p->adj_row_ids, p->a_width,
+                       samples, static_cast<float*>(gA));
+  }
+  return check_launch("adjoint_parts_reduce_kernel");
 }
 
 int ye3t_hip_product_plan_select(ye3t_hip_product_plan* p, int use_interpreter) {
