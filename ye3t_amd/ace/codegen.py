@@ -801,14 +801,25 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
             for n in sorted(needed):
                 for c in range(nodes[n]["dim"]):
                     w(f"      REAL g{n}_{c} = (REAL)0;")
-            # the chunk's output gradients, `group` columns at a time
+            # the chunk's output gradients, `group` columns at a time: a fixed,
+            # unrolled set of loads (rows past the tile re-read its last row),
+            # all issued before the LDS writes
             for g0 in range(first, last, group):
                 g1 = min(g0 + group, last)
                 width = g1 - g0
                 w("      __syncthreads();")
-                w(f"      for (int i = lane; i < rows * {width}; i += 64) {{")
-                w(f"        const int r = i / {width}, c = i - r * {width};")
-                w(f"        st[c][r] = gB[(s0 + r) * {F}L + {g0} + c];")
+                w("      {")
+                w(f"        GT t[{width}];")
+                w("#pragma unroll")
+                w(f"        for (int u = 0; u < {width}; ++u) {{")
+                w(f"          const int i = lane + 64 * u, r = i / {width}, c = i - r * {width};")
+                w(f"          t[u] = gB[(s0 + (r < rows ? r : rows - 1)) * {F}L + {g0} + c];")
+                w("        }")
+                w("#pragma unroll")
+                w(f"        for (int u = 0; u < {width}; ++u) {{")
+                w(f"          const int i = lane + 64 * u, r = i / {width}, c = i - r * {width};")
+                w("          st[c][r] = t[u];")
+                w("        }")
                 w("      }")
                 w("      __syncthreads();")
                 for f in range(g0, g1):

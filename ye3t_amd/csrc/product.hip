@@ -1302,10 +1302,24 @@ __global__ __launch_bounds__(256) void adjoint_parts_reduce_kernel(const Real* _
   const int64_t s0 = int64_t(blockIdx.x) * 64, k0 = int64_t(blockIdx.y) * 64;
   const int rows = samples - s0 < 64 ? int(samples - s0) : 64;
   const int cols = W - k0 < 64 ? int(W - k0) : 64;
+  // the map is wave-uniform: read through the scalar cache; eight partial rows
+  // in flight per step, added in the listed order
+  typedef const __attribute__((address_space(4))) int64_t* cptr;
+  const cptr off = (cptr)(col_off);
+  const cptr ids = (cptr)(row_ids);
+  const Real* __restrict__ Ps = P + s0 + lane;
   for (int c = cw; c < cols; c += 4) {
     Real v = Real(0);
-    const int64_t e = col_off[k0 + c + 1];
-    for (int64_t q = col_off[k0 + c]; q < e; ++q) v += P[row_ids[q] * ldp + s0 + lane];
+    int64_t q = off[k0 + c];
+    const int64_t e = off[k0 + c + 1];
+    for (; q + 8 <= e; q += 8) {
+      Real t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = Ps[ids[q + u] * ldp];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v += t[u];
+    }
+    for (; q < e; ++q) v += Ps[ids[q] * ldp];
     tile[c][lane] = v;
   }
   __syncthreads();
