@@ -36,8 +36,12 @@ def to_device_inputs(inp, dtype, device="cuda"):
 # larger plans run the generic interpreter (hipRTC time grows with code size)
 GENERATED_MAX_TERMS = 5000
 # plans up to this size run on a generated kernel in parts (one hipRTC module per
-# 9 chunks, compiled once and cached); larger ones on the interpreter
-PARTS_MAX_TERMS = 200000
+# 9 chunks, compiled once and cached: config 5's 1.32 M terms are 143 parts);
+# larger ones on the interpreter
+PARTS_MAX_TERMS = 2000000
+# the reverse mode runs in parts up to this plan size (config 3: 196 parts), above
+# it on the term stream's reverse mode
+ADJOINT_PARTS_MAX_TERMS = 200000
 # the reverse mode's parts: chunks of fewer node values (values and gradients are
 # live together; 128 compiles without spills at config 2) and chunks per part
 ADJOINT_PART_MAX_LIVE = 128
@@ -78,6 +82,7 @@ class ACEPipeline:
             raise ValueError(f"unknown product kernel {kernel!r}")
         self.plan = plan if plan is not None else ProductPlan(feature_spec)
         terms = sum(len(nd.get("terms", ())) for nd in self.plan.nodes)
+        self._terms = terms
         use_gen = kernel == "generated" or (kernel == "auto" and terms <= GENERATED_MAX_TERMS)
         use_parts = kernel == "parts" or (kernel == "auto" and not use_gen and terms <= PARTS_MAX_TERMS)
         if self.density_dtype != self.accumulate and not (use_gen or use_parts):
@@ -170,7 +175,7 @@ class ACEPipeline:
         term stream's reverse mode on the column-major density.  Plans whose
         workspace is too wide for the term stream raise ``NotImplementedError``."""
         self.last_adjoint_backend = None
-        if self.kernel == "parts":
+        if self.kernel == "parts" and self._terms <= ADJOINT_PARTS_MAX_TERMS:
             return self._adjoint_parts(A_rows, gB, out)
         if self.kernel != "generated":
             if self._adjoint_handle is None:

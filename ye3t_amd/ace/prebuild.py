@@ -8,7 +8,7 @@ no GPU, so this runs on a build host; the code objects land in the JIT cache
 (``ye3t_amd/jit_cache`` unless ``YE3T_AMD_JIT_CACHE`` says otherwise), keyed by
 source hash, and travel with the tree.
 
-    python -m ye3t_amd.ace.prebuild            # configs 2 and 3, every dtype they are benchmarked in
+    python -m ye3t_amd.ace.prebuild            # configs 2, 3 and 5, every dtype they are benchmarked in
     python -m ye3t_amd.ace.prebuild 2 --dtype f64
 """
 
@@ -34,11 +34,11 @@ def _compile(source):
     return len(source)
 
 
-def prebuild(config_ids=(2, 3), dtypes=None, workers=None, log=print):
+def prebuild(config_ids=(2, 3, 5), dtypes=None, workers=None, log=print):
     from ye3t_amd.ace import workloads as W
     from ye3t_amd.ace.codegen import generate_adjoint_parts, generate_parts
-    from ye3t_amd.ace.pipeline import (ADJOINT_PART_CHUNKS, ADJOINT_PART_MAX_LIVE, GENERATED_MAX_TERMS,
-                                       PARTS_MAX_TERMS)
+    from ye3t_amd.ace.pipeline import (ADJOINT_PART_CHUNKS, ADJOINT_PART_MAX_LIVE, ADJOINT_PARTS_MAX_TERMS,
+                                       GENERATED_MAX_TERMS, PARTS_MAX_TERMS)
     from ye3t_amd.ace.plan import ProductPlan
     from ye3t_amd.runtime import native
 
@@ -53,9 +53,11 @@ def prebuild(config_ids=(2, 3), dtypes=None, workers=None, log=print):
         for dtype in dtypes or cfg.dtypes:
             accumulate, density = precisions(cfg, dtype)
             parts = generate_parts(plan, accumulate, out_dtype=dtype, in_dtype=density)
-            adjoint, _ = generate_adjoint_parts(plan, accumulate, max_live=ADJOINT_PART_MAX_LIVE,
-                                                chunks_per_part=ADJOINT_PART_CHUNKS, grad_dtype=dtype,
-                                                in_dtype=density)
+            adjoint = []
+            if terms <= ADJOINT_PARTS_MAX_TERMS:
+                adjoint, _ = generate_adjoint_parts(plan, accumulate, max_live=ADJOINT_PART_MAX_LIVE,
+                                                    chunks_per_part=ADJOINT_PART_CHUNKS, grad_dtype=dtype,
+                                                    in_dtype=density)
             t0 = time.time()
             # worker processes (spawned: nothing of this process is inherited) compile in parallel
             with ProcessPoolExecutor(workers, mp_context=multiprocessing.get_context("spawn")) as pool:
@@ -66,7 +68,7 @@ def prebuild(config_ids=(2, 3), dtypes=None, workers=None, log=print):
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("configs", nargs="*", type=int, default=[2, 3])
+    ap.add_argument("configs", nargs="*", type=int, default=[2, 3, 5])
     ap.add_argument("--dtype", action="append", help="storage dtype (default: every dtype of the config)")
     ap.add_argument("--workers", type=int, default=None)
     args = ap.parse_args(argv)
