@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 57 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 58 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -340,6 +340,34 @@ int64_t ye3t_hip_product_adjoint_parts_workspace_bytes(const ye3t_hip_product_pl
 int ye3t_hip_product_adjoint_parts(const ye3t_hip_product_plan* plan, const void* A, int64_t lda, int columns,
                                    const void* gB, int64_t samples, void* workspace, int64_t workspace_bytes,
                                    void* gA, ye3t_stream_t stream);
+
+/* Fused linear readout of a plan in parts (code objects of
+ * ye3t_amd/ace/codegen.py:generate_readout_parts, kernel signature
+ * (const T* A, long samples, R* P, const R* W, long row_stride,
+ * long col_stride, long ldp)): part i writes, for each of its chunk_counts[i]
+ * chunks, the chunk's partial dot product sum_{k in chunk} W[k] B[s, k] as one
+ * row of P.  No reference counterpart: the plan-specialised form of the
+ * reference's factorized_angular_linear (execution_plan.py:13793-13850) for
+ * the plans of ye3t_hip_product_plan_attach_generated_parts. */
+int ye3t_hip_product_plan_attach_readout_parts(ye3t_hip_product_plan* plan, int64_t part_count,
+                                               const void* const* codes, const int64_t* sizes,
+                                               const char* const* kernel_names, const int64_t* chunk_counts);
+
+/* Bytes of the partial buffer ye3t_hip_product_linear_forward_parts needs
+ * (chunks x samples rounded up to 64 x the plan's element size); 0 without
+ * readout parts, -1 on error. */
+int64_t ye3t_hip_product_linear_parts_workspace_bytes(const ye3t_hip_product_plan* plan, int64_t samples);
+
+/* out[s] = bias + sum_k B[s, k] weight[k] on the attached readout parts,
+ * without materialising B: A row-major [samples, a_width] (lda == a_width) or,
+ * with `columns`, column-major [a_width, lda] (lda >= samples); weight
+ * [feature_count] of the plan's dtype; out of its out_dtype.  The parts run on
+ * the plan's streams, then one reduction adds the bias and the chunks' rows in
+ * chunk order.  Replaces the same reference op as
+ * ye3t_hip_product_linear_forward. */
+int ye3t_hip_product_linear_forward_parts(const ye3t_hip_product_plan* plan, const void* A, int64_t lda, int columns,
+                                          int64_t samples, const void* weight, double bias, void* workspace,
+                                          int64_t workspace_bytes, void* out, ye3t_stream_t stream);
 
 /* Attach a plan-specialised fused linear readout kernel (code object of
  * ye3t_amd/ace/codegen.py:generate_readout compiled with ye3t_hip_rtc_compile).

@@ -364,16 +364,19 @@ def test_end_to_end_small(gpu, cid, dtype, atoms):
     assert err < TOL[dtype]
 
 
-@pytest.mark.parametrize("cid,dtype,atoms", [(4, "f32", 257), (2, "f64", 129)])
-def test_linear_readout(gpu, cid, dtype, atoms):
-    """Fused (generated plans) and block-materialised (interpreted plans) readouts vs B_ref @ w + bias."""
-    flush(f"linear readout config {cid} {dtype} atoms={atoms}")
+@pytest.mark.parametrize("cid,dtype,atoms,kernel", [(4, "f32", 257, "auto"), (2, "f64", 129, "auto"),
+                                                   (3, "f32", 67, "auto"), (2, "f64", 129, "interpreter")])
+def test_linear_readout(gpu, cid, dtype, atoms, kernel):
+    """Fused (generated plans, whole or in parts) and block-materialised
+    (interpreted plans) readouts vs B_ref @ w + bias."""
+    flush(f"linear readout config {cid} {dtype} atoms={atoms} kernel={kernel}")
     import torch
 
     cfg = W.config(cid, atom_count=atoms)
     inp = cfg.density.generate()
-    pipe = ACEPipeline(cfg.feature_spec, dtype, accumulate=cfg.accumulate if dtype == "f32" else None,
-                       density=cfg.density_dtype if dtype == "f32" else None)
+    f32 = dtype == "f32"
+    pipe = ACEPipeline(cfg.feature_spec, dtype, kernel=kernel, accumulate=cfg.accumulate if f32 else None,
+                       density=cfg.density_dtype if f32 and kernel != "interpreter" else None)
     A = pipe.density(to_device_inputs(inp, dtype, gpu))
     rows = A.reshape(-1, pipe.plan.a_width)
     F = pipe.feature_count
@@ -382,7 +385,7 @@ def test_linear_readout(gpu, cid, dtype, atoms):
     got = pipe.linear(rows, torch.as_tensor(w, device=gpu), 0.37)
     backend = pipe.last_linear_backend
     flush(f"  backend {backend}")
-    assert backend == ("fused_generated" if pipe.kernel == "generated" else "materialized_blocks")
+    assert backend == {"generated": "fused_generated", "parts": "fused_parts"}.get(pipe.kernel, "materialized_blocks")
     A_ref = oracle.ace_density(rounded_inputs(inp, dtype)).reshape(-1, pipe.plan.a_width)
     ref = oracle.linear_readout(oracle.ace_product_flat(A_ref, pipe.plan.flat_arrays()), w, 0.37)
     rms = float(np.sqrt(np.mean(ref * ref)))

@@ -156,3 +156,31 @@ def test_adjoint_parts_reduction_map():
         assert written == list(range(meta["first_row"], meta["last_row"]))
         first = meta["last_row"]
     assert first == red["partial_rows"]
+
+
+def test_readout_parts_weight_every_feature_once():
+    """``codegen.generate_readout_parts``: the parts use the chunks of the
+    forward parts, every feature's weight enters exactly one chunk's partial
+    sum, each chunk writes its own partial row, and the features are emitted
+    with the same text as the forward parts (so they agree bit for bit)."""
+    import re
+
+    from ye3t_amd.ace import codegen
+
+    plan = ProductPlan(W.config(4).feature_spec)
+    chunks = codegen._chunks(plan, 96)
+    parts, count = codegen.generate_readout_parts(plan, "f64", max_live=96, chunks_per_part=3)
+    assert count == len(chunks) and len(parts) == -(-count // 3)
+    weights, rows = [], []
+    for src, meta in parts:
+        assert meta["kernel"] == "ye3t_product_readout_part" and src.count("  case ") == meta["chunks"]
+        weights += [int(g) for g in re.findall(r"W\[(\d+)\]", src)]
+        rows += [int(g) for g in re.findall(r"P\[(\d+)L \* ldp \+ s\]", src)]
+    assert sorted(weights) == list(range(plan.feature_count))
+    assert rows == list(range(count))
+    fwd = "\n".join(s for s, _ in codegen.generate_parts(plan, "f64", max_live=96, chunks_per_part=3))
+    node_lines = {ln.strip() for ln in fwd.splitlines() if ln.strip().startswith("const REAL v")}
+    for src, _ in parts:
+        for ln in src.splitlines():
+            if ln.strip().startswith("const REAL v"):
+                assert ln.strip() in node_lines

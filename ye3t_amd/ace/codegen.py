@@ -157,6 +157,53 @@ def _emit_node_code(w, nodes, n, emitted, dtype, src, lit=None):
         w(f"      const REAL v{n}_{c} = {chains[0]};")
 
 
+def _emit_one_chain(w, nodes, n, emitted, dtype, leaf, indent="    "):
+    """Emit node ``n`` (and its dependencies) as straight-line register code,
+    one fma chain per component: terms grouped by their first factor,
+    ``sum_a x_a * (sum c * rest)``.  ``leaf(c)`` is the expression of density
+    column ``c``.  The generated parts and their fused readout share it, so a
+    feature has the same bits in both."""
+    if n in emitted:
+        return
+    nd = nodes[n]
+    for d in nd["deps"]:
+        _emit_one_chain(w, nodes, d, emitted, dtype, leaf, indent)
+    emitted.add(n)
+    fma = "fma" if dtype == "f64" else "fmaf"
+    if nd["kind"] == "leaf":
+        for c in range(nd["dim"]):
+            w(f"{indent}const REAL v{n}_{c} = {leaf(nd['a_offset'] + c)};")
+        return
+    per = [[] for _ in range(nd["dim"])]
+    if nd["kind"] == "sym":
+        src = nd["deps"][0]
+        for oc, value, factors in nd["terms"]:
+            per[oc].append((value, tuple(f"v{src}_{q}" for q in factors)))
+    else:
+        da, db = nd["deps"]
+        for oc, value, (i, j) in nd["terms"]:
+            per[oc].append((value, (f"v{da}_{i}", f"v{db}_{j}")))
+    for c, terms in enumerate(per):
+        if not terms:
+            w(f"{indent}const REAL v{n}_{c} = (REAL)0;")
+            continue
+        groups = {}
+        for value, fac in terms:
+            groups.setdefault(fac[0], []).append((value, fac[1:]))
+        parts = []
+        for head, rest in groups.items():
+            inner = None
+            for value, tail in rest:
+                prod = " * ".join(tail) if tail else "(REAL)1"
+                inner = (f"{_lit(value, dtype)} * {prod}" if inner is None
+                         else f"{fma}({_lit(value, dtype)}, {prod}, {inner})")
+            parts.append((head, inner))
+        expr = None
+        for head, inner in parts:
+            expr = f"{head} * ({inner})" if expr is None else f"{fma}({head}, {inner}, {expr})"
+        w(f"{indent}const REAL v{n}_{c} = {expr};")
+
+
 def _split_outputs(plan, parts):
     """Contiguous output ranges of about equal arithmetic (terms of the nodes
     each range computes, shared nodes counted in every range that needs them)."""
@@ -586,50 +633,13 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
         w(f"  case {ci}: {{")
         emitted = set()
 
+        # unconditional loads: lanes past the last sample read sample 0 (a valid
+        # address) and their outputs are never stored; a select per load would
+        # turn each into a branch that waits for its own data
+        leaf = (lambda c: f"(REAL)a[{c}L * col_stride]") if strided else (lambda c: f"(REAL)a[{c}]")
+
         def emit(n):
-            if n in emitted:
-                return
-            nd = nodes[n]
-            for d in nd["deps"]:
-                emit(d)
-            emitted.add(n)
-            if nd["kind"] == "leaf":
-                for c in range(nd["dim"]):
-                    # unconditional: lanes past the last sample read sample 0 (a valid
-                    # address) and their outputs are never stored; a select per load
-                    # would turn each into a branch that waits for its own data
-                    at = f"{nd['a_offset'] + c}L * col_stride" if strided else f"{nd['a_offset'] + c}"
-                    w(f"    const REAL v{n}_{c} = (REAL)a[{at}];")
-                return
-            per = [[] for _ in range(nd["dim"])]
-            if nd["kind"] == "sym":
-                src = nd["deps"][0]
-                for oc, value, factors in nd["terms"]:
-                    per[oc].append((value, tuple(f"v{src}_{q}" for q in factors)))
-            else:
-                da, db = nd["deps"]
-                for oc, value, (i, j) in nd["terms"]:
-                    per[oc].append((value, (f"v{da}_{i}", f"v{db}_{j}")))
-            for c, terms in enumerate(per):
-                if not terms:
-                    w(f"    const REAL v{n}_{c} = (REAL)0;")
-                    continue
-                # group by the first factor: sum_a x_a * (sum c * rest)
-                groups = {}
-                for value, fac in terms:
-                    groups.setdefault(fac[0], []).append((value, fac[1:]))
-                parts = []
-                for head, rest in groups.items():
-                    inner = None
-                    for value, tail in rest:
-                        prod = " * ".join(tail) if tail else "(REAL)1"
-                        inner = (f"{_lit(value, dtype)} * {prod}" if inner is None
-                                 else f"{fma}({_lit(value, dtype)}, {prod}, {inner})")
-                    parts.append((head, inner))
-                expr = None
-                for head, inner in parts:
-                    expr = f"{head} * ({inner})" if expr is None else f"{fma}({head}, {inner}, {expr})"
-                w(f"    const REAL v{n}_{c} = {expr};")
+            _emit_one_chain(w, nodes, n, emitted, dtype, leaf)
 
         if strided:
             # every density value of the chunk requested up front (independent loads in flight together)
@@ -862,3 +872,83 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
                 "hash": hashlib.sha256(source.encode()).hexdigest()[:16]}
         parts.append((source, meta))
     return parts, {"partial_rows": row_base[-1], "col_off": col_off, "rows": rows}
+
+
+def generate_readout_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per_part=PART_CHUNKS, in_dtype=None):
+    """Fused linear readout of a plan in parts: ``out[s] = bias + sum_k B[s, k]
+    weight[k]`` without writing B (counterpart of the reference's
+    ``factorized_angular_linear``, ``execution_plan.py:13793-13850``).
+
+    The chunks and parts are those of :func:`generate_parts`.  For each tile
+    of 64 samples a chunk computes its outputs in registers (density through
+    row and column strides) and writes ``sum_{k in chunk} weight[k] B[s, k]``
+    to row ``chunk`` of a partial buffer ``P[chunk * ldp + s]``; the weights
+    are read through the scalar cache.  A reduction adds the bias and the
+    chunks' rows in chunk order.  Kernel signature: ``(const AIN* A, long
+    samples, REAL* P, const REAL* W, long row_stride, long col_stride, long
+    ldp)``.  Returns ``(parts, chunk_count)``.
+    """
+    in_dtype = _check_in_dtype(dtype, in_dtype)
+    if chunks_per_part < 1:
+        raise ValueError("chunks_per_part must be positive")
+    real = "double" if dtype == "f64" else "float"
+    fma = "fma" if dtype == "f64" else "fmaf"
+    nodes = plan.nodes
+    F, Wd = plan.feature_count, plan.a_width
+    chunks = _chunks(plan, max_live)
+    parts = []
+    for p0 in range(0, len(chunks), chunks_per_part):
+        sub = list(range(p0, min(len(chunks), p0 + chunks_per_part)))
+        out = []
+        w = out.append
+        w("// generated by ye3t_amd.ace.codegen (readout part) -- do not edit (compiled with hipRTC)")
+        w(f"#define REAL {real}")
+        w(f"#define AIN {_ctype(in_dtype)}")
+        w("typedef const __attribute__((address_space(4))) REAL* wptr;")
+        w("extern \"C\" __global__ __launch_bounds__(64) void ye3t_product_readout_part(")
+        w("    const AIN* __restrict__ A, long samples, REAL* __restrict__ P, const REAL* __restrict__ Wt,")
+        w("    long row_stride, long col_stride, long ldp) {")
+        w("  const int lane = threadIdx.x;")
+        w("  const wptr W = (wptr)Wt;")
+        w("  const long wg = (long)blockIdx.y * gridDim.x + blockIdx.x;")
+        w("  const long per = gridDim.x >> 3, k = wg >> 3;")
+        w("  const long tile = (wg & 7) * per + k % per;")
+        w("  const int chunk = (int)(k / per);")
+        w("  const long s0 = tile * 64;")
+        w("  if (s0 >= samples) return;")
+        w("  const long s = s0 + lane;")
+        w("  const AIN* __restrict__ a = A + (s < samples ? s : 0) * row_stride;")
+        w("  switch (chunk) {")
+        for lc, ci in enumerate(sub):
+            first, last, members = chunks[ci]
+            w(f"  case {lc}: {{")
+            emitted = set()
+            leaf = lambda c: f"(REAL)a[{c}L * col_stride]"  # noqa: E731
+            for n in sorted((m for m in members if nodes[m]["kind"] == "leaf"), key=lambda m: nodes[m]["a_offset"]):
+                _emit_one_chain(w, nodes, n, emitted, dtype, leaf, "      ")
+            # the chunk's dot product as CHAINS independent partial sums, added in a fixed
+            # order; the features are computed exactly as the forward parts compute them
+            names = [None] * min(CHAINS, last - first)
+            for f in range(first, last):
+                root, comp = plan.outputs[f]
+                _emit_one_chain(w, nodes, root, emitted, dtype, leaf, "      ")
+                j = (f - first) % len(names)
+                prev = names[j]
+                expr = f"W[{f}] * v{root}_{comp}" if prev is None else f"{fma}(W[{f}], v{root}_{comp}, {prev})"
+                w(f"      const REAL r{j}_{f} = {expr};")
+                names[j] = f"r{j}_{f}"
+            total = names[0]
+            for x in names[1:]:
+                total = f"({total} + {x})"
+            w(f"      P[{ci}L * ldp + s] = {total};")
+            w("      break;")
+            w("  }")
+        w("  default: break;")
+        w("  }")
+        w("}")
+        source = "\n".join(out) + "\n"
+        meta = {"kernel": "ye3t_product_readout_part", "chunks": len(sub), "feature_count": F, "a_width": Wd,
+                "dtype": dtype, "in_dtype": in_dtype, "first_chunk": sub[0],
+                "hash": hashlib.sha256(source.encode()).hexdigest()[:16]}
+        parts.append((source, meta))
+    return parts, len(chunks)

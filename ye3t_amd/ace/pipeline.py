@@ -251,10 +251,11 @@ class ACEPipeline:
         """Linear readout ``out[s] = bias + sum_k B[s, k] weight[k]`` (reference
         ``factorized_angular_linear``, ``execution_plan.py:13793-13850``).
 
-        Plans with a generated product kernel use a fused, plan-specialised
-        readout kernel that never stores B (compiled on first use).  Larger
-        plans materialise B in sample blocks of at most ``block_bytes`` and
-        reduce each row with ``rows_dot`` (the reference's materialised path).
+        Plans with a generated product kernel, whole or in parts, use a fused,
+        plan-specialised readout that never stores B (compiled on first use).
+        Interpreter plans materialise B in sample blocks of at most
+        ``block_bytes`` and reduce each row with ``rows_dot`` (the reference's
+        materialised path).
         ``last_linear_backend`` records which ran.
         """
         import torch
@@ -267,6 +268,25 @@ class ACEPipeline:
         out_t = torch.float64 if self.dtype == "f64" else torch.float32
         if out is None:
             out = torch.empty((S,), dtype=out_t, device=A_rows.device)
+        if self.kernel == "parts":
+            from ye3t_amd.ace.codegen import PART_CHUNKS, PART_MAX_LIVE, generate_readout_parts
+
+            if getattr(self.handle, "readout_part_meta", None) is None:
+                live = int(os.environ.get("YE3T_PARTS_MAX_LIVE", PART_MAX_LIVE))
+                per = int(os.environ.get("YE3T_PARTS_CHUNKS", PART_CHUNKS))
+                parts, _ = generate_readout_parts(self.plan, self.accumulate, max_live=live, chunks_per_part=per,
+                                                  in_dtype=self.density_dtype)
+                self.handle.attach_readout_parts(parts)
+            w = weight.to(torch.float64 if self.accumulate == "f64" else torch.float32).contiguous()
+            if S == 0:
+                return out
+            ld = (S + 63) // 64 * 64
+            key = (int(A_rows.shape[1]), ld, A_rows.dtype, A_rows.device)
+            if self._At is None or self._At[0] != key:
+                self._At = (key, torch.empty((key[0], ld), dtype=A_rows.dtype, device=A_rows.device))
+            At = native.transpose(A_rows.contiguous(), out=self._At[1], ld=ld)
+            self.last_linear_backend = "fused_parts"
+            return self.handle.linear_parts(At, w, float(bias), samples=S, columns=True, out=out)
         if self.kernel == "generated":
             if getattr(self.handle, "readout", None) is None:
                 from ye3t_amd.ace.codegen import generate_readout

@@ -1,8 +1,9 @@
 """Compile the generated product kernels of benchmark configurations ahead of use.
 
 Plans between ``GENERATED_MAX_TERMS`` and ``PARTS_MAX_TERMS`` terms run on a
-generated kernel in parts (``codegen.generate_parts``), one hipRTC module per
-9 chunks.  hipRTC compiles one module at a time per process (~15 s for a
+generated kernel in parts (``codegen.generate_parts``, with the reverse sweep
+``generate_adjoint_parts`` and the fused readout ``generate_readout_parts``),
+one hipRTC module per 9 chunks.  hipRTC compiles one module at a time per process (~15 s for a
 config-3 part), so the parts are spread over worker processes.  hipRTC needs
 no GPU, so this runs on a build host; the code objects land in the JIT cache
 (``ye3t_amd/jit_cache`` unless ``YE3T_AMD_JIT_CACHE`` says otherwise), keyed by
@@ -36,7 +37,7 @@ def _compile(source):
 
 def prebuild(config_ids=(2, 3, 5), dtypes=None, workers=None, log=print):
     from ye3t_amd.ace import workloads as W
-    from ye3t_amd.ace.codegen import generate_adjoint_parts, generate_parts
+    from ye3t_amd.ace.codegen import generate_adjoint_parts, generate_parts, generate_readout_parts
     from ye3t_amd.ace.pipeline import (ADJOINT_PART_CHUNKS, ADJOINT_PART_MAX_LIVE, ADJOINT_PARTS_MAX_TERMS,
                                        GENERATED_MAX_TERMS, PARTS_MAX_TERMS)
     from ye3t_amd.ace.plan import ProductPlan
@@ -53,6 +54,7 @@ def prebuild(config_ids=(2, 3, 5), dtypes=None, workers=None, log=print):
         for dtype in dtypes or cfg.dtypes:
             accumulate, density = precisions(cfg, dtype)
             parts = generate_parts(plan, accumulate, out_dtype=dtype, in_dtype=density)
+            readout, _ = generate_readout_parts(plan, accumulate, in_dtype=density)
             adjoint = []
             if terms <= ADJOINT_PARTS_MAX_TERMS:
                 adjoint, _ = generate_adjoint_parts(plan, accumulate, max_live=ADJOINT_PART_MAX_LIVE,
@@ -61,9 +63,10 @@ def prebuild(config_ids=(2, 3, 5), dtypes=None, workers=None, log=print):
             t0 = time.time()
             # worker processes (spawned: nothing of this process is inherited) compile in parallel
             with ProcessPoolExecutor(workers, mp_context=multiprocessing.get_context("spawn")) as pool:
-                list(pool.map(_compile, [part[0] for part in parts + adjoint]))
-            log(f"config {cid} {dtype} (arithmetic {accumulate}, density {density}): {len(parts)} forward and "
-                f"{len(adjoint)} adjoint parts in {time.time() - t0:.1f} s -> {native._jit_cache_dir()}")
+                list(pool.map(_compile, [part[0] for part in parts + adjoint + readout]))
+            log(f"config {cid} {dtype} (arithmetic {accumulate}, density {density}): {len(parts)} forward, "
+                f"{len(adjoint)} adjoint and {len(readout)} readout parts in {time.time() - t0:.1f} s "
+                f"-> {native._jit_cache_dir()}")
 
 
 def main(argv=None):

@@ -68,6 +68,13 @@ struct ye3t_hip_product_plan {
   int64_t adj_rows;
   int64_t* adj_col_off;  // device [a_width + 1]
   int64_t* adj_row_ids;  // device [adj_col_off[a_width]]
+  // fused linear readout in parts: part i writes the partial dot products of
+  // ro_chunks[i] chunks as rows of P[ro_total][ldp]
+  int64_t ro_count;
+  hipModule_t* ro_modules;
+  hipFunction_t* ro_fns;
+  int64_t* ro_chunks;
+  int64_t ro_total;
   int use_interpreter;
   // plan-specialised fused linear readout (optional)
   hipModule_t readout_module;
@@ -1328,8 +1335,40 @@ __global__ __launch_bounds__(256) void adjoint_parts_reduce_kernel(const Real* _
     gA[(s0 + r) * W + k0 + c] = Out(tile[c][r]);
   }
 }
+// out[s] = bias + sum over rows c < rows of P[c * ldp + s], in row order
+template <typename Real, typename Out>
+__global__ __launch_bounds__(256) void readout_parts_reduce_kernel(const Real* __restrict__ P, int64_t ldp,
+                                                                   int64_t rows, Real bias, int64_t samples,
+                                                                   Out* __restrict__ out) {
+  const int64_t s = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (s >= samples) return;
+  Real v = bias;
+  int64_t c = 0;
+  for (; c + 8 <= rows; c += 8) {
+    Real t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = P[(c + u) * ldp + s];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v += t[u];
+  }
+  for (; c < rows; ++c) v += P[c * ldp + s];
+  out[s] = Out(v);
+}
 }  // namespace ye3t
 }  // extern "C++"
+
+static void release_readout_parts(ye3t_hip_product_plan* p) {
+  for (int64_t i = 0; i < p->ro_count; ++i)
+    if (p->ro_modules[i]) (void)hipModuleUnload(p->ro_modules[i]);
+  delete[] p->ro_modules;
+  delete[] p->ro_fns;
+  delete[] p->ro_chunks;
+  p->ro_modules = nullptr;
+  p->ro_fns = nullptr;
+  p->ro_chunks = nullptr;
+  p->ro_count = 0;
+  p->ro_total = 0;
+}
 
 static void release_adjoint_parts(ye3t_hip_product_plan* p) {
   for (int64_t i = 0; i < p->adj_count; ++i)
@@ -1388,6 +1427,7 @@ void ye3t_hip_product_plan_destroy(ye3t_hip_product_plan* p) {
   if (p->adjoint_module) (void)hipModuleUnload(p->adjoint_module);
   release_parts(p);
   release_adjoint_parts(p);
+  release_readout_parts(p);
   (void)hipSetDevice(prev);
   delete p;
 }
@@ -1719,6 +1759,116 @@ int ye3t_hip_product_adjoint_parts(const ye3t_hip_product_plan* p, const void* A
                        samples, static_cast<float*>(gA));
   }
   return check_launch("adjoint_parts_reduce_kernel");
+}
+
+int ye3t_hip_product_plan_attach_readout_parts(ye3t_hip_product_plan* p, int64_t part_count,
+                                               const void* const* codes, const int64_t* sizes,
+                                               const char* const* kernel_names, const int64_t* chunk_counts) {
+  clear_error();
+  YE3T_REQUIRE(p && codes && sizes && kernel_names && chunk_counts, "NULL argument");
+  YE3T_REQUIRE(part_count >= 1 && part_count <= (int64_t(1) << 20), "part_count must be in [1, 2^20]");
+  int64_t total = 0;
+  for (int64_t i = 0; i < part_count; ++i) {
+    YE3T_REQUIRE(codes[i] && sizes[i] > 0 && kernel_names[i], "NULL or empty part %lld", (long long)i);
+    YE3T_REQUIRE(chunk_counts[i] >= 1 && chunk_counts[i] <= 65535, "bad chunk count of part %lld", (long long)i);
+    total += chunk_counts[i];
+  }
+  int prev = 0;
+  YE3T_CHECK_HIP(hipGetDevice(&prev));
+  YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
+  auto* modules = new hipModule_t[size_t(part_count)]();
+  auto* fns = new hipFunction_t[size_t(part_count)]();
+  auto* chunks = new int64_t[size_t(part_count)];
+  for (int64_t i = 0; i < part_count; ++i) {
+    chunks[i] = chunk_counts[i];
+    hipError_t e = hipModuleLoadData(&modules[i], codes[i]);
+    if (e == hipSuccess && hipModuleGetFunction(&fns[i], modules[i], kernel_names[i]) != hipSuccess)
+      e = hipErrorNotFound;
+    if (e != hipSuccess) {
+      for (int64_t j = 0; j <= i; ++j)
+        if (modules[j]) (void)hipModuleUnload(modules[j]);
+      delete[] modules;
+      delete[] fns;
+      delete[] chunks;
+      return set_error(YE3T_EINVAL, "readout part %lld: code object not loadable or kernel %s not found",
+                       (long long)i, kernel_names[i]);
+    }
+  }
+  release_readout_parts(p);
+  p->ro_modules = modules;
+  p->ro_fns = fns;
+  p->ro_chunks = chunks;
+  p->ro_count = part_count;
+  p->ro_total = total;
+  return YE3T_OK;
+}
+
+int64_t ye3t_hip_product_linear_parts_workspace_bytes(const ye3t_hip_product_plan* p, int64_t samples) {
+  clear_error();
+  if (!p || samples < 0) {
+    set_error(YE3T_EINVAL, "NULL plan or negative sample count");
+    return -1;
+  }
+  if (p->ro_count == 0 || samples == 0) return 0;
+  return p->ro_total * ((samples + kLanes - 1) / kLanes * kLanes) * int64_t(p->dtype == YE3T_F64 ? 8 : 4);
+}
+
+int ye3t_hip_product_linear_forward_parts(const ye3t_hip_product_plan* p, const void* A, int64_t lda, int columns,
+                                          int64_t samples, const void* weight, double bias, void* workspace,
+                                          int64_t workspace_bytes, void* out, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(p != nullptr, "NULL plan");
+  YE3T_REQUIRE(samples >= 0, "negative sample count");
+  if (samples == 0) return YE3T_OK;
+  YE3T_REQUIRE(p->ro_count > 0, "no readout parts attached");
+  YE3T_REQUIRE(A && weight && out, "NULL input or output");
+  if (columns) {
+    YE3T_REQUIRE(lda >= samples, "lda must cover the samples");
+  } else {
+    YE3T_REQUIRE(lda == p->a_width, "a row-major density has lda == a_width");
+  }
+  const int64_t tiles = (samples + kLanes - 1) / kLanes;
+  const int64_t ldp = tiles * kLanes;
+  const int64_t need = p->ro_total * ldp * int64_t(p->dtype == YE3T_F64 ? 8 : 4);
+  YE3T_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace of %lld bytes needed", (long long)need);
+  const int64_t gx = (tiles + 7) & ~int64_t(7);  // the parts deal tiles to XCDs by linear workgroup id
+  YE3T_REQUIRE(gx <= int64_t(0x7FFFFFF8), "too many samples for one launch");
+  const hipStream_t s = as_stream(stream);
+  long s_arg = long(samples), rs_arg = long(columns ? 1 : p->a_width), cs_arg = long(columns ? lda : 1);
+  long ldp_arg = long(ldp);
+  const void* a_arg = A;
+  void* w_arg = workspace;
+  const void* wt_arg = weight;
+  void* args[] = {&a_arg, &s_arg, &w_arg, &wt_arg, &rs_arg, &cs_arg, &ldp_arg};
+  const int lanes = p->part_lanes;
+  if (lanes > 1) {
+    YE3T_CHECK_HIP(hipEventRecord(p->part_fork, s));
+    for (int k = 0; k < lanes; ++k) YE3T_CHECK_HIP(hipStreamWaitEvent(p->part_streams[k], p->part_fork, 0));
+  }
+  for (int64_t i = 0; i < p->ro_count; ++i)
+    YE3T_CHECK_HIP(hipModuleLaunchKernel(p->ro_fns[i], unsigned(gx), unsigned(p->ro_chunks[i]), 1, kLanes, 1, 1, 0,
+                                         lanes > 1 ? p->part_streams[i % lanes] : s, args, nullptr));
+  if (lanes > 1) {
+    for (int k = 0; k < lanes; ++k) {
+      YE3T_CHECK_HIP(hipEventRecord(p->part_join[k], p->part_streams[k]));
+      YE3T_CHECK_HIP(hipStreamWaitEvent(s, p->part_join[k], 0));
+    }
+  }
+  const unsigned grid = unsigned((samples + 255) / 256);
+  if (p->dtype == YE3T_F64 && p->out_dtype == YE3T_F64) {
+    hipLaunchKernelGGL((readout_parts_reduce_kernel<double, double>), dim3(grid), dim3(256), 0, s,
+                       static_cast<const double*>(workspace), ldp, p->ro_total, bias, samples,
+                       static_cast<double*>(out));
+  } else if (p->dtype == YE3T_F64) {
+    hipLaunchKernelGGL((readout_parts_reduce_kernel<double, float>), dim3(grid), dim3(256), 0, s,
+                       static_cast<const double*>(workspace), ldp, p->ro_total, bias, samples,
+                       static_cast<float*>(out));
+  } else {
+    hipLaunchKernelGGL((readout_parts_reduce_kernel<float, float>), dim3(grid), dim3(256), 0, s,
+                       static_cast<const float*>(workspace), ldp, p->ro_total, float(bias), samples,
+                       static_cast<float*>(out));
+  }
+  return check_launch("readout_parts_reduce_kernel");
 }
 
 int ye3t_hip_product_plan_select(ye3t_hip_product_plan* p, int use_interpreter) {

@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 57
+ABI_VERSION = 58
 _LIB = None
 
 F32, F64 = 0, 1
@@ -138,6 +138,12 @@ def lib():
     L.ye3t_hip_product_adjoint_parts_workspace_bytes.argtypes = [_vp, _i64]
     L.ye3t_hip_product_adjoint_parts_workspace_bytes.restype = _i64
     L.ye3t_hip_product_adjoint_parts.argtypes = [_vp, _vp, _i64, ctypes.c_int, _vp, _i64, _vp, _i64, _vp, _vp]
+    L.ye3t_hip_product_plan_attach_readout_parts.argtypes = [_vp, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_i64),
+                                                             ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i64)]
+    L.ye3t_hip_product_linear_parts_workspace_bytes.argtypes = [_vp, _i64]
+    L.ye3t_hip_product_linear_parts_workspace_bytes.restype = _i64
+    L.ye3t_hip_product_linear_forward_parts.argtypes = [_vp, _vp, _i64, ctypes.c_int, _i64, _vp, ctypes.c_double,
+                                                        _vp, _i64, _vp, _vp]
     L.ye3t_hip_product_plan_attach_readout.argtypes = [_vp, _vp, _i64, ctypes.c_char_p, ctypes.c_int]
     L.ye3t_hip_product_linear_forward.argtypes = [_vp, _vp, _i64, _vp, ctypes.c_double, _vp, _vp]
     L.ye3t_hip_rows_dot.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, ctypes.c_double, _vp, _vp]
@@ -188,7 +194,8 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_product_plan_attach_generated", "ye3t_hip_product_plan_select", "ye3t_hip_last_density_kernel",
     "ye3t_hip_fp64_pipe_probe", "ye3t_hip_product_plan_attach_generated_parts",
     "ye3t_hip_product_plan_attach_adjoint_parts", "ye3t_hip_product_adjoint_parts_workspace_bytes",
-    "ye3t_hip_product_adjoint_parts",
+    "ye3t_hip_product_adjoint_parts", "ye3t_hip_product_plan_attach_readout_parts",
+    "ye3t_hip_product_linear_parts_workspace_bytes", "ye3t_hip_product_linear_forward_parts",
     "ye3t_hip_density_accumulate_adjoint", "ye3t_hip_product_plan_attach_readout", "ye3t_hip_product_linear_forward",
     "ye3t_hip_rows_dot", "ye3t_hip_product_plan_attach_adjoint", "ye3t_hip_product_adjoint",
     "ye3t_hip_neighbor_workspace_bytes", "ye3t_hip_neighbor_count", "ye3t_hip_neighbor_fill",
@@ -830,6 +837,69 @@ class ProductPlanHandle:
             col_off.ctypes.data, rows.ctypes.data if rows.size else None),
             "ye3t_hip_product_plan_attach_adjoint_parts")
         self.adjoint_part_meta = [m for _, m in parts]
+
+    def attach_readout_parts(self, parts, workers=None):
+        """Compile and attach the fused linear readout in parts
+        (``ye3t_amd.ace.codegen.generate_readout_parts``)."""
+        from concurrent.futures import ThreadPoolExecutor
+
+        for _source, meta in parts:
+            if meta["feature_count"] != self.feature_count or meta["a_width"] != self.program["a_width"]:
+                raise ValueError("readout part does not match this plan")
+            if meta["dtype"] != self.dtype or meta["in_dtype"] != self.in_dtype:
+                raise ValueError("readout part dtypes do not match this plan")
+        workers = workers or min(16, os.cpu_count() or 1)
+        with ThreadPoolExecutor(max(1, workers)) as pool:
+            blobs = list(pool.map(lambda part: rtc_compile(part[0]), parts))
+        n = len(parts)
+        self._readout_part_code = [ctypes.create_string_buffer(b, len(b)) for b in blobs]
+        codes = (_vp * n)(*[ctypes.cast(c, _vp) for c in self._readout_part_code])
+        sizes = (_i64 * n)(*[len(b) for b in blobs])
+        names = (ctypes.c_char_p * n)(*[m["kernel"].encode() for _, m in parts])
+        chunks = (_i64 * n)(*[int(m["chunks"]) for _, m in parts])
+        _check(lib().ye3t_hip_product_plan_attach_readout_parts(self._handle, n, codes, sizes, names, chunks),
+               "ye3t_hip_product_plan_attach_readout_parts")
+        self.readout_part_meta = [m for _, m in parts]
+
+    def linear_parts(self, A, weight, bias, samples=None, columns=False, out=None):
+        """``out[s] = bias + sum_k B[s, k] weight[k]`` on the attached readout
+        parts (B never stored): ``A`` row-major or, with ``columns``, a
+        column-major view ``[a_width, >= samples]``; ``weight`` in the plan's
+        dtype; ``out`` in its out_dtype."""
+        import torch
+
+        want = torch.float64 if self.in_dtype == "f64" else torch.float32
+        w_t = torch.float64 if self.dtype == "f64" else torch.float32
+        o_t = torch.float64 if self.out_dtype == "f64" else torch.float32
+        W = int(self.program["a_width"])
+        if A.dtype != want or A.ndim != 2:
+            raise ValueError(f"A must be a 2-d {want} tensor")
+        if columns:
+            if int(A.shape[0]) != W or (A.stride(1) != 1 and int(A.shape[1]) > 1) or int(A.shape[1]) < int(samples):
+                raise ValueError(f"A must be a column-major [{W}, >= samples] view")
+            S, lda = int(samples), int(A.stride(0))
+        else:
+            if int(A.shape[1]) != W or not A.is_contiguous():
+                raise ValueError(f"A must be contiguous [samples, {W}]")
+            S, lda = int(A.shape[0]), W
+        if weight.dtype != w_t or tuple(weight.shape) != (self.feature_count,) or not weight.is_contiguous():
+            raise ValueError(f"weight must be a contiguous {w_t} vector of {self.feature_count}")
+        if out is None:
+            out = torch.empty((S,), dtype=o_t, device=A.device)
+        elif tuple(out.shape) != (S,) or out.dtype != o_t or not out.is_contiguous():
+            raise ValueError("out has the wrong shape or dtype")
+        L = lib()
+        nbytes = int(L.ye3t_hip_product_linear_parts_workspace_bytes(self._handle, S))
+        if nbytes < 0:
+            _check(-1, "ye3t_hip_product_linear_parts_workspace_bytes")
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=A.device)
+        if not A.is_cuda:
+            raise ValueError("A must be a GPU tensor")
+        _check(L.ye3t_hip_product_linear_forward_parts(self._handle, ctypes.c_void_p(A.data_ptr()), lda,
+                                                       1 if columns else 0, S, _dev(weight, "weight"), float(bias),
+                                                       _dev(ws, "workspace"), nbytes, _dev(out, "out"), _stream()),
+               "ye3t_hip_product_linear_forward_parts")
+        return out
 
     def adjoint_parts(self, A, gB, samples=None, columns=False, out=None):
         """``gA[s] = J(A[s])^T gB[s]`` on the attached adjoint parts: ``A``
