@@ -690,9 +690,22 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
 # recompute fewer shared nodes until they spill
 PART_MAX_LIVE = 400
 PART_CHUNKS = 9
+# plans above PART_LARGE_TERMS terms in fp64 arithmetic take 300-value chunks:
+# config 3 (fp64) 3.67 ms at (300, 9) against 4.06 ms at (400, 9), 3.95 at
+# (400, 16), 4.23 at (400, 5) and 4.69 at (500, 9); config 5 (fp64 arithmetic)
+# 158 ms against 174 ms.  In fp32 arithmetic (half the registers per value)
+# config 3 took 1.85 ms at 300 against 1.72 ms at 400.
+PART_MAX_LIVE_LARGE = 300
+PART_LARGE_TERMS = 100_000
 
 
-def generate_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per_part=PART_CHUNKS, out_dtype=None,
+def part_max_live(plan, dtype="f64"):
+    """Node values per chunk of the generated parts of ``plan`` in ``dtype`` arithmetic."""
+    terms = sum(len(nd.get("terms", ())) for nd in plan.nodes)
+    return PART_MAX_LIVE_LARGE if dtype == "f64" and terms > PART_LARGE_TERMS else PART_MAX_LIVE
+
+
+def generate_parts(plan, dtype="f64", max_live=None, chunks_per_part=PART_CHUNKS, out_dtype=None,
                    in_dtype=None, group=GROUP):
     """``[(source, meta), ...]``: the plan's generated product kernel cut into
     parts of ``chunks_per_part`` consecutive output chunks (each chunk holds
@@ -707,6 +720,7 @@ def generate_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per_part=PA
     samples is then one contiguous 512-byte load instead of 64 cache lines."""
     if chunks_per_part < 1:
         raise ValueError("chunks_per_part must be positive")
+    max_live = max_live or part_max_live(plan, dtype)
     chunks = _chunks(plan, max_live)
     parts = []
     for i in range(0, len(chunks), chunks_per_part):
@@ -874,7 +888,7 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
     return parts, {"partial_rows": row_base[-1], "col_off": col_off, "rows": rows}
 
 
-def generate_readout_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per_part=PART_CHUNKS, in_dtype=None):
+def generate_readout_parts(plan, dtype="f64", max_live=None, chunks_per_part=PART_CHUNKS, in_dtype=None):
     """Fused linear readout of a plan in parts: ``out[s] = bias + sum_k B[s, k]
     weight[k]`` without writing B (counterpart of the reference's
     ``factorized_angular_linear``, ``execution_plan.py:13793-13850``).
@@ -895,7 +909,7 @@ def generate_readout_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
     fma = "fma" if dtype == "f64" else "fmaf"
     nodes = plan.nodes
     F, Wd = plan.feature_count, plan.a_width
-    chunks = _chunks(plan, max_live)
+    chunks = _chunks(plan, max_live or part_max_live(plan, dtype))
     parts = []
     for p0 in range(0, len(chunks), chunks_per_part):
         sub = list(range(p0, min(len(chunks), p0 + chunks_per_part)))

@@ -119,16 +119,30 @@ class ACEPipeline:
             self.handle.attach_generated(source, meta)
             self.kernel = "generated"
         elif use_parts:
-            from ye3t_amd.ace.codegen import PART_CHUNKS, PART_MAX_LIVE, generate_parts
+            from ye3t_amd.ace.codegen import PART_CHUNKS, generate_parts
 
             # node values per chunk and chunks per part (tuning)
-            live = int(os.environ.get("YE3T_PARTS_MAX_LIVE", PART_MAX_LIVE))
+            live = self._parts_max_live()
             per = int(os.environ.get("YE3T_PARTS_CHUNKS", PART_CHUNKS))
             group = int(os.environ.get("YE3T_PARTS_GROUP", 32))  # output columns per staged store
             self.handle.attach_generated_parts(generate_parts(self.plan, self.accumulate, max_live=live,
                                                               chunks_per_part=per, out_dtype=dtype,
                                                               in_dtype=self.density_dtype, group=group))
             self.kernel = "parts"
+
+    def _parts_max_live(self):
+        """Node values per chunk of the generated parts: ``YE3T_PARTS_MAX_LIVE``
+        or ``codegen.part_max_live``.  Chunks above ``PART_MAX_LIVE`` (400) are
+        refused: config 5 in 550-value chunks (1.2 KB of scratch per lane) took
+        a memory aperture violation on the GPU whose cause is not established,
+        while 300 and 400 ran clean there."""
+        from ye3t_amd.ace.codegen import PART_MAX_LIVE, part_max_live
+
+        env = os.environ.get("YE3T_PARTS_MAX_LIVE")
+        live = part_max_live(self.plan, self.accumulate) if env is None else int(env)
+        if not 1 <= live <= PART_MAX_LIVE:
+            raise ValueError(f"YE3T_PARTS_MAX_LIVE must be in [1, {PART_MAX_LIVE}], got {live}")
+        return live
 
     @property
     def feature_count(self):
@@ -269,10 +283,10 @@ class ACEPipeline:
         if out is None:
             out = torch.empty((S,), dtype=out_t, device=A_rows.device)
         if self.kernel == "parts":
-            from ye3t_amd.ace.codegen import PART_CHUNKS, PART_MAX_LIVE, generate_readout_parts
+            from ye3t_amd.ace.codegen import PART_CHUNKS, generate_readout_parts
 
             if getattr(self.handle, "readout_part_meta", None) is None:
-                live = int(os.environ.get("YE3T_PARTS_MAX_LIVE", PART_MAX_LIVE))
+                live = self._parts_max_live()
                 per = int(os.environ.get("YE3T_PARTS_CHUNKS", PART_CHUNKS))
                 parts, _ = generate_readout_parts(self.plan, self.accumulate, max_live=live, chunks_per_part=per,
                                                   in_dtype=self.density_dtype)
