@@ -611,11 +611,13 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     if strided:
         # XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by
         # linear id, so XCD x gets the tiles [x * per, (x + 1) * per) of every
-        # chunk and its L2 holds one eighth of the density (gridDim.x = 8 * per)
+        # chunk (gridDim.x = 8 * per, gridDim.y = the part's chunks); on an XCD
+        # the chunks of one tile run back to back, so the tile's density rows
+        # are read from HBM once per part and then from L2
         w("  const long wg = (long)blockIdx.y * gridDim.x + blockIdx.x;")
         w("  const long per = gridDim.x >> 3, k = wg >> 3;")
-        w("  const long tile = (wg & 7) * per + k % per;")
-        w("  const int chunk = (int)(k / per);")
+        w("  const long tile = (wg & 7) * per + k / gridDim.y;")
+        w("  const int chunk = (int)(k % gridDim.y);")
         w(f"  const long s0 = tile * {R};")
         w("  if (s0 >= samples) return;")
     else:
@@ -798,8 +800,8 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
         # the forward parts' XCD-aware (tile, chunk) order
         w("  const long wg = (long)blockIdx.y * gridDim.x + blockIdx.x;")
         w("  const long per = gridDim.x >> 3, k = wg >> 3;")
-        w("  const long tile = (wg & 7) * per + k % per;")
-        w("  const int chunk = (int)(k / per);")
+        w("  const long tile = (wg & 7) * per + k / gridDim.y;")
+        w("  const int chunk = (int)(k % gridDim.y);")
         w("  const long s0 = tile * 64;")
         w("  if (s0 >= samples) return;")
         w("  const long s = s0 + lane;")
@@ -926,8 +928,8 @@ def generate_readout_parts(plan, dtype="f64", max_live=None, chunks_per_part=PAR
         w("  const wptr W = (wptr)Wt;")
         w("  const long wg = (long)blockIdx.y * gridDim.x + blockIdx.x;")
         w("  const long per = gridDim.x >> 3, k = wg >> 3;")
-        w("  const long tile = (wg & 7) * per + k % per;")
-        w("  const int chunk = (int)(k / per);")
+        w("  const long tile = (wg & 7) * per + k / gridDim.y;")
+        w("  const int chunk = (int)(k % gridDim.y);")
         w("  const long s0 = tile * 64;")
         w("  if (s0 >= samples) return;")
         w("  const long s = s0 + lane;")
