@@ -701,13 +701,28 @@ PART_MAX_LIVE_LARGE = 300
 PART_LARGE_TERMS = 100_000
 
 
+# plans above PART_LARGE_TERMS terms take 64 chunks per part: each part reads a
+# tile's density rows from HBM once, so fewer parts re-read less (config 3 fp64
+# 3.49 / 3.27 / 3.00 / 2.86 ms at 9 / 16 / 32 / 64 chunks per part, config 5
+# 129 / 126 / 118 / 113 ms; a 64-chunk part compiles in about a minute)
+PART_CHUNKS_LARGE = 64
+
+
+def _plan_terms(plan):
+    return sum(len(nd.get("terms", ())) for nd in plan.nodes)
+
+
+def part_chunks(plan):
+    """Chunks per generated part of ``plan``."""
+    return PART_CHUNKS_LARGE if _plan_terms(plan) > PART_LARGE_TERMS else PART_CHUNKS
+
+
 def part_max_live(plan, dtype="f64"):
     """Node values per chunk of the generated parts of ``plan`` in ``dtype`` arithmetic."""
-    terms = sum(len(nd.get("terms", ())) for nd in plan.nodes)
-    return PART_MAX_LIVE_LARGE if dtype == "f64" and terms > PART_LARGE_TERMS else PART_MAX_LIVE
+    return PART_MAX_LIVE_LARGE if dtype == "f64" and _plan_terms(plan) > PART_LARGE_TERMS else PART_MAX_LIVE
 
 
-def generate_parts(plan, dtype="f64", max_live=None, chunks_per_part=PART_CHUNKS, out_dtype=None,
+def generate_parts(plan, dtype="f64", max_live=None, chunks_per_part=None, out_dtype=None,
                    in_dtype=None, group=GROUP):
     """``[(source, meta), ...]``: the plan's generated product kernel cut into
     parts of ``chunks_per_part`` consecutive output chunks (each chunk holds
@@ -720,6 +735,7 @@ def generate_parts(plan, dtype="f64", max_live=None, chunks_per_part=PART_CHUNKS
     read the density through row and column strides (``strided``), so the
     column-major copy the interpreter reads serves them too: a leaf of 64
     samples is then one contiguous 512-byte load instead of 64 cache lines."""
+    chunks_per_part = chunks_per_part or part_chunks(plan)
     if chunks_per_part < 1:
         raise ValueError("chunks_per_part must be positive")
     max_live = max_live or part_max_live(plan, dtype)
@@ -890,7 +906,7 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
     return parts, {"partial_rows": row_base[-1], "col_off": col_off, "rows": rows}
 
 
-def generate_readout_parts(plan, dtype="f64", max_live=None, chunks_per_part=PART_CHUNKS, in_dtype=None):
+def generate_readout_parts(plan, dtype="f64", max_live=None, chunks_per_part=None, in_dtype=None):
     """Fused linear readout of a plan in parts: ``out[s] = bias + sum_k B[s, k]
     weight[k]`` without writing B (counterpart of the reference's
     ``factorized_angular_linear``, ``execution_plan.py:13793-13850``).
@@ -905,6 +921,7 @@ def generate_readout_parts(plan, dtype="f64", max_live=None, chunks_per_part=PAR
     ldp)``.  Returns ``(parts, chunk_count)``.
     """
     in_dtype = _check_in_dtype(dtype, in_dtype)
+    chunks_per_part = chunks_per_part or part_chunks(plan)
     if chunks_per_part < 1:
         raise ValueError("chunks_per_part must be positive")
     real = "double" if dtype == "f64" else "float"

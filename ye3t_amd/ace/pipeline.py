@@ -119,11 +119,11 @@ class ACEPipeline:
             self.handle.attach_generated(source, meta)
             self.kernel = "generated"
         elif use_parts:
-            from ye3t_amd.ace.codegen import PART_CHUNKS, generate_parts
+            from ye3t_amd.ace.codegen import generate_parts, part_chunks
 
             # node values per chunk and chunks per part (tuning)
             live = self._parts_max_live()
-            per = int(os.environ.get("YE3T_PARTS_CHUNKS", PART_CHUNKS))
+            per = int(os.environ.get("YE3T_PARTS_CHUNKS", 0)) or part_chunks(self.plan)
             group = int(os.environ.get("YE3T_PARTS_GROUP", 32))  # output columns per staged store
             self.handle.attach_generated_parts(generate_parts(self.plan, self.accumulate, max_live=live,
                                                               chunks_per_part=per, out_dtype=dtype,
@@ -283,11 +283,11 @@ class ACEPipeline:
         if out is None:
             out = torch.empty((S,), dtype=out_t, device=A_rows.device)
         if self.kernel == "parts":
-            from ye3t_amd.ace.codegen import PART_CHUNKS, generate_readout_parts
+            from ye3t_amd.ace.codegen import generate_readout_parts, part_chunks
 
             if getattr(self.handle, "readout_part_meta", None) is None:
                 live = self._parts_max_live()
-                per = int(os.environ.get("YE3T_PARTS_CHUNKS", PART_CHUNKS))
+                per = int(os.environ.get("YE3T_PARTS_CHUNKS", 0)) or part_chunks(self.plan)
                 parts, _ = generate_readout_parts(self.plan, self.accumulate, max_live=live, chunks_per_part=per,
                                                   in_dtype=self.density_dtype)
                 self.handle.attach_readout_parts(parts)

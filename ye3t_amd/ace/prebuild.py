@@ -3,7 +3,8 @@
 Plans between ``GENERATED_MAX_TERMS`` and ``PARTS_MAX_TERMS`` terms run on a
 generated kernel in parts (``codegen.generate_parts``, with the reverse sweep
 ``generate_adjoint_parts`` and the fused readout ``generate_readout_parts``),
-one hipRTC module per 9 chunks.  hipRTC compiles one module at a time per process (~15 s for a
+one hipRTC module per 9 chunks (64 for plans above 100 000 terms).  hipRTC
+compiles one module at a time per process (one to five minutes for a 64-chunk
 config-3 part), so the parts are spread over worker processes.  hipRTC needs
 no GPU, so this runs on a build host; the code objects land in the JIT cache
 (``ye3t_amd/jit_cache`` unless ``YE3T_AMD_JIT_CACHE`` says otherwise), keyed by
