@@ -43,9 +43,11 @@ PARTS_MAX_TERMS = 2000000
 # it on the term stream's reverse mode
 ADJOINT_PARTS_MAX_TERMS = 200000
 # the reverse mode's parts: chunks of fewer node values (values and gradients are
-# live together; 128 compiles without spills at config 2) and chunks per part
+# live together; 128 compiles without spills at config 2) and chunks per part:
+# a part's chunks run back to back on a tile, so fewer parts re-read less of the
+# density and gB (config 3 fp64 21.8 -> 16.7 ms and config 2 658 -> 631 us at 8 -> 32)
 ADJOINT_PART_MAX_LIVE = 128
-ADJOINT_PART_CHUNKS = 8
+ADJOINT_PART_CHUNKS = 32
 
 
 class ACEPipeline:
