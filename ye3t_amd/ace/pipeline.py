@@ -45,9 +45,10 @@ ADJOINT_PARTS_MAX_TERMS = 200000
 # the reverse mode's parts: chunks of fewer node values (values and gradients are
 # live together; 128 compiles without spills at config 2) and chunks per part:
 # a part's chunks run back to back on a tile, so fewer parts re-read less of the
-# density and gB (config 3 fp64 21.8 -> 16.7 ms and config 2 658 -> 631 us at 8 -> 32)
+# density and gB (config 3 fp64 21.8 / 16.7 / 16.0 ms at 8 / 32 / 64 chunks per
+# part; config 2 658 / 633 / 634 us)
 ADJOINT_PART_MAX_LIVE = 128
-ADJOINT_PART_CHUNKS = 32
+ADJOINT_PART_CHUNKS = 64
 
 
 class ACEPipeline:
