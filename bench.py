@@ -314,35 +314,6 @@ def bench_op(args, cfg):
             "note": "us_per_call: the whole build through the Python binding, including its host "
                     "synchronisation on the edge count and the output allocations"})
         line["config"].update({"atoms": N, "edges": E, "cutoff": cutoff, "box_edge": box})
-    elif args.op == "fp64_pipe":
-        # matrix-core and vector fp64 work of one SIMD: modes 0 (four independent fp64 MFMAs per
-        # round) and 1 (64 fp64 FMAs per lane per round, the same flops) alone at one workgroup per
-        # SIMD, then mode 3 at two per SIMD, one wave of each kind on every SIMD
-        simds = native.device_caps(0)["cu_count"] * 4
-        rounds = 200
-        out = torch.empty(2 * simds * 64, dtype=torch.float64, device="cuda")
-        times = {}
-        for mode, wg in ((0, simds), (1, simds), (0, 2 * simds), (1, 2 * simds), (2, simds), (3, 2 * simds)):
-            t = _time_kernel(lambda: native.fp64_pipe_probe(mode, wg, rounds, out), args.steps, args.warmup)
-            times[f"mode{mode}_x{wg // simds}"] = t * 1e6
-        native.fp64_pipe_probe(3, 2 * simds, rounds, out)
-        ids = out[::64].cpu().numpy().astype(np.int64)
-
-        def simd(v):  # XCC, SE, SH, CU and SIMD fields of XCC_ID:HW_ID
-            hw = v & 0xFFFFFFFF
-            return (v >> 32, (hw >> 13) & 7, (hw >> 12) & 1, (hw >> 8) & 15, (hw >> 4) & 3)
-        second = {simd(v) for v in ids[simds:]}
-        paired = sum(simd(v) in second for v in ids[:simds]) / simds
-        t0, t1, t3 = times["mode0_x1"], times["mode1_x1"], times["mode3_x2"]
-        flops = simds * rounds * 8192
-        line.update({
-            "metric": "fp64 matrix/vector overlap on one SIMD", "value": (t0 + t1 - t3) / min(t0, t1),
-            "unit": "fraction (1: the shorter kind hides fully under the longer, 0: they take turns)",
-            "higher_is_better": True, "dtype": "f64", "us": times, "pairs_on_one_simd": paired,
-            "mfma_tflops_x1": flops / (t0 * 1e-6) / 1e12, "fma_tflops_x1": flops / (t1 * 1e-6) / 1e12,
-            "note": "mode 3 runs one MFMA wave and one FMA wave on every SIMD (pairs_on_one_simd checks "
-                    "this from the waves' HW_ID / XCC_ID); taking turns puts it near mode0_x1 + mode1_x1"})
-        line["config"] = {"workload": "fp64-pipe-probe", "simds": simds, "rounds": rounds}
     elif args.op == "density_edge_gradient":
         inp = cfg.density.generate()
         dev = to_device_inputs(inp, dtype, "cuda")
@@ -411,7 +382,7 @@ def main():
     ap.add_argument("--kernel", default="auto", choices=["auto", "generated", "parts", "interpreter"])
     ap.add_argument("--op", default="pipeline",
                     choices=["pipeline", "linear_readout", "density_accumulate_adjoint", "product_adjoint",
-                             "neighbor_list", "density_edge_gradient", "fp64_pipe"],
+                             "neighbor_list", "density_edge_gradient"],
                     help="pipeline: the headline step (stage 1 + stage 2); the others time one widened op "
                          "on the config's shapes and print its own JSON line")
     ap.add_argument("--copy-probe", action="store_true",

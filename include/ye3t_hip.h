@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 58 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 59 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -139,19 +139,6 @@ int ye3t_hip_ace_density_forward(const ye3t_density_args* args, void* A, ye3t_st
  * launched ("" if none), for profiling.  No reference counterpart. */
 const char* ye3t_hip_last_density_kernel(void);
 
-/* Diagnostic, no reference counterpart: `workgroups` 64-thread workgroups each
- * run `iterations` rounds of fp64 work -- mode 0: four independent
- * v_mfma_f64_16x16x4f64 (8192 flops), 1: 64 fp64 FMAs per lane on 8 chains
- * (8192 flops), 2: both in every wave, 3: the second half of the workgroups
- * the MFMAs, the first half the FMAs -- and write one value per lane to
- * out[workgroups * 64]: lane 0 of each wave its SIMD's identity
- * ((XCC_ID << 32) | HW_ID, exact in a double), the others a sink value.
- * At two workgroups per SIMD, mode 3 against modes 0 and 1 at one workgroup
- * per SIMD shows whether a SIMD's matrix-core and vector fp64 work overlap
- * (near the larger of the two) or take turns (near their sum), which bounds
- * the fused density kernel. */
-int ye3t_hip_fp64_pipe_probe(int mode, int64_t workgroups, int iterations, double* out, ye3t_stream_t stream);
-
 /* Edge-vector gradient of the fused stage 1 (forces): edge_gradient[e, :] =
  * d <density_adjoint, A> / d edge_vectors[e, :] for density_adjoint shaped like
  * A ([N, C, R, (l_max+1)^2], dtype adjoint_dtype: YE3T_F64, or YE3T_F32 /
@@ -210,6 +197,47 @@ int ye3t_hip_symmetric_power_shared_monomial_adjoint(int dtype, const void* outp
                                                      const int64_t* coefficient_terms,
                                                      const void* coefficient_values, int64_t coefficient_count,
                                                      int64_t output_dim, void* input_adjoint, ye3t_stream_t stream);
+
+/* Shared form with sparse monomial supports: monomial t is
+ *   prod_{q in [term_offsets[t], term_offsets[t+1])} input[b, term_components[q]]^term_exponents[q]
+ * (monomial_count = t range, support_count = q range), and
+ * S[b, o] = sum_{k in [output_offsets[o], output_offsets[o+1])} coefficient_values[k] * monomial_{coefficient_terms[k]}.
+ * Every table index must be in range and every exponent positive (checked on
+ * the host by the Python layer).  Replaces
+ * ye3t_runtime::symmetric_power_shared_sparse_monomial (schema
+ * execution_plan_torch.cpp:7562-7567; CUDA execution_plan_cuda.cu:11012-11104). */
+int ye3t_hip_symmetric_power_shared_sparse_monomial(int dtype, const void* input, int64_t batch, int64_t input_dim,
+                                                    const int64_t* term_offsets, const int64_t* term_components,
+                                                    const int64_t* term_exponents, int64_t monomial_count,
+                                                    int64_t support_count, const int64_t* output_offsets,
+                                                    const int64_t* coefficient_terms, const void* coefficient_values,
+                                                    int64_t coefficient_count, int64_t output_dim, void* output,
+                                                    ye3t_stream_t stream);
+
+/* input_adjoint[b, c] of the sparse shared form: zero factors add their
+ * exponents into a zero degree; degree one gives the cofactor, a higher degree
+ * nothing (execution_plan_cuda.cu:5757-5813).  Replaces
+ * ye3t_runtime::symmetric_power_shared_sparse_monomial_adjoint (schema
+ * execution_plan_torch.cpp:7568-7573; CUDA :11106-11204). */
+int ye3t_hip_symmetric_power_shared_sparse_monomial_adjoint(
+    int dtype, const void* output_adjoint, const void* input, int64_t batch, int64_t input_dim,
+    const int64_t* term_offsets, const int64_t* term_components, const int64_t* term_exponents,
+    int64_t monomial_count, int64_t support_count, const int64_t* output_offsets, const int64_t* coefficient_terms,
+    const void* coefficient_values, int64_t coefficient_count, int64_t output_dim, void* input_adjoint,
+    ye3t_stream_t stream);
+
+/* Second order of the sparse shared form along input_adjoint_tangent v:
+ * output_tangent[b, o] = d S[b, o] . v, input_tangent[b, c] = sum over
+ * coefficients of output_adjoint[b, o] value_k (Hessian of the monomial) v
+ * (execution_plan_cuda.cu:5815-5955).  Replaces
+ * ye3t_runtime::symmetric_power_shared_sparse_monomial_double_backward (schema
+ * execution_plan_torch.cpp:7574-7580; CUDA :11206-11330). */
+int ye3t_hip_symmetric_power_shared_sparse_monomial_double_backward(
+    int dtype, const void* input_adjoint_tangent, const void* output_adjoint, const void* input, int64_t batch,
+    int64_t input_dim, const int64_t* term_offsets, const int64_t* term_components, const int64_t* term_exponents,
+    int64_t monomial_count, int64_t support_count, const int64_t* output_offsets, const int64_t* coefficient_terms,
+    const void* coefficient_values, int64_t coefficient_count, int64_t output_dim, void* output_tangent,
+    void* input_tangent, ye3t_stream_t stream);
 
 /* out[b, k] = sum_{t in k} coeffs[t] prod_blk block_values[b, label_k, blk, block_m_indices[t, blk]].
  * Device counterpart of evaluate_factorized_schedule_cpu

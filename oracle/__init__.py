@@ -577,3 +577,68 @@ def symmetric_power_shared_monomial_adjoint(output_adjoint, inp, monomial_counts
         ws = np.zeros(max(M, 1))
         fn(_vp(g), _vp(x), I(B), I(D), _vp(counts), I(M), _vp(offs), _vp(terms), _vp(vals), I(O), _vp(ws), _vp(out))
     return out
+
+
+def _sparse_tables(term_offsets, term_components, term_exponents, output_offsets, coefficient_terms,
+                   coefficient_values):
+    toff, comp, ex = _i64a(term_offsets), _i64a(term_components), _i64a(term_exponents)
+    offs, terms = _i64a(output_offsets), _i64a(coefficient_terms)
+    outs = np.repeat(np.arange(offs.shape[0] - 1, dtype=np.int64), np.diff(offs))
+    return toff, comp, ex, offs, terms, outs, _f64(coefficient_values)
+
+
+def symmetric_power_shared_sparse_monomial(inp, term_offsets, term_components, term_exponents, output_offsets,
+                                           coefficient_terms, coefficient_values):
+    """``symmetric_power_shared_sparse_monomial`` (execution_plan_cuda.cu:5720-5755, 5962-6000)."""
+    x = _f64(inp)
+    B, D = x.shape
+    toff, comp, ex, offs, terms, _, vals = _sparse_tables(term_offsets, term_components, term_exponents,
+                                                           output_offsets, coefficient_terms, coefficient_values)
+    M, O = toff.shape[0] - 1, offs.shape[0] - 1
+    out = np.zeros((B, O))
+    fn = lib().oracle_symmetric_power_shared_sparse_monomial
+    fn.restype = None
+    ws = np.zeros(max(M, 1))
+    fn(_vp(x), _I(B), _I(D), _vp(toff), _vp(comp), _vp(ex), _I(M), _vp(offs), _vp(terms), _vp(vals), _I(O),
+       _vp(ws), _vp(out))
+    return out
+
+
+def symmetric_power_shared_sparse_monomial_adjoint(output_adjoint, inp, term_offsets, term_components,
+                                                   term_exponents, output_offsets, coefficient_terms,
+                                                   coefficient_values):
+    """``..._sparse_monomial_adjoint`` (execution_plan_cuda.cu:5757-5813, 6002-6030)."""
+    x = _f64(inp)
+    B, D = x.shape
+    toff, comp, ex, offs, terms, outs, vals = _sparse_tables(term_offsets, term_components, term_exponents,
+                                                              output_offsets, coefficient_terms, coefficient_values)
+    M, O, C = toff.shape[0] - 1, offs.shape[0] - 1, terms.shape[0]
+    g = _f64(output_adjoint).reshape(B, O)
+    out = np.zeros((B, D))
+    fn = lib().oracle_symmetric_power_shared_sparse_monomial_adjoint
+    fn.restype = None
+    ws = np.zeros(max(M, 1))
+    fn(_vp(g), _vp(x), _I(B), _I(D), _vp(toff), _vp(comp), _vp(ex), _I(M), _vp(terms), _vp(outs), _vp(vals), _I(C),
+       _I(O), _vp(ws), _vp(out))
+    return out
+
+
+def symmetric_power_shared_sparse_monomial_double_backward(input_adjoint_tangent, output_adjoint, inp,
+                                                           term_offsets, term_components, term_exponents,
+                                                           output_offsets, coefficient_terms, coefficient_values):
+    """``..._sparse_monomial_double_backward`` (execution_plan_cuda.cu:5815-5955, host :11206-11330):
+    returns ``(output_tangent, input_tangent)``."""
+    x = _f64(inp)
+    B, D = x.shape
+    toff, comp, ex, offs, terms, outs, vals = _sparse_tables(term_offsets, term_components, term_exponents,
+                                                              output_offsets, coefficient_terms, coefficient_values)
+    M, O, C = toff.shape[0] - 1, offs.shape[0] - 1, terms.shape[0]
+    v = _f64(input_adjoint_tangent).reshape(B, D)
+    g = _f64(output_adjoint).reshape(B, O)
+    ot, it = np.zeros((B, O)), np.zeros((B, D))
+    fn = lib().oracle_symmetric_power_shared_sparse_monomial_double_backward
+    fn.restype = None
+    ws = np.zeros(max(M, 1))
+    fn(_vp(v), _vp(g), _vp(x), _I(B), _I(D), _vp(toff), _vp(comp), _vp(ex), _I(M), _vp(offs), _vp(terms),
+       _vp(outs), _vp(vals), _I(C), _I(O), _vp(ws), _vp(ot), _vp(it))
+    return ot, it

@@ -444,3 +444,144 @@ void oracle_symmetric_power_shared_monomial_adjoint(const double* gout, const do
     }
   }
 }
+
+/* ---- sparse shared monomials -----------------------------------------------
+ * symmetric_power_shared_sparse_monomial{,_adjoint,_double_backward}
+ * (execution_plan_cuda.cu:5720-5955, host :11012-11330; the reference has no
+ * CPU kernel for them).  Monomial t is the product over its support
+ * q in [term_offsets[t], term_offsets[t+1]) of x[comp[q]]^exp[q]; outputs are
+ * sparse combinations of monomials as in the dense shared form.  The device
+ * code accumulates its adjoints with atomics; this restatement takes the
+ * coefficients and supports in index order. */
+
+static void sparse_monomial_values(const double* x, const int64_t* toff, const int64_t* comp, const int64_t* ex,
+                                   int64_t monomials, double* ws) {
+  for (int64_t t = 0; t < monomials; ++t) {
+    double v = 1.0;
+    for (int64_t q = toff[t]; q < toff[t + 1]; ++q) v *= ipow_r(x[comp[q]], ex[q]);
+    ws[t] = v;
+  }
+}
+
+static void sparse_term_adjoint(const double* gout_row, const int64_t* coef_terms, const int64_t* coef_outputs,
+                                const double* coef_values, int64_t coefs, int64_t monomials, double* ws) {
+  for (int64_t t = 0; t < monomials; ++t) ws[t] = 0.0;
+  for (int64_t k = 0; k < coefs; ++k) ws[coef_terms[k]] += gout_row[coef_outputs[k]] * coef_values[k];
+}
+
+void oracle_symmetric_power_shared_sparse_monomial(const double* input, int64_t batch, int64_t in_dim,
+                                                   const int64_t* toff, const int64_t* comp, const int64_t* ex,
+                                                   int64_t monomials, const int64_t* out_off,
+                                                   const int64_t* coef_terms, const double* coef_values,
+                                                   int64_t out_dim, double* mono_ws, double* out) {
+  for (int64_t b = 0; b < batch; ++b) {
+    sparse_monomial_values(input + b * in_dim, toff, comp, ex, monomials, mono_ws);
+    for (int64_t o = 0; o < out_dim; ++o) {
+      double v = 0.0;
+      for (int64_t k = out_off[o]; k < out_off[o + 1]; ++k) v += coef_values[k] * mono_ws[coef_terms[k]];
+      out[b * out_dim + o] = v;
+    }
+  }
+}
+
+/* :5757-5813 -- zero factors accumulate their exponents ("zero degree"): degree
+ * one gives the cofactor to the zero component, a higher degree nothing,
+ * degree zero e m / x per support entry. */
+void oracle_symmetric_power_shared_sparse_monomial_adjoint(const double* gout, const double* input, int64_t batch,
+                                                           int64_t in_dim, const int64_t* toff, const int64_t* comp,
+                                                           const int64_t* ex, int64_t monomials,
+                                                           const int64_t* coef_terms, const int64_t* coef_outputs,
+                                                           const double* coef_values, int64_t coefs,
+                                                           int64_t out_dim, double* mono_ws, double* gin) {
+  for (int64_t b = 0; b < batch; ++b) {
+    const double* x = input + b * in_dim;
+    double* g = gin + b * in_dim;
+    for (int64_t c = 0; c < in_dim; ++c) g[c] = 0.0;
+    sparse_term_adjoint(gout + b * out_dim, coef_terms, coef_outputs, coef_values, coefs, monomials, mono_ws);
+    for (int64_t t = 0; t < monomials; ++t) {
+      const double tg = mono_ws[t];
+      double mono = 1.0;
+      int64_t zdeg = 0, zc = -1;
+      for (int64_t q = toff[t]; q < toff[t + 1]; ++q) {
+        if (x[comp[q]] == 0.0) {
+          zdeg += ex[q];
+          zc = comp[q];
+        } else {
+          mono *= ipow_r(x[comp[q]], ex[q]);
+        }
+      }
+      if (zdeg == 1) {
+        g[zc] += tg * mono;
+        continue;
+      }
+      if (zdeg != 0) continue;
+      for (int64_t q = toff[t]; q < toff[t + 1]; ++q) g[comp[q]] += tg * ((double)ex[q] * mono / x[comp[q]]);
+    }
+  }
+}
+
+/* :5815-5955 and host :11206-11330: the monomial adjoints are replaced by the
+ * directional derivatives of the monomials along the tangent (which the
+ * output kernel turns into the output tangent), and each monomial adds its
+ * Hessian along the tangent, weighted by its adjoint, to the input tangent. */
+void oracle_symmetric_power_shared_sparse_monomial_double_backward(
+    const double* tangent, const double* gout, const double* input, int64_t batch, int64_t in_dim,
+    const int64_t* toff, const int64_t* comp, const int64_t* ex, int64_t monomials, const int64_t* out_off,
+    const int64_t* coef_terms, const int64_t* coef_outputs, const double* coef_values, int64_t coefs,
+    int64_t out_dim, double* mono_ws, double* out_tangent, double* in_tangent) {
+  for (int64_t b = 0; b < batch; ++b) {
+    const double* x = input + b * in_dim;
+    const double* v = tangent + b * in_dim;
+    double* it = in_tangent + b * in_dim;
+    for (int64_t c = 0; c < in_dim; ++c) it[c] = 0.0;
+    sparse_term_adjoint(gout + b * out_dim, coef_terms, coef_outputs, coef_values, coefs, monomials, mono_ws);
+    for (int64_t t = 0; t < monomials; ++t) {
+      const double tg = mono_ws[t];
+      double mono = 1.0;
+      int64_t zdeg = 0, z1 = -1, z2 = -1;
+      for (int64_t q = toff[t]; q < toff[t + 1]; ++q) {
+        if (x[comp[q]] == 0.0) {
+          zdeg += ex[q];
+          if (z1 < 0) z1 = comp[q];
+          else if (z2 < 0) z2 = comp[q];
+        } else {
+          mono *= ipow_r(x[comp[q]], ex[q]);
+        }
+      }
+      double dir = 0.0;
+      if (zdeg == 0) {
+        double logdir = 0.0;
+        for (int64_t q = toff[t]; q < toff[t + 1]; ++q) logdir += (double)ex[q] * v[comp[q]] / x[comp[q]];
+        dir = mono * logdir;
+        for (int64_t q = toff[t]; q < toff[t + 1]; ++q) {
+          const int64_t c = comp[q];
+          it[c] += tg * ((double)ex[q] * mono / x[c] * (logdir - v[c] / x[c]));
+        }
+      } else if (zdeg == 1) {
+        dir = v[z1] * mono;
+        double zdir = 0.0;
+        for (int64_t q = toff[t]; q < toff[t + 1]; ++q) {
+          const int64_t c = comp[q];
+          if (c == z1) continue;
+          const double d = (double)ex[q] * mono / x[c];
+          zdir += v[c] * d;
+          it[c] += tg * (v[z1] * d);
+        }
+        it[z1] += tg * zdir;
+      } else if (zdeg == 2) {
+        if (z2 < 0) {
+          it[z1] += tg * (2.0 * mono * v[z1]);
+        } else {
+          it[z1] += tg * (mono * v[z2]);
+          it[z2] += tg * (mono * v[z1]);
+        }
+      }
+      mono_ws[t] = dir;
+    }
+    for (int64_t o = 0; o < out_dim; ++o) {
+      double s = 0.0;
+      for (int64_t k = out_off[o]; k < out_off[o + 1]; ++k) s += coef_values[k] * mono_ws[coef_terms[k]];
+      out_tangent[b * out_dim + o] = s;
+    }
+  }
+}

@@ -126,3 +126,94 @@ def test_inconsistent_tables_are_refused(gpu):
         symmetric_power_shared_monomial_contraction(x, counts, offs, bad_terms, outs, vals)
     with pytest.raises(NotImplementedError, match="reference"):
         symmetric_power_monomial_contraction(x, counts[terms], offs, outs, vals, backend="reference")
+
+
+def _sparse_tables(seed, D=6, M=11, O=5, C=23):
+    """Random sparse supports (a component may appear twice in one support)."""
+    rng = np.random.default_rng(seed)
+    toff, comp, ex = [0], [], []
+    for _ in range(M):
+        for _ in range(int(rng.integers(1, 4))):
+            comp.append(int(rng.integers(0, D)))
+            ex.append(int(rng.integers(1, 3)))
+        toff.append(len(comp))
+    per = np.diff(np.sort(np.concatenate([[0, C], rng.integers(0, C, O - 1)])))
+    offs = np.concatenate([[0], np.cumsum(per)])
+    terms = rng.integers(0, M, C)
+    outs = np.repeat(np.arange(O), per)
+    return (np.array(toff), np.array(comp), np.array(ex), offs, terms, outs, rng.normal(size=C))
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+def test_sparse_shared_monomials_against_the_oracle(gpu, dtype):
+    """Forward, adjoint (autograd through the mirror) and double backward
+    (autograd of the Torch adjoint operator) against the pinned oracle, with
+    rows holding one, two and all-zero factors."""
+    flush(f"sparse shared monomials, random tables, {dtype}")
+    import torch
+
+    from ye3t_amd.runtime import symmetric_power_shared_sparse_monomial_contraction, torch_ops
+
+    toff, comp, ex, offs, terms, outs, vals = _sparse_tables(11)
+    rng = np.random.default_rng(12)
+    B, D, O = 257, 6, len(offs) - 1
+    x = rng.normal(size=(B, D))
+    x[3, 2] = 0.0
+    x[7, 1] = x[7, 4] = 0.0
+    x[9, :] = 0.0
+    real = torch.float64 if dtype == "f64" else torch.float32
+    xd = torch.as_tensor(x, dtype=real, device=gpu)
+    xr = xd.double().cpu().numpy()
+    vr = torch.as_tensor(vals, dtype=real).double().numpy()
+    gd = torch.as_tensor(rng.normal(size=(B, O)), dtype=real, device=gpu)
+    gr = gd.double().cpu().numpy()
+    vd = torch.as_tensor(rng.normal(size=(B, D)), dtype=real, device=gpu)
+    tables = (toff, comp, ex, offs, terms, outs, vals)
+    xs = xd.clone().requires_grad_(True)
+    out = symmetric_power_shared_sparse_monomial_contraction(xs, *tables)
+    (gx,) = torch.autograd.grad(out, xs, gd)
+    ref = oracle.symmetric_power_shared_sparse_monomial(xr, toff, comp, ex, offs, terms, vr)
+    gref = oracle.symmetric_power_shared_sparse_monomial_adjoint(gr, xr, toff, comp, ex, offs, terms, vr)
+    # the Torch operators: the adjoint is differentiable through the double backward
+    torch_ops.register()
+    ops = torch.ops.ye3t_runtime
+    dev_tables = [torch.as_tensor(a, dtype=torch.int64, device=gpu) for a in (toff, comp, ex, offs, terms, outs)]
+    dev_tables.append(torch.as_tensor(vals, dtype=real, device=gpu))
+    g_req = gd.clone().requires_grad_(True)
+    x_req = xd.clone().requires_grad_(True)
+    adj = ops.symmetric_power_shared_sparse_monomial_adjoint(g_req, x_req, *dev_tables)
+    ot, it = torch.autograd.grad(adj, (g_req, x_req), vd)
+    ot_ref, it_ref = oracle.symmetric_power_shared_sparse_monomial_double_backward(
+        vd.double().cpu().numpy(), gr, xr, toff, comp, ex, offs, terms, vr)
+    errs = [column_rel_error(out.detach().cpu().numpy(), ref), column_rel_error(gx.cpu().numpy(), gref),
+            column_rel_error(adj.detach().cpu().numpy(), gref), column_rel_error(ot.cpu().numpy(), ot_ref),
+            column_rel_error(it.cpu().numpy(), it_ref)]
+    flush("  " + " ".join(f"{e:.2e}" for e in errs))
+    assert max(errs) < TOL[dtype]
+    # the operators pass Torch's operator checks (schema, fake, autograd registration)
+    if dtype == "f64":
+        for op, args in ((ops.symmetric_power_shared_sparse_monomial.default, (xd, *dev_tables)),
+                         (ops.symmetric_power_shared_sparse_monomial_adjoint.default, (gd, xd, *dev_tables)),
+                         (ops.symmetric_power_shared_sparse_monomial_double_backward.default,
+                          (vd, gd, xd, *dev_tables))):
+            result = torch.library.opcheck(op, args, raise_exception=False)
+            assert all(v == "SUCCESS" for v in result.values()), result
+
+
+def test_sparse_tables_are_refused_on_bad_indices(gpu):
+    import torch
+
+    from ye3t_amd.runtime import symmetric_power_shared_sparse_monomial_contraction
+
+    toff, comp, ex, offs, terms, outs, vals = _sparse_tables(13)
+    x = torch.zeros((4, 6), dtype=torch.float64, device=gpu)
+    bad = comp.copy()
+    bad[0] = 6
+    with pytest.raises(ValueError, match="term_components"):
+        symmetric_power_shared_sparse_monomial_contraction(x, toff, bad, ex, offs, terms, outs, vals)
+    bad = ex.copy()
+    bad[1] = 0
+    with pytest.raises(ValueError, match="positive"):
+        symmetric_power_shared_sparse_monomial_contraction(x, toff, comp, bad, offs, terms, outs, vals)
+    with pytest.raises(ValueError, match="equal length"):
+        symmetric_power_shared_sparse_monomial_contraction(x, toff, comp[:-1], ex, offs, terms, outs, vals)

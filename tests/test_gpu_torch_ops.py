@@ -140,3 +140,35 @@ def test_density_and_monomial_operators(gpu):
     y, gy = ops.spherical_harmonics_table_with_derivative(e, 3, True, 1e-12)
     y2, gy2 = runtime.spherical_harmonics_table_with_derivative(e, 3, real_output=True)
     assert torch.equal(y, y2) and torch.equal(gy, gy2)
+
+
+def test_capability_report_hip_branch(gpu):
+    """On the GPU the report's HIP branch is on: the ``cuda`` keys describe
+    torch's ``cuda`` device type (the HIP device on ROCm), every listed
+    operator has a device kernel registered, and the device facts are read
+    from the library."""
+    flush("capability report, HIP branch")
+    import torch
+
+    from ye3t_amd import runtime
+    from ye3t_amd.runtime import native, torch_ops
+
+    report = runtime.native_execution_plan_capabilities()
+    assert report["hip"] is True and report["cuda"] is True
+    assert report["hip_operations"] == report["operations"] and report["operations"]
+    torch_ops.register()
+    for name in report["cuda_operations"]:
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(f"ye3t_runtime::{name}", "CUDA"), name
+    for name in ("symmetric_power_monomial", "symmetric_power_shared_monomial", "factorized_angular",
+                 "density_accumulate", "symmetric_power_shared_sparse_monomial_double_backward"):
+        assert name in report["cuda_operations"], name
+    assert report["symmetric_power_shared_sparse_monomial"] is True
+    assert report["symmetric_power_shared_cuda_min_reuse"] == 8.0
+    assert report["symmetric_power_shared_cuda_grad_min_batch"] == 256
+    assert report["symmetric_power_shared_cuda_forward_min_batch"] == 1024
+    assert report["cuda_density_auto_min_work_items"] == 0
+    dev = report["hip_device"]
+    caps = native.device_caps(torch.cuda.current_device())
+    assert dev == caps
+    flush(f"  hip_device {dev}")
+    assert "gfx950" in str(dev.get("arch", dev))

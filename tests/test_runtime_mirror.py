@@ -13,12 +13,28 @@ import torch
 from ye3t_amd import runtime
 from ye3t_amd.runtime import native
 
-# keys of the reference report that consumers test (execution_plan.py:6316-6662)
-REFERENCE_KEYS = ("schema", "torch_independent_core_source", "prebuilt_extension", "cpu", "cuda",
-                  "cuda_operations", "cuda_density_auto_min_work_items", "segmented_factorized_angular",
-                  "heterogeneous_factorized_roots", "triton_available", "triton_cuda_available",
-                  "triton_operations", "core_abi_version", "factorized_workspace_metadata", "dtypes",
-                  "analysis_orientation", "operations")
+# every key of the reference report, in its order (execution_plan.py:6316-6849)
+REFERENCE_KEYS = (
+    "schema", "torch_independent_core_source", "cmake_core_target", "prebuilt_extension", "cpu", "cuda",
+    "cuda_operations", "cuda_density_auto_min_work_items", "cuda_edge_outer_auto_min_work_items",
+    "cpu_edge_outer_auto_min_work_items", "cpu_carrier_gated_scatter_auto_min_work_items",
+    "cuda_carrier_gated_scatter_auto_min_work_items", "real_control_carrier_gates", "residual_carrier_gated_scatter",
+    "segmented_carrier_gated_scatter", "segmented_factorized_angular", "source_arena_gather",
+    "source_arena_channel_transform", "carrier_channel_transform", "carrier_role_channel_map_adjoint",
+    "cuda_segmented_carrier_scatter_min_node_feature_work", "real_control_carrier_channel_update",
+    "scheduled_softmax_gaussian_role_density", "symmetric_power_monomial_double_backward",
+    "symmetric_power_shared_monomial_double_backward", "symmetric_power_shared_monomial_factored_double_backward",
+    "symmetric_power_shared_double_backward_default_algorithm", "symmetric_power_shared_sparse_monomial",
+    "cpu_carrier_channel_update_auto_max_work_items", "cuda_carrier_channel_update_auto_max_work_items",
+    "cuda_carrier_channel_update_auto_min_work_items", "symmetric_power_cpu_auto_max_batch",
+    "symmetric_power_cpu_auto_min_power", "symmetric_power_shared_cpu_min_reuse",
+    "symmetric_power_shared_cpu_min_batch", "symmetric_power_shared_cuda_min_reuse",
+    "symmetric_power_shared_cuda_grad_min_batch", "symmetric_power_shared_cuda_forward_min_batch",
+    "triton_available", "triton_cuda_available", "triton_real_convention_id", "triton_operations",
+    "core_abi_version", "factorized_workspace_metadata", "heterogeneous_factorized_roots",
+    "cached_heterogeneous_factorized_reverse", "dtypes", "analysis_orientation", "operations",
+    "compact_exterior_power_max_native_order",
+)
 
 # operation names of the reference report's ``operations`` tuple for the ops
 # this backend implements (execution_plan.py:6662-6850)
@@ -28,10 +44,18 @@ REFERENCE_NAMES = {"cheb_exp_cos_radial_table_with_derivative", "real_spherical_
 
 def test_capability_report_keys_and_names():
     report = runtime.native_execution_plan_capabilities()
-    for key in REFERENCE_KEYS:
-        assert key in report, key
+    assert len(REFERENCE_KEYS) == len(set(REFERENCE_KEYS)) == 50
+    assert [k for k in report if k in REFERENCE_KEYS] == list(REFERENCE_KEYS)
     assert report["schema"] == "ye3t_execution_plan_v1"
-    assert report["cuda"] is False and report["cuda_operations"] == ()
+    # the reference's own assertions on its report (tests/test_execution_plan_native.py:569-585)
+    assert report["symmetric_power_cpu_auto_max_batch"] == 32
+    assert report["symmetric_power_cpu_auto_min_power"] == 6
+    assert report["symmetric_power_shared_cpu_min_reuse"] == 3.0
+    assert report["symmetric_power_shared_cpu_min_batch"] == 8
+    assert report["triton_real_convention_id"] == "real_tesseral_from_complex_condon_shortley_young_orthogonal_v1"
+    assert "dense_source_analysis_C_dagger_L_v" in report["triton_operations"]
+    assert report["compact_exterior_power_max_native_order"] == 8
+    assert report["cpu"] is False  # no reference extension in this process
     assert report["core_abi_version"] == native.ABI_VERSION >= report["minimum_core_abi_version"] == 42
     assert report["analysis_orientation"] == "conjugate_transpose"
     assert REFERENCE_NAMES <= set(report["operations"])
@@ -41,7 +65,22 @@ def test_capability_report_keys_and_names():
     # no GPU in this environment: the HIP capability is off and lists nothing
     if not torch.cuda.is_available():
         assert report["hip"] is False and report["hip_operations"] == ()
+        assert report["cuda"] is False and report["cuda_operations"] == ()
+        assert report["symmetric_power_shared_cuda_min_reuse"] is None
         assert "hip_device" not in report
+
+
+def test_symmetric_power_auto_dispatch_reads_the_report():
+    """The reference's one in-library consumer of the report
+    (``runtime/symmetric_power.py:1131-1150``), restated: on a device tensor it
+    picks the native kernel when ``cuda_operations`` names it; on the CPU it
+    reads the two CPU thresholds, which must be integers whenever
+    ``prebuilt_extension`` is true."""
+    report = runtime.native_execution_plan_capabilities()
+    if report["prebuilt_extension"]:
+        assert int(report["symmetric_power_cpu_auto_max_batch"]) == 32
+        assert int(report["symmetric_power_cpu_auto_min_power"]) == 6
+    assert ("symmetric_power_monomial" in report["cuda_operations"]) == report["cuda"]
 
 
 def test_has_hip_and_has_cpu_are_exported():

@@ -15,6 +15,8 @@ same order the reference's ``sorted(compact_label)`` produces.
 """
 
 from collections import Counter
+from collections.abc import Mapping
+from dataclasses import dataclass
 from functools import lru_cache
 
 
@@ -261,6 +263,151 @@ def compact_labels_by_L(nin, lin, tree_type="balanced"):
     tree_type = validate_tree_type(tree_type)
     return {L: [compact_label(lab, tree_type) for lab in labs]
             for L, labs in structured_labels_by_L(tuple(nin), tuple(lin), tree_type).items()}
+
+
+def _freeze_key(value):
+    if isinstance(value, Mapping):
+        raise TypeError("Compact-label basis keys cannot contain mappings.")
+    if isinstance(value, (tuple, list)):
+        return tuple(_freeze_key(v) for v in value)
+    return value
+
+
+def _label_int(value, name):
+    if isinstance(value, bool) or not isinstance(value, int):
+        raise TypeError(f"{name} values must be integers, not {value!r}.")
+    return int(value)
+
+
+def _key_from_json(value):
+    """A basis key read back from its JSON list form (``sym`` / ``sym_numeric`` / ``node`` tags)."""
+    if not isinstance(value, (tuple, list)):
+        raise TypeError("Compact-label basis_key must be a recursive sequence.")
+    key = tuple(value)
+    if not key:
+        return ()
+    if not isinstance(key[0], str):
+        raise TypeError("Compact-label basis-key tags must be strings.")
+    if key[0] in {"sym", "sym_numeric"}:
+        if len(key) != 3:
+            raise ValueError(f"Compact-label {key[0]} basis keys require tag, L, and copy index.")
+        L, copy = _label_int(key[1], "basis_key.L"), _label_int(key[2], "basis_key.copy_index")
+        if L < 0 or copy < 0:
+            raise ValueError("Compact-label symmetric basis-key indices must be non-negative.")
+        return (key[0], L, copy)
+    if key[0] == "node":
+        if len(key) != 3:
+            raise ValueError("Compact-label node basis keys require tag, left key, and right key.")
+        return ("node", _key_from_json(key[1]), _key_from_json(key[2]))
+    raise ValueError(f"Unknown compact-label basis-key tag {key[0]!r}.")
+
+
+def _key_to_json(value):
+    if isinstance(value, tuple):
+        return [_key_to_json(v) for v in value]
+    return value
+
+
+@dataclass(frozen=True)
+class CompactLabel:
+    """One exact ACE label as ``count`` reports it (reference ``ye3t/core/labels.py:65-211``).
+
+    ``n_tuple`` / ``l_tuple`` are the canonical leaf order, ``internal_Ls`` the
+    post-order internal couplings ending in ``L_R``, ``basis_key`` the nested
+    symmetric-block copy selectors (empty when every block takes copy 0).
+    """
+
+    n_tuple: tuple
+    l_tuple: tuple
+    internal_Ls: tuple
+    tree_type: str = "balanced"
+    basis_key: tuple = ()
+
+    def __post_init__(self):
+        object.__setattr__(self, "n_tuple", tuple(_label_int(v, "n_tuple") for v in self.n_tuple))
+        object.__setattr__(self, "l_tuple", tuple(_label_int(v, "l_tuple") for v in self.l_tuple))
+        object.__setattr__(self, "internal_Ls", tuple(_label_int(v, "internal_Ls") for v in self.internal_Ls))
+        if not isinstance(self.tree_type, str):
+            raise TypeError("Compact-label tree_type must be a string.")
+        object.__setattr__(self, "tree_type", validate_tree_type(self.tree_type))
+        object.__setattr__(self, "basis_key", _freeze_key(self.basis_key))
+        if not self.n_tuple or len(self.n_tuple) != len(self.l_tuple):
+            raise ValueError("Compact labels require equally sized non-empty n_tuple and l_tuple.")
+        if any(v < 0 for v in self.n_tuple):
+            raise ValueError("Compact-label radial indices must be non-negative.")
+        if any(v < 0 for v in self.l_tuple + self.internal_Ls):
+            raise ValueError("Compact-label angular momenta must be non-negative.")
+
+    @property
+    def rank(self):
+        return len(self.l_tuple)
+
+    @property
+    def L_R(self):
+        return self.internal_Ls[-1] if self.internal_Ls else self.l_tuple[0]
+
+    def angular_key(self):
+        ls = ",".join(str(x) for x in self.l_tuple)
+        Ls = ",".join(str(x) for x in self.internal_Ls)
+        key = "" if not self.basis_key else f"|{self.basis_key!r}"
+        return f"{ls}_{Ls}{key}" if self.tree_type == "balanced" else f"{self.tree_type}:{ls}_{Ls}{key}"
+
+    def full_key(self):
+        return ",".join(str(x) for x in self.n_tuple) + "|" + self.angular_key()
+
+    def compact_label(self):
+        """The 3-, 4- or 5-part tuple form (``basis/labels.py:49-56``)."""
+        head = (self.n_tuple, self.l_tuple, self.internal_Ls)
+        if not self.basis_key:
+            return head if self.tree_type == "balanced" else head + (self.tree_type,)
+        return head + (self.tree_type, self.basis_key)
+
+    def payload(self):
+        """The five-field tuple a report hashes (``couplings/__init__.py:428-440``)."""
+        return (self.n_tuple, self.l_tuple, self.internal_Ls, self.tree_type, self.basis_key)
+
+    def to_dict(self):
+        return {"n_tuple": list(self.n_tuple), "l_tuple": list(self.l_tuple), "internal_Ls": list(self.internal_Ls),
+                "L_R": int(self.L_R), "tree_type": str(self.tree_type), "basis_key": _key_to_json(self.basis_key)}
+
+    @classmethod
+    def from_dict(cls, payload):
+        if not isinstance(payload, Mapping):
+            raise TypeError("Compact-label payload must be a mapping.")
+        unknown = set(payload) - {"n_tuple", "l_tuple", "internal_Ls", "L_R", "tree_type", "basis_key"}
+        if unknown:
+            raise ValueError("Compact-label payload has unknown fields: " + ", ".join(sorted(map(str, unknown))))
+        missing = {"n_tuple", "l_tuple", "internal_Ls"} - set(payload)
+        if missing:
+            raise ValueError("Compact-label payload is missing fields: " + ", ".join(sorted(missing)))
+        label = cls(tuple(payload["n_tuple"]), tuple(payload["l_tuple"]), tuple(payload["internal_Ls"]),
+                    payload.get("tree_type", "balanced"), _key_from_json(payload.get("basis_key", ())))
+        if "L_R" in payload and _label_int(payload["L_R"], "L_R") != int(label.L_R):
+            raise ValueError("Compact-label L_R does not match its coupling label.")
+        return label
+
+    @classmethod
+    def from_tuple(cls, value):
+        value = tuple(value)
+        if len(value) == 3:
+            return cls(tuple(value[0]), tuple(value[1]), tuple(value[2]))
+        if len(value) == 4:
+            if isinstance(value[3], str):
+                return cls(tuple(value[0]), tuple(value[1]), tuple(value[2]), value[3])
+            return cls(tuple(value[0]), tuple(value[1]), tuple(value[2]), basis_key=_freeze_key(value[3]))
+        if len(value) == 5:
+            return cls(tuple(value[0]), tuple(value[1]), tuple(value[2]), str(value[3]), _freeze_key(value[4]))
+        raise ValueError("Compact label must have 3, 4, or 5 parts: "
+                         "(n_tuple, l_tuple, internal_Ls[, tree_type][, basis_key])")
+
+
+def normalize_compact_label(value):
+    """A :class:`CompactLabel` from a label, its dict form or its tuple form."""
+    if isinstance(value, CompactLabel):
+        return value
+    if isinstance(value, Mapping):
+        return CompactLabel.from_dict(value)
+    return CompactLabel.from_tuple(value)
 
 
 def counts_by_L(nin, lin):

@@ -479,10 +479,15 @@ def _as_tuple(value):
 
 
 def structured_label_from_compact(compact):
-    """The structured label whose ``compact_label`` is ``compact`` (its ``count`` order)."""
-    compact = _as_tuple(compact)
+    """The structured label whose ``compact_label`` is ``compact`` (its ``count`` order).
+
+    ``compact`` is a :class:`~ye3t_amd.core.basis.CompactLabel`, its dict form
+    or a 3-, 4- or 5-part tuple.
+    """
+    record = _basis.normalize_compact_label(_as_tuple(compact) if isinstance(compact, list) else compact)
+    compact = record.compact_label()
     n_seq, l_seq, internal = compact[0], compact[1], compact[2]
-    tree_type = compact[3] if len(compact) > 3 else "balanced"
+    tree_type = record.tree_type
     target = int(internal[-1]) if internal else int(l_seq[0])
     for lab in _basis.structured_labels_by_L(tuple(n_seq), tuple(l_seq), tree_type).get(target, ()):
         if _basis.compact_label(lab, tree_type) == compact:
@@ -560,7 +565,8 @@ def generate_real_factorized_coefficient_schedule_for_labels(labels, component_i
     (``core/couplings.py:1818-1966``): assembled label-major, components in
     ``component_indices`` order, terms in :func:`expand_real_path` order.
     """
-    labels = [_as_tuple(lab) for lab in labels]
+    labels = [_basis.normalize_compact_label(_as_tuple(lab) if isinstance(lab, list) else lab).payload()
+              for lab in labels]
     if not labels:
         return RealFactorizedCoefficientSchedule(
             rank=0, block_count=0, L_R=0, n_tuple=(), l_tuple=(), tree_type="balanced", block_specs=(),

@@ -5,18 +5,20 @@ Mirrors the reference entry points used on the hot path:
 * ``compile_ace_factorized_schedules_by_L`` / ``ACEFactorizedScheduleReport``
   (reference ``ye3t/couplings/__init__.py:2565-2706``), including the
   ``convention_hash`` payload (``:242-252, 2685-2697``);
-* ``count`` / ``plan`` for ``carrier="ACE_density"`` (``:2709-3077``), reduced to
-  the fixed-content label path; their hash payloads embed the reference's full
-  spec serialisation, which this package does not carry, so those two hashes
-  are this package's own (documented as not reproducing the reference string).
+* ``count`` / ``plan`` for ``carrier="ACE_density"`` (``:2709-3077``): the same
+  request records (:mod:`ye3t_amd.spec`), labels, reports and
+  ``convention_hash`` payloads, so the hash strings equal the reference's.
 """
 
 import hashlib
 import json
+import math
+from collections import Counter
 from dataclasses import dataclass, field
 
 from ye3t_amd.core import basis as _basis
 from ye3t_amd.core import couplings as core_couplings
+from ye3t_amd.spec import YE3TBackendPlan, YE3TSpec, coerce_spec, plan_backend, target_partition
 
 
 def _json_default(value):
@@ -132,12 +134,12 @@ def compile_ace_factorized_schedules_by_L(*, content=None, input_Ls=None, tree_s
 
 @dataclass(frozen=True, eq=False)
 class MultiplicityReport:
-    """Labels and counts of one fixed-content ACE_density request."""
+    """Valid labels and counts of one fixed-content request (reference ``:2117-2160``)."""
 
-    content: tuple
-    input_Ls: tuple
+    spec: YE3TSpec
     counts_by_target: dict
     labels_by_target: dict
+    content: tuple
     carrier: str
     target: dict
     backend: str
@@ -145,65 +147,209 @@ class MultiplicityReport:
     validation_report: dict
     provenance: dict = field(default_factory=dict)
 
-    def labels_for_target(self, target_L):
+    @property
+    def labels(self):
+        return tuple(lab for labs in self.labels_by_target.values() for lab in labs)
+
+    def labels_for_target(self, target_L=None):
+        if target_L is None:
+            target_L = int(self.spec.target_rotation.L_R)
         return tuple(self.labels_by_target.get(int(target_L), ()))
 
-    def require_label(self, label, *, target_L):
-        if tuple(label) not in set(self.labels_for_target(target_L)):
-            raise ValueError(f"Label {label!r} is not valid for target_L={target_L}.")
-        return tuple(label)
+    def contains_label(self, label, *, target_L=None):
+        candidate = _basis.normalize_compact_label(label)
+        pool = self.labels if target_L is None else self.labels_for_target(int(target_L))
+        return candidate in set(pool)
+
+    def require_label(self, label, *, target_L=None):
+        candidate = _basis.normalize_compact_label(label)
+        if not self.contains_label(candidate, target_L=target_L):
+            where = "any target" if target_L is None else f"L_R={int(target_L)}"
+            raise ValueError("Invalid descriptor label for this YE3T coupling request: "
+                             f"{candidate!r} is not in the fixed-content multiplicity report for {where}.")
+        return candidate
+
+    def to_dict(self):
+        return {
+            "content": list(self.content),
+            "carrier": self.carrier,
+            "target": dict(self.target),
+            "backend": self.backend,
+            "convention_hash": self.convention_hash,
+            "validation_report": dict(self.validation_report),
+            "counts_by_target": {int(k): int(v) for k, v in self.counts_by_target.items()},
+            "labels_by_target": {int(k): [lab.payload() for lab in labs]
+                                 for k, labs in self.labels_by_target.items()},
+            "provenance": dict(self.provenance),
+        }
 
 
 @dataclass(frozen=True, eq=False)
 class CouplerPlan:
+    """Backend plan plus the count it was made from (reference ``:2163-2215``)."""
+
+    spec: YE3TSpec
     report: MultiplicityReport
+    backend_plan: YE3TBackendPlan
+    content: tuple
+    carrier: str
+    target: dict
     backend: str
     convention_hash: str
     validation_report: dict
     provenance: dict = field(default_factory=dict)
 
 
-def count(request=None, *, content=None, input_Ls=None, target_L=None, target_permutation=None,
-          carrier=None, tree_schedule=None, **_unused):
-    """Valid compact labels of a fixed-content ACE_density request (reference ``:2709-2965``)."""
-    if request is not None:
-        raise ValueError("Only keyword fixed-content ACE_density requests are supported.")
-    carrier = "ACE_density" if carrier is None else str(carrier)
-    if carrier != "ACE_density":
-        raise ValueError("This backend supports only carrier='ACE_density'.")
-    if target_permutation not in (None, "trivial", "symmetric"):
-        raise ValueError("ACE_density supports only the globally trivial Young sector.")
-    n_in = tuple(int(v) for v in content)
-    l_in = tuple(int(v) for v in input_Ls)
-    tree_type = _basis.validate_tree_type(tree_schedule)
-    target_L = 0 if target_L is None else int(target_L)
-    labels = tuple(_basis.compact_labels_by_L(n_in, l_in, tree_type).get(target_L, ()))
-    target = {"permutation": "trivial", "rotation": {"L_R": target_L}}
-    validation = {
-        "passed": True, "carrier": carrier, "target_L": target_L, "label_kind": "compact",
-        "label_count": len(labels), "count": len(labels),
-        "valid_labels_from": "ye3t.fixed_content.FixedContentDecomposition.compact_labels_by_target",
-        "fixed_content_validation": {"passed": True},
+def _input_Ls_from_spec(spec, input_Ls=None):
+    """``input_Ls`` argument, else the spec's metadata, else all zeros (reference ``:255-266``)."""
+    values = spec.metadata.get("input_Ls", ()) if input_Ls is None else input_Ls
+    values = tuple(int(v) for v in (values or ()))
+    if not values:
+        values = tuple(0 for _ in spec.content)
+    if len(values) != len(spec.content):
+        raise ValueError(f"input_Ls length {len(values)} must match content rank {len(spec.content)}.")
+    return values
+
+
+def _fixed_content_validation(content, input_Ls, tree_type):
+    """The orbit-module summary of ``FixedContentModule.decompose`` (``fixed_content.py:222-293``).
+
+    The stabilizer is the Young subgroup permuting equal ``(n, l)`` leaves
+    (``generalized_irreps.py:69-83``), so its order is the product of the
+    factorials of the leaf multiplicities; the orbit of the ordered leaves has
+    ``rank! / order`` members, each carrying ``prod (2 l + 1)`` magnetic states.
+    The global Young x rotation sectors decompose that same space, so their
+    dimensions sum to it.
+    """
+    _basis.validate_tree_type(tree_type)
+    if not content:
+        raise ValueError("FixedContentSpec requires at least one content entry.")
+    if len(content) != len(input_Ls):
+        raise ValueError("content and input_Ls must have the same length, "
+                         f"got {len(content)} and {len(input_Ls)}.")
+    if any(L < 0 for L in input_Ls):
+        raise ValueError(f"input_Ls must be nonnegative, got {tuple(input_Ls)!r}.")
+    order = 1
+    for mult in Counter(zip(content, input_Ls)).values():
+        order *= math.factorial(mult)
+    orbit = math.factorial(len(content)) // order
+    dim = orbit
+    for L in input_Ls:
+        dim *= 2 * int(L) + 1
+    return {
+        "passed": True,
+        "scope": "fixed_content_orbit_module_decomposition",
+        "catalog_validation_passed": True,
+        "orbit_module_dim": int(dim),
+        "decomposed_dim": int(dim),
+        "stabilizer_order": int(order),
+        "orbit_dimension": int(orbit),
+        "compact_labels_from": "ye3t.core.api.YE3TAPI.compact_labels_by_target_L",
+        "global_sectors_from": "ye3t.fixed_content.FixedContentModule.decompose",
     }
-    payload = {"content": n_in, "input_Ls": l_in, "target": target, "backend": "symmetric_power_fast_path",
-               "labels": [list(map(_json_ready, lab)) for lab in labels]}
+
+
+_PRIMITIVE_MODES = {None, "exact", "full_exact_basis", "original_exact"}
+
+
+def count(request=None, *, content=None, input_Ls=None, target_L=None, target_permutation=None, carrier=None,
+          carrier_options=None, tree_schedule=None, coefficient_backend=None, fast_path_policy=None,
+          validation_scope=None, runtime_status=None, metadata=None):
+    """Valid compact labels and their count for a fixed-content ACE_density request.
+
+    Reference ``ye3t/couplings/__init__.py:2709-2965`` on its ACE_density
+    branch: the same spec merge, parity and Young-sector checks, label order,
+    reports and ``convention_hash`` payload
+    ``{spec, input_Ls, target, backend, labels}``.  Other carriers and the
+    primitive basis modes belong to the reference's wider coupler and raise.
+    """
+    spec = coerce_spec(request, content=content, input_Ls=input_Ls, target_L=target_L,
+                       target_permutation=target_permutation, carrier=carrier, carrier_options=carrier_options,
+                       tree_schedule=tree_schedule, coefficient_backend=coefficient_backend,
+                       fast_path_policy=fast_path_policy, validation_scope=validation_scope,
+                       runtime_status=runtime_status, metadata=metadata)
+    if spec.carrier != "ACE_density":
+        raise ValueError(f"carrier={spec.carrier!r} is not served by this backend; it computes only "
+                         "the ACE_density carrier.")
+    l_in = _input_Ls_from_spec(spec, input_Ls=input_Ls)
+    requested_parity = spec.target_rotation.parity
+    natural = "odd" if sum(l_in) % 2 else "even"
+    if requested_parity in {"even", "odd"} and requested_parity != natural:
+        raise ValueError(f"Requested parity={requested_parity!r} is incompatible with the natural product parity "
+                         f"{natural!r} for input_Ls={l_in!r}.")
+    partition = target_partition(spec.target_permutation, len(spec.content))
+    if partition != (len(spec.content),):
+        raise ValueError("ACE_density supports only the globally trivial Young sector.")
+    carrier_validation = {"carrier": spec.carrier, "passed": True, "scope": "generic_fixed_content_carrier"}
+    n_in = tuple(int(v) for v in spec.content)
+    fixed = _fixed_content_validation(n_in, l_in, spec.tree_schedule)
+    tree_type = _basis.validate_tree_type(spec.tree_schedule)
+    L = int(spec.target_rotation.L_R) if target_L is None else int(target_L)
+    mode = spec.carrier_options.get("basis_mode", spec.carrier_options.get("primitive_mode", None))
+    if mode not in _PRIMITIVE_MODES:
+        raise ValueError(f"basis_mode={mode!r}: primitive compact basis modes are not served by this backend.")
+    labels = tuple(_basis.CompactLabel.from_tuple(c)
+                   for c in _basis.compact_labels_by_L(n_in, l_in, tree_type).get(L, ()))
+    backend_plan = plan_backend(spec, input_Ls=l_in)
+    target = {"permutation": spec.target_permutation, "rotation": spec.target_rotation.to_dict()}
+    validation_report = {
+        "passed": True,
+        "scope": "fixed_content_young_x_SO3_multiplicity_count_with_natural_input_parity",
+        "content_rank": len(spec.content),
+        "input_Ls": l_in,
+        "natural_product_parity": natural,
+        "target_L": L,
+        "target_permutation": spec.target_permutation,
+        "target_partition": partition,
+        "carrier": spec.carrier,
+        "label_kind": "compact",
+        "label_count": len(labels),
+        "count": len(labels),
+        "fixed_content_validation": fixed,
+        "basis_mode": "exact",
+        "valid_labels_from": "ye3t.fixed_content.FixedContentDecomposition.compact_labels_by_target",
+        "carrier_validation": carrier_validation,
+    }
+    provenance = {
+        "api": "ye3t.couplings.count",
+        "lower_level_api": "ye3t.fixed_content.FixedContentModule",
+        "fixed_content_multiplicity_source": "YE3TBasisLabeler",
+        "rank_product_rule": ("LR/induction for rank-additive products; Kronecker for same-rank products "
+                              "in lower-level coupler plans"),
+        "ace_density_young_sector": "globally trivial lambda=(N)",
+        "carrier_validation_source": "ye3t.couplings",
+    }
+    payload = {"spec": spec.to_dict(), "input_Ls": l_in, "target": target,
+               "backend": backend_plan.selected_backend, "labels": [lab.payload() for lab in labels]}
     return MultiplicityReport(
-        content=n_in, input_Ls=l_in, counts_by_target={target_L: len(labels)},
-        labels_by_target={target_L: labels}, carrier=carrier, target=target,
-        backend="symmetric_power_fast_path", convention_hash=_convention_hash(payload),
-        validation_report=validation, provenance={"api": "ye3t_amd.couplings.count"})
+        spec=spec, counts_by_target={L: len(labels)}, labels_by_target={L: labels}, content=tuple(spec.content),
+        carrier=spec.carrier, target=target, backend=backend_plan.selected_backend,
+        convention_hash=_convention_hash(payload), validation_report=validation_report, provenance=provenance)
 
 
-def _json_ready(value):
-    if isinstance(value, tuple):
-        return [_json_ready(v) for v in value]
-    return value
+def plan(request=None, *, input_Ls=None, **kwargs):
+    """Backend plan with the count's provenance (reference ``:2967-3077``, ACE_density branch).
 
-
-def plan(report):
-    """Backend plan: ACE_density always takes the symmetric-power fast path (``global_coupler.py:4679-4686``)."""
-    validation = {"passed": True, "selected_backend": "symmetric_power_fast_path",
-                  "report_hash": report.convention_hash}
-    return CouplerPlan(report=report, backend="symmetric_power_fast_path",
-                       convention_hash=_convention_hash(validation), validation_report=validation,
-                       provenance={"api": "ye3t_amd.couplings.plan"})
+    ``request`` is a :class:`MultiplicityReport`, or anything :func:`count`
+    accepts.  The hash payload is ``{report: report.to_dict(), backend_plan:
+    {requested, selected, fast_path_policy}}``.
+    """
+    if isinstance(request, MultiplicityReport):
+        report = request
+    else:
+        report = count(request, input_Ls=input_Ls, **kwargs)
+    spec = report.spec
+    backend_plan = plan_backend(spec, input_Ls=_input_Ls_from_spec(spec, input_Ls=input_Ls))
+    validation_report = {**dict(report.validation_report),
+                         "backend_plan_selected": backend_plan.selected_backend,
+                         "backend_plan_reason": backend_plan.reason}
+    provenance = {**dict(report.provenance), "api": "ye3t.couplings.plan",
+                  "backend_planner": "ye3t.global_coupler.plan_ye3t_backend"}
+    payload = {"report": report.to_dict(),
+               "backend_plan": {"requested": backend_plan.requested_backend,
+                                "selected": backend_plan.selected_backend,
+                                "fast_path_policy": backend_plan.fast_path_policy}}
+    return CouplerPlan(spec=spec, report=report, backend_plan=backend_plan, content=report.content,
+                       carrier=report.carrier, target=report.target, backend=backend_plan.selected_backend,
+                       convention_hash=_convention_hash(payload), validation_report=validation_report,
+                       provenance=provenance)

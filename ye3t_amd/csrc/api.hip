@@ -228,52 +228,6 @@ inline unsigned grid_for(int64_t work, int threads) {
   return unsigned(g);
 }
 
-
-// fp64 pipe probe: per iteration a wave issues either four independent
-// v_mfma_f64_16x16x4f64 (8192 flops) or 64 fp64 FMAs over 8 independent
-// chains per lane (8192 flops), or both; MODE 3 gives the second half of the
-// workgroups the MFMAs and the first half the FMAs, so that at two
-// workgroups per SIMD (the dispatcher fills every SIMD once before it starts
-// on the second round) each SIMD holds one wave of each.  Lane 0 of every
-// wave writes its SIMD's identity (HW_ID and XCC_ID registers) instead of a
-// sink value, so the caller can check that pairing.
-template <int MODE>
-__global__ __launch_bounds__(64) void fp64_pipe_probe_kernel(double* __restrict__ out, int iterations, double a,
-                                                             double b) {
-  typedef double d4 __attribute__((ext_vector_type(4)));
-  d4 acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
-  double x[8];
-#pragma unroll
-  for (int r = 0; r < 8; ++r) x[r] = a + double(threadIdx.x + r);
-  const bool second = blockIdx.x >= gridDim.x / 2;
-  const bool matrix = MODE == 0 || MODE == 2 || (MODE == 3 && second);
-  const bool vector = MODE == 1 || MODE == 2 || (MODE == 3 && !second);
-  for (int i = 0; i < iterations; ++i) {
-    if (matrix) {
-      acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc1, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc2, 0, 0, 0);
-      acc3 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc3, 0, 0, 0);
-    }
-    if (vector) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-#pragma unroll
-        for (int r = 0; r < 8; ++r) x[r] = fma(x[r], a, b);
-    }
-  }
-  double s = acc0[0] + acc1[1] + acc2[2] + acc3[3];
-#pragma unroll
-  for (int r = 0; r < 8; ++r) s += x[r];
-  if (threadIdx.x == 0) {
-    // HW_ID (hwreg 4: wave, SIMD, CU, SH, SE fields) and XCC_ID (hwreg 20), 32 bits each
-    const unsigned hw = unsigned(__builtin_amdgcn_s_getreg((31 << 11) | 4));
-    const unsigned xcc = unsigned(__builtin_amdgcn_s_getreg((31 << 11) | 20));
-    s = double((uint64_t(xcc & 0xF) << 32) | uint64_t(hw));
-  }
-  out[int64_t(blockIdx.x) * 64 + threadIdx.x] = s;
-}
-
 }  // namespace ye3t
 
 using namespace ye3t;
@@ -400,23 +354,6 @@ int ye3t_hip_density_accumulate_adjoint(int dtype, const void* adj, const int64_
                        int(CV), N, (float*)out);
   }
   return check_launch("density_adjoint_kernel");
-}
-
-int ye3t_hip_fp64_pipe_probe(int mode, int64_t workgroups, int iterations, double* out, ye3t_stream_t stream) {
-  clear_error();
-  YE3T_REQUIRE(mode >= 0 && mode <= 3, "mode must be 0..3");
-  YE3T_REQUIRE(workgroups >= 1 && workgroups <= (int64_t(1) << 20), "workgroups must be in [1, 2^20]");
-  YE3T_REQUIRE(iterations >= 0, "negative iterations");
-  YE3T_REQUIRE(out != nullptr, "NULL output");
-  const hipStream_t s = as_stream(stream);
-  const dim3 grid = dim3(unsigned(workgroups)), block = dim3(64);
-  switch (mode) {
-    case 0: hipLaunchKernelGGL(fp64_pipe_probe_kernel<0>, grid, block, 0, s, out, iterations, 0.999, 0.001); break;
-    case 1: hipLaunchKernelGGL(fp64_pipe_probe_kernel<1>, grid, block, 0, s, out, iterations, 0.999, 0.001); break;
-    case 2: hipLaunchKernelGGL(fp64_pipe_probe_kernel<2>, grid, block, 0, s, out, iterations, 0.999, 0.001); break;
-    default: hipLaunchKernelGGL(fp64_pipe_probe_kernel<3>, grid, block, 0, s, out, iterations, 0.999, 0.001); break;
-  }
-  return check_launch("fp64_pipe_probe_kernel");
 }
 
 }  // extern "C"

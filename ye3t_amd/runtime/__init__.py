@@ -25,6 +25,9 @@ REFERENCE_OPERATIONS = (
     "symmetric_power_monomial_adjoint",
     "symmetric_power_shared_monomial",
     "symmetric_power_shared_monomial_adjoint",
+    "symmetric_power_shared_sparse_monomial",
+    "symmetric_power_shared_sparse_monomial_adjoint",
+    "symmetric_power_shared_sparse_monomial_double_backward",
     "factorized_angular",
     "factorized_angular_adjoint",
     "factorized_angular_linear",
@@ -285,7 +288,20 @@ def _monomial_functions():
             return (native.symmetric_power_shared_monomial_adjoint(g.contiguous(), x, *ctx.table),
                     None, None, None, None, None)
 
-    return _Grouped, _Shared
+    class _Sparse(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x, *tables):
+            ctx.save_for_backward(x)
+            ctx.table = tables
+            return native.symmetric_power_shared_sparse_monomial(x, *tables)
+
+        @staticmethod
+        def backward(ctx, g):
+            (x,) = ctx.saved_tensors
+            return (native.symmetric_power_shared_sparse_monomial_adjoint(g.contiguous(), x, *ctx.table),) + \
+                (None,) * len(ctx.table)
+
+    return _Grouped, _Shared, _Sparse
 
 
 _MONOMIAL_FNS = None
@@ -333,50 +349,157 @@ def symmetric_power_shared_monomial_contraction(input, monomial_counts, output_o
     return out.reshape(tuple(input.shape[:-1]) + (int(out.shape[-1]),))
 
 
+def symmetric_power_shared_sparse_monomial_contraction(input, term_offsets, term_components, term_exponents,
+                                                       output_offsets, coefficient_terms, coefficient_outputs,
+                                                       coefficient_values, *, backend="auto"):
+    """Shared-monomial contraction with sparse monomial supports: monomial t is
+    ``prod_{q in [term_offsets[t], term_offsets[t+1])} input[..., term_components[q]]^term_exponents[q]``
+    and outputs are sparse combinations of monomials (the reference's
+    ``ye3t_runtime::symmetric_power_shared_sparse_monomial``,
+    ``execution_plan_cuda.cu:5720-5755, 11012-11104``).  Differentiable; the
+    backward is the sparse adjoint (``:5757-5813``)."""
+    _backend(backend, {"auto", "native"})
+    flat = _feature_rows(input, "symmetric_power_shared_sparse_monomial_contraction")
+    out = _monomials()[2].apply(flat, term_offsets, term_components, term_exponents, output_offsets,
+                                coefficient_terms, coefficient_outputs, coefficient_values)
+    return out.reshape(tuple(input.shape[:-1]) + (int(out.shape[-1]),))
+
+
+# Thresholds and constants of the reference report (execution_plan.py:27-35,
+# 6536-6640) that keep their values here.  The symmetric-power CPU thresholds
+# steer the reference's CPU dispatch (symmetric_power.py:1131-1150), which
+# reads them whenever ``prebuilt_extension`` is true; CPU tensors are served by
+# the reference's own CPU runtime, so they are carried unchanged.
+_SYMMETRIC_POWER_CPU_AUTO_MAX_BATCH = 32
+_SYMMETRIC_POWER_CPU_AUTO_MIN_POWER = 6
+_SYMMETRIC_POWER_SHARED_CPU_MIN_REUSE = 3.0
+_SYMMETRIC_POWER_SHARED_CPU_MIN_BATCH = 8
+_SYMMETRIC_POWER_SHARED_GPU_MIN_REUSE = 8.0
+_SYMMETRIC_POWER_SHARED_GPU_GRAD_MIN_BATCH = 256
+_SYMMETRIC_POWER_SHARED_GPU_FORWARD_MIN_BATCH = 1024
+_COMPACT_EXTERIOR_POWER_MAX_NATIVE_ORDER = 8
+_REAL_TESSERAL_CONVENTION = "real_tesseral_from_complex_condon_shortley_young_orthogonal_v1"
+_TRITON_OPERATIONS = ("dense_source_analysis_C_dagger_L_v", "dense_source_analysis_channel_mixing",
+                      "packed_joint_young_angular_bilinear", "packed_joint_young_angular_channel_mixing")
+
+
+def _cpu_kernels_registered():
+    """True when the ``ye3t_runtime`` operators have CPU kernels in this process
+    (the reference's extension loaded beside this library)."""
+    try:
+        import torch
+
+        return bool(torch._C._dispatch_has_kernel_for_dispatch_key("ye3t_runtime::density_accumulate", "CPU"))
+    except Exception:
+        return False
+
+
 def native_execution_plan_capabilities():
     """Capability report (reference ``execution_plan.py:6118-6850``) with the HIP capability.
 
-    Keys the reference's consumers test keep their meaning: ``cuda`` and
-    ``cuda_operations`` are False / empty (this library has no CUDA branch),
-    ``operations`` lists what runs natively under the reference's names, and
-    ``hip`` / ``hip_operations`` carry the new capability (``has_hip()`` of
-    the library, the counterpart of the reference's ``has_cuda()``).
+    Every key of the reference report is present with the reference's
+    meaning, read for this library:
+
+    * ``cuda`` / ``cuda_operations``: native kernels for tensors whose device
+      type is ``"cuda"``, which on PyTorch-ROCm is the HIP device.  The
+      reference's consumers pick the native GPU path by testing an operation's
+      name in ``cuda_operations`` (``symmetric_power.py:1131-1137``), so it
+      lists the ``ye3t_runtime`` operator names this library gives a device
+      kernel (:mod:`ye3t_amd.runtime.torch_ops`).  ``hip`` / ``hip_operations``
+      say the same under the new capability's own name; ``hip_device`` adds
+      the device (arch, CU count, LDS, HBM peak).
+    * Capability flags of operator families this library does not build
+      (carrier scatters, role densities, source arenas, double backward of
+      the dense monomials and of the factorized-angular operators) are False,
+      and the thresholds that only those families read are None, as the
+      reference reports them when it lacks them.
+    * ``cpu``: CPU kernels of the ``ye3t_runtime`` operators are registered in
+      this process (the reference's own CPU runtime); this library has none.
+    * ``cmake_core_target``: the name of the native library that holds the
+      Torch-independent core (``libye3t_hip.so``, built by
+      ``ye3t_amd._build``; there is no CMake project).
     """
     import torch
 
     available = native.available()
     has_hip = bool(available and torch.version.hip is not None and torch.cuda.is_available()
                    and native.has_hip())
+    abi = native.ABI_VERSION if available else None
     ops = HIP_OPERATIONS if available else ()
+    cuda_ops = ()
+    if has_hip:
+        from ye3t_amd.runtime import torch_ops
+
+        cuda_ops = tuple(torch_ops.KERNELS)
+    sparse = bool(has_hip and {"symmetric_power_shared_sparse_monomial",
+                               "symmetric_power_shared_sparse_monomial_adjoint",
+                               "symmetric_power_shared_sparse_monomial_double_backward"} <= set(cuda_ops))
+    cpu = _cpu_kernels_registered()
     report = {
         "schema": "ye3t_execution_plan_v1",
         "torch_independent_core_source": True,
+        "cmake_core_target": "ye3t_hip",
         "prebuilt_extension": available,
-        "cpu": False,
-        "cuda": False,
-        "cuda_operations": (),
-        "hip": has_hip,
-        "hip_operations": ops if has_hip else (),
-        "hip_arch": "gfx950",
-        "cuda_density_auto_min_work_items": None,
-        "hip_density_reduction": "csr_segment_deterministic",
+        "cpu": cpu,
+        "cuda": has_hip,
+        "cuda_operations": cuda_ops,
+        # the HIP density reduction is a deterministic CSR segment sum at any size
+        "cuda_density_auto_min_work_items": 0 if has_hip else None,
+        "cuda_edge_outer_auto_min_work_items": None,
+        "cpu_edge_outer_auto_min_work_items": None,
+        "cpu_carrier_gated_scatter_auto_min_work_items": None,
+        "cuda_carrier_gated_scatter_auto_min_work_items": None,
+        "real_control_carrier_gates": False,
+        "residual_carrier_gated_scatter": False,
+        "segmented_carrier_gated_scatter": False,
         "segmented_factorized_angular": bool(available),
-        "heterogeneous_factorized_roots": bool(available),
+        "source_arena_gather": False,
+        "source_arena_channel_transform": False,
+        "carrier_channel_transform": False,
+        "carrier_role_channel_map_adjoint": False,
+        "cuda_segmented_carrier_scatter_min_node_feature_work": None,
+        "real_control_carrier_channel_update": False,
+        "scheduled_softmax_gaussian_role_density": False,
+        "symmetric_power_monomial_double_backward": False,
+        "symmetric_power_shared_monomial_double_backward": False,
+        "symmetric_power_shared_monomial_factored_double_backward": False,
+        "symmetric_power_shared_double_backward_default_algorithm": "auto",
+        "symmetric_power_shared_sparse_monomial": sparse,
+        "cpu_carrier_channel_update_auto_max_work_items": None,
+        "cuda_carrier_channel_update_auto_max_work_items": None,
+        "cuda_carrier_channel_update_auto_min_work_items": None,
+        "symmetric_power_cpu_auto_max_batch": _SYMMETRIC_POWER_CPU_AUTO_MAX_BATCH if available else None,
+        "symmetric_power_cpu_auto_min_power": _SYMMETRIC_POWER_CPU_AUTO_MIN_POWER if available else None,
+        "symmetric_power_shared_cpu_min_reuse": _SYMMETRIC_POWER_SHARED_CPU_MIN_REUSE if available else None,
+        "symmetric_power_shared_cpu_min_batch": _SYMMETRIC_POWER_SHARED_CPU_MIN_BATCH if available else None,
+        "symmetric_power_shared_cuda_min_reuse": _SYMMETRIC_POWER_SHARED_GPU_MIN_REUSE if has_hip else None,
+        "symmetric_power_shared_cuda_grad_min_batch": _SYMMETRIC_POWER_SHARED_GPU_GRAD_MIN_BATCH if has_hip else None,
+        "symmetric_power_shared_cuda_forward_min_batch": (_SYMMETRIC_POWER_SHARED_GPU_FORWARD_MIN_BATCH
+                                                          if has_hip else None),
         "triton_available": False,
         "triton_cuda_available": False,
-        "triton_operations": (),
-        "core_abi_version": native.ABI_VERSION if available else None,
-        "minimum_core_abi_version": _NATIVE_EXECUTION_PLAN_ABI,
+        "triton_real_convention_id": _REAL_TESSERAL_CONVENTION,
+        "triton_operations": _TRITON_OPERATIONS,
+        "core_abi_version": abi,
         "factorized_workspace_metadata": "compiler_host_scalar_no_device_read",
+        "heterogeneous_factorized_roots": bool(available),
+        # needs the heterogeneous reverse-with-workspace and its double backward
+        "cached_heterogeneous_factorized_reverse": False,
         "dtypes": ("float32", "float64", "complex64", "complex128"),
         "analysis_orientation": "conjugate_transpose",
         "operations": ops,
+        "compact_exterior_power_max_native_order": _COMPACT_EXTERIOR_POWER_MAX_NATIVE_ORDER,
+        # this backend's own keys
+        "hip": has_hip,
+        "hip_operations": ops if has_hip else (),
+        "hip_arch": "gfx950",
+        "hip_density_reduction": "csr_segment_deterministic",
+        "minimum_core_abi_version": _NATIVE_EXECUTION_PLAN_ABI,
         "density_reduction": "csr_segment_deterministic",
         "library_path": native.library_path(),
     }
     if has_hip:
-        caps = native.device_caps(torch.cuda.current_device())
-        report["hip_device"] = caps
+        report["hip_device"] = native.device_caps(torch.cuda.current_device())
     return report
 
 

@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 58
+ABI_VERSION = 59
 _LIB = None
 
 F32, F64 = 0, 1
@@ -106,7 +106,6 @@ def lib():
     L.ye3t_hip_density_accumulate_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _i64, _vp, _vp]
     L.ye3t_hip_ace_density_forward.argtypes = [ctypes.POINTER(DensityArgs), _vp, _vp]
     L.ye3t_hip_ace_density_edge_gradient.argtypes = [ctypes.POINTER(DensityArgs), ctypes.c_int, _vp, _vp, _vp]
-    L.ye3t_hip_fp64_pipe_probe.argtypes = [ctypes.c_int, _i64, ctypes.c_int, _vp, _vp]
     L.ye3t_hip_symmetric_power_monomial.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
                                                     _vp, _vp]
     L.ye3t_hip_symmetric_power_monomial_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64,
@@ -115,6 +114,13 @@ def lib():
                                                            _i64, _i64, _vp, _vp]
     L.ye3t_hip_symmetric_power_shared_monomial_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _i64, _vp,
                                                                    _vp, _vp, _i64, _i64, _vp, _vp]
+    L.ye3t_hip_symmetric_power_shared_sparse_monomial.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, _vp, _i64,
+                                                                  _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp]
+    L.ye3t_hip_symmetric_power_shared_sparse_monomial_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp,
+                                                                          _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64,
+                                                                          _i64, _vp, _vp]
+    L.ye3t_hip_symmetric_power_shared_sparse_monomial_double_backward.argtypes = [
+        ctypes.c_int, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp]
     L.ye3t_hip_evaluate_factorized_schedule.argtypes = [ctypes.c_int, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp,
                                                         _vp, _i64, _vp, _vp]
     L.ye3t_hip_product_plan_create.argtypes = [ctypes.POINTER(ProductPlanDesc), ctypes.POINTER(_vp)]
@@ -192,7 +198,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_product_plan_create", "ye3t_hip_product_plan_destroy", "ye3t_hip_product_forward",
     "ye3t_hip_product_launch_info", "ye3t_hip_rtc_compile", "ye3t_hip_free",
     "ye3t_hip_product_plan_attach_generated", "ye3t_hip_product_plan_select", "ye3t_hip_last_density_kernel",
-    "ye3t_hip_fp64_pipe_probe", "ye3t_hip_product_plan_attach_generated_parts",
+    "ye3t_hip_product_plan_attach_generated_parts",
     "ye3t_hip_product_plan_attach_adjoint_parts", "ye3t_hip_product_adjoint_parts_workspace_bytes",
     "ye3t_hip_product_adjoint_parts", "ye3t_hip_product_plan_attach_readout_parts",
     "ye3t_hip_product_linear_parts_workspace_bytes", "ye3t_hip_product_linear_forward_parts",
@@ -209,7 +215,9 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_symmetric_power_shared_monomial_adjoint", "ye3t_hip_factorized_angular_segmented_plan_create",
     "ye3t_hip_factorized_angular_segmented_plan_destroy", "ye3t_hip_factorized_angular_segmented_plan_info",
     "ye3t_hip_factorized_angular_segmented_forward", "ye3t_hip_factorized_angular_segmented_adjoint",
-    "ye3t_hip_ace_density_edge_gradient",
+    "ye3t_hip_ace_density_edge_gradient", "ye3t_hip_symmetric_power_shared_sparse_monomial",
+    "ye3t_hip_symmetric_power_shared_sparse_monomial_adjoint",
+    "ye3t_hip_symmetric_power_shared_sparse_monomial_double_backward",
 )
 
 
@@ -447,19 +455,6 @@ def last_density_kernel():
     return lib().ye3t_hip_last_density_kernel().decode()
 
 
-def fp64_pipe_probe(mode, workgroups, iterations, out):
-    """Launch the fp64 pipe probe (diagnostic, no reference counterpart) on
-    torch's current stream: mode 0 MFMAs, 1 FMAs, 2 both per wave, 3 split
-    between odd and even workgroups; ``out`` is a float64 device tensor of at
-    least ``workgroups * 64`` elements."""
-    import torch
-
-    if out.dtype != torch.float64 or out.numel() < workgroups * 64:
-        raise ValueError("out must be float64 with workgroups * 64 elements")
-    _check(lib().ye3t_hip_fp64_pipe_probe(int(mode), int(workgroups), int(iterations), _dev(out, "out"), _stream()),
-           "ye3t_hip_fp64_pipe_probe")
-
-
 def _host_i64(a):
     return np.ascontiguousarray(np.asarray(a.detach().cpu() if hasattr(a, "detach") else a), dtype=np.int64)
 
@@ -608,6 +603,116 @@ def symmetric_power_shared_monomial_adjoint(output_adjoint, x, monomial_counts, 
         _dev(do, "offsets"), _dev(dt, "terms") if C else None, _dev(dv, "values") if C else None, C, O,
         _dev(out, "input_adjoint"), _stream()), "ye3t_hip_symmetric_power_shared_monomial_adjoint")
     return out
+
+
+def check_sparse_table(D, term_offsets, term_components, term_exponents, output_offsets, coefficient_terms,
+                       coefficient_outputs, coefficient_values):
+    """Host checks of a sparse shared monomial table: the reference's host checks
+    (execution_plan_cuda.cu:11012-11060) plus every index its kernels assert
+    (:5723-5755, 5962-6030); returns the int64 host arrays."""
+    toff = _host_i64(term_offsets).reshape(-1)
+    comp = _host_i64(term_components).reshape(-1)
+    ex = _host_i64(term_exponents).reshape(-1)
+    offs = _host_i64(output_offsets).reshape(-1)
+    terms = _host_i64(coefficient_terms).reshape(-1)
+    outs = _host_i64(coefficient_outputs).reshape(-1)
+    C = int(np.asarray(_host_real(coefficient_values)).reshape(-1).shape[0])
+    if toff.size < 1:
+        raise ValueError("term_offsets must contain at least one entry")
+    if comp.size != ex.size:
+        raise ValueError("sparse support component and exponent arrays must have equal length")
+    if outs.size != terms.size or C != terms.size:
+        raise ValueError("shared symmetric-power coefficient arrays must have equal length")
+    if offs.size < 1:
+        raise ValueError("output_offsets must contain at least one entry")
+    M, S, O = int(toff.size) - 1, int(comp.size), int(offs.size) - 1
+    if toff[0] != 0 or toff[-1] != S or np.any(np.diff(toff) < 0):
+        raise ValueError("term_offsets must span the support arrays")
+    if S and (comp.min() < 0 or comp.max() >= int(D)):
+        raise ValueError("term_components contains an invalid input component")
+    if S and ex.min() <= 0:
+        raise ValueError("term_exponents must be positive")
+    if offs[0] != 0 or offs[-1] != C or np.any(np.diff(offs) < 0):
+        raise ValueError("output_offsets must span the coefficient table")
+    if C and (terms.min() < 0 or terms.max() >= M):
+        raise ValueError("coefficient_terms contains an invalid monomial")
+    if C and np.any(np.repeat(np.arange(O), np.diff(offs)) != outs):
+        raise ValueError("coefficient_outputs must agree with output_offsets")
+    return toff, comp, ex, offs, terms
+
+
+def _sparse_call(fn_name, x, tables, *tensors_before, outputs):
+    toff, comp, ex, offs, terms, values = tables
+    M, S, C, O = int(toff.size - 1), int(comp.size), int(terms.size), int(offs.size - 1)
+    import torch
+
+    dv = torch.as_tensor(_host_real(values), device=x.device).to(x.dtype).contiguous()
+    dt, dc, de = _dev_i64(toff, x.device), _dev_i64(comp, x.device), _dev_i64(ex, x.device)
+    do, dk = _dev_i64(offs, x.device), _dev_i64(terms, x.device)
+    B, D = (int(s) for s in x.shape)
+    args = [_dtype_code(x), *[_dev(t, "tensor") for t in tensors_before], _dev(x, "input"), B, D,
+            _dev(dt, "term_offsets"), _dev(dc, "term_components") if S else None,
+            _dev(de, "term_exponents") if S else None, M, S, _dev(do, "output_offsets"),
+            _dev(dk, "coefficient_terms") if C else None, _dev(dv, "coefficient_values") if C else None, C, O,
+            *[_dev(t, "output") if t.numel() else None for t in outputs], _stream()]
+    _check(getattr(lib(), fn_name)(*args), fn_name)
+
+
+def _sparse_tables(D, term_offsets, term_components, term_exponents, output_offsets, coefficient_terms,
+                   coefficient_outputs, coefficient_values):
+    toff, comp, ex, offs, terms = check_sparse_table(D, term_offsets, term_components, term_exponents,
+                                                     output_offsets, coefficient_terms, coefficient_outputs,
+                                                     coefficient_values)
+    return toff, comp, ex, offs, terms, coefficient_values
+
+
+def symmetric_power_shared_sparse_monomial(x, term_offsets, term_components, term_exponents, output_offsets,
+                                           coefficient_terms, coefficient_outputs, coefficient_values):
+    import torch
+
+    B, D = (int(s) for s in x.shape)
+    tables = _sparse_tables(D, term_offsets, term_components, term_exponents, output_offsets, coefficient_terms,
+                            coefficient_outputs, coefficient_values)
+    out = torch.empty((B, int(tables[3].size - 1)), dtype=x.dtype, device=x.device)
+    _sparse_call("ye3t_hip_symmetric_power_shared_sparse_monomial", x, tables, outputs=(out,))
+    return out
+
+
+def symmetric_power_shared_sparse_monomial_adjoint(output_adjoint, x, term_offsets, term_components, term_exponents,
+                                                   output_offsets, coefficient_terms, coefficient_outputs,
+                                                   coefficient_values):
+    import torch
+
+    B, D = (int(s) for s in x.shape)
+    tables = _sparse_tables(D, term_offsets, term_components, term_exponents, output_offsets, coefficient_terms,
+                            coefficient_outputs, coefficient_values)
+    g = output_adjoint.to(x.dtype).contiguous()
+    if tuple(g.shape) != (B, int(tables[3].size - 1)):
+        raise ValueError("output_adjoint dtype and batch must match input")
+    out = torch.empty_like(x)
+    _sparse_call("ye3t_hip_symmetric_power_shared_sparse_monomial_adjoint", x, tables, g, outputs=(out,))
+    return out
+
+
+def symmetric_power_shared_sparse_monomial_double_backward(input_adjoint_tangent, output_adjoint, x, term_offsets,
+                                                           term_components, term_exponents, output_offsets,
+                                                           coefficient_terms, coefficient_outputs,
+                                                           coefficient_values):
+    import torch
+
+    B, D = (int(s) for s in x.shape)
+    tables = _sparse_tables(D, term_offsets, term_components, term_exponents, output_offsets, coefficient_terms,
+                            coefficient_outputs, coefficient_values)
+    v = input_adjoint_tangent.to(x.dtype).contiguous()
+    g = output_adjoint.to(x.dtype).contiguous()
+    if tuple(v.shape) != (B, D):
+        raise ValueError("input_adjoint_tangent shape must match input")
+    if tuple(g.shape) != (B, int(tables[3].size - 1)):
+        raise ValueError("output_adjoint batch dimension must match input")
+    out_t, in_t = torch.empty_like(g), torch.empty_like(x)
+    _sparse_call("ye3t_hip_symmetric_power_shared_sparse_monomial_double_backward", x, tables, v, g,
+                 outputs=(out_t, in_t))
+    return out_t, in_t
 
 
 def evaluate_factorized_schedule(block_values, schedule):

@@ -16,10 +16,12 @@ device, so a call with device tensors runs this library's kernels.
   the reference's adjoint operator).
 * Operators covered: the radial and real-harmonic tables, density
   accumulation and its adjoint, the symmetric-power monomial and
-  shared-monomial contractions and adjoints, and the factorized-angular
+  shared-monomial contractions and adjoints, the sparse shared-monomial
+  contraction with its adjoint and double backward, and the factorized-angular
   forward / adjoint / linear readout / heterogeneous / segmented operators.
-  Double-backward operators are not provided: differentiating an adjoint
-  operator raises Torch's "no autograd" error.
+  The sparse shared-monomial adjoint is differentiable through its double
+  backward, as in the reference; the other adjoint operators are not
+  (differentiating one raises Torch's "no autograd" error).
 * CPU tensors are not served: the reference's CPU kernels serve them (a call
   with CPU tensors and no reference extension raises Torch's dispatch error).
 """
@@ -57,6 +59,19 @@ SCHEMAS = {
     "symmetric_power_shared_monomial_adjoint":
         "(Tensor output_adjoint, Tensor input, Tensor monomial_counts, Tensor output_offsets, "
         "Tensor coefficient_terms, Tensor coefficient_outputs, Tensor coefficient_values) -> Tensor",
+    # :7563, :7569, :7575
+    "symmetric_power_shared_sparse_monomial":
+        "(Tensor input, Tensor term_offsets, Tensor term_components, Tensor term_exponents, "
+        "Tensor output_offsets, Tensor coefficient_terms, Tensor coefficient_outputs, "
+        "Tensor coefficient_values) -> Tensor",
+    "symmetric_power_shared_sparse_monomial_adjoint":
+        "(Tensor output_adjoint, Tensor input, Tensor term_offsets, Tensor term_components, "
+        "Tensor term_exponents, Tensor output_offsets, Tensor coefficient_terms, "
+        "Tensor coefficient_outputs, Tensor coefficient_values) -> Tensor",
+    "symmetric_power_shared_sparse_monomial_double_backward":
+        "(Tensor input_adjoint_tangent, Tensor output_adjoint, Tensor input, Tensor term_offsets, "
+        "Tensor term_components, Tensor term_exponents, Tensor output_offsets, Tensor coefficient_terms, "
+        "Tensor coefficient_outputs, Tensor coefficient_values) -> (Tensor, Tensor)",
     # :7587, :7596
     "factorized_angular":
         "(Tensor packed_slots, Tensor node_offsets, Tensor node_dimensions, Tensor node_leaf_offsets, "
@@ -250,6 +265,22 @@ def _k_shared_adjoint(output_adjoint, input, monomial_counts, output_offsets, co
     return g.reshape(input.shape)
 
 
+def _k_sparse(input, *tables):
+    out = native.symmetric_power_shared_sparse_monomial(_rows(input), *tables)
+    return out.reshape(tuple(input.shape[:-1]) + (int(out.shape[-1]),))
+
+
+def _k_sparse_adjoint(output_adjoint, input, *tables):
+    g = native.symmetric_power_shared_sparse_monomial_adjoint(_rows(output_adjoint), _rows(input), *tables)
+    return g.reshape(input.shape)
+
+
+def _k_sparse_double_backward(input_adjoint_tangent, output_adjoint, input, *tables):
+    ot, it = native.symmetric_power_shared_sparse_monomial_double_backward(
+        _rows(input_adjoint_tangent), _rows(output_adjoint), _rows(input), *tables)
+    return ot.reshape(output_adjoint.shape), it.reshape(input.shape)
+
+
 def _k_fa(packed_slots, *rest):
     tables, (S, W, F) = _fa_tables(rest[:11]), rest[11:]
     return _fa_plan(packed_slots, tables, S, W, F).forward(packed_slots.contiguous())
@@ -305,6 +336,9 @@ KERNELS = {
     "symmetric_power_monomial_adjoint": _k_monomial_adjoint,
     "symmetric_power_shared_monomial": _k_shared,
     "symmetric_power_shared_monomial_adjoint": _k_shared_adjoint,
+    "symmetric_power_shared_sparse_monomial": _k_sparse,
+    "symmetric_power_shared_sparse_monomial_adjoint": _k_sparse_adjoint,
+    "symmetric_power_shared_sparse_monomial_double_backward": _k_sparse_double_backward,
     "factorized_angular": _k_fa,
     "factorized_angular_adjoint": _k_fa_adjoint,
     "factorized_angular_heterogeneous": _k_hetero,
@@ -349,6 +383,14 @@ def _f_like_input(output_adjoint, input, *rest):
     return input.new_empty(input.shape)
 
 
+def _f_sparse(input, term_offsets, term_components, term_exponents, output_offsets, *rest):
+    return input.new_empty(tuple(input.shape[:-1]) + (output_offsets.shape[0] - 1,))
+
+
+def _f_sparse_double_backward(input_adjoint_tangent, output_adjoint, input, *rest):
+    return output_adjoint.new_empty(output_adjoint.shape), input.new_empty(input.shape)
+
+
 def _f_fa(packed_slots, *rest):
     return packed_slots.new_empty((packed_slots.shape[0], int(rest[-1])))
 
@@ -375,6 +417,9 @@ FAKES = {
     "symmetric_power_monomial_adjoint": _f_like_input,
     "symmetric_power_shared_monomial": _f_monomial,
     "symmetric_power_shared_monomial_adjoint": _f_like_input,
+    "symmetric_power_shared_sparse_monomial": _f_sparse,
+    "symmetric_power_shared_sparse_monomial_adjoint": _f_like_input,
+    "symmetric_power_shared_sparse_monomial_double_backward": _f_sparse_double_backward,
     "factorized_angular": _f_fa,
     "factorized_angular_adjoint": _f_fa_adjoint,
     "factorized_angular_heterogeneous": _f_fa,
@@ -423,6 +468,20 @@ def _bw_shared(ctx, grad):
                                                            values),) + (None,) * 5
 
 
+def _bw_sparse(ctx, grad):
+    x, *tables = _inputs(ctx)
+    return (_ops().symmetric_power_shared_sparse_monomial_adjoint(grad.contiguous(), x, *tables),) + (None,) * 7
+
+
+def _bw_sparse_adjoint(ctx, grad):
+    """Backward of the adjoint operator: its double backward gives the
+    cotangents of the output adjoint and of the input (execution_plan.py:5289-5340)."""
+    g, x, *tables = _inputs(ctx)
+    ot, it = _ops().symmetric_power_shared_sparse_monomial_double_backward(grad.contiguous(), g.contiguous(),
+                                                                           x.contiguous(), *tables)
+    return (ot, it) + (None,) * 7
+
+
 def _bw_fa(ctx, grad):
     packed, *rest = _inputs(ctx)
     gx = _ops().factorized_angular_adjoint(grad.contiguous(), packed, *rest[:11], rest[11], rest[12])
@@ -454,6 +513,8 @@ BACKWARDS = {
     "density_accumulate_adjoint": _bw_density_adjoint,
     "symmetric_power_monomial": _bw_monomial,
     "symmetric_power_shared_monomial": _bw_shared,
+    "symmetric_power_shared_sparse_monomial": _bw_sparse,
+    "symmetric_power_shared_sparse_monomial_adjoint": _bw_sparse_adjoint,
     "factorized_angular": _bw_fa,
     "factorized_angular_heterogeneous": _bw_hetero,
     "factorized_angular_segmented": _bw_seg,
