@@ -188,6 +188,12 @@ def _time_kernel(fn, steps, warmup, min_warmup_s=MIN_WARMUP_S):
     return (time.perf_counter() - t0) / steps
 
 
+class _NoPlan:
+    """Stand-in plan for the stage-1 byte count (stage 2's share is unused)."""
+    a_width = 0
+    feature_count = 0
+
+
 def bench_op(args, cfg):
     """One widened op on the configuration's shapes (see ``--op``)."""
     import numpy as np
@@ -314,6 +320,40 @@ def bench_op(args, cfg):
             "note": "us_per_call: the whole build through the Python binding, including its host "
                     "synchronisation on the edge count and the output allocations"})
         line["config"].update({"atoms": N, "edges": E, "cutoff": cutoff, "box_edge": box})
+    elif args.op == "density":
+        # stage 1 alone: the fused density of the whole configuration
+        inp = cfg.density.generate()
+        dev = to_device_inputs(inp, dtype, "cuda")
+        N = d.atom_count
+        adt = torch.float64 if density == "f64" else torch.float32
+        A = torch.empty((N, d.channel_count, d.radial_rows, (d.l_max + 1) ** 2), dtype=adt, device="cuda")
+        acc_t = torch.float64 if accumulate == "f64" else torch.float32
+
+        def call(validate):  # the pipeline's stage 1 (ACEPipeline.density) without building a product plan
+            return native.ace_density_forward(
+                dev["edge_vectors"], dev["row_offsets"], dev["neighbors"], atom_count=N,
+                channel_count=d.channel_count, n_max=d.n_max, l_max=d.l_max, cutoff=inp["cutoff"],
+                lam=inp["lambda"], epsilon=inp["epsilon"], species=dev.get("species"),
+                node_features=dev.get("node_features"), radial_mix=dev.get("radial_mix"), out=A, out_dtype=adt,
+                accumulate_dtype=acc_t, validate=validate)
+
+        call(True)  # validates the CSR and neighbour indices once
+        kernel = native.last_density_kernel()
+        t = _time_kernel(lambda: call(False), args.steps, args.warmup)
+        elem = 8 if dtype == "f64" else 4
+        b1, _ = algorithmic_bytes(cfg, _NoPlan(), elem)
+        a_elem = A.element_size()
+        a_bytes = A.numel() * a_elem
+        line.update({
+            "metric": "density GB/s", "value": b1 / t / 1e9, "unit": "GB/s", "higher_is_better": True,
+            "us_per_call": t * 1e6, "atoms_per_s": N / t, "dtype": "f64", "storage_dtype": dtype,
+            "density_dtype": density, "kernel": kernel,
+            "roofline": {"bound": "hbm", "achieved": b1 / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": b1 / t / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": b1,
+                         "density_bytes": a_bytes, "density_write_frac": a_bytes / t / 1e9 / HBM_PEAK_GBS},
+            "note": "algorithmic bytes per the survey's stage-1 formula at the storage element size; "
+                    "timed through the Python binding without its CSR validation (validated once)"})
+        line["config"].update({"atoms": N, "edges": int(inp["edge_count"])})
     elif args.op == "density_edge_gradient":
         inp = cfg.density.generate()
         dev = to_device_inputs(inp, dtype, "cuda")
@@ -381,8 +421,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--kernel", default="auto", choices=["auto", "generated", "parts", "interpreter"])
     ap.add_argument("--op", default="pipeline",
-                    choices=["pipeline", "linear_readout", "density_accumulate_adjoint", "product_adjoint",
-                             "neighbor_list", "density_edge_gradient"],
+                    choices=["pipeline", "density", "linear_readout", "density_accumulate_adjoint",
+                             "product_adjoint", "neighbor_list", "density_edge_gradient"],
                     help="pipeline: the headline step (stage 1 + stage 2); the others time one widened op "
                          "on the config's shapes and print its own JSON line")
     ap.add_argument("--copy-probe", action="store_true",

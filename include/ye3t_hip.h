@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 59 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 60 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -301,6 +301,19 @@ int ye3t_hip_product_forward(const ye3t_hip_product_plan* plan, const void* A, i
  * (the reference JIT-compiles its whole extension, execution_plan.py:253-292). */
 int ye3t_hip_rtc_compile(const char* source, const char* name, const char* arch, void** code, int64_t* size);
 void ye3t_hip_free(void* ptr);
+
+/* Facts of kernel `kernel_name` read from a gfx950 code object on the host
+ * (its AMDHSA kernel descriptor): private (scratch) segment bytes per lane, LDS
+ * bytes, and whether it uses a dynamic stack.  No GPU needed.  The
+ * attach_*_parts entry points refuse a part whose private segment exceeds
+ * ye3t_hip_part_private_limit() bytes per lane (1024; YE3T_PART_PRIVATE_MAX may
+ * lower it), whose scratch over four part streams and every wave slot of the
+ * device would exceed 2 GiB, or that uses a dynamic stack.  No reference
+ * counterpart (the reference has no generated kernels). */
+int ye3t_hip_code_object_kernel_info(const void* code, int64_t size, const char* kernel_name,
+                                     int64_t* private_segment_bytes, int64_t* group_segment_bytes,
+                                     int* uses_dynamic_stack);
+int64_t ye3t_hip_part_private_limit(void);
 
 /* Attach a plan-specialised kernel (code object from ye3t_hip_rtc_compile of
  * ye3t_amd/ace/codegen.py output) to `plan`; product_forward then launches it

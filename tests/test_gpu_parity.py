@@ -704,16 +704,92 @@ def test_fp32_density_accumulated_in_fp64(gpu, mode, shape):
 
 
 def test_fp32_density_accumulated_in_fp64_needs_an_mfma_shape(gpu):
-    """Species densities have no fp64 matrix-core kernel: the mixed precision is refused."""
+    """A shape no fp64 matrix-core kernel covers (more than 16 species): the
+    mixed precision is refused."""
     import torch
 
     inp = _ragged_workload("species")
+    rng = np.random.default_rng(5)
+    inp.update(channel_count=20, species=rng.integers(0, 20, inp["atom_count"]).astype(np.int32))
     dev = to_device_inputs(inp, "f32", gpu)
     with pytest.raises(RuntimeError, match="fp64 matrix-core shapes"):
         native.ace_density_forward(
             dev["edge_vectors"], dev["row_offsets"], dev["neighbors"], atom_count=inp["atom_count"],
             channel_count=inp["channel_count"], n_max=inp["n_max"], l_max=inp["l_max"], cutoff=inp["cutoff"],
             lam=inp["lambda"], species=dev["species"], out_dtype=torch.float32, accumulate_dtype=torch.float64)
+
+
+def _species_workload(atoms, species, n_max, l_max, seed, max_degree=150):
+    """Ragged rows for the species kernel: random degrees in [0, max_degree]
+    (rows of more than 64 edges take several windows), a run of 40 empty atoms
+    (more than one chunk's worth of them), single-edge rows, and edges beyond
+    the cutoff."""
+    rng = np.random.default_rng(seed)
+    counts = rng.integers(0, max_degree + 1, atoms)
+    counts[:3] = 0
+    counts[10:50] = 0
+    counts[50:60] = 1
+    counts[-1] = 0
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    E = int(offsets[-1])
+    vec = rng.normal(size=(E, 3))
+    vec = vec / np.linalg.norm(vec, axis=1, keepdims=True) * rng.uniform(0.8, 5.2, (E, 1))
+    return {"atom_count": atoms, "edge_count": E, "centers": np.repeat(np.arange(atoms), counts),
+            "row_offsets": offsets, "neighbors": rng.integers(0, atoms, E), "edge_vectors": vec, "n_max": n_max,
+            "l_max": l_max, "cutoff": 5.0, "lambda": W.LAMBDA, "epsilon": 1e-12, "channel_count": species,
+            "species": rng.integers(0, species, atoms).astype(np.int32), "node_features": None, "radial_mix": None}
+
+
+@pytest.mark.parametrize("waves", [None, "1", "7"])
+@pytest.mark.parametrize("species,shape,max_degree", [(4, (10, 4), 150), (8, (12, 6), 150), (16, (15, 8), 90),
+                                                      (3, (0, 0), 70), (5, (3, 1), 20), (8, (12, 6), 48)])
+@pytest.mark.parametrize("storage", ["f32", "f64"])
+def test_species_density_on_the_matrix_cores(gpu, monkeypatch, species, shape, max_degree, storage, waves):
+    """The species kernel (edges grouped by (atom, species), one fp64 MFMA
+    product per group) against the oracle and the VALU kernel, on ragged rows
+    (empty runs, windows of long rows), every CT instantiation from l_max 0 to
+    8, and with the fp32 density accumulated in fp64 equal to the fp64 density
+    rounded once."""
+    flush(f"species density S={species} n_max,l_max={shape} deg<={max_degree} {storage} waves={waves}")
+    import torch
+
+    if waves is not None:
+        monkeypatch.setenv("YE3T_DENSITY_WAVES", waves)
+    inp = _species_workload(301, species, shape[0], shape[1], 40 + species, max_degree)
+    dev = to_device_inputs(inp, storage, gpu)
+    N = inp["atom_count"]
+    kw = dict(atom_count=N, channel_count=species, n_max=shape[0], l_max=shape[1], cutoff=5.0, lam=inp["lambda"],
+              epsilon=inp["epsilon"], species=dev["species"])
+    ref = oracle.ace_density(rounded_inputs(inp, storage)).reshape(N, -1)
+    A = native.ace_density_forward(dev["edge_vectors"], dev["row_offsets"], dev["neighbors"],
+                                   out_dtype=torch.float64, **kw)
+    assert native.last_density_kernel() == "ace_density_species_kernel"
+    got = A.cpu().numpy().reshape(N, -1)
+    err = column_rel_error(got, ref)
+    monkeypatch.setenv("YE3T_DENSITY_SPECIES_MFMA", "0")
+    V = native.ace_density_forward(dev["edge_vectors"], dev["row_offsets"], dev["neighbors"],
+                                   out_dtype=torch.float64, **kw)
+    assert native.last_density_kernel() == "ace_density_kernel"
+    monkeypatch.delenv("YE3T_DENSITY_SPECIES_MFMA")
+    err_valu = column_rel_error(got, V.cpu().numpy().reshape(N, -1))
+    flush(f"  err {err:.3e} (vs VALU kernel {err_valu:.3e})")
+    assert err < TOL["f64"] and err_valu < TOL["f64"]
+    empty = np.diff(inp["row_offsets"]) == 0
+    assert not np.any(got[empty])
+    # a species absent from an atom's neighbours leaves an exact zero block
+    blocks = got.reshape(N, species, -1)
+    sp_of = inp["species"][inp["neighbors"]]
+    for i in (60, 100, 200):
+        present = set(sp_of[inp["row_offsets"][i]:inp["row_offsets"][i + 1]].tolist())
+        for s in range(species):
+            if s not in present:
+                assert not np.any(blocks[i, s])
+    if storage == "f32":
+        A32 = native.ace_density_forward(dev["edge_vectors"], dev["row_offsets"], dev["neighbors"],
+                                         out_dtype=torch.float32, accumulate_dtype=torch.float64, **kw)
+        assert torch.equal(A32, A.to(torch.float32))
+        A32b = native.ace_density_forward(dev["edge_vectors"], dev["row_offsets"], dev["neighbors"], **kw)
+        assert A32b.dtype == torch.float32 and torch.equal(A32b, A32)
 
 
 def test_density_rejects_bad_indices_before_launch(gpu):

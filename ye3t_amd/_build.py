@@ -15,7 +15,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libye3t_hip.so")
-SOURCES = ("api.hip", "density.hip", "density_grad.hip", "density_mfma.hip", "density_mfma64.hip", "factorized.hip",
+SOURCES = ("api.hip", "density.hip", "density_grad.hip", "density_mfma.hip", "density_mfma64.hip", "density_species.hip", "factorized.hip",
            "monomial.hip",
            "neighbors.hip", "product.hip")
 ARCH = os.environ.get("YE3T_HIP_ARCH", "gfx950")

@@ -136,15 +136,28 @@ class ACEPipeline:
     def _parts_max_live(self):
         """Node values per chunk of the generated parts: ``YE3T_PARTS_MAX_LIVE``
         or ``codegen.part_max_live``.  Chunks above ``PART_MAX_LIVE`` (400) are
-        refused: config 5 in 550-value chunks (1.2 KB of scratch per lane) took
-        a memory aperture violation on the GPU whose cause is not established,
-        while 300 and 400 ran clean there."""
+        refused: config 5 in 550-value chunks (kernels with 1 260 and 2 052
+        bytes of scratch per lane) ended in a memory aperture violation on the
+        GPU, while 400-value chunks (772 bytes) ran clean.  The library's attach
+        entry points also refuse any part above 1 024 bytes of scratch per lane
+        (``native.part_private_limit``), whatever its chunk size."""
         from ye3t_amd.ace.codegen import PART_MAX_LIVE, part_max_live
 
         env = os.environ.get("YE3T_PARTS_MAX_LIVE")
         live = part_max_live(self.plan, self.accumulate) if env is None else int(env)
         if not 1 <= live <= PART_MAX_LIVE:
             raise ValueError(f"YE3T_PARTS_MAX_LIVE must be in [1, {PART_MAX_LIVE}], got {live}")
+        return live
+
+    @staticmethod
+    def _adjoint_parts_max_live():
+        """Node values per chunk of the reverse-mode parts:
+        ``YE3T_ADJOINT_PARTS_MAX_LIVE`` or 128, within the forward's bound."""
+        from ye3t_amd.ace.codegen import PART_MAX_LIVE
+
+        live = int(os.environ.get("YE3T_ADJOINT_PARTS_MAX_LIVE", ADJOINT_PART_MAX_LIVE))
+        if not 1 <= live <= PART_MAX_LIVE:
+            raise ValueError(f"YE3T_ADJOINT_PARTS_MAX_LIVE must be in [1, {PART_MAX_LIVE}], got {live}")
         return live
 
     @property
@@ -237,7 +250,7 @@ class ACEPipeline:
 
         if getattr(self.handle, "adjoint_part_meta", None) is None:
             # smaller chunks than the forward's: values and gradients are live together (tuning)
-            live = int(os.environ.get("YE3T_ADJOINT_PARTS_MAX_LIVE", ADJOINT_PART_MAX_LIVE))
+            live = self._adjoint_parts_max_live()
             per = int(os.environ.get("YE3T_ADJOINT_PARTS_CHUNKS", ADJOINT_PART_CHUNKS))
             parts, reduction = generate_adjoint_parts(self.plan, self.accumulate, max_live=live, chunks_per_part=per,
                                                       grad_dtype=self.dtype, in_dtype=self.density_dtype)

@@ -304,9 +304,18 @@ int launch_mode(const ye3t_density_args* a, void* A, hipStream_t s) {
 int launch_density_mfma(const ye3t_density_args* a, void* A, hipStream_t stream);
 template <typename In, typename Out>
 int launch_density_mfma64(const ye3t_density_args* a, void* A, hipStream_t stream);
+template <typename In, typename Out>
+int launch_density_species(const ye3t_density_args* a, void* A, hipStream_t stream);
 
 template <typename Real, typename In>
 int dispatch_density(const ye3t_density_args* a, void* A, hipStream_t s) {
+  // one-hot species: each (atom, species) group of edges on the fp64 matrix
+  // cores (YE3T_DENSITY_SPECIES_MFMA=0 selects the VALU kernel)
+  if (a->species && env_int("YE3T_DENSITY_SPECIES_MFMA", 1) != 0) {
+    const int rc = launch_density_species<In, Real>(a, A, s);
+    if (rc != YE3T_EUNSUPPORTED) return rc;
+    clear_error();
+  }
   if (std::is_same<Real, float>::value) {
     // fp32 single-channel and node-feature densities run on the matrix cores
     const int rc = launch_density_mfma(a, A, s);
@@ -351,11 +360,13 @@ extern "C" int ye3t_hip_ace_density_forward(const ye3t_density_args* a, void* A,
     if (a->dtype == YE3T_F32 && out_dtype == YE3T_F64) return dispatch_density<double, float>(a, A, as_stream(stream));
   } else if (a->dtype == YE3T_F32 && out_dtype == YE3T_F32 && acc_dtype == YE3T_F64) {
     // fp64 accumulation rounded once to an fp32 density: the fp64 matrix-core kernels
-    const int rc = launch_density_mfma64<float, float>(a, A, as_stream(stream));
+    const int rc = a->species ? launch_density_species<float, float>(a, A, as_stream(stream))
+                              : launch_density_mfma64<float, float>(a, A, as_stream(stream));
     if (rc != YE3T_EUNSUPPORTED) return rc;
     return set_error(YE3T_EUNSUPPORTED,
                      "an fp32 density accumulated in fp64 is built for the fp64 matrix-core shapes only "
-                     "(node features at 16 channels, n_max 8, l_max 3; single channel at (3, 8), (4, 10), (6, 12))");
+                     "(node features at 16 channels, n_max 8, l_max 3; single channel at (3, 8), (4, 10), (6, 12); "
+                     "up to 16 species with n_max <= 15, l_max <= 8)");
   }
   return set_error(YE3T_EDTYPE, "unsupported dtype combination (inputs %d, density %d, accumulation %d)", a->dtype,
                    out_dtype, acc_dtype);

@@ -19,6 +19,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <string>
 #include <vector>
 
 #include "common.h"
@@ -1105,6 +1106,108 @@ int scratch_address(int dev, void** out) {
   return YE3T_OK;
 }
 
+// ---- scratch of generated parts -------------------------------------------
+// Kernel facts read from a gfx950 code object on the host: the AMDHSA kernel
+// descriptor is the 64-byte object "<kernel>.kd" of the ELF symbol table, with
+// the private (scratch) segment size per lane at byte 4 and the kernel code
+// properties at byte 56 (bit 11: the kernel uses a dynamic stack).
+
+template <typename T>
+static bool elf_read(const unsigned char* base, uint64_t size, uint64_t off, T* out) {
+  if (off > size || size - off < sizeof(T)) return false;
+  std::memcpy(out, base + off, sizeof(T));
+  return true;
+}
+
+static int kernel_descriptor_info(const void* code, int64_t size, const char* name, uint32_t* private_bytes,
+                           uint32_t* group_bytes, int* dynamic_stack) {
+  const auto* b = static_cast<const unsigned char*>(code);
+  const uint64_t n = uint64_t(size);
+  if (!code || size < 64 || !name) return set_error(YE3T_EINVAL, "NULL or short code object");
+  if (!(b[0] == 0x7f && b[1] == 'E' && b[2] == 'L' && b[3] == 'F' && b[4] == 2))
+    return set_error(YE3T_EINVAL, "not an ELF64 code object");
+  uint64_t shoff = 0;
+  uint16_t shentsize = 0, shnum = 0;
+  if (!elf_read(b, n, 0x28, &shoff) || !elf_read(b, n, 0x3A, &shentsize) || !elf_read(b, n, 0x3C, &shnum) ||
+      shentsize != 64)
+    return set_error(YE3T_EINVAL, "bad ELF section table");
+  const std::string want = std::string(name) + ".kd";
+  for (uint16_t si = 0; si < shnum; ++si) {
+    const uint64_t sh = shoff + uint64_t(si) * 64;
+    uint32_t type = 0, link = 0;
+    uint64_t off = 0, sz = 0, entsize = 0;
+    if (!elf_read(b, n, sh + 4, &type) || !elf_read(b, n, sh + 24, &off) || !elf_read(b, n, sh + 32, &sz) ||
+        !elf_read(b, n, sh + 40, &link) || !elf_read(b, n, sh + 56, &entsize))
+      return set_error(YE3T_EINVAL, "bad ELF section header");
+    if ((type != 2 && type != 11) || entsize != 24 || link >= shnum) continue;  // SHT_SYMTAB / SHT_DYNSYM
+    uint64_t str_off = 0, str_size = 0;
+    if (!elf_read(b, n, shoff + uint64_t(link) * 64 + 24, &str_off) ||
+        !elf_read(b, n, shoff + uint64_t(link) * 64 + 32, &str_size) || str_off > n || n - str_off < str_size)
+      return set_error(YE3T_EINVAL, "bad ELF string table");
+    for (uint64_t k = 0; k + 24 <= sz; k += 24) {
+      uint32_t st_name = 0;
+      uint16_t shndx = 0;
+      uint64_t value = 0;
+      if (!elf_read(b, n, off + k, &st_name) || !elf_read(b, n, off + k + 6, &shndx) ||
+          !elf_read(b, n, off + k + 8, &value))
+        return set_error(YE3T_EINVAL, "bad ELF symbol");
+      if (st_name >= str_size || str_size - st_name < want.size() + 1) continue;
+      if (std::memcmp(b + str_off + st_name, want.c_str(), want.size() + 1) != 0) continue;
+      if (shndx == 0 || shndx >= shnum) return set_error(YE3T_EINVAL, "kernel descriptor without a section");
+      uint64_t saddr = 0, soff = 0;
+      if (!elf_read(b, n, shoff + uint64_t(shndx) * 64 + 16, &saddr) ||
+          !elf_read(b, n, shoff + uint64_t(shndx) * 64 + 24, &soff) || value < saddr)
+        return set_error(YE3T_EINVAL, "bad kernel descriptor section");
+      const uint64_t kd = soff + (value - saddr);
+      uint32_t group = 0, priv = 0;
+      uint16_t props = 0;
+      if (!elf_read(b, n, kd, &group) || !elf_read(b, n, kd + 4, &priv) || !elf_read(b, n, kd + 56, &props))
+        return set_error(YE3T_EINVAL, "kernel descriptor out of the code object");
+      *private_bytes = priv;
+      *group_bytes = group;
+      *dynamic_stack = (props >> 11) & 1;
+      return YE3T_OK;
+    }
+  }
+  return set_error(YE3T_EINVAL, "kernel descriptor %s not found", want.c_str());
+}
+
+// Largest private segment per lane a generated part may have.  Config 5's parts
+// in 550-value chunks (2052 and 1260 bytes per lane) ended in a memory aperture
+// violation on four part streams; 772 bytes (400-value chunks) ran clean.  Scratch
+// is provisioned per queue for every wave slot of the device, so four streams of
+// such parts asked for 4 x 2052 x 64 x (256 CUs x 32 slots) = 4.3 GB of it, against
+// 1.6 GB at 772 bytes.  Parts above the bound, or using a dynamic stack (whose
+// size the descriptor does not state), are refused before anything is loaded.
+constexpr uint32_t kPartPrivateMax = 1024;
+constexpr int64_t kPartScratchTotalMax = int64_t(2) << 30;  // all part streams together
+constexpr int kPartStreamsMax = 4;
+
+static int check_part_scratch(const void* code, int64_t size, const char* name, int device, const char* what, int64_t i) {
+  uint32_t priv = 0, group = 0;
+  int dyn = 0;
+  const int rc = kernel_descriptor_info(code, size, name, &priv, &group, &dyn);
+  if (rc != YE3T_OK) return rc;
+  uint32_t limit = kPartPrivateMax;
+  if (const char* e = std::getenv("YE3T_PART_PRIVATE_MAX")) {  // may only lower the bound
+    const long v = std::atol(e);
+    if (v >= 0 && uint32_t(v) < limit) limit = uint32_t(v);
+  }
+  if (dyn) return set_error(YE3T_EUNSUPPORTED, "%s %lld: kernel %s uses a dynamic stack", what, (long long)i, name);
+  if (priv > limit)
+    return set_error(YE3T_EUNSUPPORTED,
+                     "%s %lld: kernel %s needs %u bytes of scratch per lane, above the %u this library runs "
+                     "(use smaller chunks)",
+                     what, (long long)i, name, priv, limit);
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) cus = 256;
+  const int64_t total = int64_t(priv) * kLanes * int64_t(cus) * 32 * kPartStreamsMax;
+  if (total > kPartScratchTotalMax)
+    return set_error(YE3T_EUNSUPPORTED, "%s %lld: kernel %s would need %lld bytes of scratch on %d streams", what,
+                     (long long)i, name, (long long)total, kPartStreamsMax);
+  return YE3T_OK;
+}
+
 }  // namespace ye3t
 
 using namespace ye3t;
@@ -1530,6 +1633,23 @@ int ye3t_hip_rtc_compile(const char* source, const char* name, const char* arch,
 
 void ye3t_hip_free(void* ptr) { std::free(ptr); }
 
+int ye3t_hip_code_object_kernel_info(const void* code, int64_t size, const char* kernel_name,
+                                     int64_t* private_segment_bytes, int64_t* group_segment_bytes,
+                                     int* uses_dynamic_stack) {
+  clear_error();
+  YE3T_REQUIRE(private_segment_bytes && group_segment_bytes && uses_dynamic_stack, "NULL output");
+  uint32_t priv = 0, group = 0;
+  int dyn = 0;
+  const int rc = kernel_descriptor_info(code, size, kernel_name, &priv, &group, &dyn);
+  if (rc != YE3T_OK) return rc;
+  *private_segment_bytes = priv;
+  *group_segment_bytes = group;
+  *uses_dynamic_stack = dyn;
+  return YE3T_OK;
+}
+
+int64_t ye3t_hip_part_private_limit(void) { return kPartPrivateMax; }
+
 int ye3t_hip_product_plan_attach_generated(ye3t_hip_product_plan* p, const void* code, int64_t size,
                                            const char* kernel_name, int64_t chunk_count, int64_t rows_per_tile,
                                            int persistent, int threads_per_block) {
@@ -1586,6 +1706,10 @@ int ye3t_hip_product_plan_attach_generated_parts(ye3t_hip_product_plan* p, int64
   int prev = 0;
   YE3T_CHECK_HIP(hipGetDevice(&prev));
   YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
+  for (int64_t i = 0; i < part_count; ++i) {
+    const int rc = check_part_scratch(codes[i], sizes[i], kernel_names[i], p->device, "part", i);
+    if (rc != YE3T_OK) return rc;
+  }
   auto* modules = new hipModule_t[size_t(part_count)]();
   auto* fns = new hipFunction_t[size_t(part_count)]();
   auto* chunks = new int64_t[size_t(part_count)];
@@ -1648,6 +1772,10 @@ int ye3t_hip_product_plan_attach_adjoint_parts(ye3t_hip_product_plan* p, int64_t
   int prev = 0;
   YE3T_CHECK_HIP(hipGetDevice(&prev));
   YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
+  for (int64_t i = 0; i < part_count; ++i) {
+    const int rc = check_part_scratch(codes[i], sizes[i], kernel_names[i], p->device, "adjoint part", i);
+    if (rc != YE3T_OK) return rc;
+  }
   int64_t* d_off = nullptr;
   int64_t* d_ids = nullptr;
   YE3T_CHECK_HIP(hipMalloc(&d_off, size_t(W + 1) * sizeof(int64_t)));
@@ -1776,6 +1904,10 @@ int ye3t_hip_product_plan_attach_readout_parts(ye3t_hip_product_plan* p, int64_t
   int prev = 0;
   YE3T_CHECK_HIP(hipGetDevice(&prev));
   YE3T_REQUIRE(prev == p->device, "attach on the plan's device");
+  for (int64_t i = 0; i < part_count; ++i) {
+    const int rc = check_part_scratch(codes[i], sizes[i], kernel_names[i], p->device, "readout part", i);
+    if (rc != YE3T_OK) return rc;
+  }
   auto* modules = new hipModule_t[size_t(part_count)]();
   auto* fns = new hipFunction_t[size_t(part_count)]();
   auto* chunks = new int64_t[size_t(part_count)];

@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 59
+ABI_VERSION = 60
 _LIB = None
 
 F32, F64 = 0, 1
@@ -121,6 +121,9 @@ def lib():
                                                                           _i64, _vp, _vp]
     L.ye3t_hip_symmetric_power_shared_sparse_monomial_double_backward.argtypes = [
         ctypes.c_int, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp]
+    L.ye3t_hip_code_object_kernel_info.argtypes = [ctypes.c_char_p, _i64, ctypes.c_char_p, ctypes.POINTER(_i64),
+                                                   ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_int)]
+    L.ye3t_hip_part_private_limit.restype = _i64
     L.ye3t_hip_evaluate_factorized_schedule.argtypes = [ctypes.c_int, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp,
                                                         _vp, _i64, _vp, _vp]
     L.ye3t_hip_product_plan_create.argtypes = [ctypes.POINTER(ProductPlanDesc), ctypes.POINTER(_vp)]
@@ -217,7 +220,8 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_factorized_angular_segmented_forward", "ye3t_hip_factorized_angular_segmented_adjoint",
     "ye3t_hip_ace_density_edge_gradient", "ye3t_hip_symmetric_power_shared_sparse_monomial",
     "ye3t_hip_symmetric_power_shared_sparse_monomial_adjoint",
-    "ye3t_hip_symmetric_power_shared_sparse_monomial_double_backward",
+    "ye3t_hip_symmetric_power_shared_sparse_monomial_double_backward", "ye3t_hip_code_object_kernel_info",
+    "ye3t_hip_part_private_limit",
 )
 
 
@@ -785,6 +789,23 @@ def rtc_compile(source, name="ye3t_generated.hip", arch="gfx950"):
         fh.write(blob)
     os.replace(tmp, path)
     return blob
+
+
+def code_object_kernel_info(code, kernel_name):
+    """``{"private_segment_bytes", "group_segment_bytes", "uses_dynamic_stack"}``
+    of a kernel in a gfx950 code object, read on the host from its kernel
+    descriptor (``ye3t_hip_code_object_kernel_info``)."""
+    priv, group, dyn = _i64(), _i64(), ctypes.c_int()
+    _check(lib().ye3t_hip_code_object_kernel_info(bytes(code), len(code), kernel_name.encode(), ctypes.byref(priv),
+                                                  ctypes.byref(group), ctypes.byref(dyn)),
+           "ye3t_hip_code_object_kernel_info")
+    return {"private_segment_bytes": priv.value, "group_segment_bytes": group.value,
+            "uses_dynamic_stack": bool(dyn.value)}
+
+
+def part_private_limit():
+    """Bytes of scratch per lane above which the parts attach entry points refuse a kernel."""
+    return int(lib().ye3t_hip_part_private_limit())
 
 
 def _plan_desc(program, out_dtype, in_dtype=None):
