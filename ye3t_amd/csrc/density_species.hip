@@ -1,4 +1,4 @@
-// Stage 1 with one-hot species channels on the matrix cores:
+// Stage 1 with one-hot species channels (and single-channel densities):
 //
 //   A[i, s, n, lm] = sum_{e in row i, species(nbr_e) = s} R_n(|v_e|) Y_lm(v_e / |v_e|)
 //
@@ -7,7 +7,7 @@
 // 1550-1604, 1684-1702, fused).  Each (atom, species) pair is a small
 // [NR x edges] x [edges x LW] product; an edge contributes to exactly one of
 // them, so the kernel groups the edges of every atom by neighbour species and
-// multiplies each group alone -- no work on edges of other species.
+// accumulates each group alone -- no work on edges of other species.
 //
 // One wave (a 64-thread workgroup; no barriers between waves) owns a
 // contiguous atom range (as many waves as the device holds at once) and walks
@@ -15,22 +15,27 @@
 // together:
 //   sort     lane = edge; the neighbour's species is gathered, one ballot per
 //            species gives every (atom, species) group's lanes, and each lane
-//            computes its column in the chunk's tile: its atom's first
-//            column, plus the sizes of the atom's groups of smaller species,
-//            plus its rank within its own group (a stable counting sort);
+//            computes its column of the chunk's tile: its atom's first column, plus
+//            the sizes of the atom's groups of smaller species, plus its rank
+//            within its own group (a stable counting sort);
 //   phase 1  lane = edge; the radial values and real harmonics in fp64
 //            registers, written to LDS transposed at the sorted column
-//            ([n][col], [lm][col]);
+//            (R[n][col], Y[lm][col]);
 //   phase 2  per (atom, species) group, the k-blocks of four columns it
-//            covers, one v_mfma_f64_16x16x4f64 per 16-column harmonic tile
-//            (columns of neighbouring groups masked to zero), alternating
-//            between two accumulator sets; the group's [NR x LW] block then
-//            goes from registers to A (species absent from an atom get zero
-//            blocks).
-// An atom with more than 64 edges is taken alone, species by species: each of
-// its 64-edge windows in turn places its edges of that species in the tile
-// and adds their product to the same accumulators, so every block is still
-// accumulated in registers and stored once.
+//            covers, one v_mfma_f64_16x16x4f64 per 16-component harmonic
+//            tile (columns of neighbouring groups weigh zero), accumulating
+//            in fp64; the group's [NR x LW] block then goes from the
+//            accumulators to A (species absent from an atom get zero
+//            blocks).  The MFMA moves each operand through LDS once per
+//            k-block, where a lane-per-component VALU product would read the
+//            radial values as LDS broadcasts once per edge and lane.
+// Loads run two chunks ahead: chunk i + 2's edges and chunk i + 1's species
+// gather are issued right after chunk i's one wait (which follows its basis
+// math), so they hide behind chunk i's accumulation and stores and chunk
+// i + 1's basis.  An atom with more than 64 edges is taken alone,
+// species by species: each of its 64-edge windows in turn places its edges of
+// that species in the tile and adds them to the same accumulators, so every
+// block is accumulated in registers and stored once.
 // The density is accumulated in fp64 and stored as Out (fp64, or fp32
 // rounded once).  Lane layouts of the fp64 MFMA (l = lane):
 //   A[i][k] from lane i + 16 k; B[k][j] from lane j + 16 k;
@@ -43,9 +48,9 @@
 namespace ye3t {
 namespace {
 
-constexpr int kSpPitch = 67;     // LDS row pitch (doubles): odd, so 16 rows of one column spread over the banks
 constexpr int kSpMaxAtoms = 16;  // whole atoms per chunk
 constexpr int kSpMaxSpecies = 16;
+constexpr int kSpPitch = 67;  // LDS row pitch (doubles) of the transposed tile: odd, so 16 rows of a column spread over the banks
 
 typedef double sp_d4 __attribute__((ext_vector_type(4)));
 
@@ -57,8 +62,6 @@ struct SpeciesParams {
   const int32_t* __restrict__ species;  // null: one channel, every edge in it
   int S;                                // channels
   int NR;                               // radial rows, n_max + 1 (<= 16)
-  int LW;                               // (l_max + 1)^2
-  int lmax;
   int64_t waves;
   double cutoff;
   double lambda;
@@ -73,6 +76,9 @@ __device__ inline int64_t sp_offset(const int64_t* offsets, int64_t i) {
 
 __device__ inline uint64_t sp_ballot(bool v) { return __builtin_amdgcn_ballot_w64(v); }
 
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
+__device__ inline void sp_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // bits [lo, hi) of a 64-bit mask (0 <= lo <= hi <= 64)
 __device__ inline uint64_t sp_range(int lo, int hi) {
   const uint64_t below_hi = hi >= 64 ? ~uint64_t(0) : ((uint64_t(1) << hi) - 1);
@@ -80,202 +86,304 @@ __device__ inline uint64_t sp_range(int lo, int hi) {
   return below_hi & ~below_lo;
 }
 
-// ChebExpCos radial values g_0..g_{nr-1} of one distance (fp64), to out[n * stride]
-__device__ inline void sp_radial(double r, const SpeciesParams& p, double* out, int stride) {
+// Compile-time layout of one (l_max, radial rows) shape: the tile holds NRC
+// radial rows and LW harmonic rows of 64 columns; the product covers them in
+// 16-component tiles (CT of them over the harmonics).
+template <int LMAX, int NRC>
+struct SpShape {
+  static constexpr int LW = (LMAX + 1) * (LMAX + 1);
+  static constexpr int CT = (LW + 15) / 16;
+  static constexpr int ROWS = NRC + LW;
+};
+
+// Radial values g_0..g_{NRC-1} and harmonics of one edge vector, fp64, in registers.
+template <int LMAX, int NRC>
+__device__ inline void sp_basis(double vx, double vy, double vz, const SpeciesParams& p, const NormTable& nt,
+                                double (&Y)[(LMAX + 1) * (LMAX + 1)], double (&R)[NRC]) {
+  const double r = sqrt(vx * vx + vy * vy + vz * vz);
+  const double sr = r > p.eps ? r : p.eps;
+  const double inv = 1.0 / sr;
+  real_sph_row_fixed<LMAX, double, double>(vx * inv, vy * inv, vz * inv, nt, Y);
   const double s = r / p.cutoff;
-  if (s > 1.0) {
-    for (int n = 0; n < p.NR; ++n) out[n * stride] = 0.0;
-    return;
-  }
+  const bool live = s <= 1.0;
   const double env = 1.0 + cospi(s);
-  out[0] = 1.0;
-  if (p.NR > 1) out[stride] = 0.5 * env;
-  if (p.NR > 2) {
+  R[0] = live ? 1.0 : 0.0;
+  if (NRC > 1) R[1] = live ? 0.5 * env : 0.0;
+  if (NRC > 2) {
     const double x = 1.0 - 2.0 * expm1(-p.lambda * (s - 1.0)) / p.den;
     double t0 = 1.0, t1 = x;
-    for (int n = 2; n < p.NR; ++n) {
+#pragma unroll
+    for (int n = 2; n < NRC; ++n) {
       const double t2 = 2.0 * x * t1 - t0;
-      out[n * stride] = 0.25 * (1.0 - t2) * env;
+      R[n] = live ? 0.25 * (1.0 - t2) * env : 0.0;
       t0 = t1;
       t1 = t2;
     }
   }
 }
 
-// Radial values and harmonics of one edge vector, fp64, into tile column `col`.
+// The basis of one edge into tile column `col`.
+template <int LMAX, int NRC>
 __device__ inline void sp_basis_to_tile(double vx, double vy, double vz, const SpeciesParams& p, const NormTable& nt,
                                         double* Wt, double* Yt, int col) {
-  const double r = sqrt(vx * vx + vy * vy + vz * vz);
-  const double sr = r > p.eps ? r : p.eps;
-  const double inv = 1.0 / sr;
-  real_sph_row<double, double>(vx * inv, vy * inv, vz * inv, p.lmax, nt, Yt + col, kSpPitch);
-  sp_radial(r, p, Wt + col, kSpPitch);
+  using Sh = SpShape<LMAX, NRC>;
+  double Y[Sh::LW], R[NRC];
+  sp_basis<LMAX, NRC>(vx, vy, vz, p, nt, Y, R);
+#pragma unroll
+  for (int n = 0; n < NRC; ++n) Wt[n * kSpPitch + col] = R[n];
+#pragma unroll
+  for (int k = 0; k < Sh::LW; ++k) Yt[k * kSpPitch + col] = Y[k];
 }
 
-// Adds the product of tile columns [base, base + c) to the accumulators: the
-// k-blocks of four columns covering them, columns outside masked to zero
-// (they read column 0, which holds finite values, and weigh zero), two
-// accumulator sets alternating over consecutive k-blocks.
-template <int CT>
-__device__ inline void sp_group_product(const double* Wt, const double* Yt, int LW, int base, int c, int kq, int cc,
-                                        sp_d4 (&acc0)[CT], sp_d4 (&acc1)[CT]) {
+// Adds the product of tile columns [base, base + c), c >= 1, to the
+// accumulators: the k-blocks of four columns covering them, columns outside
+// weighing zero (they read column `base`, which holds finite values).  Rows
+// past the tile (i >= NRC, components >= LW) read its last row: their
+// accumulators are never stored.
+template <int LMAX, int NRC>
+__device__ inline void sp_group_product(const double* Wt, const double* Yt, int base, int c, int kq, int cc,
+                                        sp_d4 (&acc)[SpShape<LMAX, NRC>::CT]) {
+  using Sh = SpShape<LMAX, NRC>;
+  const double* const wrow = Wt + (cc < NRC ? cc : NRC - 1) * kSpPitch;
+  const double* yrow[Sh::CT];
+#pragma unroll
+  for (int ct = 0; ct < Sh::CT; ++ct) {
+    const int k = ct * 16 + cc;
+    yrow[ct] = Yt + (k < Sh::LW ? k : Sh::LW - 1) * kSpPitch;
+  }
   const int kb0 = base >> 2, kb1 = (base + c - 1) >> 2;
-  for (int kb = kb0; kb <= kb1; kb += 2) {
-    double w[2], y[2][CT];
+  for (int kb = kb0; kb <= kb1; ++kb) {
+    const int col = 4 * kb + kq;
+    const bool in = col >= base && col < base + c;
+    const int rc = in ? col : base;
+    const double w = wrow[rc];
+    double y[Sh::CT];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int cl = 4 * (kb + h) + kq;
-      const bool in = cl >= base && cl < base + c;
-      const int rc = in ? cl : 0;
-      w[h] = in ? Wt[cc * kSpPitch + rc] : 0.0;
+    for (int ct = 0; ct < Sh::CT; ++ct) y[ct] = yrow[ct][rc];
+    const double wm = in ? w : 0.0;
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const int row = ct * 16 + cc;
-        y[h][ct] = row < LW ? Yt[row * kSpPitch + rc] : 0.0;
-      }
-    }
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) acc0[ct] = __builtin_amdgcn_mfma_f64_16x16x4f64(w[0], y[0][ct], acc0[ct], 0, 0, 0);
-    if (kb + 1 <= kb1) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-        acc1[ct] = __builtin_amdgcn_mfma_f64_16x16x4f64(w[1], y[1][ct], acc1[ct], 0, 0, 0);
-    }
+    for (int ct = 0; ct < Sh::CT; ++ct) acc[ct] = __builtin_amdgcn_mfma_f64_16x16x4f64(wm, y[ct], acc[ct], 0, 0, 0);
   }
 }
 
 template <int CT>
-__device__ inline void sp_zero(sp_d4 (&acc0)[CT], sp_d4 (&acc1)[CT]) {
+__device__ inline void sp_zero(sp_d4 (&acc)[CT]) {
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) {
-    acc0[ct] = sp_d4{0.0, 0.0, 0.0, 0.0};
-    acc1[ct] = sp_d4{0.0, 0.0, 0.0, 0.0};
-  }
+  for (int ct = 0; ct < CT; ++ct) acc[ct] = sp_d4{0.0, 0.0, 0.0, 0.0};
 }
 
 // One (atom, species) block [NR x LW] from the accumulators (rounded once to Out).
-template <typename Out, int CT>
-__device__ inline void sp_store(Out* __restrict__ dst, const sp_d4 (&acc0)[CT], const sp_d4 (&acc1)[CT], int NR,
-                                int LW, int kq, int cc) {
+template <int LMAX, int NRC, typename Out>
+__device__ inline void sp_store(Out* __restrict__ dst, const sp_d4 (&acc)[SpShape<LMAX, NRC>::CT], int NR, int kq,
+                                int cc) {
+  using Sh = SpShape<LMAX, NRC>;
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct)
+  for (int ct = 0; ct < Sh::CT; ++ct)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int n = 4 * v + kq, lm = ct * 16 + cc;
-      if (n < NR && lm < LW) dst[n * LW + lm] = Out(acc0[ct][v] + acc1[ct][v]);
+      if (n < NR && lm < Sh::LW) dst[n * Sh::LW + lm] = Out(acc[ct][v]);
     }
 }
 
-template <typename In, typename Out, int CT>
-__global__ __launch_bounds__(64) void ace_density_species_kernel(SpeciesParams p, NormTable nt) {
+// The chunk starting at atom a: up to 16 whole atoms with at most 64 edges,
+// read through the scalar cache (so nothing waits on the vector stores still
+// draining); rel[j] = first edge of atom a + j relative to e0, cnt = edges.
+// na == 0: atom a alone has more than 64 edges, or a == a_end (past the
+// wave's range).
+struct SpChunk {
+  int64_t a, e0;
+  int na, cnt;
+  int rel[kSpMaxAtoms + 1];
+};
+
+__device__ inline SpChunk sp_form(const SpeciesParams& p, int64_t a, int64_t a_end) {
+  SpChunk c;
+  a = a < a_end ? a : a_end;  // past the end: an empty chunk at a_end
+  c.a = a;
+  c.e0 = sp_offset(p.offsets, a);
+  int64_t ends[kSpMaxAtoms];
+#pragma unroll
+  for (int j = 1; j <= kSpMaxAtoms; ++j) ends[j - 1] = sp_offset(p.offsets, (a + j) <= a_end ? (a + j) : a_end);
+  c.na = 0;
+  c.rel[0] = 0;
+  bool open = true;
+#pragma unroll
+  for (int j = 1; j <= kSpMaxAtoms; ++j) {
+    open = open && (a + j) <= a_end && ends[j - 1] - c.e0 <= 64;
+    c.rel[j] = open ? int(ends[j - 1] - c.e0) : 64 + 1;
+    c.na += open ? 1 : 0;
+  }
+  c.cnt = 0;
+#pragma unroll
+  for (int j = 1; j <= kSpMaxAtoms; ++j) c.cnt = (j == c.na) ? c.rel[j] : c.cnt;
+  return c;
+}
+
+// First atom after chunk c (a chunk with na == 0 is one atom).
+__device__ inline int64_t sp_after(const SpChunk& c) { return c.a + (c.na > 0 ? c.na : 1); }
+
+// One lane's edge of a chunk: its vector and neighbour (zeros past the chunk's
+// edges, and for a single-atom chunk of more than 64 edges, which loads its
+// own).
+template <typename In>
+struct SpEdges {
+  In x, y, z;
+  int64_t nb;
+};
+
+template <typename In>
+__device__ inline SpEdges<In> sp_load(const SpeciesParams& p, const In* __restrict__ vec, const SpChunk& c, int lane) {
+  SpEdges<In> r{In(0), In(0), In(0), 0};
+  if (c.na > 0 && lane < c.cnt) {
+    const int64_t e = c.e0 + lane;
+    r.x = vec[3 * e];
+    r.y = vec[3 * e + 1];
+    r.z = vec[3 * e + 2];
+    r.nb = p.nbr[e];
+  }
+  return r;
+}
+
+// The species channel of the lane's neighbour (-1 past the chunk's edges).
+__device__ inline int sp_gather(const SpeciesParams& p, const SpChunk& c, int64_t nb, int lane) {
+  if (c.na == 0 || lane >= c.cnt) return -1;
+  return p.species ? int(p.species[nb]) : 0;
+}
+
+// l_max >= 5 tiles take more than 32 KB of LDS per wave, so one wave per SIMD
+// runs anyway: let those kernels use every VGPR (the basis of a chunk is held
+// in registers across its loads)
+template <typename In, typename Out, int LMAX, int NRC>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, LMAX >= 5 ? 1 : 4))) void
+ace_density_species_kernel(SpeciesParams p, NormTable nt) {
+  using Sh = SpShape<LMAX, NRC>;
+  constexpr int LW = Sh::LW, CT = Sh::CT;
   extern __shared__ __align__(16) double sp_smem[];
-  double* const Wt = sp_smem;                  // [16][P]: rows >= NR stay zero
-  double* const Yt = sp_smem + 16 * kSpPitch;  // [LW][P]
-  __shared__ int rel[kSpMaxAtoms + 1];         // chunk-relative atom starts
+  double* const Wt = sp_smem;                    // [NRC][P]
+  double* const Yt = sp_smem + NRC * kSpPitch;  // [LW][P]
 
   const int lane = threadIdx.x;
   const int kq = lane >> 4, cc = lane & 15;
-  const int NR = p.NR, LW = p.LW, S = p.S;
+  // the exact-shape instantiations (NRC < 16) run only with NR == NRC
+  const int NR = NRC < 16 ? NRC : p.NR, S = p.S;
   const int64_t a_begin = int64_t(blockIdx.x) * p.N / p.waves;
   const int64_t a_end = (int64_t(blockIdx.x) + 1) * p.N / p.waves;
   if (a_begin >= a_end) return;
-  for (int q = lane; q < (16 + LW) * kSpPitch; q += 64) sp_smem[q] = 0.0;
   const In* __restrict__ vec = static_cast<const In*>(p.vec);
   Out* __restrict__ Aout = static_cast<Out*>(p.A);
   const int64_t block = int64_t(NR) * LW;  // one (atom, species) block
   const uint64_t lt = sp_range(0, lane);   // lanes below this one
-  __syncthreads();
 
-  sp_d4 acc0[CT], acc1[CT];
-  int64_t a = a_begin;
-  while (a < a_end) {
-    // ---- the chunk: whole atoms [a, a + na) within 64 edges
-    const int64_t e0 = sp_offset(p.offsets, a);
-    // lane l (1..16) tests whether atoms a .. a + l - 1 fit in 64 edges; the
-    // fitting lanes are a prefix 1..na (offsets do not decrease)
-    const int64_t al = a + lane;
-    const int64_t endl = (lane >= 1 && lane <= kSpMaxAtoms && al <= a_end) ? sp_offset(p.offsets, al) : e0 + 65;
-    const int na = __builtin_popcountll(sp_ballot(lane >= 1 && endl - e0 <= 64));
-
-    if (na == 0) {
+  sp_d4 acc[CT];
+  // Software pipeline over chunks.  On entry to chunk i (with at most 64
+  // edges) the lane holds chunk i's edge vector, the gather of its neighbour's
+  // species is in flight, and so are chunk i + 1's loads: the one wait, after
+  // chunk i's basis, finds them (and chunk i - 1's stores) done, and chunk
+  // i + 1's gather and chunk i + 2's loads then go out behind chunk i's
+  // accumulation and stores and chunk i + 1's basis.
+  SpChunk cur = sp_form(p, a_begin, a_end);
+  SpEdges<In> E = sp_load(p, vec, cur, lane);
+  int sp = sp_gather(p, cur, E.nb, lane);
+  SpChunk nxt = sp_form(p, sp_after(cur), a_end);
+  SpEdges<In> NE = sp_load(p, vec, nxt, lane);
+  while (cur.a < a_end) {
+    if (cur.na == 0) {
       // ---- atom a has more than 64 edges: per species, every 64-edge window
-      // of the atom in turn, accumulating in registers; each block is stored
-      // once, whatever the number of windows
+      // of the atom in turn, accumulating in registers; each block is stored once
+      const int64_t a = cur.a;
       const int64_t hi = sp_offset(p.offsets, a + 1);
       for (int s = 0; s < S; ++s) {
-        sp_zero<CT>(acc0, acc1);
-        for (int64_t t0 = e0; t0 < hi; t0 += 64) {
+        sp_zero<CT>(acc);
+        for (int64_t t0 = cur.e0; t0 < hi; t0 += 64) {
           const int64_t e = t0 + lane;
           const bool in_s = e < hi && (p.species ? int(p.species[p.nbr[e]]) : 0) == s;
           const uint64_t m = sp_ballot(in_s);
           const int c = __builtin_popcountll(m);
           if (c == 0) continue;
-          if (in_s) sp_basis_to_tile(double(vec[3 * e]), double(vec[3 * e + 1]), double(vec[3 * e + 2]), p, nt, Wt,
-                                     Yt, __builtin_popcountll(m & lt));
+          if (in_s)
+            sp_basis_to_tile<LMAX, NRC>(double(vec[3 * e]), double(vec[3 * e + 1]), double(vec[3 * e + 2]), p, nt,
+                                        Wt, Yt, __builtin_popcountll(m & lt));
           __syncthreads();
-          sp_group_product<CT>(Wt, Yt, LW, 0, c, kq, cc, acc0, acc1);
+          sp_group_product<LMAX, NRC>(Wt, Yt, 0, c, kq, cc, acc);
           __syncthreads();  // operand reads done before the next window's writes
         }
-        sp_store<Out, CT>(Aout + (a * S + s) * block, acc0, acc1, NR, LW, kq, cc);
+        sp_store<LMAX, NRC, Out>(Aout + (a * S + s) * block, acc, NR, kq, cc);
       }
-      a += 1;
+      // refill the pipeline from the chunk after the atom (its loads are out)
+      cur = nxt;
+      E = NE;
+      sp = sp_gather(p, cur, E.nb, lane);
+      nxt = sp_form(p, sp_after(cur), a_end);
+      NE = sp_load(p, vec, nxt, lane);
       continue;
     }
 
-    if (lane <= na) rel[lane] = lane == 0 ? 0 : int(endl - e0);
-    const int cnt = __builtin_amdgcn_readlane(int(endl - e0), na);
-    __syncthreads();
+    // ---- chunk i: basis in registers, the one wait, the next loads out
+    const bool valid = lane < cur.cnt;
+    double Y[LW], R[NRC];
+    sp_basis<LMAX, NRC>(double(E.x), double(E.y), double(E.z), p, nt, Y, R);
+    sp_wait_vmem();
+    const int nsp = sp_gather(p, nxt, NE.nb, lane);
+    const SpChunk nn = sp_form(p, sp_after(nxt), a_end);
+    const SpEdges<In> NNE = sp_load(p, vec, nn, lane);
 
     // ---- sort: (atom, species) groups in column order
-    const bool valid = lane < cnt;
-    const int64_t e = e0 + lane;
-    double vx = 0.0, vy = 0.0, vz = 0.0;
-    int sp = -1;
-    if (valid) {
-      vx = double(vec[3 * e]);
-      vy = double(vec[3 * e + 1]);
-      vz = double(vec[3 * e + 2]);
-      sp = p.species ? int(p.species[p.nbr[e]]) : 0;
-    }
     int la = 0;  // the lane's atom within the chunk
-    for (int j = 1; j < na; ++j) la += (lane >= rel[j]) ? 1 : 0;
-    const uint64_t amask = sp_range(rel[la], rel[la + 1]);
-    int col = rel[la];
+#pragma unroll
+    for (int j = 1; j < kSpMaxAtoms; ++j) la += (j < cur.na && lane >= cur.rel[j]) ? 1 : 0;
+    int lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < kSpMaxAtoms; ++j) {
+      lo = la == j ? cur.rel[j] : lo;
+      hi = la == j ? cur.rel[j + 1] : hi;
+    }
+    const uint64_t amask = sp_range(lo, hi);
+    int col = lo;
 #pragma unroll
     for (int s = 0; s < kSpMaxSpecies; ++s) {
       if (s >= S) break;
       const uint64_t m = sp_ballot(valid && sp == s) & amask;
       col += s < sp ? __builtin_popcountll(m) : (s == sp ? __builtin_popcountll(m & lt) : 0);
     }
-
-    // ---- phase 1: radial values and harmonics of this lane's edge at its column
-    if (valid) sp_basis_to_tile(vx, vy, vz, p, nt, Wt, Yt, col);
+    if (valid) {
+#pragma unroll
+      for (int n = 0; n < NRC; ++n) Wt[n * kSpPitch + col] = R[n];
+#pragma unroll
+      for (int k = 0; k < LW; ++k) Yt[k * kSpPitch + col] = Y[k];
+    }
     __syncthreads();
 
     // ---- phase 2: one product per (atom, species) group
-    for (int j = 0; j < na; ++j) {
-      const uint64_t am = sp_range(rel[j], rel[j + 1]);
-      int base = rel[j];
+    for (int j = 0; j < cur.na; ++j) {
+      int rj = 0, rj1 = 0;  // chunk-relative columns of atom j
+#pragma unroll
+      for (int k = 0; k < kSpMaxAtoms; ++k) {
+        rj = k == j ? cur.rel[k] : rj;
+        rj1 = k == j ? cur.rel[k + 1] : rj1;
+      }
+      const uint64_t am = sp_range(rj, rj1);
+      int base = rj;
       for (int s = 0; s < S; ++s) {
         const int c = __builtin_popcountll(sp_ballot(valid && sp == s) & am);
-        Out* __restrict__ dst = Aout + ((a + j) * S + s) * block;
-        if (c == 0) {
-          for (int q = lane; q < block; q += 64) dst[q] = Out(0);
-          continue;
-        }
-        sp_zero<CT>(acc0, acc1);
-        sp_group_product<CT>(Wt, Yt, LW, base, c, kq, cc, acc0, acc1);
-        sp_store<Out, CT>(dst, acc0, acc1, NR, LW, kq, cc);
+        sp_zero<CT>(acc);
+        if (c > 0) sp_group_product<LMAX, NRC>(Wt, Yt, base, c, kq, cc, acc);
+        sp_store<LMAX, NRC, Out>(Aout + ((cur.a + j) * S + s) * block, acc, NR, kq, cc);
         base += c;
       }
     }
     __syncthreads();  // tile reads done before the next chunk's writes
-    a += na;
+    cur = nxt;
+    E = NE;
+    sp = nsp;
+    nxt = nn;
+    NE = NNE;
   }
 }
 
-template <typename In, typename Out, int CT>
+template <typename In, typename Out, int LMAX, int NRC>
 int launch_species(const ye3t_density_args* a, void* A, hipStream_t stream) {
+  using Sh = SpShape<LMAX, NRC>;
   SpeciesParams p;
   p.N = a->atom_count;
   p.offsets = a->row_offsets;
@@ -284,15 +392,13 @@ int launch_species(const ye3t_density_args* a, void* A, hipStream_t stream) {
   p.species = a->species;
   p.S = int(a->channel_count);
   p.NR = int(a->max_radial_index) + 1;
-  p.LW = int((a->max_angular + 1) * (a->max_angular + 1));
-  p.lmax = int(a->max_angular);
   p.cutoff = a->cutoff > 2.220446049250313e-16 ? a->cutoff : 2.220446049250313e-16;
   p.lambda = a->lambda;
   p.den = std::expm1(a->lambda);
   p.eps = a->epsilon;
   p.A = A;
-  const size_t lds = sizeof(double) * size_t(16 + p.LW) * kSpPitch;
-  const void* kernel = reinterpret_cast<const void*>(&ace_density_species_kernel<In, Out, CT>);
+  const size_t lds = sizeof(double) * size_t(Sh::ROWS) * kSpPitch;
+  const void* kernel = reinterpret_cast<const void*>(&ace_density_species_kernel<In, Out, LMAX, NRC>);
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
@@ -303,10 +409,21 @@ int launch_species(const ye3t_density_args* a, void* A, hipStream_t stream) {
   if (waves < 1) waves = 1;
   if (waves > p.N) waves = p.N;
   p.waves = waves;
-  hipLaunchKernelGGL((ace_density_species_kernel<In, Out, CT>), dim3(unsigned(waves)), dim3(64), lds, stream, p,
-                     norm_table());
+  hipLaunchKernelGGL((ace_density_species_kernel<In, Out, LMAX, NRC>), dim3(unsigned(waves)), dim3(64), lds, stream,
+                     p, norm_table());
   set_density_kernel("ace_density_species_kernel");
   return check_launch("ace_density_species_kernel");
+}
+
+// The benchmark shapes get their exact radial row count; every other n_max
+// runs with 16 rows computed and the unused ones not stored.
+template <typename In, typename Out, int LMAX>
+int launch_species_l(const ye3t_density_args* a, void* A, hipStream_t stream) {
+  const int64_t nr = a->max_radial_index + 1;
+  if (LMAX == 3 && nr == 9) return launch_species<In, Out, LMAX, 9>(a, A, stream);
+  if (LMAX == 4 && nr == 11) return launch_species<In, Out, LMAX, 11>(a, A, stream);
+  if (LMAX == 6 && nr == 13) return launch_species<In, Out, LMAX, 13>(a, A, stream);
+  return launch_species<In, Out, LMAX, 16>(a, A, stream);
 }
 
 }  // namespace
@@ -320,14 +437,16 @@ int launch_density_species(const ye3t_density_args* a, void* A, hipStream_t stre
   if (a->max_radial_index > 15 || a->max_angular > 8) return YE3T_EUNSUPPORTED;
   if (a->channel_count > kSpMaxSpecies || (!a->species && a->channel_count != 1)) return YE3T_EUNSUPPORTED;
   if (a->atom_count == 0) return YE3T_OK;
-  const int LW = int((a->max_angular + 1) * (a->max_angular + 1));
-  switch ((LW + 15) / 16) {
-    case 1: return launch_species<In, Out, 1>(a, A, stream);
-    case 2: return launch_species<In, Out, 2>(a, A, stream);
-    case 3: return launch_species<In, Out, 3>(a, A, stream);
-    case 4: return launch_species<In, Out, 4>(a, A, stream);
-    case 5: return launch_species<In, Out, 5>(a, A, stream);
-    default: return launch_species<In, Out, 6>(a, A, stream);
+  switch (a->max_angular) {
+    case 0: return launch_species_l<In, Out, 0>(a, A, stream);
+    case 1: return launch_species_l<In, Out, 1>(a, A, stream);
+    case 2: return launch_species_l<In, Out, 2>(a, A, stream);
+    case 3: return launch_species_l<In, Out, 3>(a, A, stream);
+    case 4: return launch_species_l<In, Out, 4>(a, A, stream);
+    case 5: return launch_species_l<In, Out, 5>(a, A, stream);
+    case 6: return launch_species_l<In, Out, 6>(a, A, stream);
+    case 7: return launch_species_l<In, Out, 7>(a, A, stream);
+    default: return launch_species_l<In, Out, 8>(a, A, stream);
   }
 }
 
