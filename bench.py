@@ -340,6 +340,12 @@ def bench_op(args, cfg):
         call(True)  # validates the CSR and neighbour indices once
         kernel = native.last_density_kernel()
         t = _time_kernel(lambda: call(False), args.steps, args.warmup)
+        if args.copy_probe:  # a plain elementwise copy of A's size, for the FETCH_SIZE / WRITE_SIZE scales
+            probe = torch.empty_like(A)
+            torch.neg(A, out=probe)
+            torch.cuda.synchronize()
+            line["copy_probe_bytes"] = {"read": A.numel() * A.element_size(), "write": probe.numel() * probe.element_size()}
+            del probe
         elem = 8 if dtype == "f64" else 4
         b1, _ = algorithmic_bytes(cfg, _NoPlan(), elem)
         a_elem = A.element_size()

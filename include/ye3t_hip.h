@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define YE3T_HIP_ABI_VERSION 60 /* reference native ABI floor is 42 (execution_plan.py:35) */
+#define YE3T_HIP_ABI_VERSION 61 /* reference native ABI floor is 42 (execution_plan.py:35) */
 
 typedef struct ihipStream_t* ye3t_stream_t; /* == hipStream_t */
 
@@ -301,6 +301,14 @@ int ye3t_hip_product_forward(const ye3t_hip_product_plan* plan, const void* A, i
  * (the reference JIT-compiles its whole extension, execution_plan.py:253-292). */
 int ye3t_hip_rtc_compile(const char* source, const char* name, const char* arch, void** code, int64_t* size);
 void ye3t_hip_free(void* ptr);
+
+/* What besides the source and the architecture decides ye3t_hip_rtc_compile's
+ * output, as text: the hipRTC version, its options and this ABI version
+ * ("hiprtc 7.2 | options -O3 ... | abi 61"), NUL-terminated into buf
+ * (capacity bytes).  Callers caching code objects on disk key them by it.
+ * No reference counterpart (the reference caches its whole extension build by
+ * source and flags, execution_plan.py:253-292). */
+int ye3t_hip_rtc_fingerprint(char* buf, int64_t capacity);
 
 /* Facts of kernel `kernel_name` read from a gfx950 code object on the host
  * (its AMDHSA kernel descriptor): private (scratch) segment bytes per lane, LDS
@@ -715,11 +723,16 @@ int ye3t_hip_product_adjoint_stream(const ye3t_hip_product_plan* plan, const voi
 /* ye3t_hip_product_adjoint_stream without a workspace argument and without
  * any allocation: the per-group partial gradients live in a static device
  * array of 64 MiB (one per device the library runs on, held until the process
- * ends), cleared by the call with a fill kernel.  Fewer groups than the
- * workspace form may be used, so sums are grouped differently (same values to
- * rounding).  YE3T_EUNSUPPORTED when one group's partials exceed 64 MiB
- * (a_width * samples rounded up to 64 * element size).  Calls that overlap on
- * one device (other streams or threads) share the array and race.
+ * ends), cleared by the call with a fill kernel.  Its address and an ordering
+ * event are looked up when a term-stream plan is created, so the call itself
+ * makes no set-up call.  Fewer groups than the workspace form may be used, so
+ * sums are grouped differently (same values to rounding).  YE3T_EUNSUPPORTED
+ * when one group's partials exceed 64 MiB (a_width * samples rounded up to 64
+ * * element size).  Calls on one device are serialised: host threads take a
+ * lock, and an eager call on another stream than the previous call's waits on
+ * the GPU (hipStreamWaitEvent) for the previous call's kernels.  Under stream
+ * capture the call records its kernels only; a graph holding it must not run
+ * concurrently with other users of the scratch on that device.
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under stream capture, tight serving loops, allocation-free
  * harnesses). */

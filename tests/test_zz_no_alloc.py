@@ -63,3 +63,82 @@ def test_noalloc_stream_adjoint_refuses_sizes_beyond_the_scratch(gpu):
     out = torch.empty_like(A)
     with pytest.raises(RuntimeError, match="static scratch"):
         pipe.handle.adjoint_stream_noalloc(A, gB, out)
+
+
+def _inputs(rng, pipe, samples, real, gpu):
+    import torch
+
+    A = torch.as_tensor(rng.normal(size=(samples, pipe.plan.a_width)), dtype=real, device=gpu)
+    gB = torch.as_tensor(rng.normal(size=(samples, pipe.feature_count)), dtype=real, device=gpu)
+    return A, gB
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(gpu):
+    """Back-to-back calls on two streams share the scratch: the second waits
+    for the first's kernels, so each equals the same call made alone."""
+    import torch
+
+    pipe = ACEPipeline(W.config(2).feature_spec, "f64", kernel="interpreter")
+    handle = pipe.handle
+    rng = np.random.default_rng(62)
+    A1, gB1 = _inputs(rng, pipe, 4000, torch.float64, gpu)
+    A2, gB2 = _inputs(rng, pipe, 700, torch.float64, gpu)
+    alone = []
+    for A, gB in ((A1, gB1), (A2, gB2)):
+        out = torch.empty_like(A)
+        handle.adjoint_stream_noalloc(A, gB, out)
+        torch.cuda.synchronize()
+        alone.append(out)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = [torch.full_like(A1, float("nan")), torch.full_like(A2, float("nan")), torch.full_like(A1, float("nan"))]
+    flush("noalloc: calls on streams s1, s2, s1 without host synchronisation")
+    with torch.cuda.stream(s1):
+        handle.adjoint_stream_noalloc(A1, gB1, outs[0])
+    with torch.cuda.stream(s2):
+        handle.adjoint_stream_noalloc(A2, gB2, outs[1])
+    with torch.cuda.stream(s1):
+        handle.adjoint_stream_noalloc(A1, gB1, outs[2])
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], alone[0])
+    assert torch.equal(outs[1], alone[1])
+    assert torch.equal(outs[2], alone[0])
+
+
+def test_noalloc_call_captured_in_a_graph(gpu):
+    """A captured call (its fill kernel clears the scratch: no memset node)
+    replays to the eager result, with eager calls that reuse the scratch and
+    host synchronisations between the replays."""
+    import torch
+
+    pipe = ACEPipeline(W.config(2).feature_spec, "f64", kernel="interpreter")
+    handle = pipe.handle
+    rng = np.random.default_rng(63)
+    A, gB = _inputs(rng, pipe, 1500, torch.float64, gpu)
+    A2, gB2 = _inputs(rng, pipe, 900, torch.float64, gpu)
+    want = torch.empty_like(A)
+    handle.adjoint_stream_noalloc(A, gB, want)
+    want2 = torch.empty_like(A2)
+    handle.adjoint_stream_noalloc(A2, gB2, want2)
+    torch.cuda.synchronize()
+    out = torch.empty_like(A)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up outside the capture
+        handle.adjoint_stream_noalloc(A, gB, out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    flush("noalloc: capturing the call into a graph")
+    with torch.cuda.graph(graph):
+        handle.adjoint_stream_noalloc(A, gB, out)
+    torch.cuda.synchronize()
+    for replay in range(3):
+        flush(f"noalloc: replay {replay}")
+        out.fill_(float("nan"))
+        other = torch.full_like(A2, float("nan"))
+        handle.adjoint_stream_noalloc(A2, gB2, other)  # eager use of the scratch between replays
+        torch.cuda.synchronize()
+        assert torch.equal(other, want2)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)

@@ -8,7 +8,8 @@ compiles one module at a time per process (one to five minutes for a 64-chunk
 config-3 part), so the parts are spread over worker processes.  hipRTC needs
 no GPU, so this runs on a build host; the code objects land in the JIT cache
 (``ye3t_amd/jit_cache`` unless ``YE3T_AMD_JIT_CACHE`` says otherwise), keyed by
-source hash, and travel with the tree.
+architecture, compiler fingerprint (hipRTC version, options, ABI) and source
+(``native.rtc_cache_key``), and travel with the tree.
 
     python -m ye3t_amd.ace.prebuild            # configs 2, 3 and 5, every dtype they are benchmarked in
     python -m ye3t_amd.ace.prebuild 2 --dtype f64

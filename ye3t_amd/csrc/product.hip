@@ -1086,13 +1086,20 @@ constexpr int64_t kNoAllocScratchBytes = int64_t(64) << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mutex;
+std::mutex g_scratch_mutex;  // held across each call's set-up and launches
 void* g_scratch_address[kMaxScratchDevices] = {};
+// Last eager use of each device's scratch: its stream and an event recorded
+// after its kernels, so a call on another stream first waits for it.
+hipEvent_t g_scratch_done[kMaxScratchDevices] = {};
+hipStream_t g_scratch_stream[kMaxScratchDevices] = {};
+bool g_scratch_used[kMaxScratchDevices] = {};
 
-// Device address of `scratch` on device `dev` (the current device).
-int scratch_address(int dev, void** out) {
+// Device address of `scratch` on device `dev` (the current device), and the
+// event that orders its users.  Done once per device, at plan creation (never
+// under stream capture), with the device current.  Caller holds
+// g_scratch_mutex.
+int scratch_setup_locked(int dev) {
   YE3T_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "device %d beyond the scratch table", dev);
-  std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (!g_scratch_address[dev]) {
     void* ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
@@ -1102,8 +1109,20 @@ int scratch_address(int dev, void** out) {
     }
     g_scratch_address[dev] = ptr;
   }
-  *out = g_scratch_address[dev];
+  if (!g_scratch_done[dev]) {
+    const hipError_t e = hipEventCreateWithFlags(&g_scratch_done[dev], hipEventDisableTiming);
+    if (e != hipSuccess) {
+      g_scratch_done[dev] = nullptr;
+      return set_error(YE3T_ELAUNCH, "hipEventCreate for the scratch failed on device %d: %s", dev,
+                       hipGetErrorString(e));
+    }
+  }
   return YE3T_OK;
+}
+
+int scratch_setup(int dev) {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  return scratch_setup_locked(dev);
 }
 
 // ---- scratch of generated parts -------------------------------------------
@@ -1171,6 +1190,10 @@ static int kernel_descriptor_info(const void* code, int64_t size, const char* na
   }
   return set_error(YE3T_EINVAL, "kernel descriptor %s not found", want.c_str());
 }
+
+// hipRTC options of every generated kernel (after --offload-arch); they are
+// part of the fingerprint that keys the on-disk code-object cache.
+const char* const kRtcOptions[] = {"-O3", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
 
 // Largest private segment per lane a generated part may have.  Config 5's parts
 // in 550-value chunks (2052 and 1260 bytes per lane) ended in a memory aperture
@@ -1320,12 +1343,31 @@ int ye3t_hip_product_adjoint_stream_noalloc(const ye3t_hip_product_plan* p, cons
                      (long long)(kNoAllocScratchBytes / (p->a_width * (p->dtype == YE3T_F64 ? 8 : 4)) / kLanes *
                                  kLanes));
   }
-  void* P = nullptr;
-  const int rc = scratch_address(dev, &P);
-  if (rc != YE3T_OK) return rc;
   const hipStream_t s = as_stream(stream);
-  return columns ? launch_stream_adjoint<true>(p, A, lda, gB, samples, P, groups, gA, s)
-                 : launch_stream_adjoint<false>(p, A, lda, gB, samples, P, groups, gA, s);
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  YE3T_CHECK_HIP(hipStreamIsCapturing(s, &capture));
+  // One call at a time per device: host threads queue on the mutex, and an
+  // eager call on another stream than the last one waits on the GPU for the
+  // last one's kernels.  Under capture no event is recorded or waited on: the
+  // captured kernels are ordered by the stream the graph is launched on.
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_address[dev] || !g_scratch_done[dev]) {
+    YE3T_REQUIRE(capture == hipStreamCaptureStatusNone,
+                 "the scratch of device %d is set up by plan creation, not under stream capture", dev);
+    const int rc = scratch_setup_locked(dev);
+    if (rc != YE3T_OK) return rc;
+  }
+  void* const P = g_scratch_address[dev];
+  const bool eager = capture == hipStreamCaptureStatusNone;
+  if (eager && g_scratch_used[dev] && g_scratch_stream[dev] != s)
+    YE3T_CHECK_HIP(hipStreamWaitEvent(s, g_scratch_done[dev], 0));
+  const int rc = columns ? launch_stream_adjoint<true>(p, A, lda, gB, samples, P, groups, gA, s)
+                         : launch_stream_adjoint<false>(p, A, lda, gB, samples, P, groups, gA, s);
+  if (rc != YE3T_OK || !eager) return rc;
+  YE3T_CHECK_HIP(hipEventRecord(g_scratch_done[dev], s));
+  g_scratch_stream[dev] = s;
+  g_scratch_used[dev] = true;
+  return YE3T_OK;
 }
 
 int ye3t_hip_transpose(int dtype, const void* A, int64_t rows, int64_t cols, void* At, int64_t ld,
@@ -1591,8 +1633,27 @@ int ye3t_hip_product_plan_create(const ye3t_product_plan_desc* d, ye3t_hip_produ
     p->use_stream = 1;
     const char* per = std::getenv("YE3T_STREAM_TILES");
     p->stream_tiles = per ? std::atoll(per) : 0;
+    // the allocation-free adjoint's scratch address and ordering event, looked
+    // up here so that entry point makes no set-up call (it may run under capture)
+    if ((rc = scratch_setup(p->device)) != YE3T_OK) {
+      ye3t_hip_product_plan_destroy(p);
+      return rc;
+    }
   }
   *out = p;
+  return YE3T_OK;
+}
+
+int ye3t_hip_rtc_fingerprint(char* buf, int64_t capacity) {
+  clear_error();
+  YE3T_REQUIRE(buf && capacity > 0, "NULL argument");
+  int major = 0, minor = 0;
+  if (hiprtcVersion(&major, &minor) != HIPRTC_SUCCESS) return set_error(YE3T_ELAUNCH, "hiprtcVersion failed");
+  std::string fp = "hiprtc " + std::to_string(major) + "." + std::to_string(minor) + " | options";
+  for (const char* o : ye3t::kRtcOptions) fp += std::string(" ") + o;
+  fp += " | abi " + std::to_string(YE3T_HIP_ABI_VERSION);
+  YE3T_REQUIRE(int64_t(fp.size()) < capacity, "fingerprint buffer too small");
+  std::memcpy(buf, fp.c_str(), fp.size() + 1);
   return YE3T_OK;
 }
 
@@ -1602,7 +1663,8 @@ int ye3t_hip_rtc_compile(const char* source, const char* name, const char* arch,
   *code = nullptr;
   *size = 0;
   std::string arch_opt = std::string("--offload-arch=") + (arch && *arch ? arch : "gfx950");
-  const char* opts[] = {arch_opt.c_str(), "-O3", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  const char* opts[1 + sizeof(ye3t::kRtcOptions) / sizeof(ye3t::kRtcOptions[0])] = {arch_opt.c_str()};
+  for (size_t i = 0; i < sizeof(ye3t::kRtcOptions) / sizeof(ye3t::kRtcOptions[0]); ++i) opts[i + 1] = ye3t::kRtcOptions[i];
   hiprtcProgram prog;
   if (hiprtcCreateProgram(&prog, source, name ? name : "ye3t_generated.hip", 0, nullptr, nullptr) !=
       HIPRTC_SUCCESS) {

@@ -12,7 +12,7 @@ import numpy as np
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "libye3t_hip.so")
-ABI_VERSION = 60
+ABI_VERSION = 61
 _LIB = None
 
 F32, F64 = 0, 1
@@ -132,6 +132,7 @@ def lib():
     L.ye3t_hip_product_forward.argtypes = [_vp, _vp, _i64, _vp, _vp]
     L.ye3t_hip_product_launch_info.argtypes = [_vp, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                                                ctypes.POINTER(_i64)]
+    L.ye3t_hip_rtc_fingerprint.argtypes = [ctypes.c_char_p, _i64]
     L.ye3t_hip_rtc_compile.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_vp),
                                        ctypes.POINTER(_i64)]
     L.ye3t_hip_free.argtypes = [_vp]
@@ -199,7 +200,7 @@ EXPORTED_SYMBOLS = (
     "ye3t_hip_real_sph_table", "ye3t_hip_density_accumulate_csr", "ye3t_hip_ace_density_forward",
     "ye3t_hip_symmetric_power_monomial", "ye3t_hip_evaluate_factorized_schedule",
     "ye3t_hip_product_plan_create", "ye3t_hip_product_plan_destroy", "ye3t_hip_product_forward",
-    "ye3t_hip_product_launch_info", "ye3t_hip_rtc_compile", "ye3t_hip_free",
+    "ye3t_hip_product_launch_info", "ye3t_hip_rtc_compile", "ye3t_hip_rtc_fingerprint", "ye3t_hip_free",
     "ye3t_hip_product_plan_attach_generated", "ye3t_hip_product_plan_select", "ye3t_hip_last_density_kernel",
     "ye3t_hip_product_plan_attach_generated_parts",
     "ye3t_hip_product_plan_attach_adjoint_parts", "ye3t_hip_product_adjoint_parts_workspace_bytes",
@@ -751,7 +752,7 @@ def evaluate_factorized_schedule(block_values, schedule):
 
 
 def _jit_cache_dir():
-    """Code objects of generated kernels, keyed by source hash: ``YE3T_AMD_JIT_CACHE``,
+    """Code objects of generated kernels, keyed by ``rtc_cache_key``: ``YE3T_AMD_JIT_CACHE``,
     else ``jit_cache/`` beside this package (built ahead with
     ``python -m ye3t_amd.ace.prebuild`` it travels with the tree), else a
     temporary directory when the package directory is read-only."""
@@ -768,11 +769,27 @@ def _jit_cache_dir():
     return path
 
 
-def rtc_compile(source, name="ye3t_generated.hip", arch="gfx950"):
-    """Compile HIP source with hipRTC (cached on disk by source hash); returns the code object bytes."""
+def rtc_fingerprint():
+    """hipRTC version, options and ABI version of ``ye3t_hip_rtc_compile``
+    (``ye3t_hip_rtc_fingerprint``): with the source and architecture, what
+    decides a generated code object."""
+    buf = ctypes.create_string_buffer(512)
+    _check(lib().ye3t_hip_rtc_fingerprint(buf, len(buf)), "ye3t_hip_rtc_fingerprint")
+    return buf.value.decode()
+
+
+def rtc_cache_key(source, arch="gfx950"):
+    """Name of a code object in the JIT cache: a hash of the architecture, the
+    compiler fingerprint and the source, so a different hipRTC, option set or
+    ABI never reads another's code object."""
     import hashlib
 
-    key = hashlib.sha256((arch + "\0" + source).encode()).hexdigest()[:24]
+    return hashlib.sha256((arch + "\0" + rtc_fingerprint() + "\0" + source).encode()).hexdigest()[:24]
+
+
+def rtc_compile(source, name="ye3t_generated.hip", arch="gfx950"):
+    """Compile HIP source with hipRTC (cached on disk under ``rtc_cache_key``); returns the code object bytes."""
+    key = rtc_cache_key(source, arch)
     path = os.path.join(_jit_cache_dir(), key + ".co")
     if os.path.exists(path):
         with open(path, "rb") as fh:
@@ -1160,7 +1177,10 @@ class ProductPlanHandle:
     def adjoint_stream_noalloc(self, A, gB, out, samples=None, columns=False):
         """:meth:`adjoint_stream` through the library's allocation-free entry
         point (partial gradients in its static device scratch; ``out`` must be
-        given).  Calls that overlap on one device race on that scratch."""
+        given).  Calls on one device are serialised by the library (an eager
+        call on another stream waits for the previous call's kernels); a call
+        captured into a graph records its kernels only, so a replay must not
+        overlap other users of the scratch on that device."""
         import torch
 
         want = torch.float64 if self.dtype == "f64" else torch.float32
