@@ -203,7 +203,9 @@ int ye3t_hip_symmetric_power_shared_monomial_adjoint(int dtype, const void* outp
  * (monomial_count = t range, support_count = q range), and
  * S[b, o] = sum_{k in [output_offsets[o], output_offsets[o+1])} coefficient_values[k] * monomial_{coefficient_terms[k]}.
  * Every table index must be in range and every exponent positive (checked on
- * the host by the Python layer).  Replaces
+ * the host by the Python layer).  dtype YE3T_F32, YE3T_F64, YE3T_C64 or
+ * YE3T_C128 (input, coefficients and outputs alike; complex as (re, im)
+ * pairs), as the reference dispatches floating and complex types.  Replaces
  * ye3t_runtime::symmetric_power_shared_sparse_monomial (schema
  * execution_plan_torch.cpp:7562-7567; CUDA execution_plan_cuda.cu:11012-11104). */
 int ye3t_hip_symmetric_power_shared_sparse_monomial(int dtype, const void* input, int64_t batch, int64_t input_dim,
@@ -216,7 +218,9 @@ int ye3t_hip_symmetric_power_shared_sparse_monomial(int dtype, const void* input
 
 /* input_adjoint[b, c] of the sparse shared form: zero factors add their
  * exponents into a zero degree; degree one gives the cofactor, a higher degree
- * nothing (execution_plan_cuda.cu:5757-5813).  Replaces
+ * nothing (execution_plan_cuda.cu:5757-5813).  For complex data each
+ * contribution is g * conj(coefficient) * conj(derivative), the reference's
+ * conjugate-transpose rule (:6002-6033).  Replaces
  * ye3t_runtime::symmetric_power_shared_sparse_monomial_adjoint (schema
  * execution_plan_torch.cpp:7568-7573; CUDA :11106-11204). */
 int ye3t_hip_symmetric_power_shared_sparse_monomial_adjoint(
@@ -229,7 +233,8 @@ int ye3t_hip_symmetric_power_shared_sparse_monomial_adjoint(
 /* Second order of the sparse shared form along input_adjoint_tangent v:
  * output_tangent[b, o] = d S[b, o] . v, input_tangent[b, c] = sum over
  * coefficients of output_adjoint[b, o] value_k (Hessian of the monomial) v
- * (execution_plan_cuda.cu:5815-5955).  Replaces
+ * (execution_plan_cuda.cu:5815-5955); for complex data
+ * output_adjoint * conj(value_k) * conj(Hessian . v).  Replaces
  * ye3t_runtime::symmetric_power_shared_sparse_monomial_double_backward (schema
  * execution_plan_torch.cpp:7574-7580; CUDA :11206-11330). */
 int ye3t_hip_symmetric_power_shared_sparse_monomial_double_backward(

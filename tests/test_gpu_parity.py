@@ -506,6 +506,42 @@ def test_parts_product_adjoint(gpu, cid, dtype, accumulate, samples, tol):
     assert torch.equal(blocked, gA)
 
 
+@pytest.fixture(scope="module")
+def config3_plan():
+    from ye3t_amd.ace.plan import ProductPlan
+
+    flush("building the config-3 product plan on the host (about a minute)")
+    return ProductPlan(W.config(3).feature_spec)
+
+
+@pytest.mark.parametrize("dtype,tol", [("f64", 1e-12), ("f32", 2e-5)])
+def test_config3_adjoint_runs_in_parts(gpu, config3_plan, dtype, tol):
+    """The benchmark's own config-3 plan with the kernel chosen automatically
+    takes its reverse mode in parts (the default chunk sizes, precompiled),
+    matches the oracle's reverse mode, and gives the same bits in small sample
+    blocks."""
+    import torch
+
+    flush(f"config-3 adjoint in parts, {dtype}")
+    pipe = ACEPipeline(W.config(3).feature_spec, dtype, plan=config3_plan)
+    assert pipe.kernel == "parts"
+    real = torch.float64 if dtype == "f64" else torch.float32
+    rng = np.random.default_rng(53)
+    samples = 130
+    A = torch.as_tensor(rng.normal(size=(samples, pipe.plan.a_width)), dtype=real).to(gpu)
+    gB = torch.as_tensor(rng.normal(size=(samples, pipe.feature_count)), dtype=real).to(gpu)
+    gA = pipe.product_adjoint(A, gB)
+    assert pipe.last_adjoint_backend == "parts"
+    ref = oracle.ace_product_flat_adjoint(A.double().cpu().numpy(), gB.double().cpu().numpy(),
+                                          pipe.plan.flat_arrays())
+    err = column_rel_error(gA.cpu().double().numpy(), ref)
+    flush(f"  err {err:.3e}")
+    assert err < tol
+    elem = 8 if dtype == "f64" else 4
+    blocked = pipe._adjoint_parts(A, gB, None, block_bytes=pipe._adjoint_rows * elem * 64)
+    assert torch.equal(blocked, gA)
+
+
 def test_product_adjoint_needs_a_term_stream(gpu, monkeypatch):
     """A workspace too wide for the term stream has no device adjoint; one whose
     forward stream fits 64 KB of LDS but whose reverse mode (values and

@@ -14,6 +14,51 @@
 namespace ye3t {
 namespace {
 
+// Complex scalar of the sparse kernels (YE3T_C64 / YE3T_C128: interleaved
+// (re, im) pairs, as torch stores complex tensors), with the arithmetic the
+// kernels use.  Division is Smith's algorithm (R. L. Smith, "Algorithm 116:
+// Complex division", CACM 5(8), 1962): the larger of |c| and |d| scales the
+// denominator, so no intermediate overflows for finite operands.
+template <typename R>
+struct cplx {
+  R re, im;
+  cplx() = default;
+  __device__ constexpr cplx(R r, R i) : re(r), im(i) {}
+  __device__ constexpr cplx(int v) : re(R(v)), im(R(0)) {}
+  __device__ constexpr cplx(int64_t v) : re(R(v)), im(R(0)) {}
+};
+template <typename R>
+__device__ inline cplx<R> operator+(cplx<R> a, cplx<R> b) { return {a.re + b.re, a.im + b.im}; }
+template <typename R>
+__device__ inline cplx<R> operator-(cplx<R> a, cplx<R> b) { return {a.re - b.re, a.im - b.im}; }
+template <typename R>
+__device__ inline cplx<R> operator*(cplx<R> a, cplx<R> b) {
+  return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re};
+}
+template <typename R>
+__device__ inline cplx<R> operator/(cplx<R> a, cplx<R> b) {
+  if (fabs(b.re) >= fabs(b.im)) {
+    const R t = b.im / b.re, s = R(1) / (b.re + b.im * t);
+    return {(a.re + a.im * t) * s, (a.im - a.re * t) * s};
+  }
+  const R t = b.re / b.im, s = R(1) / (b.im + b.re * t);
+  return {(a.re * t + a.im) * s, (a.im * t - a.re) * s};
+}
+template <typename R>
+__device__ inline cplx<R>& operator+=(cplx<R>& a, cplx<R> b) { return a = a + b; }
+template <typename R>
+__device__ inline cplx<R>& operator*=(cplx<R>& a, cplx<R> b) { return a = a * b; }
+template <typename R>
+__device__ inline bool operator==(cplx<R> a, cplx<R> b) { return a.re == b.re && a.im == b.im; }
+
+// conjugate (the identity for real scalars): the adjoints multiply by the
+// conjugates of coefficients and derivatives, as the reference's complex
+// kernels do (execution_plan_cuda.cu:5757-5955, 6002-6033)
+template <typename Real>
+__device__ inline Real conjv(Real a) { return a; }
+template <typename R>
+__device__ inline cplx<R> conjv(cplx<R> a) { return {a.re, -a.im}; }
+
 // integer_power of the reference core (ye3t_runtime_core.cpp:98-110): square and multiply
 template <typename Real>
 __device__ inline Real ipow(Real b, int64_t e) {
@@ -218,12 +263,13 @@ __global__ __launch_bounds__(256) void sparse_monomial_adjoint_kernel(
       const Real g = gout[b * O + o];
       for (int64_t k = offsets[o]; k < offsets[o + 1]; ++k) {
         const int64_t t = terms[k];
-        const Real w = g * values[k];
+        const Real w = g * conjv(values[k]);
         const SparseFactors<Real> f = sparse_factors(row, toff, comp, ex, t);
         if (f.zdeg == 1) {
-          grad[f.z1] += w * f.mono;
+          grad[f.z1] += w * conjv(f.mono);
         } else if (f.zdeg == 0) {
-          for (int64_t q = toff[t]; q < toff[t + 1]; ++q) grad[comp[q]] += w * (Real(ex[q]) * f.mono / row[comp[q]]);
+          for (int64_t q = toff[t]; q < toff[t + 1]; ++q)
+            grad[comp[q]] += w * conjv(Real(ex[q]) * f.mono / row[comp[q]]);
         }
       }
     }
@@ -280,14 +326,14 @@ __global__ __launch_bounds__(256) void sparse_monomial_hessian_kernel(
       const Real g = gout[b * O + o];
       for (int64_t k = offsets[o]; k < offsets[o + 1]; ++k) {
         const int64_t t = terms[k];
-        const Real w = g * values[k];
+        const Real w = g * conjv(values[k]);
         const SparseFactors<Real> f = sparse_factors(row, toff, comp, ex, t);
         if (f.zdeg == 0) {
           Real logdir = Real(0);
           for (int64_t q = toff[t]; q < toff[t + 1]; ++q) logdir += Real(ex[q]) * v[comp[q]] / row[comp[q]];
           for (int64_t q = toff[t]; q < toff[t + 1]; ++q) {
             const int64_t c = comp[q];
-            it[c] += w * (Real(ex[q]) * f.mono / row[c] * (logdir - v[c] / row[c]));
+            it[c] += w * conjv(Real(ex[q]) * f.mono / row[c] * (logdir - v[c] / row[c]));
           }
         } else if (f.zdeg == 1) {
           Real zdir = Real(0);
@@ -296,15 +342,15 @@ __global__ __launch_bounds__(256) void sparse_monomial_hessian_kernel(
             if (c == f.z1) continue;
             const Real d = Real(ex[q]) * f.mono / row[c];
             zdir += v[c] * d;
-            it[c] += w * (v[f.z1] * d);
+            it[c] += w * conjv(v[f.z1] * d);
           }
-          it[f.z1] += w * zdir;
+          it[f.z1] += w * conjv(zdir);
         } else if (f.zdeg == 2) {
           if (f.z2 < 0) {
-            it[f.z1] += w * (Real(2) * f.mono * v[f.z1]);
+            it[f.z1] += w * conjv(Real(2) * f.mono * v[f.z1]);
           } else {
-            it[f.z1] += w * (f.mono * v[f.z2]);
-            it[f.z2] += w * (f.mono * v[f.z1]);
+            it[f.z1] += w * conjv(f.mono * v[f.z2]);
+            it[f.z2] += w * conjv(f.mono * v[f.z1]);
           }
         }
       }
@@ -423,6 +469,12 @@ int ye3t_hip_symmetric_power_shared_monomial_adjoint(int dtype, const void* outp
     } else if (dtype == YE3T_F32) {                                                                        \
       using Real = float;                                                                                  \
       hipLaunchKernelGGL(KERNEL<float>, dim3(GRID), dim3(256), 0, as_stream(stream), __VA_ARGS__);         \
+    } else if (dtype == YE3T_C128) {                                                                       \
+      using Real = cplx<double>;                                                                           \
+      hipLaunchKernelGGL(KERNEL<Real>, dim3(GRID), dim3(256), 0, as_stream(stream), __VA_ARGS__);          \
+    } else if (dtype == YE3T_C64) {                                                                        \
+      using Real = cplx<float>;                                                                            \
+      hipLaunchKernelGGL(KERNEL<Real>, dim3(GRID), dim3(256), 0, as_stream(stream), __VA_ARGS__);          \
     } else {                                                                                               \
       return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);                                        \
     }                                                                                                      \

@@ -514,6 +514,11 @@ def __getattr__(name):
         from ye3t_amd.runtime.execution_plan import ExecutionPlan
 
         return ExecutionPlan
+    if name in ("YE3THierarchicalRepeatedBlockModule", "YE3THierarchicalRepeatedBlockModuleGroup",
+                "symmetric_power_product_plan_contraction", "symmetric_power_product_plan_table_report"):
+        import importlib
+
+        return getattr(importlib.import_module("ye3t_amd.runtime.hierarchical"), name)
     raise AttributeError(name)
 
 

@@ -655,12 +655,92 @@ def _sparse_call(fn_name, x, tables, *tensors_before, outputs):
     dt, dc, de = _dev_i64(toff, x.device), _dev_i64(comp, x.device), _dev_i64(ex, x.device)
     do, dk = _dev_i64(offs, x.device), _dev_i64(terms, x.device)
     B, D = (int(s) for s in x.shape)
-    args = [_dtype_code(x), *[_dev(t, "tensor") for t in tensors_before], _dev(x, "input"), B, D,
+    args = [_any_dtype_code(x.dtype), *[_dev(t, "tensor") for t in tensors_before], _dev(x, "input"), B, D,
             _dev(dt, "term_offsets"), _dev(dc, "term_components") if S else None,
             _dev(de, "term_exponents") if S else None, M, S, _dev(do, "output_offsets"),
             _dev(dk, "coefficient_terms") if C else None, _dev(dv, "coefficient_values") if C else None, C, O,
             *[_dev(t, "output") if t.numel() else None for t in outputs], _stream()]
     _check(getattr(lib(), fn_name)(*args), fn_name)
+
+
+class SparseMonomialTable:
+    """A sparse shared monomial table validated once (``check_sparse_table``)
+    and resident on one device in one dtype (real or complex), for callers
+    that apply it many times (the hierarchical runtime's block powers)."""
+
+    def __init__(self, D, term_offsets, term_components, term_exponents, output_offsets, coefficient_terms,
+                 coefficient_outputs, coefficient_values, device, dtype):
+        import torch
+
+        toff, comp, ex, offs, terms = check_sparse_table(D, term_offsets, term_components, term_exponents,
+                                                         output_offsets, coefficient_terms, coefficient_outputs,
+                                                         coefficient_values)
+        self.D = int(D)
+        self.M, self.S, self.C, self.O = int(toff.size - 1), int(comp.size), int(terms.size), int(offs.size - 1)
+        self.dtype = dtype
+        self.code = _any_dtype_code(dtype)
+        self.term_offsets = _dev_i64(toff, device)
+        self.term_components = _dev_i64(comp, device)
+        self.term_exponents = _dev_i64(ex, device)
+        self.output_offsets = _dev_i64(offs, device)
+        self.coefficient_terms = _dev_i64(terms, device)
+        self.coefficient_values = torch.as_tensor(_host_real(coefficient_values)).to(device=device,
+                                                                                     dtype=dtype).contiguous()
+
+    def _args(self):
+        return (_dev(self.term_offsets, "term_offsets"),
+                _dev(self.term_components, "term_components") if self.S else None,
+                _dev(self.term_exponents, "term_exponents") if self.S else None, self.M, self.S,
+                _dev(self.output_offsets, "output_offsets"),
+                _dev(self.coefficient_terms, "coefficient_terms") if self.C else None,
+                _dev(self.coefficient_values, "coefficient_values") if self.C else None, self.C, self.O)
+
+    def _rows(self, x):
+        if x.dtype != self.dtype or x.ndim != 2 or int(x.shape[1]) != self.D:
+            raise ValueError(f"input must be [batch, {self.D}] of {self.dtype}")
+        return int(x.shape[0])
+
+    def forward(self, x):
+        import torch
+
+        B = self._rows(x)
+        out = torch.empty((B, self.O), dtype=self.dtype, device=x.device)
+        if B * self.O:
+            _check(lib().ye3t_hip_symmetric_power_shared_sparse_monomial(
+                self.code, _dev(x, "input"), B, self.D, *self._args(), _dev(out, "output"), _stream()),
+                "ye3t_hip_symmetric_power_shared_sparse_monomial")
+        return out
+
+    def adjoint(self, g, x):
+        import torch
+
+        B = self._rows(x)
+        if g.dtype != self.dtype or tuple(g.shape) != (B, self.O):
+            raise ValueError("output_adjoint must match the table's outputs and dtype")
+        out = torch.empty_like(x)
+        if B * self.D:
+            _check(lib().ye3t_hip_symmetric_power_shared_sparse_monomial_adjoint(
+                self.code, _dev(g, "output_adjoint") if self.O else None, _dev(x, "input"), B, self.D,
+                *self._args(), _dev(out, "input_adjoint"), _stream()),
+                "ye3t_hip_symmetric_power_shared_sparse_monomial_adjoint")
+        return out
+
+    def double_backward(self, v, g, x):
+        import torch
+
+        B = self._rows(x)
+        if v.dtype != self.dtype or tuple(v.shape) != (B, self.D):
+            raise ValueError("input_adjoint_tangent must match the input")
+        if g.dtype != self.dtype or tuple(g.shape) != (B, self.O):
+            raise ValueError("output_adjoint must match the table's outputs and dtype")
+        out_t, in_t = torch.empty_like(g), torch.empty_like(x)
+        if B:
+            _check(lib().ye3t_hip_symmetric_power_shared_sparse_monomial_double_backward(
+                self.code, _dev(v, "input_adjoint_tangent") if self.D else None,
+                _dev(g, "output_adjoint") if self.O else None, _dev(x, "input"), B, self.D, *self._args(),
+                _dev(out_t, "output_tangent") if self.O else None, _dev(in_t, "input_tangent") if self.D else None,
+                _stream()), "ye3t_hip_symmetric_power_shared_sparse_monomial_double_backward")
+        return out_t, in_t
 
 
 def _sparse_tables(D, term_offsets, term_components, term_exponents, output_offsets, coefficient_terms,
