@@ -303,10 +303,12 @@ def test_interpreter_column_major_density(gpu, cid, dtype, samples, max_slots):
     assert err < TOL[dtype]
 
 
-def test_parts_and_interpreter_agree_on_config2(gpu):
+def test_parts_and_interpreter_agree_on_config2(gpu, monkeypatch):
     """Config 2's full plan (16 810 terms) at its full 10 000 samples: the
     generated kernel in parts (the default for this plan size) against the
-    term-stream interpreter, and against the flat oracle on a slice."""
+    term-stream interpreter, and against the flat oracle on a slice; the parts
+    run in sample blocks of 512 (YE3T_PARTS_BLOCK_MB=1, 20 blocks, the last
+    ragged) give the same bits as in one block."""
     flush("generated parts vs interpreter, config 2 full sample count")
     import torch
 
@@ -324,6 +326,9 @@ def test_parts_and_interpreter_agree_on_config2(gpu):
     assert err < TOL["f64"]
     ref = oracle.ace_product_flat(A[:96].cpu().numpy(), pipe.plan.flat_arrays())
     assert column_rel_error(B_parts[:96].cpu().numpy(), ref) < TOL["f64"]
+    monkeypatch.setenv("YE3T_PARTS_BLOCK_MB", "1")
+    assert torch.equal(pipe.product(A), B_parts)
+    assert torch.equal(pipe.product(A[:1000]), B_parts[:1000])
 
 
 def test_generated_and_interpreter_agree_on_config4(gpu):

@@ -1392,30 +1392,62 @@ int ye3t_hip_transpose(int dtype, const void* A, int64_t rows, int64_t cols, voi
   return check_launch("transpose_kernel");
 }
 
+// Samples per block of part launches (tuning; off by default): with
+// YE3T_PARTS_BLOCK_MB = m > 0 every part runs over one block of samples whose
+// density rows take at most m MiB before any part starts the next block, so
+// the parts after the first could re-read those rows from the device's
+// last-level cache.  Measured at config 5 (28 parts, 200 000 samples): one
+// block 113 ms, 192 MiB blocks 125 ms, 96 MiB 133 ms, 32 MiB 197 ms -- the
+// smaller launches cost more than the reuse saves.  Blocks hold whole
+// 64-sample tiles in multiples of 8 (one per XCD).
+static int64_t part_block_samples(const ye3t_hip_product_plan* p, int64_t samples) {
+  const char* env = std::getenv("YE3T_PARTS_BLOCK_MB");
+  const int64_t mb = (env && *env) ? std::atoll(env) : 0;
+  if (mb <= 0) return samples;
+  const int64_t row = p->a_width * (p->in_dtype == YE3T_F64 ? 8 : 4);
+  int64_t block = (mb << 20) / (row > 0 ? row : 1);
+  block = block / (8 * kLanes) * (8 * kLanes);
+  if (block < 8 * kLanes) block = 8 * kLanes;
+  return block < samples ? block : samples;
+}
+
 // the generated kernel in parts, in order: density value (s, k) at A[s * row_stride + k * col_stride]
 static int launch_parts(const ye3t_hip_product_plan* p, const void* A, int64_t row_stride, int64_t col_stride,
                         int64_t samples, void* B, hipStream_t stream) {
+  const int64_t block = part_block_samples(p, samples);
   // a multiple of 8 tile columns: the parts deal tiles to XCDs by linear workgroup id
-  const int64_t tiles = ((samples + kLanes - 1) / kLanes + 7) & ~int64_t(7);
-  YE3T_REQUIRE(tiles <= int64_t(0x7FFFFFF8), "too many samples for one launch");
-  long s_arg = long(samples), rs_arg = long(row_stride), cs_arg = long(col_stride);
-  const void* a_arg = A;
-  void* b_arg = B;
-  void* args[] = {&a_arg, &s_arg, &b_arg, &rs_arg, &cs_arg};
+  const int64_t max_tiles = ((block + kLanes - 1) / kLanes + 7) & ~int64_t(7);
+  YE3T_REQUIRE(max_tiles <= int64_t(0x7FFFFFF8), "too many samples for one launch");
+  const size_t a_elem = p->in_dtype == YE3T_F64 ? 8 : 4, b_elem = p->out_dtype == YE3T_F64 ? 8 : 4;
+  long rs_arg = long(row_stride), cs_arg = long(col_stride);
   const int lanes = p->part_lanes;
-  if (lanes <= 1) {
+  // launches every part over samples [s0, s0 + n)
+  auto launch_block = [&](int64_t s0, int64_t n, bool on_lanes) -> int {
+    const int64_t tiles = ((n + kLanes - 1) / kLanes + 7) & ~int64_t(7);
+    long s_arg = long(n);
+    const void* a_arg = static_cast<const unsigned char*>(A) + size_t(s0 * row_stride) * a_elem;
+    void* b_arg = static_cast<unsigned char*>(B) + size_t(s0) * size_t(p->feature_count) * b_elem;
+    void* args[] = {&a_arg, &s_arg, &b_arg, &rs_arg, &cs_arg};
     for (int64_t i = 0; i < p->part_count; ++i)
       YE3T_CHECK_HIP(hipModuleLaunchKernel(p->part_fns[i], unsigned(tiles), unsigned(p->part_chunks[i]), 1, kLanes,
-                                           1, 1, 0, stream, args, nullptr));
+                                           1, 1, 0, on_lanes ? p->part_streams[i % lanes] : stream, args, nullptr));
+    return YE3T_OK;
+  };
+  if (lanes <= 1) {
+    for (int64_t s0 = 0; s0 < samples; s0 += block) {
+      const int rc = launch_block(s0, std::min(block, samples - s0), false);
+      if (rc != YE3T_OK) return rc;
+    }
     return YE3T_OK;
   }
   // fork: the plan's streams start after the caller's prior work; join: the
   // caller's stream continues after every part
   YE3T_CHECK_HIP(hipEventRecord(p->part_fork, stream));
   for (int k = 0; k < lanes; ++k) YE3T_CHECK_HIP(hipStreamWaitEvent(p->part_streams[k], p->part_fork, 0));
-  for (int64_t i = 0; i < p->part_count; ++i)
-    YE3T_CHECK_HIP(hipModuleLaunchKernel(p->part_fns[i], unsigned(tiles), unsigned(p->part_chunks[i]), 1, kLanes,
-                                         1, 1, 0, p->part_streams[i % lanes], args, nullptr));
+  for (int64_t s0 = 0; s0 < samples; s0 += block) {
+    const int rc = launch_block(s0, std::min(block, samples - s0), true);
+    if (rc != YE3T_OK) return rc;
+  }
   for (int k = 0; k < lanes; ++k) {
     YE3T_CHECK_HIP(hipEventRecord(p->part_join[k], p->part_streams[k]));
     YE3T_CHECK_HIP(hipStreamWaitEvent(stream, p->part_join[k], 0));
