@@ -745,10 +745,11 @@ int ye3t_hip_product_adjoint_stream_noalloc(const ye3t_hip_product_plan* plan, c
                                             int columns, const void* gB, int64_t samples, void* gA,
                                             ye3t_stream_t stream);
 
-/* 1 if the plan's interpreter is the term stream (LDS-staged records; the
- * plan also accepts ye3t_hip_product_forward_columns), 0 for the program-word
- * interpreter (workspaces too wide for the stream's 16-bit offsets or 64 KB of
- * LDS).  No reference counterpart. */
+/* 1 if the plan's interpreter is the term stream (workspace in LDS, records
+ * and flags read through the scalar cache, column loads and output slots
+ * staged in LDS; the plan also accepts ye3t_hip_product_forward_columns), 0 for
+ * the program-word interpreter (workspaces too wide for the stream's 16-bit
+ * offsets or 64 KB of LDS).  No reference counterpart. */
 int ye3t_hip_product_plan_uses_stream(const ye3t_hip_product_plan* plan);
 
 /* Kernel name/launch geometry of the last product_forward (for profiling). */
