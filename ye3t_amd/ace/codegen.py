@@ -20,6 +20,7 @@ from ye3t_amd.ace.program import _closure
 
 GROUP = 32  # output columns staged per flush
 CHAINS = 4  # independent partial sums per output component (persistent kernel)
+STORE_BATCH = 16  # staged elements read from LDS ahead of their stores (generated parts)
 
 
 def _ctype(dtype):
@@ -592,6 +593,8 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     w(f"#define REAL {real}")
     w(f"#define OUT {outt}")
     w(f"#define AIN {_ctype(in_dtype)}")
+    if strided:
+        w("typedef unsigned v2u __attribute__((ext_vector_type(2)));")
     w(f"extern \"C\" __global__ __launch_bounds__(64) void {kernel_name}(")
     if strided:
         # density value (s, k) at A[s * row_stride + k * col_stride]: rows (a_width, 1) or columns (1, ld)
@@ -625,7 +628,15 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
     w("  const long s = s0 + lane;")
     w(f"  const bool valid = lane < {R} && s < samples;")
     if strided:
-        w("  const AIN* __restrict__ a = A + (valid ? s : 0) * row_stride;")
+        # wave-uniform tile bases and 32-bit byte offsets of the lane (the host
+        # keeps 63 * row_stride elements and a tile of B below 4 GiB): a density
+        # load is one global_load from the column's address in SGPRs plus the
+        # lane's offset, a store likewise, with no 64-bit address arithmetic
+        w("  const char* __restrict__ at = (const char*)(A + s0 * row_stride);")
+        w("  const long cs = col_stride * (long)sizeof(AIN);")
+        w("  const unsigned alane = (unsigned)(valid ? lane : 0) * (unsigned)(row_stride * (long)sizeof(AIN));")
+        w(f"  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)(B + s0 * {F}L), (short)0, "
+          f"{64 * F * (8 if out_dtype == 'f64' else 4)}, 0x00020000);")
     else:
         w(f"  const AIN* __restrict__ a = A + (valid ? s : 0) * {plan.a_width}L;")
     w("  const long rem = samples - s0;")
@@ -638,7 +649,8 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
         # unconditional loads: lanes past the last sample read sample 0 (a valid
         # address) and their outputs are never stored; a select per load would
         # turn each into a branch that waits for its own data
-        leaf = (lambda c: f"(REAL)a[{c}L * col_stride]") if strided else (lambda c: f"(REAL)a[{c}]")
+        leaf = ((lambda c: f"(REAL)*(const AIN*)(at + {c}L * cs + alane)") if strided
+                else (lambda c: f"(REAL)a[{c}]"))
 
         def emit(n):
             _emit_one_chain(w, nodes, n, emitted, dtype, leaf)
@@ -668,10 +680,47 @@ def generate(plan, dtype="f32", max_live=None, kernel_name="ye3t_product_generat
                 w(f"    st[{f - g0}][lane] = (OUT)v{root}_{comp};")
             width = g1 - g0
             w("    __syncthreads();")
+            if strided:
+                # a full tile: the [64, width] block as `width` stores of 64
+                # consecutive row-major elements, LDS reads issued in batches
+                # ahead of their stores (no loop, no wait per element)
+                out_elem = 8 if out_dtype == "f64" else 4
+                if out_elem == 8:
+                    store = "__builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, {v}), rb, {vo}, {so}, 0);"
+                else:
+                    store = "__builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, {v}), rb, {vo}, {so}, 0);"
+                w("    if (rows == 64) {")
+                if 64 % width == 0:
+                    # store k covers rows r0 + k * 64 / width: constant LDS
+                    # offsets and a constant scalar offset into B's tile
+                    step = 64 // width
+                    w(f"      const int r0 = lane / {width}, c0 = lane - r0 * {width};")
+                    w("      const OUT* sp = &st[c0][r0];")
+                    w(f"      const unsigned u0 = (unsigned)(r0 * {F} + {g0} + c0) * {out_elem}u;")
+                for b0 in range(0, width, STORE_BATCH):
+                    b1 = min(b0 + STORE_BATCH, width)
+                    w("    {")
+                    for k in range(b0, b1):
+                        if 64 % width == 0:
+                            w(f"      const OUT o{k} = sp[{k * step}];")
+                        else:
+                            w(f"      const int i{k} = lane + {64 * k}, r{k} = i{k} / {width}, "
+                              f"c{k} = i{k} - r{k} * {width};")
+                            w(f"      const OUT o{k} = st[c{k}][r{k}];")
+                    for k in range(b0, b1):
+                        if 64 % width == 0:
+                            w("      " + store.format(v=f"o{k}", vo="u0", so=f"{k * step * F * out_elem}"))
+                        else:
+                            w("      " + store.format(v=f"o{k}", vo=f"(unsigned)(r{k} * {F} + {g0} + c{k}) * {out_elem}u",
+                                                      so="0"))
+                    w("    }")
+                w("    } else {")
             w(f"    for (int i = lane; i < rows * {width}; i += 64) {{")
             w(f"      const int r = i / {width}, c = i - r * {width};")
             w(f"      B[(s0 + r) * {F}L + {g0} + c] = st[c][r];")
             w("    }")
+            if strided:
+                w("    }")
             w("    __syncthreads();")
         w("    break;")
         w("  }")
@@ -738,6 +787,8 @@ def generate_parts(plan, dtype="f64", max_live=None, chunks_per_part=None, out_d
     chunks_per_part = chunks_per_part or part_chunks(plan)
     if chunks_per_part < 1:
         raise ValueError("chunks_per_part must be positive")
+    if 64 * plan.feature_count * (8 if (out_dtype or dtype) == "f64" else 4) >= 1 << 32:
+        raise ValueError("a 64-sample tile of B must stay below 4 GiB for the generated parts")
     max_live = max_live or part_max_live(plan, dtype)
     chunks = _chunks(plan, max_live)
     parts = []

@@ -1419,6 +1419,11 @@ static int launch_parts(const ye3t_hip_product_plan* p, const void* A, int64_t r
   const int64_t max_tiles = ((block + kLanes - 1) / kLanes + 7) & ~int64_t(7);
   YE3T_REQUIRE(max_tiles <= int64_t(0x7FFFFFF8), "too many samples for one launch");
   const size_t a_elem = p->in_dtype == YE3T_F64 ? 8 : 4, b_elem = p->out_dtype == YE3T_F64 ? 8 : 4;
+  // the parts address a lane's density values and a tile of B with 32-bit byte offsets
+  YE3T_REQUIRE(row_stride >= 0 && col_stride >= 0 && uint64_t(63 * row_stride) * a_elem < (uint64_t(1) << 32),
+               "density rows too wide for the generated parts");
+  YE3T_REQUIRE(uint64_t(64) * uint64_t(p->feature_count) * b_elem < (uint64_t(1) << 32),
+               "feature rows too wide for the generated parts");
   long rs_arg = long(row_stride), cs_arg = long(col_stride);
   const int lanes = p->part_lanes;
   // launches every part over samples [s0, s0 + n)
