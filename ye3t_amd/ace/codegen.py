@@ -41,22 +41,35 @@ def _lit(value, dtype):
     return repr(float(value)) + "f"
 
 
-def _chunks(plan, max_live):
+def _chunks(plan, max_live, align=1):
+    """``[(first, last, nodes)]``: consecutive output ranges whose node closures
+    hold at most ``max_live`` values (one output may exceed it alone).  With
+    ``align`` > 1 every range but the last ends on a multiple of ``align``
+    outputs where that leaves it non-empty (the outputs past that multiple
+    start the next range), so ranges of B columns meet on cache-line
+    boundaries."""
     nodes = plan.nodes
+    outs = plan.outputs
     chunks = []
-    cur, first, cost = set(), 0, 0
-    for f, (root, _c) in enumerate(plan.outputs):
-        need = _closure(nodes, root, set())
-        new = need - cur
-        add = sum(nodes[n]["dim"] for n in new)
-        if cur and cost + add > max_live:
-            chunks.append((first, f, cur))
-            cur, first, cost = set(), f, 0
-            new = need
+    first = 0
+    while first < len(outs):
+        cur, cost, f = set(), 0, first
+        while f < len(outs):
+            new = _closure(nodes, outs[f][0], set()) - cur
             add = sum(nodes[n]["dim"] for n in new)
-        cur |= new
-        cost += add
-    chunks.append((first, len(plan.outputs), cur))
+            if cur and cost + add > max_live:
+                break
+            cur |= new
+            cost += add
+            f += 1
+        cut = f - f % align
+        if f < len(outs) and first < cut < f:
+            f = cut
+            cur = set()
+            for g in range(first, f):
+                cur |= _closure(nodes, outs[g][0], set())
+        chunks.append((first, f, cur))
+        first = f
     return chunks
 
 
@@ -790,7 +803,13 @@ def generate_parts(plan, dtype="f64", max_live=None, chunks_per_part=None, out_d
     if 64 * plan.feature_count * (8 if (out_dtype or dtype) == "f64" else 4) >= 1 << 32:
         raise ValueError("a 64-sample tile of B must stay below 4 GiB for the generated parts")
     max_live = max_live or part_max_live(plan, dtype)
-    chunks = _chunks(plan, max_live)
+    # where every row of B starts on a 128-byte line, chunks end on line
+    # boundaries: no line of B is then written in part by two workgroups
+    # (config 3 fp64 stage 2 2.49 -> 1.87 ms, fp32 1.31 -> 0.99 ms, with 18 %
+    # more chunks)
+    out_elem = 8 if (out_dtype or dtype) == "f64" else 4
+    align = 128 // out_elem if (plan.feature_count * out_elem) % 128 == 0 else 1
+    chunks = _chunks(plan, max_live, align)
     parts = []
     for i in range(0, len(chunks), chunks_per_part):
         parts.append(generate(plan, dtype, max_live, kernel_name="ye3t_product_part", out_dtype=out_dtype,
