@@ -11,7 +11,8 @@ GPU needed) and check:
   array indexed at run time, and none) and against malformed input;
 * that the default chunk sizes of config 2 (forward, reverse mode and readout
   parts) stay within the bound;
-* that the chunk-size knobs refuse values above 400.
+* that the chunk-size knobs refuse values above 400;
+* that parts above the bound are regenerated in smaller chunks.
 """
 
 import pytest
@@ -107,3 +108,23 @@ def test_attach_refuses_a_part_above_the_bound(gpu):
         assert b"scratch per lane" in lib.ye3t_hip_last_error()
     A = torch.zeros((64, pipe.plan.a_width), dtype=torch.float32, device=gpu)
     assert torch.equal(pipe.product(A), torch.zeros((64, pipe.feature_count), dtype=torch.float32, device=gpu))
+
+
+def test_parts_above_the_bound_are_regenerated_in_smaller_chunks():
+    """``fit_parts_to_scratch`` steps the node-value budget down until every
+    compiled part is within the bound: here a real kernel of known scratch
+    stands for the parts made at 300 values, a scratch-free one for 250 and
+    below, so the fit settles on 250."""
+    from ye3t_amd.ace.pipeline import PART_LIVE_STEP, fit_parts_to_scratch
+
+    asked = []
+
+    def make(n):
+        asked.append(n)
+        return [(SMALL, {}), (BIG if n > 250 else SMALL, {})]
+
+    parts = fit_parts_to_scratch(make, 300, "probe")
+    assert asked == [300, 300 - PART_LIVE_STEP] and PART_LIVE_STEP == 50
+    assert [src for src, _ in parts] == [SMALL, SMALL]
+    # a budget that cannot get smaller is returned as it is (the attach entry points then refuse it)
+    assert [src for src, _ in fit_parts_to_scratch(lambda n: [(BIG, {})], PART_LIVE_STEP, "probe")] == [BIG]

@@ -824,7 +824,10 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
     ``gA[s] = J(A[s])^T gB[s]`` (counterpart of the reference's
     ``factorized_angular_adjoint``, ``execution_plan_cuda.cu:6361``).
 
-    The chunks and parts are those of :func:`generate_parts`.  For each tile
+    Chunks and parts are formed as in :func:`generate_parts`, without its
+    alignment of chunk ends to lines of B (nothing here writes B), and a
+    feature's emitted code is the forward's, so its value has the same bits
+    however the outputs are chunked.  For each tile
     of 64 samples a chunk recomputes the forward values its outputs depend on
     (density read through row and column strides), loads its outputs'
     gradients from ``gB`` (row segments staged through LDS, ``group`` columns
@@ -981,7 +984,10 @@ def generate_readout_parts(plan, dtype="f64", max_live=None, chunks_per_part=Non
     weight[k]`` without writing B (counterpart of the reference's
     ``factorized_angular_linear``, ``execution_plan.py:13793-13850``).
 
-    The chunks and parts are those of :func:`generate_parts`.  For each tile
+    Chunks and parts are formed as in :func:`generate_parts`, without its
+    alignment of chunk ends to lines of B (nothing here writes B), and a
+    feature's emitted code is the forward's, so its value has the same bits
+    however the outputs are chunked.  For each tile
     of 64 samples a chunk computes its outputs in registers (density through
     row and column strides) and writes ``sum_{k in chunk} weight[k] B[s, k]``
     to row ``chunk`` of a partial buffer ``P[chunk * ldp + s]``; the weights
@@ -1020,13 +1026,17 @@ def generate_readout_parts(plan, dtype="f64", max_live=None, chunks_per_part=Non
         w("  const long s0 = tile * 64;")
         w("  if (s0 >= samples) return;")
         w("  const long s = s0 + lane;")
-        w("  const AIN* __restrict__ a = A + (s < samples ? s : 0) * row_stride;")
+        # density loads as in the forward parts: the column's address in SGPRs
+        # plus the lane's 32-bit byte offset (the host keeps it below 4 GiB)
+        w("  const char* __restrict__ at = (const char*)(A + s0 * row_stride);")
+        w("  const long cs = col_stride * (long)sizeof(AIN);")
+        w("  const unsigned alane = (unsigned)(s < samples ? lane : 0) * (unsigned)(row_stride * (long)sizeof(AIN));")
         w("  switch (chunk) {")
         for lc, ci in enumerate(sub):
             first, last, members = chunks[ci]
             w(f"  case {lc}: {{")
             emitted = set()
-            leaf = lambda c: f"(REAL)a[{c}L * col_stride]"  # noqa: E731
+            leaf = lambda c: f"(REAL)*(const AIN*)(at + {c}L * cs + alane)"  # noqa: E731
             for n in sorted((m for m in members if nodes[m]["kind"] == "leaf"), key=lambda m: nodes[m]["a_offset"]):
                 _emit_one_chain(w, nodes, n, emitted, dtype, leaf, "      ")
             # the chunk's dot product as CHAINS independent partial sums, added in a fixed

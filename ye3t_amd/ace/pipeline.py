@@ -49,6 +49,29 @@ ADJOINT_PARTS_MAX_TERMS = 200000
 # part; config 2 658 / 633 / 634 us)
 ADJOINT_PART_MAX_LIVE = 128
 ADJOINT_PART_CHUNKS = 64
+# node values taken off a chunk when a compiled part needs more scratch than the
+# library runs (config 5's fused readout at 300 values: one part at 1 060 bytes)
+PART_LIVE_STEP = 50
+
+
+def fit_parts_to_scratch(make, live, kernel, compile_all=None):
+    """``make(n)`` for the largest node-value budget ``n`` from ``live`` down,
+    in steps of ``PART_LIVE_STEP``, whose every compiled part (``kernel`` in
+    each code object) needs at most ``native.part_private_limit()`` bytes of
+    scratch per lane; the attach entry points refuse any part above it.
+    ``make(n)`` returns ``[(source, meta), ...]``; ``compile_all(sources)``
+    returns their code objects (default: hipRTC through the JIT cache, one at
+    a time)."""
+    limit = native.part_private_limit()
+    if compile_all is None:
+        compile_all = lambda sources: [native.rtc_compile(src) for src in sources]  # noqa: E731
+    while True:
+        parts = make(live)
+        codes = compile_all([src for src, _meta in parts])
+        worst = max(native.code_object_kernel_info(code, kernel)["private_segment_bytes"] for code in codes)
+        if worst <= limit or live <= PART_LIVE_STEP:
+            return parts
+        live -= PART_LIVE_STEP
 
 
 class ACEPipeline:
@@ -128,9 +151,11 @@ class ACEPipeline:
             live = self._parts_max_live()
             per = int(os.environ.get("YE3T_PARTS_CHUNKS", 0)) or part_chunks(self.plan)
             group = int(os.environ.get("YE3T_PARTS_GROUP", 32))  # output columns per staged store
-            self.handle.attach_generated_parts(generate_parts(self.plan, self.accumulate, max_live=live,
-                                                              chunks_per_part=per, out_dtype=dtype,
-                                                              in_dtype=self.density_dtype, group=group))
+            parts = fit_parts_to_scratch(
+                lambda n: generate_parts(self.plan, self.accumulate, max_live=n, chunks_per_part=per,
+                                         out_dtype=dtype, in_dtype=self.density_dtype, group=group),
+                live, "ye3t_product_part")
+            self.handle.attach_generated_parts(parts)
             self.kernel = "parts"
 
     def _parts_max_live(self):
@@ -304,8 +329,10 @@ class ACEPipeline:
             if getattr(self.handle, "readout_part_meta", None) is None:
                 live = self._parts_max_live()
                 per = int(os.environ.get("YE3T_PARTS_CHUNKS", 0)) or part_chunks(self.plan)
-                parts, _ = generate_readout_parts(self.plan, self.accumulate, max_live=live, chunks_per_part=per,
-                                                  in_dtype=self.density_dtype)
+                parts = fit_parts_to_scratch(
+                    lambda n: generate_readout_parts(self.plan, self.accumulate, max_live=n, chunks_per_part=per,
+                                                     in_dtype=self.density_dtype)[0],
+                    live, "ye3t_product_readout_part")
                 self.handle.attach_readout_parts(parts)
             w = weight.to(torch.float64 if self.accumulate == "f64" else torch.float32).contiguous()
             if S == 0:

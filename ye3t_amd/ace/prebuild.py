@@ -33,15 +33,15 @@ def precisions(cfg, dtype):
 def _compile(source):
     from ye3t_amd.runtime import native
 
-    native.rtc_compile(source)
-    return len(source)
+    return native.rtc_compile(source)
 
 
 def prebuild(config_ids=(2, 3, 5), dtypes=None, workers=None, log=print):
     from ye3t_amd.ace import workloads as W
-    from ye3t_amd.ace.codegen import generate_adjoint_parts, generate_parts, generate_readout_parts
+    from ye3t_amd.ace.codegen import (generate_adjoint_parts, generate_parts, generate_readout_parts, part_chunks,
+                                      part_max_live)
     from ye3t_amd.ace.pipeline import (ADJOINT_PART_CHUNKS, ADJOINT_PART_MAX_LIVE, ADJOINT_PARTS_MAX_TERMS,
-                                       GENERATED_MAX_TERMS, PARTS_MAX_TERMS)
+                                       GENERATED_MAX_TERMS, PARTS_MAX_TERMS, fit_parts_to_scratch)
     from ye3t_amd.ace.plan import ProductPlan
     from ye3t_amd.runtime import native
 
@@ -55,17 +55,26 @@ def prebuild(config_ids=(2, 3, 5), dtypes=None, workers=None, log=print):
             continue
         for dtype in dtypes or cfg.dtypes:
             accumulate, density = precisions(cfg, dtype)
-            parts = generate_parts(plan, accumulate, out_dtype=dtype, in_dtype=density)
-            readout, _ = generate_readout_parts(plan, accumulate, in_dtype=density)
+            live, per = part_max_live(plan, accumulate), part_chunks(plan)
             adjoint = []
             if terms <= ADJOINT_PARTS_MAX_TERMS:
                 adjoint, _ = generate_adjoint_parts(plan, accumulate, max_live=ADJOINT_PART_MAX_LIVE,
                                                     chunks_per_part=ADJOINT_PART_CHUNKS, grad_dtype=dtype,
                                                     in_dtype=density)
             t0 = time.time()
-            # worker processes (spawned: nothing of this process is inherited) compile in parallel
+            # worker processes (spawned: nothing of this process is inherited) compile in parallel;
+            # parts above the library's scratch bound are regenerated in smaller chunks, as the
+            # pipeline does (fit_parts_to_scratch)
             with ProcessPoolExecutor(workers, mp_context=multiprocessing.get_context("spawn")) as pool:
-                list(pool.map(_compile, [part[0] for part in parts + adjoint + readout]))
+                compile_all = lambda sources: list(pool.map(_compile, sources))  # noqa: E731
+                parts = fit_parts_to_scratch(
+                    lambda n: generate_parts(plan, accumulate, max_live=n, chunks_per_part=per, out_dtype=dtype,
+                                             in_dtype=density), live, "ye3t_product_part", compile_all)
+                readout = fit_parts_to_scratch(
+                    lambda n: generate_readout_parts(plan, accumulate, max_live=n, chunks_per_part=per,
+                                                     in_dtype=density)[0], live, "ye3t_product_readout_part",
+                    compile_all)
+                compile_all([part[0] for part in adjoint])
             log(f"config {cid} {dtype} (arithmetic {accumulate}, density {density}): {len(parts)} forward, "
                 f"{len(adjoint)} adjoint and {len(readout)} readout parts in {time.time() - t0:.1f} s "
                 f"-> {native._jit_cache_dir()}")
