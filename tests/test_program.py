@@ -152,7 +152,7 @@ def test_adjoint_parts_reduction_map():
     first = 0
     for src, meta in parts:
         assert meta["first_row"] == first
-        written = sorted(int(r) for r in re.findall(r"P\[(\d+)L \* ldp \+ s\]", src))
+        written = sorted(int(r) for r in re.findall(r"\*\(REAL\*\)\(pt \+ (\d+)L \* pb \+ plane\)", src))
         assert written == list(range(meta["first_row"], meta["last_row"]))
         first = meta["last_row"]
     assert first == red["partial_rows"]

@@ -825,9 +825,7 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
     ``factorized_angular_adjoint``, ``execution_plan_cuda.cu:6361``).
 
     Chunks and parts are formed as in :func:`generate_parts`, without its
-    alignment of chunk ends to lines of B (nothing here writes B), and a
-    feature's emitted code is the forward's, so its value has the same bits
-    however the outputs are chunked.  For each tile
+    alignment of chunk ends to lines of B (nothing here writes B).  For each tile
     of 64 samples a chunk recomputes the forward values its outputs depend on
     (density read through row and column strides), loads its outputs'
     gradients from ``gB`` (row segments staged through LDS, ``group`` columns
@@ -851,6 +849,8 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
         raise ValueError("an f32 plan takes f32 gradients")
     if chunks_per_part < 1:
         raise ValueError("chunks_per_part must be positive")
+    if 64 * plan.feature_count * (8 if grad_dtype == "f64" else 4) >= 1 << 32:
+        raise ValueError("a 64-sample tile of gB must stay below 4 GiB for the adjoint parts")
     real = "double" if dtype == "f64" else "float"
     gt = "double" if grad_dtype == "f64" else "float"
     fma = "fma" if dtype == "f64" else "fmaf"
@@ -881,6 +881,7 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
         w(f"#define REAL {real}")
         w(f"#define GT {gt}")
         w(f"#define AIN {_ctype(in_dtype)}")
+        w("typedef unsigned v2u __attribute__((ext_vector_type(2)));")
         w("extern \"C\" __global__ __launch_bounds__(64) void ye3t_product_adjoint_part(")
         w("    const AIN* __restrict__ A, const GT* __restrict__ gB, long samples, REAL* __restrict__ P,")
         w("    long row_stride, long col_stride, long ldp) {")
@@ -894,7 +895,18 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
         w("  const long s0 = tile * 64;")
         w("  if (s0 >= samples) return;")
         w("  const long s = s0 + lane;")
-        w("  const AIN* __restrict__ a = A + (s < samples ? s : 0) * row_stride;")
+        # scalar bases and 32-bit lane offsets, as in the forward parts: the
+        # density column's address, the tile's rows of gB (a buffer resource)
+        # and the partial row's address sit in SGPRs (the host keeps the
+        # offsets below 4 GiB)
+        w("  const char* __restrict__ at = (const char*)(A + s0 * row_stride);")
+        w("  const long cs = col_stride * (long)sizeof(AIN);")
+        w("  const unsigned alane = (unsigned)(s < samples ? lane : 0) * (unsigned)(row_stride * (long)sizeof(AIN));")
+        w(f"  const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc((void*)(gB + s0 * {F}L), (short)0, "
+          f"{64 * F * (8 if grad_dtype == 'f64' else 4)}, 0x00020000);")
+        w("  char* __restrict__ pt = (char*)(P + s0);")
+        w("  const long pb = ldp * (long)sizeof(REAL);")
+        w("  const unsigned plane = (unsigned)lane * (unsigned)sizeof(REAL);")
         w("  const long rem = samples - s0;")
         w("  const int rows = rem < 64 ? (int)rem : 64;")
         w("  switch (chunk) {")
@@ -902,17 +914,18 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
             first, last, members = chunks[ci]
             w(f"  case {lc}: {{")
             emitted = set()
+            aleaf = lambda c: f"(REAL)*(const AIN*)(at + {c}L * cs + alane)"  # noqa: E731
             # every density value of the chunk, unconditionally (lanes past the
             # last sample read sample 0 and write only partial rows never summed)
             for n in sorted((m for m in members if nodes[m]["kind"] == "leaf"), key=lambda m: nodes[m]["a_offset"]):
-                _emit_node_code(w, nodes, n, emitted, dtype, lambda c: f"(REAL)a[{c}L * col_stride]")
+                _emit_node_code(w, nodes, n, emitted, dtype, aleaf)
             roots = sorted({plan.outputs[f][0] for f in range(first, last)})
             needed = set()
             for r in roots:
                 _closure(nodes, r, needed)
             for r in roots:
                 for d in nodes[r]["deps"]:
-                    _emit_node_code(w, nodes, d, emitted, dtype, lambda c: f"(REAL)a[{c}L * col_stride]")
+                    _emit_node_code(w, nodes, d, emitted, dtype, aleaf)
             for n in sorted(needed):
                 for c in range(nodes[n]["dim"]):
                     w(f"      REAL g{n}_{c} = (REAL)0;")
@@ -925,11 +938,31 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
                 w("      __syncthreads();")
                 w("      {")
                 w(f"        GT t[{width}];")
-                w("#pragma unroll")
-                w(f"        for (int u = 0; u < {width}; ++u) {{")
-                w(f"          const int i = lane + 64 * u, r = i / {width}, c = i - r * {width};")
-                w(f"          t[u] = gB[(s0 + (r < rows ? r : rows - 1)) * {F}L + {g0} + c];")
-                w("        }")
+                gsz = 8 if grad_dtype == "f64" else 4
+                load = ("__builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rg, {vo}, {so}, 0))"
+                        if gsz == 8 else
+                        "__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, {vo}, {so}, 0))")
+                if 64 % width == 0:
+                    # load u covers rows r0 + u * 64 / width: a constant scalar
+                    # offset on a full tile, the row clamped otherwise
+                    step = 64 // width
+                    w(f"        const int r0 = lane / {width}, c0 = lane - r0 * {width};")
+                    w(f"        const unsigned u0 = (unsigned)(r0 * {F} + {g0} + c0) * {gsz}u;")
+                    w("        if (rows == 64) {")
+                    for u in range(width):
+                        w("          t[" + str(u) + "] = " + load.format(vo="u0", so=f"{u * step * F * gsz}") + ";")
+                    w("        } else {")
+                    for u in range(width):
+                        vo = f"(unsigned)(min(r0 + {u * step}, rows - 1) * {F} + {g0} + c0) * {gsz}u"
+                        w("          t[" + str(u) + "] = " + load.format(vo=vo, so="0") + ";")
+                    w("        }")
+                else:
+                    w("#pragma unroll")
+                    w(f"        for (int u = 0; u < {width}; ++u) {{")
+                    w(f"          const int i = lane + 64 * u, r = i / {width}, c = i - r * {width};")
+                    vo = f"(unsigned)((r < rows ? r : rows - 1) * {F} + {g0} + c) * {gsz}u"
+                    w("          t[u] = " + load.format(vo=vo, so="0") + ";")
+                    w("        }")
                 w("#pragma unroll")
                 w(f"        for (int u = 0; u < {width}; ++u) {{")
                 w(f"          const int i = lane + 64 * u, r = i / {width}, c = i - r * {width};")
@@ -964,7 +997,7 @@ def generate_adjoint_parts(plan, dtype="f64", max_live=PART_MAX_LIVE, chunks_per
                     for c in range(nodes[n]["dim"]):
                         leaf_of[nodes[n]["a_offset"] + c] = f"g{n}_{c}"
             for j, col in enumerate(touched[ci]):
-                w(f"      P[{row_base[ci] + j}L * ldp + s] = {leaf_of.get(col, '(REAL)0')};")
+                w(f"      *(REAL*)(pt + {row_base[ci] + j}L * pb + plane) = {leaf_of.get(col, '(REAL)0')};")
             w("      break;")
             w("  }")
         w("  default: break;")

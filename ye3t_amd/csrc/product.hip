@@ -1952,9 +1952,12 @@ int ye3t_hip_product_adjoint_parts(const ye3t_hip_product_plan* p, const void* A
   YE3T_REQUIRE(gx <= int64_t(0x7FFFFFF8), "too many samples for one launch");
   const hipStream_t s = as_stream(stream);
   long s_arg = long(samples), rs_arg = long(columns ? 1 : p->a_width), cs_arg = long(columns ? lda : 1);
-  // the parts address a lane's density values with 32-bit byte offsets
+  // the parts address a lane's density values and a tile of gB with 32-bit byte offsets
   YE3T_REQUIRE(uint64_t(63 * rs_arg) * (p->in_dtype == YE3T_F64 ? 8u : 4u) < (uint64_t(1) << 32),
-               "density rows too wide for the readout parts");
+               "density rows too wide for the adjoint parts");
+  YE3T_REQUIRE(uint64_t(64) * uint64_t(p->feature_count) * (p->out_dtype == YE3T_F64 ? 8u : 4u) <
+                   (uint64_t(1) << 32),
+               "feature rows too wide for the adjoint parts");
   long ldp_arg = long(ldp);
   const void* a_arg = A;
   const void* g_arg = gB;
