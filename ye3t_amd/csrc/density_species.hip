@@ -136,11 +136,12 @@ __device__ inline void sp_basis_to_tile(double vx, double vy, double vz, const S
 }
 
 // Adds the product of tile columns [base, base + c), c >= 1, to the
-// accumulators: the k-blocks of four columns covering them, columns outside
-// weighing zero (they read column `base`, which holds finite values).  Rows
-// past the tile (i >= NRC, components >= LW) read its last row: their
+// accumulators (FRESH: sets them to it, the first k-block's MFMAs taking a
+// zero accumulator): the k-blocks of four columns covering them, columns
+// outside weighing zero (they read column `base`, which holds finite values).
+// Rows past the tile (i >= NRC, components >= LW) read its last row: their
 // accumulators are never stored.
-template <int LMAX, int NRC>
+template <int LMAX, int NRC, bool FRESH>
 __device__ inline void sp_group_product(const double* Wt, const double* Yt, int base, int c, int kq, int cc,
                                         sp_d4 (&acc)[SpShape<LMAX, NRC>::CT]) {
   using Sh = SpShape<LMAX, NRC>;
@@ -161,8 +162,14 @@ __device__ inline void sp_group_product(const double* Wt, const double* Yt, int 
 #pragma unroll
     for (int ct = 0; ct < Sh::CT; ++ct) y[ct] = yrow[ct][rc];
     const double wm = in ? w : 0.0;
+    if (FRESH && kb == kb0) {
 #pragma unroll
-    for (int ct = 0; ct < Sh::CT; ++ct) acc[ct] = __builtin_amdgcn_mfma_f64_16x16x4f64(wm, y[ct], acc[ct], 0, 0, 0);
+      for (int ct = 0; ct < Sh::CT; ++ct)
+        acc[ct] = __builtin_amdgcn_mfma_f64_16x16x4f64(wm, y[ct], sp_d4{0.0, 0.0, 0.0, 0.0}, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int ct = 0; ct < Sh::CT; ++ct) acc[ct] = __builtin_amdgcn_mfma_f64_16x16x4f64(wm, y[ct], acc[ct], 0, 0, 0);
+    }
   }
 }
 
@@ -172,18 +179,62 @@ __device__ inline void sp_zero(sp_d4 (&acc)[CT]) {
   for (int ct = 0; ct < CT; ++ct) acc[ct] = sp_d4{0.0, 0.0, 0.0, 0.0};
 }
 
-// One (atom, species) block [NR x LW] from the accumulators (rounded once to Out).
+typedef unsigned sp_u2 __attribute__((ext_vector_type(2)));
+// per-lane byte offsets of the CT x 4 accumulator elements (see sp_store_offsets)
+template <int CT>
+struct SpOffsets {
+  unsigned o[CT][4];
+};
+
+// Byte offsets of the lane's accumulator elements (row n = 4 v + kq,
+// component lm = 16 ct + cc) in an (atom, species) block [NR x LW] of Out,
+// and past the block for elements outside it: a buffer store there is
+// dropped, so the stores need no lane masks.
 template <int LMAX, int NRC, typename Out>
-__device__ inline void sp_store(Out* __restrict__ dst, const sp_d4 (&acc)[SpShape<LMAX, NRC>::CT], int NR, int kq,
-                                int cc) {
+__device__ inline void sp_store_offsets(SpOffsets<SpShape<LMAX, NRC>::CT>& off, int NR, int kq, int cc) {
   using Sh = SpShape<LMAX, NRC>;
 #pragma unroll
   for (int ct = 0; ct < Sh::CT; ++ct)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int n = 4 * v + kq, lm = ct * 16 + cc;
-      if (n < NR && lm < Sh::LW) dst[n * Sh::LW + lm] = Out(acc[ct][v]);
+      off.o[ct][v] = (n < NR && lm < Sh::LW) ? unsigned(n * Sh::LW + lm) * unsigned(sizeof(Out)) : 0x7ffffff0u;
     }
+}
+
+template <typename Out>
+__device__ inline void sp_put(__amdgpu_buffer_rsrc_t rb, unsigned off, double x) {
+  if constexpr (sizeof(Out) == 8) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(sp_u2, x), rb, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, float(x)), rb, off, 0, 0);
+  }
+}
+
+// One (atom, species) block [NR x LW] from the accumulators (rounded once to
+// Out), through a buffer resource spanning the block.
+template <int LMAX, int NRC, typename Out>
+__device__ inline void sp_store(Out* __restrict__ dst, const sp_d4 (&acc)[SpShape<LMAX, NRC>::CT], int NR,
+                                const SpOffsets<SpShape<LMAX, NRC>::CT>& off) {
+  using Sh = SpShape<LMAX, NRC>;
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc(dst, (short)0, NR * Sh::LW * int(sizeof(Out)), 0x00020000);
+#pragma unroll
+  for (int ct = 0; ct < Sh::CT; ++ct)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sp_put<Out>(rb, off.o[ct][v], acc[ct][v]);
+}
+
+// A zero block (a species absent from the atom).
+template <int LMAX, int NRC, typename Out>
+__device__ inline void sp_store_zero(Out* __restrict__ dst, int NR, const SpOffsets<SpShape<LMAX, NRC>::CT>& off) {
+  using Sh = SpShape<LMAX, NRC>;
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc(dst, (short)0, NR * Sh::LW * int(sizeof(Out)), 0x00020000);
+#pragma unroll
+  for (int ct = 0; ct < Sh::CT; ++ct)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sp_put<Out>(rb, off.o[ct][v], 0.0);
 }
 
 // The chunk starting at atom a: up to 16 whole atoms with at most 64 edges,
@@ -274,6 +325,8 @@ ace_density_species_kernel(SpeciesParams p, NormTable nt) {
   Out* __restrict__ Aout = static_cast<Out*>(p.A);
   const int64_t block = int64_t(NR) * LW;  // one (atom, species) block
   const uint64_t lt = sp_range(0, lane);   // lanes below this one
+  SpOffsets<CT> soff;
+  sp_store_offsets<LMAX, NRC, Out>(soff, NR, kq, cc);
 
   sp_d4 acc[CT];
   // Software pipeline over chunks.  On entry to chunk i (with at most 64
@@ -305,10 +358,10 @@ ace_density_species_kernel(SpeciesParams p, NormTable nt) {
             sp_basis_to_tile<LMAX, NRC>(double(vec[3 * e]), double(vec[3 * e + 1]), double(vec[3 * e + 2]), p, nt,
                                         Wt, Yt, __builtin_popcountll(m & lt));
           __syncthreads();
-          sp_group_product<LMAX, NRC>(Wt, Yt, 0, c, kq, cc, acc);
+          sp_group_product<LMAX, NRC, false>(Wt, Yt, 0, c, kq, cc, acc);
           __syncthreads();  // operand reads done before the next window's writes
         }
-        sp_store<LMAX, NRC, Out>(Aout + (a * S + s) * block, acc, NR, kq, cc);
+        sp_store<LMAX, NRC, Out>(Aout + (a * S + s) * block, acc, NR, soff);
       }
       // refill the pipeline from the chunk after the atom (its loads are out)
       cur = nxt;
@@ -366,9 +419,13 @@ ace_density_species_kernel(SpeciesParams p, NormTable nt) {
       int base = rj;
       for (int s = 0; s < S; ++s) {
         const int c = __builtin_popcountll(sp_ballot(valid && sp == s) & am);
-        sp_zero<CT>(acc);
-        if (c > 0) sp_group_product<LMAX, NRC>(Wt, Yt, base, c, kq, cc, acc);
-        sp_store<LMAX, NRC, Out>(Aout + ((cur.a + j) * S + s) * block, acc, NR, kq, cc);
+        Out* __restrict__ dst = Aout + ((cur.a + j) * S + s) * block;
+        if (c > 0) {
+          sp_group_product<LMAX, NRC, true>(Wt, Yt, base, c, kq, cc, acc);
+          sp_store<LMAX, NRC, Out>(dst, acc, NR, soff);
+        } else {
+          sp_store_zero<LMAX, NRC, Out>(dst, NR, soff);
+        }
         base += c;
       }
     }
