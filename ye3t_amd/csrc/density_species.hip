@@ -11,7 +11,7 @@
 //
 // One wave (a 64-thread workgroup; no barriers between waves) owns a
 // contiguous atom range (as many waves as the device holds at once) and walks
-// it in chunks of up to 16 consecutive whole atoms with at most 64 edges
+// it in chunks of up to 16 (4 for l_max >= 5) consecutive whole atoms with at most 64 edges
 // together:
 //   sort     lane = edge; the neighbour's species is gathered, one ballot per
 //            species gives every (atom, species) group's lanes, and each lane
@@ -48,7 +48,11 @@
 namespace ye3t {
 namespace {
 
-constexpr int kSpMaxAtoms = 16;  // whole atoms per chunk
+// whole atoms per chunk: 16, or 4 for l_max >= 5 (sp_max_atoms), whose
+// one-wave kernels would otherwise keep the chunk bounds in VGPRs for want of
+// SGPRs and select them with a VALU chain per atom
+template <int LMAX>
+constexpr int sp_max_atoms() { return LMAX >= 5 ? 4 : 16; }
 constexpr int kSpMaxSpecies = 16;
 constexpr int kSpPitch = 67;  // LDS row pitch (doubles) of the transposed tile: odd, so 16 rows of a column spread over the banks
 
@@ -242,37 +246,40 @@ __device__ inline void sp_store_zero(Out* __restrict__ dst, int NR, const SpOffs
 // draining); rel[j] = first edge of atom a + j relative to e0, cnt = edges.
 // na == 0: atom a alone has more than 64 edges, or a == a_end (past the
 // wave's range).
+template <int MAXA>
 struct SpChunk {
   int64_t a, e0;
   int na, cnt;
-  int rel[kSpMaxAtoms + 1];
+  int rel[MAXA + 1];
 };
 
-__device__ inline SpChunk sp_form(const SpeciesParams& p, int64_t a, int64_t a_end) {
-  SpChunk c;
+template <int MAXA>
+__device__ inline SpChunk<MAXA> sp_form(const SpeciesParams& p, int64_t a, int64_t a_end) {
+  SpChunk<MAXA> c;
   a = a < a_end ? a : a_end;  // past the end: an empty chunk at a_end
   c.a = a;
   c.e0 = sp_offset(p.offsets, a);
-  int64_t ends[kSpMaxAtoms];
+  int64_t ends[MAXA];
 #pragma unroll
-  for (int j = 1; j <= kSpMaxAtoms; ++j) ends[j - 1] = sp_offset(p.offsets, (a + j) <= a_end ? (a + j) : a_end);
+  for (int j = 1; j <= MAXA; ++j) ends[j - 1] = sp_offset(p.offsets, (a + j) <= a_end ? (a + j) : a_end);
   c.na = 0;
   c.rel[0] = 0;
   bool open = true;
 #pragma unroll
-  for (int j = 1; j <= kSpMaxAtoms; ++j) {
+  for (int j = 1; j <= MAXA; ++j) {
     open = open && (a + j) <= a_end && ends[j - 1] - c.e0 <= 64;
     c.rel[j] = open ? int(ends[j - 1] - c.e0) : 64 + 1;
     c.na += open ? 1 : 0;
   }
   c.cnt = 0;
 #pragma unroll
-  for (int j = 1; j <= kSpMaxAtoms; ++j) c.cnt = (j == c.na) ? c.rel[j] : c.cnt;
+  for (int j = 1; j <= MAXA; ++j) c.cnt = (j == c.na) ? c.rel[j] : c.cnt;
   return c;
 }
 
 // First atom after chunk c (a chunk with na == 0 is one atom).
-__device__ inline int64_t sp_after(const SpChunk& c) { return c.a + (c.na > 0 ? c.na : 1); }
+template <int MAXA>
+__device__ inline int64_t sp_after(const SpChunk<MAXA>& c) { return c.a + (c.na > 0 ? c.na : 1); }
 
 // One lane's edge of a chunk: its vector and neighbour (zeros past the chunk's
 // edges, and for a single-atom chunk of more than 64 edges, which loads its
@@ -283,8 +290,9 @@ struct SpEdges {
   int64_t nb;
 };
 
-template <typename In>
-__device__ inline SpEdges<In> sp_load(const SpeciesParams& p, const In* __restrict__ vec, const SpChunk& c, int lane) {
+template <typename In, int MAXA>
+__device__ inline SpEdges<In> sp_load(const SpeciesParams& p, const In* __restrict__ vec, const SpChunk<MAXA>& c,
+                                      int lane) {
   SpEdges<In> r{In(0), In(0), In(0), 0};
   if (c.na > 0 && lane < c.cnt) {
     const int64_t e = c.e0 + lane;
@@ -297,7 +305,8 @@ __device__ inline SpEdges<In> sp_load(const SpeciesParams& p, const In* __restri
 }
 
 // The species channel of the lane's neighbour (-1 past the chunk's edges).
-__device__ inline int sp_gather(const SpeciesParams& p, const SpChunk& c, int64_t nb, int lane) {
+template <int MAXA>
+__device__ inline int sp_gather(const SpeciesParams& p, const SpChunk<MAXA>& c, int64_t nb, int lane) {
   if (c.na == 0 || lane >= c.cnt) return -1;
   return p.species ? int(p.species[nb]) : 0;
 }
@@ -335,10 +344,11 @@ ace_density_species_kernel(SpeciesParams p, NormTable nt) {
   // chunk i's basis, finds them (and chunk i - 1's stores) done, and chunk
   // i + 1's gather and chunk i + 2's loads then go out behind chunk i's
   // accumulation and stores and chunk i + 1's basis.
-  SpChunk cur = sp_form(p, a_begin, a_end);
+  constexpr int MAXA = sp_max_atoms<LMAX>();
+  SpChunk<MAXA> cur = sp_form<MAXA>(p, a_begin, a_end);
   SpEdges<In> E = sp_load(p, vec, cur, lane);
   int sp = sp_gather(p, cur, E.nb, lane);
-  SpChunk nxt = sp_form(p, sp_after(cur), a_end);
+  SpChunk<MAXA> nxt = sp_form<MAXA>(p, sp_after(cur), a_end);
   SpEdges<In> NE = sp_load(p, vec, nxt, lane);
   while (cur.a < a_end) {
     if (cur.na == 0) {
@@ -367,7 +377,7 @@ ace_density_species_kernel(SpeciesParams p, NormTable nt) {
       cur = nxt;
       E = NE;
       sp = sp_gather(p, cur, E.nb, lane);
-      nxt = sp_form(p, sp_after(cur), a_end);
+      nxt = sp_form<MAXA>(p, sp_after(cur), a_end);
       NE = sp_load(p, vec, nxt, lane);
       continue;
     }
@@ -378,16 +388,16 @@ ace_density_species_kernel(SpeciesParams p, NormTable nt) {
     sp_basis<LMAX, NRC>(double(E.x), double(E.y), double(E.z), p, nt, Y, R);
     sp_wait_vmem();
     const int nsp = sp_gather(p, nxt, NE.nb, lane);
-    const SpChunk nn = sp_form(p, sp_after(nxt), a_end);
+    const SpChunk<MAXA> nn = sp_form<MAXA>(p, sp_after(nxt), a_end);
     const SpEdges<In> NNE = sp_load(p, vec, nn, lane);
 
     // ---- sort: (atom, species) groups in column order
     int la = 0;  // the lane's atom within the chunk
 #pragma unroll
-    for (int j = 1; j < kSpMaxAtoms; ++j) la += (j < cur.na && lane >= cur.rel[j]) ? 1 : 0;
+    for (int j = 1; j < MAXA; ++j) la += (j < cur.na && lane >= cur.rel[j]) ? 1 : 0;
     int lo = 0, hi = 0;
 #pragma unroll
-    for (int j = 0; j < kSpMaxAtoms; ++j) {
+    for (int j = 0; j < MAXA; ++j) {
       lo = la == j ? cur.rel[j] : lo;
       hi = la == j ? cur.rel[j + 1] : hi;
     }
@@ -411,7 +421,7 @@ ace_density_species_kernel(SpeciesParams p, NormTable nt) {
     for (int j = 0; j < cur.na; ++j) {
       int rj = 0, rj1 = 0;  // chunk-relative columns of atom j
 #pragma unroll
-      for (int k = 0; k < kSpMaxAtoms; ++k) {
+      for (int k = 0; k < MAXA; ++k) {
         rj = k == j ? cur.rel[k] : rj;
         rj1 = k == j ? cur.rel[k + 1] : rj1;
       }
@@ -421,8 +431,9 @@ ace_density_species_kernel(SpeciesParams p, NormTable nt) {
         const int c = __builtin_popcountll(sp_ballot(valid && sp == s) & am);
         Out* __restrict__ dst = Aout + ((cur.a + j) * S + s) * block;
         if (c > 0) {
-          sp_group_product<LMAX, NRC, true>(Wt, Yt, base, c, kq, cc, acc);
-          sp_store<LMAX, NRC, Out>(dst, acc, NR, soff);
+          sp_d4 g[CT];  // the group's own accumulators, set by its first k-block
+          sp_group_product<LMAX, NRC, true>(Wt, Yt, base, c, kq, cc, g);
+          sp_store<LMAX, NRC, Out>(dst, g, NR, soff);
         } else {
           sp_store_zero<LMAX, NRC, Out>(dst, NR, soff);
         }
