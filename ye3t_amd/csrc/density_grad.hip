@@ -230,13 +230,37 @@ __global__ __launch_bounds__(64) void density_edge_gradient_kernel(GradParams<In
     channel_terms<LW>(p, grow, s, 1.0, R, dR, Y, a, t);
   } else if (p.mix) {
     // channel index uniform across the wave (the mix row is read through the
-    // scalar cache); the channel's adjoint row is loaded whole before it is used
+    // scalar cache).  For l_max <= 3 the next channel's adjoint row and
+    // feature value are requested before this channel's arithmetic, so their
+    // latency hides behind it (config 4: 198 -> 181 us); larger rows would not
+    // fit twice in the registers, and each is loaded just before its use.
+    constexpr bool kPrefetch = LW <= 16;
+    G gn[kPrefetch ? LW : 1];
+    In wn = In(1);
+    if constexpr (kPrefetch) {
+      wn = p.feats ? p.feats[j * p.C] : In(1);
+#pragma unroll
+      for (int k = 0; k < LW; ++k) gn[k] = grow[k];
+    }
     for (int c = 0; c < p.C; ++c) {
       G g[LW];
-      const double w = p.feats ? double(p.feats[j * p.C + c]) : 1.0;
-      const G* gr = grow + int64_t(c) * LW;
+      double w;
+      if constexpr (kPrefetch) {
 #pragma unroll
-      for (int k = 0; k < LW; ++k) g[k] = gr[k];
+        for (int k = 0; k < LW; ++k) g[k] = gn[k];
+        w = double(wn);
+        if (c + 1 < p.C) {
+          const G* gr = grow + int64_t(c + 1) * LW;
+#pragma unroll
+          for (int k = 0; k < LW; ++k) gn[k] = gr[k];
+          wn = p.feats ? p.feats[j * p.C + c + 1] : In(1);
+        }
+      } else {
+        w = p.feats ? double(p.feats[j * p.C + c]) : 1.0;
+        const G* gr = grow + int64_t(c) * LW;
+#pragma unroll
+        for (int k = 0; k < LW; ++k) g[k] = gr[k];
+      }
       double rad = 0.0, drad = 0.0;
 #pragma unroll
       for (int q = 0; q < kGradMaxRadial; ++q) {
