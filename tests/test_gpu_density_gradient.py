@@ -5,7 +5,8 @@
 inputs: one-hot species, node features with a radial mix, one channel; every
 l_max the kernel is built for (0..8); ragged CSR rows with empty atoms, edges
 beyond the cutoff and near zero length; fp64 (1e-12) and fp32 edge vectors with
-fp32 or fp64 adjoints (2e-5), column-relative over the three components.
+fp32 or fp64 adjoints (2e-5), column-relative over the three components;
+config 4's 16-channel mix shape (its own kernel path) in the three dtype pairs.
 Autograd through ``runtime.ace_density`` gives the same gradient, and an
 fp64 config-sized case is checked at full size.
 """
@@ -137,3 +138,27 @@ def test_edge_gradient_empty_and_errors(gpu):
     with pytest.raises(RuntimeError, match="l_max"):
         native.ace_density_edge_gradient(torch.zeros((5, 1, 4, 100), dtype=torch.float64, device=gpu),
                                          d["edge_vectors"], d["row_offsets"], d["neighbors"], **kw9)
+
+
+@pytest.mark.parametrize("dtype,adjoint", [("f64", "f64"), ("f32", "f32"), ("f32", "f64")])
+def test_edge_gradient_sixteen_channel_mix(gpu, dtype, adjoint):
+    """Config 4's shape (16 feature channels with a radial mix, n_max 8,
+    l_max 3), which runs the kernel's unrolled-row path: the neighbour's
+    feature row read once, each channel's adjoint row one channel ahead."""
+    flush(f"density edge gradient, 16 channels with a mix, dtype={dtype} adjoint={adjoint}")
+    import torch
+
+    from ye3t_amd.runtime import native
+
+    cfg = W.config(4, atom_count=700)
+    inp = cfg.density.generate()
+    assert inp["channel_count"] == 16 and inp["n_max"] == 8 and inp["l_max"] == 3
+    d, kw = _device({**inp, "species": inp.get("species")}, dtype, gpu)
+    shape = (inp["atom_count"], 16, 1, 16)
+    adt = torch.float64 if adjoint == "f64" else torch.float32
+    gA = torch.as_tensor(np.random.default_rng(41).normal(size=shape), dtype=adt, device=gpu)
+    got = native.ace_density_edge_gradient(gA, d["edge_vectors"], d["row_offsets"], d["neighbors"], **kw)
+    ref = oracle.ace_density_edge_gradient(rounded_inputs(inp, dtype), gA.double().cpu().numpy())
+    err = column_rel_error(got.cpu().numpy(), ref)
+    flush(f"  err {err:.3e}")
+    assert err < TOL["f64" if dtype == "f64" else "f32"], err

@@ -148,13 +148,13 @@ __device__ inline void sph_gradient_dot(double x, double y, double z, const Norm
 // t_k += w sum_r rad_{c,r} gA[c, r, k], z_{c,r} = sum_k gA[c, r, k] Y_k.  The
 // radial values R, dR are register arrays of kGradMaxRadial entries (computed
 // to the fixed length; entries from nr on are not read).
-template <int LW, typename In, typename G>
+template <int LW, int NRMAX, typename In, typename G>
 __device__ inline void channel_terms(const GradParams<In, G>& p, const G* grow, int c, double w, const double* R,
                                      const double* dR, const double* Y, double& a, double* t) {
   if (p.mix) {
     double rad = 0.0, drad = 0.0;
 #pragma unroll
-    for (int q = 0; q < kGradMaxRadial; ++q) {
+    for (int q = 0; q < NRMAX; ++q) {
       if (q < p.nr) {
         const double mq = double(p.mix[c * p.nr + q]);
         rad += mq * R[q];
@@ -171,7 +171,7 @@ __device__ inline void channel_terms(const GradParams<In, G>& p, const G* grow, 
     for (int k = 0; k < LW; ++k) t[k] += coef * double(gr[k]);
   } else {
 #pragma unroll
-    for (int n = 0; n < kGradMaxRadial; ++n) {
+    for (int n = 0; n < NRMAX; ++n) {
       if (n < p.nr) {
         const G* gr = grow + (int64_t(c) * p.nr + n) * LW;
         double z = 0.0;
@@ -186,7 +186,12 @@ __device__ inline void channel_terms(const GradParams<In, G>& p, const G* grow, 
   }
 }
 
-template <int LMAX, typename In, typename G>
+// NRMAX: length of the radial register arrays (>= p.nr).  MIX16: node
+// features with a mix over exactly 16 channels and l_max <= 3 (config 4's
+// shape): the channel loop is unrolled, the neighbour's feature row is read
+// once as a 64-byte row rather than as 16 four-byte gathers, and each
+// channel's adjoint row is requested one channel ahead.
+template <int LMAX, int NRMAX, bool MIX16, typename In, typename G>
 __global__ __launch_bounds__(64) void density_edge_gradient_kernel(GradParams<In, G> p) {
   constexpr int LW = (LMAX + 1) * (LMAX + 1);
   const int lane = threadIdx.x;
@@ -217,8 +222,8 @@ __global__ __launch_bounds__(64) void density_edge_gradient_kernel(GradParams<In
   const double ux = vx / sr, uy = vy / sr, uz = vz / sr;
   double Y[LW];
   sph_values<LMAX>(ux, uy, uz, p.nt, Y);
-  double R[kGradMaxRadial], dR[kGradMaxRadial];
-  cheb_exp_cos_row<double, true, double>(r, p.cutoff, p.lambda, kGradMaxRadial - 1, R, dR);
+  double R[NRMAX], dR[NRMAX];
+  cheb_exp_cos_row<double, true, double>(r, p.cutoff, p.lambda, NRMAX - 1, R, dR);
   double a = 0.0;
   double t[LW];
 #pragma unroll
@@ -227,7 +232,47 @@ __global__ __launch_bounds__(64) void density_edge_gradient_kernel(GradParams<In
   if (p.species) {  // one-hot: the neighbour's channel only
     int s = p.species[j];
     s = s < 0 ? 0 : (s >= p.C ? p.C - 1 : s);
-    channel_terms<LW>(p, grow, s, 1.0, R, dR, Y, a, t);
+    channel_terms<LW, NRMAX>(p, grow, s, 1.0, R, dR, Y, a, t);
+  } else if constexpr (MIX16) {
+    // the neighbour's 16 features as one 64-byte row (the channel index is
+    // wave-uniform, so h[c] is a register-relative move), each channel's
+    // adjoint row requested one channel ahead; the loop stays rolled so the
+    // loads stay where they are written
+    constexpr int C = 16;
+    In h[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) h[c] = p.feats[j * C + c];
+    G gn[LW];
+#pragma unroll
+    for (int k = 0; k < LW; ++k) gn[k] = grow[k];
+#pragma unroll 1
+    for (int c = 0; c < C; ++c) {
+      G g[LW];
+#pragma unroll
+      for (int k = 0; k < LW; ++k) g[k] = gn[k];
+      if (c + 1 < C) {
+        const G* gr = grow + (c + 1) * LW;
+#pragma unroll
+        for (int k = 0; k < LW; ++k) gn[k] = gr[k];
+      }
+      const double w = double(h[c]);
+      double rad = 0.0, drad = 0.0;
+#pragma unroll
+      for (int q = 0; q < NRMAX; ++q) {
+        if (q < p.nr) {
+          const double mq = double(p.mix[c * p.nr + q]);
+          rad += mq * R[q];
+          drad += mq * dR[q];
+        }
+      }
+      double z = 0.0;
+#pragma unroll
+      for (int k = 0; k < LW; ++k) z += double(g[k]) * Y[k];
+      a += w * drad * z;
+      const double coef = w * rad;
+#pragma unroll
+      for (int k = 0; k < LW; ++k) t[k] += coef * double(g[k]);
+    }
   } else if (p.mix) {
     // channel index uniform across the wave (the mix row is read through the
     // scalar cache).  For l_max <= 3 the next channel's adjoint row and
@@ -263,7 +308,7 @@ __global__ __launch_bounds__(64) void density_edge_gradient_kernel(GradParams<In
       }
       double rad = 0.0, drad = 0.0;
 #pragma unroll
-      for (int q = 0; q < kGradMaxRadial; ++q) {
+      for (int q = 0; q < NRMAX; ++q) {
         if (q < p.nr) {
           const double mq = double(p.mix[c * p.nr + q]);
           rad += mq * R[q];
@@ -280,7 +325,7 @@ __global__ __launch_bounds__(64) void density_edge_gradient_kernel(GradParams<In
     }
   } else {  // channel index uniform across the wave
     for (int c = 0; c < p.C; ++c)
-      channel_terms<LW>(p, grow, c, p.feats ? double(p.feats[j * p.C + c]) : 1.0, R, dR, Y, a, t);
+      channel_terms<LW, NRMAX>(p, grow, c, p.feats ? double(p.feats[j * p.C + c]) : 1.0, R, dR, Y, a, t);
   }
   double gx, gy, gz;
   sph_gradient_dot<LMAX>(ux, uy, uz, p.nt, t, gx, gy, gz);
@@ -302,7 +347,14 @@ __global__ __launch_bounds__(64) void density_edge_gradient_kernel(GradParams<In
 template <int LMAX, typename In, typename G>
 int launch_lmax(const GradParams<In, G>& p, hipStream_t s) {
   const int64_t blocks = (p.E + 63) / 64;
-  hipLaunchKernelGGL((density_edge_gradient_kernel<LMAX, In, G>), dim3(unsigned(blocks)), dim3(64), 0, s, p);
+  if constexpr (LMAX == 3) {
+    if (!p.species && p.mix && p.feats && p.C == 16 && p.nr <= 9) {
+      hipLaunchKernelGGL((density_edge_gradient_kernel<3, 9, true, In, G>), dim3(unsigned(blocks)), dim3(64), 0, s, p);
+      return check_launch("density_edge_gradient_kernel");
+    }
+  }
+  hipLaunchKernelGGL((density_edge_gradient_kernel<LMAX, kGradMaxRadial, false, In, G>), dim3(unsigned(blocks)),
+                     dim3(64), 0, s, p);
   return check_launch("density_edge_gradient_kernel");
 }
 
