@@ -195,10 +195,14 @@ template <int LMAX, int NRMAX, bool MIX16, typename In, typename G>
 __global__ __launch_bounds__(64) void density_edge_gradient_kernel(GradParams<In, G> p) {
   constexpr int LW = (LMAX + 1) * (LMAX + 1);
   const int lane = threadIdx.x;
-  // centre of each edge: row_offsets[i] <= e < row_offsets[i + 1].  The block's
-  // first and last edges are located by wave-uniform searches (scalar loads),
-  // then each lane searches the few rows between them; every search stays
-  // inside [0, N).
+  // centre of each edge: the largest i with row_offsets[i] <= e (then
+  // e < row_offsets[i + 1]; rows of empty atoms own nothing).  `centre`
+  // bisects [lo, hi) given row_offsets[lo] <= target and hi == N or
+  // row_offsets[hi] > target.  The block's first edge is bracketed by
+  // galloping from the atom a uniform degree would give it, its last edge by
+  // galloping from the first's centre (wave-uniform, scalar loads: a few
+  // dependent loads instead of log2 N), then each lane bisects the few rows
+  // between them; every access stays inside [0, N).
   auto centre = [&](int64_t target, int64_t lo, int64_t hi) {
     while (hi - lo > 1) {
       const int64_t mid = (lo + hi) >> 1;
@@ -207,13 +211,49 @@ __global__ __launch_bounds__(64) void density_edge_gradient_kernel(GradParams<In
     }
     return lo;
   };
+  auto gallop = [&](int64_t target, int64_t lo_bound, int64_t guess) {
+    int64_t lo, hi;
+    guess = guess < lo_bound ? lo_bound : (guess > p.N - 1 ? p.N - 1 : guess);
+    if (p.row_offsets[guess] <= target) {  // bracket upwards
+      lo = guess;
+      int64_t step = 1;
+      hi = lo + step;
+      while (hi < p.N && p.row_offsets[hi] <= target) {
+        lo = hi;
+        step *= 2;
+        hi = lo + step;
+      }
+      hi = hi < p.N ? hi : p.N;
+    } else {  // bracket downwards: row_offsets[lo_bound] <= target holds
+      hi = guess;
+      int64_t step = 1;
+      lo = hi - step;
+      while (lo > lo_bound && p.row_offsets[lo] > target) {
+        hi = lo;
+        step *= 2;
+        lo = hi - step;
+      }
+      lo = lo > lo_bound ? lo : lo_bound;
+    }
+    return centre(target, lo, hi);
+  };
   const int64_t e_first = int64_t(blockIdx.x) * 64;
   const int64_t e_last = e_first + 63 < p.E ? e_first + 63 : p.E - 1;
-  const int64_t i_first = centre(e_first, 0, p.N);
-  const int64_t i_last = centre(e_last, i_first, p.N);
+  const int64_t i_first = gallop(e_first, 0, int64_t(double(e_first) * double(p.N) / double(p.E)));
+  const int64_t i_last = gallop(e_last, i_first, i_first);
   const int64_t e = e_first + lane;
   if (e >= p.E) return;
-  const int64_t i = centre(e, i_first, i_last + 1);
+  // a lane's centre: with few rows in the block, i_first plus the number of
+  // rows k in (i_first, i_last] with row_offsets[k] <= e (the offsets rise, so
+  // those rows are a prefix), the offsets read through the scalar cache
+  // independently of one another; otherwise a per-lane bisection
+  int64_t i;
+  if (i_last - i_first <= 16) {
+    i = i_first;
+    for (int64_t k = i_first + 1; k <= i_last; ++k) i += p.row_offsets[k] <= e ? 1 : 0;
+  } else {
+    i = centre(e, i_first, i_last + 1);
+  }
   int64_t j = p.neighbors ? p.neighbors[e] : 0;
   j = j < 0 ? 0 : (j >= p.N ? p.N - 1 : j);  // out-of-range input is clamped, never dereferenced
   const double vx = double(p.vec[3 * e]), vy = double(p.vec[3 * e + 1]), vz = double(p.vec[3 * e + 2]);
