@@ -142,6 +142,37 @@ def test_density_and_monomial_operators(gpu):
     assert torch.equal(y, y2) and torch.equal(gy, gy2)
 
 
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+def test_complex_harmonic_table(gpu, dtype):
+    """``real_output=False`` (the reference's default) on the device: the
+    complex table and gradient from the HIP real table equal the oracle's real
+    table put through the same conversion on the CPU (pinned against SciPy's
+    complex harmonics in ``test_complex_sph``), to the north-star tolerance,
+    through the runtime function and the Torch operator alike."""
+    flush(f"complex harmonic table {dtype}")
+    import torch
+
+    from ye3t_amd import runtime
+
+    ops = _ops()
+    l_max = 5
+    tdt = torch.float64 if dtype == "f64" else torch.float32
+    rng = np.random.default_rng(21)
+    v = rng.normal(size=(500, 3)) * rng.uniform(0.5, 3.0, size=(500, 1))
+    e = torch.as_tensor(v, dtype=tdt, device=gpu)
+    y, g = runtime.spherical_harmonics_table_with_derivative(e, l_max)
+    assert y.dtype == (torch.complex128 if dtype == "f64" else torch.complex64) and g.shape == (500, 36, 3)
+    y2, g2 = ops.spherical_harmonics_table_with_derivative(e, l_max, False, 1e-12)
+    assert torch.equal(y, y2) and torch.equal(g, g2)
+    rv, rg = oracle.real_sph_table(e.double().cpu().numpy(), l_max)
+    ry, rgc = runtime.complex_from_real_table(torch.from_numpy(rv), torch.from_numpy(rg), l_max)
+    for got, ref in ((y, ry), (g, rgc)):
+        got, ref = got.cpu().to(torch.complex128).numpy(), ref.numpy()
+        err = max(column_rel_error(got.real, ref.real), column_rel_error(got.imag, ref.imag))
+        flush(f"  column error {err:.3e}")
+        assert err <= TOL[dtype]
+
+
 def test_capability_report_hip_branch(gpu):
     """On the GPU the report's HIP branch is on: the ``cuda`` keys describe
     torch's ``cuda`` device type (the HIP device on ROCm), every listed

@@ -19,6 +19,7 @@ _NATIVE_EXECUTION_PLAN_ABI = 42
 REFERENCE_OPERATIONS = (
     "cheb_exp_cos_radial_table_with_derivative",
     "real_spherical_harmonics_table_with_derivative",
+    "complex_spherical_harmonics_table_with_derivative",
     "density_accumulate",
     "density_accumulate_adjoint",
     "symmetric_power_monomial",
@@ -80,21 +81,78 @@ def cheb_exp_cos_radial_table_with_derivative(radii, cutoffs, lambdas, maximum_r
                                maximum_radial_index)
 
 
+def _complex_rows(l_max):
+    """Per packed complex column ``(l, m)``: the real columns and weights with
+    ``Y_lm = wr * R[re] + i * wi * R[im]``.
+
+    The reference forms its real rows from the complex ones
+    (``execution_plan.py:6943-6963``): ``R_l0 = Re Y_l0``, and for ``m > 0``
+    ``R_lm = sqrt2 (-1)^m Re Y_lm``, ``R_l,-m = -sqrt2 (-1)^m Im Y_lm``.  With
+    ``Y_l,-m = (-1)^m conj(Y_lm)`` (``core/spherical.py:183-187``) this inverts
+    to ``Y_lm = (-1)^m (R_lm - i R_l,-m) / sqrt2`` and
+    ``Y_l,-m = (R_lm + i R_l,-m) / sqrt2``.
+    """
+    h = 0.5 ** 0.5
+    re, im, wr, wi = [], [], [], []
+    for l in range(l_max + 1):
+        base = l * l + l
+        for m in range(-l, l + 1):
+            a = abs(m)
+            re.append(base + a)
+            im.append(base - a)
+            if m == 0:
+                wr.append(1.0)
+                wi.append(0.0)
+            elif m > 0:
+                s = -1.0 if m % 2 else 1.0
+                wr.append(s * h)
+                wi.append(-s * h)
+            else:
+                wr.append(h)
+                wi.append(h)
+    return re, im, wr, wi
+
+
+def complex_from_real_table(values, derivative, maximum_angular_momentum):
+    """The reference's complex SH table and its Cartesian gradient from the
+    packed real table ``values [E, W]`` and gradient ``derivative [E, W, 3]``.
+
+    A fixed unitary per ``l`` (see :func:`_complex_rows`), applied on the
+    tensors' own device.  The gradient is ``d Re Y + i d Im Y`` per
+    component, as the reference's autograd rows (``execution_plan.py:7547-7578``).
+    """
+    import torch
+
+    re, im, wr, wi = _complex_rows(int(maximum_angular_momentum))
+    dev, dt = values.device, values.dtype
+    re = torch.tensor(re, dtype=torch.int64, device=dev)
+    im = torch.tensor(im, dtype=torch.int64, device=dev)
+    wr = torch.tensor(wr, dtype=dt, device=dev)
+    wi = torch.tensor(wi, dtype=dt, device=dev)
+    y = torch.complex(values[:, re] * wr, values[:, im] * wi)
+    g = torch.complex(derivative[:, re, :] * wr[:, None], derivative[:, im, :] * wi[:, None])
+    return y, g
+
+
 def spherical_harmonics_table_with_derivative(edge_vectors, maximum_angular_momentum, *, real_output=False,
                                               epsilon=1.0e-12, backend="auto"):
-    """Packed real SH table and Cartesian gradient (reference ``execution_plan.py:7479-7580``).
+    """Packed SH table and Cartesian gradient (reference ``execution_plan.py:7479-7580``).
 
-    Only ``real_output=True`` is provided: the ACE path of this backend works
-    in the real basis and converts with an explicit unitary where needed.
+    ``real_output=True``: the real tesseral table ``[E, (L+1)^2]`` and gradient
+    ``[E, (L+1)^2, 3]`` from the HIP kernel.  ``real_output=False`` (the
+    reference's default): the complex table and gradient (complex64 for
+    float32 input, complex128 for float64), formed on the device from the
+    HIP real table by :func:`complex_from_real_table`.
     """
     _backend(backend, {"auto", "native"})
-    if not real_output:
-        raise NotImplementedError("only real_output=True is implemented by the HIP backend")
     maximum_angular_momentum = int(maximum_angular_momentum)
     if maximum_angular_momentum < 0:
         raise ValueError("maximum_angular_momentum must be non-negative")
     _require_device(edge_vectors, "spherical_harmonics_table_with_derivative")
-    return native.real_sph_table(edge_vectors.contiguous(), maximum_angular_momentum, epsilon)
+    v, g = native.real_sph_table(edge_vectors.contiguous(), maximum_angular_momentum, epsilon)
+    if real_output:
+        return v, g
+    return complex_from_real_table(v, g, maximum_angular_momentum)
 
 
 def validate_density_csr(row_offsets, neighbors, atom_count, edge_count, *, species=None, species_count=None):

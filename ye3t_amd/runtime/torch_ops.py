@@ -216,11 +216,11 @@ def _k_radial(radii, cutoffs, lambdas, maximum_radial_index):
 
 
 def _k_sph(edge_vectors, maximum_angular_momentum, real_output, epsilon):
-    if not real_output:
-        raise NotImplementedError("spherical_harmonics_table_with_derivative: the HIP kernels provide "
-                                  "real_output=True only")
-    v, g = native.real_sph_table(edge_vectors.contiguous(), int(maximum_angular_momentum), float(epsilon))
-    return v, g
+    from ye3t_amd import runtime
+
+    return runtime.spherical_harmonics_table_with_derivative(edge_vectors, maximum_angular_momentum,
+                                                             real_output=bool(real_output),
+                                                             epsilon=float(epsilon))
 
 
 def _k_density(edge_values, centers, atom_count):
