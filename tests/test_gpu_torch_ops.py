@@ -173,6 +173,42 @@ def test_complex_harmonic_table(gpu, dtype):
         assert err <= TOL[dtype]
 
 
+def test_single_index_radial_and_harmonics(gpu):
+    """``cheb_exp_cos_radial_with_derivative`` (one radial index, radii of any
+    shape, scalar cutoff and lambda broadcast as the reference does) and
+    ``spherical_harmonics_with_derivative`` (one ``l``, real and complex): the
+    oracle's radial table column (reference-core bit-exact on the CPU) to the
+    north-star fp64 tolerance, and the table op's columns bit for bit, through
+    the runtime functions and the Torch operators."""
+    flush("single-index radial function and single-l harmonics")
+    import torch
+
+    from ye3t_amd import runtime
+
+    ops = _ops()
+    rng = np.random.default_rng(5)
+    r = torch.as_tensor(rng.uniform(0.3, 5.5, size=(6, 7)), device=gpu)
+    for n in (0, 1, 4, 8):
+        v, d = runtime.cheb_exp_cos_radial_with_derivative(r, 5.0, 1.5, n)
+        assert v.shape == r.shape and d.shape == r.shape
+        rv, rd = oracle.radial_table(r.cpu().numpy().reshape(-1), np.full(42, 5.0), np.full(42, 1.5), n)
+        assert column_rel_error(v.cpu().numpy().reshape(-1, 1), rv[:, n:n + 1]) <= TOL["f64"]
+        assert column_rel_error(d.cpu().numpy().reshape(-1, 1), rd[:, n:n + 1]) <= TOL["f64"]
+        tv, td = runtime.cheb_exp_cos_radial_table_with_derivative(r.reshape(-1), 5.0, 1.5, n)
+        assert torch.equal(v.reshape(-1), tv[:, n]) and torch.equal(d.reshape(-1), td[:, n])
+        v2, d2 = ops.cheb_exp_cos_radial_with_derivative(r, torch.full_like(r, 5.0), torch.full_like(r, 1.5), n)
+        assert torch.equal(v, v2) and torch.equal(d, d2)
+    e = torch.as_tensor(rng.normal(size=(50, 3)), device=gpu)
+    for real in (True, False):
+        tv, tg = runtime.spherical_harmonics_table_with_derivative(e, 4, real_output=real)
+        for l in range(5):
+            v, g = runtime.spherical_harmonics_with_derivative(e, l, real_output=real)
+            assert v.shape == (50, 2 * l + 1) and g.shape == (50, 2 * l + 1, 3)
+            assert torch.equal(v, tv[:, l * l:(l + 1) * (l + 1)]) and torch.equal(g, tg[:, l * l:(l + 1) * (l + 1)])
+            v2, g2 = ops.spherical_harmonics_with_derivative(e, l, real, 1e-12)
+            assert torch.equal(v, v2) and torch.equal(g, g2)
+
+
 def test_capability_report_hip_branch(gpu):
     """On the GPU the report's HIP branch is on: the ``cuda`` keys describe
     torch's ``cuda`` device type (the HIP device on ROCm), every listed

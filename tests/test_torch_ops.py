@@ -71,6 +71,12 @@ def test_fake_shapes_on_meta_tensors():
     assert v.shape == (7, 16) and g.shape == (7, 16, 3) and v.dtype == torch.float64
     v, _ = ops.spherical_harmonics_table_with_derivative(_m(7, 3, dtype=torch.float32), 2, False, 1e-12)
     assert v.dtype == torch.complex64 and v.shape == (7, 9)
+    v, d = ops.cheb_exp_cos_radial_with_derivative(_m(7), _m(7), _m(7), 5)
+    assert v.shape == (7,) and d.shape == (7,)
+    v, g = ops.spherical_harmonics_with_derivative(_m(7, 3), 3, True, 1e-12)
+    assert v.shape == (7, 7) and g.shape == (7, 7, 3) and v.dtype == torch.float64
+    v, g = ops.spherical_harmonics_with_derivative(_m(7, 3), 2, False, 1e-12)
+    assert v.dtype == torch.complex128 and v.shape == (7, 5) and g.shape == (7, 5, 3)
     assert ops.density_accumulate(_m(9, 4), _i(9), 3).shape == (3, 4)
     assert ops.density_accumulate_adjoint(_m(3, 4), _i(9)).shape == (9, 4)
     x = _m(5, 3)

@@ -17,9 +17,12 @@ _NATIVE_EXECUTION_PLAN_ABI = 42
 # names (the ``operations`` tuple of ``native_execution_plan_capabilities``,
 # reference ``execution_plan.py:6662-6850``), then this backend's fused ops.
 REFERENCE_OPERATIONS = (
+    "cheb_exp_cos_radial_with_derivative",
     "cheb_exp_cos_radial_table_with_derivative",
-    "real_spherical_harmonics_table_with_derivative",
+    "complex_spherical_harmonics_with_derivative",
+    "real_spherical_harmonics_with_derivative",
     "complex_spherical_harmonics_table_with_derivative",
+    "real_spherical_harmonics_table_with_derivative",
     "density_accumulate",
     "density_accumulate_adjoint",
     "symmetric_power_monomial",
@@ -70,15 +73,41 @@ def _backend(backend, allowed):
     return backend
 
 
+def _radial_operands(radii, cutoffs, lambdas, name):
+    """Radii as a tensor, with cutoffs and lambdas in its dtype and device,
+    broadcast to its shape (scalars or one value per radius), as the
+    reference prepares them (``execution_plan.py:7245-7275``)."""
+    import torch
+
+    radii = torch.as_tensor(radii)
+    _require_device(radii, name)
+    cutoffs = torch.as_tensor(cutoffs, dtype=radii.dtype, device=radii.device).expand_as(radii).contiguous()
+    lambdas = torch.as_tensor(lambdas, dtype=radii.dtype, device=radii.device).expand_as(radii).contiguous()
+    return radii.contiguous(), cutoffs, lambdas
+
+
 def cheb_exp_cos_radial_table_with_derivative(radii, cutoffs, lambdas, maximum_radial_index, backend="auto"):
-    """ChebExpCos radial table and derivative (reference ``execution_plan.py:7298-7379``)."""
+    """ChebExpCos radial table and derivative (reference ``execution_plan.py:7298-7379``):
+    ``radii [E]`` to values and ``d/dr`` ``[E, maximum_radial_index + 1]``."""
     _backend(backend, {"auto", "native"})
     maximum_radial_index = int(maximum_radial_index)
     if maximum_radial_index < 0:
         raise ValueError("maximum_radial_index must be non-negative")
-    _require_device(radii, "cheb_exp_cos_radial_table_with_derivative")
-    return native.radial_table(radii.contiguous(), cutoffs.contiguous(), lambdas.contiguous(),
-                               maximum_radial_index)
+    radii, cutoffs, lambdas = _radial_operands(radii, cutoffs, lambdas, "cheb_exp_cos_radial_table_with_derivative")
+    return native.radial_table(radii, cutoffs, lambdas, maximum_radial_index)
+
+
+def cheb_exp_cos_radial_with_derivative(radii, cutoffs, lambdas, radial_index, backend="auto"):
+    """One ChebExpCos radial function and its ``d/dr`` (reference
+    ``execution_plan.py:7220-7295``), elementwise over ``radii`` of any shape:
+    column ``radial_index`` of the HIP radial table."""
+    _backend(backend, {"auto", "native"})
+    radial_index = int(radial_index)
+    if radial_index < 0:
+        raise ValueError("radial_index must be non-negative")
+    radii, cutoffs, lambdas = _radial_operands(radii, cutoffs, lambdas, "cheb_exp_cos_radial_with_derivative")
+    v, d = native.radial_table(radii.reshape(-1), cutoffs.reshape(-1), lambdas.reshape(-1), radial_index)
+    return v[:, radial_index].reshape(radii.shape), d[:, radial_index].reshape(radii.shape)
 
 
 def _complex_rows(l_max):
@@ -153,6 +182,23 @@ def spherical_harmonics_table_with_derivative(edge_vectors, maximum_angular_mome
     if real_output:
         return v, g
     return complex_from_real_table(v, g, maximum_angular_momentum)
+
+
+def spherical_harmonics_with_derivative(edge_vectors, angular_momentum, *, real_output=False, epsilon=1.0e-12,
+                                        backend="auto"):
+    """Harmonics of one ``l`` and their Cartesian gradient (reference
+    ``execution_plan.py:7381-7476``): ``[E, 2l + 1]`` and ``[E, 2l + 1, 3]``,
+    real or complex as in :func:`spherical_harmonics_table_with_derivative`,
+    whose columns ``l^2 .. (l + 1)^2 - 1`` they are."""
+    import torch
+
+    angular_momentum = int(angular_momentum)
+    if angular_momentum < 0:
+        raise ValueError("angular_momentum must be non-negative")
+    v, g = spherical_harmonics_table_with_derivative(torch.as_tensor(edge_vectors), angular_momentum,
+                                                     real_output=real_output, epsilon=epsilon, backend=backend)
+    lo = angular_momentum * angular_momentum
+    return v[:, lo:].contiguous(), g[:, lo:].contiguous()
 
 
 def validate_density_csr(row_offsets, neighbors, atom_count, edge_count, *, species=None, species_count=None):

@@ -14,7 +14,8 @@ device, so a call with device tensors runs this library's kernels.
   with the reference's exact signatures, together with fake implementations
   and the first-order autograd formulas of the forward operators (backward =
   the reference's adjoint operator).
-* Operators covered: the radial and real-harmonic tables, density
+* Operators covered: the radial function and table, the harmonics of one
+  ``l`` and the harmonic table (real and complex output), density
   accumulation and its adjoint, the symmetric-power monomial and
   shared-monomial contractions and adjoints, the sparse shared-monomial
   contraction with its adjoint and double backward, and the factorized-angular
@@ -36,9 +37,15 @@ NAMESPACE = "ye3t_runtime"
 
 # name -> schema (the reference's, execution_plan_torch.cpp line cited per entry)
 SCHEMAS = {
+    # :7235
+    "cheb_exp_cos_radial_with_derivative":
+        "(Tensor radii, Tensor cutoffs, Tensor lambdas, int radial_index) -> (Tensor, Tensor)",
     # :7238
     "cheb_exp_cos_radial_table_with_derivative":
         "(Tensor radii, Tensor cutoffs, Tensor lambdas, int maximum_radial_index) -> (Tensor, Tensor)",
+    # :7247
+    "spherical_harmonics_with_derivative":
+        "(Tensor edge_vectors, int angular_momentum, bool real_output, float epsilon) -> (Tensor, Tensor)",
     # :7251
     "spherical_harmonics_table_with_derivative":
         "(Tensor edge_vectors, int maximum_angular_momentum, bool real_output, float epsilon) -> (Tensor, Tensor)",
@@ -215,6 +222,19 @@ def _k_radial(radii, cutoffs, lambdas, maximum_radial_index):
     return v, d
 
 
+def _k_radial_one(radii, cutoffs, lambdas, radial_index):
+    from ye3t_amd import runtime
+
+    return runtime.cheb_exp_cos_radial_with_derivative(radii, cutoffs, lambdas, int(radial_index))
+
+
+def _k_sph_one(edge_vectors, angular_momentum, real_output, epsilon):
+    from ye3t_amd import runtime
+
+    return runtime.spherical_harmonics_with_derivative(edge_vectors, angular_momentum,
+                                                       real_output=bool(real_output), epsilon=float(epsilon))
+
+
 def _k_sph(edge_vectors, maximum_angular_momentum, real_output, epsilon):
     from ye3t_amd import runtime
 
@@ -330,6 +350,8 @@ def _k_seg_adjoint(output_adjoint, packed_slots, *rest):
 KERNELS = {
     "cheb_exp_cos_radial_table_with_derivative": _k_radial,
     "spherical_harmonics_table_with_derivative": _k_sph,
+    "cheb_exp_cos_radial_with_derivative": _k_radial_one,
+    "spherical_harmonics_with_derivative": _k_sph_one,
     "density_accumulate": _k_density,
     "density_accumulate_adjoint": _k_density_adjoint,
     "symmetric_power_monomial": _k_monomial,
@@ -355,6 +377,20 @@ KERNELS = {
 def _f_radial(radii, cutoffs, lambdas, maximum_radial_index):
     shape = (radii.shape[0], int(maximum_radial_index) + 1)
     return radii.new_empty(shape), radii.new_empty(shape)
+
+
+def _f_radial_one(radii, cutoffs, lambdas, radial_index):
+    return radii.new_empty(radii.shape), radii.new_empty(radii.shape)
+
+
+def _f_sph_one(edge_vectors, angular_momentum, real_output, epsilon):
+    import torch
+
+    width = 2 * int(angular_momentum) + 1
+    dt = edge_vectors.dtype if real_output else (torch.complex64 if edge_vectors.dtype == torch.float32
+                                                 else torch.complex128)
+    values = edge_vectors.new_empty((edge_vectors.shape[0], width), dtype=dt)
+    return values, values.new_empty((edge_vectors.shape[0], width, 3))
 
 
 def _f_sph(edge_vectors, maximum_angular_momentum, real_output, epsilon):
@@ -411,6 +447,8 @@ def _f_fa_linear_adjoint(output_adjoint, packed_slots, *rest):
 FAKES = {
     "cheb_exp_cos_radial_table_with_derivative": _f_radial,
     "spherical_harmonics_table_with_derivative": _f_sph,
+    "cheb_exp_cos_radial_with_derivative": _f_radial_one,
+    "spherical_harmonics_with_derivative": _f_sph_one,
     "density_accumulate": _f_density,
     "density_accumulate_adjoint": _f_density_adjoint,
     "symmetric_power_monomial": _f_monomial,
