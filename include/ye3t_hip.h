@@ -83,6 +83,30 @@ int ye3t_hip_radial_table(int dtype, const void* radii, const void* cutoffs, con
 int ye3t_hip_real_sph_table(int dtype, const void* edge_vectors, int64_t edge_count, int64_t l_max,
                             double epsilon, void* values, void* gradients, ye3t_stream_t stream);
 
+/* Scheduled radial-angular edge channels and their Cartesian derivatives:
+ * edge_values[e, k] = channel_scales[k] * R[e, ri_k] * Y[e, ai_k] where
+ * channel_types[k] is -1 or edge_types[e] (zero otherwise), and
+ * edge_derivatives[e, k, :] = channel_scales[k] * (dR[e, ri_k] *
+ * radial_directions[e, :] * Y[e, ai_k] + R[e, ri_k] * dY[e, ai_k, :]), from the
+ * radial table R, dR [E, radial_width], the angular table Y [E, angular_width]
+ * with dY [E, angular_width, 3] and unit directions [E, 3].  Rounded as the
+ * reference core rounds (ye3t_runtime_core.cpp:1550-1604): bit-identical.
+ * Channel indices must lie in their tables and types be >= -1 (checked by the
+ * caller; the kernel clamps indices instead of faulting).  Replaces
+ * ye3t_runtime::scheduled_radial_angular_channels_with_derivative (schema
+ * execution_plan_torch.cpp:7268-7274, CPU execution_plan_torch.cpp:1230-1336,
+ * CUDA kernel execution_plan_cuda.cu:4568, launcher :9946-10060). */
+int ye3t_hip_scheduled_radial_angular_channels(int dtype, int64_t edge_count, int64_t radial_width,
+                                               int64_t angular_width, int64_t channel_count,
+                                               const void* radial_values, const void* radial_derivatives,
+                                               const void* angular_values, const void* angular_derivatives,
+                                               const void* radial_directions, const int64_t* edge_types,
+                                               const int64_t* channel_radial_indices,
+                                               const int64_t* channel_angular_indices,
+                                               const int64_t* channel_types, const void* channel_scales,
+                                               void* edge_values, void* edge_derivatives,
+                                               ye3t_stream_t stream);
+
 /* out[i, c] = sum over edges e in [row_offsets[i], row_offsets[i+1]) of
  * edge_values[e, c]; deterministic CSR segment reduction, no atomics.
  * Replaces ye3t_runtime::density_accumulate (schema execution_plan_torch.cpp:7284-7286,

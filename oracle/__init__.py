@@ -43,6 +43,8 @@ def lib():
         L.oracle_real_sph_table.argtypes = [_d, _I, _I, ctypes.c_double, _d, _d]
         L.oracle_density_accumulate.argtypes = [_d, _i64, _I, _I, _I, _d]
         L.oracle_density_accumulate_adjoint.argtypes = [_d, _i64, _I, _I, _d]
+        L.oracle_scheduled_channels.argtypes = [_d, _d, _d, _d, _d, _i64, _i64, _i64, _i64, _d, _I, _I, _I, _I,
+                                                _d, _d]
         L.oracle_ace_density_edge_gradient.argtypes = [_I, _I, _i64, _i64, _d, _i32, _d, _d, _I, _I, _I,
                                                        ctypes.c_double, ctypes.c_double, ctypes.c_double, _d, _d]
         L.oracle_ace_density.argtypes = [_I, _I, _i64, _i64, _d, _i32, _d, _d, _I, _I, _I,
@@ -70,6 +72,9 @@ def ref_lib():
         if hasattr(_REF, "ref_density_accumulate_adjoint"):
             _REF.ref_density_accumulate_adjoint.argtypes = [_d, _i64, _I, _I, _d]
         _REF.ref_symmetric_power_monomial.argtypes = [_d, _I, _I, _i64, _i64, _d, _I, _I, _d]
+        if hasattr(_REF, "ref_scheduled_channels"):
+            _REF.ref_scheduled_channels.argtypes = [_d, _d, _d, _d, _d, _i64, _i64, _i64, _i64, _d, _I, _I, _I, _I,
+                                                    _d, _d]
     return _REF
 
 
@@ -116,6 +121,26 @@ def real_sph_table(vectors, l_max, epsilon=1e-12, *, use_reference=False):
     else:
         lib().oracle_real_sph_table(_p(vectors), E, l_max, epsilon, _p(v), _p(g))
     return v, g
+
+
+def scheduled_channels(radial_values, radial_derivatives, angular_values, angular_derivatives, radial_directions,
+                       edge_types, channel_radial_indices, channel_angular_indices, channel_types, channel_scales,
+                       *, use_reference=False):
+    """Scheduled radial-angular edge channels ``(values [E, K], derivatives [E, K, 3])``
+    (``ye3t_runtime_core.cpp:1550-1604``); ``use_reference`` runs the reference core in ``_ref``."""
+    rv, rd = _f64(radial_values), _f64(radial_derivatives)
+    av, ad, dr = _f64(angular_values), _f64(angular_derivatives), _f64(radial_directions)
+    et, cri, cai, ct = (_i64a(a) for a in (edge_types, channel_radial_indices, channel_angular_indices,
+                                           channel_types))
+    cs = _f64(channel_scales)
+    E, NR = rv.shape
+    NA, K = av.shape[1], cs.shape[0]
+    v = np.zeros((E, K))
+    d = np.zeros((E, K, 3))
+    f = ref_lib().ref_scheduled_channels if use_reference else lib().oracle_scheduled_channels
+    f(_p(rv), _p(rd), _p(av), _p(ad), _p(dr), _p(et, _i64), _p(cri, _i64), _p(cai, _i64), _p(ct, _i64), _p(cs),
+      E, NR, NA, K, _p(v), _p(d))
+    return v, d
 
 
 def density_accumulate(edge_values, centers, atom_count, *, use_reference=False):

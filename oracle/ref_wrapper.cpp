@@ -48,6 +48,13 @@ void ref_radial_table(const double* r, const double* c, const double* l, int64_t
 void ref_real_sph_table(const double* vec, int64_t e, int64_t lmax, double eps, double* v, double* d) {
   ye3t::runtime::real_spherical_harmonics_table_with_derivative<double>(vec, e, lmax, eps, v, d);
 }
+void ref_scheduled_channels(const double* rv, const double* rd, const double* av, const double* ad,
+                            const double* dir, const int64_t* et, const int64_t* cri, const int64_t* cai,
+                            const int64_t* ct, const double* cs, int64_t e, int64_t nr, int64_t na, int64_t k,
+                            double* v, double* d) {
+  ye3t::runtime::scheduled_radial_angular_channels_with_derivative<double>(rv, rd, av, ad, dir, et, cri, cai, ct, cs,
+                                                                           e, nr, na, k, v, d);
+}
 void ref_density_accumulate(const double* ev, const int64_t* centers, int64_t e, int64_t c, int64_t n,
                             double* out) {
   ye3t::runtime::density_accumulate_forward<double>(ev, centers, e, c, n, out);

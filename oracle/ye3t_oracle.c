@@ -6,7 +6,7 @@
  * nothing in the product library links, loads or calls it.
  *
  * Each function cites the reference routine it restates:
- *   ye3t/runtime/csrc/ye3t_runtime_core.cpp   (radial, real SH, density, monomials)
+ *   ye3t/runtime/csrc/ye3t_runtime_core.cpp   (radial, real SH, scheduled edge channels, density, monomials)
  *   ye3t/core/csrc/factorized_runtime.cpp     (componentwise schedule evaluation)
  */
 #include <math.h>
@@ -209,6 +209,32 @@ void oracle_density_accumulate_adjoint(const double* atomic_adjoint, const int64
     const double* src = atomic_adjoint + centers[e] * channel_count;
     double* dst = edge_adjoint + e * channel_count;
     for (int64_t c = 0; c < channel_count; ++c) dst[c] = src[c];
+  }
+}
+
+/* Scheduled radial-angular edge channels and their Cartesian derivatives
+ * (ye3t_runtime_core.cpp:1550-1604): channel k of edge e is
+ * scale_k R[e, ri_k] Y[e, ai_k] (products left to right) when channel_types[k]
+ * is negative or equals edge_types[e], zero otherwise; the derivative is
+ * scale_k (dR dir Y + R dY) per axis, in that order. */
+void oracle_scheduled_channels(const double* rv, const double* rd, const double* av, const double* ad,
+                               const double* dir, const int64_t* edge_types, const int64_t* cri,
+                               const int64_t* cai, const int64_t* ctype, const double* cscale, int64_t edge_count,
+                               int64_t radial_width, int64_t angular_width, int64_t channel_count,
+                               double* values, double* derivs) {
+  for (int64_t e = 0; e < edge_count; ++e) {
+    for (int64_t k = 0; k < channel_count; ++k) {
+      const int64_t o = e * channel_count + k;
+      if (ctype[k] >= 0 && edge_types[e] != ctype[k]) {
+        values[o] = 0.0;
+        derivs[3 * o] = derivs[3 * o + 1] = derivs[3 * o + 2] = 0.0;
+        continue;
+      }
+      const int64_t r_at = e * radial_width + cri[k], a_at = e * angular_width + cai[k];
+      const double r = rv[r_at], a = av[a_at], sc = cscale[k];
+      values[o] = sc * r * a;
+      for (int x = 0; x < 3; ++x) derivs[3 * o + x] = sc * (rd[r_at] * dir[3 * e + x] * a + r * ad[3 * a_at + x]);
+    }
   }
 }
 

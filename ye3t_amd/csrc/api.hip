@@ -74,6 +74,44 @@ __global__ __launch_bounds__(256) void radial_table_kernel(const Real* __restric
   }
 }
 
+// Scheduled radial-angular edge channels: output (e, k) is
+// scale_k R[e, ri_k] Y[e, ai_k] when channel k takes every edge type
+// (type -1) or edge e's type, zero otherwise, with its Cartesian derivative
+// scale_k (dR[e, ri_k] dir[e] Y[e, ai_k] + R[e, ri_k] dY[e, ai_k]).  One thread
+// per output.  The products are rounded in the reference core's order
+// (ye3t_runtime_core.cpp:1550-1604) with no fused multiply-adds, so the
+// results are the core's bit for bit.  Indices are validated by the caller;
+// the kernel clamps them into the tables rather than faulting.
+template <typename Real>
+__global__ __launch_bounds__(256) void scheduled_channels_kernel(
+    const Real* __restrict__ rv, const Real* __restrict__ rd, const Real* __restrict__ av,
+    const Real* __restrict__ ad, const Real* __restrict__ dir, const int64_t* __restrict__ edge_types,
+    const int64_t* __restrict__ cri, const int64_t* __restrict__ cai, const int64_t* __restrict__ ctype,
+    const Real* __restrict__ cscale, int64_t E, int64_t NR, int64_t NA, int64_t K, Real* __restrict__ values,
+    Real* __restrict__ derivs) {
+#pragma clang fp contract(off)
+  const int64_t total = E * K;
+  for (int64_t o = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; o < total; o += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t e = o / K, k = o - e * K;
+    const int64_t t = ctype[k];
+    Real* const d = derivs + 3 * o;
+    if (t >= 0 && edge_types[e] != t) {
+      values[o] = Real(0);
+      d[0] = d[1] = d[2] = Real(0);
+      continue;
+    }
+    int64_t ri = cri[k], ai = cai[k];
+    ri = ri < 0 ? 0 : (ri >= NR ? NR - 1 : ri);
+    ai = ai < 0 ? 0 : (ai >= NA ? NA - 1 : ai);
+    const Real r = rv[e * NR + ri], a = av[e * NA + ai], sc = cscale[k];
+    const Real dr = rd[e * NR + ri];
+    values[o] = sc * r * a;
+    const Real* const ya = ad + 3 * (e * NA + ai);
+    const Real* const u = dir + 3 * e;
+    for (int x = 0; x < 3; ++x) d[x] = sc * (dr * u[x] * a + r * ya[x]);
+  }
+}
+
 // Real SH table with optional Cartesian gradient.  Gradients w.r.t. the unit
 // vector use d/dz Q_l^m = Q_l^{m+1}, projected with (I - u u^T)/|r|
 // (reference ye3t_runtime_core.cpp:226-286, 808-843).
@@ -286,6 +324,45 @@ int ye3t_hip_radial_table(int dtype, const void* radii, const void* cutoffs, con
     return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);
   }
   return check_launch("radial_table_kernel");
+}
+
+int ye3t_hip_scheduled_radial_angular_channels(int dtype, int64_t edge_count, int64_t radial_width,
+                                               int64_t angular_width, int64_t channel_count,
+                                               const void* radial_values, const void* radial_derivatives,
+                                               const void* angular_values, const void* angular_derivatives,
+                                               const void* radial_directions, const int64_t* edge_types,
+                                               const int64_t* channel_radial_indices,
+                                               const int64_t* channel_angular_indices,
+                                               const int64_t* channel_types, const void* channel_scales,
+                                               void* edge_values, void* edge_derivatives, ye3t_stream_t stream) {
+  clear_error();
+  YE3T_REQUIRE(edge_count >= 0 && channel_count >= 0, "edge and channel counts must be non-negative");
+  if (edge_count == 0 || channel_count == 0) return YE3T_OK;
+  YE3T_REQUIRE(radial_width > 0 && angular_width > 0, "radial and angular tables must not be empty");
+  YE3T_REQUIRE(edge_count <= INT64_MAX / channel_count / 3, "edge_count * channel_count overflows");
+  YE3T_REQUIRE(radial_values && radial_derivatives && angular_values && angular_derivatives && radial_directions &&
+                   edge_types && channel_radial_indices && channel_angular_indices && channel_types &&
+                   channel_scales && edge_values && edge_derivatives,
+               "NULL input or output");
+  const unsigned grid = grid_for(edge_count * channel_count, 256);
+  if (dtype == YE3T_F64) {
+    hipLaunchKernelGGL(scheduled_channels_kernel<double>, dim3(grid), dim3(256), 0, as_stream(stream),
+                       (const double*)radial_values, (const double*)radial_derivatives,
+                       (const double*)angular_values, (const double*)angular_derivatives,
+                       (const double*)radial_directions, edge_types, channel_radial_indices,
+                       channel_angular_indices, channel_types, (const double*)channel_scales, edge_count,
+                       radial_width, angular_width, channel_count, (double*)edge_values, (double*)edge_derivatives);
+  } else if (dtype == YE3T_F32) {
+    hipLaunchKernelGGL(scheduled_channels_kernel<float>, dim3(grid), dim3(256), 0, as_stream(stream),
+                       (const float*)radial_values, (const float*)radial_derivatives,
+                       (const float*)angular_values, (const float*)angular_derivatives,
+                       (const float*)radial_directions, edge_types, channel_radial_indices,
+                       channel_angular_indices, channel_types, (const float*)channel_scales, edge_count,
+                       radial_width, angular_width, channel_count, (float*)edge_values, (float*)edge_derivatives);
+  } else {
+    return set_error(YE3T_EDTYPE, "unsupported dtype %d", dtype);
+  }
+  return check_launch("scheduled_channels_kernel");
 }
 
 int ye3t_hip_real_sph_table(int dtype, const void* vec, int64_t E, int64_t lmax, double eps, void* values,

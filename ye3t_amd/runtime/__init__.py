@@ -23,6 +23,7 @@ REFERENCE_OPERATIONS = (
     "real_spherical_harmonics_with_derivative",
     "complex_spherical_harmonics_table_with_derivative",
     "real_spherical_harmonics_table_with_derivative",
+    "scheduled_radial_angular_channels_with_derivative",
     "density_accumulate",
     "density_accumulate_adjoint",
     "symmetric_power_monomial",
@@ -199,6 +200,37 @@ def spherical_harmonics_with_derivative(edge_vectors, angular_momentum, *, real_
                                                      real_output=real_output, epsilon=epsilon, backend=backend)
     lo = angular_momentum * angular_momentum
     return v[:, lo:].contiguous(), g[:, lo:].contiguous()
+
+
+def scheduled_radial_angular_channels_with_derivative(radial_values, radial_derivatives, angular_values,
+                                                      angular_derivatives, radial_directions, edge_types,
+                                                      channel_radial_indices, channel_angular_indices,
+                                                      channel_types, channel_scales, backend="auto"):
+    """Scheduled radial-angular edge channels and their Cartesian derivatives
+    (reference ``execution_plan.py:7675-7787``; CPU core
+    ``ye3t_runtime_core.cpp:1550-1604``): ``(edge_values [E, K],
+    edge_derivatives [E, K, 3])`` from the radial and angular tables, each
+    channel ``k`` taking radial column ``channel_radial_indices[k]``, angular
+    column ``channel_angular_indices[k]``, edges of type ``channel_types[k]``
+    (all edges for -1) and the factor ``channel_scales[k]``.  Bit-identical to
+    the reference core.  Data arguments are converted to ``radial_values``'s
+    dtype and device and the index arguments to int64, as the reference does."""
+    import torch
+
+    _backend(backend, {"auto", "native"})
+    radial_values = torch.as_tensor(radial_values)
+    _require_device(radial_values, "scheduled_radial_angular_channels_with_derivative")
+    dev, dt = radial_values.device, radial_values.dtype
+    (radial_derivatives, angular_values, angular_derivatives, radial_directions, channel_scales) = (
+        torch.as_tensor(t, dtype=dt, device=dev) for t in (radial_derivatives, angular_values, angular_derivatives,
+                                                           radial_directions, channel_scales))
+    (edge_types, channel_radial_indices, channel_angular_indices, channel_types) = (
+        torch.as_tensor(t, dtype=torch.int64, device=dev) for t in (edge_types, channel_radial_indices,
+                                                                    channel_angular_indices, channel_types))
+    return native.scheduled_radial_angular_channels(radial_values, radial_derivatives, angular_values,
+                                                    angular_derivatives, radial_directions, edge_types,
+                                                    channel_radial_indices, channel_angular_indices, channel_types,
+                                                    channel_scales)
 
 
 def validate_density_csr(row_offsets, neighbors, atom_count, edge_count, *, species=None, species_count=None):

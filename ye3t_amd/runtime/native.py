@@ -102,6 +102,7 @@ def lib():
     L.ye3t_hip_device_caps.argtypes = [ctypes.c_int, ctypes.POINTER(Caps)]
     L.ye3t_hip_radial_table.argtypes = [ctypes.c_int, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp]
     L.ye3t_hip_real_sph_table.argtypes = [ctypes.c_int, _vp, _i64, _i64, ctypes.c_double, _vp, _vp, _vp]
+    L.ye3t_hip_scheduled_radial_angular_channels.argtypes = [ctypes.c_int, _i64, _i64, _i64, _i64] + [_vp] * 13
     L.ye3t_hip_density_accumulate_csr.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _vp]
     L.ye3t_hip_density_accumulate_adjoint.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _i64, _vp, _vp]
     L.ye3t_hip_ace_density_forward.argtypes = [ctypes.POINTER(DensityArgs), _vp, _vp]
@@ -197,7 +198,7 @@ def lib():
 
 EXPORTED_SYMBOLS = (
     "ye3t_hip_abi_version", "ye3t_hip_has_hip", "ye3t_hip_has_cpu", "ye3t_hip_last_error", "ye3t_hip_device_caps", "ye3t_hip_radial_table",
-    "ye3t_hip_real_sph_table", "ye3t_hip_density_accumulate_csr", "ye3t_hip_ace_density_forward",
+    "ye3t_hip_real_sph_table", "ye3t_hip_scheduled_radial_angular_channels", "ye3t_hip_density_accumulate_csr", "ye3t_hip_ace_density_forward",
     "ye3t_hip_symmetric_power_monomial", "ye3t_hip_evaluate_factorized_schedule",
     "ye3t_hip_product_plan_create", "ye3t_hip_product_plan_destroy", "ye3t_hip_product_forward",
     "ye3t_hip_product_launch_info", "ye3t_hip_rtc_compile", "ye3t_hip_rtc_fingerprint", "ye3t_hip_free",
@@ -298,6 +299,63 @@ def radial_table(radii, cutoffs, lambdas, n_max, with_derivative=True):
     _check(lib().ye3t_hip_radial_table(_dtype_code(radii), _dev(radii, "radii"), _dev(cutoffs, "cutoffs"),
                                        _dev(lambdas, "lambdas"), E, int(n_max), _dev(values, "values"),
                                        _opt(derivs, "derivatives"), _stream()), "ye3t_hip_radial_table")
+    return values, derivs
+
+
+def scheduled_radial_angular_channels(radial_values, radial_derivatives, angular_values, angular_derivatives,
+                                      radial_directions, edge_types, channel_radial_indices,
+                                      channel_angular_indices, channel_types, channel_scales):
+    """``ye3t_hip_scheduled_radial_angular_channels`` with the reference's
+    argument checks and messages (``execution_plan_torch.cpp:1241-1305``);
+    the index ranges are checked by one device reduction each.  Returns
+    ``(edge_values [E, K], edge_derivatives [E, K, 3])``."""
+    import torch
+
+    data = (radial_values, radial_derivatives, angular_values, angular_derivatives, radial_directions,
+            channel_scales)
+    dtype = radial_values.dtype
+    if dtype not in (torch.float32, torch.float64):
+        raise ValueError("scheduled radial-angular channels require float32 or float64")
+    if any(t.dtype != dtype for t in data):
+        raise ValueError("scheduled radial-angular data tensors must share one dtype")
+    idx = (edge_types, channel_radial_indices, channel_angular_indices, channel_types)
+    if any(t.dtype != torch.int64 or t.ndim != 1 for t in idx):
+        raise ValueError("edge_types and the channel schedule arrays must be int64 vectors")
+    if radial_values.ndim != 2 or angular_values.ndim != 2 or channel_scales.ndim != 1:
+        raise ValueError("radial_values and angular_values must be [edge_count, width], channel_scales a vector")
+    E, NR = (int(v) for v in radial_values.shape)
+    NA, K = int(angular_values.shape[1]), int(channel_scales.numel())
+    if tuple(radial_derivatives.shape) != (E, NR):
+        raise ValueError("radial derivatives must match radial values")
+    if tuple(angular_derivatives.shape) != (E, NA, 3):
+        raise ValueError("angular derivatives must have shape [edge_count, angular_width, 3]")
+    if int(angular_values.shape[0]) != E:
+        raise ValueError("radial and angular tables must share one edge axis")
+    if tuple(radial_directions.shape) != (E, 3):
+        raise ValueError("radial directions must have shape [edge_count, 3]")
+    if int(edge_types.numel()) != E:
+        raise ValueError("edge_types must have length edge_count")
+    if not (channel_radial_indices.numel() == channel_angular_indices.numel() == channel_types.numel() == K):
+        raise ValueError("channel schedule arrays must have length channel_count")
+    if K > 0:
+        if int(channel_radial_indices.min()) < 0 or int(channel_radial_indices.max()) >= NR:
+            raise ValueError("channel radial indices must lie in the radial table")
+        if int(channel_angular_indices.min()) < 0 or int(channel_angular_indices.max()) >= NA:
+            raise ValueError("channel angular indices must lie in the angular table")
+        if int(channel_types.min()) < -1:
+            raise ValueError("channel types must be -1 or a nonnegative edge type")
+    values = torch.empty((E, K), dtype=dtype, device=radial_values.device)
+    derivs = torch.empty((E, K, 3), dtype=dtype, device=radial_values.device)
+    inputs = [t.contiguous() for t in (radial_values, radial_derivatives, angular_values, angular_derivatives,
+                                        radial_directions, edge_types, channel_radial_indices,
+                                        channel_angular_indices, channel_types, channel_scales)]
+    args = [_dev(t, n) for t, n in zip(inputs, (
+        "radial_values", "radial_derivatives", "angular_values", "angular_derivatives", "radial_directions",
+        "edge_types", "channel_radial_indices", "channel_angular_indices", "channel_types", "channel_scales"))]
+    _check(lib().ye3t_hip_scheduled_radial_angular_channels(_dtype_code(radial_values), E, NR, NA, K, *args,
+                                                            _dev(values, "edge_values"),
+                                                            _dev(derivs, "edge_derivatives"), _stream()),
+           "ye3t_hip_scheduled_radial_angular_channels")
     return values, derivs
 
 

@@ -15,8 +15,8 @@ device, so a call with device tensors runs this library's kernels.
   and the first-order autograd formulas of the forward operators (backward =
   the reference's adjoint operator).
 * Operators covered: the radial function and table, the harmonics of one
-  ``l`` and the harmonic table (real and complex output), density
-  accumulation and its adjoint, the symmetric-power monomial and
+  ``l`` and the harmonic table (real and complex output), the scheduled
+  radial-angular edge channels, density accumulation and its adjoint, the symmetric-power monomial and
   shared-monomial contractions and adjoints, the sparse shared-monomial
   contraction with its adjoint and double backward, and the factorized-angular
   forward / adjoint / linear readout / heterogeneous / segmented operators.
@@ -49,6 +49,11 @@ SCHEMAS = {
     # :7251
     "spherical_harmonics_table_with_derivative":
         "(Tensor edge_vectors, int maximum_angular_momentum, bool real_output, float epsilon) -> (Tensor, Tensor)",
+    # :7268
+    "scheduled_radial_angular_channels_with_derivative":
+        "(Tensor radial_values, Tensor radial_derivatives, Tensor angular_values, Tensor angular_derivatives, "
+        "Tensor radial_directions, Tensor edge_types, Tensor channel_radial_indices, "
+        "Tensor channel_angular_indices, Tensor channel_types, Tensor channel_scales) -> (Tensor, Tensor)",
     # :7285, :7288
     "density_accumulate": "(Tensor edge_values, Tensor centers, int atom_count) -> Tensor",
     "density_accumulate_adjoint": "(Tensor atomic_adjoint, Tensor centers) -> Tensor",
@@ -235,6 +240,10 @@ def _k_sph_one(edge_vectors, angular_momentum, real_output, epsilon):
                                                        real_output=bool(real_output), epsilon=float(epsilon))
 
 
+def _k_scheduled(*args):
+    return native.scheduled_radial_angular_channels(*args)
+
+
 def _k_sph(edge_vectors, maximum_angular_momentum, real_output, epsilon):
     from ye3t_amd import runtime
 
@@ -352,6 +361,7 @@ KERNELS = {
     "spherical_harmonics_table_with_derivative": _k_sph,
     "cheb_exp_cos_radial_with_derivative": _k_radial_one,
     "spherical_harmonics_with_derivative": _k_sph_one,
+    "scheduled_radial_angular_channels_with_derivative": _k_scheduled,
     "density_accumulate": _k_density,
     "density_accumulate_adjoint": _k_density_adjoint,
     "symmetric_power_monomial": _k_monomial,
@@ -391,6 +401,12 @@ def _f_sph_one(edge_vectors, angular_momentum, real_output, epsilon):
                                                  else torch.complex128)
     values = edge_vectors.new_empty((edge_vectors.shape[0], width), dtype=dt)
     return values, values.new_empty((edge_vectors.shape[0], width, 3))
+
+
+def _f_scheduled(radial_values, radial_derivatives, angular_values, angular_derivatives, radial_directions,
+                 edge_types, channel_radial_indices, channel_angular_indices, channel_types, channel_scales):
+    E, K = radial_values.shape[0], channel_scales.numel()
+    return radial_values.new_empty((E, K)), radial_values.new_empty((E, K, 3))
 
 
 def _f_sph(edge_vectors, maximum_angular_momentum, real_output, epsilon):
@@ -449,6 +465,7 @@ FAKES = {
     "spherical_harmonics_table_with_derivative": _f_sph,
     "cheb_exp_cos_radial_with_derivative": _f_radial_one,
     "spherical_harmonics_with_derivative": _f_sph_one,
+    "scheduled_radial_angular_channels_with_derivative": _f_scheduled,
     "density_accumulate": _f_density,
     "density_accumulate_adjoint": _f_density_adjoint,
     "symmetric_power_monomial": _f_monomial,
