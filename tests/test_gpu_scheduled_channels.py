@@ -90,3 +90,36 @@ def test_scheduled_channels_empty_and_refused(gpu):
     case["channel_angular_indices"] = case["channel_angular_indices"] + 100
     with pytest.raises(ValueError, match="channel angular indices must lie in the angular table"):
         runtime.scheduled_radial_angular_channels_with_derivative(*case.values())
+
+
+def test_scheduled_channels_autograd(gpu):
+    """The Torch operator's backward: gradients in the radial table, the
+    angular table and the channel scales equal autograd through the
+    reference's value formula (``execution_plan.py:7007-7033``) in fp64, the
+    derivative output is not differentiable, and ``opcheck`` passes."""
+    flush("scheduled channels: autograd and opcheck")
+    import torch
+
+    from ye3t_amd.runtime import torch_ops
+
+    torch_ops.register()
+    op = torch.ops.ye3t_runtime.scheduled_radial_angular_channels_with_derivative
+    case = _device_case(_case(6, E=64, K=17), torch.float64, gpu)
+    leaves = {k: case[k].clone().requires_grad_(True) for k in ("radial_values", "angular_values", "channel_scales")}
+    args = dict(case, **leaves)
+    values, derivs = op(*args.values())
+    assert not derivs.requires_grad
+    w = torch.randn_like(values)
+    got = torch.autograd.grad((values * w).sum(), tuple(leaves.values()))
+    ref_leaves = {k: case[k].clone().requires_grad_(True) for k in leaves}
+    act = ((case["channel_types"] < 0).unsqueeze(0)
+           | (case["edge_types"].unsqueeze(1) == case["channel_types"].unsqueeze(0))).to(torch.float64)
+    ref_values = (ref_leaves["radial_values"].index_select(1, case["channel_radial_indices"])
+                  * ref_leaves["angular_values"].index_select(1, case["channel_angular_indices"])
+                  * act * ref_leaves["channel_scales"].unsqueeze(0))
+    torch.testing.assert_close(values, ref_values.detach(), rtol=1e-14, atol=1e-14)
+    want = torch.autograd.grad((ref_values * w).sum(), tuple(ref_leaves.values()))
+    for g, r in zip(got, want):
+        torch.testing.assert_close(g, r, rtol=1e-13, atol=1e-13)
+    result = torch.library.opcheck(op.default, tuple(args.values()), raise_exception=False)
+    assert all(v == "SUCCESS" for v in result.values()), result

@@ -563,7 +563,42 @@ def _bw_fa_linear(ctx, grad):
     return (gx,) + (None,) * 13 + (gw, gb.reshape(bias.shape))
 
 
+def _setup_scheduled(ctx, inputs, output):
+    _setup_saving_inputs(ctx, inputs, output)
+    ctx.mark_non_differentiable(output[1])
+
+
+def _bw_scheduled(ctx, values_adjoint, derivatives_adjoint):
+    """Gradients of the channel values in the radial table, the angular table
+    and the channel scales (the derivative output is not differentiable), as
+    the reference's formula (``execution_plan.py:3054-3151``) gives them."""
+    import torch
+
+    (radial_values, _, angular_values, _, _, edge_types, channel_radial_indices, channel_angular_indices,
+     channel_types, channel_scales) = _inputs(ctx)
+    if values_adjoint is None:
+        return (None,) * 10
+    active = ((channel_types < 0).unsqueeze(0)
+              | (edge_types.unsqueeze(1) == channel_types.unsqueeze(0))).to(radial_values.dtype)
+    weighted = values_adjoint * active
+    radial = radial_values.index_select(1, channel_radial_indices)
+    angular = angular_values.index_select(1, channel_angular_indices)
+    g_radial = g_angular = g_scales = None
+    if ctx.needs_input_grad[0]:
+        g_radial = torch.zeros_like(radial_values).index_add_(1, channel_radial_indices,
+                                                              weighted * angular * channel_scales)
+    if ctx.needs_input_grad[2]:
+        g_angular = torch.zeros_like(angular_values).index_add_(1, channel_angular_indices,
+                                                                weighted * radial * channel_scales)
+    if ctx.needs_input_grad[9]:
+        g_scales = (weighted * radial * angular).sum(0)
+    return g_radial, None, g_angular, None, None, None, None, None, None, g_scales
+
+
+SETUPS = {"scheduled_radial_angular_channels_with_derivative": _setup_scheduled}
+
 BACKWARDS = {
+    "scheduled_radial_angular_channels_with_derivative": _bw_scheduled,
     "density_accumulate": _bw_density,
     "density_accumulate_adjoint": _bw_density_adjoint,
     "symmetric_power_monomial": _bw_monomial,
@@ -602,7 +637,7 @@ def register():
             torch.library.register_fake(f"{NAMESPACE}::{name}", FAKES[name], lib=lib_def)
             if name in BACKWARDS:
                 torch.library.register_autograd(f"{NAMESPACE}::{name}", BACKWARDS[name],
-                                                setup_context=_setup_saving_inputs, lib=lib_def)
+                                                setup_context=SETUPS.get(name, _setup_saving_inputs), lib=lib_def)
         _STATE["registered"] = True
         _STATE["defined"] = tuple(defined)
         return _STATE["defined"]
