@@ -209,6 +209,58 @@ def test_single_index_radial_and_harmonics(gpu):
             assert torch.equal(v, v2) and torch.equal(g, g2)
 
 
+def test_radial_and_harmonic_operators_differentiate(gpu):
+    """First-order autograd of the radial and harmonic operators: the
+    gradient in the radii / edge vectors equals central differences of the
+    operator's own values (fp64, real and complex harmonics, one index and
+    the table); a second derivative raises instead of dropping terms."""
+    flush("torch ops: radial and harmonic autograd")
+    import torch
+
+    ops = _ops()
+    rng = np.random.default_rng(11)
+    r = torch.as_tensor(rng.uniform(0.4, 4.5, size=30), device=gpu)
+    c, lam = torch.full_like(r, 5.0), torch.full_like(r, 1.5)
+    e = torch.as_tensor(rng.normal(size=(30, 3)), device=gpu)
+    h = 1e-6
+
+    def check(f, x, tol):
+        xg = x.clone().requires_grad_(True)
+        loss = f(xg)
+        (g,) = torch.autograd.grad(loss, xg)
+        fd = torch.zeros_like(x)
+        flat = fd.view(-1)
+        for i in range(x.numel()):
+            step = torch.zeros_like(x).view(-1)
+            step[i] = h
+            step = step.view(x.shape)
+            flat[i] = (f(x + step) - f(x - step)) / (2 * h)
+        torch.testing.assert_close(g, fd, rtol=tol, atol=tol)
+
+    w_tab = torch.as_tensor(rng.normal(size=(30, 8)), device=gpu)
+    check(lambda x: (ops.cheb_exp_cos_radial_table_with_derivative(x, c, lam, 7)[0] * w_tab).sum(), r, 1e-6)
+    check(lambda x: (ops.cheb_exp_cos_radial_with_derivative(x, c, lam, 5)[0] * w_tab[:, 0]).sum(), r, 1e-6)
+    w_sh = torch.as_tensor(rng.normal(size=(30, 16)), device=gpu)
+    w_im = torch.as_tensor(rng.normal(size=(30, 16)), device=gpu)
+    check(lambda x: (ops.spherical_harmonics_table_with_derivative(x, 3, True, 1e-12)[0] * w_sh).sum(), e, 1e-6)
+
+    def complex_loss(x):
+        y = ops.spherical_harmonics_table_with_derivative(x, 3, False, 1e-12)[0]
+        return (y.real * w_sh + y.imag * w_im).sum()
+
+    check(complex_loss, e, 1e-6)
+    check(lambda x: (ops.spherical_harmonics_with_derivative(x, 2, True, 1e-12)[0] * w_sh[:, :5]).sum(), e, 1e-6)
+    xg = e.clone().requires_grad_(True)
+    (g,) = torch.autograd.grad((ops.spherical_harmonics_table_with_derivative(xg, 2, True, 1e-12)[0]).sum(), xg,
+                               create_graph=False)
+    assert g.shape == e.shape
+    _opcheck(ops.cheb_exp_cos_radial_table_with_derivative.default, (r.clone().requires_grad_(True), c, lam, 7))
+    _opcheck(ops.spherical_harmonics_table_with_derivative.default, (e.clone().requires_grad_(True), 3, True, 1e-12))
+    with pytest.raises(Exception, match="first-order gradients only"):
+        torch.autograd.grad((ops.spherical_harmonics_table_with_derivative(xg, 2, True, 1e-12)[0]).sum(), xg,
+                            create_graph=True)
+
+
 def test_capability_report_hip_branch(gpu):
     """On the GPU the report's HIP branch is on: the ``cuda`` keys describe
     torch's ``cuda`` device type (the HIP device on ROCm), every listed

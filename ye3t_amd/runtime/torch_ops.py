@@ -13,7 +13,9 @@ device, so a call with device tensors runs this library's kernels.
   only the device kernels are added; otherwise the schemas are defined here,
   with the reference's exact signatures, together with fake implementations
   and the first-order autograd formulas of the forward operators (backward =
-  the reference's adjoint operator).
+  the reference's adjoint operator; for the radial and harmonic operators,
+  the saved derivative output contracted with the incoming gradient, and an
+  error for a second derivative).
 * Operators covered: the radial function and table, the harmonics of one
   ``l`` and the harmonic table (real and complex output), the scheduled
   radial-angular edge channels, density accumulation and its adjoint, the symmetric-power monomial and
@@ -595,9 +597,70 @@ def _bw_scheduled(ctx, values_adjoint, derivatives_adjoint):
     return g_radial, None, g_angular, None, None, None, None, None, None, g_scales
 
 
-SETUPS = {"scheduled_radial_angular_channels_with_derivative": _setup_scheduled}
+def _setup_basis(ctx, inputs, output):
+    """Radial and harmonic operators: keep the inputs and the derivative output
+    (which is not differentiable)."""
+    import torch
+
+    ctx.save_for_backward(*(x for x in inputs if isinstance(x, torch.Tensor)), output[1])
+    ctx.scalars = tuple(x for x in inputs if not isinstance(x, torch.Tensor))
+    ctx.mark_non_differentiable(output[1])
+
+
+def _first_order_only(name):
+    import torch
+
+    if torch.is_grad_enabled():
+        raise NotImplementedError(f"{name}: the HIP backend gives first-order gradients only "
+                                  "(no double backward through this operator)")
+
+
+def _bw_radial(ctx, values_adjoint, derivatives_adjoint):
+    """``d loss / d radii`` from the saved ``d/dr`` output, as the reference's
+    first-order formula (``execution_plan.py:2534-2599``); gradients in the
+    cutoffs or lambdas are not provided."""
+    radii, cutoffs, lambdas, derivative = ctx.saved_tensors
+    if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+        raise NotImplementedError("cheb_exp_cos_radial: gradients with respect to cutoffs or lambdas are not "
+                                  "provided by the HIP backend")
+    if values_adjoint is None or not ctx.needs_input_grad[0]:
+        return None, None, None, None
+    _first_order_only("cheb_exp_cos_radial")
+    grad = values_adjoint * derivative
+    if grad.ndim == radii.ndim + 1:  # the table: sum over the radial index
+        grad = grad.sum(-1)
+    return grad, None, None, None
+
+
+def _bw_sph(ctx, values_adjoint, derivatives_adjoint):
+    """``d loss / d edge_vectors`` from the saved Cartesian gradient output:
+    ``sum_lm g[e, lm] dY[e, lm, :]``, with ``Re(conj(g) dY)`` for complex
+    output (Torch's convention for a real input of a complex function), as
+    the reference's first-order formulas (``execution_plan.py:2845-2935``)."""
+    edge_vectors, derivative = ctx.saved_tensors
+    if values_adjoint is None or not ctx.needs_input_grad[0]:
+        return None, None, None, None
+    _first_order_only("spherical_harmonics")
+    if derivative.is_complex():
+        grad = (values_adjoint.conj().unsqueeze(-1) * derivative).real.sum(1)
+    else:
+        grad = (values_adjoint.unsqueeze(-1) * derivative).sum(1)
+    return grad.to(edge_vectors.dtype), None, None, None
+
+
+SETUPS = {
+    "scheduled_radial_angular_channels_with_derivative": _setup_scheduled,
+    "cheb_exp_cos_radial_with_derivative": _setup_basis,
+    "cheb_exp_cos_radial_table_with_derivative": _setup_basis,
+    "spherical_harmonics_with_derivative": _setup_basis,
+    "spherical_harmonics_table_with_derivative": _setup_basis,
+}
 
 BACKWARDS = {
+    "cheb_exp_cos_radial_with_derivative": _bw_radial,
+    "cheb_exp_cos_radial_table_with_derivative": _bw_radial,
+    "spherical_harmonics_with_derivative": _bw_sph,
+    "spherical_harmonics_table_with_derivative": _bw_sph,
     "scheduled_radial_angular_channels_with_derivative": _bw_scheduled,
     "density_accumulate": _bw_density,
     "density_accumulate_adjoint": _bw_density_adjoint,
