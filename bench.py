@@ -107,8 +107,8 @@ def host_facts():
 
 def cpu_calibration():
     """Restatement-over-reference time ratios measured in the development
-    container (the reference's own CPU core compiled from its sources; it is
-    never shipped to the GPU box), from the committed summary's
+    container (the reference's own CPU core compiled from its sources, which
+    only that container can build), from the committed summary's
     ``calibration:`` lines."""
     path = os.path.join(ROOT, "profiles", "cpu_baseline_calibration.md")
     out = {}

@@ -5,7 +5,7 @@ ref`` has compiled the reference's CPU core (``_ref/libye3t_ref.so``) and its
 schedule runtime (``_ref/ye3t_factorized_ref.so``) from their sources.  Both
 sides run on identical inputs, on one thread, best of ``repeats`` runs; the
 ratio restatement/reference says how far the ``cpu_baseline`` figure (which
-times the restatement on the GPU box, where the reference is never shipped)
+times the restatement on the GPU box's host cores)
 sits from the reference's own CPU speed.
 
     python -m oracle.calibrate [output.md]
