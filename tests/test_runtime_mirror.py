@@ -162,3 +162,28 @@ def test_monomial_table_checks():
         native.check_shared_table(2, counts, offs, np.array([0, 1, 3]), idx, vals)
     with pytest.raises(ValueError, match="coefficient_outputs"):
         native.check_shared_table(2, counts, offs, np.array([0, 1, 2]), np.array([1, 1, 1]), vals)
+
+
+REF_EXECUTION_PLAN = "/root/reference/ye3t/runtime/execution_plan.py"
+
+
+@pytest.mark.skipif(not __import__("os").path.exists(REF_EXECUTION_PLAN), reason="reference tree not present")
+def test_reference_operation_names_are_the_reference_report_names():
+    """Every name this backend reports under the reference's names appears,
+    quoted, among the operation names of the reference's capability report
+    (``cuda_operations`` and ``operations``, ``execution_plan.py:6118-6850``;
+    adjacent string literals joined), and each has a runtime function or an
+    operator (the ``real_`` / ``complex_`` harmonic names are the
+    ``spherical_harmonics_*`` functions with ``real_output`` set)."""
+    import re
+
+    with open(REF_EXECUTION_PLAN) as fh:
+        text = fh.read()
+    start = text.index("def native_execution_plan_capabilities")
+    body = re.sub(r'"\s*\n\s*"', "", text[start:start + 40000])
+    names = set(re.findall(r'"([a-z_0-9]+)"', body))
+    for name in runtime.REFERENCE_OPERATIONS:
+        assert name in names, name
+        base = re.sub(r"^(real|complex)_(?=spherical)", "", name)
+        assert hasattr(runtime, base) or hasattr(runtime, base + "_contraction") or base.startswith(
+            ("factorized_angular", "symmetric_power")), name
