@@ -143,6 +143,9 @@ def _complex_rows(l_max):
     return re, im, wr, wi
 
 
+_COMPLEX_ROWS = {}
+
+
 def complex_from_real_table(values, derivative, maximum_angular_momentum):
     """The reference's complex SH table and its Cartesian gradient from the
     packed real table ``values [E, W]`` and gradient ``derivative [E, W, 3]``.
@@ -153,12 +156,14 @@ def complex_from_real_table(values, derivative, maximum_angular_momentum):
     """
     import torch
 
-    re, im, wr, wi = _complex_rows(int(maximum_angular_momentum))
-    dev, dt = values.device, values.dtype
-    re = torch.tensor(re, dtype=torch.int64, device=dev)
-    im = torch.tensor(im, dtype=torch.int64, device=dev)
-    wr = torch.tensor(wr, dtype=dt, device=dev)
-    wi = torch.tensor(wi, dtype=dt, device=dev)
+    key = (int(maximum_angular_momentum), values.device, values.dtype)
+    tables = _COMPLEX_ROWS.get(key)
+    if tables is None:  # built once per (l_max, device, dtype)
+        re, im, wr, wi = _complex_rows(key[0])
+        tables = (torch.tensor(re, dtype=torch.int64, device=key[1]), torch.tensor(im, dtype=torch.int64, device=key[1]),
+                  torch.tensor(wr, dtype=key[2], device=key[1]), torch.tensor(wi, dtype=key[2], device=key[1]))
+        _COMPLEX_ROWS[key] = tables
+    re, im, wr, wi = tables
     y = torch.complex(values[:, re] * wr, values[:, im] * wi)
     g = torch.complex(derivative[:, re, :] * wr[:, None], derivative[:, im, :] * wi[:, None])
     return y, g
