@@ -210,10 +210,11 @@ def test_single_index_radial_and_harmonics(gpu):
 
 
 def test_radial_and_harmonic_operators_differentiate(gpu):
-    """First-order autograd of the radial and harmonic operators: the
-    gradient in the radii / edge vectors equals central differences of the
-    operator's own values (fp64, real and complex harmonics, one index and
-    the table); a second derivative raises instead of dropping terms."""
+    """Autograd of the radial and harmonic operators: the gradient in the
+    radii / edge vectors equals central differences of the operator's own
+    values (fp64, real and complex harmonics, one index and the table), and
+    the second derivative (the backward differentiated again) equals central
+    differences of the first-order gradient."""
     flush("torch ops: radial and harmonic autograd")
     import torch
 
@@ -250,15 +251,36 @@ def test_radial_and_harmonic_operators_differentiate(gpu):
 
     check(complex_loss, e, 1e-6)
     check(lambda x: (ops.spherical_harmonics_with_derivative(x, 2, True, 1e-12)[0] * w_sh[:, :5]).sum(), e, 1e-6)
-    xg = e.clone().requires_grad_(True)
-    (g,) = torch.autograd.grad((ops.spherical_harmonics_table_with_derivative(xg, 2, True, 1e-12)[0]).sum(), xg,
-                               create_graph=False)
-    assert g.shape == e.shape
     _opcheck(ops.cheb_exp_cos_radial_table_with_derivative.default, (r.clone().requires_grad_(True), c, lam, 7))
     _opcheck(ops.spherical_harmonics_table_with_derivative.default, (e.clone().requires_grad_(True), 3, True, 1e-12))
-    with pytest.raises(Exception, match="first-order gradients only"):
-        torch.autograd.grad((ops.spherical_harmonics_table_with_derivative(xg, 2, True, 1e-12)[0]).sum(), xg,
-                            create_graph=True)
+
+    # second derivatives: the gradient taken with create_graph equals the
+    # first-order one, and its own gradient equals central differences of the
+    # first-order gradient (which the HIP derivative outputs give)
+    def first(f, x):
+        xg = x.clone().requires_grad_(True)
+        return torch.autograd.grad(f(xg), xg)[0]
+
+    def second(f, x, w2):
+        xg = x.clone().requires_grad_(True)
+        (g,) = torch.autograd.grad(f(xg), xg, create_graph=True)
+        torch.testing.assert_close(g.detach(), first(f, x), rtol=1e-12, atol=1e-12)
+        (h,) = torch.autograd.grad((g * w2).sum(), xg)
+        fd = torch.zeros_like(x)
+        for i in range(x.numel()):
+            step = torch.zeros_like(x).view(-1)
+            step[i] = h_step
+            step = step.view(x.shape)
+            fd.view(-1)[i] = ((first(f, x + step) - first(f, x - step)) * w2).sum() / (2 * h_step)
+        torch.testing.assert_close(h, fd, rtol=1e-6, atol=1e-6)
+
+    h_step = 1e-6
+    second(lambda x: (ops.cheb_exp_cos_radial_table_with_derivative(x, c, lam, 7)[0] * w_tab).sum(), r,
+           torch.as_tensor(rng.normal(size=30), device=gpu))
+    w2 = torch.as_tensor(rng.normal(size=(30, 3)), device=gpu)
+    second(lambda x: (ops.spherical_harmonics_table_with_derivative(x, 3, True, 1e-12)[0] * w_sh).sum(), e, w2)
+    second(complex_loss, e, w2)
+    second(lambda x: (ops.spherical_harmonics_with_derivative(x, 2, True, 1e-12)[0] * w_sh[:, :5]).sum(), e, w2)
 
 
 def test_capability_report_hip_branch(gpu):

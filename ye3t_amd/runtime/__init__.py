@@ -146,6 +146,21 @@ def _complex_rows(l_max):
 _COMPLEX_ROWS = {}
 
 
+def _complex_tables(values, maximum_angular_momentum):
+    """The columns and weights of :func:`_complex_rows` as tensors on
+    ``values``'s device and dtype, built once per (l_max, device, dtype)."""
+    import torch
+
+    key = (int(maximum_angular_momentum), values.device, values.dtype)
+    tables = _COMPLEX_ROWS.get(key)
+    if tables is None:
+        re, im, wr, wi = _complex_rows(key[0])
+        tables = (torch.tensor(re, dtype=torch.int64, device=key[1]), torch.tensor(im, dtype=torch.int64, device=key[1]),
+                  torch.tensor(wr, dtype=key[2], device=key[1]), torch.tensor(wi, dtype=key[2], device=key[1]))
+        _COMPLEX_ROWS[key] = tables
+    return tables
+
+
 def complex_from_real_table(values, derivative, maximum_angular_momentum):
     """The reference's complex SH table and its Cartesian gradient from the
     packed real table ``values [E, W]`` and gradient ``derivative [E, W, 3]``.
@@ -156,14 +171,7 @@ def complex_from_real_table(values, derivative, maximum_angular_momentum):
     """
     import torch
 
-    key = (int(maximum_angular_momentum), values.device, values.dtype)
-    tables = _COMPLEX_ROWS.get(key)
-    if tables is None:  # built once per (l_max, device, dtype)
-        re, im, wr, wi = _complex_rows(key[0])
-        tables = (torch.tensor(re, dtype=torch.int64, device=key[1]), torch.tensor(im, dtype=torch.int64, device=key[1]),
-                  torch.tensor(wr, dtype=key[2], device=key[1]), torch.tensor(wi, dtype=key[2], device=key[1]))
-        _COMPLEX_ROWS[key] = tables
-    re, im, wr, wi = tables
+    re, im, wr, wi = _complex_tables(values, maximum_angular_momentum)
     y = torch.complex(values[:, re] * wr, values[:, im] * wi)
     g = torch.complex(derivative[:, re, :] * wr[:, None], derivative[:, im, :] * wi[:, None])
     return y, g

@@ -14,8 +14,9 @@ device, so a call with device tensors runs this library's kernels.
   with the reference's exact signatures, together with fake implementations
   and the first-order autograd formulas of the forward operators (backward =
   the reference's adjoint operator; for the radial and harmonic operators,
-  the saved derivative output contracted with the incoming gradient, and an
-  error for a second derivative).
+  the saved derivative output contracted with the incoming gradient, and for
+  a second derivative autograd through a differentiable Torch expression of
+  the basis, as the reference does without its native double backward).
 * Operators covered: the radial function and table, the harmonics of one
   ``l`` and the harmonic table (real and complex output), the scheduled
   radial-angular edge channels, density accumulation and its adjoint, the symmetric-power monomial and
@@ -607,40 +608,68 @@ def _setup_basis(ctx, inputs, output):
     ctx.mark_non_differentiable(output[1])
 
 
-def _first_order_only(name):
+def _bw_radial(ctx, values_adjoint, derivatives_adjoint):
+    """``d loss / d radii``: the saved ``d/dr`` output contracted with the
+    incoming gradient, as the reference's first-order formula
+    (``execution_plan.py:2534-2670``).  When the backward is itself
+    differentiated (``create_graph``), autograd through the differentiable
+    Torch expression of the basis (:mod:`ye3t_amd.runtime.basis_torch`)
+    instead, as the reference does without its native double backward.
+    Gradients in the cutoffs or lambdas are not provided."""
     import torch
 
-    if torch.is_grad_enabled():
-        raise NotImplementedError(f"{name}: the HIP backend gives first-order gradients only "
-                                  "(no double backward through this operator)")
-
-
-def _bw_radial(ctx, values_adjoint, derivatives_adjoint):
-    """``d loss / d radii`` from the saved ``d/dr`` output, as the reference's
-    first-order formula (``execution_plan.py:2534-2599``); gradients in the
-    cutoffs or lambdas are not provided."""
     radii, cutoffs, lambdas, derivative = ctx.saved_tensors
     if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
         raise NotImplementedError("cheb_exp_cos_radial: gradients with respect to cutoffs or lambdas are not "
                                   "provided by the HIP backend")
     if values_adjoint is None or not ctx.needs_input_grad[0]:
         return None, None, None, None
-    _first_order_only("cheb_exp_cos_radial")
+    table = derivative.ndim == radii.ndim + 1
+    if torch.is_grad_enabled():
+        from ye3t_amd.runtime import basis_torch
+
+        (index,) = ctx.scalars
+        values = basis_torch.cheb_exp_cos_radial(radii, cutoffs, lambdas, int(index))
+        if not table:
+            values = values[..., int(index)]
+        if not values.requires_grad:  # index 0: a constant
+            return torch.zeros_like(radii), None, None, None
+        (grad,) = torch.autograd.grad(values, radii, values_adjoint, create_graph=True)
+        return grad, None, None, None
     grad = values_adjoint * derivative
-    if grad.ndim == radii.ndim + 1:  # the table: sum over the radial index
+    if table:  # the table: sum over the radial index
         grad = grad.sum(-1)
     return grad, None, None, None
 
 
 def _bw_sph(ctx, values_adjoint, derivatives_adjoint):
-    """``d loss / d edge_vectors`` from the saved Cartesian gradient output:
-    ``sum_lm g[e, lm] dY[e, lm, :]``, with ``Re(conj(g) dY)`` for complex
-    output (Torch's convention for a real input of a complex function), as
-    the reference's first-order formulas (``execution_plan.py:2845-2935``)."""
+    """``d loss / d edge_vectors``: ``sum_lm g[e, lm] dY[e, lm, :]`` from the
+    saved Cartesian gradient output, with ``Re(conj(g) dY)`` for complex
+    output (Torch's convention for a real input of a complex function), as the
+    reference's first-order formulas (``execution_plan.py:2845-2935``).  When
+    the backward is itself differentiated, autograd through the differentiable
+    Torch expression of the harmonics (:mod:`ye3t_amd.runtime.basis_torch`)."""
+    import torch
+
     edge_vectors, derivative = ctx.saved_tensors
     if values_adjoint is None or not ctx.needs_input_grad[0]:
         return None, None, None, None
-    _first_order_only("spherical_harmonics")
+    if torch.is_grad_enabled():
+        from ye3t_amd import runtime
+        from ye3t_amd.runtime import basis_torch
+
+        l, real_output, epsilon = ctx.scalars
+        l = int(l)
+        values = basis_torch.real_harmonics(edge_vectors, l, float(epsilon))
+        if not real_output:
+            re, im, wr, wi = runtime._complex_tables(values, l)
+            values = torch.complex(values[:, re] * wr, values[:, im] * wi)
+        if derivative.shape[1] != values.shape[1]:  # one l: its columns of the table
+            values = values[:, l * l:]
+        if not values.requires_grad:  # l = 0: a constant
+            return torch.zeros_like(edge_vectors), None, None, None
+        (grad,) = torch.autograd.grad(values, edge_vectors, values_adjoint, create_graph=True)
+        return grad, None, None, None
     if derivative.is_complex():
         grad = (values_adjoint.conj().unsqueeze(-1) * derivative).real.sum(1)
     else:
